@@ -1,0 +1,156 @@
+/* tsn.h — C ABI of the MI355X (gfx950) DiT velocity path: libtsn.so.
+ *
+ * Drop-in boundary for the ThinkSound-native hot path. Each entry point names the reference
+ * interface it replaces (path:line into the ThinkSound-native sources). All pointers to tensors are
+ * DEVICE pointers obtained from tsn_alloc unless the parameter name ends in _host. Every call
+ * returns a tsn_status (0 = ok); on failure tsn_last_error() returns a message for the calling
+ * thread. Launchers are asynchronous on the runtime's single HIP stream (the reference batches
+ * into one Metal command buffer, src/gpu.mm:118-162); tsn_commit / tsn_sync wait.
+ * A runtime handle is not re-entrant: calls on one handle must not overlap.
+ *
+ * Layout conventions: row-major; GEMM weights [N][K] (out, in); conv weights [OC][IC][K] in the
+ * reference's layout, prepared once with tsn_conv1d_prepare.
+ */
+#ifndef TSN_H
+#define TSN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    TSN_OK = 0,
+    TSN_ERR_ARG = 1,          /* invalid argument (null pointer, bad shape) */
+    TSN_ERR_HIP = 2,          /* HIP runtime error */
+    TSN_ERR_UNSUPPORTED = 3,  /* valid but not implemented on this path (e.g. strided conv) */
+    TSN_ERR_OOM = 4,          /* device allocation failed */
+    TSN_ERR_STATE = 5         /* call out of order */
+} tsn_status;
+
+typedef enum { TSN_F32 = 0, TSN_F16 = 1, TSN_BF16 = 2 } tsn_dtype;
+
+typedef struct tsn_runtime tsn_runtime;
+typedef struct tsn_dit tsn_dit;
+
+const char *tsn_last_error(void);
+int tsn_version(void);
+
+/* ---------------- device harness: replaces tn::gpu::Device (src/gpu.h:20-48) ---------------- */
+int tsn_runtime_create(int device, tsn_runtime **out);          /* Device::init   src/gpu.h:25 */
+int tsn_runtime_destroy(tsn_runtime *rt);                       /* Device::~Device src/gpu.h:22 */
+int tsn_alloc(tsn_runtime *rt, size_t bytes, void **dptr);      /* Device::alloc  src/gpu.h:26; zero-filled */
+int tsn_free(tsn_runtime *rt, void *dptr);                      /* (no reference counterpart: Metal buffers live
+                                                                    for the process, src/gpu.mm:52-64) */
+/* Unified memory is replaced by explicit copies (host writes to Buf.p: src/dit_fwd.cpp:120-121,
+ * src/pipeline.cpp:131-132). Both block until the copy is done. */
+int tsn_upload(tsn_runtime *rt, void *dptr, const void *src_host, size_t bytes);
+int tsn_download(tsn_runtime *rt, void *dst_host, const void *dptr, size_t bytes);
+int tsn_begin(tsn_runtime *rt);                                 /* Device::begin  src/gpu.h:31 */
+int tsn_commit(tsn_runtime *rt);                                /* Device::commit src/gpu.h:38 */
+double tsn_last_gpu_ms(tsn_runtime *rt);                        /* Device::last_gpu_ms src/gpu.h:40 */
+int tsn_sync(tsn_runtime *rt);
+
+/* ---------------- launcher runtime: tn::Runtime (src/net.h:18-51) ---------------- */
+/* Y[M,N] = X[M,K]·W[N,K]^T (+bias[N], f32). Runtime::gemm src/net.h:24-26, src/net.mm:14-23.
+ * wdtype TSN_F16 runs on MFMA (X f32 or f16, converted to f16 on load; Y f32 or f16);
+ * TSN_F32 / TSN_BF16 weights run an f32 path (X, Y f32). ld* = 0 means packed.
+ * MFMA path needs K, ldx, ldw multiples of 8 and 16-byte aligned X and W. */
+int tsn_gemm(tsn_runtime *rt, int wdtype, const void *W, const void *X, int xdtype, void *Y, int ydtype,
+             const float *bias, uint32_t M, uint32_t N, uint32_t K, uint32_t ldx, uint32_t ldw, uint32_t ldy);
+/* y[n] = bias[n] + W[n,:]·x. Runtime::gemv src/net.h:27-28, src/net.mm:51-56 (wdtype f16/bf16/f32). */
+int tsn_gemv(tsn_runtime *rt, const void *W, int wdtype, const float *x, float *y, const float *bias,
+             uint32_t N, uint32_t K, uint32_t ldw);
+/* Upload-time conv weight transform [OC][IC][K] -> [OC][K][IC] f16 (W f16, or bf16 when w_bf16).
+ * The reference converts at load (src/net.mm:141-168); this adds the tap-major reorder that lets
+ * tsn_conv1d run as an implicit GEMM. Wp holds OC*IC*K halves. */
+int tsn_conv1d_prepare(tsn_runtime *rt, const void *W, int w_bf16, void *Wp, uint32_t OC, uint32_t IC, uint32_t K);
+/* conv1d, x [T,IC] f32, y [OL,OC] f32 (+bias). Runtime::conv src/net.h:29-34, src/net.mm:25-49.
+ * Implemented: stride 1, dil 1, OL = T + 2*pad - K + 1, IC % 64 == 0 (K > 1); else TSN_ERR_UNSUPPORTED. */
+int tsn_conv1d(tsn_runtime *rt, const void *Wp, const float *bias, const float *x, float *y, uint32_t T,
+               uint32_t OL, uint32_t IC, uint32_t OC, uint32_t K, uint32_t stride, uint32_t pad, uint32_t dil);
+/* elementwise, f32 (src/net.h:37-49; shaders/ops_conv.metal:9-57,193-201) */
+int tsn_silu(tsn_runtime *rt, float *x, size_t n);
+int tsn_copy(tsn_runtime *rt, const float *x, float *y, size_t n);
+int tsn_swiglu(tsn_runtime *rt, const float *a, const float *b, float *y, size_t n);
+int tsn_add(tsn_runtime *rt, const float *a, const float *b, float *y, size_t n);
+int tsn_add_bcast_col(tsn_runtime *rt, const float *x, const float *v, float *y, uint32_t S, uint32_t H);
+int tsn_cfg_euler(tsn_runtime *rt, const float *fc, const float *fu, float *x, size_t n, float cfg, float dt);
+/* named kernels dispatched by dit_fwd.cpp (src/dit_fwd.cpp:16-22), on net.h as the north star asks:
+ * adaln_ln  — AD{H,per_row,chunks,base,eps}  shaders/ops_conv.metal:127-144 (y f32 or f16)
+ * gate_add  — GA{H,per_row,chunks,gate_idx}  shaders/ops_conv.metal:146-154
+ * rms_head  — RH{ld,hd,col_off,row_off,eps}  shaders/ops_conv.metal:115-125 (in place)
+ * rope_pairs— RP{ld,hd,col_off,row_off,fscale,base} shaders/ops_conv.metal:156-169 (in place)
+ * attention — AttnP (src/gpu.h:60-70), src/dit_fwd.cpp:83-102; hd must be 64 */
+int tsn_adaln_ln(tsn_runtime *rt, const float *x, const float *mod, void *y, int ydtype, uint32_t rows, uint32_t H,
+                 uint32_t per_row, uint32_t chunks, uint32_t base, float eps);
+int tsn_gate_add(tsn_runtime *rt, const float *x, const float *f, const float *mod, float *y, uint32_t rows,
+                 uint32_t H, uint32_t per_row, uint32_t chunks, uint32_t gate_idx);
+int tsn_rms_head(tsn_runtime *rt, float *x, const float *w, uint32_t rows, uint32_t nh, uint32_t ld, uint32_t hd,
+                 uint32_t col_off, uint32_t row_off, float eps);
+int tsn_rope_pairs(tsn_runtime *rt, float *x, const int32_t *pos, uint32_t rows, uint32_t nh, uint32_t ld,
+                   uint32_t hd, uint32_t col_off, uint32_t row_off, float fscale, float base);
+int tsn_attention(tsn_runtime *rt, const float *qkv, float *out, uint32_t S, uint32_t nh, uint32_t hd, uint32_t ld,
+                  uint32_t ldo, uint32_t q_off, uint32_t k_off, uint32_t v_off, uint32_t o_off, float scale);
+
+/* ---------------- model: tn::DitModel (src/models.h:55-85) ---------------- */
+typedef struct {
+    int B;              /* batch: CFG arms folded in (sample 2p cond, 2p+1 uncond); 1, 2, 4, 8 or 16 */
+    int La, Lt;         /* audio (latent) rows and text rows per sample */
+    int H, NH, HD, F;   /* hidden 1024, heads 16, head dim 64, FFN width 4096 */
+    int latent;         /* latent channels (64) */
+    int temb_dim;       /* timestep sinusoid width (256) */
+    int n_joint;        /* joint two-stream blocks (7) */
+    int n_fused;        /* fused single-stream blocks over La+Lt rows (14) */
+    int audio_ffn_conv; /* 1: audio FFN of joint blocks is conv1d k=3 pad=1 */
+    float rope_theta;   /* 10000 */
+    float t_max_period; /* timestep sinusoid max period (1): fr_k = (1e4/max_period)*1e4^(-2k/D) */
+    float ln_eps;       /* 1e-5 (src/dit_fwd.cpp:29) */
+    float rms_eps;      /* 1e-6 (src/dit_fwd.cpp:37) */
+} tsn_dit_spec;
+
+/* Spec of a workload: 0 one joint block (B=2, La=256), 1 one eval 8 s (B=2, La=256, Lt=141),
+ * 2 sampler 8 s (as 1), 3 sampler 30 s (La=960), 4 batch 16 at 8 s. */
+int tsn_dit_default_spec(int workload, tsn_dit_spec *out);
+/* weight manifest (the flat BF16 weight buffer order) */
+int tsn_dit_manifest_count(const tsn_dit_spec *spec);
+int tsn_dit_manifest_entry(const tsn_dit_spec *spec, int idx, char *name, int name_cap, int64_t *numel,
+                           int64_t *offset);
+int64_t tsn_dit_manifest_total(const tsn_dit_spec *spec);
+
+int tsn_dit_create(tsn_runtime *rt, const tsn_dit_spec *spec, tsn_dit **out);   /* DitModel::load src/dit.cpp:29-47 */
+int tsn_dit_destroy(tsn_dit *dit);
+/* WeightSet::load (src/net.mm:126-173) for the synthetic checkpoint: flat BF16, manifest order */
+int tsn_dit_upload_weights(tsn_dit *dit, const uint16_t *weights_host, size_t numel);
+/* One velocity evaluation. DitModel::forward (src/models.h:83-84, src/dit_fwd.cpp:104-304) with the
+ * arms batched: z [B][La][latent], text [B][Lt][H], pooled [B][H] -> v [B][La][latent]; every
+ * sample uses timestep t. Enqueued; call tsn_sync / tsn_commit before reading v. */
+int tsn_dit_forward(tsn_dit *dit, const float *z, float t, const float *text, const float *pooled, float *v);
+/* same with per-sample t (device [B]) and optional taps: X after each block, [n_blocks][B][La+Lt][H] */
+int tsn_dit_forward_ex(tsn_dit *dit, const float *z, const float *t, const float *text, const float *pooled,
+                       float *v, float *taps);
+/* one joint / fused block on X [B][La+Lt][H] in place; g [B][H] is the global conditioning (silu inside) */
+int tsn_dit_joint_block(tsn_dit *dit, int block, float *X, const float *g);
+int tsn_dit_fused_block(tsn_dit *dit, int block, float *X, const float *g);
+/* Rectified-flow Euler sampler with CFG (src/pipeline.cpp:141-155): x [B/2][La][latent] in/out */
+int tsn_dit_sample(tsn_dit *dit, float *x, const float *text, const float *pooled, int steps, float cfg);
+/* hipGraph capture of one forward (t read from device t[B]) or of the whole sampler, then replay */
+int tsn_dit_capture_forward(tsn_dit *dit, const float *z, const float *t, const float *text, const float *pooled,
+                            float *v);
+int tsn_dit_capture_sample(tsn_dit *dit, float *x, const float *text, const float *pooled, int steps, float cfg);
+int tsn_dit_replay(tsn_dit *dit);
+
+/* ---------------- synthetic data (specified generator; see thinksound-native_amd/csrc/synth.cpp) ---------------- */
+int tsn_synth_normal_f32(uint64_t seed, uint64_t index, double mean, double std, size_t n, float *out_host);
+int tsn_synth_normal_bf16(uint64_t seed, uint64_t index, double mean, double std, size_t n, uint16_t *out_host);
+int tsn_synth_uniform_f32(uint64_t seed, uint64_t index, double lo, double hi, size_t n, float *out_host);
+/* all weights of a spec, flat BF16 in manifest order: N(0, 0.02); q/k norm weights N(norm_mean, 0.02) */
+int tsn_dit_synth_weights(const tsn_dit_spec *spec, uint64_t seed, double norm_mean, uint16_t *out_host);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TSN_H */

@@ -1,0 +1,122 @@
+// oracle.h — CPU f32 restatement of the ThinkSound-native DiT velocity path.
+//
+// TEST INFRASTRUCTURE ONLY. This library is the checker: only tests/, the smoke
+// entry point and the benchmark's CPU-baseline leg load it. The product library
+// (libtsn) never links, loads or calls it.
+//
+// Every function restates the reference's op semantics in plain f32 arithmetic on
+// the host (citations are path:line into the ThinkSound-native sources). Reductions
+// run in a fixed order per output element, so results do not depend on the OpenMP
+// thread count. Pinning of each function (closed forms, brute force, invariants) is
+// done by tests/test_oracle.py; every function below is pinned there.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---------------- single ops ---------------- */
+
+// Y[m*ldy+n] = sum_k X[m*ldx+k] * W[n*ldw+k] (+ bias[n])
+// Follows shaders/gemm_mpp.metal:2-3,39-46 (Y = X·Wᵀ + b) and src/net.mm:14-23 (ld defaults).
+void orc_gemm(const float *W, const float *X, float *Y, const float *bias,
+              int M, int N, int K, int ldx, int ldw, int ldy);
+
+// y[n] = bias[n] + sum_k W[n*ldw+k] * x[k]        (shaders/gemm_attn.metal:47-74)
+void orc_gemv(const float *W, const float *x, float *y, const float *bias, int N, int K, int ldw);
+
+// conv1d, x [T,IC] row-major, y [OL,OC] row-major, W [OC][IC][K] (reference layout),
+// ti = t*stride - pad + k*dil, zero outside [0,T).   (shaders/ops_conv.metal:221-246,262-283;
+// src/net.mm:25-49). Computed as im2col + gemm, the reference's own route.
+void orc_conv1d(const float *W, const float *bias, const float *x, float *y,
+                int T, int OL, int IC, int OC, int K, int stride, int pad, int dil);
+
+// Direct (non-im2col) conv1d, same semantics; used to cross-check orc_conv1d.
+void orc_conv1d_direct(const float *W, const float *bias, const float *x, float *y,
+                       int T, int OL, int IC, int OC, int K, int stride, int pad, int dil);
+
+// y = LN(x; eps, no affine)*(1 + m[base+H+i]) + m[base+i], biased variance, two-pass.
+// m = mod + (per_row ? row*chunks*H : 0).             (shaders/ops_conv.metal:127-144)
+void orc_adaln_ln(const float *x, const float *mod, float *y, int rows, int H,
+                  int per_row, int chunks, int base, float eps);
+
+// y = x + f * m[gate_idx*H + c], m per row or broadcast. (shaders/ops_conv.metal:146-154)
+void orc_gate_add(const float *x, const float *f, const float *mod, float *y, int rows, int H,
+                  int per_row, int chunks, int gate_idx);
+
+// in-place per-head RMSNorm on a column slice: r = r*rsqrt(mean(r^2)+eps)*w[i]
+// r = x + (row_off+row)*ld + col_off + head*hd.          (shaders/ops_conv.metal:115-125)
+void orc_rms_head(float *x, const float *w, int rows, int nh, int ld, int hd,
+                  int col_off, int row_off, float eps);
+
+// in-place interleaved-pair RoPE: inv = base^(-2j/hd), ang = pos*fscale*inv
+// (pos = row when pos == NULL).                          (shaders/ops_conv.metal:156-169)
+void orc_rope_pairs(float *x, const int32_t *pos, int rows, int nh, int ld, int hd,
+                    int col_off, int row_off, float fscale, float base);
+
+// non-causal attention over a [S, ld] qkv buffer: O[q, o_off+h*hd+d] = softmax_k(scale*Q·K)·V
+// Materialised scores, max-subtracted exp, normalise.    (shaders/gemm_attn.metal:96-202,
+// src/dit_fwd.cpp:83-102)
+void orc_attention(const float *qkv, float *out, int S, int nh, int hd, int ld, int ldo,
+                   int q_off, int k_off, int v_off, int o_off, float scale);
+
+// elementwise ops (shaders/ops_conv.metal:9-13,30-57,193-201)
+void orc_silu(float *x, size_t n);
+void orc_swiglu(const float *a, const float *b, float *y, size_t n);
+void orc_add(const float *a, const float *b, float *y, size_t n);
+void orc_add_bcast_col(const float *x, const float *v, float *y, int S, int H);
+void orc_cfg_euler(const float *fc, const float *fu, float *x, size_t n, float cfg, float dt);
+
+// sinusoidal timestep embedding, cos half then sin half:
+// fr_k = (10000/max_period) * 10000^(-2k/D); out[k] = cos(t*fr_k), out[D/2+k] = sin(t*fr_k)
+// (src/dit_fwd.cpp:111-119)
+void orc_timestep_embedding(float t, int D, float max_period, float *out);
+
+/* ---------------- block graph ---------------- */
+
+// Graph spec. Field meaning mirrors the library's tsn_dit_spec.
+typedef struct {
+    int B, La, Lt;          // batch (CFG arms folded), audio rows, text rows
+    int H, NH, HD, F;       // hidden, heads, head dim, FFN width
+    int latent, temb_dim;   // latent channels, timestep sinusoid width
+    int n_joint, n_fused;   // joint blocks, fused single-stream blocks
+    int audio_ffn_conv;     // 1: audio FFN is conv1d k=3 pad=1 (joint blocks)
+    float rope_theta, t_max_period, ln_eps, rms_eps;
+} orc_spec;
+
+// Number of tensors in the weight manifest and the element count / offset of each,
+// in manifest order (the library's manifest must agree; tests check it).
+int orc_manifest_count(const orc_spec *s);
+int64_t orc_manifest_numel(const orc_spec *s, int idx);
+int64_t orc_manifest_total(const orc_spec *s);
+// Name of tensor idx written into buf (NUL-terminated, truncated to cap).
+void orc_manifest_name(const orc_spec *s, int idx, char *buf, int cap);
+
+// One joint block on X [B, La+Lt, H] (audio rows first per sample) in place;
+// gs = silu(g) [B, H] feeds the adaLN modulation.
+void orc_joint_block(const orc_spec *s, const float *weights, int block, float *X, const float *gs);
+
+// One fused single-stream block on X [B, S, H] in place.
+void orc_fused_block(const orc_spec *s, const float *weights, int block, float *X, const float *gs);
+
+// One full velocity evaluation.
+//   z [B, La, latent], t [B], text [B, Lt, H], pooled [B, H]  ->  v [B, La, latent]
+//   taps (optional, may be NULL): X [B, S, H] after each of the n_joint+n_fused blocks.
+//   gs_out (optional): silu(global cond) [B, H].
+void orc_dit_forward(const orc_spec *s, const float *weights, const float *z, const float *t,
+                     const float *text, const float *pooled, float *v, float *taps, float *gs_out);
+
+// Rectified-flow Euler sampler with CFG (src/pipeline.cpp:141-155). B = 2*P: sample 2p is the
+// conditional arm and 2p+1 the unconditional arm of prompt p. x [P, La, latent] in/out.
+// t_s = 1 - s/steps, dt = t_{s+1} - t_s; x += dt*(v_u + cfg*(v_c - v_u)).
+void orc_dit_sample(const orc_spec *s, const float *weights, float *x, const float *text,
+                    const float *pooled, int steps, float cfg);
+
+// number of OpenMP threads the oracle uses (for the CPU-baseline report)
+int orc_num_threads(void);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,375 @@
+"""thinksound-native_amd: MI355X (gfx950) DiT velocity path behind the libtsn C ABI.
+
+Python mirror of the reference host interface for this path — tn::Runtime launchers
+(src/net.h:18-51) and tn::DitModel (src/models.h:55-85) — over ctypes. No compute happens in
+Python; every call goes through libtsn.so (thinksound-native_amd/lib), which must have been built
+(build.py). Loading fails loudly when it is missing: there is no CPU fallback.
+
+The package directory name has a hyphen, so import it with importlib:
+    tsn = importlib.import_module("thinksound-native_amd")
+"""
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libtsn.so")
+
+F32, F16, BF16 = 0, 1, 2
+_NP_DT = {F32: np.float32, F16: np.float16, BF16: np.uint16}
+
+_lib = None
+
+
+class TsnError(RuntimeError):
+    def __init__(self, fn, code, msg):
+        super().__init__("%s failed (status %d): %s" % (fn, code, msg))
+        self.code = code
+
+
+class DitSpec(ctypes.Structure):
+    """tsn_dit_spec (include/tsn.h)."""
+    _fields_ = [("B", ctypes.c_int), ("La", ctypes.c_int), ("Lt", ctypes.c_int),
+                ("H", ctypes.c_int), ("NH", ctypes.c_int), ("HD", ctypes.c_int), ("F", ctypes.c_int),
+                ("latent", ctypes.c_int), ("temb_dim", ctypes.c_int),
+                ("n_joint", ctypes.c_int), ("n_fused", ctypes.c_int), ("audio_ffn_conv", ctypes.c_int),
+                ("rope_theta", ctypes.c_float), ("t_max_period", ctypes.c_float),
+                ("ln_eps", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+    def copy(self, **kw):
+        s = DitSpec()
+        for k, _ in self._fields_:
+            setattr(s, k, kw.get(k, getattr(self, k)))
+        return s
+
+
+_P = ctypes.c_void_p
+_U32 = ctypes.c_uint32
+_I = ctypes.c_int
+_SZ = ctypes.c_size_t
+_FL = ctypes.c_float
+_SIGS = {
+    "tsn_runtime_create": [_I, ctypes.POINTER(_P)],
+    "tsn_runtime_destroy": [_P],
+    "tsn_alloc": [_P, _SZ, ctypes.POINTER(_P)],
+    "tsn_free": [_P, _P],
+    "tsn_upload": [_P, _P, _P, _SZ],
+    "tsn_download": [_P, _P, _P, _SZ],
+    "tsn_begin": [_P],
+    "tsn_commit": [_P],
+    "tsn_sync": [_P],
+    "tsn_gemm": [_P, _I, _P, _P, _I, _P, _I, _P, _U32, _U32, _U32, _U32, _U32, _U32],
+    "tsn_gemv": [_P, _P, _I, _P, _P, _P, _U32, _U32, _U32],
+    "tsn_conv1d_prepare": [_P, _P, _I, _P, _U32, _U32, _U32],
+    "tsn_conv1d": [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _U32, _U32],
+    "tsn_silu": [_P, _P, _SZ],
+    "tsn_copy": [_P, _P, _P, _SZ],
+    "tsn_swiglu": [_P, _P, _P, _P, _SZ],
+    "tsn_add": [_P, _P, _P, _P, _SZ],
+    "tsn_add_bcast_col": [_P, _P, _P, _P, _U32, _U32],
+    "tsn_cfg_euler": [_P, _P, _P, _P, _SZ, _FL, _FL],
+    "tsn_adaln_ln": [_P, _P, _P, _P, _I, _U32, _U32, _U32, _U32, _U32, _FL],
+    "tsn_gate_add": [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32],
+    "tsn_rms_head": [_P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _FL],
+    "tsn_rope_pairs": [_P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _FL, _FL],
+    "tsn_attention": [_P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _U32, _U32, _U32, _FL],
+    "tsn_dit_default_spec": [_I, ctypes.POINTER(DitSpec)],
+    "tsn_dit_manifest_count": [ctypes.POINTER(DitSpec)],
+    "tsn_dit_manifest_entry": [ctypes.POINTER(DitSpec), _I, ctypes.c_char_p, _I,
+                               ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)],
+    "tsn_dit_manifest_total": [ctypes.POINTER(DitSpec)],
+    "tsn_dit_create": [_P, ctypes.POINTER(DitSpec), ctypes.POINTER(_P)],
+    "tsn_dit_destroy": [_P],
+    "tsn_dit_upload_weights": [_P, _P, _SZ],
+    "tsn_dit_forward": [_P, _P, _FL, _P, _P, _P],
+    "tsn_dit_forward_ex": [_P, _P, _P, _P, _P, _P, _P],
+    "tsn_dit_joint_block": [_P, _I, _P, _P],
+    "tsn_dit_fused_block": [_P, _I, _P, _P],
+    "tsn_dit_sample": [_P, _P, _P, _P, _I, _FL],
+    "tsn_dit_capture_forward": [_P, _P, _P, _P, _P, _P],
+    "tsn_dit_capture_sample": [_P, _P, _P, _P, _I, _FL],
+    "tsn_dit_replay": [_P],
+    "tsn_synth_normal_f32": [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, _SZ, _P],
+    "tsn_synth_normal_bf16": [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, _SZ, _P],
+    "tsn_synth_uniform_f32": [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, _SZ, _P],
+    "tsn_dit_synth_weights": [ctypes.POINTER(DitSpec), ctypes.c_uint64, ctypes.c_double, _P],
+}
+_RESTYPES = {"tsn_last_error": ctypes.c_char_p, "tsn_last_gpu_ms": ctypes.c_double,
+             "tsn_dit_manifest_total": ctypes.c_int64, "tsn_version": _I}
+
+
+def lib():
+    """Load libtsn.so (once). Raises if it has not been built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError("libtsn.so is not built (%s); run thinksound-native_amd/build.py" % LIB_PATH)
+        L = ctypes.CDLL(LIB_PATH)
+        for name, args in _SIGS.items():
+            f = getattr(L, name)
+            f.argtypes = args
+            f.restype = _RESTYPES.get(name, _I)
+        L.tsn_last_error.restype = ctypes.c_char_p
+        L.tsn_last_error.argtypes = []
+        L.tsn_last_gpu_ms.restype = ctypes.c_double
+        L.tsn_last_gpu_ms.argtypes = [_P]
+        L.tsn_version.restype = _I
+        _lib = L
+    return _lib
+
+
+def call(name, *args):
+    """Call a tsn_* entry point; raise TsnError on a non-zero status."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        raise TsnError(name, rc, lib().tsn_last_error().decode())
+    return rc
+
+
+def ptr(a):
+    """Host pointer of a contiguous numpy array."""
+    assert a.flags["C_CONTIGUOUS"]
+    return ctypes.c_void_p(a.ctypes.data)
+
+
+def default_spec(workload):
+    s = DitSpec()
+    call("tsn_dit_default_spec", workload, ctypes.byref(s))
+    return s
+
+
+def manifest(spec):
+    L = lib()
+    n = L.tsn_dit_manifest_count(ctypes.byref(spec))
+    out = []
+    buf = ctypes.create_string_buffer(256)
+    for i in range(n):
+        numel, off = ctypes.c_int64(), ctypes.c_int64()
+        call("tsn_dit_manifest_entry", ctypes.byref(spec), i, buf, 256, ctypes.byref(numel), ctypes.byref(off))
+        out.append((buf.value.decode(), numel.value, off.value))
+    return out
+
+
+def manifest_total(spec):
+    return int(lib().tsn_dit_manifest_total(ctypes.byref(spec)))
+
+
+def synth_normal_f32(seed, index, mean, std, shape):
+    a = np.empty(shape, np.float32)
+    call("tsn_synth_normal_f32", seed, index, mean, std, a.size, ptr(a))
+    return a
+
+
+def synth_normal_bf16(seed, index, mean, std, shape):
+    a = np.empty(shape, np.uint16)
+    call("tsn_synth_normal_bf16", seed, index, mean, std, a.size, ptr(a))
+    return a
+
+
+def synth_uniform_f32(seed, index, lo, hi, shape):
+    a = np.empty(shape, np.float32)
+    call("tsn_synth_uniform_f32", seed, index, lo, hi, a.size, ptr(a))
+    return a
+
+
+def synth_weights(spec, seed=4242, norm_mean=0.0):
+    w = np.empty(manifest_total(spec), np.uint16)
+    call("tsn_dit_synth_weights", ctypes.byref(spec), seed, norm_mean, ptr(w))
+    return w
+
+
+def bf16_to_f32(u16):
+    return (u16.astype(np.uint32) << 16).view(np.float32)
+
+
+class DeviceArray:
+    """A device allocation owned by a Runtime (freed with it or by free())."""
+
+    def __init__(self, rt, shape, dtype):
+        self.rt, self.shape, self.dtype = rt, tuple(shape), np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        p = ctypes.c_void_p()
+        call("tsn_alloc", rt.h, max(self.nbytes, 1), ctypes.byref(p))
+        self.ptr = p
+
+    @property
+    def p(self):
+        return self.ptr
+
+    def offset(self, elems):
+        return ctypes.c_void_p(self.ptr.value + elems * self.dtype.itemsize)
+
+    def upload(self, a):
+        a = np.ascontiguousarray(a, dtype=self.dtype)
+        assert a.nbytes == self.nbytes, (a.shape, self.shape)
+        call("tsn_upload", self.rt.h, self.ptr, ptr(a), a.nbytes)
+        return self
+
+    def numpy(self):
+        a = np.empty(self.shape, self.dtype)
+        call("tsn_download", self.rt.h, ptr(a), self.ptr, self.nbytes)
+        return a
+
+    def free(self):
+        if self.ptr is not None:
+            call("tsn_free", self.rt.h, self.ptr)
+            self.ptr = None
+
+
+class Runtime:
+    """tn::Runtime mirror (src/net.h:18-51) over one GPU and one HIP stream."""
+
+    def __init__(self, device=0):
+        h = ctypes.c_void_p()
+        call("tsn_runtime_create", device, ctypes.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().tsn_runtime_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def empty(self, shape, dtype=np.float32):
+        return DeviceArray(self, shape, dtype)
+
+    def array(self, a, dtype=None):
+        a = np.ascontiguousarray(a, dtype=dtype or a.dtype)
+        return DeviceArray(self, a.shape, a.dtype).upload(a)
+
+    def sync(self):
+        call("tsn_sync", self.h)
+
+    def begin(self):
+        call("tsn_begin", self.h)
+
+    def commit(self):
+        call("tsn_commit", self.h)
+        return lib().tsn_last_gpu_ms(self.h)
+
+    # --- launchers (names follow src/net.h) ---
+    def gemm(self, wdtype, W, X, xdtype, Y, ydtype, bias, M, N, K, ldx=0, ldw=0, ldy=0):
+        call("tsn_gemm", self.h, wdtype, W.p, X.p, xdtype, Y.p, ydtype, bias.p if bias is not None else None,
+             M, N, K, ldx, ldw, ldy)
+
+    def gemv(self, W, wdtype, x, y, bias, N, K, ldw=0):
+        call("tsn_gemv", self.h, W.p, wdtype, x.p, y.p, bias.p if bias is not None else None, N, K, ldw)
+
+    def conv1d_prepare(self, W, w_bf16, Wp, OC, IC, K):
+        call("tsn_conv1d_prepare", self.h, W.p, int(w_bf16), Wp.p, OC, IC, K)
+
+    def conv1d(self, Wp, bias, x, y, T, OL, IC, OC, K, stride, pad, dil):
+        call("tsn_conv1d", self.h, Wp.p, bias.p if bias is not None else None, x.p, y.p, T, OL, IC, OC, K,
+             stride, pad, dil)
+
+    def adaln_ln(self, x, mod, y, ydtype, rows, H, per_row, chunks, base, eps):
+        call("tsn_adaln_ln", self.h, x.p, mod.p, y.p, ydtype, rows, H, per_row, chunks, base, eps)
+
+    def gate_add(self, x, f, mod, y, rows, H, per_row, chunks, gate_idx):
+        call("tsn_gate_add", self.h, x.p, f.p, mod.p, y.p, rows, H, per_row, chunks, gate_idx)
+
+    def rms_head(self, x, w, rows, nh, ld, hd, col_off, row_off, eps):
+        call("tsn_rms_head", self.h, x.p, w.p, rows, nh, ld, hd, col_off, row_off, eps)
+
+    def rope_pairs(self, x, pos, rows, nh, ld, hd, col_off, row_off, fscale, base):
+        call("tsn_rope_pairs", self.h, x.p, pos.p if pos is not None else None, rows, nh, ld, hd, col_off,
+             row_off, fscale, base)
+
+    def attention(self, qkv, out, S, nh, hd, ld, ldo, q_off, k_off, v_off, o_off, scale):
+        call("tsn_attention", self.h, qkv.p, out.p, S, nh, hd, ld, ldo, q_off, k_off, v_off, o_off, scale)
+
+    def silu(self, x, n):
+        call("tsn_silu", self.h, x.p, n)
+
+    def copy(self, x, y, n):
+        call("tsn_copy", self.h, x.p, y.p, n)
+
+    def swiglu(self, a, b, y, n):
+        call("tsn_swiglu", self.h, a.p, b.p, y.p, n)
+
+    def add_(self, a, b, y, n):
+        call("tsn_add", self.h, a.p, b.p, y.p, n)
+
+    def add_bcast_col(self, x, v, y, S, H):
+        call("tsn_add_bcast_col", self.h, x.p, v.p, y.p, S, H)
+
+    def cfg_euler(self, fc, fu, x, n, cfg, dt):
+        call("tsn_cfg_euler", self.h, fc.p, fu.p, x.p, n, cfg, dt)
+
+
+class DitModel:
+    """tn::DitModel mirror (src/models.h:55-85) for the batched two-stream graph."""
+
+    def __init__(self, rt, spec):
+        self.rt, self.spec = rt, spec
+        h = ctypes.c_void_p()
+        call("tsn_dit_create", rt.h, ctypes.byref(spec), ctypes.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().tsn_dit_destroy(self.h)
+            self.h = None
+
+    def upload_weights(self, w_bf16):
+        w_bf16 = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+        call("tsn_dit_upload_weights", self.h, ptr(w_bf16), w_bf16.size)
+
+    def forward(self, z, t, text, pooled, v):
+        call("tsn_dit_forward", self.h, z.p, float(t), text.p if text is not None else None, pooled.p, v.p)
+
+    def forward_ex(self, z, t_dev, text, pooled, v, taps=None):
+        call("tsn_dit_forward_ex", self.h, z.p, t_dev.p, text.p if text is not None else None, pooled.p, v.p,
+             taps.p if taps is not None else None)
+
+    def joint_block(self, block, X, g):
+        call("tsn_dit_joint_block", self.h, block, X.p, g.p)
+
+    def fused_block(self, block, X, g):
+        call("tsn_dit_fused_block", self.h, block, X.p, g.p)
+
+    def sample(self, x, text, pooled, steps, cfg):
+        call("tsn_dit_sample", self.h, x.p, text.p, pooled.p, steps, cfg)
+
+    def capture_forward(self, z, t_dev, text, pooled, v):
+        call("tsn_dit_capture_forward", self.h, z.p, t_dev.p, text.p, pooled.p, v.p)
+
+    def capture_sample(self, x, text, pooled, steps, cfg):
+        call("tsn_dit_capture_sample", self.h, x.p, text.p, pooled.p, steps, cfg)
+
+    def replay(self):
+        call("tsn_dit_replay", self.h)
+
+
+# Input index space of the synthetic generator (weights use their manifest index).
+IDX_Z, IDX_TEXT, IDX_POOLED, IDX_T, IDX_G, IDX_X = 1000, 1001, 1002, 1003, 1004, 1005
+
+
+def synth_inputs(spec, seed=4242, cfg_pairs=False):
+    """Seeded inputs of a workload. cfg_pairs: samples come in (cond, uncond) pairs — the
+    unconditional arm gets zeroed text and pooled features, both arms share z and t."""
+    B, La, Lt, H, lat = spec.B, spec.La, spec.Lt, spec.H, spec.latent
+    if cfg_pairs:
+        P = B // 2
+        z1 = synth_normal_f32(seed, IDX_Z, 0.0, 1.0, (P, La, lat))
+        z = np.repeat(z1, 2, axis=0)
+        text = np.zeros((B, Lt, H), np.float32)
+        pooled = np.zeros((B, H), np.float32)
+        text[0::2] = synth_normal_f32(seed, IDX_TEXT, 0.0, 1.0, (P, Lt, H))
+        pooled[0::2] = synth_normal_f32(seed, IDX_POOLED, 0.0, 1.0, (P, H))
+        t = np.repeat(synth_uniform_f32(seed, IDX_T, 0.0, 1.0, (1,)), B).astype(np.float32)
+    else:
+        z = synth_normal_f32(seed, IDX_Z, 0.0, 1.0, (B, La, lat))
+        text = synth_normal_f32(seed, IDX_TEXT, 0.0, 1.0, (B, Lt, H))
+        pooled = synth_normal_f32(seed, IDX_POOLED, 0.0, 1.0, (B, H))
+        t = np.repeat(synth_uniform_f32(seed, IDX_T, 0.0, 1.0, (1,)), B).astype(np.float32)
+    return {"z": z, "t": t, "text": text, "pooled": pooled}

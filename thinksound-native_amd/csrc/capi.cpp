@@ -1,0 +1,233 @@
+// capi.cpp — extern "C" boundary of libtsn (declarations and reference citations in include/tsn.h).
+#include "../../include/tsn.h"
+
+#include <string.h>
+
+#include <new>
+
+#include "dit.h"
+
+namespace tsn {
+void synth_normal_f32(uint64_t seed, uint64_t idx, double mean, double std, size_t n, float *out);
+void synth_normal_bf16(uint64_t seed, uint64_t idx, double mean, double std, size_t n, uint16_t *out);
+void synth_uniform_f32(uint64_t seed, uint64_t idx, double lo, double hi, size_t n, float *out);
+}
+
+struct tsn_runtime {
+    tsn::Runtime rt;
+};
+struct tsn_dit {
+    tsn::DitModel m;
+};
+
+#define RT_CHECK(r)                                                 \
+    do {                                                            \
+        if (!(r)) { tsn::set_error("null runtime handle"); return TSN_ERR_ARG; } \
+    } while (0)
+
+static tsn::DitSpec to_spec(const tsn_dit_spec *c) {
+    tsn::DitSpec s;
+    s.B = c->B; s.La = c->La; s.Lt = c->Lt; s.H = c->H; s.NH = c->NH; s.HD = c->HD; s.F = c->F;
+    s.latent = c->latent; s.temb_dim = c->temb_dim; s.n_joint = c->n_joint; s.n_fused = c->n_fused;
+    s.audio_ffn_conv = c->audio_ffn_conv; s.rope_theta = c->rope_theta; s.t_max_period = c->t_max_period;
+    s.ln_eps = c->ln_eps; s.rms_eps = c->rms_eps;
+    return s;
+}
+
+extern "C" {
+
+const char *tsn_last_error(void) { return tsn::last_error(); }
+int tsn_version(void) { return 1; }
+
+int tsn_runtime_create(int device, tsn_runtime **out) {
+    if (!out) { tsn::set_error("null out pointer"); return TSN_ERR_ARG; }
+    *out = nullptr;
+    tsn_runtime *r = new (std::nothrow) tsn_runtime();
+    if (!r) { tsn::set_error("out of host memory"); return TSN_ERR_OOM; }
+    const int rc = r->rt.init(device);
+    if (rc != TSN_OK) { delete r; return rc; }
+    *out = r;
+    return TSN_OK;
+}
+int tsn_runtime_destroy(tsn_runtime *rt) { delete rt; return TSN_OK; }
+int tsn_alloc(tsn_runtime *rt, size_t bytes, void **dptr) { RT_CHECK(rt); return rt->rt.dev.alloc(bytes, dptr); }
+int tsn_free(tsn_runtime *rt, void *dptr) { RT_CHECK(rt); return rt->rt.dev.free(dptr); }
+int tsn_upload(tsn_runtime *rt, void *dptr, const void *src, size_t bytes) { RT_CHECK(rt); return rt->rt.dev.upload(dptr, src, bytes); }
+int tsn_download(tsn_runtime *rt, void *dst, const void *dptr, size_t bytes) { RT_CHECK(rt); return rt->rt.dev.download(dst, dptr, bytes); }
+int tsn_begin(tsn_runtime *rt) { RT_CHECK(rt); return rt->rt.dev.begin(); }
+int tsn_commit(tsn_runtime *rt) { RT_CHECK(rt); return rt->rt.dev.commit(); }
+double tsn_last_gpu_ms(tsn_runtime *rt) { return rt ? rt->rt.dev.last_gpu_ms() : -1.0; }
+int tsn_sync(tsn_runtime *rt) { RT_CHECK(rt); return rt->rt.dev.sync(); }
+
+int tsn_gemm(tsn_runtime *rt, int wdtype, const void *W, const void *X, int xdtype, void *Y, int ydtype,
+             const float *bias, uint32_t M, uint32_t N, uint32_t K, uint32_t ldx, uint32_t ldw, uint32_t ldy) {
+    RT_CHECK(rt);
+    return rt->rt.gemm(wdtype, W, X, xdtype, Y, ydtype, bias, tsn::GemmParams{M, N, K, ldx, ldw, ldy});
+}
+int tsn_gemv(tsn_runtime *rt, const void *W, int wdtype, const float *x, float *y, const float *bias, uint32_t N,
+             uint32_t K, uint32_t ldw) {
+    RT_CHECK(rt);
+    return rt->rt.gemv(W, x, y, bias, N, K, ldw, wdtype);
+}
+int tsn_conv1d_prepare(tsn_runtime *rt, const void *W, int w_bf16, void *Wp, uint32_t OC, uint32_t IC, uint32_t K) {
+    RT_CHECK(rt);
+    return rt->rt.conv_prepare(W, w_bf16, Wp, OC, IC, K);
+}
+int tsn_conv1d(tsn_runtime *rt, const void *Wp, const float *bias, const float *x, float *y, uint32_t T, uint32_t OL,
+               uint32_t IC, uint32_t OC, uint32_t K, uint32_t stride, uint32_t pad, uint32_t dil) {
+    RT_CHECK(rt);
+    return rt->rt.conv(Wp, bias, x, y, T, OL, IC, OC, K, stride, pad, dil);
+}
+int tsn_silu(tsn_runtime *rt, float *x, size_t n) { RT_CHECK(rt); return rt->rt.silu(x, n); }
+int tsn_copy(tsn_runtime *rt, const float *x, float *y, size_t n) { RT_CHECK(rt); return rt->rt.copy(x, y, n); }
+int tsn_swiglu(tsn_runtime *rt, const float *a, const float *b, float *y, size_t n) { RT_CHECK(rt); return rt->rt.swiglu(a, b, y, n); }
+int tsn_add(tsn_runtime *rt, const float *a, const float *b, float *y, size_t n) { RT_CHECK(rt); return rt->rt.add_(a, b, y, n); }
+int tsn_add_bcast_col(tsn_runtime *rt, const float *x, const float *v, float *y, uint32_t S, uint32_t H) {
+    RT_CHECK(rt);
+    return rt->rt.add_bcast_col(x, v, y, S, H);
+}
+int tsn_cfg_euler(tsn_runtime *rt, const float *fc, const float *fu, float *x, size_t n, float cfg, float dt) {
+    RT_CHECK(rt);
+    return rt->rt.cfg_euler(fc, fu, x, n, cfg, dt);
+}
+int tsn_adaln_ln(tsn_runtime *rt, const float *x, const float *mod, void *y, int ydtype, uint32_t rows, uint32_t H,
+                 uint32_t per_row, uint32_t chunks, uint32_t base, float eps) {
+    RT_CHECK(rt);
+    return rt->rt.adaln_ln(x, mod, y, ydtype, rows, H, per_row, chunks, base, eps);
+}
+int tsn_gate_add(tsn_runtime *rt, const float *x, const float *f, const float *mod, float *y, uint32_t rows, uint32_t H,
+                 uint32_t per_row, uint32_t chunks, uint32_t gate_idx) {
+    RT_CHECK(rt);
+    return rt->rt.gate_add(x, f, mod, y, rows, H, per_row, chunks, gate_idx);
+}
+int tsn_rms_head(tsn_runtime *rt, float *x, const float *w, uint32_t rows, uint32_t nh, uint32_t ld, uint32_t hd,
+                 uint32_t col_off, uint32_t row_off, float eps) {
+    RT_CHECK(rt);
+    return rt->rt.rms_head(x, w, rows, nh, ld, hd, col_off, row_off, eps);
+}
+int tsn_rope_pairs(tsn_runtime *rt, float *x, const int32_t *pos, uint32_t rows, uint32_t nh, uint32_t ld, uint32_t hd,
+                   uint32_t col_off, uint32_t row_off, float fscale, float base) {
+    RT_CHECK(rt);
+    return rt->rt.rope_pairs(x, pos, rows, nh, ld, hd, col_off, row_off, fscale, base);
+}
+int tsn_attention(tsn_runtime *rt, const float *qkv, float *out, uint32_t S, uint32_t nh, uint32_t hd, uint32_t ld,
+                  uint32_t ldo, uint32_t q_off, uint32_t k_off, uint32_t v_off, uint32_t o_off, float scale) {
+    RT_CHECK(rt);
+    return rt->rt.attention(qkv, out, S, nh, hd, ld, ldo, q_off, k_off, v_off, o_off, scale);
+}
+
+int tsn_dit_default_spec(int workload, tsn_dit_spec *out) {
+    if (!out || workload < 0 || workload > 4) { tsn::set_error("default_spec: workload must be 0..4"); return TSN_ERR_ARG; }
+    tsn_dit_spec s;
+    memset(&s, 0, sizeof s);
+    s.B = workload == 4 ? 16 : 2;
+    s.La = workload == 3 ? 960 : 256;
+    s.Lt = 141;
+    s.H = 1024; s.NH = 16; s.HD = 64; s.F = 4096;
+    s.latent = 64; s.temb_dim = 256;
+    s.n_joint = 7; s.n_fused = 14;
+    s.audio_ffn_conv = 1;
+    s.rope_theta = 10000.0f; s.t_max_period = 1.0f; s.ln_eps = 1e-5f; s.rms_eps = 1e-6f;
+    *out = s;
+    return TSN_OK;
+}
+
+int tsn_dit_manifest_count(const tsn_dit_spec *spec) {
+    if (!spec) { tsn::set_error("null spec"); return -1; }
+    return (int)tsn::dit_manifest(to_spec(spec)).size();
+}
+int tsn_dit_manifest_entry(const tsn_dit_spec *spec, int idx, char *name, int name_cap, int64_t *numel, int64_t *offset) {
+    if (!spec) { tsn::set_error("null spec"); return TSN_ERR_ARG; }
+    const auto m = tsn::dit_manifest(to_spec(spec));
+    if (idx < 0 || idx >= (int)m.size()) { tsn::set_error("manifest index out of range"); return TSN_ERR_ARG; }
+    if (name && name_cap > 0) snprintf(name, (size_t)name_cap, "%s", m[idx].name.c_str());
+    if (numel) *numel = m[idx].numel;
+    if (offset) *offset = m[idx].offset;
+    return TSN_OK;
+}
+int64_t tsn_dit_manifest_total(const tsn_dit_spec *spec) {
+    if (!spec) { tsn::set_error("null spec"); return -1; }
+    const auto m = tsn::dit_manifest(to_spec(spec));
+    return m.back().offset + m.back().numel;
+}
+
+int tsn_dit_create(tsn_runtime *rt, const tsn_dit_spec *spec, tsn_dit **out) {
+    RT_CHECK(rt);
+    if (!spec || !out) { tsn::set_error("null spec or out pointer"); return TSN_ERR_ARG; }
+    *out = nullptr;
+    tsn_dit *d = new (std::nothrow) tsn_dit();
+    if (!d) { tsn::set_error("out of host memory"); return TSN_ERR_OOM; }
+    const int rc = d->m.create(&rt->rt, to_spec(spec));
+    if (rc != TSN_OK) { delete d; return rc; }
+    *out = d;
+    return TSN_OK;
+}
+int tsn_dit_destroy(tsn_dit *dit) { delete dit; return TSN_OK; }
+int tsn_dit_upload_weights(tsn_dit *dit, const uint16_t *w, size_t numel) {
+    if (!dit) { tsn::set_error("null dit handle"); return TSN_ERR_ARG; }
+    return dit->m.upload_weights(w, numel);
+}
+int tsn_dit_forward(tsn_dit *dit, const float *z, float t, const float *text, const float *pooled, float *v) {
+    if (!dit) { tsn::set_error("null dit handle"); return TSN_ERR_ARG; }
+    tsn::DitModel &m = dit->m;
+    std::vector<float> th((size_t)m.s.B, t);
+    TSN_TRY(m.rt->dev.upload(m.t_dev, th.data(), th.size() * 4));
+    return m.enqueue_forward(z, m.t_dev, text, pooled, v, nullptr);
+}
+int tsn_dit_forward_ex(tsn_dit *dit, const float *z, const float *t, const float *text, const float *pooled, float *v,
+                       float *taps) {
+    if (!dit) { tsn::set_error("null dit handle"); return TSN_ERR_ARG; }
+    return dit->m.enqueue_forward(z, t, text, pooled, v, taps);
+}
+int tsn_dit_joint_block(tsn_dit *dit, int block, float *X, const float *g) {
+    if (!dit) { tsn::set_error("null dit handle"); return TSN_ERR_ARG; }
+    return dit->m.enqueue_joint_block(block, X, g);
+}
+int tsn_dit_fused_block(tsn_dit *dit, int block, float *X, const float *g) {
+    if (!dit) { tsn::set_error("null dit handle"); return TSN_ERR_ARG; }
+    return dit->m.enqueue_fused_block(block, X, g);
+}
+int tsn_dit_sample(tsn_dit *dit, float *x, const float *text, const float *pooled, int steps, float cfg) {
+    if (!dit) { tsn::set_error("null dit handle"); return TSN_ERR_ARG; }
+    TSN_TRY(dit->m.prepare_sample(steps));
+    return dit->m.enqueue_sample(x, text, pooled, steps, cfg);
+}
+int tsn_dit_capture_forward(tsn_dit *dit, const float *z, const float *t, const float *text, const float *pooled, float *v) {
+    if (!dit) { tsn::set_error("null dit handle"); return TSN_ERR_ARG; }
+    return dit->m.capture_forward(z, t, text, pooled, v);
+}
+int tsn_dit_capture_sample(tsn_dit *dit, float *x, const float *text, const float *pooled, int steps, float cfg) {
+    if (!dit) { tsn::set_error("null dit handle"); return TSN_ERR_ARG; }
+    return dit->m.capture_sample(x, text, pooled, steps, cfg);
+}
+int tsn_dit_replay(tsn_dit *dit) {
+    if (!dit) { tsn::set_error("null dit handle"); return TSN_ERR_ARG; }
+    return dit->m.replay();
+}
+
+int tsn_synth_normal_f32(uint64_t seed, uint64_t index, double mean, double std, size_t n, float *out) {
+    if (!out && n) { tsn::set_error("null output"); return TSN_ERR_ARG; }
+    tsn::synth_normal_f32(seed, index, mean, std, n, out);
+    return TSN_OK;
+}
+int tsn_synth_normal_bf16(uint64_t seed, uint64_t index, double mean, double std, size_t n, uint16_t *out) {
+    if (!out && n) { tsn::set_error("null output"); return TSN_ERR_ARG; }
+    tsn::synth_normal_bf16(seed, index, mean, std, n, out);
+    return TSN_OK;
+}
+int tsn_synth_uniform_f32(uint64_t seed, uint64_t index, double lo, double hi, size_t n, float *out) {
+    if (!out && n) { tsn::set_error("null output"); return TSN_ERR_ARG; }
+    tsn::synth_uniform_f32(seed, index, lo, hi, n, out);
+    return TSN_OK;
+}
+int tsn_dit_synth_weights(const tsn_dit_spec *spec, uint64_t seed, double norm_mean, uint16_t *out) {
+    if (!spec || !out) { tsn::set_error("null spec or output"); return TSN_ERR_ARG; }
+    const auto m = tsn::dit_manifest(to_spec(spec));
+    for (size_t i = 0; i < m.size(); ++i) {
+        const bool is_norm = m[i].name.find("norm.weight") != std::string::npos;
+        tsn::synth_normal_bf16(seed, (uint64_t)i, is_norm ? norm_mean : 0.0, 0.02, (size_t)m[i].numel, out + m[i].offset);
+    }
+    return TSN_OK;
+}
+
+} // extern "C"

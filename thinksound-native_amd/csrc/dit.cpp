@@ -1,0 +1,536 @@
+// dit.cpp — DitModel on HIP: weight upload, one velocity evaluation, the CFG Euler sampler.
+//
+// Per evaluation (B samples folded into GEMM rows; src/dit_fwd.cpp:104-304 for the reference
+// sequence):
+//   1 sinusoid -> 2 GEMVs (t-MLP; + pooled -> g, silu(g)) -> 1 GEMV for every adaLN modulation
+//   input projection (f32) + text rows copy
+//   per joint block: LN(both streams) | QKV (2 problems; RMS+RoPE epilogue) | flash attention |
+//                    out-proj (2 problems; gated residual) | LN | FFN1 (conv k3 + linear; SiLU) |
+//                    FFN2 (conv k3 + linear; gated residual)                        = 7 launches
+//   per fused block: the same 7 launches with one problem each
+//   final LN (f32 out) + output projection (f32)
+#include "dit.h"
+
+#include <math.h>
+#include <string.h>
+
+#include <map>
+
+namespace tsn {
+
+std::vector<ManifestEntry> dit_manifest(const DitSpec &s) {
+    std::vector<ManifestEntry> v;
+    const int64_t H = s.H, F = s.F, HD = s.HD;
+    int64_t off = 0;
+    auto add = [&](const std::string &n, int64_t numel) {
+        v.push_back({n, numel, off});
+        off += numel;
+    };
+    add("t_embed.mlp.0.weight", H * s.temb_dim);
+    add("t_embed.mlp.0.bias", H);
+    add("t_embed.mlp.2.weight", H * H);
+    add("t_embed.mlp.2.bias", H);
+    add("audio_input_proj.weight", H * s.latent);
+    add("audio_input_proj.bias", H);
+    auto block = [&](const std::string &p, int64_t taps) {
+        add(p + ".adaLN_modulation.1.weight", 6 * H * H);
+        add(p + ".adaLN_modulation.1.bias", 6 * H);
+        add(p + ".attn.qkv.weight", 3 * H * H);
+        add(p + ".attn.qkv.bias", 3 * H);
+        add(p + ".attn.q_norm.weight", HD);
+        add(p + ".attn.k_norm.weight", HD);
+        add(p + ".linear1.weight", H * H);
+        add(p + ".linear1.bias", H);
+        add(p + ".ffn.w1.weight", F * H * taps);
+        add(p + ".ffn.w2.weight", H * F * taps);
+    };
+    for (int i = 0; i < s.n_joint; ++i) {
+        block("joint_blocks." + std::to_string(i) + ".latent_block", s.audio_ffn_conv ? 3 : 1);
+        block("joint_blocks." + std::to_string(i) + ".text_block", 1);
+    }
+    for (int i = 0; i < s.n_fused; ++i) block("fused_blocks." + std::to_string(i), 1);
+    add("final_layer.adaLN_modulation.1.weight", 2 * H * H);
+    add("final_layer.adaLN_modulation.1.bias", 2 * H);
+    add("final_layer.linear.weight", (int64_t)s.latent * H);
+    add("final_layer.linear.bias", s.latent);
+    return v;
+}
+
+int dit_spec_check(const DitSpec &s) {
+    TSN_REQUIRE(s.B == 1 || s.B == 2 || s.B == 4 || s.B == 8 || s.B == 16, "spec: B must be 1, 2, 4, 8 or 16");
+    TSN_REQUIRE(s.La > 0 && s.Lt >= 0, "spec: La > 0, Lt >= 0");
+    TSN_REQUIRE(s.HD == 64, "spec: head dim must be 64");
+    TSN_REQUIRE(s.H == s.NH * s.HD && s.H % 256 == 0 && s.H <= 2048, "spec: H = NH*64, multiple of 256, <= 2048");
+    TSN_REQUIRE(s.F % 128 == 0 && s.F > 0, "spec: F must be a multiple of 128");
+    TSN_REQUIRE(s.latent > 0 && s.latent % 8 == 0, "spec: latent must be a multiple of 8");
+    TSN_REQUIRE(s.temb_dim > 0 && s.temb_dim % 8 == 0, "spec: temb_dim must be a multiple of 8");
+    TSN_REQUIRE(s.n_joint >= 0 && s.n_fused >= 0, "spec: block counts");
+    TSN_REQUIRE(s.Lt > 0 || s.n_joint == 0, "spec: joint blocks need text rows");
+    return TSN_OK;
+}
+
+DitModel::~DitModel() {
+    if (gexec_) hipGraphExecDestroy(gexec_);
+    if (graph_) hipGraphDestroy(graph_);
+    if (rt)
+        for (void *p : owned_) rt->dev.free(p);
+}
+
+int DitModel::alloc(size_t bytes, void **p) {
+    TSN_TRY(rt->dev.alloc(bytes, p));
+    owned_.push_back(*p);
+    return TSN_OK;
+}
+
+int DitModel::create(Runtime *r, const DitSpec &sp) {
+    TSN_REQUIRE(r, "dit: null runtime");
+    TSN_TRY(dit_spec_check(sp));
+    rt = r;
+    s = sp;
+    S = s.La + s.Lt;
+    Sp = (S + 63) / 64 * 64;
+    NMOD = (2 * s.n_joint + s.n_fused) * 6 * s.H + 2 * s.H;
+    const size_t B = s.B, H = s.H;
+    auto af = [&](float **p, size_t n) { return alloc(n * sizeof(float), (void **)p); };
+    auto ah = [&](half_t **p, size_t n) { return alloc(n * sizeof(half_t), (void **)p); };
+    TSN_TRY(af(&X_, B * S * H));
+    TSN_TRY(af(&MOD_, B * NMOD));
+    TSN_TRY(af(&g_, B * H));
+    TSN_TRY(af(&gs_, B * H));
+    TSN_TRY(af(&temb_, B * s.temb_dim));
+    TSN_TRY(af(&h1_, B * H));
+    TSN_TRY(af(&XF_, B * s.La * H));
+    TSN_TRY(af(&Vv_, B * s.La * s.latent));
+    TSN_TRY(af(&x2_, B * s.La * s.latent));
+    TSN_TRY(af(&t_dev, B));
+    TSN_TRY(ah(&XN_, B * S * H));
+    TSN_TRY(ah(&Q_, B * S * H));
+    TSN_TRY(ah(&K_, B * S * H));
+    TSN_TRY(ah(&Vt_, B * s.NH * 64 * (size_t)Sp));   // zero-filled: keys >= S stay zero
+    TSN_TRY(ah(&AO_, B * S * H));
+    TSN_TRY(ah(&HF_, B * S * (size_t)s.F));
+    // RoPE table: same expression as shaders/ops_conv.metal:162-164 with fscale 1 (audio rows)
+    std::vector<float> tab((size_t)s.La * 32 * 2);
+    for (int p = 0; p < s.La; ++p)
+        for (int j = 0; j < 32; ++j) {
+            const float inv = powf(s.rope_theta, -2.0f * (float)j / (float)s.HD);
+            const float ang = (float)p * 1.0f * inv;
+            tab[((size_t)p * 32 + j) * 2] = cosf(ang);
+            tab[((size_t)p * 32 + j) * 2 + 1] = sinf(ang);
+        }
+    TSN_TRY(af(&rope_, tab.size()));
+    TSN_TRY(rt->dev.upload(rope_, tab.data(), tab.size() * sizeof(float)));
+    return TSN_OK;
+}
+
+int DitModel::upload_weights(const uint16_t *host, size_t numel) {
+    TSN_REQUIRE(rt && host, "dit: not created / null weights");
+    const auto man = dit_manifest(s);
+    const size_t total = (size_t)(man.back().offset + man.back().numel);
+    TSN_REQUIRE(numel == total, "dit: weight count does not match the manifest (" + std::to_string(total) + ")");
+    TSN_TRY(alloc(total * 2, &wraw_));
+    TSN_TRY(rt->dev.upload(wraw_, host, total * 2));
+    std::map<std::string, const ManifestEntry *> idx;
+    for (const auto &e : man) idx[e.name] = &e;
+    const hipStream_t st = rt->dev.stream();
+    auto raw = [&](const std::string &n) -> const uint16_t * {
+        return (const uint16_t *)wraw_ + idx.at(n)->offset;
+    };
+    auto numel_of = [&](const std::string &n) { return (size_t)idx.at(n)->numel; };
+    auto f16 = [&](const std::string &n, const half_t **out) -> int {
+        half_t *p;
+        TSN_TRY(alloc(numel_of(n) * 2, (void **)&p));
+        TSN_TRY(launch_bf16_to_f16(raw(n), p, numel_of(n), st));
+        *out = p;
+        return TSN_OK;
+    };
+    auto f32 = [&](const std::string &n, const float **out) -> int {
+        float *p;
+        TSN_TRY(alloc(numel_of(n) * 4, (void **)&p));
+        TSN_TRY(launch_bf16_to_f32(raw(n), p, numel_of(n), st));
+        *out = p;
+        return TSN_OK;
+    };
+    auto convw = [&](const std::string &n, int OC, int IC, const half_t **out) -> int {
+        half_t *p;
+        TSN_TRY(alloc(numel_of(n) * 2, (void **)&p));
+        TSN_TRY(launch_conv_weight_reorder(raw(n), 1, p, OC, IC, 3, st));
+        *out = p;
+        return TSN_OK;
+    };
+    const size_t H = s.H;
+    uint16_t *wmod;
+    TSN_TRY(alloc((size_t)NMOD * H * 2, (void **)&wmod));
+    float *bmod;
+    TSN_TRY(alloc((size_t)NMOD * 4, (void **)&bmod));
+    int mod_row = 0;
+    auto stream = [&](const std::string &p, bool conv, StreamW &w) -> int {
+        w.mod_off = mod_row;
+        TSN_TRY(rt->dev.copy_d2d(wmod + (size_t)mod_row * H, raw(p + ".adaLN_modulation.1.weight"), 6 * H * H * 2));
+        TSN_TRY(launch_bf16_to_f32(raw(p + ".adaLN_modulation.1.bias"), bmod + mod_row, 6 * H, st));
+        mod_row += 6 * (int)H;
+        TSN_TRY(f16(p + ".attn.qkv.weight", &w.Wqkv));
+        TSN_TRY(f32(p + ".attn.qkv.bias", &w.bqkv));
+        TSN_TRY(f32(p + ".attn.q_norm.weight", &w.qn));
+        TSN_TRY(f32(p + ".attn.k_norm.weight", &w.kn));
+        TSN_TRY(f16(p + ".linear1.weight", &w.Wo));
+        TSN_TRY(f32(p + ".linear1.bias", &w.bo));
+        w.conv = conv ? 1 : 0;
+        if (conv) {
+            TSN_TRY(convw(p + ".ffn.w1.weight", s.F, s.H, &w.W1));
+            TSN_TRY(convw(p + ".ffn.w2.weight", s.H, s.F, &w.W2));
+        } else {
+            TSN_TRY(f16(p + ".ffn.w1.weight", &w.W1));
+            TSN_TRY(f16(p + ".ffn.w2.weight", &w.W2));
+        }
+        return TSN_OK;
+    };
+    ja_.assign(s.n_joint, StreamW{});
+    jt_.assign(s.n_joint, StreamW{});
+    fu_.assign(s.n_fused, StreamW{});
+    for (int i = 0; i < s.n_joint; ++i) {
+        TSN_TRY(stream("joint_blocks." + std::to_string(i) + ".latent_block", s.audio_ffn_conv != 0, ja_[i]));
+        TSN_TRY(stream("joint_blocks." + std::to_string(i) + ".text_block", false, jt_[i]));
+    }
+    for (int i = 0; i < s.n_fused; ++i) TSN_TRY(stream("fused_blocks." + std::to_string(i), false, fu_[i]));
+    fin_mod_off_ = mod_row;
+    TSN_TRY(rt->dev.copy_d2d(wmod + (size_t)mod_row * H, raw("final_layer.adaLN_modulation.1.weight"), 2 * H * H * 2));
+    TSN_TRY(launch_bf16_to_f32(raw("final_layer.adaLN_modulation.1.bias"), bmod + mod_row, 2 * H, st));
+    Wmod_ = wmod;
+    bmod_ = bmod;
+    // GEMV / f32-linear weights are read as bf16 straight from the uploaded buffer
+    Wt0_ = raw("t_embed.mlp.0.weight");
+    Wt2_ = raw("t_embed.mlp.2.weight");
+    Win_ = raw("audio_input_proj.weight");
+    Wfin_ = raw("final_layer.linear.weight");
+    TSN_TRY(f32("t_embed.mlp.0.bias", &bt0_));
+    TSN_TRY(f32("t_embed.mlp.2.bias", &bt2_));
+    TSN_TRY(f32("audio_input_proj.bias", &bin_));
+    TSN_TRY(f32("final_layer.linear.bias", &bfin_));
+    TSN_TRY(rt->dev.sync());
+    ready_ = true;
+    return TSN_OK;
+}
+
+int DitModel::modulation(const float *gs, int row0, int rows) {
+    GemvArgs a;
+    memset(&a, 0, sizeof a);
+    a.W = Wmod_ + (size_t)row0 * s.H; a.ldw = s.H; a.wdt = DT_BF16;
+    a.X = gs; a.ldx = s.H;
+    a.Y = MOD_ + row0; a.ldy = NMOD;
+    a.bias = bmod_ + row0;
+    a.N = rows; a.K = s.H; a.nb = s.B;
+    return launch_gemv(a, rt->dev.stream());
+}
+
+int DitModel::gs_from_g(const float *g) {
+    const hipStream_t st = rt->dev.stream();
+    TSN_TRY(launch_copy(g, gs_, (size_t)s.B * s.H, st));
+    return launch_silu(gs_, (size_t)s.B * s.H, st);
+}
+
+namespace {
+
+void qkv_problem(GemmProblem &p, const half_t *A, RowMap amap, int M, const half_t *W, const float *bias,
+                 const float *qn, const float *kn, int H, int nh, half_t *Q, half_t *K, half_t *Vt, int S, int Sp,
+                 int q_L, int q_soff, int rope_len, const float *rope, float eps) {
+    gemm_problem_init(p);
+    p.A = A; p.lda = H; p.amap = amap; p.taps = 1; p.Kc = H; p.pad = 0; p.a_T = amap.L;
+    p.W = W; p.ldw = H; p.bias = bias; p.M = M; p.N = 3 * H; p.K = H;
+    p.Q = Q; p.Kd = K; p.Vt = Vt; p.S_att = S; p.Sp = Sp; p.nh = nh; p.Hq = H;
+    p.q_L = q_L; p.q_soff = q_soff; p.rope_len = rope_len; p.rope = rope;
+    p.qn = qn; p.kn = kn; p.rms_eps = eps; p.q_scale = 0.125f;   // 1/sqrt(64), exact in f16
+}
+
+void resid_problem(GemmProblem &p, const half_t *A, int lda, RowMap amap, int taps, int Kc, int M, int N,
+                   const half_t *W, const float *bias, float *R, int ldr, const float *gate, int gate_ld) {
+    gemm_problem_init(p);
+    p.A = A; p.lda = lda; p.amap = amap; p.taps = taps; p.Kc = Kc; p.pad = taps / 2; p.a_T = amap.L;
+    p.W = W; p.ldw = taps * Kc; p.bias = bias; p.M = M; p.N = N; p.K = taps * Kc;
+    p.R = R; p.ldr = ldr; p.rmap = amap; p.gate = gate; p.gate_ld = gate_ld; p.gate_L = amap.L;
+}
+
+void store_problem(GemmProblem &p, const half_t *A, int lda, RowMap amap, int taps, int Kc, int M, int N,
+                   const half_t *W, half_t *Y, int ldy, int silu) {
+    gemm_problem_init(p);
+    p.A = A; p.lda = lda; p.amap = amap; p.taps = taps; p.Kc = Kc; p.pad = taps / 2; p.a_T = amap.L;
+    p.W = W; p.ldw = taps * Kc; p.bias = nullptr; p.M = M; p.N = N; p.K = taps * Kc;
+    p.Y = Y; p.ldy = ldy; p.ymap = amap; p.y_f16 = 1; p.silu = silu;
+}
+
+void ln_seg(LnSeg &g, const float *X, int H, RowMap map, half_t *Y, const float *mod, int nmod, int L,
+            int shift_off, int rows) {
+    g.X = X; g.ldx = H; g.xmap = map;
+    g.Y = Y; g.ldy = H; g.ymap = map;
+    g.mod = mod; g.mod_ld = nmod; g.mod_L = L; g.shift_off = shift_off; g.scale_off = shift_off + H;
+    g.rows = rows;
+}
+
+} // namespace
+
+// Joint block: src/dit_fwd.cpp:180-257 (pre_attn :24-49, attention :83-102, post_attn :51-81)
+int DitModel::block_joint(int i) {
+    const hipStream_t st = rt->dev.stream();
+    const StreamW &a = ja_[i], &t = jt_[i];
+    const int B = s.B, H = s.H, La = s.La, Lt = s.Lt;
+    const RowMap Sa{La, S, 0}, St{Lt, S, La};
+    LnArgs ln;
+    memset(&ln, 0, sizeof ln);
+    ln.nseg = 2; ln.H = H; ln.eps = s.ln_eps;
+    ln_seg(ln.seg[0], X_, H, Sa, XN_, MOD_, NMOD, La, a.mod_off, B * La);
+    ln_seg(ln.seg[1], X_, H, St, XN_, MOD_, NMOD, Lt, t.mod_off, B * Lt);
+    TSN_TRY(launch_ln_mod(ln, true, st));
+
+    GemmBatch qb;
+    qb.nprob = 2;
+    qkv_problem(qb.p[0], XN_, Sa, B * La, a.Wqkv, a.bqkv, a.qn, a.kn, H, s.NH, Q_, K_, Vt_, S, Sp, La, 0, La, rope_, s.rms_eps);
+    qkv_problem(qb.p[1], XN_, St, B * Lt, t.Wqkv, t.bqkv, t.qn, t.kn, H, s.NH, Q_, K_, Vt_, S, Sp, Lt, La, 0, rope_, s.rms_eps);
+    TSN_TRY(launch_gemm(qb, EPI_QKV, false, st));
+
+    AttnArgs at;
+    memset(&at, 0, sizeof at);
+    at.Q = Q_; at.K = K_; at.Vt = Vt_; at.S = S; at.Sp = Sp; at.nh = s.NH; at.BH = B * s.NH;
+    at.O = AO_; at.o_f32 = 0; at.ldo = H; at.omap = rowmap_dense(B * S);
+    at.scale_log2 = 1.4426950408889634f;
+    TSN_TRY(launch_attention(at, st));
+
+    GemmBatch ob;
+    ob.nprob = 2;
+    resid_problem(ob.p[0], AO_, H, Sa, 1, H, B * La, H, a.Wo, a.bo, X_, H, MOD_ + a.mod_off + 2 * H, NMOD);
+    resid_problem(ob.p[1], AO_, H, St, 1, H, B * Lt, H, t.Wo, t.bo, X_, H, MOD_ + t.mod_off + 2 * H, NMOD);
+    TSN_TRY(launch_gemm(ob, EPI_RESID, false, st));
+
+    ln_seg(ln.seg[0], X_, H, Sa, XN_, MOD_, NMOD, La, a.mod_off + 3 * H, B * La);
+    ln_seg(ln.seg[1], X_, H, St, XN_, MOD_, NMOD, Lt, t.mod_off + 3 * H, B * Lt);
+    TSN_TRY(launch_ln_mod(ln, true, st));
+
+    const int ta = a.conv ? 3 : 1;
+    GemmBatch f1;
+    f1.nprob = 2;
+    store_problem(f1.p[0], XN_, H, Sa, ta, H, B * La, s.F, a.W1, HF_, s.F, 1);
+    store_problem(f1.p[1], XN_, H, St, 1, H, B * Lt, s.F, t.W1, HF_, s.F, 1);
+    TSN_TRY(launch_gemm(f1, EPI_STORE, false, st));
+
+    GemmBatch f2;
+    f2.nprob = 2;
+    resid_problem(f2.p[0], HF_, s.F, Sa, ta, s.F, B * La, H, a.W2, nullptr, X_, H, MOD_ + a.mod_off + 5 * H, NMOD);
+    resid_problem(f2.p[1], HF_, s.F, St, 1, s.F, B * Lt, H, t.W2, nullptr, X_, H, MOD_ + t.mod_off + 5 * H, NMOD);
+    return launch_gemm(f2, EPI_RESID, false, st);
+}
+
+// Fused block: src/dit_fwd.cpp:267-279 over the joined rows
+int DitModel::block_fused(int i) {
+    const hipStream_t st = rt->dev.stream();
+    const StreamW &w = fu_[i];
+    const int B = s.B, H = s.H, M = B * S;
+    const RowMap D{S, S, 0};
+    LnArgs ln;
+    memset(&ln, 0, sizeof ln);
+    ln.nseg = 1; ln.H = H; ln.eps = s.ln_eps;
+    ln_seg(ln.seg[0], X_, H, D, XN_, MOD_, NMOD, S, w.mod_off, M);
+    TSN_TRY(launch_ln_mod(ln, true, st));
+
+    GemmBatch qb;
+    qb.nprob = 1;
+    qkv_problem(qb.p[0], XN_, D, M, w.Wqkv, w.bqkv, w.qn, w.kn, H, s.NH, Q_, K_, Vt_, S, Sp, S, 0, s.La, rope_, s.rms_eps);
+    TSN_TRY(launch_gemm(qb, EPI_QKV, false, st));
+
+    AttnArgs at;
+    memset(&at, 0, sizeof at);
+    at.Q = Q_; at.K = K_; at.Vt = Vt_; at.S = S; at.Sp = Sp; at.nh = s.NH; at.BH = B * s.NH;
+    at.O = AO_; at.o_f32 = 0; at.ldo = H; at.omap = rowmap_dense(M);
+    at.scale_log2 = 1.4426950408889634f;
+    TSN_TRY(launch_attention(at, st));
+
+    GemmBatch ob;
+    ob.nprob = 1;
+    resid_problem(ob.p[0], AO_, H, D, 1, H, M, H, w.Wo, w.bo, X_, H, MOD_ + w.mod_off + 2 * H, NMOD);
+    TSN_TRY(launch_gemm(ob, EPI_RESID, false, st));
+
+    ln_seg(ln.seg[0], X_, H, D, XN_, MOD_, NMOD, S, w.mod_off + 3 * H, M);
+    TSN_TRY(launch_ln_mod(ln, true, st));
+
+    GemmBatch f1;
+    f1.nprob = 1;
+    store_problem(f1.p[0], XN_, H, D, 1, H, M, s.F, w.W1, HF_, s.F, 1);
+    TSN_TRY(launch_gemm(f1, EPI_STORE, false, st));
+
+    GemmBatch f2;
+    f2.nprob = 1;
+    resid_problem(f2.p[0], HF_, s.F, D, 1, s.F, M, H, w.W2, nullptr, X_, H, MOD_ + w.mod_off + 5 * H, NMOD);
+    return launch_gemm(f2, EPI_RESID, false, st);
+}
+
+int DitModel::enqueue_forward(const float *z, const float *t, const float *text, const float *pooled, float *v,
+                              float *taps) {
+    TSN_REQUIRE(ready_, "dit: weights not uploaded");
+    TSN_REQUIRE(z && t && pooled && v && (text || s.Lt == 0), "dit forward: null input");
+    TSN_TRY(rt->dev.make_current());
+    const hipStream_t st = rt->dev.stream();
+    const int B = s.B, H = s.H;
+    // timestep embedding + MLP, g = t_emb + pooled, gs = silu(g)   (src/dit_fwd.cpp:111-140)
+    TSN_TRY(launch_temb_sinusoid(t, temb_, B, s.temb_dim, s.t_max_period, st));
+    GemvArgs g1;
+    memset(&g1, 0, sizeof g1);
+    g1.W = Wt0_; g1.ldw = s.temb_dim; g1.wdt = DT_BF16; g1.X = temb_; g1.ldx = s.temb_dim;
+    g1.Y = h1_; g1.ldy = H; g1.bias = bt0_; g1.N = H; g1.K = s.temb_dim; g1.nb = B; g1.silu = 1;
+    TSN_TRY(launch_gemv(g1, st));
+    GemvArgs g2;
+    memset(&g2, 0, sizeof g2);
+    g2.W = Wt2_; g2.ldw = H; g2.wdt = DT_BF16; g2.X = h1_; g2.ldx = H;
+    g2.Y = g_; g2.ldy = H; g2.bias = bt2_; g2.addv = pooled; g2.ld_add = H; g2.Y2 = gs_; g2.ldy2 = H;
+    g2.N = H; g2.K = H; g2.nb = B;
+    TSN_TRY(launch_gemv(g2, st));
+    // every adaLN modulation of the eval in one HBM-bound GEMV (src/dit_fwd.cpp:186-207,271-274,288-291)
+    TSN_TRY(modulation(gs_, 0, NMOD));
+    // input projection and the text stream start (src/dit_fwd.cpp:142-149,166-167)
+    LinArgs li;
+    memset(&li, 0, sizeof li);
+    li.X = z; li.ldx = s.latent; li.xmap = rowmap_dense(B * s.La);
+    li.W = Win_; li.ldw = s.latent; li.wdt = DT_BF16; li.bias = bin_;
+    li.Y = X_; li.ldy = H; li.ymap = RowMap{s.La, S, 0};
+    li.M = B * s.La; li.N = H; li.K = s.latent;
+    TSN_TRY(launch_linear_f32(li, st));
+    if (s.Lt > 0)
+        TSN_TRY(launch_copy_rows(text, H, rowmap_dense(B * s.Lt), X_, H, RowMap{s.Lt, S, s.La}, B * s.Lt, H, st));
+    const size_t tap_n = (size_t)B * S * H;
+    int tap = 0;
+    for (int i = 0; i < s.n_joint; ++i) {
+        TSN_TRY(block_joint(i));
+        if (taps) TSN_TRY(rt->dev.copy_d2d(taps + tap_n * tap++, X_, tap_n * 4));
+    }
+    for (int i = 0; i < s.n_fused; ++i) {
+        TSN_TRY(block_fused(i));
+        if (taps) TSN_TRY(rt->dev.copy_d2d(taps + tap_n * tap++, X_, tap_n * 4));
+    }
+    // final layer: adaLN (2 chunks) on audio rows, projection to latent (src/dit_fwd.cpp:287-303)
+    LnArgs ln;
+    memset(&ln, 0, sizeof ln);
+    ln.nseg = 1; ln.H = H; ln.eps = s.ln_eps;
+    LnSeg &g = ln.seg[0];
+    g.X = X_; g.ldx = H; g.xmap = RowMap{s.La, S, 0};
+    g.Y = XF_; g.ldy = H; g.ymap = rowmap_dense(B * s.La);
+    g.mod = MOD_; g.mod_ld = NMOD; g.mod_L = s.La; g.shift_off = fin_mod_off_; g.scale_off = fin_mod_off_ + H;
+    g.rows = B * s.La;
+    TSN_TRY(launch_ln_mod(ln, false, st));
+    LinArgs lo;
+    memset(&lo, 0, sizeof lo);
+    lo.X = XF_; lo.ldx = H; lo.xmap = rowmap_dense(B * s.La);
+    lo.W = Wfin_; lo.ldw = H; lo.wdt = DT_BF16; lo.bias = bfin_;
+    lo.Y = v; lo.ldy = s.latent; lo.ymap = rowmap_dense(B * s.La);
+    lo.M = B * s.La; lo.N = s.latent; lo.K = H;
+    return launch_linear_f32(lo, st);
+}
+
+int DitModel::enqueue_joint_block(int block, float *X, const float *g) {
+    TSN_REQUIRE(ready_, "dit: weights not uploaded");
+    TSN_REQUIRE(block >= 0 && block < s.n_joint && X && g, "dit joint block: arguments");
+    TSN_TRY(rt->dev.make_current());
+    const size_t n = (size_t)s.B * S * s.H;
+    TSN_TRY(gs_from_g(g));
+    TSN_TRY(modulation(gs_, ja_[block].mod_off, 12 * s.H));
+    TSN_TRY(rt->dev.copy_d2d(X_, X, n * 4));
+    TSN_TRY(block_joint(block));
+    return rt->dev.copy_d2d(X, X_, n * 4);
+}
+
+int DitModel::enqueue_fused_block(int block, float *X, const float *g) {
+    TSN_REQUIRE(ready_, "dit: weights not uploaded");
+    TSN_REQUIRE(block >= 0 && block < s.n_fused && X && g, "dit fused block: arguments");
+    TSN_TRY(rt->dev.make_current());
+    const size_t n = (size_t)s.B * S * s.H;
+    TSN_TRY(gs_from_g(g));
+    TSN_TRY(modulation(gs_, fu_[block].mod_off, 6 * s.H));
+    TSN_TRY(rt->dev.copy_d2d(X_, X, n * 4));
+    TSN_TRY(block_fused(block));
+    return rt->dev.copy_d2d(X, X_, n * 4);
+}
+
+// src/pipeline.cpp:141-155: t_s = 1 - s/steps, dt = t_{s+1} - t_s, two arms then cfg_euler
+int DitModel::enqueue_sample(float *x, const float *text, const float *pooled, int steps, float cfg) {
+    TSN_REQUIRE(ready_, "dit: weights not uploaded");
+    TSN_REQUIRE(x && pooled && (text || s.Lt == 0) && steps > 0, "dit sample: arguments");
+    TSN_REQUIRE(s.B % 2 == 0, "dit sample: B must be even (cond/uncond pairs)");
+    TSN_REQUIRE(tsched_ && tsched_steps_ == steps, "dit sample: schedule not prepared for this step count");
+    const int P = s.B / 2;
+    const size_t n = (size_t)s.La * s.latent;
+    for (int b = 0; b < s.B; ++b) TSN_TRY(rt->dev.copy_d2d(x2_ + b * n, x + (b / 2) * n, n * 4));
+    for (int st = 0; st < steps; ++st) {
+        const float t_curr = 1.0f - (float)st / (float)steps;
+        const float t_prev = 1.0f - (float)(st + 1) / (float)steps;
+        TSN_TRY(enqueue_forward(x2_, tsched_ + (size_t)st * s.B, text, pooled, Vv_, nullptr));
+        TSN_TRY(launch_cfg_euler_pairs(Vv_, x2_, P, (int)n, cfg, t_prev - t_curr, rt->dev.stream()));
+    }
+    for (int p = 0; p < P; ++p) TSN_TRY(rt->dev.copy_d2d(x + p * n, x2_ + 2 * p * n, n * 4));
+    return TSN_OK;
+}
+
+namespace {
+int prepare_schedule(Runtime *rt, int B, int steps, float **tsched, int *have, std::vector<void *> &owned) {
+    if (*tsched && *have == steps) return TSN_OK;
+    if (*tsched) {
+        TSN_TRY(rt->dev.free(*tsched));
+        for (auto it = owned.begin(); it != owned.end(); ++it)
+            if (*it == *tsched) { owned.erase(it); break; }
+        *tsched = nullptr;
+    }
+    std::vector<float> h((size_t)steps * B);
+    for (int st = 0; st < steps; ++st)
+        for (int b = 0; b < B; ++b) h[(size_t)st * B + b] = 1.0f - (float)st / (float)steps;
+    TSN_TRY(rt->dev.alloc(h.size() * 4, (void **)tsched));
+    owned.push_back(*tsched);
+    TSN_TRY(rt->dev.upload(*tsched, h.data(), h.size() * 4));
+    *have = steps;
+    return TSN_OK;
+}
+} // namespace
+
+int DitModel::capture_forward(const float *z, const float *t, const float *text, const float *pooled, float *v) {
+    TSN_REQUIRE(ready_, "dit: weights not uploaded");
+    TSN_TRY(rt->dev.make_current());
+    if (gexec_) { hipGraphExecDestroy(gexec_); gexec_ = nullptr; }
+    if (graph_) { hipGraphDestroy(graph_); graph_ = nullptr; }
+    const hipStream_t st = rt->dev.stream();
+    TSN_HIP_CHECK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    const int rc = enqueue_forward(z, t, text, pooled, v, nullptr);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(st, &g);
+    if (rc != TSN_OK) { if (g) hipGraphDestroy(g); return rc; }
+    TSN_HIP_CHECK(e);
+    graph_ = g;
+    TSN_HIP_CHECK(hipGraphInstantiate(&gexec_, graph_, nullptr, nullptr, 0));
+    return TSN_OK;
+}
+
+int DitModel::capture_sample(float *x, const float *text, const float *pooled, int steps, float cfg) {
+    TSN_REQUIRE(ready_, "dit: weights not uploaded");
+    TSN_TRY(rt->dev.make_current());
+    TSN_TRY(prepare_sample(steps));
+    if (gexec_) { hipGraphExecDestroy(gexec_); gexec_ = nullptr; }
+    if (graph_) { hipGraphDestroy(graph_); graph_ = nullptr; }
+    const hipStream_t st = rt->dev.stream();
+    TSN_HIP_CHECK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    const int rc = enqueue_sample(x, text, pooled, steps, cfg);
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(st, &g);
+    if (rc != TSN_OK) { if (g) hipGraphDestroy(g); return rc; }
+    TSN_HIP_CHECK(e);
+    graph_ = g;
+    TSN_HIP_CHECK(hipGraphInstantiate(&gexec_, graph_, nullptr, nullptr, 0));
+    return TSN_OK;
+}
+
+int DitModel::replay() {
+    TSN_REQUIRE(gexec_, "dit: no captured graph");
+    TSN_TRY(rt->dev.make_current());
+    TSN_HIP_CHECK(hipGraphLaunch(gexec_, rt->dev.stream()));
+    return TSN_OK;
+}
+
+int DitModel::prepare_sample(int steps) {
+    TSN_REQUIRE(steps > 0, "dit sample: steps must be positive");
+    TSN_TRY(rt->dev.make_current());
+    return prepare_schedule(rt, s.B, steps, &tsched_, &tsched_steps_, owned_);
+}
+
+} // namespace tsn

@@ -1,0 +1,136 @@
+// kernels.h — argument blocks and launch functions of the gfx950 kernels.
+// Every launch function checks the shapes its kernel assumes and returns a TSN_* status; the
+// kernels themselves carry no bounds checks beyond the tails they are written for.
+#pragma once
+#include "tsn_common.h"
+
+namespace tsn {
+
+/* ------------------------------------------------------------------ GEMM (MFMA) */
+// C[M,N] = A[M,K] · W[N,K]ᵀ with f16 operands and f32 accumulation; 128x128x64 tiles,
+// 4 waves (2x2, 64x64 per wave), v_mfma_f32_16x16x32_f16, LDS double-buffered.
+enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2 };
+
+struct GemmProblem {
+    // A operand rows (f16, or f32 converted on load): row m -> rowmap_phys(amap, m).
+    const void *A; int lda; RowMap amap;
+    // Convolution view of K: K = taps*Kc; column k reads channel k % Kc of source row
+    // t - pad + k / Kc of the same sample, zero outside [0, a_T). taps = 1, pad = 0 is a GEMM.
+    int taps, Kc, pad, a_T;
+    const half_t *W; int ldw;          // [N][K] row-major
+    const float *bias;                 // [N] or null
+    int M, N, K;
+    // EPI_STORE: Y[ymap(m)*ldy + n] = act(acc + bias), f16 or f32
+    void *Y; int ldy; RowMap ymap; int y_f16; int silu;
+    // EPI_RESID: R[rmap(m)*ldr + n] += gate[(m / gate_L)*gate_ld + n] * (acc + bias)
+    float *R; int ldr; RowMap rmap; const float *gate; int gate_ld; int gate_L;
+    // EPI_QKV: columns [0,Hq) q, [Hq,2Hq) k, [2Hq,3Hq) v; heads of hd = 64 columns.
+    // Row m -> sample b = m / q_L, position s = q_soff + m % q_L.
+    // q, k: per-head RMSNorm (weights qn/kn), RoPE for (m % q_L) < rope_len, q *= q_scale;
+    // stored to Q/Kd [b][h][S_att][64]; v stored transposed to Vt [b][h][64][Sp].
+    half_t *Q, *Kd, *Vt; int S_att, Sp, nh, Hq, q_L, q_soff, rope_len;
+    const float *qn, *kn; float rms_eps, q_scale;
+    const float *rope;                 // [pos][32][2] (cos, sin)
+    // filled by the launcher
+    int tile_start, tiles_m, tiles_n;
+};
+
+struct GemmBatch {
+    GemmProblem p[2];
+    int nprob;
+    int total_tiles;
+};
+
+// a_f32: A operand is f32 (converted to f16 on load). All problems share the epilogue kind.
+int launch_gemm(GemmBatch &b, int epi, bool a_f32, hipStream_t st);
+void gemm_problem_init(GemmProblem &p);
+
+/* ------------------------------------------------------------------ attention */
+// Flash attention, hd = 64, non-causal, no mask. Q/K [BH][S][64] f16, Vt [BH][64][Sp] f16
+// (keys >= S of Vt must hold finite values; the library keeps them zero).
+// O row for (b, s) is rowmap_phys(omap, b*S + s); head h writes columns h*64..h*64+63.
+struct AttnArgs {
+    const half_t *Q, *K, *Vt;
+    int S, Sp, nh, BH;
+    void *O; int o_f32; int ldo; RowMap omap;
+    float scale_log2;   // softmax scale * log2(e)
+};
+int launch_attention(const AttnArgs &a, hipStream_t st);
+
+// Pack f32 q/k/v column slices of a [S, ld] buffer into Q/K [nh][S][64] and Vt [nh][64][Sp]
+// (f16; Vt keys in [S, Sp) zeroed).
+int launch_attn_pack(const float *qkv, int S, int nh, int ld, int q_off, int k_off, int v_off,
+                     half_t *Q, half_t *K, half_t *Vt, int Sp, hipStream_t st);
+
+/* ------------------------------------------------------------------ LayerNorm + adaLN modulate */
+// y = LN(x; eps, no affine) * (1 + scale) + shift, one wave per row, H % 256 == 0, H <= 2048.
+// Virtual row v of segment s: x row xmap(v), y row ymap(v), sample b = v / mod_L,
+// shift = mod[b*mod_ld + shift_off + c], scale = mod[b*mod_ld + scale_off + c].
+struct LnSeg {
+    const float *X; int ldx; RowMap xmap;
+    void *Y; int ldy; RowMap ymap;
+    const float *mod; int mod_ld, mod_L, shift_off, scale_off;
+    int rows;
+};
+struct LnArgs {
+    LnSeg seg[2];
+    int nseg, H;
+    float eps;
+};
+int launch_ln_mod(const LnArgs &a, bool y_f16, hipStream_t st);
+
+/* ------------------------------------------------------------------ GEMV (small M) */
+// Y[b][n] = act(sum_k W[n][k] * X[b][k] + bias[n] + addv[b][n]); optional Y2 = silu(Y).
+// W is bf16, f16 or f32 (wdt); X, Y f32; nb <= 16 rows of X. HBM-bound: one wave per 4 rows of W.
+struct GemvArgs {
+    const void *W; int ldw; int wdt;
+    const float *X; int ldx;
+    float *Y; int ldy;
+    const float *bias;
+    const float *addv; int ld_add;
+    float *Y2; int ldy2;
+    int N, K, nb, silu;
+};
+int launch_gemv(const GemvArgs &a, hipStream_t st);
+
+/* ------------------------------------------------------------------ f32 SIMT linear */
+// Y[ymap(m)*ldy + n] = sum_k X[xmap(m)*ldx + k] * W[n*ldw + k] + bias[n]; W bf16 / f16 / f32.
+// Used where an f32 operand matters more than MFMA rate (K <= 1024 projections, f32 weights).
+struct LinArgs {
+    const float *X; int ldx; RowMap xmap;
+    const void *W; int ldw; int wdt;
+    const float *bias;
+    float *Y; int ldy; RowMap ymap;
+    int M, N, K;
+};
+int launch_linear_f32(const LinArgs &a, hipStream_t st);
+
+/* ------------------------------------------------------------------ small kernels */
+int launch_temb_sinusoid(const float *t, float *out, int nb, int D, float max_period, hipStream_t st);
+// dst[dmap(m)*ldd + c] = src[smap(m)*lds + c], c < H (f32)
+int launch_copy_rows(const float *src, int lds, RowMap smap, float *dst, int ldd, RowMap dmap,
+                     int M, int H, hipStream_t st);
+// sampler step on x2 [2P][n]: v = vu + (vc - vu)*cfg; x += dt*v; both arms of prompt p get x.
+int launch_cfg_euler_pairs(const float *V, float *x2, int P, int n, float cfg, float dt, hipStream_t st);
+// format conversions
+int launch_bf16_to_f16(const uint16_t *src, half_t *dst, size_t n, hipStream_t st);
+int launch_bf16_to_f32(const uint16_t *src, float *dst, size_t n, hipStream_t st);
+int launch_f16_to_f32(const half_t *src, float *dst, size_t n, hipStream_t st);
+// conv weight [OC][IC][K] (bf16 or f16, src_bf16 selects) -> [OC][K][IC] f16
+int launch_conv_weight_reorder(const void *src, int src_bf16, half_t *dst, int OC, int IC, int K, hipStream_t st);
+
+// reference-surface elementwise ops (f32)
+int launch_silu(float *x, size_t n, hipStream_t st);
+int launch_copy(const float *x, float *y, size_t n, hipStream_t st);
+int launch_swiglu(const float *a, const float *b, float *y, size_t n, hipStream_t st);
+int launch_add(const float *a, const float *b, float *y, size_t n, hipStream_t st);
+int launch_add_bcast_col(const float *x, const float *v, float *y, int S, int H, hipStream_t st);
+int launch_cfg_euler(const float *fc, const float *fu, float *x, size_t n, float cfg, float dt, hipStream_t st);
+int launch_gate_add(const float *x, const float *f, const float *mod, float *y, int rows, int H,
+                    int per_row, int chunks, int gate_idx, hipStream_t st);
+int launch_rms_head(float *x, const float *w, int rows, int nh, int ld, int hd, int col_off, int row_off,
+                    float eps, hipStream_t st);
+int launch_rope_pairs(float *x, const int32_t *pos, int rows, int nh, int ld, int hd, int col_off,
+                      int row_off, float fscale, float base, hipStream_t st);
+
+} // namespace tsn

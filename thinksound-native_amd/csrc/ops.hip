@@ -1,0 +1,506 @@
+// ops.hip — HBM-bound kernels of the DiT path on gfx950: LayerNorm+adaLN modulate, the
+// small-M GEMV (adaLN modulation, timestep MLP), an f32 SIMT linear for the K=64 input and
+// N=64 output projections, the sampler update, format conversions, and the reference-surface
+// elementwise ops.
+//
+// Reductions are wave-level butterflies (__shfl_xor), so every lane ends with the same value and
+// the order is fixed: reruns are bit-identical. No float atomics anywhere.
+#include "kernels.h"
+
+#include <string.h>
+
+namespace tsn {
+
+namespace {
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+__device__ inline float silu_f(float v) { return v / (1.0f + __expf(-v)); }
+
+/* ---------------- LayerNorm + adaLN modulate (shaders/ops_conv.metal:127-144) ---------------- */
+// one wave per row; lane holds columns 4*lane + 256*c, c < NV (H = 256*NV)
+template <bool Y_F16, int NV>
+__global__ __launch_bounds__(256) void ln_mod_kernel(const LnArgs a) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    int v = blockIdx.x * 4 + wave;
+    const int total = a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
+    if (v >= total) return;
+    int si = 0;
+    if (v >= a.seg[0].rows) { si = 1; v -= a.seg[0].rows; }
+    const LnSeg &S = a.seg[si];
+    const float *x = S.X + rowmap_phys(S.xmap, v) * (long long)S.ldx;
+    float4 xv[NV];
+    float sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        xv[c] = *(const float4 *)(x + c * 256 + lane * 4);
+        sum += (xv[c].x + xv[c].y) + (xv[c].z + xv[c].w);
+    }
+    const float inv_h = 1.0f / (float)(NV * 256);
+    const float mean = wave_sum(sum) * inv_h;
+    float var = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const float d0 = xv[c].x - mean, d1 = xv[c].y - mean, d2 = xv[c].z - mean, d3 = xv[c].w - mean;
+        var += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+    }
+    var = wave_sum(var) * inv_h;
+    const float inv = 1.0f / sqrtf(var + a.eps);
+    const int b = v / S.mod_L;
+    const float *mb = S.mod + (long long)b * S.mod_ld;
+    const long long yrow = rowmap_phys(S.ymap, v) * (long long)S.ldy;
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const int col = c * 256 + lane * 4;
+        const float4 sh = *(const float4 *)(mb + S.shift_off + col);
+        const float4 scl = *(const float4 *)(mb + S.scale_off + col);
+        const float y0 = (xv[c].x - mean) * inv * (1.0f + scl.x) + sh.x;
+        const float y1 = (xv[c].y - mean) * inv * (1.0f + scl.y) + sh.y;
+        const float y2 = (xv[c].z - mean) * inv * (1.0f + scl.z) + sh.z;
+        const float y3 = (xv[c].w - mean) * inv * (1.0f + scl.w) + sh.w;
+        if constexpr (Y_F16) {
+            *(half4 *)((half_t *)S.Y + yrow + col) = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
+        } else {
+            *(float4 *)((float *)S.Y + yrow + col) = make_float4(y0, y1, y2, y3);
+        }
+    }
+}
+
+/* ---------------- GEMV (shaders/gemm_attn.metal:47-74, batched over nb rows of X) ---------------- */
+template <typename WT>
+__device__ inline void load_w8(const WT *p, float (&w)[8]);
+template <>
+__device__ inline void load_w8<uint16_t>(const uint16_t *p, float (&w)[8]) {
+    const u16x8 u = *(const u16x8 *)p;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e] = bf16_to_f32(u[e]);
+}
+template <>
+__device__ inline void load_w8<half_t>(const half_t *p, float (&w)[8]) {
+    const half8 u = *(const half8 *)p;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e] = (float)u[e];
+}
+template <>
+__device__ inline void load_w8<float>(const float *p, float (&w)[8]) {
+    const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
+    w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w; w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+}
+
+constexpr int GEMV_ROWS = 4;   // rows of W per wave
+
+template <typename WT, int NB>
+__global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int n0 = (blockIdx.x * 4 + wave) * GEMV_ROWS;
+    if (n0 >= a.N) return;
+    const WT *W = (const WT *)a.W;
+    float acc[GEMV_ROWS][NB];
+#pragma unroll
+    for (int rr = 0; rr < GEMV_ROWS; ++rr)
+#pragma unroll
+        for (int b = 0; b < NB; ++b) acc[rr][b] = 0.0f;
+    for (int k = lane * 8; k < a.K; k += 512) {
+        float w[GEMV_ROWS][8];
+#pragma unroll
+        for (int rr = 0; rr < GEMV_ROWS; ++rr) {
+            const int n = min(n0 + rr, a.N - 1);
+            load_w8<WT>(W + (long long)n * a.ldw + k, w[rr]);
+        }
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            const float *xp = a.X + (long long)b * a.ldx + k;
+            const float4 x0 = *(const float4 *)xp, x1 = *(const float4 *)(xp + 4);
+            const float xs[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
+#pragma unroll
+            for (int rr = 0; rr < GEMV_ROWS; ++rr)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc[rr][b] += w[rr][e] * xs[e];
+        }
+    }
+#pragma unroll
+    for (int rr = 0; rr < GEMV_ROWS; ++rr) {
+        const int n = n0 + rr;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            float v = wave_sum(acc[rr][b]);
+            if (lane == b && n < a.N) {
+                if (a.bias) v += a.bias[n];
+                if (a.addv) v += a.addv[(long long)b * a.ld_add + n];
+                if (a.silu) v = silu_f(v);
+                a.Y[(long long)b * a.ldy + n] = v;
+                if (a.Y2) a.Y2[(long long)b * a.ldy2 + n] = silu_f(v);
+            }
+        }
+    }
+}
+
+/* ---------------- f32 SIMT linear: 64x64 tile, 4x4 outputs per thread ---------------- */
+template <typename WT>
+__device__ inline float load_w1(const WT *p);
+template <> __device__ inline float load_w1<uint16_t>(const uint16_t *p) { return bf16_to_f32(*p); }
+template <> __device__ inline float load_w1<half_t>(const half_t *p) { return (float)*p; }
+template <> __device__ inline float load_w1<float>(const float *p) { return *p; }
+
+template <typename WT>
+__global__ __launch_bounds__(256) void linear_f32_kernel(const LinArgs a) {
+    __shared__ float sX[16][65];
+    __shared__ float sW[16][65];
+    const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+    const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+    const WT *W = (const WT *)a.W;
+    float acc[4][4] = {};
+    for (int k0 = 0; k0 < a.K; k0 += 16) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int idx = tid + 256 * e;       // 1024 = 64 rows x 16 k
+            const int rr = idx >> 4, kk = idx & 15;
+            const int m = m0 + rr, n = n0 + rr, k = k0 + kk;
+            sX[kk][rr] = (m < a.M && k < a.K) ? a.X[rowmap_phys(a.xmap, m) * (long long)a.ldx + k] : 0.0f;
+            sW[kk][rr] = (n < a.N && k < a.K) ? load_w1<WT>(W + (long long)n * a.ldw + k) : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < 16; ++kk) {
+            float xr[4], wr[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) xr[i] = sX[kk][ty + 16 * i];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) wr[j] = sW[kk][tx + 16 * j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) acc[i][j] += xr[i] * wr[j];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int m = m0 + ty + 16 * i;
+        if (m >= a.M) continue;
+        float *y = a.Y + rowmap_phys(a.ymap, m) * (long long)a.ldy;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int n = n0 + tx + 16 * j;
+            if (n < a.N) y[n] = acc[i][j] + (a.bias ? a.bias[n] : 0.0f);
+        }
+    }
+}
+
+/* ---------------- small kernels ---------------- */
+// src/dit_fwd.cpp:111-119: fr_k = (10000/max_period) * 10000^(-2k/D), cos half then sin half
+__global__ void temb_kernel(const float *t, float *out, int nb, int D, float max_period) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    const int half = D / 2;
+    if (idx >= nb * half) return;
+    const int b = idx / half, k = idx - b * half;
+    const float fr = (10000.0f / max_period) * powf(10000.0f, -2.0f * (float)k / (float)D);
+    const float arg = t[b] * fr;
+    out[(long long)b * D + k] = cosf(arg);
+    out[(long long)b * D + half + k] = sinf(arg);
+}
+
+__global__ void copy_rows_kernel(const float *src, int lds, RowMap smap, float *dst, int ldd, RowMap dmap, int M, int H) {
+    const int m = blockIdx.x;
+    if (m >= M) return;
+    const float *s = src + rowmap_phys(smap, m) * (long long)lds;
+    float *d = dst + rowmap_phys(dmap, m) * (long long)ldd;
+    for (int c = threadIdx.x; c < H; c += blockDim.x) d[c] = s[c];
+}
+
+// shaders/ops_conv.metal:193-201 applied to CFG pairs; both arms of prompt p receive the new x
+__global__ void cfg_euler_pairs_kernel(const float *V, float *x2, int P, int n, float cfg, float dt) {
+    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (long long)P * n) return;
+    const int p = (int)(idx / n), i = (int)(idx - (long long)p * n);
+    const float fc = V[(long long)(2 * p) * n + i], fu = V[(long long)(2 * p + 1) * n + i];
+    const float v = fu + (fc - fu) * cfg;
+    const float xn = x2[(long long)(2 * p) * n + i] + dt * v;
+    x2[(long long)(2 * p) * n + i] = xn;
+    x2[(long long)(2 * p + 1) * n + i] = xn;
+}
+
+__global__ void bf16_to_f16_kernel(const uint16_t *s, half_t *d, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) d[i] = (half_t)bf16_to_f32(s[i]);
+}
+__global__ void bf16_to_f32_kernel(const uint16_t *s, float *d, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) d[i] = bf16_to_f32(s[i]);
+}
+__global__ void f16_to_f32_kernel(const half_t *s, float *d, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) d[i] = (float)s[i];
+}
+// [OC][IC][K] -> [OC][K][IC]
+__global__ void conv_reorder_kernel(const void *src, int src_bf16, half_t *dst, int OC, int IC, int K) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long total = (long long)OC * IC * K;
+    if (i >= total) return;
+    const int ic = (int)(i % IC);
+    const long long r = i / IC;
+    const int k = (int)(r % K);
+    const int oc = (int)(r / K);
+    const long long si = ((long long)oc * IC + ic) * K + k;
+    dst[i] = src_bf16 ? (half_t)bf16_to_f32(((const uint16_t *)src)[si]) : ((const half_t *)src)[si];
+}
+
+// reference-surface elementwise kernels (shaders/ops_conv.metal:9-57,146-169,193-201)
+__global__ void silu_kernel(float *x, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) x[i] = x[i] / (1.0f + expf(-x[i]));
+}
+__global__ void copy_kernel(const float *x, float *y, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = x[i];
+}
+__global__ void swiglu_kernel(const float *a, const float *b, float *y, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) { const float va = a[i]; y[i] = (va / (1.0f + expf(-va))) * b[i]; }
+}
+__global__ void add_kernel(const float *a, const float *b, float *y, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = a[i] + b[i];
+}
+__global__ void add_bcast_col_kernel(const float *x, const float *v, float *y, int H, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = x[i] + v[i % H];
+}
+__global__ void cfg_euler_kernel(const float *fc, const float *fu, float *x, size_t n, float cfg, float dt) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) { const float v = fu[i] + (fc[i] - fu[i]) * cfg; x[i] += dt * v; }
+}
+__global__ void gate_add_kernel(const float *x, const float *f, const float *mod, float *y, int H, int per_row,
+                                int chunks, int gate_idx, size_t n) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const size_t s = i / H, c = i % H;
+    const float *m = mod + (per_row ? s * (size_t)chunks * H : 0);
+    y[i] = x[i] + f[i] * m[(size_t)gate_idx * H + c];
+}
+// one wave per (row, head)
+__global__ void rms_head_kernel(float *x, const float *w, int rows, int nh, int ld, int hd, int col_off,
+                                int row_off, float eps) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int id = blockIdx.x * 4 + wave;
+    if (id >= rows * nh) return;
+    const int r = id / nh, h = id - r * nh;
+    float *p = x + (long long)(row_off + r) * ld + col_off + (long long)h * hd;
+    float ss = 0.0f;
+    for (int i = lane; i < hd; i += 64) ss += p[i] * p[i];
+    ss = wave_sum(ss);
+    const float inv = 1.0f / sqrtf(ss / (float)hd + eps);
+    for (int i = lane; i < hd; i += 64) p[i] = p[i] * inv * w[i];
+}
+__global__ void rope_pairs_kernel(float *x, const int32_t *pos, int rows, int nh, int ld, int hd, int col_off,
+                                  int row_off, float fscale, float base) {
+    const long long id = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const int npair = hd / 2;
+    if (id >= (long long)rows * nh * npair) return;
+    const int r = (int)(id / (nh * npair));
+    const int rem = (int)(id - (long long)r * nh * npair);
+    const int h = rem / npair, j = rem - h * npair;
+    const float inv = powf(base, -2.0f * (float)j / (float)hd);
+    const float ang = (float)(pos ? pos[r] : r) * fscale * inv;
+    const float cs = cosf(ang), sn = sinf(ang);
+    float *p = x + (long long)(row_off + r) * ld + col_off + (long long)h * hd;
+    const float x0 = p[2 * j], x1 = p[2 * j + 1];
+    p[2 * j] = x0 * cs - x1 * sn;
+    p[2 * j + 1] = x0 * sn + x1 * cs;
+}
+
+inline unsigned blocks_for(size_t n, unsigned t = 256) { return (unsigned)((n + t - 1) / t); }
+
+} // namespace
+
+int launch_ln_mod(const LnArgs &a, bool y_f16, hipStream_t st) {
+    TSN_REQUIRE(a.nseg >= 1 && a.nseg <= 2, "ln: 1 or 2 segments");
+    TSN_REQUIRE(a.H % 256 == 0 && a.H >= 256 && a.H <= 2048, "ln: H must be a multiple of 256 in [256, 2048]");
+    int total = 0;
+    for (int i = 0; i < a.nseg; ++i) {
+        const LnSeg &s = a.seg[i];
+        TSN_REQUIRE(s.X && s.Y && s.mod && s.rows > 0 && s.mod_L > 0 && s.xmap.L > 0 && s.ymap.L > 0, "ln: segment");
+        TSN_REQUIRE(s.ldx % 4 == 0 && s.ldy % 4 == 0 && s.mod_ld % 4 == 0 && s.shift_off % 4 == 0 && s.scale_off % 4 == 0,
+                    "ln: strides and offsets must be multiples of 4");
+        total += s.rows;
+    }
+    dim3 grid((total + 3) / 4), block(256);
+    const int nv = a.H / 256;
+#define TSN_LN_CASE(NVV)                                                                           \
+    case NVV:                                                                                      \
+        if (y_f16) hipLaunchKernelGGL((ln_mod_kernel<true, NVV>), grid, block, 0, st, a);          \
+        else hipLaunchKernelGGL((ln_mod_kernel<false, NVV>), grid, block, 0, st, a);               \
+        break;
+    switch (nv) {
+        TSN_LN_CASE(1) TSN_LN_CASE(2) TSN_LN_CASE(3) TSN_LN_CASE(4)
+        TSN_LN_CASE(5) TSN_LN_CASE(6) TSN_LN_CASE(7) TSN_LN_CASE(8)
+        default: set_error("ln: unsupported H"); return TSN_ERR_UNSUPPORTED;
+    }
+#undef TSN_LN_CASE
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+
+int launch_gemv(const GemvArgs &a, hipStream_t st) {
+    TSN_REQUIRE(a.W && a.X && a.Y && a.N > 0 && a.K > 0, "gemv: arguments");
+    TSN_REQUIRE(a.nb >= 1 && a.nb <= 16, "gemv: 1..16 input rows");
+    TSN_REQUIRE(a.K % 8 == 0 && a.ldw % 8 == 0 && a.ldx % 4 == 0, "gemv: K, ldw multiple of 8; ldx multiple of 4");
+    const int rows_per_block = 4 * GEMV_ROWS;
+    dim3 grid((a.N + rows_per_block - 1) / rows_per_block), block(256);
+#define TSN_GEMV_NB(WT, NBV)                                                                       \
+    case NBV: hipLaunchKernelGGL((gemv_kernel<WT, NBV>), grid, block, 0, st, a); break;
+#define TSN_GEMV_W(WT)                                                                             \
+    switch (nb) {                                                                                  \
+        TSN_GEMV_NB(WT, 1) TSN_GEMV_NB(WT, 2) TSN_GEMV_NB(WT, 4) TSN_GEMV_NB(WT, 8)                \
+        TSN_GEMV_NB(WT, 16)                                                                        \
+        default: break;                                                                            \
+    }
+    // round nb up to a compiled batch count; extra rows are computed but never written
+    int nb = a.nb <= 1 ? 1 : a.nb <= 2 ? 2 : a.nb <= 4 ? 4 : a.nb <= 8 ? 8 : 16;
+    if (nb != a.nb) {
+        // the kernel reads X rows up to nb-1: only valid when the caller's X has them
+        set_error("gemv: nb must be 1, 2, 4, 8 or 16");
+        return TSN_ERR_UNSUPPORTED;
+    }
+    if (a.wdt == DT_BF16) { TSN_GEMV_W(uint16_t) }
+    else if (a.wdt == DT_F16) { TSN_GEMV_W(half_t) }
+    else if (a.wdt == DT_F32) { TSN_GEMV_W(float) }
+    else { set_error("gemv: weight dtype"); return TSN_ERR_ARG; }
+#undef TSN_GEMV_W
+#undef TSN_GEMV_NB
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+
+int launch_linear_f32(const LinArgs &a, hipStream_t st) {
+    TSN_REQUIRE(a.X && a.W && a.Y && a.M > 0 && a.N > 0 && a.K > 0, "linear_f32: arguments");
+    TSN_REQUIRE(a.xmap.L > 0 && a.ymap.L > 0, "linear_f32: row maps");
+    dim3 grid((a.N + 63) / 64, (a.M + 63) / 64), block(256);
+    if (a.wdt == DT_BF16) hipLaunchKernelGGL(linear_f32_kernel<uint16_t>, grid, block, 0, st, a);
+    else if (a.wdt == DT_F16) hipLaunchKernelGGL(linear_f32_kernel<half_t>, grid, block, 0, st, a);
+    else if (a.wdt == DT_F32) hipLaunchKernelGGL(linear_f32_kernel<float>, grid, block, 0, st, a);
+    else { set_error("linear_f32: weight dtype"); return TSN_ERR_ARG; }
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+
+int launch_temb_sinusoid(const float *t, float *out, int nb, int D, float max_period, hipStream_t st) {
+    TSN_REQUIRE(t && out && nb > 0 && D > 0 && D % 2 == 0, "temb: arguments");
+    hipLaunchKernelGGL(temb_kernel, dim3(blocks_for((size_t)nb * D / 2)), dim3(256), 0, st, t, out, nb, D, max_period);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+
+int launch_copy_rows(const float *src, int lds, RowMap smap, float *dst, int ldd, RowMap dmap, int M, int H, hipStream_t st) {
+    TSN_REQUIRE(src && dst && M > 0 && H > 0 && smap.L > 0 && dmap.L > 0, "copy_rows: arguments");
+    hipLaunchKernelGGL(copy_rows_kernel, dim3(M), dim3(256), 0, st, src, lds, smap, dst, ldd, dmap, M, H);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+
+int launch_cfg_euler_pairs(const float *V, float *x2, int P, int n, float cfg, float dt, hipStream_t st) {
+    TSN_REQUIRE(V && x2 && P > 0 && n > 0, "cfg_euler_pairs: arguments");
+    hipLaunchKernelGGL(cfg_euler_pairs_kernel, dim3(blocks_for((size_t)P * n)), dim3(256), 0, st, V, x2, P, n, cfg, dt);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+
+int launch_bf16_to_f16(const uint16_t *src, half_t *dst, size_t n, hipStream_t st) {
+    if (n == 0) return TSN_OK;
+    hipLaunchKernelGGL(bf16_to_f16_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, dst, n);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_bf16_to_f32(const uint16_t *src, float *dst, size_t n, hipStream_t st) {
+    if (n == 0) return TSN_OK;
+    hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, dst, n);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_f16_to_f32(const half_t *src, float *dst, size_t n, hipStream_t st) {
+    if (n == 0) return TSN_OK;
+    hipLaunchKernelGGL(f16_to_f32_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, dst, n);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_conv_weight_reorder(const void *src, int src_bf16, half_t *dst, int OC, int IC, int K, hipStream_t st) {
+    TSN_REQUIRE(src && dst && OC > 0 && IC > 0 && K > 0, "conv_reorder: arguments");
+    const size_t n = (size_t)OC * IC * K;
+    hipLaunchKernelGGL(conv_reorder_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, src_bf16, dst, OC, IC, K);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+
+int launch_silu(float *x, size_t n, hipStream_t st) {
+    TSN_REQUIRE(x || n == 0, "silu: null");
+    if (n == 0) return TSN_OK;
+    hipLaunchKernelGGL(silu_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, n);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_copy(const float *x, float *y, size_t n, hipStream_t st) {
+    TSN_REQUIRE((x && y) || n == 0, "copy: null");
+    if (n == 0) return TSN_OK;
+    hipLaunchKernelGGL(copy_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, y, n);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_swiglu(const float *a, const float *b, float *y, size_t n, hipStream_t st) {
+    TSN_REQUIRE((a && b && y) || n == 0, "swiglu: null");
+    if (n == 0) return TSN_OK;
+    hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(n)), dim3(256), 0, st, a, b, y, n);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_add(const float *a, const float *b, float *y, size_t n, hipStream_t st) {
+    TSN_REQUIRE((a && b && y) || n == 0, "add: null");
+    if (n == 0) return TSN_OK;
+    hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n)), dim3(256), 0, st, a, b, y, n);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_add_bcast_col(const float *x, const float *v, float *y, int S, int H, hipStream_t st) {
+    TSN_REQUIRE(x && v && y && S > 0 && H > 0, "add_bcast_col: arguments");
+    const size_t n = (size_t)S * H;
+    hipLaunchKernelGGL(add_bcast_col_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, v, y, H, n);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_cfg_euler(const float *fc, const float *fu, float *x, size_t n, float cfg, float dt, hipStream_t st) {
+    TSN_REQUIRE((fc && fu && x) || n == 0, "cfg_euler: null");
+    if (n == 0) return TSN_OK;
+    hipLaunchKernelGGL(cfg_euler_kernel, dim3(blocks_for(n)), dim3(256), 0, st, fc, fu, x, n, cfg, dt);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_gate_add(const float *x, const float *f, const float *mod, float *y, int rows, int H, int per_row,
+                    int chunks, int gate_idx, hipStream_t st) {
+    TSN_REQUIRE(x && f && mod && y && rows > 0 && H > 0 && gate_idx >= 0 && gate_idx < chunks, "gate_add: arguments");
+    const size_t n = (size_t)rows * H;
+    hipLaunchKernelGGL(gate_add_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, f, mod, y, H, per_row, chunks, gate_idx, n);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_rms_head(float *x, const float *w, int rows, int nh, int ld, int hd, int col_off, int row_off,
+                    float eps, hipStream_t st) {
+    TSN_REQUIRE(x && w && rows > 0 && nh > 0 && hd > 0, "rms_head: arguments");
+    const int n = rows * nh;
+    hipLaunchKernelGGL(rms_head_kernel, dim3((n + 3) / 4), dim3(256), 0, st, x, w, rows, nh, ld, hd, col_off, row_off, eps);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_rope_pairs(float *x, const int32_t *pos, int rows, int nh, int ld, int hd, int col_off, int row_off,
+                      float fscale, float base, hipStream_t st) {
+    TSN_REQUIRE(x && rows > 0 && nh > 0 && hd > 0 && hd % 2 == 0, "rope_pairs: arguments");
+    const size_t n = (size_t)rows * nh * (hd / 2);
+    hipLaunchKernelGGL(rope_pairs_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, pos, rows, nh, ld, hd, col_off,
+                       row_off, fscale, base);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+
+} // namespace tsn

@@ -142,6 +142,19 @@ int tsn_dit_capture_forward(tsn_dit *dit, const float *z, const float *t, const 
 int tsn_dit_capture_sample(tsn_dit *dit, float *x, const float *text, const float *pooled, int steps, float cfg);
 int tsn_dit_replay(tsn_dit *dit);
 
+/* Observability (no reference counterpart: the reference times only whole command buffers,
+ * src/gpu.mm:168-174). One eager evaluation with a HIP event pair around every launch on the
+ * runtime's stream; per kernel symbol: launches, summed ms, algorithmic flops and HBM bytes. */
+typedef struct {
+    char name[64];
+    int launches;
+    double total_ms;
+    double flops;
+    double bytes;
+} tsn_kernel_stat;
+int tsn_dit_profile_forward(tsn_dit *dit, const float *z, const float *t, const float *text, const float *pooled,
+                            float *v, tsn_kernel_stat *stats, int cap, int *n_stats);
+
 /* ---------------- synthetic data (specified generator; see thinksound-native_amd/csrc/synth.cpp) ---------------- */
 int tsn_synth_normal_f32(uint64_t seed, uint64_t index, double mean, double std, size_t n, float *out_host);
 int tsn_synth_normal_bf16(uint64_t seed, uint64_t index, double mean, double std, size_t n, uint16_t *out_host);

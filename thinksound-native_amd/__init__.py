@@ -47,6 +47,12 @@ class DitSpec(ctypes.Structure):
         return s
 
 
+class KernelStat(ctypes.Structure):
+    """tsn_kernel_stat (include/tsn.h)."""
+    _fields_ = [("name", ctypes.c_char * 64), ("launches", ctypes.c_int), ("total_ms", ctypes.c_double),
+                ("flops", ctypes.c_double), ("bytes", ctypes.c_double)]
+
+
 _P = ctypes.c_void_p
 _U32 = ctypes.c_uint32
 _I = ctypes.c_int
@@ -93,6 +99,7 @@ _SIGS = {
     "tsn_dit_capture_forward": [_P, _P, _P, _P, _P, _P],
     "tsn_dit_capture_sample": [_P, _P, _P, _P, _I, _FL],
     "tsn_dit_replay": [_P],
+    "tsn_dit_profile_forward": [_P, _P, _P, _P, _P, _P, ctypes.POINTER(KernelStat), _I, ctypes.POINTER(_I)],
     "tsn_synth_normal_f32": [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, _SZ, _P],
     "tsn_synth_normal_bf16": [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, _SZ, _P],
     "tsn_synth_uniform_f32": [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, _SZ, _P],
@@ -348,6 +355,15 @@ class DitModel:
 
     def replay(self):
         call("tsn_dit_replay", self.h)
+
+    def profile_forward(self, z, t_dev, text, pooled, v):
+        """Per-kernel stats of one eager evaluation: list of dicts (name, launches, ms, flops, bytes)."""
+        cap = 64
+        arr = (KernelStat * cap)()
+        n = ctypes.c_int()
+        call("tsn_dit_profile_forward", self.h, z.p, t_dev.p, text.p, pooled.p, v.p, arr, cap, ctypes.byref(n))
+        return [{"name": arr[i].name.decode(), "launches": arr[i].launches, "ms": arr[i].total_ms,
+                 "flops": arr[i].flops, "bytes": arr[i].bytes} for i in range(n.value)]
 
 
 # Input index space of the synthetic generator (weights use their manifest index).

@@ -205,6 +205,24 @@ int tsn_dit_replay(tsn_dit *dit) {
     return dit->m.replay();
 }
 
+int tsn_dit_profile_forward(tsn_dit *dit, const float *z, const float *t, const float *text, const float *pooled,
+                            float *v, tsn_kernel_stat *stats, int cap, int *n_stats) {
+    if (!dit || !stats || !n_stats || cap <= 0) { tsn::set_error("profile: null argument"); return TSN_ERR_ARG; }
+    std::vector<tsn::KernelStat> ks;
+    const int rc = dit->m.profile_forward(z, t, text, pooled, v, ks);
+    if (rc != TSN_OK) return rc;
+    const int n = (int)ks.size() < cap ? (int)ks.size() : cap;
+    for (int i = 0; i < n; ++i) {
+        snprintf(stats[i].name, sizeof stats[i].name, "%s", ks[i].name.c_str());
+        stats[i].launches = ks[i].launches;
+        stats[i].total_ms = ks[i].ms;
+        stats[i].flops = ks[i].flops;
+        stats[i].bytes = ks[i].bytes;
+    }
+    *n_stats = n;
+    return TSN_OK;
+}
+
 int tsn_synth_normal_f32(uint64_t seed, uint64_t index, double mean, double std, size_t n, float *out) {
     if (!out && n) { tsn::set_error("null output"); return TSN_ERR_ARG; }
     tsn::synth_normal_f32(seed, index, mean, std, n, out);

@@ -109,6 +109,9 @@ int DitModel::create(Runtime *r, const DitSpec &sp) {
     TSN_TRY(ah(&Vt_, B * s.NH * 64 * (size_t)Sp));   // zero-filled: keys >= S stay zero
     TSN_TRY(ah(&AO_, B * S * H));
     TSN_TRY(ah(&HF_, B * S * (size_t)s.F));
+    // split-K partials: up to 8 splits of the largest residual GEMM output (B*S x H f32)
+    ws_bytes_ = (size_t)8 * B * S * H * sizeof(float);
+    TSN_TRY(alloc(ws_bytes_, (void **)&ws_));
     // RoPE table: same expression as shaders/ops_conv.metal:162-164 with fscale 1 (audio rows)
     std::vector<float> tab((size_t)s.La * 32 * 2);
     for (int p = 0; p < s.La; ++p)
@@ -266,7 +269,49 @@ void ln_seg(LnSeg &g, const float *X, int H, RowMap map, half_t *Y, const float 
     g.rows = rows;
 }
 
+constexpr const char *K_GEMM_STORE = "gemm_f16_kernel<false, 0>";
+constexpr const char *K_GEMM_RESID = "gemm_f16_kernel<false, 1>";
+constexpr const char *K_GEMM_QKV = "gemm_f16_kernel<false, 2>";
+constexpr const char *K_ATTN = "flash_attn_kernel";
+constexpr const char *K_GEMV = "gemv_kernel";
+constexpr const char *K_LN16 = "ln_mod_kernel<true, 4>";
+constexpr const char *K_LN32 = "ln_mod_kernel<false, 4>";
+constexpr const char *K_LIN = "linear_f32_kernel";
+
+double gemm_flops(const GemmBatch &b) {
+    double f = 0;
+    for (int i = 0; i < b.nprob; ++i) f += 2.0 * b.p[i].M * (double)b.p[i].N * b.p[i].K;
+    return f;
+}
+// A once (conv taps re-read the same rows), W once, output at its storage type (residual: read + write f32)
+double gemm_bytes(const GemmBatch &b, int epi) {
+    double x = 0;
+    for (int i = 0; i < b.nprob; ++i) {
+        const GemmProblem &p = b.p[i];
+        x += 2.0 * p.M * (double)p.Kc + 2.0 * p.N * (double)p.K + (epi == EPI_RESID ? 8.0 : 2.0) * p.M * (double)p.N;
+    }
+    return x;
+}
+double ln_bytes(const LnArgs &a, bool f16) {
+    double r = 0;
+    for (int i = 0; i < a.nseg; ++i) r += a.seg[i].rows;
+    return r * a.H * (4.0 + (f16 ? 2.0 : 4.0));
+}
+
 } // namespace
+
+template <typename F>
+int DitModel::run(const char *name, double flops, double bytes, F &&launch) {
+    if (!prof_) return launch();
+    ProfRec r{name, flops, bytes, nullptr, nullptr};
+    TSN_HIP_CHECK(hipEventCreate(&r.a));
+    TSN_HIP_CHECK(hipEventCreate(&r.b));
+    prof_->push_back(r);
+    TSN_HIP_CHECK(hipEventRecord(r.a, rt->dev.stream()));
+    const int rc = launch();
+    TSN_HIP_CHECK(hipEventRecord(r.b, rt->dev.stream()));
+    return rc;
+}
 
 // Joint block: src/dit_fwd.cpp:180-257 (pre_attn :24-49, attention :83-102, post_attn :51-81)
 int DitModel::block_joint(int i) {
@@ -279,43 +324,48 @@ int DitModel::block_joint(int i) {
     ln.nseg = 2; ln.H = H; ln.eps = s.ln_eps;
     ln_seg(ln.seg[0], X_, H, Sa, XN_, MOD_, NMOD, La, a.mod_off, B * La);
     ln_seg(ln.seg[1], X_, H, St, XN_, MOD_, NMOD, Lt, t.mod_off, B * Lt);
-    TSN_TRY(launch_ln_mod(ln, true, st));
+    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, true, st); }));
 
     GemmBatch qb;
     qb.nprob = 2;
     qkv_problem(qb.p[0], XN_, Sa, B * La, a.Wqkv, a.bqkv, a.qn, a.kn, H, s.NH, Q_, K_, Vt_, S, Sp, La, 0, La, rope_, s.rms_eps);
     qkv_problem(qb.p[1], XN_, St, B * Lt, t.Wqkv, t.bqkv, t.qn, t.kn, H, s.NH, Q_, K_, Vt_, S, Sp, Lt, La, 0, rope_, s.rms_eps);
-    TSN_TRY(launch_gemm(qb, EPI_QKV, false, st));
+    TSN_TRY(run(K_GEMM_QKV, gemm_flops(qb), gemm_bytes(qb, EPI_QKV), [&] { return launch_gemm(qb, EPI_QKV, false, st); }));
 
     AttnArgs at;
     memset(&at, 0, sizeof at);
     at.Q = Q_; at.K = K_; at.Vt = Vt_; at.S = S; at.Sp = Sp; at.nh = s.NH; at.BH = B * s.NH;
     at.O = AO_; at.o_f32 = 0; at.ldo = H; at.omap = rowmap_dense(B * S);
     at.scale_log2 = 1.4426950408889634f;
-    TSN_TRY(launch_attention(at, st));
+    TSN_TRY(run(K_ATTN, 4.0 * B * s.NH * (double)S * S * 64, 8.0 * B * (double)S * H,
+                [&] { return launch_attention(at, st); }));
 
     GemmBatch ob;
     ob.nprob = 2;
+    ob.ws = ws_;
+    ob.ws_bytes = ws_bytes_;
     resid_problem(ob.p[0], AO_, H, Sa, 1, H, B * La, H, a.Wo, a.bo, X_, H, MOD_ + a.mod_off + 2 * H, NMOD);
     resid_problem(ob.p[1], AO_, H, St, 1, H, B * Lt, H, t.Wo, t.bo, X_, H, MOD_ + t.mod_off + 2 * H, NMOD);
-    TSN_TRY(launch_gemm(ob, EPI_RESID, false, st));
+    TSN_TRY(run(K_GEMM_RESID, gemm_flops(ob), gemm_bytes(ob, EPI_RESID), [&] { return launch_gemm(ob, EPI_RESID, false, st); }));
 
     ln_seg(ln.seg[0], X_, H, Sa, XN_, MOD_, NMOD, La, a.mod_off + 3 * H, B * La);
     ln_seg(ln.seg[1], X_, H, St, XN_, MOD_, NMOD, Lt, t.mod_off + 3 * H, B * Lt);
-    TSN_TRY(launch_ln_mod(ln, true, st));
+    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, true, st); }));
 
     const int ta = a.conv ? 3 : 1;
     GemmBatch f1;
     f1.nprob = 2;
     store_problem(f1.p[0], XN_, H, Sa, ta, H, B * La, s.F, a.W1, HF_, s.F, 1);
     store_problem(f1.p[1], XN_, H, St, 1, H, B * Lt, s.F, t.W1, HF_, s.F, 1);
-    TSN_TRY(launch_gemm(f1, EPI_STORE, false, st));
+    TSN_TRY(run(K_GEMM_STORE, gemm_flops(f1), gemm_bytes(f1, EPI_STORE), [&] { return launch_gemm(f1, EPI_STORE, false, st); }));
 
     GemmBatch f2;
     f2.nprob = 2;
+    f2.ws = ws_;
+    f2.ws_bytes = ws_bytes_;
     resid_problem(f2.p[0], HF_, s.F, Sa, ta, s.F, B * La, H, a.W2, nullptr, X_, H, MOD_ + a.mod_off + 5 * H, NMOD);
     resid_problem(f2.p[1], HF_, s.F, St, 1, s.F, B * Lt, H, t.W2, nullptr, X_, H, MOD_ + t.mod_off + 5 * H, NMOD);
-    return launch_gemm(f2, EPI_RESID, false, st);
+    return run(K_GEMM_RESID, gemm_flops(f2), gemm_bytes(f2, EPI_RESID), [&] { return launch_gemm(f2, EPI_RESID, false, st); });
 }
 
 // Fused block: src/dit_fwd.cpp:267-279 over the joined rows
@@ -328,37 +378,42 @@ int DitModel::block_fused(int i) {
     memset(&ln, 0, sizeof ln);
     ln.nseg = 1; ln.H = H; ln.eps = s.ln_eps;
     ln_seg(ln.seg[0], X_, H, D, XN_, MOD_, NMOD, S, w.mod_off, M);
-    TSN_TRY(launch_ln_mod(ln, true, st));
+    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, true, st); }));
 
     GemmBatch qb;
     qb.nprob = 1;
     qkv_problem(qb.p[0], XN_, D, M, w.Wqkv, w.bqkv, w.qn, w.kn, H, s.NH, Q_, K_, Vt_, S, Sp, S, 0, s.La, rope_, s.rms_eps);
-    TSN_TRY(launch_gemm(qb, EPI_QKV, false, st));
+    TSN_TRY(run(K_GEMM_QKV, gemm_flops(qb), gemm_bytes(qb, EPI_QKV), [&] { return launch_gemm(qb, EPI_QKV, false, st); }));
 
     AttnArgs at;
     memset(&at, 0, sizeof at);
     at.Q = Q_; at.K = K_; at.Vt = Vt_; at.S = S; at.Sp = Sp; at.nh = s.NH; at.BH = B * s.NH;
     at.O = AO_; at.o_f32 = 0; at.ldo = H; at.omap = rowmap_dense(M);
     at.scale_log2 = 1.4426950408889634f;
-    TSN_TRY(launch_attention(at, st));
+    TSN_TRY(run(K_ATTN, 4.0 * B * s.NH * (double)S * S * 64, 8.0 * B * (double)S * H,
+                [&] { return launch_attention(at, st); }));
 
     GemmBatch ob;
     ob.nprob = 1;
+    ob.ws = ws_;
+    ob.ws_bytes = ws_bytes_;
     resid_problem(ob.p[0], AO_, H, D, 1, H, M, H, w.Wo, w.bo, X_, H, MOD_ + w.mod_off + 2 * H, NMOD);
-    TSN_TRY(launch_gemm(ob, EPI_RESID, false, st));
+    TSN_TRY(run(K_GEMM_RESID, gemm_flops(ob), gemm_bytes(ob, EPI_RESID), [&] { return launch_gemm(ob, EPI_RESID, false, st); }));
 
     ln_seg(ln.seg[0], X_, H, D, XN_, MOD_, NMOD, S, w.mod_off + 3 * H, M);
-    TSN_TRY(launch_ln_mod(ln, true, st));
+    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, true, st); }));
 
     GemmBatch f1;
     f1.nprob = 1;
     store_problem(f1.p[0], XN_, H, D, 1, H, M, s.F, w.W1, HF_, s.F, 1);
-    TSN_TRY(launch_gemm(f1, EPI_STORE, false, st));
+    TSN_TRY(run(K_GEMM_STORE, gemm_flops(f1), gemm_bytes(f1, EPI_STORE), [&] { return launch_gemm(f1, EPI_STORE, false, st); }));
 
     GemmBatch f2;
     f2.nprob = 1;
+    f2.ws = ws_;
+    f2.ws_bytes = ws_bytes_;
     resid_problem(f2.p[0], HF_, s.F, D, 1, s.F, M, H, w.W2, nullptr, X_, H, MOD_ + w.mod_off + 5 * H, NMOD);
-    return launch_gemm(f2, EPI_RESID, false, st);
+    return run(K_GEMM_RESID, gemm_flops(f2), gemm_bytes(f2, EPI_RESID), [&] { return launch_gemm(f2, EPI_RESID, false, st); });
 }
 
 int DitModel::enqueue_forward(const float *z, const float *t, const float *text, const float *pooled, float *v,
@@ -369,20 +424,21 @@ int DitModel::enqueue_forward(const float *z, const float *t, const float *text,
     const hipStream_t st = rt->dev.stream();
     const int B = s.B, H = s.H;
     // timestep embedding + MLP, g = t_emb + pooled, gs = silu(g)   (src/dit_fwd.cpp:111-140)
-    TSN_TRY(launch_temb_sinusoid(t, temb_, B, s.temb_dim, s.t_max_period, st));
+    TSN_TRY(run("temb_kernel", 0, 0, [&] { return launch_temb_sinusoid(t, temb_, B, s.temb_dim, s.t_max_period, st); }));
     GemvArgs g1;
     memset(&g1, 0, sizeof g1);
     g1.W = Wt0_; g1.ldw = s.temb_dim; g1.wdt = DT_BF16; g1.X = temb_; g1.ldx = s.temb_dim;
     g1.Y = h1_; g1.ldy = H; g1.bias = bt0_; g1.N = H; g1.K = s.temb_dim; g1.nb = B; g1.silu = 1;
-    TSN_TRY(launch_gemv(g1, st));
+    TSN_TRY(run(K_GEMV, 2.0 * B * H * s.temb_dim, 2.0 * H * s.temb_dim, [&] { return launch_gemv(g1, st); }));
     GemvArgs g2;
     memset(&g2, 0, sizeof g2);
     g2.W = Wt2_; g2.ldw = H; g2.wdt = DT_BF16; g2.X = h1_; g2.ldx = H;
     g2.Y = g_; g2.ldy = H; g2.bias = bt2_; g2.addv = pooled; g2.ld_add = H; g2.Y2 = gs_; g2.ldy2 = H;
     g2.N = H; g2.K = H; g2.nb = B;
-    TSN_TRY(launch_gemv(g2, st));
+    TSN_TRY(run(K_GEMV, 2.0 * B * H * H, 2.0 * H * H, [&] { return launch_gemv(g2, st); }));
     // every adaLN modulation of the eval in one HBM-bound GEMV (src/dit_fwd.cpp:186-207,271-274,288-291)
-    TSN_TRY(modulation(gs_, 0, NMOD));
+    TSN_TRY(run(K_GEMV, 2.0 * B * (double)NMOD * H, 2.0 * (double)NMOD * H + 4.0 * B * NMOD,
+                [&] { return modulation(gs_, 0, NMOD); }));
     // input projection and the text stream start (src/dit_fwd.cpp:142-149,166-167)
     LinArgs li;
     memset(&li, 0, sizeof li);
@@ -390,9 +446,12 @@ int DitModel::enqueue_forward(const float *z, const float *t, const float *text,
     li.W = Win_; li.ldw = s.latent; li.wdt = DT_BF16; li.bias = bin_;
     li.Y = X_; li.ldy = H; li.ymap = RowMap{s.La, S, 0};
     li.M = B * s.La; li.N = H; li.K = s.latent;
-    TSN_TRY(launch_linear_f32(li, st));
+    TSN_TRY(run(K_LIN, 2.0 * B * s.La * (double)H * s.latent, 4.0 * B * s.La * (double)(s.latent + H),
+                [&] { return launch_linear_f32(li, st); }));
     if (s.Lt > 0)
-        TSN_TRY(launch_copy_rows(text, H, rowmap_dense(B * s.Lt), X_, H, RowMap{s.Lt, S, s.La}, B * s.Lt, H, st));
+        TSN_TRY(run("copy_rows_kernel", 0, 8.0 * B * s.Lt * (double)H, [&] {
+            return launch_copy_rows(text, H, rowmap_dense(B * s.Lt), X_, H, RowMap{s.Lt, S, s.La}, B * s.Lt, H, st);
+        }));
     const size_t tap_n = (size_t)B * S * H;
     int tap = 0;
     for (int i = 0; i < s.n_joint; ++i) {
@@ -412,14 +471,15 @@ int DitModel::enqueue_forward(const float *z, const float *t, const float *text,
     g.Y = XF_; g.ldy = H; g.ymap = rowmap_dense(B * s.La);
     g.mod = MOD_; g.mod_ld = NMOD; g.mod_L = s.La; g.shift_off = fin_mod_off_; g.scale_off = fin_mod_off_ + H;
     g.rows = B * s.La;
-    TSN_TRY(launch_ln_mod(ln, false, st));
+    TSN_TRY(run(K_LN32, 0, ln_bytes(ln, false), [&] { return launch_ln_mod(ln, false, st); }));
     LinArgs lo;
     memset(&lo, 0, sizeof lo);
     lo.X = XF_; lo.ldx = H; lo.xmap = rowmap_dense(B * s.La);
     lo.W = Wfin_; lo.ldw = H; lo.wdt = DT_BF16; lo.bias = bfin_;
     lo.Y = v; lo.ldy = s.latent; lo.ymap = rowmap_dense(B * s.La);
     lo.M = B * s.La; lo.N = s.latent; lo.K = H;
-    return launch_linear_f32(lo, st);
+    return run(K_LIN, 2.0 * B * s.La * (double)H * s.latent, 4.0 * B * s.La * (double)(s.latent + H),
+               [&] { return launch_linear_f32(lo, st); });
 }
 
 int DitModel::enqueue_joint_block(int block, float *X, const float *g) {
@@ -525,6 +585,37 @@ int DitModel::replay() {
     TSN_TRY(rt->dev.make_current());
     TSN_HIP_CHECK(hipGraphLaunch(gexec_, rt->dev.stream()));
     return TSN_OK;
+}
+
+int DitModel::profile_forward(const float *z, const float *t, const float *text, const float *pooled, float *v,
+                              std::vector<KernelStat> &stats) {
+    std::vector<ProfRec> recs;
+    prof_ = &recs;
+    const int rc = enqueue_forward(z, t, text, pooled, v, nullptr);
+    prof_ = nullptr;
+    int rc2 = rt->dev.sync();
+    stats.clear();
+    for (auto &r : recs) {
+        float ms = 0.0f;
+        if (rc == TSN_OK && rc2 == TSN_OK && hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) rc2 = TSN_ERR_HIP;
+        hipEventDestroy(r.a);
+        hipEventDestroy(r.b);
+        KernelStat *k = nullptr;
+        for (auto &e : stats)
+            if (e.name == r.name) k = &e;
+        if (!k) {
+            stats.push_back(KernelStat{});
+            k = &stats.back();
+            k->name = r.name;
+        }
+        k->launches += 1;
+        k->ms += ms;
+        k->flops += r.flops;
+        k->bytes += r.bytes;
+    }
+    if (rc != TSN_OK) return rc;
+    if (rc2 != TSN_OK) set_error("profile: event timing failed");
+    return rc2;
 }
 
 int DitModel::prepare_sample(int steps) {

@@ -29,6 +29,15 @@ struct DitSpec {   // field meaning documented in include/tsn.h (tsn_dit_spec)
     float rope_theta, t_max_period, ln_eps, rms_eps;
 };
 
+// per-kernel statistics of one profiled evaluation (event pairs around every launch)
+struct KernelStat {
+    std::string name;   // kernel symbol
+    int launches = 0;
+    double ms = 0.0;     // summed event time
+    double flops = 0.0;  // algorithmic: 2*M*N*K per GEMM (conv K = taps*IC), 4*B*NH*S^2*64 attention
+    double bytes = 0.0;  // algorithmic HBM bytes (each operand once at its storage type)
+};
+
 struct ManifestEntry {
     std::string name;
     int64_t numel;
@@ -65,6 +74,10 @@ public:
     int capture_sample(float *x, const float *text, const float *pooled, int steps, float cfg);
     int replay();
 
+    // one eager evaluation with a HIP event pair around every launch; stats per kernel symbol
+    int profile_forward(const float *z, const float *t, const float *text, const float *pooled, float *v,
+                        std::vector<KernelStat> &stats);
+
     Runtime *rt = nullptr;
     DitSpec s{};
     int S = 0, Sp = 0, NMOD = 0;
@@ -82,6 +95,14 @@ private:
     int modulation(const float *gs, int row0, int rows);
     int gs_from_g(const float *g);
     int alloc(size_t bytes, void **p);
+    template <typename F>
+    int run(const char *name, double flops, double bytes, F &&launch);
+    struct ProfRec {
+        const char *name;
+        double flops, bytes;
+        hipEvent_t a, b;
+    };
+    std::vector<ProfRec> *prof_ = nullptr;
 
     std::vector<StreamW> ja_, jt_, fu_;
     const uint16_t *Wmod_ = nullptr, *Wt0_ = nullptr, *Wt2_ = nullptr, *Win_ = nullptr, *Wfin_ = nullptr;
@@ -93,6 +114,8 @@ private:
     int tsched_steps_ = 0;
     half_t *XN_ = nullptr, *Q_ = nullptr, *K_ = nullptr, *Vt_ = nullptr, *AO_ = nullptr, *HF_ = nullptr;
     void *wraw_ = nullptr, *wf16_ = nullptr;
+    float *ws_ = nullptr;            // split-K partials of the residual GEMMs
+    size_t ws_bytes_ = 0;
     bool ready_ = false;
     hipGraph_t graph_ = nullptr;
     hipGraphExec_t gexec_ = nullptr;

@@ -19,6 +19,8 @@
 
 #include <string.h>
 
+#include <algorithm>
+
 namespace tsn {
 
 namespace {
@@ -35,106 +37,12 @@ __device__ inline half8 zero_h8() { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
 
 __device__ inline float silu_f(float v) { return v / (1.0f + __expf(-v)); }
 
-template <bool A_F32, int EPI>
-__global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const GemmBatch bt) {
-    __shared__ __attribute__((aligned(16))) half_t sA[2][BM * LDSW];
-    __shared__ __attribute__((aligned(16))) half_t sB[2][BN * LDSW];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tile = xcd_remap(blockIdx.x, gridDim.x);
-    const int pi = (bt.nprob > 1 && tile >= bt.p[1].tile_start) ? 1 : 0;
-    const GemmProblem &P = bt.p[pi];
-
-    const int local = tile - P.tile_start;
-    const int tn = local / P.tiles_m, tm = local - tn * P.tiles_m;
-    const int m0 = tm * BM, n0 = tn * BN;
-    const int M = P.M, N = P.N, K = P.K;
-
-    // loader assignment: rows lrow + 32*r (r < 4), 16-byte chunk lch of the 64-wide K slab
-    const int lrow = tid >> 3, lch = tid & 7;
-    long long a_base[4];
-    int a_t[4];
-    bool a_ok[4];
-    const half_t *b_ptr[4];
-    bool b_ok[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int m = m0 + lrow + 32 * r;
-        a_ok[r] = m < M;
-        const int mm = a_ok[r] ? m : 0;
-        const int b = mm / P.amap.L;
-        a_t[r] = mm - b * P.amap.L;
-        a_base[r] = (long long)b * P.amap.seg + P.amap.off;
-        const int n = n0 + lrow + 32 * r;
-        b_ok[r] = n < N;
-        b_ptr[r] = P.W + (long long)(b_ok[r] ? n : 0) * P.ldw + lch * 8;
-    }
-
-    half8 ra[4], rb[4];
-    auto load_tile = [&](int k0) {
-        const int tap = k0 / P.Kc;
-        const int c = k0 - tap * P.Kc + lch * 8;
-        const bool kin = (k0 + lch * 8) < K;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int ts = a_t[r] - P.pad + tap;
-            const bool ok = a_ok[r] && kin && ts >= 0 && ts < P.a_T;
-            const long long off = (a_base[r] + ts) * (long long)P.lda + c;
-            if constexpr (A_F32) {
-                const float *ap = (const float *)P.A + off;
-                float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
-                if (ok) { x0 = *(const float4 *)ap; x1 = *(const float4 *)(ap + 4); }
-                ra[r] = half8{(half_t)x0.x, (half_t)x0.y, (half_t)x0.z, (half_t)x0.w,
-                              (half_t)x1.x, (half_t)x1.y, (half_t)x1.z, (half_t)x1.w};
-            } else {
-                ra[r] = ok ? *(const half8 *)((const half_t *)P.A + off) : zero_h8();
-            }
-            rb[r] = (b_ok[r] && kin) ? *(const half8 *)(b_ptr[r] + k0) : zero_h8();
-        }
-    };
-    auto store_tile = [&](int s) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            *(half8 *)&sA[s][(lrow + 32 * r) * LDSW + lch * 8] = ra[r];
-            *(half8 *)&sB[s][(lrow + 32 * r) * LDSW + lch * 8] = rb[r];
-        }
-    };
-
-    floatx4 acc[4][4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-    const int wm = wave >> 1, wn = wave & 1;
-    const int nk = (K + BK - 1) / BK;
-    load_tile(0);
-    store_tile(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int s = kt & 1;
-        if (kt + 1 < nk) load_tile((kt + 1) * BK);
-        const half_t *as = &sA[s][(wm * 64 + (lane & 15)) * LDSW + (lane >> 4) * 8];
-        const half_t *bs = &sB[s][(wn * 64 + (lane & 15)) * LDSW + (lane >> 4) * 8];
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            half8 af[4], bf[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) af[i] = *(const half8 *)(as + i * 16 * LDSW + ks * 32);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) bf[j] = *(const half8 *)(bs + j * 16 * LDSW + ks * 32);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
-        }
-        if (kt + 1 < nk) store_tile(s ^ 1);
-        __syncthreads();
-    }
-
-    // ---------------- epilogue ----------------
-    // acc[i][j][r] holds C[row][col]: row = wm*64 + i*16 + (lane>>4)*4 + r, col = wn*64 + j*16 + (lane&15)
+// Fused epilogue shared by both kernels. acc[i][j][r] holds C[row][col] of the wave's 64x64
+// block: row = wm*64 + i*16 + (lane>>4)*4 + r, col = wn*64 + j*16 + (lane&15).
+template <int EPI>
+__device__ __forceinline__ void gemm_epilogue(const GemmProblem &P, floatx4 (&acc)[4][4], int m0, int n0, int wm,
+                                              int wn, int lane) {
+    const int M = P.M, N = P.N;
     const int col_l = wn * 64 + (lane & 15);
     const int row_l = wm * 64 + (lane >> 4) * 4;
     if constexpr (EPI == EPI_STORE) {
@@ -253,6 +161,346 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const GemmBatch bt) {
     }
 }
 
+
+template <bool A_F32, int EPI>
+__global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const GemmBatch bt) {
+    __shared__ __attribute__((aligned(16))) half_t sA[2][BM * LDSW];
+    __shared__ __attribute__((aligned(16))) half_t sB[2][BN * LDSW];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tile = xcd_remap(blockIdx.x, gridDim.x);
+    const int pi = (bt.nprob > 1 && tile >= bt.p[1].tile_start) ? 1 : 0;
+    const GemmProblem &P = bt.p[pi];
+
+    const int local = tile - P.tile_start;
+    const int tn = local / P.tiles_m, tm = local - tn * P.tiles_m;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int M = P.M, N = P.N, K = P.K;
+
+    // loader assignment: rows lrow + 32*r (r < 4), 16-byte chunk lch of the 64-wide K slab
+    const int lrow = tid >> 3, lch = tid & 7;
+    long long a_base[4];
+    int a_t[4];
+    bool a_ok[4];
+    const half_t *b_ptr[4];
+    bool b_ok[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int m = m0 + lrow + 32 * r;
+        a_ok[r] = m < M;
+        const int mm = a_ok[r] ? m : 0;
+        const int b = mm / P.amap.L;
+        a_t[r] = mm - b * P.amap.L;
+        a_base[r] = (long long)b * P.amap.seg + P.amap.off;
+        const int n = n0 + lrow + 32 * r;
+        b_ok[r] = n < N;
+        b_ptr[r] = P.W + (long long)(b_ok[r] ? n : 0) * P.ldw + lch * 8;
+    }
+
+    half8 ra[4], rb[4];
+    auto load_tile = [&](int k0) {
+        const int tap = k0 / P.Kc;
+        const int c = k0 - tap * P.Kc + lch * 8;
+        const bool kin = (k0 + lch * 8) < K;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int ts = a_t[r] - P.pad + tap;
+            const bool ok = a_ok[r] && kin && ts >= 0 && ts < P.a_T;
+            const long long off = (a_base[r] + ts) * (long long)P.lda + c;
+            if constexpr (A_F32) {
+                const float *ap = (const float *)P.A + off;
+                float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0;
+                if (ok) { x0 = *(const float4 *)ap; x1 = *(const float4 *)(ap + 4); }
+                ra[r] = half8{(half_t)x0.x, (half_t)x0.y, (half_t)x0.z, (half_t)x0.w,
+                              (half_t)x1.x, (half_t)x1.y, (half_t)x1.z, (half_t)x1.w};
+            } else {
+                ra[r] = ok ? *(const half8 *)((const half_t *)P.A + off) : zero_h8();
+            }
+            rb[r] = (b_ok[r] && kin) ? *(const half8 *)(b_ptr[r] + k0) : zero_h8();
+        }
+    };
+    auto store_tile = [&](int s) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            *(half8 *)&sA[s][(lrow + 32 * r) * LDSW + lch * 8] = ra[r];
+            *(half8 *)&sB[s][(lrow + 32 * r) * LDSW + lch * 8] = rb[r];
+        }
+    };
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int wm = wave >> 1, wn = wave & 1;
+    const int nk = (K + BK - 1) / BK;
+    load_tile(0);
+    store_tile(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+        const int s = kt & 1;
+        if (kt + 1 < nk) load_tile((kt + 1) * BK);
+        const half_t *as = &sA[s][(wm * 64 + (lane & 15)) * LDSW + (lane >> 4) * 8];
+        const half_t *bs = &sB[s][(wn * 64 + (lane & 15)) * LDSW + (lane >> 4) * 8];
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            half8 af[4], bf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) af[i] = *(const half8 *)(as + i * 16 * LDSW + ks * 32);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bf[j] = *(const half8 *)(bs + j * 16 * LDSW + ks * 32);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) store_tile(s ^ 1);
+        __syncthreads();
+    }
+
+    gemm_epilogue<EPI>(P, acc, m0, n0, wm, wn, lane);
+}
+
+
+// ---------------------------------------------------------------------------------------------
+// Pipelined kernel (f16 A, K % 64 == 0): operands go global -> LDS with buffer_load_dwordx4 ... lds
+// (no register staging, see dma16), 4 LDS stages of one 128x64 A tile + one 128x64 W tile each (128 KB),
+// three K tiles in flight while the fourth is multiplied. One barrier per K tile.
+//
+// LDS layout of a stage: row r (128 B = 8 chunks of 8 halves) keeps chunk c at slot c ^ (r & 7).
+// A direct-to-LDS load writes lane l's 16 bytes to slot l of a 1 KB block (8 rows), so lane l of
+// block b loads row 8b + (l >> 3), chunk (l & 7) ^ (l >> 3). MFMA operand reads (lane: row
+// l & 15, chunk ks*4 + (l >> 4)) then touch 8 distinct 16-byte slots per 8 lanes: no bank
+// conflicts. Rows outside the problem (M tail, conv halo, N tail) get an out-of-range buffer
+// offset and the hardware writes zeros.
+// ---------------------------------------------------------------------------------------------
+typedef __attribute__((address_space(3))) char lds_char;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// raw buffer descriptor: base, stride 0, num_records 2^31-1, 32-bit data format; an offset at or
+// above 0x80000000 is out of range and reads as zero
+__device__ __forceinline__ i32x4 make_rsrc(const void *p) {
+    const unsigned long long a = (unsigned long long)p;
+    return i32x4{(int)(unsigned)a, (int)((a >> 32) & 0xFFFF), 0x7FFFFFFF, 0x00020000};
+}
+
+// 16 bytes per lane, global -> LDS slot (lane) of the 1 KB block at lds. Issued from inline asm so
+// the compiler's own LDS-DMA bookkeeping (which turns conservative at loop merges and would wait for
+// every load in flight) stays out of the pipeline; the kernel orders it with explicit vmcnt waits
+// and barriers. s_nop 0 covers the M0-write -> LDS-DMA hazard.
+__device__ __forceinline__ void dma16(i32x4 rs, unsigned voff, lds_char *lds) {
+    const unsigned l = __builtin_amdgcn_readfirstlane((unsigned)(unsigned long)lds);
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(voff), "s"(rs), "s"(l)
+                 : "memory");
+}
+
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    // s_waitcnt vmcnt(n) with expcnt/lgkmcnt left at their maxima (no wait on them)
+    if (n >= 16) __builtin_amdgcn_s_waitcnt((16 & 0xF) | (7 << 4) | (0xF << 8) | ((16 >> 4) << 14));
+    else if (n >= 8) __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (0xF << 8));
+    else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0xF << 8));
+}
+
+__device__ __forceinline__ void block_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int EPI>
+__global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(const GemmBatch bt) {
+    __shared__ __attribute__((aligned(1024))) half_t sA0[BM * BK], sA1[BM * BK], sA2[BM * BK], sA3[BM * BK];
+    __shared__ __attribute__((aligned(1024))) half_t sB0[BN * BK], sB1[BN * BK], sB2[BN * BK], sB3[BN * BK];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tile = xcd_remap(blockIdx.x, gridDim.x);
+    const int pi = (bt.nprob > 1 && tile >= bt.p[1].tile_start) ? 1 : 0;
+    const GemmProblem &P = bt.p[pi];
+    const int M = P.M, N = P.N, K = P.K, lda = P.lda, ldw = P.ldw, Kc = P.Kc, pad = P.pad, aT = P.a_T;
+    const RowMap am = P.amap;
+    // local tile -> (split, n tile, m tile), m fastest: neighbouring workgroups share W columns
+    const int local = tile - P.tile_start;
+    const int per_split = P.tiles_m * P.tiles_n;
+    const int ks = local / per_split;
+    const int rem = local - ks * per_split;
+    const int tn = rem / P.tiles_m, tm = rem - tn * P.tiles_m;
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const i32x4 rsa = make_rsrc(P.A);
+    const i32x4 rsb = make_rsrc(P.W);
+
+    // loader rows of this lane: wave*32 + i*8 + (lane >> 3), chunk (lane & 7) ^ (lane >> 3)
+    const int lr = lane >> 3, lc = (lane & 7) ^ lr;
+    int a_row0[4], a_t[4], b_off[4];
+    bool a_ok[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int r = wave * 32 + i * 8 + lr;
+        const int m = m0 + r;
+        a_ok[i] = m < M;
+        const int mm = a_ok[i] ? m : 0;
+        const int b = mm / am.L;
+        a_t[i] = mm - b * am.L;
+        a_row0[i] = b * am.seg + am.off;
+        const int n = n0 + r;
+        b_off[i] = n < N ? (n * ldw + lc * 8) * 2 : -1;
+    }
+    // this workgroup's K tiles: [kbeg, kbeg + nk)
+    const int nk = K / BK / P.splits;
+    const int kbeg = ks * nk;
+    auto issue = [&](int kt, half_t *sa, half_t *sb) {
+        const int k0 = (kbeg + kt) * BK;
+        const int tap = k0 / Kc;
+        const int kc0 = k0 - tap * Kc + lc * 8;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int ts = a_t[i] - pad + tap;
+            const bool ok = a_ok[i] && ts >= 0 && ts < aT;
+            const unsigned vo = ok ? (unsigned)(((a_row0[i] + ts) * lda + kc0) * 2) : 0x80000000u;
+            dma16(rsa, vo, (lds_char *)sa + (wave * 4 + i) * 1024);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const unsigned vo = b_off[i] >= 0 ? (unsigned)(b_off[i] + k0 * 2) : 0x80000000u;
+            dma16(rsb, vo, (lds_char *)sb + (wave * 4 + i) * 1024);
+        }
+    };
+
+    floatx4 acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int wm = wave >> 1, wn = wave & 1;
+    // operand read offsets (halves) inside a stage for k-substep 0 and 1
+    int a_rd[2][4], b_rd[2][4];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int slot = (ks * 4 + (lane >> 4)) ^ (lane & 7);
+            a_rd[ks][i] = (wm * 64 + i * 16 + (lane & 15)) * BK + slot * 8;
+            b_rd[ks][i] = (wn * 64 + i * 16 + (lane & 15)) * BK + slot * 8;
+        }
+    auto compute = [&](const half_t *sa, const half_t *sb) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            half8 af[4], bf[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) af[i] = *(const half8 *)(sa + a_rd[ks][i]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) bf[j] = *(const half8 *)(sb + b_rd[ks][j]);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    issue(0, sA0, sB0);
+    if (nk > 1) issue(1, sA1, sB1);
+    if (nk > 2) issue(2, sA2, sB2);
+    // Loop invariant at the top of an iteration: tile kt has landed in stage kt%4 for every wave,
+    // tiles kt+1..kt+3 are in flight. Each step multiplies one stage, waits for its own DMAs of the
+    // next tile, meets the other waves at the barrier (the stage just used is now free) and refills
+    // that stage four tiles ahead. The prologue leaves the same in-flight pattern as the back-edge,
+    // and the unrolled body has no conditions, so the compiler's per-stage DMA tracking stays exact.
+    wait_vmcnt(8 * min(nk - 1, 2));
+    block_barrier();
+    if (nk > 3) issue(3, sA3, sB3);
+#define TSN_GEMM_STEP(NEXT, CA, CB)                                                             \
+    {                                                                                           \
+        compute(CA, CB);                                                                        \
+        wait_vmcnt(16);                                                                         \
+        block_barrier();                                                                        \
+        issue(NEXT, CA, CB);                                                                    \
+    }
+    int kt = 0;
+    for (; kt + 8 <= nk; kt += 4) {
+        TSN_GEMM_STEP(kt + 4, sA0, sB0)
+        TSN_GEMM_STEP(kt + 5, sA1, sB1)
+        TSN_GEMM_STEP(kt + 6, sA2, sB2)
+        TSN_GEMM_STEP(kt + 7, sA3, sB3)
+    }
+#undef TSN_GEMM_STEP
+    // tail: the last < 8 tiles; tile kt is visible, kt+1..min(kt+3, nk-1) in flight
+#define TSN_GEMM_TAIL(CA, CB)                                                                   \
+    {                                                                                           \
+        compute(CA, CB);                                                                        \
+        if (kt + 1 < nk) {                                                                      \
+            wait_vmcnt(8 * min(nk - 2 - kt, 2));                                                \
+            block_barrier();                                                                    \
+            if (kt + 4 < nk) issue(kt + 4, CA, CB);                                             \
+        }                                                                                       \
+    }
+    for (; kt < nk; ++kt) {
+        switch (kt & 3) {
+            case 0: TSN_GEMM_TAIL(sA0, sB0) break;
+            case 1: TSN_GEMM_TAIL(sA1, sB1) break;
+            case 2: TSN_GEMM_TAIL(sA2, sB2) break;
+            default: TSN_GEMM_TAIL(sA3, sB3) break;
+        }
+    }
+#undef TSN_GEMM_TAIL
+    wait_vmcnt(0);
+    if (P.splits > 1) {
+        // raw f32 partial of this split: ws[(ks*M + m)*N + n]
+        float *w = P.ws + (long long)ks * M * N;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int m = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
+                if (m >= M) continue;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int n = n0 + wn * 64 + j * 16 + (lane & 15);
+                    if (n < N) w[(long long)m * N + n] = acc[i][j][r];
+                }
+            }
+        return;
+    }
+    gemm_epilogue<EPI>(P, acc, m0, n0, wm, wn, lane);
+}
+
+// split-K reduction + residual epilogue: R[rmap(m)][n] += gate[m/gate_L][n] * (sum_ks ws[ks][m][n] + bias[n]),
+// the partials summed in split order (deterministic). One thread per 4 columns.
+__global__ __launch_bounds__(256) void splitk_resid_kernel(const GemmBatch bt) {
+    long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    int pi = 0;
+    long long n0 = (long long)bt.p[0].M * bt.p[0].N / 4;
+    if (bt.p[0].splits <= 1) n0 = 0;
+    if (idx >= n0) {
+        pi = 1;
+        idx -= n0;
+        if (bt.nprob < 2 || bt.p[1].splits <= 1 || idx >= (long long)bt.p[1].M * bt.p[1].N / 4) return;
+    }
+    const GemmProblem &P = bt.p[pi];
+    const int n4 = P.N / 4;
+    const int m = (int)(idx / n4), n = (int)(idx - (long long)m * n4) * 4;
+    float4 v = *(const float4 *)(P.ws + (long long)m * P.N + n);
+    for (int k = 1; k < P.splits; ++k) {
+        const float4 u = *(const float4 *)(P.ws + ((long long)k * P.M + m) * P.N + n);
+        v.x += u.x; v.y += u.y; v.z += u.z; v.w += u.w;
+    }
+    if (P.bias) {
+        const float4 b = *(const float4 *)(P.bias + n);
+        v.x += b.x; v.y += b.y; v.z += b.z; v.w += b.w;
+    }
+    const float4 g = *(const float4 *)(P.gate + (long long)(m / P.gate_L) * P.gate_ld + n);
+    float4 *xr = (float4 *)(P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n);
+    float4 x = *xr;
+    x.x = x.x + v.x * g.x; x.y = x.y + v.y * g.y; x.z = x.z + v.z * g.z; x.w = x.w + v.w * g.w;
+    *xr = x;
+}
+
+
 } // namespace
 
 void gemm_problem_init(GemmProblem &p) {
@@ -261,6 +509,7 @@ void gemm_problem_init(GemmProblem &p) {
     p.gate_L = 1;
     p.q_L = 1;
     p.q_scale = 1.0f;
+    p.splits = 1;
 }
 
 int launch_gemm(GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
@@ -289,8 +538,72 @@ int launch_gemm(GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
         tiles += p.tiles_m * p.tiles_n;
     }
     b.total_tiles = tiles;
+    // the pipelined kernel needs f16 A, whole 64-wide K tiles that never straddle a conv tap,
+    // 16-byte aligned rows, and every operand byte offset below 2^31 (buffer addressing)
+    bool pipe = !a_f32;
+    for (int i = 0; i < b.nprob && pipe; ++i) {
+        const GemmProblem &p = b.p[i];
+        const long long last_row = rowmap_phys(p.amap, p.M - 1) + p.a_T;
+        pipe = p.K % BK == 0 && p.Kc % BK == 0 && p.lda % 8 == 0 && p.ldw % 8 == 0 &&
+               (last_row + 1) * (long long)p.lda * 2 < (1LL << 31) && (long long)p.N * p.ldw * 2 < (1LL << 31);
+    }
+    // Split-K (pipelined kernel, residual epilogue, workspace given): one common K chunk of kc
+    // tiles for every problem, the largest kc (>= 4) that divides every problem's K tiles and gives
+    // at least 224 workgroups; otherwise the smallest such kc. Partials need splits*M*N floats.
+    for (int i = 0; i < b.nprob; ++i) { b.p[i].splits = 1; b.p[i].ws = nullptr; }
+    if (pipe && epi == EPI_RESID && b.ws) {
+        int nkmin = 1 << 30;
+        for (int i = 0; i < b.nprob; ++i) nkmin = std::min(nkmin, b.p[i].K / BK);
+        int best = 0;
+        for (int kc = nkmin; kc >= 4; --kc) {
+            bool divides = true;
+            long long wg = 0;
+            for (int i = 0; i < b.nprob; ++i) {
+                const int nkp = b.p[i].K / BK;
+                divides = divides && nkp % kc == 0;
+                wg += (long long)b.p[i].tiles_m * b.p[i].tiles_n * (nkp / kc);
+            }
+            if (!divides) continue;
+            best = kc;
+            if (wg >= 224) break;
+        }
+        if (best > 0 && best < nkmin + 1) {
+            size_t need = 0;
+            for (int i = 0; i < b.nprob; ++i)
+                need += (size_t)(b.p[i].K / BK / best) * b.p[i].M * b.p[i].N * sizeof(float);
+            bool any = false;
+            for (int i = 0; i < b.nprob; ++i) any = any || (b.p[i].K / BK / best) > 1;
+            if (any && need <= b.ws_bytes) {
+                size_t off = 0;
+                tiles = 0;
+                for (int i = 0; i < b.nprob; ++i) {
+                    GemmProblem &p = b.p[i];
+                    p.splits = p.K / BK / best;
+                    if (p.splits > 1) {
+                        TSN_REQUIRE(p.N % 4 == 0 && p.ldr % 4 == 0 && p.gate_ld % 4 == 0, "gemm split-K: N, ldr, gate_ld % 4");
+                        p.ws = b.ws + off / sizeof(float);
+                        off += (size_t)p.splits * p.M * p.N * sizeof(float);
+                    }
+                    p.tile_start = tiles;
+                    tiles += p.tiles_m * p.tiles_n * p.splits;
+                }
+                b.total_tiles = tiles;
+            }
+        }
+    }
     dim3 grid(tiles), block(256);
-    if (a_f32) {
+    if (pipe) {
+        if (epi == EPI_STORE) hipLaunchKernelGGL((gemm_pipe_kernel<EPI_STORE>), grid, block, 0, st, b);
+        else if (epi == EPI_RESID) hipLaunchKernelGGL((gemm_pipe_kernel<EPI_RESID>), grid, block, 0, st, b);
+        else if (epi == EPI_QKV) hipLaunchKernelGGL((gemm_pipe_kernel<EPI_QKV>), grid, block, 0, st, b);
+        else { set_error("gemm: unknown epilogue"); return TSN_ERR_ARG; }
+        TSN_HIP_CHECK(hipGetLastError());
+        long long red = 0;
+        for (int i = 0; i < b.nprob; ++i)
+            if (b.p[i].splits > 1) red += (long long)b.p[i].M * b.p[i].N / 4;
+        if (red > 0)
+            hipLaunchKernelGGL(splitk_resid_kernel, dim3((unsigned)((red + 255) / 256)), dim3(256), 0, st, b);
+    } else if (a_f32) {
         TSN_REQUIRE(epi == EPI_STORE, "gemm: f32 A operand only with a plain store epilogue");
         hipLaunchKernelGGL((gemm_f16_kernel<true, EPI_STORE>), grid, block, 0, st, b);
     } else if (epi == EPI_STORE) {

@@ -33,12 +33,19 @@ struct GemmProblem {
     const float *rope;                 // [pos][32][2] (cos, sin)
     // filled by the launcher
     int tile_start, tiles_m, tiles_n;
+    // split-K (filled by the launcher): splits > 1 writes f32 partials [splits][M][N] at ws, and a
+    // second kernel sums them in split order and applies the epilogue
+    int splits;
+    float *ws;
 };
 
 struct GemmBatch {
     GemmProblem p[2];
-    int nprob;
-    int total_tiles;
+    int nprob = 0;
+    int total_tiles = 0;
+    // optional f32 workspace for split-K partials (EPI_RESID only); null disables split-K
+    float *ws = nullptr;
+    size_t ws_bytes = 0;
 };
 
 // a_f32: A operand is f32 (converted to f16 on load). All problems share the epilogue kind.

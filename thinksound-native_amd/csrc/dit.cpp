@@ -99,7 +99,8 @@ int DitModel::create(Runtime *r, const DitSpec &sp) {
     TSN_TRY(af(&gs_, B * H));
     TSN_TRY(af(&temb_, B * s.temb_dim));
     TSN_TRY(af(&h1_, B * H));
-    TSN_TRY(af(&XF_, B * s.La * H));
+    TSN_TRY(ah(&XF2_, B * s.La * 2 * H));
+    TSN_TRY(ah(&Z2_, B * s.La * 2 * (size_t)s.latent));
     TSN_TRY(af(&Vv_, B * s.La * s.latent));
     TSN_TRY(af(&x2_, B * s.La * s.latent));
     TSN_TRY(af(&t_dev, B));
@@ -204,8 +205,15 @@ int DitModel::upload_weights(const uint16_t *host, size_t numel) {
     // GEMV / f32-linear weights are read as bf16 straight from the uploaded buffer
     Wt0_ = raw("t_embed.mlp.0.weight");
     Wt2_ = raw("t_embed.mlp.2.weight");
-    Win_ = raw("audio_input_proj.weight");
-    Wfin_ = raw("final_layer.linear.weight");
+    {
+        half_t *w;
+        TSN_TRY(alloc((size_t)H * 2 * s.latent * 2, (void **)&w));
+        TSN_TRY(launch_dup_cols_bf16_to_f16(raw("audio_input_proj.weight"), w, (int)H, s.latent, st));
+        Win2_ = w;
+        TSN_TRY(alloc((size_t)s.latent * 2 * H * 2, (void **)&w));
+        TSN_TRY(launch_dup_cols_bf16_to_f16(raw("final_layer.linear.weight"), w, s.latent, (int)H, st));
+        Wfin2_ = w;
+    }
     TSN_TRY(f32("t_embed.mlp.0.bias", &bt0_));
     TSN_TRY(f32("t_embed.mlp.2.bias", &bt2_));
     TSN_TRY(f32("audio_input_proj.bias", &bin_));
@@ -269,14 +277,11 @@ void ln_seg(LnSeg &g, const float *X, int H, RowMap map, half_t *Y, const float 
     g.rows = rows;
 }
 
-constexpr const char *K_GEMM_STORE = "gemm_f16_kernel<false, 0>";
-constexpr const char *K_GEMM_RESID = "gemm_f16_kernel<false, 1>";
-constexpr const char *K_GEMM_QKV = "gemm_f16_kernel<false, 2>";
 constexpr const char *K_ATTN = "flash_attn_kernel";
 constexpr const char *K_GEMV = "gemv_kernel";
-constexpr const char *K_LN16 = "ln_mod_kernel<true, 4>";
-constexpr const char *K_LN32 = "ln_mod_kernel<false, 4>";
-constexpr const char *K_LIN = "linear_f32_kernel";
+constexpr const char *K_LN16 = "ln_mod_kernel<1, 4>";
+constexpr const char *K_LNHL = "ln_mod_kernel<2, 4>";
+constexpr const char *K_SPLIT = "split_hilo_kernel";
 
 double gemm_flops(const GemmBatch &b) {
     double f = 0;
@@ -313,6 +318,19 @@ int DitModel::run(const char *name, double flops, double bytes, F &&launch) {
     return rc;
 }
 
+// plan, launch (timed under the kernel's own symbol) and, when K was split, reduce
+int DitModel::gemm_run(GemmBatch &b, int epi) {
+    const hipStream_t st = rt->dev.stream();
+    TSN_TRY(gemm_plan(b, epi, false));
+    TSN_TRY(run(b.kname, gemm_flops(b), gemm_bytes(b, epi), [&] { return gemm_launch_planned(b, epi, false, st); }));
+    if (!gemm_needs_reduce(b)) return TSN_OK;
+    double red = 0;
+    for (int i = 0; i < b.nprob; ++i)
+        if (b.p[i].splits > 1) red += (4.0 * b.p[i].splits + (epi == EPI_RESID ? 8.0 : 4.0)) * b.p[i].M * (double)b.p[i].N;
+    return run(epi == EPI_RESID ? "splitk_reduce_kernel<1>" : "splitk_reduce_kernel<0>", 0, red,
+               [&] { return launch_gemm_reduce(b, epi, st); });
+}
+
 // Joint block: src/dit_fwd.cpp:180-257 (pre_attn :24-49, attention :83-102, post_attn :51-81)
 int DitModel::block_joint(int i) {
     const hipStream_t st = rt->dev.stream();
@@ -324,13 +342,13 @@ int DitModel::block_joint(int i) {
     ln.nseg = 2; ln.H = H; ln.eps = s.ln_eps;
     ln_seg(ln.seg[0], X_, H, Sa, XN_, MOD_, NMOD, La, a.mod_off, B * La);
     ln_seg(ln.seg[1], X_, H, St, XN_, MOD_, NMOD, Lt, t.mod_off, B * Lt);
-    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, true, st); }));
+    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16, st); }));
 
     GemmBatch qb;
     qb.nprob = 2;
     qkv_problem(qb.p[0], XN_, Sa, B * La, a.Wqkv, a.bqkv, a.qn, a.kn, H, s.NH, Q_, K_, Vt_, S, Sp, La, 0, La, rope_, s.rms_eps);
     qkv_problem(qb.p[1], XN_, St, B * Lt, t.Wqkv, t.bqkv, t.qn, t.kn, H, s.NH, Q_, K_, Vt_, S, Sp, Lt, La, 0, rope_, s.rms_eps);
-    TSN_TRY(run(K_GEMM_QKV, gemm_flops(qb), gemm_bytes(qb, EPI_QKV), [&] { return launch_gemm(qb, EPI_QKV, false, st); }));
+    TSN_TRY(gemm_run(qb, EPI_QKV));
 
     AttnArgs at;
     memset(&at, 0, sizeof at);
@@ -346,18 +364,18 @@ int DitModel::block_joint(int i) {
     ob.ws_bytes = ws_bytes_;
     resid_problem(ob.p[0], AO_, H, Sa, 1, H, B * La, H, a.Wo, a.bo, X_, H, MOD_ + a.mod_off + 2 * H, NMOD);
     resid_problem(ob.p[1], AO_, H, St, 1, H, B * Lt, H, t.Wo, t.bo, X_, H, MOD_ + t.mod_off + 2 * H, NMOD);
-    TSN_TRY(run(K_GEMM_RESID, gemm_flops(ob), gemm_bytes(ob, EPI_RESID), [&] { return launch_gemm(ob, EPI_RESID, false, st); }));
+    TSN_TRY(gemm_run(ob, EPI_RESID));
 
     ln_seg(ln.seg[0], X_, H, Sa, XN_, MOD_, NMOD, La, a.mod_off + 3 * H, B * La);
     ln_seg(ln.seg[1], X_, H, St, XN_, MOD_, NMOD, Lt, t.mod_off + 3 * H, B * Lt);
-    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, true, st); }));
+    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16, st); }));
 
     const int ta = a.conv ? 3 : 1;
     GemmBatch f1;
     f1.nprob = 2;
     store_problem(f1.p[0], XN_, H, Sa, ta, H, B * La, s.F, a.W1, HF_, s.F, 1);
     store_problem(f1.p[1], XN_, H, St, 1, H, B * Lt, s.F, t.W1, HF_, s.F, 1);
-    TSN_TRY(run(K_GEMM_STORE, gemm_flops(f1), gemm_bytes(f1, EPI_STORE), [&] { return launch_gemm(f1, EPI_STORE, false, st); }));
+    TSN_TRY(gemm_run(f1, EPI_STORE));
 
     GemmBatch f2;
     f2.nprob = 2;
@@ -365,7 +383,7 @@ int DitModel::block_joint(int i) {
     f2.ws_bytes = ws_bytes_;
     resid_problem(f2.p[0], HF_, s.F, Sa, ta, s.F, B * La, H, a.W2, nullptr, X_, H, MOD_ + a.mod_off + 5 * H, NMOD);
     resid_problem(f2.p[1], HF_, s.F, St, 1, s.F, B * Lt, H, t.W2, nullptr, X_, H, MOD_ + t.mod_off + 5 * H, NMOD);
-    return run(K_GEMM_RESID, gemm_flops(f2), gemm_bytes(f2, EPI_RESID), [&] { return launch_gemm(f2, EPI_RESID, false, st); });
+    return gemm_run(f2, EPI_RESID);
 }
 
 // Fused block: src/dit_fwd.cpp:267-279 over the joined rows
@@ -378,12 +396,12 @@ int DitModel::block_fused(int i) {
     memset(&ln, 0, sizeof ln);
     ln.nseg = 1; ln.H = H; ln.eps = s.ln_eps;
     ln_seg(ln.seg[0], X_, H, D, XN_, MOD_, NMOD, S, w.mod_off, M);
-    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, true, st); }));
+    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16, st); }));
 
     GemmBatch qb;
     qb.nprob = 1;
     qkv_problem(qb.p[0], XN_, D, M, w.Wqkv, w.bqkv, w.qn, w.kn, H, s.NH, Q_, K_, Vt_, S, Sp, S, 0, s.La, rope_, s.rms_eps);
-    TSN_TRY(run(K_GEMM_QKV, gemm_flops(qb), gemm_bytes(qb, EPI_QKV), [&] { return launch_gemm(qb, EPI_QKV, false, st); }));
+    TSN_TRY(gemm_run(qb, EPI_QKV));
 
     AttnArgs at;
     memset(&at, 0, sizeof at);
@@ -398,22 +416,22 @@ int DitModel::block_fused(int i) {
     ob.ws = ws_;
     ob.ws_bytes = ws_bytes_;
     resid_problem(ob.p[0], AO_, H, D, 1, H, M, H, w.Wo, w.bo, X_, H, MOD_ + w.mod_off + 2 * H, NMOD);
-    TSN_TRY(run(K_GEMM_RESID, gemm_flops(ob), gemm_bytes(ob, EPI_RESID), [&] { return launch_gemm(ob, EPI_RESID, false, st); }));
+    TSN_TRY(gemm_run(ob, EPI_RESID));
 
     ln_seg(ln.seg[0], X_, H, D, XN_, MOD_, NMOD, S, w.mod_off + 3 * H, M);
-    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, true, st); }));
+    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16, st); }));
 
     GemmBatch f1;
     f1.nprob = 1;
     store_problem(f1.p[0], XN_, H, D, 1, H, M, s.F, w.W1, HF_, s.F, 1);
-    TSN_TRY(run(K_GEMM_STORE, gemm_flops(f1), gemm_bytes(f1, EPI_STORE), [&] { return launch_gemm(f1, EPI_STORE, false, st); }));
+    TSN_TRY(gemm_run(f1, EPI_STORE));
 
     GemmBatch f2;
     f2.nprob = 1;
     f2.ws = ws_;
     f2.ws_bytes = ws_bytes_;
     resid_problem(f2.p[0], HF_, s.F, D, 1, s.F, M, H, w.W2, nullptr, X_, H, MOD_ + w.mod_off + 5 * H, NMOD);
-    return run(K_GEMM_RESID, gemm_flops(f2), gemm_bytes(f2, EPI_RESID), [&] { return launch_gemm(f2, EPI_RESID, false, st); });
+    return gemm_run(f2, EPI_RESID);
 }
 
 int DitModel::enqueue_forward(const float *z, const float *t, const float *text, const float *pooled, float *v,
@@ -439,15 +457,22 @@ int DitModel::enqueue_forward(const float *z, const float *t, const float *text,
     // every adaLN modulation of the eval in one HBM-bound GEMV (src/dit_fwd.cpp:186-207,271-274,288-291)
     TSN_TRY(run(K_GEMV, 2.0 * B * (double)NMOD * H, 2.0 * (double)NMOD * H + 4.0 * B * NMOD,
                 [&] { return modulation(gs_, 0, NMOD); }));
-    // input projection and the text stream start (src/dit_fwd.cpp:142-149,166-167)
-    LinArgs li;
-    memset(&li, 0, sizeof li);
-    li.X = z; li.ldx = s.latent; li.xmap = rowmap_dense(B * s.La);
-    li.W = Win_; li.ldw = s.latent; li.wdt = DT_BF16; li.bias = bin_;
-    li.Y = X_; li.ldy = H; li.ymap = RowMap{s.La, S, 0};
-    li.M = B * s.La; li.N = H; li.K = s.latent;
-    TSN_TRY(run(K_LIN, 2.0 * B * s.La * (double)H * s.latent, 4.0 * B * s.La * (double)(s.latent + H),
-                [&] { return launch_linear_f32(li, st); }));
+    // input projection (src/dit_fwd.cpp:142-149): z split into f16 hi|lo halves, one MFMA GEMM
+    // against [W|W] (f32-accurate), bias added, written into the audio rows of X
+    TSN_TRY(run(K_SPLIT, 0, 8.0 * B * s.La * s.latent, [&] {
+        return launch_split_hilo(z, s.latent, rowmap_dense(B * s.La), Z2_, B * s.La, s.latent, st);
+    }));
+    {
+        GemmBatch ib;
+        ib.nprob = 1;
+        GemmProblem &p = ib.p[0];
+        gemm_problem_init(p);
+        p.A = Z2_; p.lda = 2 * s.latent; p.amap = rowmap_dense(B * s.La); p.taps = 1; p.Kc = 2 * s.latent;
+        p.a_T = B * s.La; p.W = Win2_; p.ldw = 2 * s.latent; p.bias = bin_;
+        p.M = B * s.La; p.N = H; p.K = 2 * s.latent;
+        p.Y = X_; p.ldy = H; p.ymap = RowMap{s.La, S, 0}; p.y_f16 = 0;
+        TSN_TRY(gemm_run(ib, EPI_STORE));
+    }
     if (s.Lt > 0)
         TSN_TRY(run("copy_rows_kernel", 0, 8.0 * B * s.Lt * (double)H, [&] {
             return launch_copy_rows(text, H, rowmap_dense(B * s.Lt), X_, H, RowMap{s.Lt, S, s.La}, B * s.Lt, H, st);
@@ -462,24 +487,28 @@ int DitModel::enqueue_forward(const float *z, const float *t, const float *text,
         TSN_TRY(block_fused(i));
         if (taps) TSN_TRY(rt->dev.copy_d2d(taps + tap_n * tap++, X_, tap_n * 4));
     }
-    // final layer: adaLN (2 chunks) on audio rows, projection to latent (src/dit_fwd.cpp:287-303)
+    // final layer: adaLN (2 chunks) on audio rows as f16 hi|lo, projection to latent by one MFMA
+    // GEMM against [W|W] (f32-accurate), split over K (src/dit_fwd.cpp:287-303)
     LnArgs ln;
     memset(&ln, 0, sizeof ln);
     ln.nseg = 1; ln.H = H; ln.eps = s.ln_eps;
     LnSeg &g = ln.seg[0];
     g.X = X_; g.ldx = H; g.xmap = RowMap{s.La, S, 0};
-    g.Y = XF_; g.ldy = H; g.ymap = rowmap_dense(B * s.La);
+    g.Y = XF2_; g.ldy = 2 * H; g.ymap = rowmap_dense(B * s.La);
     g.mod = MOD_; g.mod_ld = NMOD; g.mod_L = s.La; g.shift_off = fin_mod_off_; g.scale_off = fin_mod_off_ + H;
     g.rows = B * s.La;
-    TSN_TRY(run(K_LN32, 0, ln_bytes(ln, false), [&] { return launch_ln_mod(ln, false, st); }));
-    LinArgs lo;
-    memset(&lo, 0, sizeof lo);
-    lo.X = XF_; lo.ldx = H; lo.xmap = rowmap_dense(B * s.La);
-    lo.W = Wfin_; lo.ldw = H; lo.wdt = DT_BF16; lo.bias = bfin_;
-    lo.Y = v; lo.ldy = s.latent; lo.ymap = rowmap_dense(B * s.La);
-    lo.M = B * s.La; lo.N = s.latent; lo.K = H;
-    return run(K_LIN, 2.0 * B * s.La * (double)H * s.latent, 4.0 * B * s.La * (double)(s.latent + H),
-               [&] { return launch_linear_f32(lo, st); });
+    TSN_TRY(run(K_LNHL, 0, B * s.La * (double)H * 8.0, [&] { return launch_ln_mod(ln, LN_F16_HILO, st); }));
+    GemmBatch fb;
+    fb.nprob = 1;
+    fb.ws = ws_;
+    fb.ws_bytes = ws_bytes_;
+    GemmProblem &p = fb.p[0];
+    gemm_problem_init(p);
+    p.A = XF2_; p.lda = 2 * H; p.amap = rowmap_dense(B * s.La); p.taps = 1; p.Kc = 2 * H; p.a_T = B * s.La;
+    p.W = Wfin2_; p.ldw = 2 * H; p.bias = bfin_;
+    p.M = B * s.La; p.N = s.latent; p.K = 2 * H;
+    p.Y = v; p.ldy = s.latent; p.ymap = rowmap_dense(B * s.La); p.y_f16 = 0;
+    return gemm_run(fb, EPI_STORE);
 }
 
 int DitModel::enqueue_joint_block(int block, float *X, const float *g) {

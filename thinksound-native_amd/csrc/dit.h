@@ -97,6 +97,7 @@ private:
     int alloc(size_t bytes, void **p);
     template <typename F>
     int run(const char *name, double flops, double bytes, F &&launch);
+    int gemm_run(GemmBatch &b, int epi);
     struct ProfRec {
         const char *name;
         double flops, bytes;
@@ -105,12 +106,14 @@ private:
     std::vector<ProfRec> *prof_ = nullptr;
 
     std::vector<StreamW> ja_, jt_, fu_;
-    const uint16_t *Wmod_ = nullptr, *Wt0_ = nullptr, *Wt2_ = nullptr, *Win_ = nullptr, *Wfin_ = nullptr;
+    const uint16_t *Wmod_ = nullptr, *Wt0_ = nullptr, *Wt2_ = nullptr;
+    const half_t *Win2_ = nullptr, *Wfin2_ = nullptr;   // [W|W] f16 for the hi|lo projections
     const float *bmod_ = nullptr, *bt0_ = nullptr, *bt2_ = nullptr, *bin_ = nullptr, *bfin_ = nullptr;
     int fin_mod_off_ = 0;
     float *rope_ = nullptr;
     float *X_ = nullptr, *MOD_ = nullptr, *g_ = nullptr, *gs_ = nullptr, *temb_ = nullptr, *h1_ = nullptr;
-    float *XF_ = nullptr, *Vv_ = nullptr, *x2_ = nullptr, *tsched_ = nullptr;
+    half_t *XF2_ = nullptr, *Z2_ = nullptr;               // hi|lo operands of the projections
+    float *Vv_ = nullptr, *x2_ = nullptr, *tsched_ = nullptr;
     int tsched_steps_ = 0;
     half_t *XN_ = nullptr, *Q_ = nullptr, *K_ = nullptr, *Vt_ = nullptr, *AO_ = nullptr, *HF_ = nullptr;
     void *wraw_ = nullptr, *wf16_ = nullptr;

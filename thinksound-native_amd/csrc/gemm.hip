@@ -265,9 +265,14 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const GemmBatch bt) {
 
 
 // ---------------------------------------------------------------------------------------------
-// Pipelined kernel (f16 A, K % 64 == 0): operands go global -> LDS with buffer_load_dwordx4 ... lds
-// (no register staging, see dma16), 4 LDS stages of one 128x64 A tile + one 128x64 W tile each (128 KB),
-// three K tiles in flight while the fourth is multiplied. One barrier per K tile.
+// Pipelined kernel (f16 A, K % 64 == 0). 512 threads = 8 waves, two per SIMD: waves 0-3 and 4-7
+// own the same four 64x64 output quadrants and split every 64-wide K tile between them (k 0..31 /
+// 32..63); the halves are summed through LDS at the end. Two waves per SIMD let one wave's LDS
+// reads hide behind the other's MFMAs, which a single wave per SIMD cannot do.
+//
+// Operands go global -> LDS with buffer_load_dwordx4 ... lds (no register staging, see dma16) into
+// 4 stages of one 128x64 A tile + one 128x64 W tile each (128 KB): three K tiles are in flight
+// while the fourth is multiplied, with one barrier per K tile.
 //
 // LDS layout of a stage: row r (128 B = 8 chunks of 8 halves) keeps chunk c at slot c ^ (r & 7).
 // A direct-to-LDS load writes lane l's 16 bytes to slot l of a 1 KB block (8 rows), so lane l of
@@ -298,10 +303,11 @@ __device__ __forceinline__ void dma16(i32x4 rs, unsigned voff, lds_char *lds) {
                  : "memory");
 }
 
+// s_waitcnt vmcnt(n) (n in {0, 4, 8, 12}) with expcnt/lgkmcnt left at their maxima
 __device__ __forceinline__ void wait_vmcnt(int n) {
-    // s_waitcnt vmcnt(n) with expcnt/lgkmcnt left at their maxima (no wait on them)
-    if (n >= 16) __builtin_amdgcn_s_waitcnt((16 & 0xF) | (7 << 4) | (0xF << 8) | ((16 >> 4) << 14));
+    if (n >= 12) __builtin_amdgcn_s_waitcnt(12 | (7 << 4) | (0xF << 8));
     else if (n >= 8) __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (0xF << 8));
+    else if (n >= 4) __builtin_amdgcn_s_waitcnt(4 | (7 << 4) | (0xF << 8));
     else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0xF << 8));
 }
 
@@ -311,19 +317,167 @@ __device__ __forceinline__ void block_barrier() {
     asm volatile("" ::: "memory");
 }
 
+constexpr int STAGE = BM * BK;   // halves per operand tile of one stage
+constexpr int NS = 5;            // LDS stages (5 x 32 KB = 160 KB): NS-1 K tiles in flight
+constexpr int TP = 132;          // pitch (floats) of the f32 C tile staged in LDS for the epilogue:
+                                 // 4 rows apart = 528 floats = 16 banks apart, so MFMA-layout writes
+                                 // from the 4 lane groups of a wave never collide
+
+// Epilogue on the LDS-staged C tile (row-major f32, pitch TP). Thread tid handles 8-column chunks
+// c = tid + 512*p (row c >> 4, columns (c & 15)*8 .. +7) — 16-byte reads from LDS and 16-byte
+// global stores. Requires N % 8 == 0 and 16-byte aligned output rows (checked by the launcher).
+__device__ __forceinline__ void load8(const float *t, float (&v)[8]) {
+    const floatx4 a = *(const floatx4 *)t, b = *(const floatx4 *)(t + 4);
+    v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3]; v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
+}
+__device__ __forceinline__ void add8(float (&v)[8], const float *p) {
+    const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
+    v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w; v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
+}
+
 template <int EPI>
-__global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(const GemmBatch bt) {
-    __shared__ __attribute__((aligned(1024))) half_t sA0[BM * BK], sA1[BM * BK], sA2[BM * BK], sA3[BM * BK];
-    __shared__ __attribute__((aligned(1024))) half_t sB0[BN * BK], sB1[BN * BK], sB2[BN * BK], sB3[BN * BK];
+__device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float *tile, int m0, int n0, int ks, int tid) {
+    const int M = P.M, N = P.N;
+    if (P.splits > 1) {
+        // raw f32 partial of this split: ws[(ks*M + m)*N + n]
+        float *w = P.ws + (long long)ks * M * N;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int c = tid + 512 * p, row = c >> 4, col = (c & 15) * 8;
+            const int m = m0 + row, n = n0 + col;
+            if (m < M && n < N) {
+                float *o = w + (long long)m * N + n;
+                *(floatx4 *)o = *(const floatx4 *)(tile + row * TP + col);
+                *(floatx4 *)(o + 4) = *(const floatx4 *)(tile + row * TP + col + 4);
+            }
+        }
+        return;
+    }
+    if constexpr (EPI == EPI_STORE) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int c = tid + 512 * p, row = c >> 4, col = (c & 15) * 8;
+            const int m = m0 + row, n = n0 + col;
+            if (m >= M || n >= N) continue;
+            float v[8];
+            load8(tile + row * TP + col, v);
+            if (P.bias) add8(v, P.bias + n);
+            if (P.silu)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = silu_f(v[e]);
+            const long long o = rowmap_phys(P.ymap, m) * (long long)P.ldy + n;
+            if (P.y_f16) {
+                *(half8 *)((half_t *)P.Y + o) = half8{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3],
+                                                      (half_t)v[4], (half_t)v[5], (half_t)v[6], (half_t)v[7]};
+            } else {
+                float *y = (float *)P.Y + o;
+                *(float4 *)y = make_float4(v[0], v[1], v[2], v[3]);
+                *(float4 *)(y + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            }
+        }
+    } else if constexpr (EPI == EPI_RESID) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int c = tid + 512 * p, row = c >> 4, col = (c & 15) * 8;
+            const int m = m0 + row, n = n0 + col;
+            if (m >= M || n >= N) continue;
+            float v[8];
+            load8(tile + row * TP + col, v);
+            if (P.bias) add8(v, P.bias + n);
+            const float *g = P.gate + (long long)(m / P.gate_L) * P.gate_ld + n;
+            float *x = P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n;
+            const float4 g0 = *(const float4 *)g, g1 = *(const float4 *)(g + 4);
+            float4 x0 = *(float4 *)x, x1 = *(float4 *)(x + 4);
+            x0.x = x0.x + v[0] * g0.x; x0.y = x0.y + v[1] * g0.y; x0.z = x0.z + v[2] * g0.z; x0.w = x0.w + v[3] * g0.w;
+            x1.x = x1.x + v[4] * g1.x; x1.y = x1.y + v[5] * g1.y; x1.z = x1.z + v[6] * g1.z; x1.w = x1.w + v[7] * g1.w;
+            *(float4 *)x = x0;
+            *(float4 *)(x + 4) = x1;
+        }
+    } else {  // EPI_QKV: the 128 columns of the tile lie in one of q, k, v (Hq % 128 == 0)
+        const int region = n0 / P.Hq;
+        if (region < 2) {
+            const float *nw = region == 0 ? P.qn : P.kn;
+            half_t *dst = region == 0 ? P.Q : P.Kd;
+            const float sc = region == 0 ? P.q_scale : 1.0f;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int c = tid + 512 * p, row = c >> 4, col = (c & 15) * 8;
+                const int m = m0 + row, n = n0 + col;
+                const int h = (n - region * P.Hq) >> 6, d0 = n & 63;
+                float v[8];
+                load8(tile + row * TP + col, v);
+                if (P.bias) add8(v, P.bias + n);
+                // per-head RMS over the 64 columns held by 8 neighbouring lanes (same row, same head)
+                float ss = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+                ss += __shfl_xor(ss, 1);
+                ss += __shfl_xor(ss, 2);
+                ss += __shfl_xor(ss, 4);
+                const float inv = 1.0f / sqrtf(ss / 64.0f + P.rms_eps);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = v[e] * inv * nw[d0 + e];
+                if (m >= M) continue;
+                const int b = m / P.q_L, t = m - b * P.q_L, s = P.q_soff + t;
+                if (t < P.rope_len) {
+                    const float *cs = P.rope + (t * 32 + (d0 >> 1)) * 2;
+#pragma unroll
+                    for (int e = 0; e < 8; e += 2) {
+                        const float c0 = cs[e], s0 = cs[e + 1];
+                        const float x0 = v[e], x1 = v[e + 1];
+                        v[e] = x0 * c0 - x1 * s0;
+                        v[e + 1] = x0 * s0 + x1 * c0;
+                    }
+                }
+                half_t *o = dst + (((long long)b * P.nh + h) * P.S_att + s) * 64 + d0;
+                *(half8 *)o = half8{(half_t)(v[0] * sc), (half_t)(v[1] * sc), (half_t)(v[2] * sc), (half_t)(v[3] * sc),
+                                    (half_t)(v[4] * sc), (half_t)(v[5] * sc), (half_t)(v[6] * sc), (half_t)(v[7] * sc)};
+            }
+        } else {
+            // V: column-wise pass, 8 consecutive rows of one column per chunk, stored along s of Vt
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int c = tid + 512 * p, col = c & 127, row8 = (c >> 7) * 8;
+                const int n = n0 + col;
+                const int h = (n - 2 * P.Hq) >> 6, d = n & 63;
+                const float bn = P.bias ? P.bias[n] : 0.0f;
+                const int mb = m0 + row8;
+                if (mb >= M) continue;
+                const int b = mb / P.q_L, t = mb - b * P.q_L;
+                half_t *o = P.Vt + (((long long)b * P.nh + h) * 64 + d) * P.Sp;
+                if (mb + 8 <= M && t + 8 <= P.q_L && ((P.q_soff + t) & 7) == 0) {
+                    half8 hv;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) hv[e] = (half_t)(tile[(row8 + e) * TP + col] + bn);
+                    *(half8 *)(o + P.q_soff + t) = hv;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const int m = mb + e;
+                        if (m >= M) break;
+                        const int bb = m / P.q_L, tt = m - bb * P.q_L;
+                        P.Vt[(((long long)bb * P.nh + h) * 64 + d) * P.Sp + P.q_soff + tt] =
+                            (half_t)(tile[(row8 + e) * TP + col] + bn);
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
+    // stage s: A tile at smem + s*STAGE, W tile at smem + (NS + s)*STAGE; reused for the C tile
+    __shared__ __attribute__((aligned(1024))) half_t smem[2 * NS * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tile = xcd_remap(blockIdx.x, gridDim.x);
-    const int pi = (bt.nprob > 1 && tile >= bt.p[1].tile_start) ? 1 : 0;
+    const int tid_g = xcd_remap(blockIdx.x, gridDim.x);
+    const int pi = (bt.nprob > 1 && tid_g >= bt.p[1].tile_start) ? 1 : 0;
     const GemmProblem &P = bt.p[pi];
     const int M = P.M, N = P.N, K = P.K, lda = P.lda, ldw = P.ldw, Kc = P.Kc, pad = P.pad, aT = P.a_T;
     const RowMap am = P.amap;
     // local tile -> (split, n tile, m tile), m fastest: neighbouring workgroups share W columns
-    const int local = tile - P.tile_start;
+    const int local = tid_g - P.tile_start;
     const int per_split = P.tiles_m * P.tiles_n;
     const int ks = local / per_split;
     const int rem = local - ks * per_split;
@@ -333,40 +487,42 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(const GemmBatch bt) {
     const i32x4 rsa = make_rsrc(P.A);
     const i32x4 rsb = make_rsrc(P.W);
 
-    // loader rows of this lane: wave*32 + i*8 + (lane >> 3), chunk (lane & 7) ^ (lane >> 3)
+    // loader rows of this lane: wave*16 + i*8 + (lane >> 3), chunk (lane & 7) ^ (lane >> 3).
+    // A row offsets are kept for tap 0 (byte offset of source row t - pad); tap j adds j*lda.
     const int lr = lane >> 3, lc = (lane & 7) ^ lr;
-    int a_row0[4], a_t[4], b_off[4];
-    bool a_ok[4];
+    int a_base[2], a_ts0[2], b_off[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int r = wave * 32 + i * 8 + lr;
+    for (int i = 0; i < 2; ++i) {
+        const int r = wave * 16 + i * 8 + lr;
         const int m = m0 + r;
-        a_ok[i] = m < M;
-        const int mm = a_ok[i] ? m : 0;
+        const int mm = m < M ? m : 0;
         const int b = mm / am.L;
-        a_t[i] = mm - b * am.L;
-        a_row0[i] = b * am.seg + am.off;
+        const int t = mm - b * am.L;
+        a_ts0[i] = m < M ? t - pad : -(1 << 29);   // source position at tap 0; invalid rows never pass
+        a_base[i] = ((b * am.seg + am.off + t - pad) * lda + lc * 8) * 2;
         const int n = n0 + r;
         b_off[i] = n < N ? (n * ldw + lc * 8) * 2 : -1;
     }
     // this workgroup's K tiles: [kbeg, kbeg + nk)
     const int nk = K / BK / P.splits;
     const int kbeg = ks * nk;
-    auto issue = [&](int kt, half_t *sa, half_t *sb) {
+    const int lda2 = lda * 2;
+    auto issue = [&](int kt, int stage) {
         const int k0 = (kbeg + kt) * BK;
         const int tap = k0 / Kc;
-        const int kc0 = k0 - tap * Kc + lc * 8;
+        const int kc2 = (k0 - tap * Kc) * 2 + tap * lda2;
+        lds_char *sa = (lds_char *)(smem + stage * STAGE) + wave * 2048;
+        lds_char *sb = (lds_char *)(smem + (NS + stage) * STAGE) + wave * 2048;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int ts = a_t[i] - pad + tap;
-            const bool ok = a_ok[i] && ts >= 0 && ts < aT;
-            const unsigned vo = ok ? (unsigned)(((a_row0[i] + ts) * lda + kc0) * 2) : 0x80000000u;
-            dma16(rsa, vo, (lds_char *)sa + (wave * 4 + i) * 1024);
+        for (int i = 0; i < 2; ++i) {
+            const int ts = a_ts0[i] + tap;
+            const unsigned vo = (ts >= 0 && ts < aT) ? (unsigned)(a_base[i] + kc2) : 0x80000000u;
+            dma16(rsa, vo, sa + i * 1024);
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 2; ++i) {
             const unsigned vo = b_off[i] >= 0 ? (unsigned)(b_off[i] + k0 * 2) : 0x80000000u;
-            dma16(rsb, vo, (lds_char *)sb + (wave * 4 + i) * 1024);
+            dma16(rsb, vo, sb + i * 1024);
         }
     };
 
@@ -376,102 +532,99 @@ __global__ __launch_bounds__(256, 1) void gemm_pipe_kernel(const GemmBatch bt) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    const int wm = wave >> 1, wn = wave & 1;
-    // operand read offsets (halves) inside a stage for k-substep 0 and 1
-    int a_rd[2][4], b_rd[2][4];
+    const int kh = wave >> 2, wq = wave & 3, wm = wq >> 1, wn = wq & 1;
+    // operand read offsets (halves) inside a stage for this wave's 32-wide K half
+    int a_rd[4], b_rd[4];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int i = 0; i < 4; ++i) {
+        const int slot = (kh * 4 + (lane >> 4)) ^ (lane & 7);
+        a_rd[i] = (wm * 64 + i * 16 + (lane & 15)) * BK + slot * 8;
+        b_rd[i] = (wn * 64 + i * 16 + (lane & 15)) * BK + slot * 8;
+    }
+    auto compute = [&](int stage) {
+        const half_t *sa = smem + stage * STAGE, *sb = smem + (NS + stage) * STAGE;
+        half8 af[4], bf[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int slot = (ks * 4 + (lane >> 4)) ^ (lane & 7);
-            a_rd[ks][i] = (wm * 64 + i * 16 + (lane & 15)) * BK + slot * 8;
-            b_rd[ks][i] = (wn * 64 + i * 16 + (lane & 15)) * BK + slot * 8;
+        for (int i = 0; i < 4; ++i) af[i] = *(const half8 *)(sa + a_rd[i]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bf[j] = *(const half8 *)(sb + b_rd[j]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    };
+
+    // Loop invariant at the top of an iteration: tile kt has landed in stage kt%NS for every wave,
+    // tiles kt+1..kt+NS-1 are in flight. Each step multiplies one stage, waits for its own DMAs of
+    // the next tile (4 per wave per tile), meets the other waves at the barrier (the stage just used
+    // is now free) and refills that stage NS tiles ahead.
+    issue(0, 0);
+#pragma unroll
+    for (int j = 1; j < NS - 1; ++j)
+        if (nk > j) issue(j, j);
+    wait_vmcnt(4 * min(nk - 1, NS - 2));
+    block_barrier();
+    if (nk > NS - 1) issue(NS - 1, NS - 1);
+#define TSN_GEMM_STEP(NEXT, S)                                                                  \
+    {                                                                                           \
+        compute(S);                                                                             \
+        wait_vmcnt(4 * (NS - 2));                                                               \
+        block_barrier();                                                                        \
+        issue(NEXT, S);                                                                         \
+    }
+    int kt = 0;
+    for (; kt + 2 * NS <= nk; kt += NS) {
+        TSN_GEMM_STEP(kt + NS + 0, 0)
+        TSN_GEMM_STEP(kt + NS + 1, 1)
+        TSN_GEMM_STEP(kt + NS + 2, 2)
+        TSN_GEMM_STEP(kt + NS + 3, 3)
+        TSN_GEMM_STEP(kt + NS + 4, 4)
+    }
+#undef TSN_GEMM_STEP
+    // tail: the last < 2*NS tiles; tile kt is visible, kt+1..min(kt+NS-1, nk-1) in flight
+    for (; kt < nk; ++kt) {
+        const int st = kt % NS;
+        compute(st);
+        if (kt + 1 < nk) {
+            wait_vmcnt(4 * min(nk - 2 - kt, NS - 2));
+            block_barrier();
+            if (kt + NS < nk) issue(kt + NS, st);
         }
-    auto compute = [&](const half_t *sa, const half_t *sb) {
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            half8 af[4], bf[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) af[i] = *(const half8 *)(sa + a_rd[ks][i]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) bf[j] = *(const half8 *)(sb + b_rd[ks][j]);
+    }
+    // Every DMA has landed (the last tile was waited for). Sum the two K halves into a row-major
+    // f32 C tile in LDS, then all 8 waves run the epilogue on 8-column chunks (16-byte accesses).
+    block_barrier();
+    float *tile = (float *)smem;
+    {
+        const int rb = wm * 64 + (lane >> 4) * 4, cb = wn * 64 + (lane & 15);
+        if (kh == 0) {
 #pragma unroll
             for (int i = 0; i < 4; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) tile[(rb + i * 16 + r) * TP + cb + j * 16] = acc[i][j][r];
         }
-    };
-
-    issue(0, sA0, sB0);
-    if (nk > 1) issue(1, sA1, sB1);
-    if (nk > 2) issue(2, sA2, sB2);
-    // Loop invariant at the top of an iteration: tile kt has landed in stage kt%4 for every wave,
-    // tiles kt+1..kt+3 are in flight. Each step multiplies one stage, waits for its own DMAs of the
-    // next tile, meets the other waves at the barrier (the stage just used is now free) and refills
-    // that stage four tiles ahead. The prologue leaves the same in-flight pattern as the back-edge,
-    // and the unrolled body has no conditions, so the compiler's per-stage DMA tracking stays exact.
-    wait_vmcnt(8 * min(nk - 1, 2));
-    block_barrier();
-    if (nk > 3) issue(3, sA3, sB3);
-#define TSN_GEMM_STEP(NEXT, CA, CB)                                                             \
-    {                                                                                           \
-        compute(CA, CB);                                                                        \
-        wait_vmcnt(16);                                                                         \
-        block_barrier();                                                                        \
-        issue(NEXT, CA, CB);                                                                    \
-    }
-    int kt = 0;
-    for (; kt + 8 <= nk; kt += 4) {
-        TSN_GEMM_STEP(kt + 4, sA0, sB0)
-        TSN_GEMM_STEP(kt + 5, sA1, sB1)
-        TSN_GEMM_STEP(kt + 6, sA2, sB2)
-        TSN_GEMM_STEP(kt + 7, sA3, sB3)
-    }
-#undef TSN_GEMM_STEP
-    // tail: the last < 8 tiles; tile kt is visible, kt+1..min(kt+3, nk-1) in flight
-#define TSN_GEMM_TAIL(CA, CB)                                                                   \
-    {                                                                                           \
-        compute(CA, CB);                                                                        \
-        if (kt + 1 < nk) {                                                                      \
-            wait_vmcnt(8 * min(nk - 2 - kt, 2));                                                \
-            block_barrier();                                                                    \
-            if (kt + 4 < nk) issue(kt + 4, CA, CB);                                             \
-        }                                                                                       \
-    }
-    for (; kt < nk; ++kt) {
-        switch (kt & 3) {
-            case 0: TSN_GEMM_TAIL(sA0, sB0) break;
-            case 1: TSN_GEMM_TAIL(sA1, sB1) break;
-            case 2: TSN_GEMM_TAIL(sA2, sB2) break;
-            default: TSN_GEMM_TAIL(sA3, sB3) break;
+        block_barrier();
+        if (kh == 1) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) tile[(rb + i * 16 + r) * TP + cb + j * 16] += acc[i][j][r];
         }
+        block_barrier();
     }
-#undef TSN_GEMM_TAIL
-    wait_vmcnt(0);
-    if (P.splits > 1) {
-        // raw f32 partial of this split: ws[(ks*M + m)*N + n]
-        float *w = P.ws + (long long)ks * M * N;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int m = m0 + wm * 64 + i * 16 + (lane >> 4) * 4 + r;
-                if (m >= M) continue;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int n = n0 + wn * 64 + j * 16 + (lane & 15);
-                    if (n < N) w[(long long)m * N + n] = acc[i][j][r];
-                }
-            }
-        return;
-    }
-    gemm_epilogue<EPI>(P, acc, m0, n0, wm, wn, lane);
+    tile_epilogue<EPI>(P, tile, m0, n0, ks, tid);
 }
 
-// split-K reduction + residual epilogue: R[rmap(m)][n] += gate[m/gate_L][n] * (sum_ks ws[ks][m][n] + bias[n]),
-// the partials summed in split order (deterministic). One thread per 4 columns.
-__global__ __launch_bounds__(256) void splitk_resid_kernel(const GemmBatch bt) {
+// split-K reduction + epilogue, one thread per 4 columns; partials summed in split order
+// (deterministic). EPI_RESID: R[rmap(m)][n] += gate[m/gate_L][n] * (sum + bias[n]);
+// EPI_STORE: Y[ymap(m)][n] = act(sum + bias[n]) as f16 or f32.
+template <int EPI>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmBatch bt) {
     long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     int pi = 0;
     long long n0 = (long long)bt.p[0].M * bt.p[0].N / 4;
@@ -493,15 +646,45 @@ __global__ __launch_bounds__(256) void splitk_resid_kernel(const GemmBatch bt) {
         const float4 b = *(const float4 *)(P.bias + n);
         v.x += b.x; v.y += b.y; v.z += b.z; v.w += b.w;
     }
-    const float4 g = *(const float4 *)(P.gate + (long long)(m / P.gate_L) * P.gate_ld + n);
-    float4 *xr = (float4 *)(P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n);
-    float4 x = *xr;
-    x.x = x.x + v.x * g.x; x.y = x.y + v.y * g.y; x.z = x.z + v.z * g.z; x.w = x.w + v.w * g.w;
-    *xr = x;
+    if constexpr (EPI == EPI_RESID) {
+        const float4 g = *(const float4 *)(P.gate + (long long)(m / P.gate_L) * P.gate_ld + n);
+        float4 *xr = (float4 *)(P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n);
+        float4 x = *xr;
+        x.x = x.x + v.x * g.x; x.y = x.y + v.y * g.y; x.z = x.z + v.z * g.z; x.w = x.w + v.w * g.w;
+        *xr = x;
+    } else {
+        if (P.silu) { v.x = silu_f(v.x); v.y = silu_f(v.y); v.z = silu_f(v.z); v.w = silu_f(v.w); }
+        const long long o = rowmap_phys(P.ymap, m) * (long long)P.ldy + n;
+        if (P.y_f16) *(half4 *)((half_t *)P.Y + o) = half4{(half_t)v.x, (half_t)v.y, (half_t)v.z, (half_t)v.w};
+        else *(float4 *)((float *)P.Y + o) = v;
+    }
 }
 
-
 } // namespace
+
+int launch_gemm(GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
+    TSN_TRY(gemm_plan(b, epi, a_f32));
+    return gemm_launch_planned(b, epi, a_f32, st);
+}
+
+int launch_gemm_reduce(const GemmBatch &b, int epi, hipStream_t st) {
+    long long red = 0;
+    for (int i = 0; i < b.nprob; ++i)
+        if (b.p[i].splits > 1) red += (long long)b.p[i].M * b.p[i].N / 4;
+    if (red == 0) return TSN_OK;
+    const dim3 grid((unsigned)((red + 255) / 256)), block(256);
+    if (epi == EPI_RESID) hipLaunchKernelGGL(splitk_reduce_kernel<EPI_RESID>, grid, block, 0, st, b);
+    else if (epi == EPI_STORE) hipLaunchKernelGGL(splitk_reduce_kernel<EPI_STORE>, grid, block, 0, st, b);
+    else { set_error("gemm reduce: epilogue without split-K support"); return TSN_ERR_ARG; }
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+
+bool gemm_needs_reduce(const GemmBatch &b) {
+    for (int i = 0; i < b.nprob; ++i)
+        if (b.p[i].splits > 1) return true;
+    return false;
+}
 
 void gemm_problem_init(GemmProblem &p) {
     memset(&p, 0, sizeof p);
@@ -512,7 +695,7 @@ void gemm_problem_init(GemmProblem &p) {
     p.splits = 1;
 }
 
-int launch_gemm(GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
+int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     TSN_REQUIRE(b.nprob >= 1 && b.nprob <= 2, "gemm: 1 or 2 problems");
     int tiles = 0;
     for (int i = 0; i < b.nprob; ++i) {
@@ -544,14 +727,20 @@ int launch_gemm(GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
     for (int i = 0; i < b.nprob && pipe; ++i) {
         const GemmProblem &p = b.p[i];
         const long long last_row = rowmap_phys(p.amap, p.M - 1) + p.a_T;
-        pipe = p.K % BK == 0 && p.Kc % BK == 0 && p.lda % 8 == 0 && p.ldw % 8 == 0 &&
-               (last_row + 1) * (long long)p.lda * 2 < (1LL << 31) && (long long)p.N * p.ldw * 2 < (1LL << 31);
+        pipe = p.K % BK == 0 && p.Kc % BK == 0 && p.lda % 8 == 0 && p.ldw % 8 == 0 && p.N % 8 == 0 &&
+               (last_row + 1) * (long long)p.lda * 2 < (1LL << 31) && (long long)p.N * p.ldw * 2 < (1LL << 31) &&
+               (((uintptr_t)p.bias) & 15) == 0;
+        // the C-tile epilogue writes 8 columns with 16-byte accesses
+        if (epi == EPI_STORE) pipe = pipe && (((uintptr_t)p.Y) & 15) == 0 && p.ldy % (p.y_f16 ? 8 : 4) == 0;
+        if (epi == EPI_RESID)
+            pipe = pipe && (((uintptr_t)p.R) & 15) == 0 && (((uintptr_t)p.gate) & 15) == 0 && p.ldr % 4 == 0 &&
+                   p.gate_ld % 4 == 0;
     }
     // Split-K (pipelined kernel, residual epilogue, workspace given): one common K chunk of kc
     // tiles for every problem, the largest kc (>= 4) that divides every problem's K tiles and gives
     // at least 224 workgroups; otherwise the smallest such kc. Partials need splits*M*N floats.
     for (int i = 0; i < b.nprob; ++i) { b.p[i].splits = 1; b.p[i].ws = nullptr; }
-    if (pipe && epi == EPI_RESID && b.ws) {
+    if (pipe && (epi == EPI_RESID || epi == EPI_STORE) && b.ws) {
         int nkmin = 1 << 30;
         for (int i = 0; i < b.nprob; ++i) nkmin = std::min(nkmin, b.p[i].K / BK);
         int best = 0;
@@ -580,7 +769,9 @@ int launch_gemm(GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
                     GemmProblem &p = b.p[i];
                     p.splits = p.K / BK / best;
                     if (p.splits > 1) {
-                        TSN_REQUIRE(p.N % 4 == 0 && p.ldr % 4 == 0 && p.gate_ld % 4 == 0, "gemm split-K: N, ldr, gate_ld % 4");
+                        TSN_REQUIRE(p.N % 4 == 0 && (epi == EPI_STORE ? p.ldy % 4 == 0
+                                                                      : p.ldr % 4 == 0 && p.gate_ld % 4 == 0),
+                                    "gemm split-K: N and output strides must be multiples of 4");
                         p.ws = b.ws + off / sizeof(float);
                         off += (size_t)p.splits * p.M * p.N * sizeof(float);
                     }
@@ -591,20 +782,24 @@ int launch_gemm(GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
             }
         }
     }
-    dim3 grid(tiles), block(256);
-    if (pipe) {
+    b.pipe = pipe ? 1 : 0;
+    b.kname = pipe ? (epi == EPI_STORE ? "gemm_pipe_kernel<0>" : epi == EPI_RESID ? "gemm_pipe_kernel<1>" : "gemm_pipe_kernel<2>")
+                   : a_f32 ? "gemm_f16_kernel<true, 0>"
+                   : (epi == EPI_STORE ? "gemm_f16_kernel<false, 0>" : epi == EPI_RESID ? "gemm_f16_kernel<false, 1>"
+                                                                        : "gemm_f16_kernel<false, 2>");
+    if (a_f32) TSN_REQUIRE(epi == EPI_STORE, "gemm: f32 A operand only with a plain store epilogue");
+    TSN_REQUIRE(epi == EPI_STORE || epi == EPI_RESID || epi == EPI_QKV, "gemm: unknown epilogue");
+    return TSN_OK;
+}
+
+int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
+    dim3 grid(b.total_tiles), block(b.pipe ? 512 : 256);
+    if (b.pipe) {
         if (epi == EPI_STORE) hipLaunchKernelGGL((gemm_pipe_kernel<EPI_STORE>), grid, block, 0, st, b);
         else if (epi == EPI_RESID) hipLaunchKernelGGL((gemm_pipe_kernel<EPI_RESID>), grid, block, 0, st, b);
         else if (epi == EPI_QKV) hipLaunchKernelGGL((gemm_pipe_kernel<EPI_QKV>), grid, block, 0, st, b);
         else { set_error("gemm: unknown epilogue"); return TSN_ERR_ARG; }
-        TSN_HIP_CHECK(hipGetLastError());
-        long long red = 0;
-        for (int i = 0; i < b.nprob; ++i)
-            if (b.p[i].splits > 1) red += (long long)b.p[i].M * b.p[i].N / 4;
-        if (red > 0)
-            hipLaunchKernelGGL(splitk_resid_kernel, dim3((unsigned)((red + 255) / 256)), dim3(256), 0, st, b);
     } else if (a_f32) {
-        TSN_REQUIRE(epi == EPI_STORE, "gemm: f32 A operand only with a plain store epilogue");
         hipLaunchKernelGGL((gemm_f16_kernel<true, EPI_STORE>), grid, block, 0, st, b);
     } else if (epi == EPI_STORE) {
         hipLaunchKernelGGL((gemm_f16_kernel<false, EPI_STORE>), grid, block, 0, st, b);

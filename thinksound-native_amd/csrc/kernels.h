@@ -43,13 +43,24 @@ struct GemmBatch {
     GemmProblem p[2];
     int nprob = 0;
     int total_tiles = 0;
-    // optional f32 workspace for split-K partials (EPI_RESID only); null disables split-K
+    // optional f32 workspace for split-K partials (EPI_RESID / EPI_STORE); null disables split-K
     float *ws = nullptr;
     size_t ws_bytes = 0;
+    // set by gemm_plan: pipelined kernel chosen, and the symbol of the kernel that will run
+    int pipe = 0;
+    const char *kname = nullptr;
 };
 
 // a_f32: A operand is f32 (converted to f16 on load). All problems share the epilogue kind.
+// With a workspace (EPI_RESID / EPI_STORE, pipelined kernel) the launcher may split K; the
+// partial sums are then reduced and the epilogue applied by launch_gemm_reduce, which must follow
+// on the same stream (it returns at once when no problem was split).
 int launch_gemm(GemmBatch &b, int epi, bool a_f32, hipStream_t st);
+// launch_gemm = gemm_plan (checks, tiling, split-K choice, kernel choice) + gemm_launch_planned
+int gemm_plan(GemmBatch &b, int epi, bool a_f32);
+int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st);
+int launch_gemm_reduce(const GemmBatch &b, int epi, hipStream_t st);
+bool gemm_needs_reduce(const GemmBatch &b);
 void gemm_problem_init(GemmProblem &p);
 
 /* ------------------------------------------------------------------ attention */
@@ -84,7 +95,10 @@ struct LnArgs {
     int nseg, H;
     float eps;
 };
-int launch_ln_mod(const LnArgs &a, bool y_f16, hipStream_t st);
+// ymode: 0 f32 output, 1 f16 output, 2 f16 hi|lo pair (y_hi at column c, y_lo = f16(y - y_hi) at
+// column H + c; ldy >= 2H): an f16 GEMM over [hi|lo] against a [W|W] weight reproduces the f32 y.
+enum { LN_F32 = 0, LN_F16 = 1, LN_F16_HILO = 2 };
+int launch_ln_mod(const LnArgs &a, int ymode, hipStream_t st);
 
 /* ------------------------------------------------------------------ GEMV (small M) */
 // Y[b][n] = act(sum_k W[n][k] * X[b][k] + bias[n] + addv[b][n]); optional Y2 = silu(Y).
@@ -119,6 +133,10 @@ int launch_copy_rows(const float *src, int lds, RowMap smap, float *dst, int ldd
                      int M, int H, hipStream_t st);
 // sampler step on x2 [2P][n]: v = vu + (vc - vu)*cfg; x += dt*v; both arms of prompt p get x.
 int launch_cfg_euler_pairs(const float *V, float *x2, int P, int n, float cfg, float dt, hipStream_t st);
+// x f32 rows -> out [M][2K] f16: out[m][k] = hi = f16(x), out[m][K + k] = f16(x - hi)
+int launch_split_hilo(const float *x, int ldx, RowMap xmap, half_t *out, int M, int K, hipStream_t st);
+// bf16 [N][K] -> f16 [N][2K] = [W | W] (weight of a GEMM over a hi|lo operand)
+int launch_dup_cols_bf16_to_f16(const uint16_t *src, half_t *dst, int N, int K, hipStream_t st);
 // format conversions
 int launch_bf16_to_f16(const uint16_t *src, half_t *dst, size_t n, hipStream_t st);
 int launch_bf16_to_f32(const uint16_t *src, float *dst, size_t n, hipStream_t st);

@@ -23,7 +23,7 @@ __device__ inline float silu_f(float v) { return v / (1.0f + __expf(-v)); }
 
 /* ---------------- LayerNorm + adaLN modulate (shaders/ops_conv.metal:127-144) ---------------- */
 // one wave per row; lane holds columns 4*lane + 256*c, c < NV (H = 256*NV)
-template <bool Y_F16, int NV>
+template <int YMODE, int NV>
 __global__ __launch_bounds__(256) void ln_mod_kernel(const LnArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     int v = blockIdx.x * 4 + wave;
@@ -62,8 +62,14 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const LnArgs a) {
         const float y1 = (xv[c].y - mean) * inv * (1.0f + scl.y) + sh.y;
         const float y2 = (xv[c].z - mean) * inv * (1.0f + scl.z) + sh.z;
         const float y3 = (xv[c].w - mean) * inv * (1.0f + scl.w) + sh.w;
-        if constexpr (Y_F16) {
+        if constexpr (YMODE == LN_F16) {
             *(half4 *)((half_t *)S.Y + yrow + col) = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
+        } else if constexpr (YMODE == LN_F16_HILO) {
+            const half4 hi = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
+            const half4 lo = half4{(half_t)(y0 - (float)hi[0]), (half_t)(y1 - (float)hi[1]),
+                                   (half_t)(y2 - (float)hi[2]), (half_t)(y3 - (float)hi[3])};
+            *(half4 *)((half_t *)S.Y + yrow + col) = hi;
+            *(half4 *)((half_t *)S.Y + yrow + NV * 256 + col) = lo;
         } else {
             *(float4 *)((float *)S.Y + yrow + col) = make_float4(y0, y1, y2, y3);
         }
@@ -224,6 +230,23 @@ __global__ void cfg_euler_pairs_kernel(const float *V, float *x2, int P, int n, 
     x2[(long long)(2 * p + 1) * n + i] = xn;
 }
 
+__global__ void split_hilo_kernel(const float *x, int ldx, RowMap xmap, half_t *out, int M, int K) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)M * K) return;
+    const int m = (int)(i / K), k = (int)(i - (long long)m * K);
+    const float v = x[rowmap_phys(xmap, m) * (long long)ldx + k];
+    const half_t hi = (half_t)v;
+    out[(long long)m * 2 * K + k] = hi;
+    out[(long long)m * 2 * K + K + k] = (half_t)(v - (float)hi);
+}
+__global__ void dup_cols_kernel(const uint16_t *src, half_t *dst, int N, int K) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)N * K) return;
+    const int n = (int)(i / K), k = (int)(i - (long long)n * K);
+    const half_t w = (half_t)bf16_to_f32(src[i]);
+    dst[(long long)n * 2 * K + k] = w;
+    dst[(long long)n * 2 * K + K + k] = w;
+}
 __global__ void bf16_to_f16_kernel(const uint16_t *s, half_t *d, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) d[i] = (half_t)bf16_to_f32(s[i]);
@@ -317,7 +340,8 @@ inline unsigned blocks_for(size_t n, unsigned t = 256) { return (unsigned)((n + 
 
 } // namespace
 
-int launch_ln_mod(const LnArgs &a, bool y_f16, hipStream_t st) {
+int launch_ln_mod(const LnArgs &a, int ymode, hipStream_t st) {
+    TSN_REQUIRE(ymode == LN_F32 || ymode == LN_F16 || ymode == LN_F16_HILO, "ln: output mode");
     TSN_REQUIRE(a.nseg >= 1 && a.nseg <= 2, "ln: 1 or 2 segments");
     TSN_REQUIRE(a.H % 256 == 0 && a.H >= 256 && a.H <= 2048, "ln: H must be a multiple of 256 in [256, 2048]");
     int total = 0;
@@ -326,14 +350,17 @@ int launch_ln_mod(const LnArgs &a, bool y_f16, hipStream_t st) {
         TSN_REQUIRE(s.X && s.Y && s.mod && s.rows > 0 && s.mod_L > 0 && s.xmap.L > 0 && s.ymap.L > 0, "ln: segment");
         TSN_REQUIRE(s.ldx % 4 == 0 && s.ldy % 4 == 0 && s.mod_ld % 4 == 0 && s.shift_off % 4 == 0 && s.scale_off % 4 == 0,
                     "ln: strides and offsets must be multiples of 4");
+        TSN_REQUIRE(ymode != LN_F16_HILO || s.ldy >= 2 * a.H, "ln: hi|lo output needs ldy >= 2H");
         total += s.rows;
     }
     dim3 grid((total + 3) / 4), block(256);
     const int nv = a.H / 256;
 #define TSN_LN_CASE(NVV)                                                                           \
     case NVV:                                                                                      \
-        if (y_f16) hipLaunchKernelGGL((ln_mod_kernel<true, NVV>), grid, block, 0, st, a);          \
-        else hipLaunchKernelGGL((ln_mod_kernel<false, NVV>), grid, block, 0, st, a);               \
+        if (ymode == LN_F16) hipLaunchKernelGGL((ln_mod_kernel<LN_F16, NVV>), grid, block, 0, st, a); \
+        else if (ymode == LN_F16_HILO)                                                             \
+            hipLaunchKernelGGL((ln_mod_kernel<LN_F16_HILO, NVV>), grid, block, 0, st, a);          \
+        else hipLaunchKernelGGL((ln_mod_kernel<LN_F32, NVV>), grid, block, 0, st, a);              \
         break;
     switch (nv) {
         TSN_LN_CASE(1) TSN_LN_CASE(2) TSN_LN_CASE(3) TSN_LN_CASE(4)
@@ -409,6 +436,18 @@ int launch_cfg_euler_pairs(const float *V, float *x2, int P, int n, float cfg, f
     return TSN_OK;
 }
 
+int launch_split_hilo(const float *x, int ldx, RowMap xmap, half_t *out, int M, int K, hipStream_t st) {
+    TSN_REQUIRE(x && out && M > 0 && K > 0 && xmap.L > 0, "split_hilo: arguments");
+    hipLaunchKernelGGL(split_hilo_kernel, dim3(blocks_for((size_t)M * K)), dim3(256), 0, st, x, ldx, xmap, out, M, K);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_dup_cols_bf16_to_f16(const uint16_t *src, half_t *dst, int N, int K, hipStream_t st) {
+    TSN_REQUIRE(src && dst && N > 0 && K > 0, "dup_cols: arguments");
+    hipLaunchKernelGGL(dup_cols_kernel, dim3(blocks_for((size_t)N * K)), dim3(256), 0, st, src, dst, N, K);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
 int launch_bf16_to_f16(const uint16_t *src, half_t *dst, size_t n, hipStream_t st) {
     if (n == 0) return TSN_OK;
     hipLaunchKernelGGL(bf16_to_f16_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, dst, n);

@@ -243,7 +243,7 @@ int Runtime::adaln_ln(const float *x, const float *mod, void *y, int ydt, uint32
     s.shift_off = (int)base; s.scale_off = (int)(base + H);
     s.rows = (int)rows;
     a.nseg = 1; a.H = (int)H; a.eps = eps;
-    return launch_ln_mod(a, ydt == DT_F16, dev.stream());
+    return launch_ln_mod(a, ydt == DT_F16 ? LN_F16 : LN_F32, dev.stream());
 }
 
 int Runtime::gate_add(const float *x, const float *f, const float *mod, float *y, uint32_t rows, uint32_t H,

@@ -1,0 +1,117 @@
+"""C ABI of libtsn without a GPU: the library loads, exports every entry point include/tsn.h
+declares, agrees with the oracle on the weight manifest, reproduces the specified synthetic-data
+generator, and reports errors on bad input (no compute call needs a device here)."""
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from conftest import ROOT
+
+
+def declared_symbols():
+    text = open(os.path.join(ROOT, "include", "tsn.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(tsn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol(tsn):
+    L = tsn.lib()
+    syms = declared_symbols()
+    assert len(syms) >= 40
+    missing = [s for s in syms if not hasattr(L, s)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_every_symbol(tsn):
+    bound = set(tsn._SIGS) | {"tsn_last_error", "tsn_last_gpu_ms", "tsn_version"}
+    assert set(declared_symbols()) <= bound
+
+
+def test_manifest_matches_oracle(tsn, orc):
+    for wl in (0, 1, 3, 4):
+        spec = tsn.default_spec(wl)
+        assert tsn.manifest(spec) == orc.manifest(spec.as_dict())
+    spec = tsn.default_spec(1)
+    assert tsn.manifest_total(spec) == 649757248
+    assert len(tsn.manifest(spec)) == 290
+
+
+def _mix64(z):
+    z = (z + np.uint64(0x9E3779B97F4A7C15))
+    z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+    z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+    return z ^ (z >> np.uint64(31))
+
+
+def _synth_normal_ref(seed, index, mean, std, n):
+    """independent numpy restatement of the generator specified in csrc/synth.cpp"""
+    with np.errstate(over="ignore"):
+        key = _mix64(_mix64(np.uint64(seed)) ^ (np.uint64(index) * np.uint64(0xD1B54A32D192ED03)))
+        i = np.arange(n, dtype=np.uint64)
+        p = i >> np.uint64(1)
+        def uni(j):
+            return ((_mix64(key ^ _mix64(j)) >> np.uint64(11)).astype(np.float64) + 0.5) * 2.0 ** -53
+        u1, u2 = uni(np.uint64(2) * p), uni(np.uint64(2) * p + np.uint64(1))
+    rad = np.sqrt(-2.0 * np.log(u1))
+    ang = 2 * np.pi * u2
+    z = np.where(i & np.uint64(1), rad * np.sin(ang), rad * np.cos(ang))
+    return (mean + std * z).astype(np.float32)
+
+
+def test_synth_generator_known_answers(tsn):
+    ref = _synth_normal_ref(4242, 1000, 0.0, 1.0, 4096)
+    got = tsn.synth_normal_f32(4242, 1000, 0.0, 1.0, (4096,))
+    assert np.abs(got.astype(np.float64) - ref).max() <= 1e-6
+    assert (got == ref).mean() > 0.999
+    # bf16 rounding: nearest-even of the f32 value
+    w = tsn.synth_normal_bf16(4242, 3, 0.0, 0.02, (4096,))
+    f = _synth_normal_ref(4242, 3, 0.0, 0.02, 4096)
+    u = f.view(np.uint32).astype(np.uint64)
+    rne = ((u + np.uint64(0x7FFF) + ((u >> np.uint64(16)) & np.uint64(1))) >> np.uint64(16)).astype(np.uint16)
+    assert (w == rne).mean() > 0.999
+    # moments
+    big = tsn.synth_normal_f32(1, 1, 0.0, 1.0, (1 << 18,))
+    assert abs(big.mean()) < 0.01 and abs(big.std() - 1) < 0.01
+    u01 = tsn.synth_uniform_f32(1, 2, 0.0, 1.0, (1 << 16,))
+    assert u01.min() > 0 and u01.max() < 1 and abs(u01.mean() - 0.5) < 0.01
+
+
+def test_synth_weights_layout(tsn):
+    spec = tsn.default_spec(1).copy(La=8, Lt=4, n_joint=1, n_fused=1)
+    w = tsn.synth_weights(spec, 4242, 1.0)
+    man = tsn.manifest(spec)
+    for name, n, off in man:
+        vals = tsn.bf16_to_f32(w[off:off + n])
+        if "norm.weight" in name:
+            assert abs(vals.mean() - 1.0) < 0.02
+        else:
+            assert abs(vals.mean()) < 0.01 and 0.015 < vals.std() < 0.025
+    # tensor k is drawn from stream (seed, k): regenerating one tensor alone gives the same bits
+    name, n, off = man[7]
+    alone = tsn.synth_normal_bf16(4242, 7, 0.0, 0.02, (n,))
+    assert np.array_equal(alone, w[off:off + n])
+
+
+def test_error_paths_without_gpu(tsn):
+    L = tsn.lib()
+    h = ctypes.c_void_p()
+    rc = L.tsn_runtime_create(0, ctypes.byref(h))
+    if rc == 0:
+        L.tsn_runtime_destroy(h)
+        pytest.skip("a GPU is present")
+    assert rc == 2 and L.tsn_last_error()
+    assert L.tsn_alloc(None, 16, ctypes.byref(h)) == 1
+    assert L.tsn_gemm(None, 1, None, None, 0, None, 0, None, 1, 1, 8, 0, 0, 0) == 1
+    s = tsn.DitSpec()
+    assert L.tsn_dit_default_spec(7, ctypes.byref(s)) == 1
+    assert L.tsn_dit_default_spec(1, ctypes.byref(s)) == 0 and s.La == 256 and s.Lt == 141
+    assert L.tsn_dit_manifest_entry(ctypes.byref(s), 100000, None, 0, None, None) == 1
+    with pytest.raises(tsn.TsnError):
+        tsn.call("tsn_dit_forward", None, None, 0.5, None, None, None)
+
+
+def test_oracle_builds_and_reports_threads(orc):
+    assert orc.num_threads() >= 1

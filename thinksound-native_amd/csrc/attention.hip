@@ -3,8 +3,12 @@
 // Replaces the reference's three-pass attention (src/dit_fwd.cpp:83-102 dispatching
 // shaders/gemm_attn.metal:96-202: attn_qk materialises [nh,S,S] f32 scores, softmax_rows runs one
 // thread per row, attn_pav reads the scores back). Here one workgroup owns 64 queries of one
-// (sample, head); 4 waves own 16 queries each; K and Vᵀ tiles of 64 keys are staged in LDS
-// (two stages, register prefetch) and the softmax is online, so no score buffer exists.
+// (sample, head) and the softmax is online, so no score buffer exists.
+//
+// 8 waves: wave w serves queries 16*(w&3)..+15; waves 0-3 take the even 64-key blocks and waves
+// 4-7 the odd ones, each half keeping its own running max / sum / output, merged through LDS at
+// the end. K and Vᵀ blocks reach LDS by direct-to-LDS buffer loads (no register staging) into a
+// ring of 4 stages x 2 blocks (128 KB); at S <= 512 every key is resident after the prologue.
 //
 // MFMA formulation (v_mfma_f32_16x16x32_f16; A row = lane&15, B col = lane&15, K group = lane>>4,
 // D[4*(lane>>4)+r][lane&15]):
@@ -16,49 +20,84 @@
 //                per-query rescale and the final 1/l are lane-local.
 // Probabilities are rounded to f16 before both the PV product and the row sum, so numerator and
 // denominator see the same values.
+//
+// LDS rows are 128 B (64 halves = 8 chunks of 16 B); chunk c of row r sits at slot c ^ (r & 7)
+// (the same swizzle as the GEMM), so the 16 rows an MFMA operand read touches hit distinct banks.
 #include "kernels.h"
 
 namespace tsn {
 
 namespace {
 
-constexpr int KB = 64, LDSW = 72;
+constexpr int AKB = 64;       // keys per block
+constexpr int ANS = 4;        // ring stages, each two key blocks: K 2 x 8 KB + Vt 2 x 8 KB
+constexpr int ASTAGE = 16384; // halves per stage
+
+typedef __attribute__((address_space(3))) char lds_char;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 __device__ inline half8 zero_h8() { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
 
-__global__ __launch_bounds__(256) void flash_attn_kernel(const AttnArgs a) {
-    __shared__ __attribute__((aligned(16))) half_t sK[2][KB * LDSW];
-    __shared__ __attribute__((aligned(16))) half_t sV[2][KB * LDSW];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+__device__ __forceinline__ i32x4 make_rsrc(const void *p) {
+    const unsigned long long a = (unsigned long long)p;
+    return i32x4{(int)(unsigned)a, (int)((a >> 32) & 0xFFFF), 0x7FFFFFFF, 0x00020000};
+}
+// 16 bytes per lane, global -> LDS slot (lane) of the 1 KB block at lds (see gemm.hip: issued from
+// inline asm and ordered by explicit vmcnt waits; s_nop 0 covers the M0 -> LDS-DMA hazard)
+__device__ __forceinline__ void dma16(i32x4 rs, unsigned voff, lds_char *lds) {
+    const unsigned l = __builtin_amdgcn_readfirstlane((unsigned)(unsigned long)lds);
+    asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                 :
+                 : "v"(voff), "s"(rs), "s"(l)
+                 : "memory");
+}
+__device__ __forceinline__ void wait_vmcnt(int n) {
+    if (n >= 8) __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (0xF << 8));
+    else if (n >= 4) __builtin_amdgcn_s_waitcnt(4 | (7 << 4) | (0xF << 8));
+    else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0xF << 8));
+}
+__device__ __forceinline__ void block_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+__global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
+    __shared__ __attribute__((aligned(1024))) half_t smem[ANS * ASTAGE];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar DMA choices
+    const int half = wave >> 2, wq = wave & 3;
     const int bh = blockIdx.y;
     const int S = a.S, Sp = a.Sp;
     const half_t *Qp = a.Q + (long long)bh * S * 64;
-    const half_t *Kp = a.K + (long long)bh * S * 64;
-    const half_t *Vp = a.Vt + (long long)bh * 64 * Sp;
+    const i32x4 rk = make_rsrc(a.K + (long long)bh * S * 64);
+    const i32x4 rv = make_rsrc(a.Vt + (long long)bh * 64 * Sp);
 
-    const int q = blockIdx.x * 64 + wave * 16 + (lane & 15);
+    const int q = blockIdx.x * 64 + wq * 16 + (lane & 15);
     const int g = lane >> 4;
     half8 qf[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
         qf[ks] = q < S ? *(const half8 *)(Qp + (long long)q * 64 + ks * 32 + g * 8) : zero_h8();
 
-    const int lrow = tid >> 3, lch = tid & 7;
-    half8 rk[2], rv[2];
-    auto load = [&](int kb) {
-        const int key0 = kb * KB;
+    const int nkb = (S + AKB - 1) / AKB;
+    const int npair = (nkb + 1) / 2;
+    // DMA of pair p: 32 blocks of 1 KB (K of block 2p, K of 2p+1, Vt of 2p, Vt of 2p+1, 8 each);
+    // wave w issues blocks 4w..4w+3. Lane row lr = lane >> 3, chunk lc = (lane & 7) ^ lr.
+    const int lr = lane >> 3, lc = (lane & 7) ^ lr;
+    auto issue = [&](int p, int stage) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const int key = key0 + lrow + 32 * r;
-            rk[r] = key < S ? *(const half8 *)(Kp + (long long)key * 64 + lch * 8) : zero_h8();
-            rv[r] = *(const half8 *)(Vp + (long long)(lrow + 32 * r) * Sp + key0 + lch * 8);
-        }
-    };
-    auto store = [&](int s) {
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            *(half8 *)&sK[s][(lrow + 32 * r) * LDSW + lch * 8] = rk[r];
-            *(half8 *)&sV[s][(lrow + 32 * r) * LDSW + lch * 8] = rv[r];
+        for (int i = 0; i < 4; ++i) {
+            const int d = wave * 4 + i, part = d >> 3, sub = d & 7;
+            const int blk = 2 * p + (part & 1);
+            unsigned vo = 0x80000000u;
+            if (part < 2) {
+                const int key = blk * AKB + sub * 8 + lr;
+                if (key < S) vo = (unsigned)((key * 64 + lc * 8) * 2);
+            } else if (blk < nkb) {
+                vo = (unsigned)(((sub * 8 + lr) * Sp + blk * AKB + lc * 8) * 2);
+            }
+            dma16(part < 2 ? rk : rv, vo, (lds_char *)(smem + stage * ASTAGE + part * 4096 + sub * 512));
         }
     };
 
@@ -67,20 +106,18 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(const AttnArgs a) {
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    const int nkb = (S + KB - 1) / KB;
-    load(0);
-    store(0);
-    __syncthreads();
-    for (int kb = 0; kb < nkb; ++kb) {
-        const int s = kb & 1;
-        if (kb + 1 < nkb) load(kb + 1);
+    // key block blk of this half, resident in stage st
+    auto compute = [&](int st, int blk) {
+        const half_t *sK = smem + st * ASTAGE + half * 4096;
+        const half_t *sV = smem + st * ASTAGE + 8192 + half * 4096;
         floatx4 sc[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             sc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            const int r = j * 16 + (lane & 15);
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-                const half8 kf = *(const half8 *)&sK[s][(j * 16 + (lane & 15)) * LDSW + ks * 32 + g * 8];
+                const half8 kf = *(const half8 *)(sK + r * 64 + (((ks * 4 + g) ^ (r & 7)) * 8));
                 sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], sc[j], 0, 0, 0);
             }
         }
@@ -90,7 +127,7 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(const AttnArgs a) {
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const int key = kb * KB + j * 16 + g * 4 + r;
+                const int key = blk * AKB + j * 16 + g * 4 + r;
                 x[j][r] = key < S ? sc[j][r] * a.scale_log2 : -INFINITY;
                 mx = fmaxf(mx, x[j][r]);
             }
@@ -119,18 +156,60 @@ __global__ __launch_bounds__(256) void flash_attn_kernel(const AttnArgs a) {
                                    ph[2 * c + 1][0], ph[2 * c + 1][1], ph[2 * c + 1][2], ph[2 * c + 1][3]};
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const half_t *vr = &sV[s][(dt * 16 + (lane & 15)) * LDSW + c * 32 + g * 4];
-                const half4 lo = *(const half4 *)vr, hi = *(const half4 *)(vr + 16);
+                // Vt row d = 16dt + (lane&15); keys 32c + 4g + 0..3 and 32c + 16 + 4g + 0..3
+                const int d = dt * 16 + (lane & 15);
+                const half_t *row = sV + d * 64;
+                const int c0 = c * 4 + (g >> 1), c1 = c0 + 2, hb = (g & 1) * 4;
+                const half4 lo = *(const half4 *)(row + ((c0 ^ (d & 7)) * 8) + hb);
+                const half4 hi = *(const half4 *)(row + ((c1 ^ (d & 7)) * 8) + hb);
                 const half8 vf = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[dt], 0, 0, 0);
             }
         }
-        if (kb + 1 < nkb) store(s ^ 1);
-        __syncthreads();
+    };
+
+    // ring over pairs of key blocks, as in the GEMM: pair p in stage p % ANS
+    issue(0, 0);
+    if (npair > 1) issue(1, 1);
+    if (npair > 2) issue(2, 2);
+    wait_vmcnt(4 * min(npair - 1, 2));
+    block_barrier();
+    if (npair > 3) issue(3, 3);
+    for (int p = 0; p < npair; ++p) {
+        const int st = p % ANS;
+        if (2 * p + half < nkb) compute(st, 2 * p + half);
+        if (p + 1 < npair) {
+            wait_vmcnt(4 * min(npair - 2 - p, 2));
+            block_barrier();
+            if (p + ANS < npair) issue(p + ANS, st);
+        }
     }
 
+    // merge the two halves: waves 4-7 park (m, l, O) in LDS, waves 0-3 combine and store
+    block_barrier();
+    float *red = (float *)smem;
+    float *slot = red + (wq * 64 + lane) * 18;
+    if (half == 1) {
+        slot[0] = m_i;
+        slot[1] = l_i;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) slot[2 + dt * 4 + r] = o[dt][r];
+    }
+    block_barrier();
+    if (half == 1) return;
+    const float m1 = slot[0], l1 = slot[1];
+    const float m = fmaxf(m_i, m1);
+    const float f0 = exp2f(m_i - m), f1 = exp2f(m1 - m);
+    const float l = l_i * f0 + l1 * f1;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[dt][r] = o[dt][r] * f0 + slot[2 + dt * 4 + r] * f1;
+
     if (q < S) {
-        const float inv = 1.0f / l_i;
+        const float inv = 1.0f / l;
         const int b = bh / a.nh, h = bh - b * a.nh;
         const long long orow = rowmap_phys(a.omap, b * S + q) * (long long)a.ldo + h * 64;
 #pragma unroll
@@ -178,8 +257,10 @@ int launch_attention(const AttnArgs &a, hipStream_t st) {
     TSN_REQUIRE(a.ldo % 4 == 0, "attention: ldo must be a multiple of 4");
     TSN_REQUIRE((((uintptr_t)a.Q) & 15) == 0 && (((uintptr_t)a.K) & 15) == 0 && (((uintptr_t)a.Vt) & 15) == 0,
                 "attention: 16-byte aligned Q/K/Vt");
-    dim3 grid((a.S + 63) / 64, a.BH), block(256);
-    hipLaunchKernelGGL(flash_attn_kernel, grid, block, 0, st, a);
+    TSN_REQUIRE((long long)a.S * 64 * 2 < (1LL << 31) && (long long)a.Sp * 64 * 2 < (1LL << 31),
+                "attention: per-head K/Vt extent must stay below 2 GB (buffer addressing)");
+    dim3 grid((a.S + 63) / 64, a.BH), block(512);
+    TSN_LAUNCH(flash_attn_kernel, grid, block, 0, st, a);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
@@ -189,7 +270,7 @@ int launch_attn_pack(const float *qkv, int S, int nh, int ld, int q_off, int k_o
     TSN_REQUIRE(qkv && Q && K && Vt && S > 0 && nh > 0 && Sp >= S, "attn_pack: arguments");
     const long long total = (long long)nh * Sp * 64;
     const int blocks = (int)((total + 255) / 256);
-    hipLaunchKernelGGL(attn_pack_kernel, dim3(blocks), dim3(256), 0, st, qkv, S, nh, ld, q_off, k_off, v_off, Q, K, Vt, Sp);
+    TSN_LAUNCH(attn_pack_kernel, dim3(blocks), dim3(256), 0, st, qkv, S, nh, ld, q_off, k_off, v_off, Q, K, Vt, Sp);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }

@@ -311,10 +311,18 @@ int DitModel::run(const char *name, double flops, double bytes, F &&launch) {
     ProfRec r{name, flops, bytes, nullptr, nullptr};
     TSN_HIP_CHECK(hipEventCreate(&r.a));
     TSN_HIP_CHECK(hipEventCreate(&r.b));
-    prof_->push_back(r);
-    TSN_HIP_CHECK(hipEventRecord(r.a, rt->dev.stream()));
+    LaunchEvents &ev = next_launch_events();
+    ev.start = r.a;
+    ev.stop = r.b;
     const int rc = launch();
-    TSN_HIP_CHECK(hipEventRecord(r.b, rt->dev.stream()));
+    const bool consumed = ev.start == nullptr;
+    ev.start = ev.stop = nullptr;
+    if (!consumed) {   // nothing was launched: no timing for this record
+        hipEventDestroy(r.a);
+        hipEventDestroy(r.b);
+        return rc;
+    }
+    prof_->push_back(r);
     return rc;
 }
 

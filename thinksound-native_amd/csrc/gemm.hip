@@ -451,13 +451,14 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
                     for (int e = 0; e < 8; ++e) hv[e] = (half_t)(tile[(row8 + e) * TP + col] + bn);
                     *(half8 *)(o + P.q_soff + t) = hv;
                 } else {
+                    // unaligned or crossing a sample boundary: element stores, (b, t) stepped along
+                    int bb = b, tt = t;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        const int m = mb + e;
-                        if (m >= M) break;
-                        const int bb = m / P.q_L, tt = m - bb * P.q_L;
+                        if (mb + e >= M) break;
                         P.Vt[(((long long)bb * P.nh + h) * 64 + d) * P.Sp + P.q_soff + tt] =
                             (half_t)(tile[(row8 + e) * TP + col] + bn);
+                        if (++tt == P.q_L) { tt = 0; ++bb; }
                     }
                 }
             }
@@ -673,8 +674,8 @@ int launch_gemm_reduce(const GemmBatch &b, int epi, hipStream_t st) {
         if (b.p[i].splits > 1) red += (long long)b.p[i].M * b.p[i].N / 4;
     if (red == 0) return TSN_OK;
     const dim3 grid((unsigned)((red + 255) / 256)), block(256);
-    if (epi == EPI_RESID) hipLaunchKernelGGL(splitk_reduce_kernel<EPI_RESID>, grid, block, 0, st, b);
-    else if (epi == EPI_STORE) hipLaunchKernelGGL(splitk_reduce_kernel<EPI_STORE>, grid, block, 0, st, b);
+    if (epi == EPI_RESID) TSN_LAUNCH(splitk_reduce_kernel<EPI_RESID>, grid, block, 0, st, b);
+    else if (epi == EPI_STORE) TSN_LAUNCH(splitk_reduce_kernel<EPI_STORE>, grid, block, 0, st, b);
     else { set_error("gemm reduce: epilogue without split-K support"); return TSN_ERR_ARG; }
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
@@ -795,18 +796,18 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
 int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
     dim3 grid(b.total_tiles), block(b.pipe ? 512 : 256);
     if (b.pipe) {
-        if (epi == EPI_STORE) hipLaunchKernelGGL((gemm_pipe_kernel<EPI_STORE>), grid, block, 0, st, b);
-        else if (epi == EPI_RESID) hipLaunchKernelGGL((gemm_pipe_kernel<EPI_RESID>), grid, block, 0, st, b);
-        else if (epi == EPI_QKV) hipLaunchKernelGGL((gemm_pipe_kernel<EPI_QKV>), grid, block, 0, st, b);
+        if (epi == EPI_STORE) TSN_LAUNCH((gemm_pipe_kernel<EPI_STORE>), grid, block, 0, st, b);
+        else if (epi == EPI_RESID) TSN_LAUNCH((gemm_pipe_kernel<EPI_RESID>), grid, block, 0, st, b);
+        else if (epi == EPI_QKV) TSN_LAUNCH((gemm_pipe_kernel<EPI_QKV>), grid, block, 0, st, b);
         else { set_error("gemm: unknown epilogue"); return TSN_ERR_ARG; }
     } else if (a_f32) {
-        hipLaunchKernelGGL((gemm_f16_kernel<true, EPI_STORE>), grid, block, 0, st, b);
+        TSN_LAUNCH((gemm_f16_kernel<true, EPI_STORE>), grid, block, 0, st, b);
     } else if (epi == EPI_STORE) {
-        hipLaunchKernelGGL((gemm_f16_kernel<false, EPI_STORE>), grid, block, 0, st, b);
+        TSN_LAUNCH((gemm_f16_kernel<false, EPI_STORE>), grid, block, 0, st, b);
     } else if (epi == EPI_RESID) {
-        hipLaunchKernelGGL((gemm_f16_kernel<false, EPI_RESID>), grid, block, 0, st, b);
+        TSN_LAUNCH((gemm_f16_kernel<false, EPI_RESID>), grid, block, 0, st, b);
     } else if (epi == EPI_QKV) {
-        hipLaunchKernelGGL((gemm_f16_kernel<false, EPI_QKV>), grid, block, 0, st, b);
+        TSN_LAUNCH((gemm_f16_kernel<false, EPI_QKV>), grid, block, 0, st, b);
     } else {
         set_error("gemm: unknown epilogue");
         return TSN_ERR_ARG;

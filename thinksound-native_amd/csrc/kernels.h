@@ -100,6 +100,27 @@ struct LnArgs {
 enum { LN_F32 = 0, LN_F16 = 1, LN_F16_HILO = 2 };
 int launch_ln_mod(const LnArgs &a, int ymode, hipStream_t st);
 
+/* ------------------------------------------------------------------ split-K reduce + residual + LN */
+// One wave per row of H columns (H % 256 == 0), for the rows of up to two GEMM problems:
+//   if splits > 1: x = X[row] + gate[b] * (sum_ks ws[ks][m] + bias), stored back to X
+//   (splits <= 1: the GEMM epilogue already updated X; x = X[row]);
+//   then, when ln is set and (m % mod_L) < ln_len: y = LN(x)*(1 + scale) + shift -> Y (f16, or f16
+//   hi|lo pair), shift/scale = mod[(m / mod_L)*mod_ld + shift_off / scale_off + c].
+struct RedLnSeg {
+    const float *ws; int splits, M;
+    const float *bias; const float *gate; int gate_ld, gate_L;
+    float *X; int ldx; RowMap xmap;
+    int ln, ln_len;
+    const float *mod; int mod_ld, mod_L, shift_off, scale_off;
+    void *Y; int ldy; RowMap ymap;
+};
+struct RedLnArgs {
+    RedLnSeg seg[2];
+    int nseg, H, ymode;
+    float eps;
+};
+int launch_reduce_ln(const RedLnArgs &a, hipStream_t st);
+
 /* ------------------------------------------------------------------ GEMV (small M) */
 // Y[b][n] = act(sum_k W[n][k] * X[b][k] + bias[n] + addv[b][n]); optional Y2 = silu(Y).
 // W is bf16, f16 or f32 (wdt); X, Y f32; nb <= 16 rows of X. HBM-bound: one wave per 4 rows of W.

@@ -76,6 +76,79 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const LnArgs a) {
     }
 }
 
+
+/* ---------------- split-K reduce + gated residual + LayerNorm/adaLN (one wave per row) ---------------- */
+template <int YMODE, int NV>
+__global__ __launch_bounds__(256) void reduce_ln_kernel(const RedLnArgs a) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    int v = blockIdx.x * 4 + wave;
+    const int total = a.seg[0].M + (a.nseg > 1 ? a.seg[1].M : 0);
+    if (v >= total) return;
+    int si = 0;
+    if (v >= a.seg[0].M) { si = 1; v -= a.seg[0].M; }
+    const RedLnSeg &S = a.seg[si];
+    const int H = NV * 256;
+    float *x = S.X + rowmap_phys(S.xmap, v) * (long long)S.ldx;
+    float4 xv[NV];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) xv[c] = *(const float4 *)(x + c * 256 + lane * 4);
+    if (S.splits > 1) {
+        const float *g = S.gate + (long long)(v / S.gate_L) * S.gate_ld;
+#pragma unroll
+        for (int c = 0; c < NV; ++c) {
+            const int col = c * 256 + lane * 4;
+            float4 acc = *(const float4 *)(S.ws + (long long)v * H + col);
+            for (int k = 1; k < S.splits; ++k) {
+                const float4 u = *(const float4 *)(S.ws + ((long long)k * S.M + v) * H + col);
+                acc.x += u.x; acc.y += u.y; acc.z += u.z; acc.w += u.w;
+            }
+            if (S.bias) {
+                const float4 b = *(const float4 *)(S.bias + col);
+                acc.x += b.x; acc.y += b.y; acc.z += b.z; acc.w += b.w;
+            }
+            const float4 gg = *(const float4 *)(g + col);
+            xv[c].x = xv[c].x + acc.x * gg.x; xv[c].y = xv[c].y + acc.y * gg.y;
+            xv[c].z = xv[c].z + acc.z * gg.z; xv[c].w = xv[c].w + acc.w * gg.w;
+            *(float4 *)(x + col) = xv[c];
+        }
+    }
+    if (!S.ln) return;
+    const int b = v / S.mod_L;
+    if (v - b * S.mod_L >= S.ln_len) return;
+    float sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV; ++c) sum += (xv[c].x + xv[c].y) + (xv[c].z + xv[c].w);
+    const float inv_h = 1.0f / (float)H;
+    const float mean = wave_sum(sum) * inv_h;
+    float var = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const float d0 = xv[c].x - mean, d1 = xv[c].y - mean, d2 = xv[c].z - mean, d3 = xv[c].w - mean;
+        var += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+    }
+    var = wave_sum(var) * inv_h;
+    const float inv = 1.0f / sqrtf(var + a.eps);
+    const float *mb = S.mod + (long long)b * S.mod_ld;
+    const long long yrow = rowmap_phys(S.ymap, v) * (long long)S.ldy;
+#pragma unroll
+    for (int c = 0; c < NV; ++c) {
+        const int col = c * 256 + lane * 4;
+        const float4 sh = *(const float4 *)(mb + S.shift_off + col);
+        const float4 scl = *(const float4 *)(mb + S.scale_off + col);
+        const float y0 = (xv[c].x - mean) * inv * (1.0f + scl.x) + sh.x;
+        const float y1 = (xv[c].y - mean) * inv * (1.0f + scl.y) + sh.y;
+        const float y2 = (xv[c].z - mean) * inv * (1.0f + scl.z) + sh.z;
+        const float y3 = (xv[c].w - mean) * inv * (1.0f + scl.w) + sh.w;
+        const half4 hi = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
+        *(half4 *)((half_t *)S.Y + yrow + col) = hi;
+        if constexpr (YMODE == LN_F16_HILO) {
+            const half4 lo = half4{(half_t)(y0 - (float)hi[0]), (half_t)(y1 - (float)hi[1]),
+                                   (half_t)(y2 - (float)hi[2]), (half_t)(y3 - (float)hi[3])};
+            *(half4 *)((half_t *)S.Y + yrow + H + col) = lo;
+        }
+    }
+}
+
 /* ---------------- GEMV (shaders/gemm_attn.metal:47-74, batched over nb rows of X) ---------------- */
 template <typename WT>
 __device__ inline void load_w8(const WT *p, float (&w)[8]);
@@ -357,10 +430,10 @@ int launch_ln_mod(const LnArgs &a, int ymode, hipStream_t st) {
     const int nv = a.H / 256;
 #define TSN_LN_CASE(NVV)                                                                           \
     case NVV:                                                                                      \
-        if (ymode == LN_F16) hipLaunchKernelGGL((ln_mod_kernel<LN_F16, NVV>), grid, block, 0, st, a); \
+        if (ymode == LN_F16) TSN_LAUNCH((ln_mod_kernel<LN_F16, NVV>), grid, block, 0, st, a); \
         else if (ymode == LN_F16_HILO)                                                             \
-            hipLaunchKernelGGL((ln_mod_kernel<LN_F16_HILO, NVV>), grid, block, 0, st, a);          \
-        else hipLaunchKernelGGL((ln_mod_kernel<LN_F32, NVV>), grid, block, 0, st, a);              \
+            TSN_LAUNCH((ln_mod_kernel<LN_F16_HILO, NVV>), grid, block, 0, st, a);          \
+        else TSN_LAUNCH((ln_mod_kernel<LN_F32, NVV>), grid, block, 0, st, a);              \
         break;
     switch (nv) {
         TSN_LN_CASE(1) TSN_LN_CASE(2) TSN_LN_CASE(3) TSN_LN_CASE(4)
@@ -372,6 +445,27 @@ int launch_ln_mod(const LnArgs &a, int ymode, hipStream_t st) {
     return TSN_OK;
 }
 
+int launch_reduce_ln(const RedLnArgs &a, hipStream_t st) {
+    TSN_REQUIRE(a.nseg >= 1 && a.nseg <= 2, "reduce_ln: 1 or 2 segments");
+    TSN_REQUIRE(a.H == 1024, "reduce_ln: H must be 1024");
+    TSN_REQUIRE(a.ymode == LN_F16 || a.ymode == LN_F16_HILO, "reduce_ln: output mode");
+    int total = 0;
+    for (int i = 0; i < a.nseg; ++i) {
+        const RedLnSeg &s = a.seg[i];
+        TSN_REQUIRE(s.X && s.M > 0 && s.xmap.L > 0 && s.ldx % 4 == 0, "reduce_ln: residual rows");
+        TSN_REQUIRE(s.splits <= 1 || (s.ws && s.gate && s.gate_L > 0 && s.gate_ld % 4 == 0), "reduce_ln: partials");
+        TSN_REQUIRE(!s.ln || (s.mod && s.Y && s.mod_L > 0 && s.ymap.L > 0 && s.mod_ld % 4 == 0 &&
+                              s.shift_off % 4 == 0 && s.scale_off % 4 == 0 && s.ldy % 4 == 0),
+                    "reduce_ln: layer-norm output");
+        total += s.M;
+    }
+    dim3 grid((total + 3) / 4), block(256);
+    if (a.ymode == LN_F16_HILO) TSN_LAUNCH((reduce_ln_kernel<LN_F16_HILO, 4>), grid, block, 0, st, a);
+    else TSN_LAUNCH((reduce_ln_kernel<LN_F16, 4>), grid, block, 0, st, a);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+
 int launch_gemv(const GemvArgs &a, hipStream_t st) {
     TSN_REQUIRE(a.W && a.X && a.Y && a.N > 0 && a.K > 0, "gemv: arguments");
     TSN_REQUIRE(a.nb >= 1 && a.nb <= 16, "gemv: 1..16 input rows");
@@ -379,7 +473,7 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
     const int rows_per_block = 4 * GEMV_ROWS;
     dim3 grid((a.N + rows_per_block - 1) / rows_per_block), block(256);
 #define TSN_GEMV_NB(WT, NBV)                                                                       \
-    case NBV: hipLaunchKernelGGL((gemv_kernel<WT, NBV>), grid, block, 0, st, a); break;
+    case NBV: TSN_LAUNCH((gemv_kernel<WT, NBV>), grid, block, 0, st, a); break;
 #define TSN_GEMV_W(WT)                                                                             \
     switch (nb) {                                                                                  \
         TSN_GEMV_NB(WT, 1) TSN_GEMV_NB(WT, 2) TSN_GEMV_NB(WT, 4) TSN_GEMV_NB(WT, 8)                \
@@ -407,9 +501,9 @@ int launch_linear_f32(const LinArgs &a, hipStream_t st) {
     TSN_REQUIRE(a.X && a.W && a.Y && a.M > 0 && a.N > 0 && a.K > 0, "linear_f32: arguments");
     TSN_REQUIRE(a.xmap.L > 0 && a.ymap.L > 0, "linear_f32: row maps");
     dim3 grid((a.N + 63) / 64, (a.M + 63) / 64), block(256);
-    if (a.wdt == DT_BF16) hipLaunchKernelGGL(linear_f32_kernel<uint16_t>, grid, block, 0, st, a);
-    else if (a.wdt == DT_F16) hipLaunchKernelGGL(linear_f32_kernel<half_t>, grid, block, 0, st, a);
-    else if (a.wdt == DT_F32) hipLaunchKernelGGL(linear_f32_kernel<float>, grid, block, 0, st, a);
+    if (a.wdt == DT_BF16) TSN_LAUNCH(linear_f32_kernel<uint16_t>, grid, block, 0, st, a);
+    else if (a.wdt == DT_F16) TSN_LAUNCH(linear_f32_kernel<half_t>, grid, block, 0, st, a);
+    else if (a.wdt == DT_F32) TSN_LAUNCH(linear_f32_kernel<float>, grid, block, 0, st, a);
     else { set_error("linear_f32: weight dtype"); return TSN_ERR_ARG; }
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
@@ -417,59 +511,59 @@ int launch_linear_f32(const LinArgs &a, hipStream_t st) {
 
 int launch_temb_sinusoid(const float *t, float *out, int nb, int D, float max_period, hipStream_t st) {
     TSN_REQUIRE(t && out && nb > 0 && D > 0 && D % 2 == 0, "temb: arguments");
-    hipLaunchKernelGGL(temb_kernel, dim3(blocks_for((size_t)nb * D / 2)), dim3(256), 0, st, t, out, nb, D, max_period);
+    TSN_LAUNCH(temb_kernel, dim3(blocks_for((size_t)nb * D / 2)), dim3(256), 0, st, t, out, nb, D, max_period);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
 
 int launch_copy_rows(const float *src, int lds, RowMap smap, float *dst, int ldd, RowMap dmap, int M, int H, hipStream_t st) {
     TSN_REQUIRE(src && dst && M > 0 && H > 0 && smap.L > 0 && dmap.L > 0, "copy_rows: arguments");
-    hipLaunchKernelGGL(copy_rows_kernel, dim3(M), dim3(256), 0, st, src, lds, smap, dst, ldd, dmap, M, H);
+    TSN_LAUNCH(copy_rows_kernel, dim3(M), dim3(256), 0, st, src, lds, smap, dst, ldd, dmap, M, H);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
 
 int launch_cfg_euler_pairs(const float *V, float *x2, int P, int n, float cfg, float dt, hipStream_t st) {
     TSN_REQUIRE(V && x2 && P > 0 && n > 0, "cfg_euler_pairs: arguments");
-    hipLaunchKernelGGL(cfg_euler_pairs_kernel, dim3(blocks_for((size_t)P * n)), dim3(256), 0, st, V, x2, P, n, cfg, dt);
+    TSN_LAUNCH(cfg_euler_pairs_kernel, dim3(blocks_for((size_t)P * n)), dim3(256), 0, st, V, x2, P, n, cfg, dt);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
 
 int launch_split_hilo(const float *x, int ldx, RowMap xmap, half_t *out, int M, int K, hipStream_t st) {
     TSN_REQUIRE(x && out && M > 0 && K > 0 && xmap.L > 0, "split_hilo: arguments");
-    hipLaunchKernelGGL(split_hilo_kernel, dim3(blocks_for((size_t)M * K)), dim3(256), 0, st, x, ldx, xmap, out, M, K);
+    TSN_LAUNCH(split_hilo_kernel, dim3(blocks_for((size_t)M * K)), dim3(256), 0, st, x, ldx, xmap, out, M, K);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
 int launch_dup_cols_bf16_to_f16(const uint16_t *src, half_t *dst, int N, int K, hipStream_t st) {
     TSN_REQUIRE(src && dst && N > 0 && K > 0, "dup_cols: arguments");
-    hipLaunchKernelGGL(dup_cols_kernel, dim3(blocks_for((size_t)N * K)), dim3(256), 0, st, src, dst, N, K);
+    TSN_LAUNCH(dup_cols_kernel, dim3(blocks_for((size_t)N * K)), dim3(256), 0, st, src, dst, N, K);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
 int launch_bf16_to_f16(const uint16_t *src, half_t *dst, size_t n, hipStream_t st) {
     if (n == 0) return TSN_OK;
-    hipLaunchKernelGGL(bf16_to_f16_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, dst, n);
+    TSN_LAUNCH(bf16_to_f16_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, dst, n);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
 int launch_bf16_to_f32(const uint16_t *src, float *dst, size_t n, hipStream_t st) {
     if (n == 0) return TSN_OK;
-    hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, dst, n);
+    TSN_LAUNCH(bf16_to_f32_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, dst, n);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
 int launch_f16_to_f32(const half_t *src, float *dst, size_t n, hipStream_t st) {
     if (n == 0) return TSN_OK;
-    hipLaunchKernelGGL(f16_to_f32_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, dst, n);
+    TSN_LAUNCH(f16_to_f32_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, dst, n);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
 int launch_conv_weight_reorder(const void *src, int src_bf16, half_t *dst, int OC, int IC, int K, hipStream_t st) {
     TSN_REQUIRE(src && dst && OC > 0 && IC > 0 && K > 0, "conv_reorder: arguments");
     const size_t n = (size_t)OC * IC * K;
-    hipLaunchKernelGGL(conv_reorder_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, src_bf16, dst, OC, IC, K);
+    TSN_LAUNCH(conv_reorder_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, src_bf16, dst, OC, IC, K);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
@@ -477,42 +571,42 @@ int launch_conv_weight_reorder(const void *src, int src_bf16, half_t *dst, int O
 int launch_silu(float *x, size_t n, hipStream_t st) {
     TSN_REQUIRE(x || n == 0, "silu: null");
     if (n == 0) return TSN_OK;
-    hipLaunchKernelGGL(silu_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, n);
+    TSN_LAUNCH(silu_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, n);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
 int launch_copy(const float *x, float *y, size_t n, hipStream_t st) {
     TSN_REQUIRE((x && y) || n == 0, "copy: null");
     if (n == 0) return TSN_OK;
-    hipLaunchKernelGGL(copy_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, y, n);
+    TSN_LAUNCH(copy_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, y, n);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
 int launch_swiglu(const float *a, const float *b, float *y, size_t n, hipStream_t st) {
     TSN_REQUIRE((a && b && y) || n == 0, "swiglu: null");
     if (n == 0) return TSN_OK;
-    hipLaunchKernelGGL(swiglu_kernel, dim3(blocks_for(n)), dim3(256), 0, st, a, b, y, n);
+    TSN_LAUNCH(swiglu_kernel, dim3(blocks_for(n)), dim3(256), 0, st, a, b, y, n);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
 int launch_add(const float *a, const float *b, float *y, size_t n, hipStream_t st) {
     TSN_REQUIRE((a && b && y) || n == 0, "add: null");
     if (n == 0) return TSN_OK;
-    hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n)), dim3(256), 0, st, a, b, y, n);
+    TSN_LAUNCH(add_kernel, dim3(blocks_for(n)), dim3(256), 0, st, a, b, y, n);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
 int launch_add_bcast_col(const float *x, const float *v, float *y, int S, int H, hipStream_t st) {
     TSN_REQUIRE(x && v && y && S > 0 && H > 0, "add_bcast_col: arguments");
     const size_t n = (size_t)S * H;
-    hipLaunchKernelGGL(add_bcast_col_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, v, y, H, n);
+    TSN_LAUNCH(add_bcast_col_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, v, y, H, n);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
 int launch_cfg_euler(const float *fc, const float *fu, float *x, size_t n, float cfg, float dt, hipStream_t st) {
     TSN_REQUIRE((fc && fu && x) || n == 0, "cfg_euler: null");
     if (n == 0) return TSN_OK;
-    hipLaunchKernelGGL(cfg_euler_kernel, dim3(blocks_for(n)), dim3(256), 0, st, fc, fu, x, n, cfg, dt);
+    TSN_LAUNCH(cfg_euler_kernel, dim3(blocks_for(n)), dim3(256), 0, st, fc, fu, x, n, cfg, dt);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
@@ -520,7 +614,7 @@ int launch_gate_add(const float *x, const float *f, const float *mod, float *y, 
                     int chunks, int gate_idx, hipStream_t st) {
     TSN_REQUIRE(x && f && mod && y && rows > 0 && H > 0 && gate_idx >= 0 && gate_idx < chunks, "gate_add: arguments");
     const size_t n = (size_t)rows * H;
-    hipLaunchKernelGGL(gate_add_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, f, mod, y, H, per_row, chunks, gate_idx, n);
+    TSN_LAUNCH(gate_add_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, f, mod, y, H, per_row, chunks, gate_idx, n);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
@@ -528,7 +622,7 @@ int launch_rms_head(float *x, const float *w, int rows, int nh, int ld, int hd, 
                     float eps, hipStream_t st) {
     TSN_REQUIRE(x && w && rows > 0 && nh > 0 && hd > 0, "rms_head: arguments");
     const int n = rows * nh;
-    hipLaunchKernelGGL(rms_head_kernel, dim3((n + 3) / 4), dim3(256), 0, st, x, w, rows, nh, ld, hd, col_off, row_off, eps);
+    TSN_LAUNCH(rms_head_kernel, dim3((n + 3) / 4), dim3(256), 0, st, x, w, rows, nh, ld, hd, col_off, row_off, eps);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }
@@ -536,7 +630,7 @@ int launch_rope_pairs(float *x, const int32_t *pos, int rows, int nh, int ld, in
                       float fscale, float base, hipStream_t st) {
     TSN_REQUIRE(x && rows > 0 && nh > 0 && hd > 0 && hd % 2 == 0, "rope_pairs: arguments");
     const size_t n = (size_t)rows * nh * (hd / 2);
-    hipLaunchKernelGGL(rope_pairs_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, pos, rows, nh, ld, hd, col_off,
+    TSN_LAUNCH(rope_pairs_kernel, dim3(blocks_for(n)), dim3(256), 0, st, x, pos, rows, nh, ld, hd, col_off,
                        row_off, fscale, base);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;

@@ -12,6 +12,10 @@ namespace {
 thread_local std::string g_last_error;
 }
 void set_error(const std::string &msg) { g_last_error = msg; }
+LaunchEvents &next_launch_events() {
+    static thread_local LaunchEvents ev;
+    return ev;
+}
 const char *last_error() { return g_last_error.c_str(); }
 
 /* ---------------------------------------------------------------- Device */

@@ -1,5 +1,6 @@
 // tsn_common.h — shared types and helpers for the gfx950 DiT velocity path.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -61,6 +62,25 @@ const char *last_error();
     do {                                                                                \
         int s_ = (expr);                                                                \
         if (s_ != TSN_OK) return s_;                                                    \
+    } while (0)
+
+// Event pair armed for the next kernel launch of the calling thread (per-kernel profiling). Every
+// kernel goes through TSN_LAUNCH: when a pair is armed it is attached to the dispatch itself with
+// hipExtLaunchKernelGGL, so the events bracket exactly that kernel's execution, and disarmed.
+struct LaunchEvents {
+    hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchEvents &next_launch_events();
+
+#define TSN_LAUNCH(kernel, grid, block, shm, st, ...)                                           \
+    do {                                                                                        \
+        ::tsn::LaunchEvents &ev_ = ::tsn::next_launch_events();                                 \
+        if (ev_.start) {                                                                        \
+            hipExtLaunchKernelGGL(kernel, grid, block, shm, st, ev_.start, ev_.stop, 0, __VA_ARGS__); \
+            ev_.start = ev_.stop = nullptr;                                                     \
+        } else {                                                                                \
+            hipLaunchKernelGGL(kernel, grid, block, shm, st, __VA_ARGS__);                      \
+        }                                                                                       \
     } while (0)
 
 // bf16 bits -> f32 (exact)

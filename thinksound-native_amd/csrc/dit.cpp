@@ -282,6 +282,8 @@ constexpr const char *K_GEMV = "gemv_kernel";
 constexpr const char *K_LN16 = "ln_mod_kernel<1, 4>";
 constexpr const char *K_LNHL = "ln_mod_kernel<2, 4>";
 constexpr const char *K_SPLIT = "split_hilo_kernel";
+constexpr const char *K_RLN16 = "reduce_ln_kernel<1>";
+constexpr const char *K_RLNHL = "reduce_ln_kernel<2>";
 
 double gemm_flops(const GemmBatch &b) {
     double f = 0;
@@ -339,18 +341,75 @@ int DitModel::gemm_run(GemmBatch &b, int epi) {
                [&] { return launch_gemm_reduce(b, epi, st); });
 }
 
+// Residual GEMM batch followed by one reduce kernel that finishes the split-K sum into X
+// (x += gate * (sum + bias), fixed split order) and applies the adaLN that follows (r.seg[i].ln).
+// Segment i covers the rows of problem i. Without split and without a following LN the reduce
+// kernel is skipped (the GEMM epilogue already updated X).
+int DitModel::resid_ln(GemmBatch &b, RedLnArgs &r) {
+    const hipStream_t st = rt->dev.stream();
+    TSN_TRY(gemm_plan(b, EPI_RESID, false));
+    TSN_TRY(run(b.kname, gemm_flops(b), gemm_bytes(b, EPI_RESID), [&] { return gemm_launch_planned(b, EPI_RESID, false, st); }));
+    r.nseg = b.nprob;
+    r.H = s.H;
+    r.eps = s.ln_eps;
+    bool work = false;
+    double bytes = 0;
+    for (int i = 0; i < b.nprob; ++i) {
+        const GemmProblem &p = b.p[i];
+        RedLnSeg &g = r.seg[i];
+        g.ws = p.ws; g.splits = p.splits; g.M = p.M;
+        g.bias = p.bias; g.gate = p.gate; g.gate_ld = p.gate_ld; g.gate_L = p.gate_L;
+        g.X = p.R; g.ldx = p.ldr; g.xmap = p.rmap;
+        work = work || g.ln || g.splits > 1;
+        bytes += (double)p.M * p.N * (4.0 + (p.splits > 1 ? 4.0 * p.splits + 4.0 : 0.0));
+        if (g.ln) bytes += (double)g.ln_len * (p.M / g.mod_L) * p.N * (r.ymode == LN_F16_HILO ? 4.0 : 2.0);
+    }
+    if (!work) return TSN_OK;
+    return run(r.ymode == LN_F16_HILO ? K_RLNHL : K_RLN16, 0, bytes, [&] { return launch_reduce_ln(r, st); });
+}
+
+// Fill the LN part of r's segments (one per row map of the residual GEMM) for the adaLN that
+// runs next: LN1 of a joint or fused block (f16 into XN), or the final layer's (f16 hi|lo of the
+// audio rows into XF2).
+void DitModel::next_ln(RedLnArgs &r, Next next, const RowMap *maps, int nseg) {
+    memset(&r, 0, sizeof r);
+    r.ymode = next.kind == NEXT_FINAL ? LN_F16_HILO : LN_F16;
+    for (int i = 0; i < nseg; ++i) {
+        RedLnSeg &g = r.seg[i];
+        const RowMap &m = maps[i];
+        const bool text = m.off >= s.La;   // rows of the text stream inside the joint layout
+        g.mod = MOD_; g.mod_ld = NMOD; g.mod_L = m.L; g.ln_len = m.L;
+        g.Y = XN_; g.ldy = s.H; g.ymap = m;
+        switch (next.kind) {
+        case NEXT_JOINT: g.ln = 1; g.shift_off = (text ? jt_ : ja_)[next.idx].mod_off; break;
+        case NEXT_FUSED: g.ln = 1; g.shift_off = fu_[next.idx].mod_off; break;
+        case NEXT_FINAL:
+            g.ln = text ? 0 : 1;
+            g.shift_off = fin_mod_off_;
+            g.ln_len = m.L < s.La ? m.L : s.La;
+            g.Y = XF2_; g.ldy = 2 * s.H; g.ymap = RowMap{m.L, s.La, 0};   // audio row t of sample b -> b*La + t
+            break;
+        default: g.ln = 0; break;
+        }
+        g.scale_off = g.shift_off + s.H;
+    }
+}
+
 // Joint block: src/dit_fwd.cpp:180-257 (pre_attn :24-49, attention :83-102, post_attn :51-81)
-int DitModel::block_joint(int i) {
+int DitModel::block_joint(int i, bool ln1, Next next) {
     const hipStream_t st = rt->dev.stream();
     const StreamW &a = ja_[i], &t = jt_[i];
     const int B = s.B, H = s.H, La = s.La, Lt = s.Lt;
     const RowMap Sa{La, S, 0}, St{Lt, S, La};
-    LnArgs ln;
-    memset(&ln, 0, sizeof ln);
-    ln.nseg = 2; ln.H = H; ln.eps = s.ln_eps;
-    ln_seg(ln.seg[0], X_, H, Sa, XN_, MOD_, NMOD, La, a.mod_off, B * La);
-    ln_seg(ln.seg[1], X_, H, St, XN_, MOD_, NMOD, Lt, t.mod_off, B * Lt);
-    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16, st); }));
+    const RowMap maps[2] = {Sa, St};
+    if (ln1) {   // otherwise the previous block's last reduce kernel produced it
+        LnArgs ln;
+        memset(&ln, 0, sizeof ln);
+        ln.nseg = 2; ln.H = H; ln.eps = s.ln_eps;
+        ln_seg(ln.seg[0], X_, H, Sa, XN_, MOD_, NMOD, La, a.mod_off, B * La);
+        ln_seg(ln.seg[1], X_, H, St, XN_, MOD_, NMOD, Lt, t.mod_off, B * Lt);
+        TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16, st); }));
+    }
 
     GemmBatch qb;
     qb.nprob = 2;
@@ -372,11 +431,11 @@ int DitModel::block_joint(int i) {
     ob.ws_bytes = ws_bytes_;
     resid_problem(ob.p[0], AO_, H, Sa, 1, H, B * La, H, a.Wo, a.bo, X_, H, MOD_ + a.mod_off + 2 * H, NMOD);
     resid_problem(ob.p[1], AO_, H, St, 1, H, B * Lt, H, t.Wo, t.bo, X_, H, MOD_ + t.mod_off + 2 * H, NMOD);
-    TSN_TRY(gemm_run(ob, EPI_RESID));
-
-    ln_seg(ln.seg[0], X_, H, Sa, XN_, MOD_, NMOD, La, a.mod_off + 3 * H, B * La);
-    ln_seg(ln.seg[1], X_, H, St, XN_, MOD_, NMOD, Lt, t.mod_off + 3 * H, B * Lt);
-    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16, st); }));
+    RedLnArgs r;
+    next_ln(r, Next{NEXT_JOINT, i}, maps, 2);   // LN2 of this block: modulation chunks 3, 4
+    r.seg[0].shift_off += 3 * H; r.seg[0].scale_off += 3 * H;
+    r.seg[1].shift_off += 3 * H; r.seg[1].scale_off += 3 * H;
+    TSN_TRY(resid_ln(ob, r));
 
     const int ta = a.conv ? 3 : 1;
     GemmBatch f1;
@@ -391,20 +450,23 @@ int DitModel::block_joint(int i) {
     f2.ws_bytes = ws_bytes_;
     resid_problem(f2.p[0], HF_, s.F, Sa, ta, s.F, B * La, H, a.W2, nullptr, X_, H, MOD_ + a.mod_off + 5 * H, NMOD);
     resid_problem(f2.p[1], HF_, s.F, St, 1, s.F, B * Lt, H, t.W2, nullptr, X_, H, MOD_ + t.mod_off + 5 * H, NMOD);
-    return gemm_run(f2, EPI_RESID);
+    next_ln(r, next, maps, 2);
+    return resid_ln(f2, r);
 }
 
 // Fused block: src/dit_fwd.cpp:267-279 over the joined rows
-int DitModel::block_fused(int i) {
+int DitModel::block_fused(int i, bool ln1, Next next) {
     const hipStream_t st = rt->dev.stream();
     const StreamW &w = fu_[i];
     const int B = s.B, H = s.H, M = B * S;
     const RowMap D{S, S, 0};
-    LnArgs ln;
-    memset(&ln, 0, sizeof ln);
-    ln.nseg = 1; ln.H = H; ln.eps = s.ln_eps;
-    ln_seg(ln.seg[0], X_, H, D, XN_, MOD_, NMOD, S, w.mod_off, M);
-    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16, st); }));
+    if (ln1) {   // otherwise the previous block's last reduce kernel produced it
+        LnArgs ln;
+        memset(&ln, 0, sizeof ln);
+        ln.nseg = 1; ln.H = H; ln.eps = s.ln_eps;
+        ln_seg(ln.seg[0], X_, H, D, XN_, MOD_, NMOD, S, w.mod_off, M);
+        TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16, st); }));
+    }
 
     GemmBatch qb;
     qb.nprob = 1;
@@ -424,10 +486,10 @@ int DitModel::block_fused(int i) {
     ob.ws = ws_;
     ob.ws_bytes = ws_bytes_;
     resid_problem(ob.p[0], AO_, H, D, 1, H, M, H, w.Wo, w.bo, X_, H, MOD_ + w.mod_off + 2 * H, NMOD);
-    TSN_TRY(gemm_run(ob, EPI_RESID));
-
-    ln_seg(ln.seg[0], X_, H, D, XN_, MOD_, NMOD, S, w.mod_off + 3 * H, M);
-    TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16, st); }));
+    RedLnArgs r;
+    next_ln(r, Next{NEXT_FUSED, i}, &D, 1);   // LN2 of this block: modulation chunks 3, 4
+    r.seg[0].shift_off += 3 * H; r.seg[0].scale_off += 3 * H;
+    TSN_TRY(resid_ln(ob, r));
 
     GemmBatch f1;
     f1.nprob = 1;
@@ -439,7 +501,8 @@ int DitModel::block_fused(int i) {
     f2.ws = ws_;
     f2.ws_bytes = ws_bytes_;
     resid_problem(f2.p[0], HF_, s.F, D, 1, s.F, M, H, w.W2, nullptr, X_, H, MOD_ + w.mod_off + 5 * H, NMOD);
-    return gemm_run(f2, EPI_RESID);
+    next_ln(r, next, &D, 1);
+    return resid_ln(f2, r);
 }
 
 int DitModel::enqueue_forward(const float *z, const float *t, const float *text, const float *pooled, float *v,
@@ -487,25 +550,30 @@ int DitModel::enqueue_forward(const float *z, const float *t, const float *text,
         }));
     const size_t tap_n = (size_t)B * S * H;
     int tap = 0;
-    for (int i = 0; i < s.n_joint; ++i) {
-        TSN_TRY(block_joint(i));
-        if (taps) TSN_TRY(rt->dev.copy_d2d(taps + tap_n * tap++, X_, tap_n * 4));
-    }
-    for (int i = 0; i < s.n_fused; ++i) {
-        TSN_TRY(block_fused(i));
+    // each block's last reduce kernel also applies the next adaLN (the next block's LN1, or the
+    // final layer's)
+    const int nblk = s.n_joint + s.n_fused;
+    for (int k = 0; k < nblk; ++k) {
+        const Next next = k + 1 == nblk ? Next{NEXT_FINAL, 0}
+                          : k + 1 < s.n_joint ? Next{NEXT_JOINT, k + 1}
+                                              : Next{NEXT_FUSED, k + 1 - s.n_joint};
+        if (k < s.n_joint) TSN_TRY(block_joint(k, k == 0, next));
+        else TSN_TRY(block_fused(k - s.n_joint, k == 0, next));
         if (taps) TSN_TRY(rt->dev.copy_d2d(taps + tap_n * tap++, X_, tap_n * 4));
     }
     // final layer: adaLN (2 chunks) on audio rows as f16 hi|lo, projection to latent by one MFMA
     // GEMM against [W|W] (f32-accurate), split over K (src/dit_fwd.cpp:287-303)
-    LnArgs ln;
-    memset(&ln, 0, sizeof ln);
-    ln.nseg = 1; ln.H = H; ln.eps = s.ln_eps;
-    LnSeg &g = ln.seg[0];
-    g.X = X_; g.ldx = H; g.xmap = RowMap{s.La, S, 0};
-    g.Y = XF2_; g.ldy = 2 * H; g.ymap = rowmap_dense(B * s.La);
-    g.mod = MOD_; g.mod_ld = NMOD; g.mod_L = s.La; g.shift_off = fin_mod_off_; g.scale_off = fin_mod_off_ + H;
-    g.rows = B * s.La;
-    TSN_TRY(run(K_LNHL, 0, B * s.La * (double)H * 8.0, [&] { return launch_ln_mod(ln, LN_F16_HILO, st); }));
+    if (nblk == 0) {
+        LnArgs ln;
+        memset(&ln, 0, sizeof ln);
+        ln.nseg = 1; ln.H = H; ln.eps = s.ln_eps;
+        LnSeg &g = ln.seg[0];
+        g.X = X_; g.ldx = H; g.xmap = RowMap{s.La, S, 0};
+        g.Y = XF2_; g.ldy = 2 * H; g.ymap = rowmap_dense(B * s.La);
+        g.mod = MOD_; g.mod_ld = NMOD; g.mod_L = s.La; g.shift_off = fin_mod_off_; g.scale_off = fin_mod_off_ + H;
+        g.rows = B * s.La;
+        TSN_TRY(run(K_LNHL, 0, B * s.La * (double)H * 8.0, [&] { return launch_ln_mod(ln, LN_F16_HILO, st); }));
+    }
     GemmBatch fb;
     fb.nprob = 1;
     fb.ws = ws_;
@@ -527,7 +595,7 @@ int DitModel::enqueue_joint_block(int block, float *X, const float *g) {
     TSN_TRY(gs_from_g(g));
     TSN_TRY(modulation(gs_, ja_[block].mod_off, 12 * s.H));
     TSN_TRY(rt->dev.copy_d2d(X_, X, n * 4));
-    TSN_TRY(block_joint(block));
+    TSN_TRY(block_joint(block, true, Next{NEXT_NONE, 0}));
     return rt->dev.copy_d2d(X, X_, n * 4);
 }
 
@@ -539,7 +607,7 @@ int DitModel::enqueue_fused_block(int block, float *X, const float *g) {
     TSN_TRY(gs_from_g(g));
     TSN_TRY(modulation(gs_, fu_[block].mod_off, 6 * s.H));
     TSN_TRY(rt->dev.copy_d2d(X_, X, n * 4));
-    TSN_TRY(block_fused(block));
+    TSN_TRY(block_fused(block, true, Next{NEXT_NONE, 0}));
     return rt->dev.copy_d2d(X, X_, n * 4);
 }
 

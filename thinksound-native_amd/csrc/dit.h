@@ -90,8 +90,16 @@ private:
         int conv = 0;
         int mod_off = 0;
     };
-    int block_joint(int i);
-    int block_fused(int i);
+    // The adaLN that follows a block's last residual GEMM, fused into that GEMM's reduce kernel:
+    // the next joint block's, the next fused block's, the final layer's, or none.
+    enum { NEXT_NONE = 0, NEXT_JOINT = 1, NEXT_FUSED = 2, NEXT_FINAL = 3 };
+    struct Next {
+        int kind, idx;
+    };
+    int block_joint(int i, bool ln1, Next next);
+    int block_fused(int i, bool ln1, Next next);
+    int resid_ln(GemmBatch &b, RedLnArgs &r);
+    void next_ln(RedLnArgs &r, Next next, const RowMap *maps, int nseg);
     int modulation(const float *gs, int row0, int rows);
     int gs_from_g(const float *g);
     int alloc(size_t bytes, void **p);

@@ -77,76 +77,67 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const LnArgs a) {
 }
 
 
-/* ---------------- split-K reduce + gated residual + LayerNorm/adaLN (one wave per row) ---------------- */
-template <int YMODE, int NV>
-__global__ __launch_bounds__(256) void reduce_ln_kernel(const RedLnArgs a) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    int v = blockIdx.x * 4 + wave;
-    const int total = a.seg[0].M + (a.nseg > 1 ? a.seg[1].M : 0);
-    if (v >= total) return;
-    int si = 0;
+/* ---------------- split-K reduce + gated residual + LayerNorm/adaLN (one workgroup per row) ---------------- */
+// H/4 threads per row, 4 consecutive columns (one float4) per thread; the split partials of a row
+// are summed in fixed split order, the LN statistics are two-pass (mean, then centred squares)
+// with fixed-order wave and cross-wave sums.
+__device__ __forceinline__ float block_sum(float v, float *red, int nw) {
+    v = wave_sum(v);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+    __syncthreads();
+    float t = 0.0f;
+    for (int w = 0; w < nw; ++w) t += red[w];
+    return t;
+}
+
+template <int YMODE>
+__global__ __launch_bounds__(512) void reduce_ln_kernel(const RedLnArgs a) {
+    __shared__ float red[2][8];
+    int v = blockIdx.x, si = 0;
     if (v >= a.seg[0].M) { si = 1; v -= a.seg[0].M; }
     const RedLnSeg &S = a.seg[si];
-    const int H = NV * 256;
-    float *x = S.X + rowmap_phys(S.xmap, v) * (long long)S.ldx;
-    float4 xv[NV];
-#pragma unroll
-    for (int c = 0; c < NV; ++c) xv[c] = *(const float4 *)(x + c * 256 + lane * 4);
+    const int H = a.H, col = threadIdx.x * 4;
+    float *x = S.X + rowmap_phys(S.xmap, v) * (long long)S.ldx + col;
+    float4 xv = *(const float4 *)x;
     if (S.splits > 1) {
-        const float *g = S.gate + (long long)(v / S.gate_L) * S.gate_ld;
-#pragma unroll
-        for (int c = 0; c < NV; ++c) {
-            const int col = c * 256 + lane * 4;
-            float4 acc = *(const float4 *)(S.ws + (long long)v * H + col);
-            for (int k = 1; k < S.splits; ++k) {
-                const float4 u = *(const float4 *)(S.ws + ((long long)k * S.M + v) * H + col);
-                acc.x += u.x; acc.y += u.y; acc.z += u.z; acc.w += u.w;
-            }
-            if (S.bias) {
-                const float4 b = *(const float4 *)(S.bias + col);
-                acc.x += b.x; acc.y += b.y; acc.z += b.z; acc.w += b.w;
-            }
-            const float4 gg = *(const float4 *)(g + col);
-            xv[c].x = xv[c].x + acc.x * gg.x; xv[c].y = xv[c].y + acc.y * gg.y;
-            xv[c].z = xv[c].z + acc.z * gg.z; xv[c].w = xv[c].w + acc.w * gg.w;
-            *(float4 *)(x + col) = xv[c];
+        const float *w = S.ws + (long long)v * H + col;
+        const long long step = (long long)S.M * H;
+        float4 acc = *(const float4 *)w;
+#pragma unroll 4
+        for (int k = 1; k < S.splits; ++k) {
+            const float4 u = *(const float4 *)(w + k * step);
+            acc.x += u.x; acc.y += u.y; acc.z += u.z; acc.w += u.w;
         }
+        if (S.bias) {
+            const float4 b = *(const float4 *)(S.bias + col);
+            acc.x += b.x; acc.y += b.y; acc.z += b.z; acc.w += b.w;
+        }
+        const float4 g = *(const float4 *)(S.gate + (long long)(v / S.gate_L) * S.gate_ld + col);
+        xv.x = xv.x + acc.x * g.x; xv.y = xv.y + acc.y * g.y; xv.z = xv.z + acc.z * g.z; xv.w = xv.w + acc.w * g.w;
+        *(float4 *)x = xv;
     }
-    if (!S.ln) return;
+    if (!S.ln) return;   // uniform over the workgroup
     const int b = v / S.mod_L;
     if (v - b * S.mod_L >= S.ln_len) return;
-    float sum = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NV; ++c) sum += (xv[c].x + xv[c].y) + (xv[c].z + xv[c].w);
+    const int nw = blockDim.x >> 6;
     const float inv_h = 1.0f / (float)H;
-    const float mean = wave_sum(sum) * inv_h;
-    float var = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NV; ++c) {
-        const float d0 = xv[c].x - mean, d1 = xv[c].y - mean, d2 = xv[c].z - mean, d3 = xv[c].w - mean;
-        var += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
-    }
-    var = wave_sum(var) * inv_h;
+    const float mean = block_sum((xv.x + xv.y) + (xv.z + xv.w), red[0], nw) * inv_h;
+    const float d0 = xv.x - mean, d1 = xv.y - mean, d2 = xv.z - mean, d3 = xv.w - mean;
+    const float var = block_sum((d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3), red[1], nw) * inv_h;
     const float inv = 1.0f / sqrtf(var + a.eps);
     const float *mb = S.mod + (long long)b * S.mod_ld;
-    const long long yrow = rowmap_phys(S.ymap, v) * (long long)S.ldy;
-#pragma unroll
-    for (int c = 0; c < NV; ++c) {
-        const int col = c * 256 + lane * 4;
-        const float4 sh = *(const float4 *)(mb + S.shift_off + col);
-        const float4 scl = *(const float4 *)(mb + S.scale_off + col);
-        const float y0 = (xv[c].x - mean) * inv * (1.0f + scl.x) + sh.x;
-        const float y1 = (xv[c].y - mean) * inv * (1.0f + scl.y) + sh.y;
-        const float y2 = (xv[c].z - mean) * inv * (1.0f + scl.z) + sh.z;
-        const float y3 = (xv[c].w - mean) * inv * (1.0f + scl.w) + sh.w;
-        const half4 hi = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
-        *(half4 *)((half_t *)S.Y + yrow + col) = hi;
-        if constexpr (YMODE == LN_F16_HILO) {
-            const half4 lo = half4{(half_t)(y0 - (float)hi[0]), (half_t)(y1 - (float)hi[1]),
-                                   (half_t)(y2 - (float)hi[2]), (half_t)(y3 - (float)hi[3])};
-            *(half4 *)((half_t *)S.Y + yrow + H + col) = lo;
-        }
-    }
+    const float4 sh = *(const float4 *)(mb + S.shift_off + col);
+    const float4 scl = *(const float4 *)(mb + S.scale_off + col);
+    const float y0 = d0 * inv * (1.0f + scl.x) + sh.x;
+    const float y1 = d1 * inv * (1.0f + scl.y) + sh.y;
+    const float y2 = d2 * inv * (1.0f + scl.z) + sh.z;
+    const float y3 = d3 * inv * (1.0f + scl.w) + sh.w;
+    half_t *y = (half_t *)S.Y + rowmap_phys(S.ymap, v) * (long long)S.ldy + col;
+    const half4 hi = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
+    *(half4 *)y = hi;
+    if constexpr (YMODE == LN_F16_HILO)
+        *(half4 *)(y + H) = half4{(half_t)(y0 - (float)hi[0]), (half_t)(y1 - (float)hi[1]),
+                                  (half_t)(y2 - (float)hi[2]), (half_t)(y3 - (float)hi[3])};
 }
 
 /* ---------------- GEMV (shaders/gemm_attn.metal:47-74, batched over nb rows of X) ---------------- */
@@ -447,7 +438,7 @@ int launch_ln_mod(const LnArgs &a, int ymode, hipStream_t st) {
 
 int launch_reduce_ln(const RedLnArgs &a, hipStream_t st) {
     TSN_REQUIRE(a.nseg >= 1 && a.nseg <= 2, "reduce_ln: 1 or 2 segments");
-    TSN_REQUIRE(a.H == 1024, "reduce_ln: H must be 1024");
+    TSN_REQUIRE(a.H % 256 == 0 && a.H >= 256 && a.H <= 2048, "reduce_ln: H must be a multiple of 256 in [256, 2048]");
     TSN_REQUIRE(a.ymode == LN_F16 || a.ymode == LN_F16_HILO, "reduce_ln: output mode");
     int total = 0;
     for (int i = 0; i < a.nseg; ++i) {
@@ -459,9 +450,9 @@ int launch_reduce_ln(const RedLnArgs &a, hipStream_t st) {
                     "reduce_ln: layer-norm output");
         total += s.M;
     }
-    dim3 grid((total + 3) / 4), block(256);
-    if (a.ymode == LN_F16_HILO) TSN_LAUNCH((reduce_ln_kernel<LN_F16_HILO, 4>), grid, block, 0, st, a);
-    else TSN_LAUNCH((reduce_ln_kernel<LN_F16, 4>), grid, block, 0, st, a);
+    dim3 grid(total), block(a.H / 4);
+    if (a.ymode == LN_F16_HILO) TSN_LAUNCH((reduce_ln_kernel<LN_F16_HILO>), grid, block, 0, st, a);
+    else TSN_LAUNCH((reduce_ln_kernel<LN_F16>), grid, block, 0, st, a);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }

@@ -25,10 +25,127 @@ sys.path.insert(0, ROOT)
 
 PEAK_F16_TFLOPS = 2500.0      # MI355X dense FP16/BF16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+CAL_COPY_FLOATS = 16 << 20    # calibration copy: 64 MiB read + 64 MiB written
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_dit_eval_b2_la256.txt")
+CPU_SAMPLE_S = 10.0           # CPU baseline: whole evaluations until this much time has passed
 
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def short_kernel_name(full):
+    """'void ns::(anonymous namespace)::k<1, 4>(Args)' -> 'k<1, 4>' (the library's own kernel names)."""
+    depth, end = 0, len(full)
+    for i, ch in enumerate(full):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0 and i > 0 and full[i - 1] != ":":
+            end = i
+            break
+    name = full[:end].strip()
+    if name.startswith("void "):
+        name = name[5:]
+    depth, cut = 0, 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == ":" and depth == 0:
+            cut = i + 1
+    return name[cut:]
+
+
+def read_counter_csv(path, counter):
+    """Per-dispatch values of one counter from a rocprofv3 counter-collection CSV -> {kernel: [values]}."""
+    import csv
+    out = {}
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            if row.get("Counter_Name") != counter:
+                continue
+            out.setdefault(short_kernel_name(row["Kernel_Name"]), []).append(float(row["Counter_Value"]))
+    return out
+
+
+def pmc_summary(fetch_csv, write_csv, cmd):
+    """Text summary of FETCH_SIZE / WRITE_SIZE (KiB per dispatch) per kernel, scaled by the ratio of
+    the calibration copy's known bytes to what the same counter reads for it."""
+    fetch = read_counter_csv(fetch_csv, "FETCH_SIZE")
+    write = read_counter_csv(write_csv, "WRITE_SIZE")
+    cal_kib = CAL_COPY_FLOATS * 4 / 1024.0
+    cf = cal_kib / statistics.mean(fetch["copy_kernel"])
+    cw = cal_kib / statistics.mean(write["copy_kernel"])
+    lines = ["# HBM traffic per dispatch, one 21-block DiT evaluation (B=2, La=256, Lt=141, S=397)",
+             "# commands (rocprofv3 counter passes, one counter each):",
+             "#   " + cmd.replace("{C}", "FETCH_SIZE"),
+             "#   " + cmd.replace("{C}", "WRITE_SIZE"),
+             "# calibration: copy_kernel of %d MiB read + %d MiB written reads FETCH %.1f KiB, WRITE %.1f KiB"
+             % (cal_kib / 1024, cal_kib / 1024, statistics.mean(fetch["copy_kernel"]),
+                statistics.mean(write["copy_kernel"])),
+             "# scale factors: fetch %.4f, write %.4f (traffic = FETCH*1024*fetch_scale + WRITE*1024*write_scale)"
+             % (cf, cw),
+             "%-28s %10s %14s %14s %16s" % ("kernel", "dispatches", "FETCH KiB/d", "WRITE KiB/d", "traffic B/d")]
+    for k in sorted(set(fetch) & set(write), key=lambda n: -statistics.mean(fetch[n])):
+        fk, wk = statistics.mean(fetch[k]), statistics.mean(write[k])
+        lines.append("%-28s %10d %14.1f %14.1f %16.0f" % (k, len(fetch[k]), fk, wk, fk * 1024 * cf + wk * 1024 * cw))
+    return "\n".join(lines) + "\n"
+
+
+def read_traffic(kernel):
+    """traffic (HBM bytes per dispatch) of a kernel from the committed counter summary, or None"""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.rsplit(None, 4)
+                if not line.startswith("#") and len(parts) == 5 and parts[0] == kernel:
+                    return float(parts[4])
+    except OSError:
+        pass
+    return None
+
+
+def stats_summary(stats_csv, cmd):
+    """Text summary of a rocprofv3 --kernel-trace --stats kernel_stats.csv"""
+    import csv
+    rows = []
+    with open(stats_csv, newline="") as f:
+        for r in csv.DictReader(f):
+            rows.append((short_kernel_name(r["Name"]), int(r["Calls"]), float(r["TotalDurationNs"]) / 1e6,
+                         float(r["AverageNs"]) / 1e3, float(r["MinNs"]) / 1e3, float(r["MaxNs"]) / 1e3,
+                         float(r["Percentage"])))
+    lines = ["# rocprofv3 kernel statistics, eager launches of the DiT evaluation (B=2, La=256, Lt=141, S=397)",
+             "# command: " + cmd,
+             "%-28s %8s %12s %10s %10s %10s %7s" % ("kernel", "calls", "total ms", "avg us", "min us", "max us", "%")]
+    for r in sorted(rows, key=lambda r: -r[2]):
+        lines.append("%-28s %8d %12.3f %10.3f %10.3f %10.3f %7.2f" % r)
+    return "\n".join(lines) + "\n"
+
+
+def pmc_pass():
+    """workload for counter runs: three eager evaluations and three calibration copies"""
+    import numpy as np
+    tsn = importlib.import_module("thinksound-native_amd")
+    spec = tsn.default_spec(1)
+    rt = tsn.Runtime(0)
+    m = tsn.DitModel(rt, spec)
+    m.upload_weights(tsn.synth_weights(spec, 4242, 0.0))
+    inp = tsn.synth_inputs(spec, 4242, cfg_pairs=True)
+    z, tt, text, pooled = (rt.array(inp[k]) for k in ("z", "t", "text", "pooled"))
+    v = rt.empty((spec.B, spec.La, spec.latent))
+    a = rt.array(np.ones(CAL_COPY_FLOATS, np.float32))
+    b = rt.empty((CAL_COPY_FLOATS,))
+    for i in range(3):
+        m.forward_ex(z, tt, text, pooled, v)
+        rt.copy(a, b, CAL_COPY_FLOATS)
+        rt.sync()
+        log("pmc pass: eval %d done" % i)
+    m.close()
+    rt.close()
+    return 0
 
 
 def main():
@@ -40,11 +157,26 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--eager", action="store_true",
                     help="launch kernel by kernel instead of replaying hipGraphs (for profilers that do not follow graphs)")
+    ap.add_argument("--pmc-pass", action="store_true",
+                    help="only run three eager evaluations and a 64 MiB calibration copy (workload for rocprofv3 --pmc)")
+    ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "CMD"),
+                    help="print the traffic summary of two counter-collection CSVs (no GPU use)")
+    ap.add_argument("--stats-summary", nargs=2, metavar=("STATS_CSV", "CMD"),
+                    help="print the summary of a rocprofv3 kernel_stats.csv (no GPU use)")
     args = ap.parse_args()
+    if args.pmc_summary:
+        sys.stdout.write(pmc_summary(*args.pmc_summary))
+        return 0
+    if args.stats_summary:
+        sys.stdout.write(stats_summary(*args.stats_summary))
+        return 0
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (one process, one MI355X); --gpus %d is not supported"
               % args.gpus, file=sys.stderr)
         return 2
+
+    if args.pmc_pass:
+        return pmc_pass()
 
     tsn = importlib.import_module("thinksound-native_amd")
     spec = tsn.default_spec(1)
@@ -102,6 +234,10 @@ def main():
         achieved = (dom["bytes"] / dom["launches"]) / (avg_launch_ms * 1e-3) / 1e9
         peak, unit = PEAK_HBM_GBS, "GB/s"
     eval_flops = sum(k["flops"] for k in stats)
+    traffic = read_traffic(dom["name"])
+    if traffic is not None:
+        log("bench: %s HBM traffic %.0f B/dispatch (counters), algorithmic %.0f B/dispatch"
+            % (dom["name"], traffic, dom["bytes"] / dom["launches"]))
 
     # ---------------- the 24-step CFG sampler (graph replay) ----------------
     P = spec.B // 2
@@ -131,13 +267,18 @@ def main():
         if not os.path.exists(pyoracle.LIB_PATH):
             pyoracle.build()
         w32 = tsn.bf16_to_f32(w16)
+        n_ev = 0
         c0 = time.perf_counter()
-        pyoracle.dit_forward(spec, w32, inp["z"], inp["t"], inp["text"], inp["pooled"])
-        cpu_s = time.perf_counter() - c0
-        cpu = {"value": round(1.0 / cpu_s, 4), "unit": "evals/s", "cores": pyoracle.num_threads(), "kind": "port",
-               "sample": "one full 21-block evaluation of the timed workload (B=2, La=256, Lt=141), f32, %.2f s"
-                         % cpu_s}
-        log("bench: CPU oracle %.2f s per eval on %d threads" % (cpu_s, pyoracle.num_threads()))
+        while True:
+            pyoracle.dit_forward(spec, w32, inp["z"], inp["t"], inp["text"], inp["pooled"])
+            n_ev += 1
+            cpu_s = time.perf_counter() - c0
+            if cpu_s >= CPU_SAMPLE_S:
+                break
+        cpu = {"value": round(n_ev / cpu_s, 4), "unit": "evals/s", "cores": pyoracle.num_threads(), "kind": "port",
+               "sample": "%d full 21-block evaluations of the timed workload (B=2, La=256, Lt=141), f32 host C++ "
+                         "oracle, %.2f s" % (n_ev, cpu_s)}
+        log("bench: CPU oracle %d evals in %.2f s on %d threads" % (n_ev, cpu_s, pyoracle.num_threads()))
 
     out = {
         "metric": "DiT evals/s (8 s, CFG batch 2); 24-step sampler ms; % BF16 MFMA peak",
@@ -160,7 +301,7 @@ def main():
         "eval_gflop": round(eval_flops / 1e9, 2),
         "mfma_frac_eval": round(eval_flops / (ms_per_eval * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4),
         "roofline": {"kernel": dom["name"], "bound": bound, "achieved": round(achieved, 2), "peak": peak,
-                     "unit": unit, "frac": round(achieved / peak, 4), "traffic": None,
+                     "unit": unit, "frac": round(achieved / peak, 4), "traffic": traffic,
                      "launches_per_eval": dom["launches"], "avg_launch_us": round(avg_launch_ms * 1e3, 3)},
         "kernels": [{"name": k["name"], "launches": k["launches"], "ms": round(k["ms"], 4),
                      "share": round(k["ms"] / tot_ms, 4)} for k in stats],

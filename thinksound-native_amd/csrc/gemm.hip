@@ -399,14 +399,22 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             const float *nw = region == 0 ? P.qn : P.kn;
             half_t *dst = region == 0 ? P.Q : P.Kd;
             const float sc = region == 0 ? P.q_scale : 1.0f;
+            // this thread's 8 columns are the same in every pass: bias and norm weight loaded once
+            const int col = (tid & 15) * 8, n = n0 + col;
+            const int h = (n - region * P.Hq) >> 6, d0 = n & 63;
+            float bw[8], nwv[8];
+            if (P.bias) load8(P.bias + n, bw);
+            else
+#pragma unroll
+                for (int e = 0; e < 8; ++e) bw[e] = 0.0f;
+            load8(nw + d0, nwv);
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
-                const int c = tid + 512 * p, row = c >> 4, col = (c & 15) * 8;
-                const int m = m0 + row, n = n0 + col;
-                const int h = (n - region * P.Hq) >> 6, d0 = n & 63;
+                const int row = (tid >> 4) + 32 * p, m = m0 + row;
                 float v[8];
                 load8(tile + row * TP + col, v);
-                if (P.bias) add8(v, P.bias + n);
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] += bw[e];
                 // per-head RMS over the 64 columns held by 8 neighbouring lanes (same row, same head)
                 float ss = 0.0f;
 #pragma unroll
@@ -416,17 +424,18 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
                 ss += __shfl_xor(ss, 4);
                 const float inv = 1.0f / sqrtf(ss / 64.0f + P.rms_eps);
 #pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = v[e] * inv * nw[d0 + e];
+                for (int e = 0; e < 8; ++e) v[e] = v[e] * inv * nwv[e];
                 if (m >= M) continue;
                 const int b = m / P.q_L, t = m - b * P.q_L, s = P.q_soff + t;
                 if (t < P.rope_len) {
                     const float *cs = P.rope + (t * 32 + (d0 >> 1)) * 2;
+                    float cv[8];
+                    load8(cs, cv);
 #pragma unroll
                     for (int e = 0; e < 8; e += 2) {
-                        const float c0 = cs[e], s0 = cs[e + 1];
                         const float x0 = v[e], x1 = v[e + 1];
-                        v[e] = x0 * c0 - x1 * s0;
-                        v[e + 1] = x0 * s0 + x1 * c0;
+                        v[e] = x0 * cv[e] - x1 * cv[e + 1];
+                        v[e + 1] = x0 * cv[e + 1] + x1 * cv[e];
                     }
                 }
                 half_t *o = dst + (((long long)b * P.nh + h) * P.S_att + s) * 64 + d0;
@@ -434,31 +443,42 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
                                     (half_t)(v[4] * sc), (half_t)(v[5] * sc), (half_t)(v[6] * sc), (half_t)(v[7] * sc)};
             }
         } else {
-            // V: column-wise pass, 8 consecutive rows of one column per chunk, stored along s of Vt
-#pragma unroll
-            for (int p = 0; p < 4; ++p) {
-                const int c = tid + 512 * p, col = c & 127, row8 = (c >> 7) * 8;
-                const int n = n0 + col;
-                const int h = (n - 2 * P.Hq) >> 6, d = n & 63;
-                const float bn = P.bias ? P.bias[n] : 0.0f;
-                const int mb = m0 + row8;
-                if (mb >= M) continue;
-                const int b = mb / P.q_L, t = mb - b * P.q_L;
-                half_t *o = P.Vt + (((long long)b * P.nh + h) * 64 + d) * P.Sp;
-                if (mb + 8 <= M && t + 8 <= P.q_L && ((P.q_soff + t) & 7) == 0) {
+            // V, stored transposed along s: Vt[b][h][d][s]. The tile's rows are cut into chunks of 8
+            // positions aligned in s (per sample), so interior chunks are one 16-byte store; chunks at
+            // a sample or tile edge store only their valid elements. Lanes run along columns, so the
+            // LDS reads of a chunk (8 rows, one column) are conflict-free.
+            const int col = tid & 127, n = n0 + col;
+            const int h = (n - 2 * P.Hq) >> 6, d = n & 63;
+            const float bn = P.bias ? P.bias[n] : 0.0f;
+            const int m1 = min(m0 + BM, M);
+            const int b0 = m0 / P.q_L, b1 = (m1 - 1) / P.q_L;
+            int total = 0;
+            for (int b = b0; b <= b1; ++b) {
+                const int ta = max(m0 - b * P.q_L, 0), tb = min(m1 - b * P.q_L, P.q_L);
+                total += (P.q_soff + tb + 7) / 8 - (P.q_soff + ta) / 8;
+            }
+            for (int g = tid >> 7; g < total; g += 4) {
+                int b = b0, j = g, ta = 0, tb = 0;
+                for (;; ++b) {   // the sample this chunk belongs to (every g < total has one)
+                    ta = max(m0 - b * P.q_L, 0);
+                    tb = min(m1 - b * P.q_L, P.q_L);
+                    const int nb = (P.q_soff + tb + 7) / 8 - (P.q_soff + ta) / 8;
+                    if (j < nb) break;
+                    j -= nb;
+                }
+                const int s8 = ((P.q_soff + ta) / 8 + j) * 8;    // first s of the chunk
+                const int r8 = b * P.q_L + (s8 - P.q_soff) - m0;  // tile row of s8 (may lie outside)
+                half_t *o = P.Vt + (((long long)b * P.nh + h) * 64 + d) * P.Sp + s8;
+                if (s8 >= P.q_soff + ta && s8 + 8 <= P.q_soff + tb) {
                     half8 hv;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) hv[e] = (half_t)(tile[(row8 + e) * TP + col] + bn);
-                    *(half8 *)(o + P.q_soff + t) = hv;
+                    for (int e = 0; e < 8; ++e) hv[e] = (half_t)(tile[(r8 + e) * TP + col] + bn);
+                    *(half8 *)o = hv;
                 } else {
-                    // unaligned or crossing a sample boundary: element stores, (b, t) stepped along
-                    int bb = b, tt = t;
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
-                        if (mb + e >= M) break;
-                        P.Vt[(((long long)bb * P.nh + h) * 64 + d) * P.Sp + P.q_soff + tt] =
-                            (half_t)(tile[(row8 + e) * TP + col] + bn);
-                        if (++tt == P.q_L) { tt = 0; ++bb; }
+                        const int ss = s8 + e;
+                        if (ss >= P.q_soff + ta && ss < P.q_soff + tb) o[e] = (half_t)(tile[(r8 + e) * TP + col] + bn);
                     }
                 }
             }
@@ -736,6 +756,11 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         if (epi == EPI_RESID)
             pipe = pipe && (((uintptr_t)p.R) & 15) == 0 && (((uintptr_t)p.gate) & 15) == 0 && p.ldr % 4 == 0 &&
                    p.gate_ld % 4 == 0;
+        // q/k rows and s-aligned chunks of Vt rows as 16-byte stores; norm weights and rope rows as
+        // 16-byte loads
+        if (epi == EPI_QKV)
+            pipe = pipe && ((((uintptr_t)p.Q) | ((uintptr_t)p.Kd) | ((uintptr_t)p.Vt) | ((uintptr_t)p.qn) |
+                             ((uintptr_t)p.kn) | ((uintptr_t)p.rope)) & 15) == 0 && p.Sp % 8 == 0;
     }
     // Split-K (pipelined kernel, residual epilogue, workspace given): one common K chunk of kc
     // tiles for every problem, the largest kc (>= 4) that divides every problem's K tiles and gives

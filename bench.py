@@ -34,8 +34,29 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def _demangled_tail(mangled):
+    """last component (with integer template arguments) of an Itanium nested name: _ZN..k..ILi1ELi4EE.. -> k<1, 4>"""
+    i, name, args = 3, mangled, []
+    while i < len(mangled) and mangled[i].isdigit():
+        j = i
+        while mangled[j].isdigit():
+            j += 1
+        n = int(mangled[i:j])
+        name, args, i = mangled[j:j + n], [], j + n
+        if mangled.startswith("IL", i):   # integer template arguments L<type><value>E ... E
+            i += 1
+            while mangled.startswith("L", i):
+                e = mangled.index("E", i)
+                args.append(mangled[i + 2:e].replace("n", "-"))
+                i = e + 1
+            i += 1
+    return name + ("<%s>" % ", ".join(args) if args else "")
+
+
 def short_kernel_name(full):
     """'void ns::(anonymous namespace)::k<1, 4>(Args)' -> 'k<1, 4>' (the library's own kernel names)."""
+    if full.startswith("_ZN"):
+        return _demangled_tail(full)
     depth, end = 0, len(full)
     for i, ch in enumerate(full):
         if ch == "<":

@@ -98,6 +98,9 @@ def test_forward_bit_identical_and_graph(tsn, rt, orc, model):
         rt.sync()
         c = v3.numpy()
         assert np.array_equal(a.view(np.uint32), c.view(np.uint32))
+        # eager work on the same buffers between replays
+        m.forward_ex(dev["z"], dev["t"], dev["text"], dev["pooled"], v2)
+        rt.sync()
     # scalar-t entry point (DitModel::forward signature) matches the device-t one
     m.forward(dev["z"], float(inp["t"][0]), dev["text"], dev["pooled"], v2)
     rt.sync()

@@ -330,6 +330,16 @@ __device__ __forceinline__ void load8(const float *t, float (&v)[8]) {
     const floatx4 a = *(const floatx4 *)t, b = *(const floatx4 *)(t + 4);
     v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3]; v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
 }
+// the C tile is held as two f32 halves (the two K halves of the workgroup), TSZ floats apart;
+// every epilogue read sums them (half 0 + half 1, the accumulation order of the K loop)
+constexpr int TSZ = BM * TP;
+__device__ __forceinline__ void ldsum8(const float *t, int off, float (&v)[8]) {
+    const floatx4 a = *(const floatx4 *)(t + off), b = *(const floatx4 *)(t + off + 4);
+    const floatx4 c = *(const floatx4 *)(t + TSZ + off), d = *(const floatx4 *)(t + TSZ + off + 4);
+    v[0] = a[0] + c[0]; v[1] = a[1] + c[1]; v[2] = a[2] + c[2]; v[3] = a[3] + c[3];
+    v[4] = b[0] + d[0]; v[5] = b[1] + d[1]; v[6] = b[2] + d[2]; v[7] = b[3] + d[3];
+}
+__device__ __forceinline__ float ldsum1(const float *t, int off) { return t[off] + t[TSZ + off]; }
 __device__ __forceinline__ void add8(float (&v)[8], const float *p) {
     const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
     v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w; v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
@@ -347,8 +357,10 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             const int m = m0 + row, n = n0 + col;
             if (m < M && n < N) {
                 float *o = w + (long long)m * N + n;
-                *(floatx4 *)o = *(const floatx4 *)(tile + row * TP + col);
-                *(floatx4 *)(o + 4) = *(const floatx4 *)(tile + row * TP + col + 4);
+                float v[8];
+                ldsum8(tile, row * TP + col, v);
+                *(float4 *)o = make_float4(v[0], v[1], v[2], v[3]);
+                *(float4 *)(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
             }
         }
         return;
@@ -360,7 +372,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             const int m = m0 + row, n = n0 + col;
             if (m >= M || n >= N) continue;
             float v[8];
-            load8(tile + row * TP + col, v);
+            ldsum8(tile, row * TP + col, v);
             if (P.bias) add8(v, P.bias + n);
             if (P.silu)
 #pragma unroll
@@ -382,7 +394,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             const int m = m0 + row, n = n0 + col;
             if (m >= M || n >= N) continue;
             float v[8];
-            load8(tile + row * TP + col, v);
+            ldsum8(tile, row * TP + col, v);
             if (P.bias) add8(v, P.bias + n);
             const float *g = P.gate + (long long)(m / P.gate_L) * P.gate_ld + n;
             float *x = P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n;
@@ -412,7 +424,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             for (int p = 0; p < 4; ++p) {
                 const int row = (tid >> 4) + 32 * p, m = m0 + row;
                 float v[8];
-                load8(tile + row * TP + col, v);
+                ldsum8(tile, row * TP + col, v);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] += bw[e];
                 // per-head RMS over the 64 columns held by 8 neighbouring lanes (same row, same head)
@@ -472,13 +484,13 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
                 if (s8 >= P.q_soff + ta && s8 + 8 <= P.q_soff + tb) {
                     half8 hv;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) hv[e] = (half_t)(tile[(r8 + e) * TP + col] + bn);
+                    for (int e = 0; e < 8; ++e) hv[e] = (half_t)(ldsum1(tile, (r8 + e) * TP + col) + bn);
                     *(half8 *)o = hv;
                 } else {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int ss = s8 + e;
-                        if (ss >= P.q_soff + ta && ss < P.q_soff + tb) o[e] = (half_t)(tile[(r8 + e) * TP + col] + bn);
+                        if (ss >= P.q_soff + ta && ss < P.q_soff + tb) o[e] = (half_t)(ldsum1(tile, (r8 + e) * TP + col) + bn);
                     }
                 }
             }
@@ -618,24 +630,16 @@ __global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
     block_barrier();
     float *tile = (float *)smem;
     {
+        // both K halves store their partial tile at once (half kh at tile + kh*TSZ); the epilogue
+        // reads add them
         const int rb = wm * 64 + (lane >> 4) * 4, cb = wn * 64 + (lane & 15);
-        if (kh == 0) {
+        float *th = tile + kh * TSZ;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+            for (int j = 0; j < 4; ++j)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) tile[(rb + i * 16 + r) * TP + cb + j * 16] = acc[i][j][r];
-        }
-        block_barrier();
-        if (kh == 1) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) tile[(rb + i * 16 + r) * TP + cb + j * 16] += acc[i][j][r];
-        }
+                for (int r = 0; r < 4; ++r) th[(rb + i * 16 + r) * TP + cb + j * 16] = acc[i][j][r];
         block_barrier();
     }
     tile_epilogue<EPI>(P, tile, m0, n0, ks, tid);

@@ -8,7 +8,9 @@
 // 8 waves: wave w serves queries 16*(w&3)..+15; waves 0-3 take the even 64-key blocks and waves
 // 4-7 the odd ones, each half keeping its own running max / sum / output, merged through LDS at
 // the end. K and Vᵀ blocks reach LDS by direct-to-LDS buffer loads (no register staging) into a
-// ring of 4 stages x 2 blocks (128 KB); at S <= 512 every key is resident after the prologue.
+// ring of 4 stages x 2 blocks (128 KB); at S <= 512 all of them are loaded at once and the key
+// loop runs without barriers. The running max is shared by the four lanes holding a query's keys
+// (row-swap permutes); the running sum is an MFMA product of the probabilities with ones.
 //
 // MFMA formulation (v_mfma_f32_16x16x32_f16; A row = lane&15, B col = lane&15, K group = lane>>4,
 // D[4*(lane>>4)+r][lane&15]):
@@ -62,6 +64,17 @@ __device__ __forceinline__ void block_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// Max over the four 16-lane rows holding one query's keys (lanes l, l^16, l^32, l^48),
+// with the gfx950 row-swap permutes (VALU, no LDS round trip). permlane16_swap(x, x) yields the
+// even-row and the odd-row copy of each row pair, permlane32_swap(x, x) the lower- and the
+// upper-half copy; combining them gives every lane of a group the same value.
+__device__ __forceinline__ float rows_max(float v) {
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+
 __global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
     __shared__ __attribute__((aligned(1024))) half_t smem[ANS * ASTAGE];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -101,10 +114,15 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
         }
     };
 
-    float m_i = -INFINITY, l_i = 0.0f;
-    floatx4 o[4];
+    // running max m_i (scaled, log2 units); Oᵀ and the running row sum live in MFMA accumulators:
+    // the sum is Pᵀ multiplied by a tile of ones, i.e. exactly the f32 sum of the f16 probabilities
+    // the numerator uses, already reduced over all keys of the block.
+    float m_i = -INFINITY;
+    floatx4 o[4], lsum = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const half8 ones = half8{1, 1, 1, 1, 1, 1, 1, 1};
+    const float scale = a.scale_log2;
 
     // key block blk of this half, resident in stage st
     auto compute = [&](int st, int blk) {
@@ -121,35 +139,27 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
                 sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], sc[j], 0, 0, 0);
             }
         }
-        float x[4][4];
+        if (blk * AKB + AKB > S) {   // the last, partial key block only (wave-uniform)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (blk * AKB + j * 16 + g * 4 + r >= S) sc[j][r] = -INFINITY;
+        }
         float mx = -INFINITY;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int key = blk * AKB + j * 16 + g * 4 + r;
-                x[j][r] = key < S ? sc[j][r] * a.scale_log2 : -INFINITY;
-                mx = fmaxf(mx, x[j][r]);
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_i, mx);
-        const float alpha = exp2f(m_i - m_new);
-        half_t ph[4][4];
-        float psum = 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                ph[j][r] = (half_t)exp2f(x[j][r] - m_new);
-                psum += (float)ph[j][r];
-            }
-        psum += __shfl_xor(psum, 16);
-        psum += __shfl_xor(psum, 32);
-        l_i = l_i * alpha + psum;
+        for (int j = 0; j < 4; ++j) mx = fmaxf(fmaxf(mx, fmaxf(sc[j][0], sc[j][1])), fmaxf(sc[j][2], sc[j][3]));
+        const float m_new = fmaxf(m_i, rows_max(mx) * scale);   // scale > 0: max commutes with it
+        const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
         m_i = m_new;
+        half_t ph[4][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ph[j][r] = (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r], scale, -m_new));
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+        lsum *= alpha;
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const half8 pf = half8{ph[2 * c][0], ph[2 * c][1], ph[2 * c][2], ph[2 * c][3],
@@ -165,25 +175,36 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
                 const half8 vf = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                 o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[dt], 0, 0, 0);
             }
+            lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lsum, 0, 0, 0);
         }
     };
 
-    // ring over pairs of key blocks, as in the GEMM: pair p in stage p % ANS
-    issue(0, 0);
-    if (npair > 1) issue(1, 1);
-    if (npair > 2) issue(2, 2);
-    wait_vmcnt(4 * min(npair - 1, 2));
-    block_barrier();
-    if (npair > 3) issue(3, 3);
-    for (int p = 0; p < npair; ++p) {
-        const int st = p % ANS;
-        if (2 * p + half < nkb) compute(st, 2 * p + half);
-        if (p + 1 < npair) {
-            wait_vmcnt(4 * min(npair - 2 - p, 2));
-            block_barrier();
-            if (p + ANS < npair) issue(p + ANS, st);
+    if (npair <= ANS) {
+        // every key block fits the ring: load all, one wait, no barrier inside the loop
+        for (int p = 0; p < npair; ++p) issue(p, p);
+        wait_vmcnt(0);
+        block_barrier();
+        for (int p = 0; p < npair; ++p)
+            if (2 * p + half < nkb) compute(p, 2 * p + half);
+    } else {
+        // ring over pairs of key blocks, as in the GEMM: pair p in stage p % ANS
+        issue(0, 0);
+        issue(1, 1);
+        issue(2, 2);
+        wait_vmcnt(8);
+        block_barrier();
+        issue(3, 3);
+        for (int p = 0; p < npair; ++p) {
+            const int st = p % ANS;
+            if (2 * p + half < nkb) compute(st, 2 * p + half);
+            if (p + 1 < npair) {
+                wait_vmcnt(4 * min(npair - 2 - p, 2));
+                block_barrier();
+                if (p + ANS < npair) issue(p + ANS, st);
+            }
         }
     }
+    float l_i = lsum[0];   // every row of the ones product holds the same sum
 
     // merge the two halves: waves 4-7 park (m, l, O) in LDS, waves 0-3 combine and store
     block_barrier();

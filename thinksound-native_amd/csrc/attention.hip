@@ -14,17 +14,16 @@
 //
 // MFMA formulation (v_mfma_f32_16x16x32_f16; A row = lane&15, B col = lane&15, K group = lane>>4,
 // D[4*(lane>>4)+r][lane&15]):
-//   Sᵀ = K·Qᵀ  : A = K rows from LDS, B = the wave's Q rows (registers). Lane l then holds the
-//                scores of query l&15 for keys 16j + 4(l>>4) + r.
-//   Oᵀ += Vᵀ·Pᵀ: B = the lane's own probabilities (keys 32c + 4g + r and 32c + 16 + 4g + r form
-//                the 8 K-values of group g = l>>4 — the same key order is used for Vᵀ), A = Vᵀ
-//                rows read from LDS. Lane l holds Oᵀ[d = 16dt + 4g + r][query l&15], so the
-//                per-query rescale and the final 1/l are lane-local.
+//   Sᵀ = K·Qᵀ  : A = K rows from LDS (row order permuted, see compute), B = the wave's Q rows
+//                (registers). Lane l then holds the scores of query l&15 for keys 32c + 8g + 0..7
+//                of each 32-key chunk c (g = l>>4).
+//   Oᵀ += Vᵀ·Pᵀ: B = the lane's own probabilities (those 8 keys are the 8 K-values of group g),
+//                A = Vᵀ rows read from LDS, one 16-byte chunk per lane. Lane l holds
+//                Oᵀ[d = 16dt + 4g + r][query l&15], so the per-query rescale and 1/l are lane-local.
 // Probabilities are rounded to f16 before both the PV product and the row sum, so numerator and
 // denominator see the same values.
 //
-// LDS rows are 128 B (64 halves = 8 chunks of 16 B); chunk c of row r sits at slot c ^ (r & 7)
-// (the same swizzle as the GEMM), so the 16 rows an MFMA operand read touches hit distinct banks.
+// LDS rows are 128 B (64 halves = 8 chunks of 16 B); chunk c of row r sits at slot c ^ sw(r).
 #include "kernels.h"
 
 namespace tsn {
@@ -48,6 +47,9 @@ __device__ __forceinline__ i32x4 make_rsrc(const void *p) {
 // inline asm and ordered by explicit vmcnt waits; s_nop 0 covers the M0 -> LDS-DMA hazard)
 __device__ __forceinline__ void dma16(i32x4 rs, unsigned voff, lds_char *lds) {
     const unsigned l = __builtin_amdgcn_readfirstlane((unsigned)(unsigned long)lds);
+    // the resource is wave-uniform; make that explicit so it is kept in SGPRs
+    rs = i32x4{__builtin_amdgcn_readfirstlane(rs[0]), __builtin_amdgcn_readfirstlane(rs[1]),
+               __builtin_amdgcn_readfirstlane(rs[2]), __builtin_amdgcn_readfirstlane(rs[3])};
     asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
                  :
                  : "v"(voff), "s"(rs), "s"(l)
@@ -75,6 +77,10 @@ __device__ __forceinline__ float rows_max(float v) {
     return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
 
+// LDS slot of 16-byte chunk c of row r: c ^ sw(r). Rows 8 apart get different slots too, so the
+// 16 rows one operand read touches (K rows 8 apart, see below) fall in distinct banks.
+__device__ __forceinline__ int sw(int r) { return (r & 7) ^ ((r >> 3) & 7); }
+
 __global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
     __shared__ __attribute__((aligned(1024))) half_t smem[ANS * ASTAGE];
     const int tid = threadIdx.x, lane = tid & 63;
@@ -96,12 +102,14 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
     const int nkb = (S + AKB - 1) / AKB;
     const int npair = (nkb + 1) / 2;
     // DMA of pair p: 32 blocks of 1 KB (K of block 2p, K of 2p+1, Vt of 2p, Vt of 2p+1, 8 each);
-    // wave w issues blocks 4w..4w+3. Lane row lr = lane >> 3, chunk lc = (lane & 7) ^ lr.
-    const int lr = lane >> 3, lc = (lane & 7) ^ lr;
+    // wave w issues blocks 4w..4w+3. Block sub holds rows 8sub..8sub+7; lane l writes slot l & 7
+    // of row lr = l >> 3, i.e. source chunk lc = (l & 7) ^ sw(8sub + lr).
+    const int lr = lane >> 3;
     auto issue = [&](int p, int stage) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int d = wave * 4 + i, part = d >> 3, sub = d & 7;
+            const int lc = (lane & 7) ^ lr ^ sub;
             const int blk = 2 * p + (part & 1);
             unsigned vo = 0x80000000u;
             if (part < 2) {
@@ -128,14 +136,18 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
     auto compute = [&](int st, int blk) {
         const half_t *sK = smem + st * ASTAGE + half * 4096;
         const half_t *sV = smem + st * ASTAGE + 8192 + half * 4096;
+        // Sᵀ row i of MFMA block j is key 32(j>>1) + 8(i>>2) + 4(j&1) + (i&3), so lane group g
+        // ends up with keys 32c + 8g + 0..7 of each 32-key chunk c (j = 2c, 2c+1): exactly the K
+        // order of one contiguous 16-byte Vᵀ read in the PV product.
         floatx4 sc[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             sc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-            const int r = j * 16 + (lane & 15);
+            const int i = lane & 15;
+            const int r = 32 * (j >> 1) + 8 * (i >> 2) + 4 * (j & 1) + (i & 3);
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-                const half8 kf = *(const half8 *)(sK + r * 64 + (((ks * 4 + g) ^ (r & 7)) * 8));
+                const half8 kf = *(const half8 *)(sK + r * 64 + (((ks * 4 + g) ^ sw(r)) * 8));
                 sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], sc[j], 0, 0, 0);
             }
         }
@@ -144,7 +156,7 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int r = 0; r < 4; ++r)
-                    if (blk * AKB + j * 16 + g * 4 + r >= S) sc[j][r] = -INFINITY;
+                    if (blk * AKB + 32 * (j >> 1) + 8 * g + 4 * (j & 1) + r >= S) sc[j][r] = -INFINITY;
         }
         float mx = -INFINITY;
 #pragma unroll
@@ -166,13 +178,9 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
                                    ph[2 * c + 1][0], ph[2 * c + 1][1], ph[2 * c + 1][2], ph[2 * c + 1][3]};
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                // Vt row d = 16dt + (lane&15); keys 32c + 4g + 0..3 and 32c + 16 + 4g + 0..3
+                // Vt row d = 16dt + (lane&15), keys 32c + 8g + 0..7 (chunk 4c + g)
                 const int d = dt * 16 + (lane & 15);
-                const half_t *row = sV + d * 64;
-                const int c0 = c * 4 + (g >> 1), c1 = c0 + 2, hb = (g & 1) * 4;
-                const half4 lo = *(const half4 *)(row + ((c0 ^ (d & 7)) * 8) + hb);
-                const half4 hi = *(const half4 *)(row + ((c1 ^ (d & 7)) * 8) + hb);
-                const half8 vf = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                const half8 vf = *(const half8 *)(sV + d * 64 + (((c * 4 + g) ^ sw(d)) * 8));
                 o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[dt], 0, 0, 0);
             }
             lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lsum, 0, 0, 0);

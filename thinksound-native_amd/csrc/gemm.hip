@@ -35,7 +35,8 @@ __device__ inline int xcd_remap(int bid, int nwg) {
 
 __device__ inline half8 zero_h8() { return half8{0, 0, 0, 0, 0, 0, 0, 0}; }
 
-__device__ inline float silu_f(float v) { return v / (1.0f + __expf(-v)); }
+// x·sigmoid(x) with the hardware reciprocal (1 ulp): exp(-v) = inf gives rcp = 0, so silu -> -0
+__device__ inline float silu_f(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 
 // Fused epilogue shared by both kernels. acc[i][j][r] holds C[row][col] of the wave's 64x64
 // block: row = wm*64 + i*16 + (lane>>4)*4 + r, col = wn*64 + j*16 + (lane&15).

@@ -266,14 +266,14 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const GemmBatch bt) {
 
 
 // ---------------------------------------------------------------------------------------------
-// Pipelined kernel (f16 A, K % 64 == 0). 512 threads = 8 waves, two per SIMD: waves 0-3 and 4-7
-// own the same four 64x64 output quadrants and split every 64-wide K tile between them (k 0..31 /
-// 32..63); the halves are summed through LDS at the end. Two waves per SIMD let one wave's LDS
-// reads hide behind the other's MFMAs, which a single wave per SIMD cannot do.
+// Pipelined kernel (f16 A, K % 64 == 0). 512 threads = 8 waves, two per SIMD; wave w owns the
+// 32x64 block (rows 32*(w>>1), columns 64*(w&1)) of the 128x128 tile over the full K. Two waves
+// per SIMD let one wave's LDS reads hide behind the other's MFMAs.
 //
 // Operands go global -> LDS with buffer_load_dwordx4 ... lds (no register staging, see dma16) into
-// 4 stages of one 128x64 A tile + one 128x64 W tile each (128 KB): three K tiles are in flight
-// while the fourth is multiplied, with one barrier per K tile.
+// NS = 5 stages of one 128x64 A tile + one 128x64 W tile each (160 KB): four K tiles are in flight
+// while the fifth is multiplied, with one barrier per K tile. The C tile is staged through LDS for
+// the epilogue (f32, pitch TP).
 //
 // LDS layout of a stage: row r (128 B = 8 chunks of 8 halves) keeps chunk c at slot c ^ (r & 7).
 // A direct-to-LDS load writes lane l's 16 bytes to slot l of a 1 KB block (8 rows), so lane l of
@@ -331,16 +331,8 @@ __device__ __forceinline__ void load8(const float *t, float (&v)[8]) {
     const floatx4 a = *(const floatx4 *)t, b = *(const floatx4 *)(t + 4);
     v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3]; v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
 }
-// the C tile is held as two f32 halves (the two K halves of the workgroup), TSZ floats apart;
-// every epilogue read sums them (half 0 + half 1, the accumulation order of the K loop)
-constexpr int TSZ = BM * TP;
-__device__ __forceinline__ void ldsum8(const float *t, int off, float (&v)[8]) {
-    const floatx4 a = *(const floatx4 *)(t + off), b = *(const floatx4 *)(t + off + 4);
-    const floatx4 c = *(const floatx4 *)(t + TSZ + off), d = *(const floatx4 *)(t + TSZ + off + 4);
-    v[0] = a[0] + c[0]; v[1] = a[1] + c[1]; v[2] = a[2] + c[2]; v[3] = a[3] + c[3];
-    v[4] = b[0] + d[0]; v[5] = b[1] + d[1]; v[6] = b[2] + d[2]; v[7] = b[3] + d[3];
-}
-__device__ __forceinline__ float ldsum1(const float *t, int off) { return t[off] + t[TSZ + off]; }
+__device__ __forceinline__ void ldsum8(const float *t, int off, float (&v)[8]) { load8(t + off, v); }
+__device__ __forceinline__ float ldsum1(const float *t, int off) { return t[off]; }
 __device__ __forceinline__ void add8(float (&v)[8], const float *p) {
     const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
     v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w; v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
@@ -560,33 +552,40 @@ __global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
         }
     };
 
-    floatx4 acc[4][4];
+    // wave w owns rows 32*(w>>1)..+31 and columns 64*(w&1)..+63 of the tile over the full K:
+    // 2 x 4 MFMA blocks of 16x16, two 32-wide K halves per 64-wide stage
+    floatx4 acc[2][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    const int kh = wave >> 2, wq = wave & 3, wm = wq >> 1, wn = wq & 1;
-    // operand read offsets (halves) inside a stage for this wave's 32-wide K half
-    int a_rd[4], b_rd[4];
+    const int wm = wave >> 1, wn = wave & 1;
+    // operand read offsets (halves) inside a stage, per K half kh: slot (4kh + lane>>4) ^ (row & 7)
+    int a_rd[2][2], b_rd[2][4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int kh = 0; kh < 2; ++kh) {
         const int slot = (kh * 4 + (lane >> 4)) ^ (lane & 7);
-        a_rd[i] = (wm * 64 + i * 16 + (lane & 15)) * BK + slot * 8;
-        b_rd[i] = (wn * 64 + i * 16 + (lane & 15)) * BK + slot * 8;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) a_rd[kh][i] = (wm * 32 + i * 16 + (lane & 15)) * BK + slot * 8;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b_rd[kh][j] = (wn * 64 + j * 16 + (lane & 15)) * BK + slot * 8;
     }
     auto compute = [&](int stage) {
         const half_t *sa = smem + stage * STAGE, *sb = smem + (NS + stage) * STAGE;
-        half8 af[4], bf[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) af[i] = *(const half8 *)(sa + a_rd[i]);
+        for (int kh = 0; kh < 2; ++kh) {
+            half8 af[2], bf[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bf[j] = *(const half8 *)(sb + b_rd[j]);
+            for (int i = 0; i < 2; ++i) af[i] = *(const half8 *)(sa + a_rd[kh][i]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+            for (int j = 0; j < 4; ++j) bf[j] = *(const half8 *)(sb + b_rd[kh][j]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
     };
 
     // Loop invariant at the top of an iteration: tile kt has landed in stage kt%NS for every wave,
@@ -626,21 +625,19 @@ __global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
             if (kt + NS < nk) issue(kt + NS, st);
         }
     }
-    // Every DMA has landed (the last tile was waited for). Sum the two K halves into a row-major
-    // f32 C tile in LDS, then all 8 waves run the epilogue on 8-column chunks (16-byte accesses).
+    // Every DMA has landed (the last tile was waited for). The waves store their accumulators as a
+    // row-major f32 C tile in LDS, then all 8 waves run the epilogue on 8-column chunks (16-byte
+    // accesses).
     block_barrier();
     float *tile = (float *)smem;
     {
-        // both K halves store their partial tile at once (half kh at tile + kh*TSZ); the epilogue
-        // reads add them
-        const int rb = wm * 64 + (lane >> 4) * 4, cb = wn * 64 + (lane & 15);
-        float *th = tile + kh * TSZ;
+        const int rb = wm * 32 + (lane >> 4) * 4, cb = wn * 64 + (lane & 15);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) th[(rb + i * 16 + r) * TP + cb + j * 16] = acc[i][j][r];
+                for (int r = 0; r < 4; ++r) tile[(rb + i * 16 + r) * TP + cb + j * 16] = acc[i][j][r];
         block_barrier();
     }
     tile_epilogue<EPI>(P, tile, m0, n0, ks, tid);

@@ -378,7 +378,7 @@ void DitModel::next_ln(RedLnArgs &r, Next next, const RowMap *maps, int nseg) {
         RedLnSeg &g = r.seg[i];
         const RowMap &m = maps[i];
         const bool text = m.off >= s.La;   // rows of the text stream inside the joint layout
-        g.mod = MOD_; g.mod_ld = NMOD; g.mod_L = m.L; g.ln_len = m.L;
+        g.mod = mod_; g.mod_ld = NMOD; g.mod_L = m.L; g.ln_len = m.L;
         g.Y = XN_; g.ldy = s.H; g.ymap = m;
         switch (next.kind) {
         case NEXT_JOINT: g.ln = 1; g.shift_off = (text ? jt_ : ja_)[next.idx].mod_off; break;
@@ -406,8 +406,8 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
         LnArgs ln;
         memset(&ln, 0, sizeof ln);
         ln.nseg = 2; ln.H = H; ln.eps = s.ln_eps;
-        ln_seg(ln.seg[0], X_, H, Sa, XN_, MOD_, NMOD, La, a.mod_off, B * La);
-        ln_seg(ln.seg[1], X_, H, St, XN_, MOD_, NMOD, Lt, t.mod_off, B * Lt);
+        ln_seg(ln.seg[0], X_, H, Sa, XN_, mod_, NMOD, La, a.mod_off, B * La);
+        ln_seg(ln.seg[1], X_, H, St, XN_, mod_, NMOD, Lt, t.mod_off, B * Lt);
         TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16, st); }));
     }
 
@@ -429,8 +429,8 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
     ob.nprob = 2;
     ob.ws = ws_;
     ob.ws_bytes = ws_bytes_;
-    resid_problem(ob.p[0], AO_, H, Sa, 1, H, B * La, H, a.Wo, a.bo, X_, H, MOD_ + a.mod_off + 2 * H, NMOD);
-    resid_problem(ob.p[1], AO_, H, St, 1, H, B * Lt, H, t.Wo, t.bo, X_, H, MOD_ + t.mod_off + 2 * H, NMOD);
+    resid_problem(ob.p[0], AO_, H, Sa, 1, H, B * La, H, a.Wo, a.bo, X_, H, mod_ + a.mod_off + 2 * H, NMOD);
+    resid_problem(ob.p[1], AO_, H, St, 1, H, B * Lt, H, t.Wo, t.bo, X_, H, mod_ + t.mod_off + 2 * H, NMOD);
     RedLnArgs r;
     next_ln(r, Next{NEXT_JOINT, i}, maps, 2);   // LN2 of this block: modulation chunks 3, 4
     r.seg[0].shift_off += 3 * H; r.seg[0].scale_off += 3 * H;
@@ -448,8 +448,8 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
     f2.nprob = 2;
     f2.ws = ws_;
     f2.ws_bytes = ws_bytes_;
-    resid_problem(f2.p[0], HF_, s.F, Sa, ta, s.F, B * La, H, a.W2, nullptr, X_, H, MOD_ + a.mod_off + 5 * H, NMOD);
-    resid_problem(f2.p[1], HF_, s.F, St, 1, s.F, B * Lt, H, t.W2, nullptr, X_, H, MOD_ + t.mod_off + 5 * H, NMOD);
+    resid_problem(f2.p[0], HF_, s.F, Sa, ta, s.F, B * La, H, a.W2, nullptr, X_, H, mod_ + a.mod_off + 5 * H, NMOD);
+    resid_problem(f2.p[1], HF_, s.F, St, 1, s.F, B * Lt, H, t.W2, nullptr, X_, H, mod_ + t.mod_off + 5 * H, NMOD);
     next_ln(r, next, maps, 2);
     return resid_ln(f2, r);
 }
@@ -464,7 +464,7 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
         LnArgs ln;
         memset(&ln, 0, sizeof ln);
         ln.nseg = 1; ln.H = H; ln.eps = s.ln_eps;
-        ln_seg(ln.seg[0], X_, H, D, XN_, MOD_, NMOD, S, w.mod_off, M);
+        ln_seg(ln.seg[0], X_, H, D, XN_, mod_, NMOD, S, w.mod_off, M);
         TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16, st); }));
     }
 
@@ -485,7 +485,7 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
     ob.nprob = 1;
     ob.ws = ws_;
     ob.ws_bytes = ws_bytes_;
-    resid_problem(ob.p[0], AO_, H, D, 1, H, M, H, w.Wo, w.bo, X_, H, MOD_ + w.mod_off + 2 * H, NMOD);
+    resid_problem(ob.p[0], AO_, H, D, 1, H, M, H, w.Wo, w.bo, X_, H, mod_ + w.mod_off + 2 * H, NMOD);
     RedLnArgs r;
     next_ln(r, Next{NEXT_FUSED, i}, &D, 1);   // LN2 of this block: modulation chunks 3, 4
     r.seg[0].shift_off += 3 * H; r.seg[0].scale_off += 3 * H;
@@ -500,34 +500,66 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
     f2.nprob = 1;
     f2.ws = ws_;
     f2.ws_bytes = ws_bytes_;
-    resid_problem(f2.p[0], HF_, s.F, D, 1, s.F, M, H, w.W2, nullptr, X_, H, MOD_ + w.mod_off + 5 * H, NMOD);
+    resid_problem(f2.p[0], HF_, s.F, D, 1, s.F, M, H, w.W2, nullptr, X_, H, mod_ + w.mod_off + 5 * H, NMOD);
     next_ln(r, next, &D, 1);
     return resid_ln(f2, r);
 }
 
+// timestep embedding + MLP, g = t_emb + pooled, gs = silu(g) (src/dit_fwd.cpp:111-140), then every
+// adaLN modulation in one HBM-bound GEMV (src/dit_fwd.cpp:186-207,271-274,288-291). Rows are
+// processed in GEMV batches of up to 16 (the weights are read once per batch); pooled row r is
+// pooled[r % 16] (callers pass B rows for B <= 16 batches, or the 16-row repetition).
+int DitModel::enqueue_conditioning(const float *t, int rows, const float *pooled, float *temb, float *h1, float *g,
+                                   float *gs, float *mod) {
+    const hipStream_t st = rt->dev.stream();
+    const int H = s.H;
+    TSN_TRY(run("temb_kernel", 0, 0, [&] { return launch_temb_sinusoid(t, temb, rows, s.temb_dim, s.t_max_period, st); }));
+    for (int r0 = 0; r0 < rows; r0 += 16) {
+        const int rem = rows - r0;
+        const int nb = rem >= 16 ? 16 : rem > 8 ? 16 : rem > 4 ? 8 : rem > 2 ? 4 : rem;   // rows past `rows` are padding
+        GemvArgs g1;
+        memset(&g1, 0, sizeof g1);
+        g1.W = Wt0_; g1.ldw = s.temb_dim; g1.wdt = DT_BF16; g1.X = temb + (size_t)r0 * s.temb_dim; g1.ldx = s.temb_dim;
+        g1.Y = h1 + (size_t)r0 * H; g1.ldy = H; g1.bias = bt0_; g1.N = H; g1.K = s.temb_dim; g1.nb = nb; g1.silu = 1;
+        TSN_TRY(run(K_GEMV, 2.0 * nb * H * s.temb_dim, 2.0 * H * s.temb_dim, [&] { return launch_gemv(g1, st); }));
+        GemvArgs g2;
+        memset(&g2, 0, sizeof g2);
+        g2.W = Wt2_; g2.ldw = H; g2.wdt = DT_BF16; g2.X = h1 + (size_t)r0 * H; g2.ldx = H;
+        g2.Y = g + (size_t)r0 * H; g2.ldy = H; g2.bias = bt2_; g2.addv = pooled; g2.ld_add = H;
+        g2.Y2 = gs + (size_t)r0 * H; g2.ldy2 = H; g2.N = H; g2.K = H; g2.nb = nb;
+        TSN_TRY(run(K_GEMV, 2.0 * nb * H * H, 2.0 * H * H, [&] { return launch_gemv(g2, st); }));
+        GemvArgs m;
+        memset(&m, 0, sizeof m);
+        m.W = Wmod_; m.ldw = H; m.wdt = DT_BF16;
+        m.X = gs + (size_t)r0 * H; m.ldx = H;
+        m.Y = mod + (size_t)r0 * NMOD; m.ldy = NMOD;
+        m.bias = bmod_; m.N = NMOD; m.K = H; m.nb = nb;
+        TSN_TRY(run(K_GEMV, 2.0 * nb * (double)NMOD * H, 2.0 * (double)NMOD * H + 4.0 * nb * NMOD,
+                    [&] { return launch_gemv(m, st); }));
+    }
+    return TSN_OK;
+}
+
 int DitModel::enqueue_forward(const float *z, const float *t, const float *text, const float *pooled, float *v,
                               float *taps) {
+    return enqueue_eval(z, t, text, pooled, v, taps, nullptr);
+}
+
+// One evaluation. mod_pre: this evaluation's modulation rows, computed beforehand (the sampler);
+// null: computed here from t and pooled.
+int DitModel::enqueue_eval(const float *z, const float *t, const float *text, const float *pooled, float *v,
+                           float *taps, const float *mod_pre) {
     TSN_REQUIRE(ready_, "dit: weights not uploaded");
-    TSN_REQUIRE(z && t && pooled && v && (text || s.Lt == 0), "dit forward: null input");
+    TSN_REQUIRE(z && (t || mod_pre) && (pooled || mod_pre) && v && (text || s.Lt == 0), "dit forward: null input");
     TSN_TRY(rt->dev.make_current());
     const hipStream_t st = rt->dev.stream();
     const int B = s.B, H = s.H;
-    // timestep embedding + MLP, g = t_emb + pooled, gs = silu(g)   (src/dit_fwd.cpp:111-140)
-    TSN_TRY(run("temb_kernel", 0, 0, [&] { return launch_temb_sinusoid(t, temb_, B, s.temb_dim, s.t_max_period, st); }));
-    GemvArgs g1;
-    memset(&g1, 0, sizeof g1);
-    g1.W = Wt0_; g1.ldw = s.temb_dim; g1.wdt = DT_BF16; g1.X = temb_; g1.ldx = s.temb_dim;
-    g1.Y = h1_; g1.ldy = H; g1.bias = bt0_; g1.N = H; g1.K = s.temb_dim; g1.nb = B; g1.silu = 1;
-    TSN_TRY(run(K_GEMV, 2.0 * B * H * s.temb_dim, 2.0 * H * s.temb_dim, [&] { return launch_gemv(g1, st); }));
-    GemvArgs g2;
-    memset(&g2, 0, sizeof g2);
-    g2.W = Wt2_; g2.ldw = H; g2.wdt = DT_BF16; g2.X = h1_; g2.ldx = H;
-    g2.Y = g_; g2.ldy = H; g2.bias = bt2_; g2.addv = pooled; g2.ld_add = H; g2.Y2 = gs_; g2.ldy2 = H;
-    g2.N = H; g2.K = H; g2.nb = B;
-    TSN_TRY(run(K_GEMV, 2.0 * B * H * H, 2.0 * H * H, [&] { return launch_gemv(g2, st); }));
-    // every adaLN modulation of the eval in one HBM-bound GEMV (src/dit_fwd.cpp:186-207,271-274,288-291)
-    TSN_TRY(run(K_GEMV, 2.0 * B * (double)NMOD * H, 2.0 * (double)NMOD * H + 4.0 * B * NMOD,
-                [&] { return modulation(gs_, 0, NMOD); }));
+    if (mod_pre) {
+        mod_ = mod_pre;
+    } else {
+        TSN_TRY(enqueue_conditioning(t, B, pooled, temb_, h1_, g_, gs_, MOD_));
+        mod_ = MOD_;
+    }
     // input projection (src/dit_fwd.cpp:142-149): z split into f16 hi|lo halves, one MFMA GEMM
     // against [W|W] (f32-accurate), bias added, written into the audio rows of X
     TSN_TRY(run(K_SPLIT, 0, 8.0 * B * s.La * s.latent, [&] {
@@ -570,7 +602,7 @@ int DitModel::enqueue_forward(const float *z, const float *t, const float *text,
         LnSeg &g = ln.seg[0];
         g.X = X_; g.ldx = H; g.xmap = RowMap{s.La, S, 0};
         g.Y = XF2_; g.ldy = 2 * H; g.ymap = rowmap_dense(B * s.La);
-        g.mod = MOD_; g.mod_ld = NMOD; g.mod_L = s.La; g.shift_off = fin_mod_off_; g.scale_off = fin_mod_off_ + H;
+        g.mod = mod_; g.mod_ld = NMOD; g.mod_L = s.La; g.shift_off = fin_mod_off_; g.scale_off = fin_mod_off_ + H;
         g.rows = B * s.La;
         TSN_TRY(run(K_LNHL, 0, B * s.La * (double)H * 8.0, [&] { return launch_ln_mod(ln, LN_F16_HILO, st); }));
     }
@@ -594,6 +626,7 @@ int DitModel::enqueue_joint_block(int block, float *X, const float *g) {
     const size_t n = (size_t)s.B * S * s.H;
     TSN_TRY(gs_from_g(g));
     TSN_TRY(modulation(gs_, ja_[block].mod_off, 12 * s.H));
+    mod_ = MOD_;
     TSN_TRY(rt->dev.copy_d2d(X_, X, n * 4));
     TSN_TRY(block_joint(block, true, Next{NEXT_NONE, 0}));
     return rt->dev.copy_d2d(X, X_, n * 4);
@@ -606,6 +639,7 @@ int DitModel::enqueue_fused_block(int block, float *X, const float *g) {
     const size_t n = (size_t)s.B * S * s.H;
     TSN_TRY(gs_from_g(g));
     TSN_TRY(modulation(gs_, fu_[block].mod_off, 6 * s.H));
+    mod_ = MOD_;
     TSN_TRY(rt->dev.copy_d2d(X_, X, n * 4));
     TSN_TRY(block_fused(block, true, Next{NEXT_NONE, 0}));
     return rt->dev.copy_d2d(X, X_, n * 4);
@@ -620,10 +654,15 @@ int DitModel::enqueue_sample(float *x, const float *text, const float *pooled, i
     const int P = s.B / 2;
     const size_t n = (size_t)s.La * s.latent;
     for (int b = 0; b < s.B; ++b) TSN_TRY(rt->dev.copy_d2d(x2_ + b * n, x + (b / 2) * n, n * 4));
+    // the conditioning depends on t only: every step's modulation in one pass over the weights
+    // per 16 rows, before the step loop (row st*B + b = step st, sample b)
+    TSN_TRY(launch_copy_rows(pooled, s.H, RowMap{s.B, 0, 0}, pooled_rep_, s.H, rowmap_dense(16), 16, s.H,
+                             rt->dev.stream()));
+    TSN_TRY(enqueue_conditioning(tsched_, steps * s.B, pooled_rep_, temb_all_, h1_all_, g_all_, gs_all_, mod_all_));
     for (int st = 0; st < steps; ++st) {
         const float t_curr = 1.0f - (float)st / (float)steps;
         const float t_prev = 1.0f - (float)(st + 1) / (float)steps;
-        TSN_TRY(enqueue_forward(x2_, tsched_ + (size_t)st * s.B, text, pooled, Vv_, nullptr));
+        TSN_TRY(enqueue_eval(x2_, nullptr, text, nullptr, Vv_, nullptr, mod_all_ + (size_t)st * s.B * NMOD));
         TSN_TRY(launch_cfg_euler_pairs(Vv_, x2_, P, (int)n, cfg, t_prev - t_curr, rt->dev.stream()));
     }
     for (int p = 0; p < P; ++p) TSN_TRY(rt->dev.copy_d2d(x + p * n, x2_ + 2 * p * n, n * 4));
@@ -725,8 +764,27 @@ int DitModel::profile_forward(const float *z, const float *t, const float *text,
 
 int DitModel::prepare_sample(int steps) {
     TSN_REQUIRE(steps > 0, "dit sample: steps must be positive");
+    TSN_REQUIRE(s.B <= 16 && 16 % s.B == 0, "dit sample: B must divide 16");
     TSN_TRY(rt->dev.make_current());
-    return prepare_schedule(rt, s.B, steps, &tsched_, &tsched_steps_, owned_);
+    const bool same = tsched_ && tsched_steps_ == steps && cond_;
+    TSN_TRY(prepare_schedule(rt, s.B, steps, &tsched_, &tsched_steps_, owned_));
+    if (same) return TSN_OK;
+    if (cond_) {
+        TSN_TRY(rt->dev.free(cond_));
+        for (auto it = owned_.begin(); it != owned_.end(); ++it)
+            if (*it == cond_) { owned_.erase(it); break; }
+        cond_ = nullptr;
+    }
+    const size_t R = ((size_t)steps * s.B + 15) / 16 * 16, H = s.H;
+    const size_t n_temb = R * s.temb_dim, n_h = R * H, n_mod = R * (size_t)NMOD, n_rep = 16 * H;
+    TSN_TRY(alloc((n_temb + 3 * n_h + n_h + n_mod + n_rep) * sizeof(float), (void **)&cond_));   // zero-filled
+    temb_all_ = cond_;
+    h1_all_ = temb_all_ + n_temb;
+    g_all_ = h1_all_ + n_h;
+    gs_all_ = g_all_ + n_h;
+    mod_all_ = gs_all_ + n_h + n_h;
+    pooled_rep_ = mod_all_ + n_mod;
+    return TSN_OK;
 }
 
 } // namespace tsn

@@ -96,6 +96,13 @@ private:
     struct Next {
         int kind, idx;
     };
+    // timestep embedding -> t-MLP (+ pooled) -> silu -> every adaLN modulation, for `rows` rows
+    // (t [rows], pooled rows [rows][H] at ld H or repeated with period per, outputs [rows][.]),
+    // in GEMV batches of up to 16 rows
+    int enqueue_conditioning(const float *t, int rows, const float *pooled, float *temb, float *h1, float *g,
+                             float *gs, float *mod);
+    int enqueue_eval(const float *z, const float *t, const float *text, const float *pooled, float *v, float *taps,
+                     const float *mod_pre);
     int block_joint(int i, bool ln1, Next next);
     int block_fused(int i, bool ln1, Next next);
     int resid_ln(GemmBatch &b, RedLnArgs &r);
@@ -123,6 +130,11 @@ private:
     half_t *XF2_ = nullptr, *Z2_ = nullptr;               // hi|lo operands of the projections
     float *Vv_ = nullptr, *x2_ = nullptr, *tsched_ = nullptr;
     int tsched_steps_ = 0;
+    // sampler: conditioning of every step computed before the step loop (rows = steps*B, padded
+    // to 16): temb, h1, g, gs, modulation, and pooled repeated over 16 rows
+    float *cond_ = nullptr, *temb_all_ = nullptr, *h1_all_ = nullptr, *g_all_ = nullptr, *gs_all_ = nullptr;
+    float *mod_all_ = nullptr, *pooled_rep_ = nullptr;
+    const float *mod_ = nullptr;      // modulation rows the blocks of the current evaluation read
     half_t *XN_ = nullptr, *Q_ = nullptr, *K_ = nullptr, *Vt_ = nullptr, *AO_ = nullptr, *HF_ = nullptr;
     void *wraw_ = nullptr, *wf16_ = nullptr;
     float *ws_ = nullptr;            // split-K partials of the residual GEMMs

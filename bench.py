@@ -255,6 +255,10 @@ def main():
         achieved = (dom["bytes"] / dom["launches"]) / (avg_launch_ms * 1e-3) / 1e9
         peak, unit = PEAK_HBM_GBS, "GB/s"
     eval_flops = sum(k["flops"] for k in stats)
+    # the denominators this GPU actually reaches (f16 MFMA chains, 1 GiB device copy)
+    meas_tflops, meas_gbs = rt.probe_peaks()
+    log("bench: measured peaks %.0f TFLOP/s dense f16 MFMA, %.0f GB/s device copy" % (meas_tflops, meas_gbs))
+    meas_peak = meas_tflops if bound == "mfma" else meas_gbs
     traffic = read_traffic(dom["name"])
     if traffic is not None:
         log("bench: %s HBM traffic %.0f B/dispatch (counters), algorithmic %.0f B/dispatch"
@@ -321,8 +325,10 @@ def main():
         "sampler_config": "24 Euler steps, CFG 5.0, 1 prompt x 2 arms, same model and sizes",
         "eval_gflop": round(eval_flops / 1e9, 2),
         "mfma_frac_eval": round(eval_flops / (ms_per_eval * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4),
+        "measured_peaks": {"mfma_f16_tflops": round(meas_tflops, 1), "copy_gbs": round(meas_gbs, 1)},
         "roofline": {"kernel": dom["name"], "bound": bound, "achieved": round(achieved, 2), "peak": peak,
                      "unit": unit, "frac": round(achieved / peak, 4), "traffic": traffic,
+                     "peak_measured": round(meas_peak, 1), "frac_of_measured": round(achieved / meas_peak, 4),
                      "launches_per_eval": dom["launches"], "avg_launch_us": round(avg_launch_ms * 1e3, 3)},
         "kernels": [{"name": k["name"], "launches": k["launches"], "ms": round(k["ms"], 4),
                      "share": round(k["ms"] / tot_ms, 4)} for k in stats],

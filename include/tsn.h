@@ -95,6 +95,12 @@ int tsn_rope_pairs(tsn_runtime *rt, float *x, const int32_t *pos, uint32_t rows,
 int tsn_attention(tsn_runtime *rt, const float *qkv, float *out, uint32_t S, uint32_t nh, uint32_t hd, uint32_t ld,
                   uint32_t ldo, uint32_t q_off, uint32_t k_off, uint32_t v_off, uint32_t o_off, float scale);
 
+/* Calibration (no reference counterpart: it measures the denominators a roofline is quoted
+ * against). Sustained dense f16 MFMA rate (about 20 ms of one workgroup of 8 waves per CU running
+ * independent v_mfma_f32_16x16x32_f16 chains), and device copy bandwidth (read + write of 1 GiB), both timed with
+ * HIP events on the runtime's stream. Allocates and frees 2 GiB of device memory. */
+int tsn_probe_peaks(tsn_runtime *rt, double *mfma_tflops, double *hbm_gbs);
+
 /* ---------------- model: tn::DitModel (src/models.h:55-85) ---------------- */
 typedef struct {
     int B;              /* batch: CFG arms folded in (sample 2p cond, 2p+1 uncond); 1, 2, 4, 8 or 16 */

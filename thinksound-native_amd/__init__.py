@@ -99,6 +99,7 @@ _SIGS = {
     "tsn_dit_capture_forward": [_P, _P, _P, _P, _P, _P],
     "tsn_dit_capture_sample": [_P, _P, _P, _P, _I, _FL],
     "tsn_dit_replay": [_P],
+    "tsn_probe_peaks": [_P, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double)],
     "tsn_dit_profile_forward": [_P, _P, _P, _P, _P, _P, ctypes.POINTER(KernelStat), _I, ctypes.POINTER(_I)],
     "tsn_synth_normal_f32": [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, _SZ, _P],
     "tsn_synth_normal_bf16": [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, _SZ, _P],
@@ -311,6 +312,12 @@ class Runtime:
 
     def cfg_euler(self, fc, fu, x, n, cfg, dt):
         call("tsn_cfg_euler", self.h, fc.p, fu.p, x.p, n, cfg, dt)
+
+    def probe_peaks(self):
+        """(achievable dense f16 MFMA TFLOP/s, device copy GB/s) measured on this GPU"""
+        t, g = ctypes.c_double(), ctypes.c_double()
+        call("tsn_probe_peaks", self.h, ctypes.byref(t), ctypes.byref(g))
+        return t.value, g.value
 
 
 class DitModel:

@@ -116,6 +116,11 @@ int tsn_attention(tsn_runtime *rt, const float *qkv, float *out, uint32_t S, uin
     return rt->rt.attention(qkv, out, S, nh, hd, ld, ldo, q_off, k_off, v_off, o_off, scale);
 }
 
+int tsn_probe_peaks(tsn_runtime *rt, double *mfma_tflops, double *hbm_gbs) {
+    RT_CHECK(rt);
+    return rt->rt.probe_peaks(mfma_tflops, hbm_gbs);
+}
+
 int tsn_dit_default_spec(int workload, tsn_dit_spec *out) {
     if (!out || workload < 0 || workload > 4) { tsn::set_error("default_spec: workload must be 0..4"); return TSN_ERR_ARG; }
     tsn_dit_spec s;

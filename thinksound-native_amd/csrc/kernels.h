@@ -121,6 +121,13 @@ struct RedLnArgs {
 };
 int launch_reduce_ln(const RedLnArgs &a, hipStream_t st);
 
+/* ------------------------------------------------------------------ calibration probes */
+// nwg workgroups x 8 waves, each wave 16 x iters MFMAs 16x16x32 f16 (16384 flops each); out holds
+// nwg*512 floats
+int launch_mfma_peak(float *out, int nwg, int iters, hipStream_t st);
+// dst[i] = src[i] for n4 float4 elements
+int launch_copy_peak(const float *src, float *dst, size_t n4, hipStream_t st);
+
 /* ------------------------------------------------------------------ GEMV (small M) */
 // Y[b][n] = act(sum_k W[n][k] * X[b][k] + bias[n] + addv[b][n]); optional Y2 = silu(Y).
 // W is bf16, f16 or f32 (wdt); X, Y f32; nb <= 16 rows of X. HBM-bound: one wave per 4 rows of W.

@@ -140,6 +140,30 @@ __global__ __launch_bounds__(512) void reduce_ln_kernel(const RedLnArgs a) {
                                   (half_t)(y2 - (float)hi[2]), (half_t)(y3 - (float)hi[3])};
 }
 
+/* ---------------- calibration probes (achievable MFMA and HBM rates) ---------------- */
+// 16 independent v_mfma_f32_16x16x32_f16 chains per wave, iters rounds; the result is written so
+// the chains stay live
+__global__ __launch_bounds__(512) void mfma_peak_kernel(float *out, int iters) {
+    floatx4 acc[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    half8 x, y;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) { x[e] = (half_t)((threadIdx.x & 7) * 1e-3f); y[e] = (half_t)(e * 1e-3f); }
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(x, y, acc[i], 0, 0, 0);
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) sum += (acc[i][0] + acc[i][1]) + (acc[i][2] + acc[i][3]);
+    out[blockIdx.x * blockDim.x + threadIdx.x] = sum;
+}
+__global__ __launch_bounds__(256) void copy_peak_kernel(const float4 *src, float4 *dst, size_t n) {
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
 /* ---------------- GEMV (shaders/gemm_attn.metal:47-74, batched over nb rows of X) ---------------- */
 template <typename WT>
 __device__ inline void load_w8(const WT *p, float (&w)[8]);
@@ -453,6 +477,19 @@ int launch_reduce_ln(const RedLnArgs &a, hipStream_t st) {
     dim3 grid(total), block(a.H / 4);
     if (a.ymode == LN_F16_HILO) TSN_LAUNCH((reduce_ln_kernel<LN_F16_HILO>), grid, block, 0, st, a);
     else TSN_LAUNCH((reduce_ln_kernel<LN_F16>), grid, block, 0, st, a);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+
+int launch_mfma_peak(float *out, int nwg, int iters, hipStream_t st) {
+    TSN_REQUIRE(out && nwg > 0 && iters > 0, "mfma probe: arguments");
+    TSN_LAUNCH(mfma_peak_kernel, dim3(nwg), dim3(512), 0, st, out, iters);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_copy_peak(const float *src, float *dst, size_t n4, hipStream_t st) {
+    TSN_REQUIRE(src && dst && n4 > 0, "copy probe: arguments");
+    TSN_LAUNCH(copy_peak_kernel, dim3(8192), dim3(256), 0, st, (const float4 *)src, (float4 *)dst, n4);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }

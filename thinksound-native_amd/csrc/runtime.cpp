@@ -294,4 +294,47 @@ int Runtime::attention(const float *qkv, float *out, uint32_t S, uint32_t nh, ui
     return launch_attention(a, dev.stream());
 }
 
+int Runtime::probe_peaks(double *mfma_tflops, double *hbm_gbs) {
+    TSN_REQUIRE(mfma_tflops && hbm_gbs, "probe: null output");
+    TSN_TRY(dev.make_current());
+    const hipStream_t st = dev.stream();
+    int ncu = 0;
+    TSN_HIP_CHECK(hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev.device()));
+    TSN_REQUIRE(ncu > 0, "probe: no compute units");
+    const size_t copy_bytes = (size_t)1 << 30;
+    float *buf = nullptr, *src = nullptr, *dst = nullptr;
+    TSN_TRY(dev.alloc((size_t)ncu * 512 * sizeof(float), (void **)&buf));
+    int rc = dev.alloc(copy_bytes, (void **)&src);
+    if (rc == TSN_OK) rc = dev.alloc(copy_bytes, (void **)&dst);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    if (rc == TSN_OK && (hipEventCreate(&e0) != hipSuccess || hipEventCreate(&e1) != hipSuccess)) {
+        set_error("probe: event creation failed");
+        rc = TSN_ERR_HIP;
+    }
+    const int iters = 40000;   // about 20 ms: the sustained rate, after clocks settle under MFMA load
+    float ms_mfma = 0.0f, ms_copy = 0.0f;
+    if (rc == TSN_OK) rc = launch_mfma_peak(buf, ncu, 100, st);   // warm-up
+    if (rc == TSN_OK && hipEventRecord(e0, st) != hipSuccess) rc = TSN_ERR_HIP;
+    if (rc == TSN_OK) rc = launch_mfma_peak(buf, ncu, iters, st);
+    if (rc == TSN_OK && hipEventRecord(e1, st) != hipSuccess) rc = TSN_ERR_HIP;
+    if (rc == TSN_OK && (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms_mfma, e0, e1) != hipSuccess))
+        rc = TSN_ERR_HIP;
+    if (rc == TSN_OK) rc = launch_copy_peak(src, dst, copy_bytes / 16, st);   // warm-up
+    if (rc == TSN_OK && hipEventRecord(e0, st) != hipSuccess) rc = TSN_ERR_HIP;
+    for (int r = 0; r < 5 && rc == TSN_OK; ++r) rc = launch_copy_peak(src, dst, copy_bytes / 16, st);
+    if (rc == TSN_OK && hipEventRecord(e1, st) != hipSuccess) rc = TSN_ERR_HIP;
+    if (rc == TSN_OK && (hipEventSynchronize(e1) != hipSuccess || hipEventElapsedTime(&ms_copy, e0, e1) != hipSuccess))
+        rc = TSN_ERR_HIP;
+    if (rc == TSN_ERR_HIP && last_error()[0] == 0) set_error("probe: HIP event failure");
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    if (dst) dev.free(dst);
+    if (src) dev.free(src);
+    dev.free(buf);
+    if (rc != TSN_OK) return rc;
+    *mfma_tflops = (double)ncu * 8 * iters * 16 * 16384.0 / (ms_mfma * 1e-3) / 1e12;
+    *hbm_gbs = 5.0 * 2.0 * copy_bytes / (ms_copy * 1e-3) / 1e9;
+    return TSN_OK;
+}
+
 } // namespace tsn

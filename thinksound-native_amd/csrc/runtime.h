@@ -87,6 +87,10 @@ public:
     int attention(const float *qkv, float *out, uint32_t S, uint32_t nh, uint32_t hd, uint32_t ld,
                   uint32_t ldo, uint32_t q_off, uint32_t k_off, uint32_t v_off, uint32_t o_off, float scale);
 
+    // calibration: achievable dense f16 MFMA TFLOP/s (one workgroup of 8 waves per CU) and
+    // device-to-device copy GB/s (read + write of a 1 GiB buffer), timed with events on the stream
+    int probe_peaks(double *mfma_tflops, double *hbm_gbs);
+
 private:
     // grow-on-demand scratch (the role of the reference's im2col buffer, src/net.h:34)
     int scratch(size_t bytes, void **p);

@@ -159,9 +159,10 @@ __global__ __launch_bounds__(512) void mfma_peak_kernel(float *out, int iters) {
     for (int i = 0; i < 16; ++i) sum += (acc[i][0] + acc[i][1]) + (acc[i][2] + acc[i][3]);
     out[blockIdx.x * blockDim.x + threadIdx.x] = sum;
 }
+// one float4 per thread over n/256 workgroups: the fastest plain copy shape measured here
 __global__ __launch_bounds__(256) void copy_peak_kernel(const float4 *src, float4 *dst, size_t n) {
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        dst[i] = src[i];
+    const size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    if (i < n) dst[i] = src[i];
 }
 
 /* ---------------- GEMV (shaders/gemm_attn.metal:47-74, batched over nb rows of X) ---------------- */
@@ -489,7 +490,8 @@ int launch_mfma_peak(float *out, int nwg, int iters, hipStream_t st) {
 }
 int launch_copy_peak(const float *src, float *dst, size_t n4, hipStream_t st) {
     TSN_REQUIRE(src && dst && n4 > 0, "copy probe: arguments");
-    TSN_LAUNCH(copy_peak_kernel, dim3(8192), dim3(256), 0, st, (const float4 *)src, (float4 *)dst, n4);
+    TSN_REQUIRE((n4 + 255) / 256 <= 0x7FFFFFFFull, "copy probe: too many elements");
+    TSN_LAUNCH(copy_peak_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, (const float4 *)src, (float4 *)dst, n4);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }

@@ -114,6 +114,35 @@ void orc_dit_forward(const orc_spec *s, const float *weights, const float *z, co
 void orc_dit_sample(const orc_spec *s, const float *weights, float *x, const float *text,
                     const float *pooled, int steps, float cfg);
 
+/* ---------------- the reference's own three-stream graph (oracle_ref.cpp) ---------------- */
+
+// B samples (CFG arms), T latent rows, C clip rows, TS text rows; F = SwiGLU width (H_ffn);
+// the timestep sinusoid is H wide; the last joint block is pre-only.
+typedef struct {
+    int B, T, C, TS;
+    int H, NH, HD, F;
+    int latent;
+    int n_joint, n_fused;
+    float rope_theta, t_max_period, ln_eps, rms_eps;
+} orc_ref_spec;
+
+int orc_ref_manifest_count(const orc_ref_spec *s);
+int64_t orc_ref_manifest_numel(const orc_ref_spec *s, int idx);
+void orc_ref_manifest_name(const orc_ref_spec *s, int idx, char *buf, int cap);
+
+// One velocity evaluation of the reference graph per sample (src/dit_fwd.cpp:104-304):
+//   x [B, T, latent], t [B], clip_pp [B, C, H], text_pp [B, TS, H], gcmlp [B, H],
+//   sync_gather [B, T, H]  ->  v [B, T, latent];
+//   taps (optional): the joint state [B, T+C+TS, H] (latent, clip, text rows) after each block.
+void orc_ref_dit_forward(const orc_ref_spec *s, const float *weights, const float *x, const float *t,
+                         const float *clip_pp, const float *text_pp, const float *gcmlp,
+                         const float *sync_gather, float *v, float *taps);
+
+// CFG Euler sampler over the reference graph: sample 2p cond, 2p+1 uncond; x [B/2, T, latent].
+void orc_ref_dit_sample(const orc_ref_spec *s, const float *weights, float *x, const float *clip_pp,
+                        const float *text_pp, const float *gcmlp, const float *sync_gather, int steps,
+                        float cfg);
+
 // number of OpenMP threads the oracle uses (for the CPU-baseline report)
 int orc_num_threads(void);
 

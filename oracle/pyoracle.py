@@ -24,6 +24,13 @@ class OrcSpec(ctypes.Structure):
                 ("rope_theta", _F), ("t_max_period", _F), ("ln_eps", _F), ("rms_eps", _F)]
 
 
+class RefSpec(ctypes.Structure):
+    """orc_ref_spec: the reference's three-stream graph"""
+    _fields_ = [("B", _I), ("T", _I), ("C", _I), ("TS", _I), ("H", _I), ("NH", _I), ("HD", _I), ("F", _I),
+                ("latent", _I), ("n_joint", _I), ("n_fused", _I),
+                ("rope_theta", _F), ("t_max_period", _F), ("ln_eps", _F), ("rms_eps", _F)]
+
+
 _SIGS = {
     "orc_gemm": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
     "orc_gemv": [_P, _P, _P, _P, _I, _I, _I],
@@ -49,9 +56,14 @@ _SIGS = {
     "orc_dit_forward": [ctypes.POINTER(OrcSpec), _P, _P, _P, _P, _P, _P, _P, _P],
     "orc_dit_sample": [ctypes.POINTER(OrcSpec), _P, _P, _P, _P, _I, _F],
     "orc_num_threads": [],
+    "orc_ref_manifest_count": [ctypes.POINTER(RefSpec)],
+    "orc_ref_manifest_numel": [ctypes.POINTER(RefSpec), _I],
+    "orc_ref_manifest_name": [ctypes.POINTER(RefSpec), _I, ctypes.c_char_p, _I],
+    "orc_ref_dit_forward": [ctypes.POINTER(RefSpec), _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "orc_ref_dit_sample": [ctypes.POINTER(RefSpec), _P, _P, _P, _P, _P, _P, _I, _F],
 }
 _RES = {"orc_manifest_count": _I, "orc_manifest_numel": ctypes.c_int64, "orc_manifest_total": ctypes.c_int64,
-        "orc_num_threads": _I}
+        "orc_num_threads": _I, "orc_ref_manifest_count": _I, "orc_ref_manifest_numel": ctypes.c_int64}
 
 _lib = None
 
@@ -247,3 +259,42 @@ def dit_sample(spec, W, x, text, pooled, steps, cfg):
 
 def num_threads():
     return lib().orc_num_threads()
+
+
+# ---------------- the reference's three-stream graph ----------------
+def ref_spec_from(spec):
+    if isinstance(spec, RefSpec):
+        return spec
+    d = spec if isinstance(spec, dict) else {k: getattr(spec, k) for k, _ in RefSpec._fields_}
+    return RefSpec(**{k: d[k] for k, _ in RefSpec._fields_})
+
+
+def ref_manifest(spec):
+    s = ref_spec_from(spec)
+    L = lib()
+    out, buf = [], ctypes.create_string_buffer(256)
+    off = 0
+    for i in range(L.orc_ref_manifest_count(ctypes.byref(s))):
+        L.orc_ref_manifest_name(ctypes.byref(s), i, buf, 256)
+        n = L.orc_ref_manifest_numel(ctypes.byref(s), i)
+        out.append((buf.value.decode(), n, off))
+        off += n
+    return out
+
+
+def ref_dit_forward(spec, W, x, t, clip_pp, text_pp, gcmlp, sync_gather, taps=False):
+    s = ref_spec_from(spec)
+    S = s.T + s.C + s.TS
+    v = np.empty((s.B, s.T, s.latent), np.float32)
+    tp = np.empty((s.n_joint + s.n_fused, s.B, S, s.H), np.float32) if taps else None
+    lib().orc_ref_dit_forward(ctypes.byref(s), p(W), p(f32(x)), p(f32(t)), p(f32(clip_pp)), p(f32(text_pp)),
+                              p(f32(gcmlp)), p(f32(sync_gather)), p(v), p(tp))
+    return (v, tp) if taps else v
+
+
+def ref_dit_sample(spec, W, x, clip_pp, text_pp, gcmlp, sync_gather, steps, cfg):
+    s = ref_spec_from(spec)
+    x = f32(x).copy()
+    lib().orc_ref_dit_sample(ctypes.byref(s), p(W), p(x), p(f32(clip_pp)), p(f32(text_pp)), p(f32(gcmlp)),
+                             p(f32(sync_gather)), steps, cfg)
+    return x

@@ -170,7 +170,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const GemmBatch bt) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tile = xcd_remap(blockIdx.x, gridDim.x);
-    const int pi = (bt.nprob > 1 && tile >= bt.p[1].tile_start) ? 1 : 0;
+    const int pi = (bt.nprob > 2 && tile >= bt.p[2].tile_start) ? 2 : (bt.nprob > 1 && tile >= bt.p[1].tile_start) ? 1 : 0;
     const GemmProblem &P = bt.p[pi];
 
     const int local = tile - P.tile_start;
@@ -380,6 +380,21 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
                 *(float4 *)(y + 4) = make_float4(v[4], v[5], v[6], v[7]);
             }
         }
+    } else if constexpr (EPI == EPI_SWIGLU) {
+        // tile columns 0..63: w1 rows 64j.., columns 64..127: the matching w3 rows (j = n0 / 128)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const int c = tid + 512 * p, row = c >> 3, col = (c & 7) * 8;
+            const int m = m0 + row;
+            if (m >= M) continue;
+            float a[8], b[8];
+            ldsum8(tile, row * TP + col, a);
+            ldsum8(tile, row * TP + 64 + col, b);
+            half8 o;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = (half_t)(silu_f(a[e]) * b[e]);
+            *(half8 *)((half_t *)P.Y + rowmap_phys(P.ymap, m) * (long long)P.ldy + n0 / 2 + col) = o;
+        }
     } else if constexpr (EPI == EPI_RESID) {
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
@@ -498,7 +513,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int tid_g = xcd_remap(blockIdx.x, gridDim.x);
-    const int pi = (bt.nprob > 1 && tid_g >= bt.p[1].tile_start) ? 1 : 0;
+    const int pi = (bt.nprob > 2 && tid_g >= bt.p[2].tile_start) ? 2 : (bt.nprob > 1 && tid_g >= bt.p[1].tile_start) ? 1 : 0;
     const GemmProblem &P = bt.p[pi];
     const int M = P.M, N = P.N, K = P.K, lda = P.lda, ldw = P.ldw, Kc = P.Kc, pad = P.pad, aT = P.a_T;
     const RowMap am = P.amap;
@@ -649,14 +664,15 @@ __global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
 template <int EPI>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmBatch bt) {
     long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    int pi = 0;
-    long long n0 = (long long)bt.p[0].M * bt.p[0].N / 4;
-    if (bt.p[0].splits <= 1) n0 = 0;
-    if (idx >= n0) {
-        pi = 1;
-        idx -= n0;
-        if (bt.nprob < 2 || bt.p[1].splits <= 1 || idx >= (long long)bt.p[1].M * bt.p[1].N / 4) return;
+    // problems with a split come one after the other, M*N/4 threads each
+    int pi = -1;
+    for (int q = 0; q < bt.nprob; ++q) {
+        if (bt.p[q].splits <= 1) continue;
+        const long long nq = (long long)bt.p[q].M * bt.p[q].N / 4;
+        if (idx < nq) { pi = q; break; }
+        idx -= nq;
     }
+    if (pi < 0) return;
     const GemmProblem &P = bt.p[pi];
     const int n4 = P.N / 4;
     const int m = (int)(idx / n4), n = (int)(idx - (long long)m * n4) * 4;
@@ -719,7 +735,7 @@ void gemm_problem_init(GemmProblem &p) {
 }
 
 int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
-    TSN_REQUIRE(b.nprob >= 1 && b.nprob <= 2, "gemm: 1 or 2 problems");
+    TSN_REQUIRE(b.nprob >= 1 && b.nprob <= 3, "gemm: 1 to 3 problems");
     int tiles = 0;
     for (int i = 0; i < b.nprob; ++i) {
         GemmProblem &p = b.p[i];
@@ -730,6 +746,10 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         TSN_REQUIRE(p.amap.L > 0 && p.a_T > 0, "gemm: row map");
         TSN_REQUIRE((((uintptr_t)p.A) & 15) == 0 && (((uintptr_t)p.W) & 15) == 0, "gemm: A and W must be 16-byte aligned");
         if (epi == EPI_STORE) TSN_REQUIRE(p.Y && p.ymap.L > 0, "gemm: output");
+        if (epi == EPI_SWIGLU)
+            TSN_REQUIRE(p.Y && p.ymap.L > 0 && p.y_f16 && p.N % BN == 0 && p.ldy % 8 == 0 &&
+                            (((uintptr_t)p.Y) & 15) == 0,
+                        "gemm swiglu: f16 output, N (= 2F) a multiple of 128, 16-byte aligned rows");
         if (epi == EPI_RESID) TSN_REQUIRE(p.R && p.gate && p.rmap.L > 0 && p.gate_L > 0, "gemm: residual output");
         if (epi == EPI_QKV) {
             TSN_REQUIRE(p.Q && p.Kd && p.Vt && p.qn && p.kn, "gemm qkv: outputs and norm weights");
@@ -810,13 +830,15 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
             }
         }
     }
+    TSN_REQUIRE(pipe || epi != EPI_SWIGLU, "gemm swiglu: needs K and row strides the pipelined kernel takes");
     b.pipe = pipe ? 1 : 0;
-    b.kname = pipe ? (epi == EPI_STORE ? "gemm_pipe_kernel<0>" : epi == EPI_RESID ? "gemm_pipe_kernel<1>" : "gemm_pipe_kernel<2>")
+    b.kname = pipe ? (epi == EPI_STORE ? "gemm_pipe_kernel<0>" : epi == EPI_RESID ? "gemm_pipe_kernel<1>"
+                      : epi == EPI_QKV ? "gemm_pipe_kernel<2>" : "gemm_pipe_kernel<3>")
                    : a_f32 ? "gemm_f16_kernel<true, 0>"
                    : (epi == EPI_STORE ? "gemm_f16_kernel<false, 0>" : epi == EPI_RESID ? "gemm_f16_kernel<false, 1>"
                                                                         : "gemm_f16_kernel<false, 2>");
     if (a_f32) TSN_REQUIRE(epi == EPI_STORE, "gemm: f32 A operand only with a plain store epilogue");
-    TSN_REQUIRE(epi == EPI_STORE || epi == EPI_RESID || epi == EPI_QKV, "gemm: unknown epilogue");
+    TSN_REQUIRE(epi == EPI_STORE || epi == EPI_RESID || epi == EPI_QKV || epi == EPI_SWIGLU, "gemm: unknown epilogue");
     return TSN_OK;
 }
 
@@ -826,6 +848,7 @@ int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st)
         if (epi == EPI_STORE) TSN_LAUNCH((gemm_pipe_kernel<EPI_STORE>), grid, block, 0, st, b);
         else if (epi == EPI_RESID) TSN_LAUNCH((gemm_pipe_kernel<EPI_RESID>), grid, block, 0, st, b);
         else if (epi == EPI_QKV) TSN_LAUNCH((gemm_pipe_kernel<EPI_QKV>), grid, block, 0, st, b);
+        else if (epi == EPI_SWIGLU) TSN_LAUNCH((gemm_pipe_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
         else { set_error("gemm: unknown epilogue"); return TSN_ERR_ARG; }
     } else if (a_f32) {
         TSN_LAUNCH((gemm_f16_kernel<true, EPI_STORE>), grid, block, 0, st, b);

@@ -8,8 +8,8 @@ namespace tsn {
 
 /* ------------------------------------------------------------------ GEMM (MFMA) */
 // C[M,N] = A[M,K] · W[N,K]ᵀ with f16 operands and f32 accumulation; 128x128x64 tiles,
-// 4 waves (2x2, 64x64 per wave), v_mfma_f32_16x16x32_f16, LDS double-buffered.
-enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2 };
+// v_mfma_f32_16x16x32_f16 (pipelined kernel: 8 waves, 5 direct-to-LDS stages).
+enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
 
 struct GemmProblem {
     // A operand rows (f16, or f32 converted on load): row m -> rowmap_phys(amap, m).
@@ -21,6 +21,8 @@ struct GemmProblem {
     const float *bias;                 // [N] or null
     int M, N, K;
     // EPI_STORE: Y[ymap(m)*ldy + n] = act(acc + bias), f16 or f32
+    // EPI_SWIGLU: W rows interleaved in 64-row blocks (w1 block j, then w3 block j), N = 2F;
+    // Y[ymap(m)*ldy + 64j + c] = silu(w1 row 64j+c · a) * (w3 row 64j+c · a), f16, no bias
     void *Y; int ldy; RowMap ymap; int y_f16; int silu;
     // EPI_RESID: R[rmap(m)*ldr + n] += gate[(m / gate_L)*gate_ld + n] * (acc + bias)
     float *R; int ldr; RowMap rmap; const float *gate; int gate_ld; int gate_L;
@@ -40,7 +42,7 @@ struct GemmProblem {
 };
 
 struct GemmBatch {
-    GemmProblem p[2];
+    GemmProblem p[3];
     int nprob = 0;
     int total_tiles = 0;
     // optional f32 workspace for split-K partials (EPI_RESID / EPI_STORE); null disables split-K
@@ -91,7 +93,7 @@ struct LnSeg {
     int rows;
 };
 struct LnArgs {
-    LnSeg seg[2];
+    LnSeg seg[3];
     int nseg, H;
     float eps;
 };
@@ -115,7 +117,7 @@ struct RedLnSeg {
     void *Y; int ldy; RowMap ymap;
 };
 struct RedLnArgs {
-    RedLnSeg seg[2];
+    RedLnSeg seg[3];
     int nseg, H, ymode;
     float eps;
 };

@@ -27,10 +27,9 @@ template <int YMODE, int NV>
 __global__ __launch_bounds__(256) void ln_mod_kernel(const LnArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     int v = blockIdx.x * 4 + wave;
-    const int total = a.seg[0].rows + (a.nseg > 1 ? a.seg[1].rows : 0);
-    if (v >= total) return;
     int si = 0;
-    if (v >= a.seg[0].rows) { si = 1; v -= a.seg[0].rows; }
+    while (si < a.nseg && v >= a.seg[si].rows) v -= a.seg[si++].rows;
+    if (si >= a.nseg) return;
     const LnSeg &S = a.seg[si];
     const float *x = S.X + rowmap_phys(S.xmap, v) * (long long)S.ldx;
     float4 xv[NV];
@@ -94,7 +93,8 @@ template <int YMODE>
 __global__ __launch_bounds__(512) void reduce_ln_kernel(const RedLnArgs a) {
     __shared__ float red[2][8];
     int v = blockIdx.x, si = 0;
-    if (v >= a.seg[0].M) { si = 1; v -= a.seg[0].M; }
+    while (si < a.nseg && v >= a.seg[si].M) v -= a.seg[si++].M;
+    if (si >= a.nseg) return;   // uniform over the workgroup
     const RedLnSeg &S = a.seg[si];
     const int H = a.H, col = threadIdx.x * 4;
     float *x = S.X + rowmap_phys(S.xmap, v) * (long long)S.ldx + col;
@@ -431,7 +431,7 @@ inline unsigned blocks_for(size_t n, unsigned t = 256) { return (unsigned)((n + 
 
 int launch_ln_mod(const LnArgs &a, int ymode, hipStream_t st) {
     TSN_REQUIRE(ymode == LN_F32 || ymode == LN_F16 || ymode == LN_F16_HILO, "ln: output mode");
-    TSN_REQUIRE(a.nseg >= 1 && a.nseg <= 2, "ln: 1 or 2 segments");
+    TSN_REQUIRE(a.nseg >= 1 && a.nseg <= 3, "ln: 1 to 3 segments");
     TSN_REQUIRE(a.H % 256 == 0 && a.H >= 256 && a.H <= 2048, "ln: H must be a multiple of 256 in [256, 2048]");
     int total = 0;
     for (int i = 0; i < a.nseg; ++i) {
@@ -462,7 +462,7 @@ int launch_ln_mod(const LnArgs &a, int ymode, hipStream_t st) {
 }
 
 int launch_reduce_ln(const RedLnArgs &a, hipStream_t st) {
-    TSN_REQUIRE(a.nseg >= 1 && a.nseg <= 2, "reduce_ln: 1 or 2 segments");
+    TSN_REQUIRE(a.nseg >= 1 && a.nseg <= 3, "reduce_ln: 1 to 3 segments");
     TSN_REQUIRE(a.H % 256 == 0 && a.H >= 256 && a.H <= 2048, "reduce_ln: H must be a multiple of 256 in [256, 2048]");
     TSN_REQUIRE(a.ymode == LN_F16 || a.ymode == LN_F16_HILO, "reduce_ln: output mode");
     int total = 0;

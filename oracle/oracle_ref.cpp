@@ -30,7 +30,8 @@ namespace {
 struct Tensor { std::string name; int64_t numel; };
 
 // Weight manifest of the reference graph, in flat-buffer order. Conv weights are [OC][IC][K],
-// linear weights [N][K]; adaLN weights [chunks*H][H].
+// linear weights [N][K]; adaLN weights [chunks*H][H]; qkv weight [3H][H] and bias [3H] with rows
+// element-interleaved (row 3c + j: channel c of q, k, v).
 std::vector<Tensor> ref_manifest(const orc_ref_spec &s) {
     std::vector<Tensor> v;
     const int64_t H = s.H, F = s.F, HD = s.HD, L = s.latent;
@@ -109,15 +110,22 @@ void swiglu_ffn(const RefWeights &W, const std::string &p, const float *x, float
     else orc_gemm(W.get(p + ".w2.weight"), h1.data(), y, nullptr, L, H, F, F, F, H);
 }
 
-// adaLN (base 0) -> QKV + b -> RMS q, k -> RoPE (fscale; none when fscale == 0) into rows
-// [row_off, row_off + L) of J [S, 3H]. mod: per row (stride chunks*H) or one row.
+// adaLN (base 0) -> QKV + b -> de-interleave -> RMS q, k -> RoPE (fscale; none when fscale == 0)
+// into rows [row_off, row_off + L) of J [S, 3H]. mod: per row (stride chunks*H) or one row.
+// The checkpoint's qkv weight and bias are element-interleaved: output column 3c + j is channel c
+// of q (j = 0), k (1) or v (2); it lands at column j*H + c of J (qkv_split3,
+// shaders/ops_conv.metal:60-74, called at src/dit_fwd.cpp:33-36).
 void ref_pre_attn(const orc_ref_spec &s, const RefWeights &W, const std::string &p, const float *x, int L,
                   const float *mod, int per_row, int chunks, float fscale, float *J, int row_off) {
     const int H = s.H;
-    std::vector<float> xn((size_t)L * H);
+    std::vector<float> xn((size_t)L * H), qi((size_t)L * 3 * H);
     orc_adaln_ln(x, mod, xn.data(), L, H, per_row, chunks, 0, s.ln_eps);
-    orc_gemm(W.get(p + ".attn.qkv.weight"), xn.data(), J + (size_t)row_off * 3 * H, W.get(p + ".attn.qkv.bias"),
-             L, 3 * H, H, H, H, 3 * H);
+    orc_gemm(W.get(p + ".attn.qkv.weight"), xn.data(), qi.data(), W.get(p + ".attn.qkv.bias"), L, 3 * H, H, H, H,
+             3 * H);
+    for (int r = 0; r < L; ++r)
+        for (int c = 0; c < H; ++c)
+            for (int j = 0; j < 3; ++j)
+                J[(size_t)(row_off + r) * 3 * H + (size_t)j * H + c] = qi[(size_t)r * 3 * H + 3 * c + j];
     orc_rms_head(J, W.get(p + ".attn.q_norm.weight"), L, s.NH, 3 * H, s.HD, 0, row_off, s.rms_eps);
     orc_rms_head(J, W.get(p + ".attn.k_norm.weight"), L, s.NH, 3 * H, s.HD, H, row_off, s.rms_eps);
     if (fscale != 0.0f) {

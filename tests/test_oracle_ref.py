@@ -2,8 +2,8 @@
 
 Checked against:
   * a float64 NumPy restatement of the three-stream graph written here from the reference forward
-    (per-row adaLN from extended_c, SwiGLU conv-MLPs, conv-k3 out-proj, clip RoPE scaled by T/C,
-    pre-only last joint block, conv-k7 final layer);
+    (per-row adaLN from extended_c, element-interleaved qkv rows, SwiGLU conv-MLPs, conv-k3 out-proj,
+    clip RoPE scaled by T/C, pre-only last joint block, conv-k7 final layer);
   * structure: the pre-only block leaves the clip and text rows untouched, fused blocks never touch
     them, samples do not mix;
   * closed form: a zero final conv makes the velocity its bias and the sampler moves x by -bias.
@@ -97,6 +97,7 @@ def np_ref_forward(spec, w, idx, x, t, clip_pp, text_pp, gcmlp, sync_gather):
     def pre(p, xs, mod, fscale):
         xn = _ln(xs, eps) * (1 + mod[..., H:2 * H]) + mod[..., :H]
         qkv = xn @ get(p + ".attn.qkv.weight", (3 * H, H)).T + get(p + ".attn.qkv.bias")
+        qkv = np.concatenate([qkv[:, 0::3], qkv[:, 1::3], qkv[:, 2::3]], 1)   # interleaved rows 3c + j
         out = []
         for c, nm in ((0, "q_norm"), (H, "k_norm")):
             hh = qkv[:, c:c + H].reshape(len(xs), NH, -1)

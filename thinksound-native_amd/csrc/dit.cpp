@@ -69,19 +69,6 @@ int dit_spec_check(const DitSpec &s) {
     return TSN_OK;
 }
 
-DitModel::~DitModel() {
-    if (gexec_) hipGraphExecDestroy(gexec_);
-    if (graph_) hipGraphDestroy(graph_);
-    if (rt)
-        for (void *p : owned_) rt->dev.free(p);
-}
-
-int DitModel::alloc(size_t bytes, void **p) {
-    TSN_TRY(rt->dev.alloc(bytes, p));
-    owned_.push_back(*p);
-    return TSN_OK;
-}
-
 int DitModel::create(Runtime *r, const DitSpec &sp) {
     TSN_REQUIRE(r, "dit: null runtime");
     TSN_TRY(dit_spec_check(sp));
@@ -240,134 +227,6 @@ int DitModel::gs_from_g(const float *g) {
     return launch_silu(gs_, (size_t)s.B * s.H, st);
 }
 
-namespace {
-
-void qkv_problem(GemmProblem &p, const half_t *A, RowMap amap, int M, const half_t *W, const float *bias,
-                 const float *qn, const float *kn, int H, int nh, half_t *Q, half_t *K, half_t *Vt, int S, int Sp,
-                 int q_L, int q_soff, int rope_len, const float *rope, float eps) {
-    gemm_problem_init(p);
-    p.A = A; p.lda = H; p.amap = amap; p.taps = 1; p.Kc = H; p.pad = 0; p.a_T = amap.L;
-    p.W = W; p.ldw = H; p.bias = bias; p.M = M; p.N = 3 * H; p.K = H;
-    p.Q = Q; p.Kd = K; p.Vt = Vt; p.S_att = S; p.Sp = Sp; p.nh = nh; p.Hq = H;
-    p.q_L = q_L; p.q_soff = q_soff; p.rope_len = rope_len; p.rope = rope;
-    p.qn = qn; p.kn = kn; p.rms_eps = eps; p.q_scale = 0.125f;   // 1/sqrt(64), exact in f16
-}
-
-void resid_problem(GemmProblem &p, const half_t *A, int lda, RowMap amap, int taps, int Kc, int M, int N,
-                   const half_t *W, const float *bias, float *R, int ldr, const float *gate, int gate_ld) {
-    gemm_problem_init(p);
-    p.A = A; p.lda = lda; p.amap = amap; p.taps = taps; p.Kc = Kc; p.pad = taps / 2; p.a_T = amap.L;
-    p.W = W; p.ldw = taps * Kc; p.bias = bias; p.M = M; p.N = N; p.K = taps * Kc;
-    p.R = R; p.ldr = ldr; p.rmap = amap; p.gate = gate; p.gate_ld = gate_ld; p.gate_L = amap.L;
-}
-
-void store_problem(GemmProblem &p, const half_t *A, int lda, RowMap amap, int taps, int Kc, int M, int N,
-                   const half_t *W, half_t *Y, int ldy, int silu) {
-    gemm_problem_init(p);
-    p.A = A; p.lda = lda; p.amap = amap; p.taps = taps; p.Kc = Kc; p.pad = taps / 2; p.a_T = amap.L;
-    p.W = W; p.ldw = taps * Kc; p.bias = nullptr; p.M = M; p.N = N; p.K = taps * Kc;
-    p.Y = Y; p.ldy = ldy; p.ymap = amap; p.y_f16 = 1; p.silu = silu;
-}
-
-void ln_seg(LnSeg &g, const float *X, int H, RowMap map, half_t *Y, const float *mod, int nmod, int L,
-            int shift_off, int rows) {
-    g.X = X; g.ldx = H; g.xmap = map;
-    g.Y = Y; g.ldy = H; g.ymap = map;
-    g.mod = mod; g.mod_ld = nmod; g.mod_L = L; g.shift_off = shift_off; g.scale_off = shift_off + H;
-    g.rows = rows;
-}
-
-constexpr const char *K_ATTN = "flash_attn_kernel";
-constexpr const char *K_GEMV = "gemv_kernel";
-constexpr const char *K_LN16 = "ln_mod_kernel<1, 4>";
-constexpr const char *K_LNHL = "ln_mod_kernel<2, 4>";
-constexpr const char *K_SPLIT = "split_hilo_kernel";
-constexpr const char *K_RLN16 = "reduce_ln_kernel<1>";
-constexpr const char *K_RLNHL = "reduce_ln_kernel<2>";
-
-double gemm_flops(const GemmBatch &b) {
-    double f = 0;
-    for (int i = 0; i < b.nprob; ++i) f += 2.0 * b.p[i].M * (double)b.p[i].N * b.p[i].K;
-    return f;
-}
-// A once (conv taps re-read the same rows), W once, output at its storage type (residual: read + write f32)
-double gemm_bytes(const GemmBatch &b, int epi) {
-    double x = 0;
-    for (int i = 0; i < b.nprob; ++i) {
-        const GemmProblem &p = b.p[i];
-        x += 2.0 * p.M * (double)p.Kc + 2.0 * p.N * (double)p.K + (epi == EPI_RESID ? 8.0 : 2.0) * p.M * (double)p.N;
-    }
-    return x;
-}
-double ln_bytes(const LnArgs &a, bool f16) {
-    double r = 0;
-    for (int i = 0; i < a.nseg; ++i) r += a.seg[i].rows;
-    return r * a.H * (4.0 + (f16 ? 2.0 : 4.0));
-}
-
-} // namespace
-
-template <typename F>
-int DitModel::run(const char *name, double flops, double bytes, F &&launch) {
-    if (!prof_) return launch();
-    ProfRec r{name, flops, bytes, nullptr, nullptr};
-    TSN_HIP_CHECK(hipEventCreate(&r.a));
-    TSN_HIP_CHECK(hipEventCreate(&r.b));
-    LaunchEvents &ev = next_launch_events();
-    ev.start = r.a;
-    ev.stop = r.b;
-    const int rc = launch();
-    const bool consumed = ev.start == nullptr;
-    ev.start = ev.stop = nullptr;
-    if (!consumed) {   // nothing was launched: no timing for this record
-        hipEventDestroy(r.a);
-        hipEventDestroy(r.b);
-        return rc;
-    }
-    prof_->push_back(r);
-    return rc;
-}
-
-// plan, launch (timed under the kernel's own symbol) and, when K was split, reduce
-int DitModel::gemm_run(GemmBatch &b, int epi) {
-    const hipStream_t st = rt->dev.stream();
-    TSN_TRY(gemm_plan(b, epi, false));
-    TSN_TRY(run(b.kname, gemm_flops(b), gemm_bytes(b, epi), [&] { return gemm_launch_planned(b, epi, false, st); }));
-    if (!gemm_needs_reduce(b)) return TSN_OK;
-    double red = 0;
-    for (int i = 0; i < b.nprob; ++i)
-        if (b.p[i].splits > 1) red += (4.0 * b.p[i].splits + (epi == EPI_RESID ? 8.0 : 4.0)) * b.p[i].M * (double)b.p[i].N;
-    return run(epi == EPI_RESID ? "splitk_reduce_kernel<1>" : "splitk_reduce_kernel<0>", 0, red,
-               [&] { return launch_gemm_reduce(b, epi, st); });
-}
-
-// Residual GEMM batch followed by one reduce kernel that finishes the split-K sum into X
-// (x += gate * (sum + bias), fixed split order) and applies the adaLN that follows (r.seg[i].ln).
-// Segment i covers the rows of problem i. Without split and without a following LN the reduce
-// kernel is skipped (the GEMM epilogue already updated X).
-int DitModel::resid_ln(GemmBatch &b, RedLnArgs &r) {
-    const hipStream_t st = rt->dev.stream();
-    TSN_TRY(gemm_plan(b, EPI_RESID, false));
-    TSN_TRY(run(b.kname, gemm_flops(b), gemm_bytes(b, EPI_RESID), [&] { return gemm_launch_planned(b, EPI_RESID, false, st); }));
-    r.nseg = b.nprob;
-    r.H = s.H;
-    r.eps = s.ln_eps;
-    bool work = false;
-    double bytes = 0;
-    for (int i = 0; i < b.nprob; ++i) {
-        const GemmProblem &p = b.p[i];
-        RedLnSeg &g = r.seg[i];
-        g.ws = p.ws; g.splits = p.splits; g.M = p.M;
-        g.bias = p.bias; g.gate = p.gate; g.gate_ld = p.gate_ld; g.gate_L = p.gate_L;
-        g.X = p.R; g.ldx = p.ldr; g.xmap = p.rmap;
-        work = work || g.ln || g.splits > 1;
-        bytes += (double)p.M * p.N * (4.0 + (p.splits > 1 ? 4.0 * p.splits + 4.0 : 0.0));
-        if (g.ln) bytes += (double)g.ln_len * (p.M / g.mod_L) * p.N * (r.ymode == LN_F16_HILO ? 4.0 : 2.0);
-    }
-    if (!work) return TSN_OK;
-    return run(r.ymode == LN_F16_HILO ? K_RLNHL : K_RLN16, 0, bytes, [&] { return launch_reduce_ln(r, st); });
-}
-
 // Fill the LN part of r's segments (one per row map of the residual GEMM) for the adaLN that
 // runs next: LN1 of a joint or fused block (f16 into XN), or the final layer's (f16 hi|lo of the
 // audio rows into XF2).
@@ -435,7 +294,7 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
     next_ln(r, Next{NEXT_JOINT, i}, maps, 2);   // LN2 of this block: modulation chunks 3, 4
     r.seg[0].shift_off += 3 * H; r.seg[0].scale_off += 3 * H;
     r.seg[1].shift_off += 3 * H; r.seg[1].scale_off += 3 * H;
-    TSN_TRY(resid_ln(ob, r));
+    TSN_TRY(resid_ln(ob, r, s.H, s.ln_eps));
 
     const int ta = a.conv ? 3 : 1;
     GemmBatch f1;
@@ -451,7 +310,7 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
     resid_problem(f2.p[0], HF_, s.F, Sa, ta, s.F, B * La, H, a.W2, nullptr, X_, H, mod_ + a.mod_off + 5 * H, NMOD);
     resid_problem(f2.p[1], HF_, s.F, St, 1, s.F, B * Lt, H, t.W2, nullptr, X_, H, mod_ + t.mod_off + 5 * H, NMOD);
     next_ln(r, next, maps, 2);
-    return resid_ln(f2, r);
+    return resid_ln(f2, r, s.H, s.ln_eps);
 }
 
 // Fused block: src/dit_fwd.cpp:267-279 over the joined rows
@@ -489,7 +348,7 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
     RedLnArgs r;
     next_ln(r, Next{NEXT_FUSED, i}, &D, 1);   // LN2 of this block: modulation chunks 3, 4
     r.seg[0].shift_off += 3 * H; r.seg[0].scale_off += 3 * H;
-    TSN_TRY(resid_ln(ob, r));
+    TSN_TRY(resid_ln(ob, r, s.H, s.ln_eps));
 
     GemmBatch f1;
     f1.nprob = 1;
@@ -502,7 +361,7 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
     f2.ws_bytes = ws_bytes_;
     resid_problem(f2.p[0], HF_, s.F, D, 1, s.F, M, H, w.W2, nullptr, X_, H, mod_ + w.mod_off + 5 * H, NMOD);
     next_ln(r, next, &D, 1);
-    return resid_ln(f2, r);
+    return resid_ln(f2, r, s.H, s.ln_eps);
 }
 
 // timestep embedding + MLP, g = t_emb + pooled, gs = silu(g) (src/dit_fwd.cpp:111-140), then every
@@ -669,112 +528,39 @@ int DitModel::enqueue_sample(float *x, const float *text, const float *pooled, i
     return TSN_OK;
 }
 
-namespace {
-int prepare_schedule(Runtime *rt, int B, int steps, float **tsched, int *have, std::vector<void *> &owned) {
-    if (*tsched && *have == steps) return TSN_OK;
-    if (*tsched) {
-        TSN_TRY(rt->dev.free(*tsched));
-        for (auto it = owned.begin(); it != owned.end(); ++it)
-            if (*it == *tsched) { owned.erase(it); break; }
-        *tsched = nullptr;
-    }
-    std::vector<float> h((size_t)steps * B);
-    for (int st = 0; st < steps; ++st)
-        for (int b = 0; b < B; ++b) h[(size_t)st * B + b] = 1.0f - (float)st / (float)steps;
-    TSN_TRY(rt->dev.alloc(h.size() * 4, (void **)tsched));
-    owned.push_back(*tsched);
-    TSN_TRY(rt->dev.upload(*tsched, h.data(), h.size() * 4));
-    *have = steps;
-    return TSN_OK;
-}
-} // namespace
-
 int DitModel::capture_forward(const float *z, const float *t, const float *text, const float *pooled, float *v) {
     TSN_REQUIRE(ready_, "dit: weights not uploaded");
-    TSN_TRY(rt->dev.make_current());
-    if (gexec_) { hipGraphExecDestroy(gexec_); gexec_ = nullptr; }
-    if (graph_) { hipGraphDestroy(graph_); graph_ = nullptr; }
-    const hipStream_t st = rt->dev.stream();
-    TSN_HIP_CHECK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-    const int rc = enqueue_forward(z, t, text, pooled, v, nullptr);
-    hipGraph_t g = nullptr;
-    const hipError_t e = hipStreamEndCapture(st, &g);
-    if (rc != TSN_OK) { if (g) hipGraphDestroy(g); return rc; }
-    TSN_HIP_CHECK(e);
-    graph_ = g;
-    TSN_HIP_CHECK(hipGraphInstantiate(&gexec_, graph_, nullptr, nullptr, 0));
-    return TSN_OK;
+    return capture([&] { return enqueue_forward(z, t, text, pooled, v, nullptr); });
 }
 
 int DitModel::capture_sample(float *x, const float *text, const float *pooled, int steps, float cfg) {
     TSN_REQUIRE(ready_, "dit: weights not uploaded");
     TSN_TRY(rt->dev.make_current());
     TSN_TRY(prepare_sample(steps));
-    if (gexec_) { hipGraphExecDestroy(gexec_); gexec_ = nullptr; }
-    if (graph_) { hipGraphDestroy(graph_); graph_ = nullptr; }
-    const hipStream_t st = rt->dev.stream();
-    TSN_HIP_CHECK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-    const int rc = enqueue_sample(x, text, pooled, steps, cfg);
-    hipGraph_t g = nullptr;
-    const hipError_t e = hipStreamEndCapture(st, &g);
-    if (rc != TSN_OK) { if (g) hipGraphDestroy(g); return rc; }
-    TSN_HIP_CHECK(e);
-    graph_ = g;
-    TSN_HIP_CHECK(hipGraphInstantiate(&gexec_, graph_, nullptr, nullptr, 0));
-    return TSN_OK;
-}
-
-int DitModel::replay() {
-    TSN_REQUIRE(gexec_, "dit: no captured graph");
-    TSN_TRY(rt->dev.make_current());
-    TSN_HIP_CHECK(hipGraphLaunch(gexec_, rt->dev.stream()));
-    return TSN_OK;
+    return capture([&] { return enqueue_sample(x, text, pooled, steps, cfg); });
 }
 
 int DitModel::profile_forward(const float *z, const float *t, const float *text, const float *pooled, float *v,
                               std::vector<KernelStat> &stats) {
-    std::vector<ProfRec> recs;
-    prof_ = &recs;
-    const int rc = enqueue_forward(z, t, text, pooled, v, nullptr);
-    prof_ = nullptr;
-    int rc2 = rt->dev.sync();
-    stats.clear();
-    for (auto &r : recs) {
-        float ms = 0.0f;
-        if (rc == TSN_OK && rc2 == TSN_OK && hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) rc2 = TSN_ERR_HIP;
-        hipEventDestroy(r.a);
-        hipEventDestroy(r.b);
-        KernelStat *k = nullptr;
-        for (auto &e : stats)
-            if (e.name == r.name) k = &e;
-        if (!k) {
-            stats.push_back(KernelStat{});
-            k = &stats.back();
-            k->name = r.name;
-        }
-        k->launches += 1;
-        k->ms += ms;
-        k->flops += r.flops;
-        k->bytes += r.bytes;
-    }
-    if (rc != TSN_OK) return rc;
-    if (rc2 != TSN_OK) set_error("profile: event timing failed");
-    return rc2;
+    return profile([&] { return enqueue_forward(z, t, text, pooled, v, nullptr); }, stats);
 }
 
 int DitModel::prepare_sample(int steps) {
     TSN_REQUIRE(steps > 0, "dit sample: steps must be positive");
     TSN_REQUIRE(s.B <= 16 && 16 % s.B == 0, "dit sample: B must divide 16");
     TSN_TRY(rt->dev.make_current());
-    const bool same = tsched_ && tsched_steps_ == steps && cond_;
-    TSN_TRY(prepare_schedule(rt, s.B, steps, &tsched_, &tsched_steps_, owned_));
-    if (same) return TSN_OK;
-    if (cond_) {
-        TSN_TRY(rt->dev.free(cond_));
-        for (auto it = owned_.begin(); it != owned_.end(); ++it)
-            if (*it == cond_) { owned_.erase(it); break; }
-        cond_ = nullptr;
-    }
+    if (tsched_ && tsched_steps_ == steps && cond_) return TSN_OK;
+    if (tsched_) TSN_TRY(release(tsched_));
+    tsched_ = nullptr;
+    // t of step st for sample b at row st*B + b (src/pipeline.cpp:146: t = 1 - st/steps)
+    std::vector<float> h((size_t)steps * s.B);
+    for (int st = 0; st < steps; ++st)
+        for (int b = 0; b < s.B; ++b) h[(size_t)st * s.B + b] = 1.0f - (float)st / (float)steps;
+    TSN_TRY(alloc(h.size() * 4, (void **)&tsched_));
+    TSN_TRY(rt->dev.upload(tsched_, h.data(), h.size() * 4));
+    tsched_steps_ = steps;
+    if (cond_) TSN_TRY(release(cond_));
+    cond_ = nullptr;
     const size_t R = ((size_t)steps * s.B + 15) / 16 * 16, H = s.H;
     const size_t n_temb = R * s.temb_dim, n_h = R * H, n_mod = R * (size_t)NMOD, n_rep = 16 * H;
     TSN_TRY(alloc((n_temb + 3 * n_h + n_h + n_mod + n_rep) * sizeof(float), (void **)&cond_));   // zero-filled

@@ -16,7 +16,7 @@
 #pragma once
 #include <vector>
 
-#include "runtime.h"
+#include "graph.h"
 
 namespace tsn {
 
@@ -29,26 +29,11 @@ struct DitSpec {   // field meaning documented in include/tsn.h (tsn_dit_spec)
     float rope_theta, t_max_period, ln_eps, rms_eps;
 };
 
-// per-kernel statistics of one profiled evaluation (event pairs around every launch)
-struct KernelStat {
-    std::string name;   // kernel symbol
-    int launches = 0;
-    double ms = 0.0;     // summed event time
-    double flops = 0.0;  // algorithmic: 2*M*N*K per GEMM (conv K = taps*IC), 4*B*NH*S^2*64 attention
-    double bytes = 0.0;  // algorithmic HBM bytes (each operand once at its storage type)
-};
-
-struct ManifestEntry {
-    std::string name;
-    int64_t numel;
-    int64_t offset;
-};
 std::vector<ManifestEntry> dit_manifest(const DitSpec &s);
 int dit_spec_check(const DitSpec &s);
 
-class DitModel {
+class DitModel : public GraphRunner {
 public:
-    ~DitModel();
     int create(Runtime *rt, const DitSpec &s);
     // WeightSet::load equivalent (src/net.mm:126-173): the flat BF16 buffer in manifest order is
     // uploaded once; GEMM weights become f16 (exact for |w| >= 2^-14), conv weights are reordered
@@ -72,13 +57,11 @@ public:
     // hipGraph of one forward on fixed pointers; replay() re-runs it
     int capture_forward(const float *z, const float *t, const float *text, const float *pooled, float *v);
     int capture_sample(float *x, const float *text, const float *pooled, int steps, float cfg);
-    int replay();
 
     // one eager evaluation with a HIP event pair around every launch; stats per kernel symbol
     int profile_forward(const float *z, const float *t, const float *text, const float *pooled, float *v,
                         std::vector<KernelStat> &stats);
 
-    Runtime *rt = nullptr;
     DitSpec s{};
     int S = 0, Sp = 0, NMOD = 0;
     float *t_dev = nullptr;   // [B] scratch for host-supplied t
@@ -105,20 +88,9 @@ private:
                      const float *mod_pre);
     int block_joint(int i, bool ln1, Next next);
     int block_fused(int i, bool ln1, Next next);
-    int resid_ln(GemmBatch &b, RedLnArgs &r);
     void next_ln(RedLnArgs &r, Next next, const RowMap *maps, int nseg);
     int modulation(const float *gs, int row0, int rows);
     int gs_from_g(const float *g);
-    int alloc(size_t bytes, void **p);
-    template <typename F>
-    int run(const char *name, double flops, double bytes, F &&launch);
-    int gemm_run(GemmBatch &b, int epi);
-    struct ProfRec {
-        const char *name;
-        double flops, bytes;
-        hipEvent_t a, b;
-    };
-    std::vector<ProfRec> *prof_ = nullptr;
 
     std::vector<StreamW> ja_, jt_, fu_;
     const uint16_t *Wmod_ = nullptr, *Wt0_ = nullptr, *Wt2_ = nullptr;
@@ -140,9 +112,6 @@ private:
     float *ws_ = nullptr;            // split-K partials of the residual GEMMs
     size_t ws_bytes_ = 0;
     bool ready_ = false;
-    hipGraph_t graph_ = nullptr;
-    hipGraphExec_t gexec_ = nullptr;
-    std::vector<void *> owned_;
 };
 
 } // namespace tsn

@@ -1,0 +1,181 @@
+// graph.cpp — GraphRunner plumbing and the GEMM-problem / LN-segment builders.
+#include "graph.h"
+
+#include <string.h>
+
+namespace tsn {
+
+GraphRunner::~GraphRunner() {
+    if (gexec_) hipGraphExecDestroy(gexec_);
+    if (graph_) hipGraphDestroy(graph_);
+    if (rt)
+        for (void *p : owned_) rt->dev.free(p);
+}
+
+int GraphRunner::alloc(size_t bytes, void **p) {
+    TSN_TRY(rt->dev.alloc(bytes, p));
+    owned_.push_back(*p);
+    return TSN_OK;
+}
+
+int GraphRunner::release(void *p) {
+    for (auto it = owned_.begin(); it != owned_.end(); ++it)
+        if (*it == p) {
+            owned_.erase(it);
+            return rt->dev.free(p);
+        }
+    TSN_REQUIRE(false, "release: not an allocation of this model");
+}
+
+int GraphRunner::capture(const std::function<int()> &enqueue) {
+    TSN_TRY(rt->dev.make_current());
+    if (gexec_) { hipGraphExecDestroy(gexec_); gexec_ = nullptr; }
+    if (graph_) { hipGraphDestroy(graph_); graph_ = nullptr; }
+    const hipStream_t st = rt->dev.stream();
+    TSN_HIP_CHECK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    const int rc = enqueue();
+    hipGraph_t g = nullptr;
+    const hipError_t e = hipStreamEndCapture(st, &g);
+    if (rc != TSN_OK) { if (g) hipGraphDestroy(g); return rc; }
+    TSN_HIP_CHECK(e);
+    graph_ = g;
+    TSN_HIP_CHECK(hipGraphInstantiate(&gexec_, graph_, nullptr, nullptr, 0));
+    return TSN_OK;
+}
+
+int GraphRunner::replay() {
+    TSN_REQUIRE(gexec_, "no captured graph");
+    TSN_TRY(rt->dev.make_current());
+    TSN_HIP_CHECK(hipGraphLaunch(gexec_, rt->dev.stream()));
+    return TSN_OK;
+}
+
+int GraphRunner::profile(const std::function<int()> &enqueue, std::vector<KernelStat> &stats) {
+    std::vector<ProfRec> recs;
+    prof_ = &recs;
+    const int rc = enqueue();
+    prof_ = nullptr;
+    int rc2 = rt->dev.sync();
+    stats.clear();
+    for (auto &r : recs) {
+        float ms = 0.0f;
+        if (rc == TSN_OK && rc2 == TSN_OK && hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess) rc2 = TSN_ERR_HIP;
+        hipEventDestroy(r.a);
+        hipEventDestroy(r.b);
+        KernelStat *k = nullptr;
+        for (auto &e : stats)
+            if (e.name == r.name) k = &e;
+        if (!k) {
+            stats.push_back(KernelStat{});
+            k = &stats.back();
+            k->name = r.name;
+        }
+        k->launches += 1;
+        k->ms += ms;
+        k->flops += r.flops;
+        k->bytes += r.bytes;
+    }
+    if (rc != TSN_OK) return rc;
+    if (rc2 != TSN_OK) set_error("profile: event timing failed");
+    return rc2;
+}
+
+int GraphRunner::gemm_run(GemmBatch &b, int epi) {
+    const hipStream_t st = rt->dev.stream();
+    TSN_TRY(gemm_plan(b, epi, false));
+    TSN_TRY(run(b.kname, gemm_flops(b), gemm_bytes(b, epi), [&] { return gemm_launch_planned(b, epi, false, st); }));
+    if (!gemm_needs_reduce(b)) return TSN_OK;
+    double red = 0;
+    for (int i = 0; i < b.nprob; ++i)
+        if (b.p[i].splits > 1) red += (4.0 * b.p[i].splits + (epi == EPI_RESID ? 8.0 : 4.0)) * b.p[i].M * (double)b.p[i].N;
+    return run(epi == EPI_RESID ? "splitk_reduce_kernel<1>" : "splitk_reduce_kernel<0>", 0, red,
+               [&] { return launch_gemm_reduce(b, epi, st); });
+}
+
+// Residual GEMM batch followed by one reduce kernel that finishes the split-K sum into X
+// (x += gate * (sum + bias), fixed split order) and applies the adaLN that follows (r.seg[i].ln).
+// Segment i covers the rows of problem i. Without split and without a following LN the reduce
+// kernel is skipped (the GEMM epilogue already updated X).
+int GraphRunner::resid_ln(GemmBatch &b, RedLnArgs &r, int H, float eps) {
+    const hipStream_t st = rt->dev.stream();
+    TSN_TRY(gemm_plan(b, EPI_RESID, false));
+    TSN_TRY(run(b.kname, gemm_flops(b), gemm_bytes(b, EPI_RESID), [&] { return gemm_launch_planned(b, EPI_RESID, false, st); }));
+    r.nseg = b.nprob;
+    r.H = H;
+    r.eps = eps;
+    bool work = false;
+    double bytes = 0;
+    for (int i = 0; i < b.nprob; ++i) {
+        const GemmProblem &p = b.p[i];
+        RedLnSeg &g = r.seg[i];
+        g.ws = p.ws; g.splits = p.splits; g.M = p.M;
+        g.bias = p.bias; g.gate = p.gate; g.gate_ld = p.gate_ld; g.gate_L = p.gate_L;
+        g.X = p.R; g.ldx = p.ldr; g.xmap = p.rmap;
+        work = work || g.ln || g.splits > 1;
+        bytes += (double)p.M * p.N * (4.0 + (p.splits > 1 ? 4.0 * p.splits + 4.0 : 0.0));
+        if (g.ln) bytes += (double)g.ln_len * (p.M / g.mod_L) * p.N * (r.ymode == LN_F16_HILO ? 4.0 : 2.0);
+    }
+    if (!work) return TSN_OK;
+    return run(r.ymode == LN_F16_HILO ? K_RLNHL : K_RLN16, 0, bytes, [&] { return launch_reduce_ln(r, st); });
+}
+
+double gemm_flops(const GemmBatch &b) {
+    double f = 0;
+    for (int i = 0; i < b.nprob; ++i) f += 2.0 * b.p[i].M * (double)b.p[i].N * b.p[i].K;
+    return f;
+}
+
+// A once (conv taps re-read the same rows), W once, output at its storage type (residual: read +
+// write f32; SwiGLU: half the columns)
+double gemm_bytes(const GemmBatch &b, int epi) {
+    double x = 0;
+    for (int i = 0; i < b.nprob; ++i) {
+        const GemmProblem &p = b.p[i];
+        const double out = epi == EPI_RESID ? 8.0 : epi == EPI_SWIGLU ? 1.0 : (p.y_f16 || epi == EPI_QKV ? 2.0 : 4.0);
+        x += 2.0 * p.M * (double)p.Kc + 2.0 * p.N * (double)p.K + out * p.M * (double)p.N;
+    }
+    return x;
+}
+
+double ln_bytes(const LnArgs &a, bool f16) {
+    double r = 0;
+    for (int i = 0; i < a.nseg; ++i) r += a.seg[i].rows;
+    return r * a.H * (4.0 + (f16 ? 2.0 : 4.0));
+}
+
+void qkv_problem(GemmProblem &p, const half_t *A, RowMap amap, int M, const half_t *W, const float *bias,
+                 const float *qn, const float *kn, int H, int nh, half_t *Q, half_t *K, half_t *Vt, int S, int Sp,
+                 int q_L, int q_soff, int rope_len, const float *rope, float eps) {
+    gemm_problem_init(p);
+    p.A = A; p.lda = H; p.amap = amap; p.taps = 1; p.Kc = H; p.pad = 0; p.a_T = amap.L;
+    p.W = W; p.ldw = H; p.bias = bias; p.M = M; p.N = 3 * H; p.K = H;
+    p.Q = Q; p.Kd = K; p.Vt = Vt; p.S_att = S; p.Sp = Sp; p.nh = nh; p.Hq = H;
+    p.q_L = q_L; p.q_soff = q_soff; p.rope_len = rope_len; p.rope = rope;
+    p.qn = qn; p.kn = kn; p.rms_eps = eps; p.q_scale = 0.125f;   // 1/sqrt(64), exact in f16
+}
+
+void resid_problem(GemmProblem &p, const half_t *A, int lda, RowMap amap, int taps, int Kc, int M, int N,
+                   const half_t *W, const float *bias, float *R, int ldr, const float *gate, int gate_ld) {
+    gemm_problem_init(p);
+    p.A = A; p.lda = lda; p.amap = amap; p.taps = taps; p.Kc = Kc; p.pad = taps / 2; p.a_T = amap.L;
+    p.W = W; p.ldw = taps * Kc; p.bias = bias; p.M = M; p.N = N; p.K = taps * Kc;
+    p.R = R; p.ldr = ldr; p.rmap = amap; p.gate = gate; p.gate_ld = gate_ld; p.gate_L = amap.L;
+}
+
+void store_problem(GemmProblem &p, const half_t *A, int lda, RowMap amap, int taps, int Kc, int M, int N,
+                   const half_t *W, half_t *Y, int ldy, int silu) {
+    gemm_problem_init(p);
+    p.A = A; p.lda = lda; p.amap = amap; p.taps = taps; p.Kc = Kc; p.pad = taps / 2; p.a_T = amap.L;
+    p.W = W; p.ldw = taps * Kc; p.bias = nullptr; p.M = M; p.N = N; p.K = taps * Kc;
+    p.Y = Y; p.ldy = ldy; p.ymap = amap; p.y_f16 = 1; p.silu = silu;
+}
+
+void ln_seg(LnSeg &g, const float *X, int H, RowMap map, half_t *Y, const float *mod, int nmod, int L,
+            int shift_off, int rows) {
+    g.X = X; g.ldx = H; g.xmap = map;
+    g.Y = Y; g.ldy = H; g.ymap = map;
+    g.mod = mod; g.mod_ld = nmod; g.mod_L = L; g.shift_off = shift_off; g.scale_off = shift_off + H;
+    g.rows = rows;
+}
+
+} // namespace tsn

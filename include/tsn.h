@@ -161,12 +161,72 @@ typedef struct {
 int tsn_dit_profile_forward(tsn_dit *dit, const float *z, const float *t, const float *text, const float *pooled,
                             float *v, tsn_kernel_stat *stats, int cap, int *n_stats);
 
+/* ---------------- model: the reference checkpoint's graph, tn::DitModel (src/models.h:55-85) ----------------
+ * The three-stream graph of src/dit_fwd.cpp:104-304: latent (T rows, RoPE), clip (C rows, RoPE
+ * positions scaled by T/C), text (TS rows, no RoPE); per-row adaLN of the latent stream from
+ * extended_c = sync_gather + global_c (global_c = gcmlp + t_emb), SwiGLU FFNs (conv k3 for latent
+ * and clip, linear for text), conv k3 out-projection for latent and clip, pre-only last joint
+ * block, fused blocks over the latent rows alone, conv k7 final layer. CFG arms are folded into
+ * the batch (sample 2p cond, 2p+1 uncond). */
+typedef struct {
+    int B;              /* batch; 1, 2, 4, 8 or 16 */
+    int T;              /* latent rows: llround(44100/2048 * dur) (src/models.h:20-22); 172 at 8 s */
+    int C;              /* clip rows: 8 * dur (src/pipeline.cpp:82) */
+    int TS;             /* text rows (154) */
+    int H, NH, HD, F;   /* hidden 1024, heads 16, head dim 64, SwiGLU width H_ffn 2816 (src/models.h:58-60) */
+    int latent;         /* latent channels (64) */
+    int n_joint;        /* joint three-stream blocks, the last one pre-only (7) */
+    int n_fused;        /* fused blocks over the latent rows (14) */
+    float rope_theta;   /* 10000 */
+    float t_max_period; /* 1: timestep sinusoid fr_k = (1e4/max_period)*1e4^(-2k/H) (src/dit_fwd.cpp:111-118) */
+    float ln_eps;       /* 1e-5 */
+    float rms_eps;      /* 1e-6 */
+} tsn_refdit_spec;
+typedef struct tsn_refdit tsn_refdit;
+
+/* geometry of a dur-second generation with B samples (src/pipeline.cpp:81-83) */
+int tsn_refdit_spec_for_duration(int dur_s, int B, tsn_refdit_spec *out);
+/* checkpoint tensor manifest (flat BF16 buffer order), the names DitModel::forward looks up with
+ * W->need (src/dit_fwd.cpp); qkv weight/bias rows are element-interleaved as in the checkpoint */
+int tsn_refdit_manifest_count(const tsn_refdit_spec *spec);
+int tsn_refdit_manifest_entry(const tsn_refdit_spec *spec, int idx, char *name, int name_cap, int64_t *numel,
+                              int64_t *offset);
+int64_t tsn_refdit_manifest_total(const tsn_refdit_spec *spec);
+int tsn_refdit_create(tsn_runtime *rt, const tsn_refdit_spec *spec, tsn_refdit **out);   /* DitModel::load src/dit.cpp:29-47 */
+int tsn_refdit_destroy(tsn_refdit *dit);
+/* WeightSet::load (src/net.mm:126-173): flat BF16 in manifest order; upload-time transforms:
+ * qkv row de-interleave (replaces qkv_split3, src/dit_fwd.cpp:33-36), conv [OC][IC][K] -> [OC][K][IC],
+ * BF16 -> FP16 */
+int tsn_refdit_upload_weights(tsn_refdit *dit, const uint16_t *weights_host, size_t numel);
+/* DitModel::forward (src/models.h:83-84, src/dit_fwd.cpp:104-304) with the arms batched:
+ * x [B][T][latent], clip_pp [B][C][H], text_pp [B][TS][H], gcmlp [B][H], sync_gather [B][T][H]
+ * -> flow [B][T][latent]; every sample at flow time t. Enqueued; tsn_sync before reading flow. */
+int tsn_refdit_forward(tsn_refdit *dit, const float *x, float t, const float *clip_pp, const float *text_pp,
+                       const float *gcmlp, const float *sync_gather, float *flow);
+/* same with per-sample t (device [B]) and optional taps: the streams [B][T+C+TS][H] after each block */
+int tsn_refdit_forward_ex(tsn_refdit *dit, const float *x, const float *t, const float *clip_pp, const float *text_pp,
+                          const float *gcmlp, const float *sync_gather, float *flow, float *taps);
+/* Euler sampler with CFG (src/pipeline.cpp:141-155): x [B/2][T][latent] in/out */
+int tsn_refdit_sample(tsn_refdit *dit, float *x, const float *clip_pp, const float *text_pp, const float *gcmlp,
+                      const float *sync_gather, int steps, float cfg);
+/* hipGraph capture of one forward (t from device t[B]) or of the whole sampler, then replay */
+int tsn_refdit_capture_forward(tsn_refdit *dit, const float *x, const float *t, const float *clip_pp,
+                               const float *text_pp, const float *gcmlp, const float *sync_gather, float *flow);
+int tsn_refdit_capture_sample(tsn_refdit *dit, float *x, const float *clip_pp, const float *text_pp,
+                              const float *gcmlp, const float *sync_gather, int steps, float cfg);
+int tsn_refdit_replay(tsn_refdit *dit);
+/* per-kernel statistics of one eager forward (no reference counterpart, as tsn_dit_profile_forward) */
+int tsn_refdit_profile_forward(tsn_refdit *dit, const float *x, const float *t, const float *clip_pp,
+                               const float *text_pp, const float *gcmlp, const float *sync_gather, float *flow,
+                               tsn_kernel_stat *stats, int cap, int *n_stats);
+
 /* ---------------- synthetic data (specified generator; see thinksound-native_amd/csrc/synth.cpp) ---------------- */
 int tsn_synth_normal_f32(uint64_t seed, uint64_t index, double mean, double std, size_t n, float *out_host);
 int tsn_synth_normal_bf16(uint64_t seed, uint64_t index, double mean, double std, size_t n, uint16_t *out_host);
 int tsn_synth_uniform_f32(uint64_t seed, uint64_t index, double lo, double hi, size_t n, float *out_host);
 /* all weights of a spec, flat BF16 in manifest order: N(0, 0.02); q/k norm weights N(norm_mean, 0.02) */
 int tsn_dit_synth_weights(const tsn_dit_spec *spec, uint64_t seed, double norm_mean, uint16_t *out_host);
+int tsn_refdit_synth_weights(const tsn_refdit_spec *spec, uint64_t seed, double norm_mean, uint16_t *out_host);
 
 #ifdef __cplusplus
 }

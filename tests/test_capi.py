@@ -115,3 +115,34 @@ def test_error_paths_without_gpu(tsn):
 
 def test_oracle_builds_and_reports_threads(orc):
     assert orc.num_threads() >= 1
+
+
+def test_ref_manifest_matches_oracle(tsn, orc):
+    spec = tsn.ref_spec_for_duration(8, 2)
+    # src/models.h:20-22 and src/pipeline.cpp:81-83 at 8 s
+    assert (spec.T, spec.C, spec.TS, spec.H, spec.F, spec.n_joint, spec.n_fused) == (172, 64, 154, 1024, 2816, 7, 14)
+    assert tsn.ref_spec_for_duration(30, 2).T == 646
+    man = tsn.ref_manifest(spec)
+    assert man == orc.ref_manifest(spec.as_dict())
+    assert tsn.ref_manifest_total(spec) == man[-1][1] + man[-1][2]
+    names = [n for n, _, _ in man]
+    # the pre-only last joint block has no clip/text out-proj or FFN, 2 modulation chunks
+    assert "joint_blocks.6.clip_block.linear1.weight" not in names
+    assert "joint_blocks.6.latent_block.linear1.weight" in names
+    d = dict((n, k) for n, k, _ in man)
+    assert d["joint_blocks.6.text_block.adaLN_modulation.1.weight"] == 2 * 1024 * 1024
+    assert d["final_layer.conv.weight"] == 64 * 1024 * 7
+    small = spec.copy(n_joint=2, n_fused=1, T=6, C=3, TS=4, H=256, NH=4, F=128, latent=32)
+    assert tsn.ref_manifest(small) == orc.ref_manifest(small.as_dict())
+
+
+def test_ref_spec_errors(tsn):
+    spec = tsn.ref_spec_for_duration(8, 2)
+    with pytest.raises(RuntimeError):
+        tsn.ref_spec_for_duration(0, 2)
+    with pytest.raises(RuntimeError):
+        tsn.ref_spec_for_duration(8, 3)   # batch must be 1, 2, 4, 8 or 16
+    rt_null = ctypes.c_void_p()
+    h = ctypes.c_void_p()
+    assert tsn.lib().tsn_refdit_create(rt_null, ctypes.byref(spec), ctypes.byref(h)) == 1
+    assert tsn.lib().tsn_refdit_replay(None) == 1

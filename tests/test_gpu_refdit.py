@@ -1,0 +1,120 @@
+"""GPU parity of the reference checkpoint's DiT graph (libtsn tsn_refdit_*) against the oracle's
+restatement of src/dit_fwd.cpp:104-304 (oracle/oracle_ref.cpp) on identical seeded weights and
+inputs, at the reference's own 8 s geometry (B = 2 CFG arms, T = 172 latent, C = 64 clip,
+TS = 154 text rows, H = 1024, SwiGLU F = 2816, 7 joint + 14 fused blocks):
+
+  * one evaluation: velocity rel-L2 <= 1e-3, the three streams after every block <= 2e-3;
+  * structure, bit-exact: the pre-only last joint block and the fused blocks leave the clip and
+    text rows untouched; samples do not mix;
+  * bit-identical reruns, eager and hipGraph replay (with eager work between replays);
+  * the CFG Euler sampler (2 steps): displacement x - x0 rel-L2 <= 2e-3, graph replay bit-identical.
+
+Tolerances are the north-star bars (f16 MFMA operands, f32 accumulation and residual streams).
+"""
+import numpy as np
+import pytest
+
+from conftest import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def ref(tsn, rt):
+    spec = tsn.ref_spec_for_duration(8, 2)
+    w16 = tsn.ref_synth_weights(spec, 4242, 1.0)     # q/k norm weights 1 + N(0, 0.02)
+    m = tsn.RefDitModel(rt, spec)
+    m.upload_weights(w16)
+    yield spec, m, tsn.bf16_to_f32(w16)
+    m.close()
+
+
+def _io(tsn, rt, spec, seed=4242, cfg_pairs=False):
+    inp = tsn.ref_synth_inputs(spec, seed, cfg_pairs=cfg_pairs)
+    return inp, {k: rt.array(v) for k, v in inp.items()}
+
+
+def _fwd(m, rt, spec, dev, taps=None):
+    v = rt.empty((spec.B, spec.T, spec.latent))
+    m.forward_ex(dev["x"], dev["t"], dev["clip_pp"], dev["text_pp"], dev["gcmlp"], dev["sync_gather"], v, taps)
+    rt.sync()
+    return v
+
+
+def test_ref_forward_parity_and_taps(tsn, rt, orc, ref):
+    spec, m, w32 = ref
+    inp, dev = _io(tsn, rt, spec)
+    nblk = spec.n_joint + spec.n_fused
+    S, T, C = spec.T + spec.C + spec.TS, spec.T, spec.C
+    taps = rt.empty((nblk, spec.B, S, spec.H))
+    v = _fwd(m, rt, spec, dev, taps).numpy()
+    vr, tr = orc.ref_dit_forward(spec.as_dict(), w32, taps=True, **inp)
+    tg = taps.numpy()
+    err = rel_l2(v, vr)
+    blk = [rel_l2(tg[i], tr[i]) for i in range(nblk)]
+    lat = [rel_l2(tg[i][:, :T], tr[i][:, :T]) for i in range(nblk)]
+    clip = [rel_l2(tg[i][:, T:T + C], tr[i][:, T:T + C]) for i in range(nblk)]
+    text = [rel_l2(tg[i][:, T + C:], tr[i][:, T + C:]) for i in range(nblk)]
+    print("velocity rel-L2 %.3g; worst block %.3g (latent %.3g, clip %.3g, text %.3g)"
+          % (err, max(blk), max(lat), max(clip), max(text)))
+    assert err <= 1e-3
+    assert max(blk) <= 2e-3 and max(lat) <= 2e-3 and max(clip) <= 2e-3 and max(text) <= 2e-3
+    # pre-only last joint block and fused blocks leave clip and text rows as they were
+    nj = spec.n_joint
+    for i in range(nj - 1, nblk):
+        assert np.array_equal(tg[i][:, T:].view(np.uint32), tg[nj - 2][:, T:].view(np.uint32))
+
+
+def test_ref_samples_do_not_mix(tsn, rt, ref):
+    spec, m, _ = ref
+    inp, dev = _io(tsn, rt, spec, seed=91)
+    a = _fwd(m, rt, spec, dev).numpy()
+    for k in ("x", "clip_pp", "text_pp", "gcmlp", "sync_gather"):
+        b = inp[k].copy()
+        b[0] = b[0][::-1] if b.ndim > 2 else -b[0]
+        d = dict(dev, **{k: rt.array(b)})
+        out = _fwd(m, rt, spec, d).numpy()
+        assert np.array_equal(out[1].view(np.uint32), a[1].view(np.uint32)), k
+        assert not np.array_equal(out[0], a[0]), k
+
+
+def test_ref_bit_identical_and_graph(tsn, rt, ref):
+    spec, m, _ = ref
+    inp, dev = _io(tsn, rt, spec, seed=77)
+    a = _fwd(m, rt, spec, dev).numpy()
+    b = _fwd(m, rt, spec, dev).numpy()
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    v3 = rt.empty((spec.B, spec.T, spec.latent))
+    m.capture_forward(dev["x"], dev["t"], dev["clip_pp"], dev["text_pp"], dev["gcmlp"], dev["sync_gather"], v3)
+    for _ in range(3):
+        m.replay()
+        rt.sync()
+        assert np.array_equal(a.view(np.uint32), v3.numpy().view(np.uint32))
+        _fwd(m, rt, spec, dev)   # eager work on the same buffers between replays
+    # scalar-t entry point (DitModel::forward signature) matches the device-t one
+    v4 = rt.empty((spec.B, spec.T, spec.latent))
+    m.forward(dev["x"], float(inp["t"][0]), dev["clip_pp"], dev["text_pp"], dev["gcmlp"], dev["sync_gather"], v4)
+    rt.sync()
+    assert np.array_equal(a.view(np.uint32), v4.numpy().view(np.uint32))
+
+
+def test_ref_sampler_two_steps(tsn, rt, orc, ref):
+    spec, m, w32 = ref
+    inp, dev = _io(tsn, rt, spec, cfg_pairs=True)
+    x0 = inp["x"][0::2].copy()
+    x = rt.array(x0)
+    args = (dev["clip_pp"], dev["text_pp"], dev["gcmlp"], dev["sync_gather"])
+    m.sample(x, *args, 2, 5.0)
+    rt.sync()
+    out = x.numpy()
+    r = orc.ref_dit_sample(spec.as_dict(), w32, x0, inp["clip_pp"], inp["text_pp"], inp["gcmlp"],
+                           inp["sync_gather"], 2, 5.0)
+    err = rel_l2(out - x0, r - x0)
+    print("reference-graph sampler displacement rel-L2 %.3g" % err)
+    assert out.shape == (spec.B // 2, spec.T, spec.latent)
+    assert err <= 2e-3
+    x2 = rt.array(x0)
+    m.capture_sample(x2, *args, 2, 5.0)
+    m.replay()
+    rt.sync()
+    assert np.array_equal(out.view(np.uint32), x2.numpy().view(np.uint32))

@@ -47,6 +47,24 @@ class DitSpec(ctypes.Structure):
         return s
 
 
+class RefDitSpec(ctypes.Structure):
+    """tsn_refdit_spec (include/tsn.h): the reference checkpoint's three-stream graph."""
+    _fields_ = [("B", ctypes.c_int), ("T", ctypes.c_int), ("C", ctypes.c_int), ("TS", ctypes.c_int),
+                ("H", ctypes.c_int), ("NH", ctypes.c_int), ("HD", ctypes.c_int), ("F", ctypes.c_int),
+                ("latent", ctypes.c_int), ("n_joint", ctypes.c_int), ("n_fused", ctypes.c_int),
+                ("rope_theta", ctypes.c_float), ("t_max_period", ctypes.c_float),
+                ("ln_eps", ctypes.c_float), ("rms_eps", ctypes.c_float)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+    def copy(self, **kw):
+        s = RefDitSpec()
+        for k, _ in self._fields_:
+            setattr(s, k, kw.get(k, getattr(self, k)))
+        return s
+
+
 class KernelStat(ctypes.Structure):
     """tsn_kernel_stat (include/tsn.h)."""
     _fields_ = [("name", ctypes.c_char * 64), ("launches", ctypes.c_int), ("total_ms", ctypes.c_double),
@@ -105,9 +123,27 @@ _SIGS = {
     "tsn_synth_normal_bf16": [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, _SZ, _P],
     "tsn_synth_uniform_f32": [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double, ctypes.c_double, _SZ, _P],
     "tsn_dit_synth_weights": [ctypes.POINTER(DitSpec), ctypes.c_uint64, ctypes.c_double, _P],
+    "tsn_refdit_spec_for_duration": [_I, _I, ctypes.POINTER(RefDitSpec)],
+    "tsn_refdit_manifest_count": [ctypes.POINTER(RefDitSpec)],
+    "tsn_refdit_manifest_entry": [ctypes.POINTER(RefDitSpec), _I, ctypes.c_char_p, _I,
+                                  ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)],
+    "tsn_refdit_manifest_total": [ctypes.POINTER(RefDitSpec)],
+    "tsn_refdit_create": [_P, ctypes.POINTER(RefDitSpec), ctypes.POINTER(_P)],
+    "tsn_refdit_destroy": [_P],
+    "tsn_refdit_upload_weights": [_P, _P, _SZ],
+    "tsn_refdit_forward": [_P, _P, _FL, _P, _P, _P, _P, _P],
+    "tsn_refdit_forward_ex": [_P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "tsn_refdit_sample": [_P, _P, _P, _P, _P, _P, _I, _FL],
+    "tsn_refdit_capture_forward": [_P, _P, _P, _P, _P, _P, _P, _P],
+    "tsn_refdit_capture_sample": [_P, _P, _P, _P, _P, _P, _I, _FL],
+    "tsn_refdit_replay": [_P],
+    "tsn_refdit_profile_forward": [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.POINTER(KernelStat), _I,
+                                   ctypes.POINTER(_I)],
+    "tsn_refdit_synth_weights": [ctypes.POINTER(RefDitSpec), ctypes.c_uint64, ctypes.c_double, _P],
 }
 _RESTYPES = {"tsn_last_error": ctypes.c_char_p, "tsn_last_gpu_ms": ctypes.c_double,
-             "tsn_dit_manifest_total": ctypes.c_int64, "tsn_version": _I}
+             "tsn_dit_manifest_total": ctypes.c_int64, "tsn_refdit_manifest_total": ctypes.c_int64,
+             "tsn_version": _I}
 
 
 def lib():
@@ -187,6 +223,35 @@ def synth_uniform_f32(seed, index, lo, hi, shape):
 def synth_weights(spec, seed=4242, norm_mean=0.0):
     w = np.empty(manifest_total(spec), np.uint16)
     call("tsn_dit_synth_weights", ctypes.byref(spec), seed, norm_mean, ptr(w))
+    return w
+
+
+def ref_spec_for_duration(dur_s, B=2):
+    """Geometry of a dur-second generation with B samples (T = llround(44100/2048*dur), C = 8*dur, TS = 154)."""
+    s = RefDitSpec()
+    call("tsn_refdit_spec_for_duration", dur_s, B, ctypes.byref(s))
+    return s
+
+
+def ref_manifest(spec):
+    L = lib()
+    n = L.tsn_refdit_manifest_count(ctypes.byref(spec))
+    out = []
+    buf = ctypes.create_string_buffer(256)
+    for i in range(n):
+        numel, off = ctypes.c_int64(), ctypes.c_int64()
+        call("tsn_refdit_manifest_entry", ctypes.byref(spec), i, buf, 256, ctypes.byref(numel), ctypes.byref(off))
+        out.append((buf.value.decode(), numel.value, off.value))
+    return out
+
+
+def ref_manifest_total(spec):
+    return int(lib().tsn_refdit_manifest_total(ctypes.byref(spec)))
+
+
+def ref_synth_weights(spec, seed=4242, norm_mean=0.0):
+    w = np.empty(ref_manifest_total(spec), np.uint16)
+    call("tsn_refdit_synth_weights", ctypes.byref(spec), seed, norm_mean, ptr(w))
     return w
 
 
@@ -373,6 +438,58 @@ class DitModel:
                  "flops": arr[i].flops, "bytes": arr[i].bytes} for i in range(n.value)]
 
 
+def _p(a):
+    return a.p if a is not None else None
+
+
+class RefDitModel:
+    """tn::DitModel mirror (src/models.h:55-85) for the reference checkpoint's three-stream graph."""
+
+    def __init__(self, rt, spec):
+        self.rt, self.spec = rt, spec
+        h = ctypes.c_void_p()
+        call("tsn_refdit_create", rt.h, ctypes.byref(spec), ctypes.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().tsn_refdit_destroy(self.h)
+            self.h = None
+
+    def upload_weights(self, w_bf16):
+        w_bf16 = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+        call("tsn_refdit_upload_weights", self.h, ptr(w_bf16), w_bf16.size)
+
+    def forward(self, x, t, clip_pp, text_pp, gcmlp, sync_gather, flow):
+        call("tsn_refdit_forward", self.h, x.p, float(t), _p(clip_pp), _p(text_pp), gcmlp.p, sync_gather.p, flow.p)
+
+    def forward_ex(self, x, t_dev, clip_pp, text_pp, gcmlp, sync_gather, flow, taps=None):
+        call("tsn_refdit_forward_ex", self.h, x.p, t_dev.p, _p(clip_pp), _p(text_pp), gcmlp.p, sync_gather.p,
+             flow.p, _p(taps))
+
+    def sample(self, x, clip_pp, text_pp, gcmlp, sync_gather, steps, cfg):
+        call("tsn_refdit_sample", self.h, x.p, _p(clip_pp), _p(text_pp), gcmlp.p, sync_gather.p, steps, cfg)
+
+    def capture_forward(self, x, t_dev, clip_pp, text_pp, gcmlp, sync_gather, flow):
+        call("tsn_refdit_capture_forward", self.h, x.p, t_dev.p, _p(clip_pp), _p(text_pp), gcmlp.p,
+             sync_gather.p, flow.p)
+
+    def capture_sample(self, x, clip_pp, text_pp, gcmlp, sync_gather, steps, cfg):
+        call("tsn_refdit_capture_sample", self.h, x.p, _p(clip_pp), _p(text_pp), gcmlp.p, sync_gather.p, steps, cfg)
+
+    def replay(self):
+        call("tsn_refdit_replay", self.h)
+
+    def profile_forward(self, x, t_dev, clip_pp, text_pp, gcmlp, sync_gather, flow):
+        cap = 64
+        arr = (KernelStat * cap)()
+        n = ctypes.c_int()
+        call("tsn_refdit_profile_forward", self.h, x.p, t_dev.p, _p(clip_pp), _p(text_pp), gcmlp.p, sync_gather.p,
+             flow.p, arr, cap, ctypes.byref(n))
+        return [{"name": arr[i].name.decode(), "launches": arr[i].launches, "ms": arr[i].total_ms,
+                 "flops": arr[i].flops, "bytes": arr[i].bytes} for i in range(n.value)]
+
+
 # Input index space of the synthetic generator (weights use their manifest index).
 IDX_Z, IDX_TEXT, IDX_POOLED, IDX_T, IDX_G, IDX_X = 1000, 1001, 1002, 1003, 1004, 1005
 
@@ -396,3 +513,22 @@ def synth_inputs(spec, seed=4242, cfg_pairs=False):
         pooled = synth_normal_f32(seed, IDX_POOLED, 0.0, 1.0, (B, H))
         t = np.repeat(synth_uniform_f32(seed, IDX_T, 0.0, 1.0, (1,)), B).astype(np.float32)
     return {"z": z, "t": t, "text": text, "pooled": pooled}
+
+
+IDX_CLIP, IDX_GCMLP, IDX_SYNC = 1006, 1007, 1008
+
+
+def ref_synth_inputs(spec, seed=4242, cfg_pairs=False):
+    """Seeded inputs of the reference graph: x [B,T,latent], t [B], clip_pp [B,C,H], text_pp [B,TS,H],
+    gcmlp [B,H], sync_gather [B,T,H]. cfg_pairs: (cond, uncond) pairs share x, t, clip_pp and
+    sync_gather (src/pipeline.cpp:146-147); the unconditional arm has its own text_pp and gcmlp."""
+    B, T, C, TS, H, lat = spec.B, spec.T, spec.C, spec.TS, spec.H, spec.latent
+    n = B // 2 if cfg_pairs else B
+    rep = (lambda a: np.repeat(a, 2, axis=0)) if cfg_pairs else (lambda a: a)
+    x = rep(synth_normal_f32(seed, IDX_X, 0.0, 1.0, (n, T, lat)))
+    clip = rep(synth_normal_f32(seed, IDX_CLIP, 0.0, 1.0, (n, C, H)))
+    sync = rep(synth_normal_f32(seed, IDX_SYNC, 0.0, 1.0, (n, T, H)))
+    text = synth_normal_f32(seed, IDX_TEXT, 0.0, 1.0, (B, TS, H))
+    gcmlp = synth_normal_f32(seed, IDX_GCMLP, 0.0, 1.0, (B, H))
+    t = np.repeat(synth_uniform_f32(seed, IDX_T, 0.0, 1.0, (1,)), B).astype(np.float32)
+    return {"x": x, "t": t, "clip_pp": clip, "text_pp": text, "gcmlp": gcmlp, "sync_gather": sync}

@@ -249,8 +249,12 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
                 *(float4 *)op = make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
             } else {
                 half_t *op = (half_t *)a.O + orow + d0;
-                *(half4 *)op = half4{(half_t)(o[dt][0] * inv), (half_t)(o[dt][1] * inv),
-                                     (half_t)(o[dt][2] * inv), (half_t)(o[dt][3] * inv)};
+                const float y0 = o[dt][0] * inv, y1 = o[dt][1] * inv, y2 = o[dt][2] * inv, y3 = o[dt][3] * inv;
+                const half4 hi = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
+                *(half4 *)op = hi;
+                if (a.o_lo)   // f16 remainder at column offset o_lo: hi + lo carries the f32 value
+                    *(half4 *)(op + a.o_lo) = half4{(half_t)(y0 - (float)hi[0]), (half_t)(y1 - (float)hi[1]),
+                                                    (half_t)(y2 - (float)hi[2]), (half_t)(y3 - (float)hi[3])};
             }
         }
     }
@@ -284,6 +288,8 @@ int launch_attention(const AttnArgs &a, hipStream_t st) {
     TSN_REQUIRE(a.BH > 0 && a.nh > 0 && a.BH % a.nh == 0, "attention: BH must be a multiple of nh");
     TSN_REQUIRE(a.omap.L > 0, "attention: output row map");
     TSN_REQUIRE(a.ldo % 4 == 0, "attention: ldo must be a multiple of 4");
+    TSN_REQUIRE(a.o_lo == 0 || (!a.o_f32 && a.o_lo % 4 == 0 && a.o_lo >= a.nh * 64 && a.ldo >= a.o_lo + a.nh * 64),
+                "attention: hi|lo output needs f16 O, o_lo >= nh*64 (multiple of 4) and ldo >= o_lo + nh*64");
     TSN_REQUIRE((((uintptr_t)a.Q) & 15) == 0 && (((uintptr_t)a.K) & 15) == 0 && (((uintptr_t)a.Vt) & 15) == 0,
                 "attention: 16-byte aligned Q/K/Vt");
     TSN_REQUIRE((long long)a.S * 64 * 2 < (1LL << 31) && (long long)a.Sp * 64 * 2 < (1LL << 31),

@@ -6,6 +6,7 @@
 #include <new>
 
 #include "dit.h"
+#include "refdit.h"
 
 namespace tsn {
 void synth_normal_f32(uint64_t seed, uint64_t idx, double mean, double std, size_t n, float *out);
@@ -18,6 +19,9 @@ struct tsn_runtime {
 };
 struct tsn_dit {
     tsn::DitModel m;
+};
+struct tsn_refdit {
+    tsn::RefDitModel m;
 };
 
 #define RT_CHECK(r)                                                 \
@@ -32,6 +36,27 @@ static tsn::DitSpec to_spec(const tsn_dit_spec *c) {
     s.audio_ffn_conv = c->audio_ffn_conv; s.rope_theta = c->rope_theta; s.t_max_period = c->t_max_period;
     s.ln_eps = c->ln_eps; s.rms_eps = c->rms_eps;
     return s;
+}
+
+static tsn::RefDitSpec to_ref_spec(const tsn_refdit_spec *c) {
+    tsn::RefDitSpec s;
+    s.B = c->B; s.T = c->T; s.C = c->C; s.TS = c->TS; s.H = c->H; s.NH = c->NH; s.HD = c->HD; s.F = c->F;
+    s.latent = c->latent; s.n_joint = c->n_joint; s.n_fused = c->n_fused; s.rope_theta = c->rope_theta;
+    s.t_max_period = c->t_max_period; s.ln_eps = c->ln_eps; s.rms_eps = c->rms_eps;
+    return s;
+}
+
+static int copy_stats(const std::vector<tsn::KernelStat> &ks, tsn_kernel_stat *stats, int cap, int *n_stats) {
+    const int n = (int)ks.size() < cap ? (int)ks.size() : cap;
+    for (int i = 0; i < n; ++i) {
+        snprintf(stats[i].name, sizeof stats[i].name, "%s", ks[i].name.c_str());
+        stats[i].launches = ks[i].launches;
+        stats[i].total_ms = ks[i].ms;
+        stats[i].flops = ks[i].flops;
+        stats[i].bytes = ks[i].bytes;
+    }
+    *n_stats = n;
+    return TSN_OK;
 }
 
 extern "C" {
@@ -216,16 +241,99 @@ int tsn_dit_profile_forward(tsn_dit *dit, const float *z, const float *t, const 
     std::vector<tsn::KernelStat> ks;
     const int rc = dit->m.profile_forward(z, t, text, pooled, v, ks);
     if (rc != TSN_OK) return rc;
-    const int n = (int)ks.size() < cap ? (int)ks.size() : cap;
-    for (int i = 0; i < n; ++i) {
-        snprintf(stats[i].name, sizeof stats[i].name, "%s", ks[i].name.c_str());
-        stats[i].launches = ks[i].launches;
-        stats[i].total_ms = ks[i].ms;
-        stats[i].flops = ks[i].flops;
-        stats[i].bytes = ks[i].bytes;
-    }
-    *n_stats = n;
+    return copy_stats(ks, stats, cap, n_stats);
+}
+
+/* ---------------- reference graph ---------------- */
+#define REF_CHECK(d)                                                              \
+    do {                                                                          \
+        if (!(d)) { tsn::set_error("null refdit handle"); return TSN_ERR_ARG; }   \
+    } while (0)
+
+int tsn_refdit_spec_for_duration(int dur_s, int B, tsn_refdit_spec *out) {
+    if (!out || dur_s <= 0) { tsn::set_error("refdit spec: null out pointer or non-positive duration"); return TSN_ERR_ARG; }
+    const tsn::RefDitSpec s = tsn::refdit_spec_for_duration(dur_s, B);
+    out->B = s.B; out->T = s.T; out->C = s.C; out->TS = s.TS; out->H = s.H; out->NH = s.NH; out->HD = s.HD;
+    out->F = s.F; out->latent = s.latent; out->n_joint = s.n_joint; out->n_fused = s.n_fused;
+    out->rope_theta = s.rope_theta; out->t_max_period = s.t_max_period; out->ln_eps = s.ln_eps; out->rms_eps = s.rms_eps;
+    return tsn::refdit_spec_check(s);
+}
+int tsn_refdit_manifest_count(const tsn_refdit_spec *spec) {
+    if (!spec) { tsn::set_error("null spec"); return -1; }
+    return (int)tsn::refdit_manifest(to_ref_spec(spec)).size();
+}
+int tsn_refdit_manifest_entry(const tsn_refdit_spec *spec, int idx, char *name, int name_cap, int64_t *numel,
+                              int64_t *offset) {
+    if (!spec) { tsn::set_error("null spec"); return TSN_ERR_ARG; }
+    const auto m = tsn::refdit_manifest(to_ref_spec(spec));
+    if (idx < 0 || idx >= (int)m.size()) { tsn::set_error("manifest index out of range"); return TSN_ERR_ARG; }
+    if (name && name_cap > 0) snprintf(name, (size_t)name_cap, "%s", m[idx].name.c_str());
+    if (numel) *numel = m[idx].numel;
+    if (offset) *offset = m[idx].offset;
     return TSN_OK;
+}
+int64_t tsn_refdit_manifest_total(const tsn_refdit_spec *spec) {
+    if (!spec) { tsn::set_error("null spec"); return -1; }
+    const auto m = tsn::refdit_manifest(to_ref_spec(spec));
+    return m.back().offset + m.back().numel;
+}
+int tsn_refdit_create(tsn_runtime *rt, const tsn_refdit_spec *spec, tsn_refdit **out) {
+    RT_CHECK(rt);
+    if (!spec || !out) { tsn::set_error("null spec or out pointer"); return TSN_ERR_ARG; }
+    *out = nullptr;
+    tsn_refdit *d = new (std::nothrow) tsn_refdit();
+    if (!d) { tsn::set_error("out of host memory"); return TSN_ERR_OOM; }
+    const int rc = d->m.create(&rt->rt, to_ref_spec(spec));
+    if (rc != TSN_OK) { delete d; return rc; }
+    *out = d;
+    return TSN_OK;
+}
+int tsn_refdit_destroy(tsn_refdit *d) { delete d; return TSN_OK; }
+int tsn_refdit_upload_weights(tsn_refdit *d, const uint16_t *w, size_t numel) {
+    REF_CHECK(d);
+    return d->m.upload_weights(w, numel);
+}
+int tsn_refdit_forward(tsn_refdit *d, const float *x, float t, const float *clip_pp, const float *text_pp,
+                       const float *gcmlp, const float *sync_gather, float *flow) {
+    REF_CHECK(d);
+    tsn::RefDitModel &m = d->m;
+    std::vector<float> th((size_t)m.s.B, t);
+    TSN_TRY(m.rt->dev.upload(m.t_dev, th.data(), th.size() * 4));
+    return m.enqueue_forward(x, m.t_dev, clip_pp, text_pp, gcmlp, sync_gather, flow, nullptr);
+}
+int tsn_refdit_forward_ex(tsn_refdit *d, const float *x, const float *t, const float *clip_pp, const float *text_pp,
+                          const float *gcmlp, const float *sync_gather, float *flow, float *taps) {
+    REF_CHECK(d);
+    return d->m.enqueue_forward(x, t, clip_pp, text_pp, gcmlp, sync_gather, flow, taps);
+}
+int tsn_refdit_sample(tsn_refdit *d, float *x, const float *clip_pp, const float *text_pp, const float *gcmlp,
+                      const float *sync_gather, int steps, float cfg) {
+    REF_CHECK(d);
+    TSN_TRY(d->m.prepare_sample(steps));
+    return d->m.enqueue_sample(x, clip_pp, text_pp, gcmlp, sync_gather, steps, cfg);
+}
+int tsn_refdit_capture_forward(tsn_refdit *d, const float *x, const float *t, const float *clip_pp,
+                               const float *text_pp, const float *gcmlp, const float *sync_gather, float *flow) {
+    REF_CHECK(d);
+    return d->m.capture_forward(x, t, clip_pp, text_pp, gcmlp, sync_gather, flow);
+}
+int tsn_refdit_capture_sample(tsn_refdit *d, float *x, const float *clip_pp, const float *text_pp, const float *gcmlp,
+                              const float *sync_gather, int steps, float cfg) {
+    REF_CHECK(d);
+    return d->m.capture_sample(x, clip_pp, text_pp, gcmlp, sync_gather, steps, cfg);
+}
+int tsn_refdit_replay(tsn_refdit *d) {
+    REF_CHECK(d);
+    return d->m.replay();
+}
+int tsn_refdit_profile_forward(tsn_refdit *d, const float *x, const float *t, const float *clip_pp,
+                               const float *text_pp, const float *gcmlp, const float *sync_gather, float *flow,
+                               tsn_kernel_stat *stats, int cap, int *n_stats) {
+    if (!d || !stats || !n_stats || cap <= 0) { tsn::set_error("profile: null argument"); return TSN_ERR_ARG; }
+    std::vector<tsn::KernelStat> ks;
+    const int rc = d->m.profile_forward(x, t, clip_pp, text_pp, gcmlp, sync_gather, flow, ks);
+    if (rc != TSN_OK) return rc;
+    return copy_stats(ks, stats, cap, n_stats);
 }
 
 int tsn_synth_normal_f32(uint64_t seed, uint64_t index, double mean, double std, size_t n, float *out) {
@@ -241,6 +349,15 @@ int tsn_synth_normal_bf16(uint64_t seed, uint64_t index, double mean, double std
 int tsn_synth_uniform_f32(uint64_t seed, uint64_t index, double lo, double hi, size_t n, float *out) {
     if (!out && n) { tsn::set_error("null output"); return TSN_ERR_ARG; }
     tsn::synth_uniform_f32(seed, index, lo, hi, n, out);
+    return TSN_OK;
+}
+int tsn_refdit_synth_weights(const tsn_refdit_spec *spec, uint64_t seed, double norm_mean, uint16_t *out) {
+    if (!spec || !out) { tsn::set_error("null spec or output"); return TSN_ERR_ARG; }
+    const auto m = tsn::refdit_manifest(to_ref_spec(spec));
+    for (size_t i = 0; i < m.size(); ++i) {
+        const bool is_norm = m[i].name.find("norm.weight") != std::string::npos;
+        tsn::synth_normal_bf16(seed, (uint64_t)i, is_norm ? norm_mean : 0.0, 0.02, (size_t)m[i].numel, out + m[i].offset);
+    }
     return TSN_OK;
 }
 int tsn_dit_synth_weights(const tsn_dit_spec *spec, uint64_t seed, double norm_mean, uint16_t *out) {

@@ -372,8 +372,16 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
                 for (int e = 0; e < 8; ++e) v[e] = silu_f(v[e]);
             const long long o = rowmap_phys(P.ymap, m) * (long long)P.ldy + n;
             if (P.y_f16) {
-                *(half8 *)((half_t *)P.Y + o) = half8{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3],
-                                                      (half_t)v[4], (half_t)v[5], (half_t)v[6], (half_t)v[7]};
+                half8 hi;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) hi[e] = (half_t)v[e];
+                *(half8 *)((half_t *)P.Y + o) = hi;
+                if (P.y_lo) {
+                    half8 lo;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) lo[e] = (half_t)(v[e] - (float)hi[e]);
+                    *(half8 *)((half_t *)P.Y + o + P.y_lo) = lo;
+                }
             } else {
                 float *y = (float *)P.Y + o;
                 *(float4 *)y = make_float4(v[0], v[1], v[2], v[3]);
@@ -390,10 +398,21 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             float a[8], b[8];
             ldsum8(tile, row * TP + col, a);
             ldsum8(tile, row * TP + 64 + col, b);
+            float y[8];
             half8 o;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) o[e] = (half_t)(silu_f(a[e]) * b[e]);
-            *(half8 *)((half_t *)P.Y + rowmap_phys(P.ymap, m) * (long long)P.ldy + n0 / 2 + col) = o;
+            for (int e = 0; e < 8; ++e) {
+                y[e] = silu_f(a[e]) * b[e];
+                o[e] = (half_t)y[e];
+            }
+            half_t *dst = (half_t *)P.Y + rowmap_phys(P.ymap, m) * (long long)P.ldy + n0 / 2 + col;
+            *(half8 *)dst = o;
+            if (P.y_lo) {
+                half8 lo;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) lo[e] = (half_t)(y[e] - (float)o[e]);
+                *(half8 *)(dst + P.y_lo) = lo;
+            }
         }
     } else if constexpr (EPI == EPI_RESID) {
 #pragma unroll
@@ -746,6 +765,12 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         TSN_REQUIRE(p.amap.L > 0 && p.a_T > 0, "gemm: row map");
         TSN_REQUIRE((((uintptr_t)p.A) & 15) == 0 && (((uintptr_t)p.W) & 15) == 0, "gemm: A and W must be 16-byte aligned");
         if (epi == EPI_STORE) TSN_REQUIRE(p.Y && p.ymap.L > 0, "gemm: output");
+        if (p.y_lo) {
+            const int wout = epi == EPI_SWIGLU ? p.N / 2 : p.N;
+            TSN_REQUIRE((epi == EPI_STORE || epi == EPI_SWIGLU) && p.y_f16 && p.y_lo % 8 == 0 && p.y_lo >= wout &&
+                            p.ldy >= p.y_lo + wout,
+                        "gemm: hi|lo output needs f16 Y, lo offset a multiple of 8 past the hi columns, ldy >= y_lo + width");
+        }
         if (epi == EPI_SWIGLU)
             TSN_REQUIRE(p.Y && p.ymap.L > 0 && p.y_f16 && p.N % BN == 0 && p.ldy % 8 == 0 &&
                             (((uintptr_t)p.Y) & 15) == 0,
@@ -787,8 +812,14 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     // Split-K (pipelined kernel, residual epilogue, workspace given): one common K chunk of kc
     // tiles for every problem, the largest kc (>= 4) that divides every problem's K tiles and gives
     // at least 224 workgroups; otherwise the smallest such kc. Partials need splits*M*N floats.
-    for (int i = 0; i < b.nprob; ++i) { b.p[i].splits = 1; b.p[i].ws = nullptr; }
-    if (pipe && (epi == EPI_RESID || epi == EPI_STORE) && b.ws) {
+    bool any_lo = false;
+    for (int i = 0; i < b.nprob; ++i) {
+        b.p[i].splits = 1;
+        b.p[i].ws = nullptr;
+        any_lo = any_lo || b.p[i].y_lo;
+    }
+    TSN_REQUIRE(pipe || !any_lo, "gemm: hi|lo output needs the pipelined kernel (f16 A, 16-byte aligned rows)");
+    if (pipe && (epi == EPI_RESID || epi == EPI_STORE) && b.ws && !any_lo) {
         int nkmin = 1 << 30;
         for (int i = 0; i < b.nprob; ++i) nkmin = std::min(nkmin, b.p[i].K / BK);
         int best = 0;

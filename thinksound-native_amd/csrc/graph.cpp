@@ -113,7 +113,7 @@ int GraphRunner::resid_ln(GemmBatch &b, RedLnArgs &r, int H, float eps) {
         g.X = p.R; g.ldx = p.ldr; g.xmap = p.rmap;
         work = work || g.ln || g.splits > 1;
         bytes += (double)p.M * p.N * (4.0 + (p.splits > 1 ? 4.0 * p.splits + 4.0 : 0.0));
-        if (g.ln) bytes += (double)g.ln_len * (p.M / g.mod_L) * p.N * (r.ymode == LN_F16_HILO ? 4.0 : 2.0);
+        if (g.ln) bytes += (double)g.ln_len * (p.M / g.mod_L) * p.N * (r.ymode == LN_F16_HILO || g.hilo ? 4.0 : 2.0);
     }
     if (!work) return TSN_OK;
     return run(r.ymode == LN_F16_HILO ? K_RLNHL : K_RLN16, 0, bytes, [&] { return launch_reduce_ln(r, st); });
@@ -131,7 +131,8 @@ double gemm_bytes(const GemmBatch &b, int epi) {
     double x = 0;
     for (int i = 0; i < b.nprob; ++i) {
         const GemmProblem &p = b.p[i];
-        const double out = epi == EPI_RESID ? 8.0 : epi == EPI_SWIGLU ? 1.0 : (p.y_f16 || epi == EPI_QKV ? 2.0 : 4.0);
+        double out = epi == EPI_RESID ? 8.0 : epi == EPI_SWIGLU ? 1.0 : (p.y_f16 || epi == EPI_QKV ? 2.0 : 4.0);
+        if (p.y_lo) out *= 2.0;
         x += 2.0 * p.M * (double)p.Kc + 2.0 * p.N * (double)p.K + out * p.M * (double)p.N;
     }
     return x;

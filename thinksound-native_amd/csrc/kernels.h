@@ -24,6 +24,9 @@ struct GemmProblem {
     // EPI_SWIGLU: W rows interleaved in 64-row blocks (w1 block j, then w3 block j), N = 2F;
     // Y[ymap(m)*ldy + 64j + c] = silu(w1 row 64j+c · a) * (w3 row 64j+c · a), f16, no bias
     void *Y; int ldy; RowMap ymap; int y_f16; int silu;
+    // f16 Y (EPI_STORE, EPI_SWIGLU): nonzero also writes lo = f16(y - f16(y)) at column offset y_lo
+    // of the same row (hi|lo operand of a following GEMM against [W | W]); K is then never split
+    int y_lo;
     // EPI_RESID: R[rmap(m)*ldr + n] += gate[(m / gate_L)*gate_ld + n] * (acc + bias)
     float *R; int ldr; RowMap rmap; const float *gate; int gate_ld; int gate_L;
     // EPI_QKV: columns [0,Hq) q, [Hq,2Hq) k, [2Hq,3Hq) v; heads of hd = 64 columns.
@@ -73,6 +76,7 @@ struct AttnArgs {
     const half_t *Q, *K, *Vt;
     int S, Sp, nh, BH;
     void *O; int o_f32; int ldo; RowMap omap;
+    int o_lo;           // f16 O: nonzero also writes lo = f16(o - f16(o)) at column offset o_lo
     float scale_log2;   // softmax scale * log2(e)
 };
 int launch_attention(const AttnArgs &a, hipStream_t st);
@@ -115,6 +119,7 @@ struct RedLnSeg {
     int ln, ln_len;
     const float *mod; int mod_ld, mod_L, shift_off, scale_off;
     void *Y; int ldy; RowMap ymap;
+    int hilo;   // this segment's LN output as an f16 hi|lo pair (lo at column H + c) whatever ymode
 };
 struct RedLnArgs {
     RedLnSeg seg[3];
@@ -173,6 +178,15 @@ int launch_bf16_to_f32(const uint16_t *src, float *dst, size_t n, hipStream_t st
 int launch_f16_to_f32(const half_t *src, float *dst, size_t n, hipStream_t st);
 // conv weight [OC][IC][K] (bf16 or f16, src_bf16 selects) -> [OC][K][IC] f16
 int launch_conv_weight_reorder(const void *src, int src_bf16, half_t *dst, int OC, int IC, int K, hipStream_t st);
+
+// Upload-time weight layout (bf16 source [OC][IC][KT]; KT = 1 for a linear weight or a vector):
+// destination row r(oc) = (oc % ra)*rb + (oc / ra)*rc + rd (ra = 1, rb = 0, rc = 1, rd = 0 keeps the
+// order), tap-major [KT][IC] within the row, channels written twice ([w | w]) when dup; f16, or f32
+// when out_f32. Every r(oc) must lie in [0, dst_rows).
+int launch_weight_prep(const uint16_t *src, void *dst, int out_f32, int OC, int IC, int KT, int dup, int ra, int rb,
+                       int rc, int rd, long long dst_rows, hipStream_t st);
+// y = silu(x[m] + v[m / L]) (x [M][H], v [M/L][H] f32) as f16 hi|lo rows [M][2H] (LN_F16_HILO layout)
+int launch_bcast_add_silu_f16(const float *x, const float *v, half_t *y, int L, int M, int H, hipStream_t st);
 
 // reference-surface elementwise ops (f32)
 int launch_silu(float *x, size_t n, hipStream_t st);

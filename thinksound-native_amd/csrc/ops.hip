@@ -135,7 +135,7 @@ __global__ __launch_bounds__(512) void reduce_ln_kernel(const RedLnArgs a) {
     half_t *y = (half_t *)S.Y + rowmap_phys(S.ymap, v) * (long long)S.ldy + col;
     const half4 hi = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
     *(half4 *)y = hi;
-    if constexpr (YMODE == LN_F16_HILO)
+    if (YMODE == LN_F16_HILO || S.hilo)   // uniform over the workgroup
         *(half4 *)(y + H) = half4{(half_t)(y0 - (float)hi[0]), (half_t)(y1 - (float)hi[1]),
                                   (half_t)(y2 - (float)hi[2]), (half_t)(y3 - (float)hi[3])};
 }
@@ -361,6 +361,43 @@ __global__ void conv_reorder_kernel(const void *src, int src_bf16, half_t *dst, 
     dst[i] = src_bf16 ? (half_t)bf16_to_f32(((const uint16_t *)src)[si]) : ((const half_t *)src)[si];
 }
 
+// Upload-time weight layout: src bf16 [OC][IC][KT] -> dst row r(oc) = (oc % ra)*rb + (oc / ra)*rc + rd,
+// tap-major [KT][IC] within the row, each tap's IC channels written twice ([w | w]) when dup.
+__global__ void weight_prep_kernel(const uint16_t *src, void *dst, int out_f32, int OC, int IC, int KT, int dup,
+                                   int ra, int rb, int rc, int rd) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)OC * IC * KT) return;
+    const int ic = (int)(i % IC);
+    const long long q = i / IC;
+    const int k = (int)(q % KT);
+    const int oc = (int)(q / KT);
+    const float w = bf16_to_f32(src[((long long)oc * IC + ic) * KT + k]);
+    const long long row = (long long)(oc % ra) * rb + (long long)(oc / ra) * rc + rd;
+    const int w_ic = IC * (dup ? 2 : 1);
+    const long long d = row * KT * w_ic + (long long)k * w_ic + ic;
+    if (out_f32) {
+        ((float *)dst)[d] = w;
+        if (dup) ((float *)dst)[d + IC] = w;
+    } else {
+        ((half_t *)dst)[d] = (half_t)w;
+        if (dup) ((half_t *)dst)[d + IC] = (half_t)w;
+    }
+}
+
+// y = silu(x[m][c] + v[m / L][c]) as an f16 hi|lo pair: y[m][c] = hi = f16(y), y[m][H + c] =
+// f16(y - hi). Rows of extended_c = sync_gather + global_c with SiLU applied, the operand of the
+// per-row modulation GEMM against [W | W] (src/dit_fwd.cpp:133-136).
+__global__ void bcast_add_silu_kernel(const float *x, const float *v, half_t *y, int L, int M, int H) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)M * H) return;
+    const int m = (int)(i / H), c = (int)(i - (long long)m * H);
+    const float a = x[i] + v[(long long)(m / L) * H + c];
+    const float s = a / (1.0f + __expf(-a));
+    const half_t hi = (half_t)s;
+    y[(long long)m * 2 * H + c] = hi;
+    y[(long long)m * 2 * H + H + c] = (half_t)(s - (float)hi);
+}
+
 // reference-surface elementwise kernels (shaders/ops_conv.metal:9-57,146-169,193-201)
 __global__ void silu_kernel(float *x, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -473,6 +510,8 @@ int launch_reduce_ln(const RedLnArgs &a, hipStream_t st) {
         TSN_REQUIRE(!s.ln || (s.mod && s.Y && s.mod_L > 0 && s.ymap.L > 0 && s.mod_ld % 4 == 0 &&
                               s.shift_off % 4 == 0 && s.scale_off % 4 == 0 && s.ldy % 4 == 0),
                     "reduce_ln: layer-norm output");
+        TSN_REQUIRE(!s.ln || (a.ymode != LN_F16_HILO && !s.hilo) || s.ldy >= 2 * a.H,
+                    "reduce_ln: hi|lo output needs ldy >= 2H");
         total += s.M;
     }
     dim3 grid(total), block(a.H / 4);
@@ -598,6 +637,25 @@ int launch_conv_weight_reorder(const void *src, int src_bf16, half_t *dst, int O
     return TSN_OK;
 }
 
+int launch_weight_prep(const uint16_t *src, void *dst, int out_f32, int OC, int IC, int KT, int dup, int ra, int rb,
+                       int rc, int rd, long long dst_rows, hipStream_t st) {
+    TSN_REQUIRE(src && dst && OC > 0 && IC > 0 && KT > 0 && ra > 0 && dst_rows > 0, "weight_prep: arguments");
+    for (int oc = 0; oc < OC; ++oc) {   // every destination row inside the destination
+        const long long row = (long long)(oc % ra) * rb + (long long)(oc / ra) * rc + rd;
+        TSN_REQUIRE(row >= 0 && row < dst_rows, "weight_prep: row map leaves the destination");
+    }
+    const size_t n = (size_t)OC * IC * KT;
+    TSN_LAUNCH(weight_prep_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, dst, out_f32, OC, IC, KT, dup, ra, rb,
+               rc, rd);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_bcast_add_silu_f16(const float *x, const float *v, half_t *y, int L, int M, int H, hipStream_t st) {
+    TSN_REQUIRE(x && v && y && L > 0 && M > 0 && H > 0, "bcast_add_silu: arguments");
+    TSN_LAUNCH(bcast_add_silu_kernel, dim3(blocks_for((size_t)M * H)), dim3(256), 0, st, x, v, y, L, M, H);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
 int launch_silu(float *x, size_t n, hipStream_t st) {
     TSN_REQUIRE(x || n == 0, "silu: null");
     if (n == 0) return TSN_OK;

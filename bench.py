@@ -169,6 +169,63 @@ def pmc_pass():
     return 0
 
 
+def bench_ref(tsn, rt, args):
+    """The reference checkpoint's own three-stream graph at 8 s (B=2, T=172, C=64, TS=154): graph
+    replays of one evaluation, the 24-step sampler, and per-kernel statistics."""
+    spec = tsn.ref_spec_for_duration(8, 2)
+    t0 = time.time()
+    w16 = tsn.ref_synth_weights(spec, 4242, 0.0)
+    log("bench ref: synthetic weights %.1f s (%d params)" % (time.time() - t0, w16.size))
+    m = tsn.RefDitModel(rt, spec)
+    m.upload_weights(w16)
+    del w16
+    inp = tsn.ref_synth_inputs(spec, 4242, cfg_pairs=True)
+    d = {k: rt.array(v) for k, v in inp.items()}
+    args_in = (d["clip_pp"], d["text_pp"], d["gcmlp"], d["sync_gather"])
+    v = rt.empty((spec.B, spec.T, spec.latent))
+    m.capture_forward(d["x"], d["t"], *args_in, v)
+    for _ in range(args.warmup):
+        m.replay()
+    rt.sync()
+    n = max(1, args.steps // 2)
+    rt.begin()
+    for _ in range(n):
+        m.replay()
+    ms = rt.commit() / n
+    stats = None
+    for _ in range(3):
+        stats = m.profile_forward(d["x"], d["t"], *args_in, v)
+    stats.sort(key=lambda k: -k["ms"])
+    tot = sum(k["ms"] for k in stats)
+    flops = sum(k["flops"] for k in stats)
+    for k in stats[:8]:
+        log("  ref %-28s %4d launches %8.3f ms  %7.1f TFLOP/s" % (k["name"], k["launches"], k["ms"],
+                                                                   k["flops"] / (k["ms"] * 1e9) if k["ms"] else 0))
+    x0 = inp["x"][0::2].copy()
+    x = rt.array(x0)
+    m.capture_sample(x, *args_in, 24, 5.0)
+    m.replay()
+    rt.sync()
+    samp = []
+    for _ in range(args.sampler_reps):
+        x.upload(x0)
+        rt.begin()
+        m.replay()
+        samp.append(rt.commit())
+    sampler_ms = statistics.median(samp)
+    log("bench ref: %.4f ms/eval (%.1f evals/s), 24-step sampler %.3f ms" % (ms, 1e3 / ms, sampler_ms))
+    m.close()
+    return {"workload": "reference checkpoint graph, one evaluation at 8 s, CFG batch 2",
+            "B": spec.B, "T": spec.T, "C": spec.C, "TS": spec.TS, "H": spec.H, "ffn": spec.F,
+            "joint_blocks": spec.n_joint, "fused_blocks": spec.n_fused,
+            "evals_per_s": round(1e3 / ms, 2), "ms_per_eval": round(ms, 5), "sampler_ms": round(sampler_ms, 3),
+            "eval_gflop": round(flops / 1e9, 2),
+            "mfma_frac_eval": round(flops / (ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4),
+            "kernels": [{"name": k["name"], "launches": k["launches"], "ms": round(k["ms"], 4),
+                         "share": round(k["ms"] / tot, 4)} for k in stats[:10]],
+            "launch": "hipGraph replay"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -176,6 +233,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sampler-reps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-ref", action="store_true", help="skip the reference checkpoint graph section")
     ap.add_argument("--eager", action="store_true",
                     help="launch kernel by kernel instead of replaying hipGraphs (for profilers that do not follow graphs)")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -284,6 +342,11 @@ def main():
     sampler_ms = statistics.median(samp)
     log("bench: 24-step sampler %.3f ms (median of %d; min %.3f)" % (sampler_ms, len(samp), min(samp)))
 
+    # ---------------- the reference checkpoint's graph (reported beside the metric) ----------------
+    ref = None
+    if not args.no_ref and not args.eager:
+        ref = bench_ref(tsn, rt, args)
+
     # ---------------- CPU baseline: the oracle, one full evaluation ----------------
     cpu = None
     if not args.no_cpu:
@@ -333,6 +396,7 @@ def main():
         "kernels": [{"name": k["name"], "launches": k["launches"], "ms": round(k["ms"], 4),
                      "share": round(k["ms"] / tot_ms, 4)} for k in stats],
         "cpu_baseline": cpu,
+        "reference_graph": ref,
         "accumulate": "f32 (f16 MFMA operands from BF16 weights; f32 residual stream)",
         "launch": "eager" if args.eager else "hipGraph replay",
     }

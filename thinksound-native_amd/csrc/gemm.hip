@@ -26,6 +26,9 @@ namespace tsn {
 namespace {
 
 constexpr int BM = 128, BN = 128, BK = 64, LDSW = BK + 8;
+// stream-K: workgroups of one grid (one per CU of an MI355X), the fewest K tiles one takes, and
+// the per-workgroup cost of pipeline fill, partial store and fixup in K-tile units
+constexpr int NCU = 256, SK_MIN_UNITS = 8, SK_OVERHEAD = 6;
 
 __device__ inline int xcd_remap(int bid, int nwg) {
     const int xcd = bid & 7, idx = bid >> 3;
@@ -525,24 +528,25 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
     }
 }
 
-template <int EPI>
-__global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
+// One C tile (rows m0.., columns n0..) over the K tiles [kbeg, kbeg + nk): the pipelined K loop,
+// then either the epilogue (part == null; ks = split index for a classic split-K partial) or a raw
+// f32 [BM][BN] store of the accumulators to part (a stream-K segment, finished by the fixup kernel).
+// HL: problems may read half-width W (hi|lo A operand); SEG: more tiles follow in this workgroup
+// (stream-K), so the LDS C tile is released with a barrier at the end.
+template <int EPI, bool HL, bool SEG>
+__device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, int kbeg, int nk, float *part, int ks,
+                                          int tid) {
     // stage s: A tile at smem + s*STAGE, W tile at smem + (NS + s)*STAGE; reused for the C tile
     __shared__ __attribute__((aligned(1024))) half_t smem[2 * NS * STAGE];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tid_g = xcd_remap(blockIdx.x, gridDim.x);
-    const int pi = (bt.nprob > 2 && tid_g >= bt.p[2].tile_start) ? 2 : (bt.nprob > 1 && tid_g >= bt.p[1].tile_start) ? 1 : 0;
-    const GemmProblem &P = bt.p[pi];
-    const int M = P.M, N = P.N, K = P.K, lda = P.lda, ldw = P.ldw, Kc = P.Kc, pad = P.pad, aT = P.a_T;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int M = P.M, N = P.N, lda = P.lda, Kc = P.Kc, pad = P.pad, aT = P.a_T;
+    // w_half: W holds hc = Kc/2 channels per tap and the A row of a tap is [hi (hc) | lo (hc)]; the
+    // tap's K tiles run interleaved (hi chunk c, lo chunk c, hi chunk c+1, ...) so the second read
+    // of a W tile follows the first at once (L2 hit)
+    const int hl = HL && P.w_half ? 1 : 0, hc = Kc / 2;
     const RowMap am = P.amap;
-    // local tile -> (split, n tile, m tile), m fastest: neighbouring workgroups share W columns
-    const int local = tid_g - P.tile_start;
-    const int per_split = P.tiles_m * P.tiles_n;
-    const int ks = local / per_split;
-    const int rem = local - ks * per_split;
-    const int tn = rem / P.tiles_m, tm = rem - tn * P.tiles_m;
-    const int m0 = tm * BM, n0 = tn * BN;
+    const int ldw = P.ldw;
 
     const i32x4 rsa = make_rsrc(P.A);
     const i32x4 rsb = make_rsrc(P.W);
@@ -563,14 +567,25 @@ __global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
         const int n = n0 + r;
         b_off[i] = n < N ? (n * ldw + lc * 8) * 2 : -1;
     }
-    // this workgroup's K tiles: [kbeg, kbeg + nk)
-    const int nk = K / BK / P.splits;
-    const int kbeg = ks * nk;
     const int lda2 = lda * 2;
+    // K tiles are issued in order kbeg, kbeg + 1, ...: the tap, the offset inside it and the W
+    // column of the next one are carried from call to call (no division in the loop)
+    int nt_tap = kbeg * BK / Kc;
+    int nt_kin = kbeg * BK - nt_tap * Kc;
+    int nt_kw = hl ? nt_tap * hc + ((nt_kin >> 7) << 6) : kbeg * BK;
     auto issue = [&](int kt, int stage) {
-        const int k0 = (kbeg + kt) * BK;
-        const int tap = k0 / Kc;
-        const int kc2 = (k0 - tap * Kc) * 2 + tap * lda2;
+        (void)kt;   // = the previous call's kt + 1
+        const int tap = nt_tap, kin = nt_kin, kw = nt_kw;
+        // hi|lo: K tile j of the tap is chunk j >> 1 of the hi (j even) or lo (j odd) half
+        const int odd = (kin >> 6) & 1;
+        const int acol = hl ? odd * hc + ((kin >> 7) << 6) : kin;
+        nt_kw += (hl && !odd) ? 0 : BK;
+        nt_kin += BK;
+        if (nt_kin == Kc) {
+            nt_kin = 0;
+            ++nt_tap;
+        }
+        const int kc2 = acol * 2 + tap * lda2;
         lds_char *sa = (lds_char *)(smem + stage * STAGE) + wave * 2048;
         lds_char *sb = (lds_char *)(smem + (NS + stage) * STAGE) + wave * 2048;
 #pragma unroll
@@ -581,7 +596,7 @@ __global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const unsigned vo = b_off[i] >= 0 ? (unsigned)(b_off[i] + k0 * 2) : 0x80000000u;
+            const unsigned vo = b_off[i] >= 0 ? (unsigned)(b_off[i] + kw * 2) : 0x80000000u;
             dma16(rsb, vo, sb + i * 1024);
         }
     };
@@ -674,7 +689,109 @@ __global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
                 for (int r = 0; r < 4; ++r) tile[(rb + i * 16 + r) * TP + cb + j * 16] = acc[i][j][r];
         block_barrier();
     }
-    tile_epilogue<EPI>(P, tile, m0, n0, ks, tid);
+    if (SEG && part) {
+        // raw partial tile, row-major [BM][BN], 16-byte stores (not unrolled: keeps registers free)
+#pragma unroll 1
+        for (int p = 0; p < 8; ++p) {
+            const int c = tid + 512 * p, row = c >> 5, col = (c & 31) * 4;
+            *(float4 *)(part + row * BN + col) = *(const float4 *)(tile + row * TP + col);
+        }
+    } else {
+        tile_epilogue<EPI>(P, tile, m0, n0, ks, tid);
+    }
+    if (SEG) block_barrier();   // the LDS C tile is free again for the next tile
+}
+
+// gemm_pipe_kernel, data-parallel: workgroup -> (problem, split, n tile, m tile), m fastest so
+// neighbouring workgroups share W columns.
+// gemm_sk_kernel, stream-K (bt.sk == 1): the batch's work is a list of units (tile, K tile), problem-major,
+// tile-major, K innermost; workgroup w of G takes units [w*U/G, (w+1)*U/G) and computes each tile it
+// touches over its part of K. A tile covered whole gets the epilogue here; a tile cut by a
+// workgroup boundary leaves f32 partials in bt.ws slot (w, 0) for the first tile of w or (w, 1) for
+// its last, which gemm_fixup_kernel sums in K order (deterministic for a given G) and finishes.
+template <int EPI, bool HL>
+__device__ __forceinline__ void pipe_dp(const GemmBatch &bt) {
+    const int tid = threadIdx.x;
+    const int wg = xcd_remap(blockIdx.x, gridDim.x);
+    const int pi = (bt.nprob > 2 && wg >= bt.p[2].tile_start) ? 2 : (bt.nprob > 1 && wg >= bt.p[1].tile_start) ? 1 : 0;
+    const GemmProblem &P = bt.p[pi];
+    const int local = wg - P.tile_start;
+    const int per_split = P.tiles_m * P.tiles_n;
+    const int ks = local / per_split;
+    const int rem = local - ks * per_split;
+    const int tn = rem / P.tiles_m, tm = rem - tn * P.tiles_m;
+    const int nk = P.K / BK / P.splits;
+    pipe_tile<EPI, HL, false>(P, tm * BM, tn * BN, ks * nk, nk, nullptr, ks, tid);
+}
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
+    pipe_dp<EPI, false>(bt);
+}
+// the same for batches with a half-width-W problem
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void gemm_pipe_hl_kernel(const GemmBatch bt) {
+    pipe_dp<EPI, true>(bt);
+}
+
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void gemm_sk_kernel(const GemmBatch bt) {
+    const int tid = threadIdx.x;
+    const int wg = xcd_remap(blockIdx.x, gridDim.x);
+    const long long U = bt.sk_units, G = gridDim.x;
+    long long u = wg * U / G;
+    const long long ue = (wg + 1) * U / G;
+    for (int seg = 0; u < ue; ++seg) {
+        const int pi = (bt.nprob > 2 && u >= bt.p[2].unit_start) ? 2 : (bt.nprob > 1 && u >= bt.p[1].unit_start) ? 1 : 0;
+        const GemmProblem &P = bt.p[pi];
+        const int nkp = P.K / BK;
+        const long long lu = u - P.unit_start;
+        const int tile = (int)(lu / nkp);
+        const int kbeg = (int)(lu - (long long)tile * nkp);
+        const int nk = (int)min((long long)(nkp - kbeg), ue - u);
+        const int tn = tile / P.tiles_m, tm = tile - tn * P.tiles_m;
+        float *part = (kbeg == 0 && nk == nkp) ? nullptr : bt.ws + ((long long)wg * 2 + (seg == 0 ? 0 : 1)) * (BM * BN);
+        pipe_tile<EPI, true, true>(P, tm * BM, tn * BN, kbeg, nk, part, 0, tid);
+        u += nk;
+    }
+}
+
+// Stream-K fixup: one workgroup per tile of the batch; tiles cut by a workgroup boundary sum their
+// partial slots in workgroup (= K) order into the LDS C tile and run the epilogue, the rest return.
+template <int EPI>
+__global__ __launch_bounds__(512) void gemm_fixup_kernel(const GemmBatch bt) {
+    __shared__ __attribute__((aligned(16))) float tile[BM * TP];
+    const int tid = threadIdx.x, t = blockIdx.x;
+    const int pi = (bt.nprob > 2 && t >= bt.p[2].tile_start) ? 2 : (bt.nprob > 1 && t >= bt.p[1].tile_start) ? 1 : 0;
+    const GemmProblem &P = bt.p[pi];
+    const int local = t - P.tile_start;
+    const int nkp = P.K / BK;
+    const long long U = bt.sk_units, G = bt.sk_g;
+    const long long a = P.unit_start + (long long)local * nkp, b = a + nkp;
+    long long w = a * G / U;   // workgroup holding unit a: B(w) <= a < B(w + 1), B(w) = w*U/G
+    while (w + 1 < G && (w + 1) * U / G <= a) ++w;
+    while (w > 0 && w * U / G > a) --w;
+    if ((w + 1) * U / G >= b) return;   // the tile lies inside one workgroup: finished there
+    float v[8][4];
+#pragma unroll
+    for (int p = 0; p < 8; ++p) v[p][0] = v[p][1] = v[p][2] = v[p][3] = 0.0f;
+    for (long long ww = w; ww < G && ww * U / G < b; ++ww) {
+        const int slot = ww * U / G >= a ? 0 : 1;   // this tile is the first of ww, or (ww == w) its last
+        const float *src = bt.ws + (ww * 2 + slot) * (BM * BN);
+#pragma unroll
+        for (int p = 0; p < 8; ++p) {
+            const int c = tid + 512 * p;
+            const float4 x = *(const float4 *)(src + c * 4);
+            v[p][0] += x.x; v[p][1] += x.y; v[p][2] += x.z; v[p][3] += x.w;
+        }
+    }
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+        const int c = tid + 512 * p, row = c >> 5, col = (c & 31) * 4;
+        *(float4 *)(tile + row * TP + col) = make_float4(v[p][0], v[p][1], v[p][2], v[p][3]);
+    }
+    __syncthreads();
+    const int tn = local / P.tiles_m, tm = local - tn * P.tiles_m;
+    tile_epilogue<EPI>(P, tile, tm * BM, tn * BN, 0, tid);
 }
 
 // split-K reduction + epilogue, one thread per 4 columns; partials summed in split order
@@ -726,6 +843,15 @@ int launch_gemm(GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
 }
 
 int launch_gemm_reduce(const GemmBatch &b, int epi, hipStream_t st) {
+    if (b.sk) {
+        const dim3 grid(b.total_tiles), block(512);
+        if (epi == EPI_STORE) TSN_LAUNCH((gemm_fixup_kernel<EPI_STORE>), grid, block, 0, st, b);
+        else if (epi == EPI_RESID) TSN_LAUNCH((gemm_fixup_kernel<EPI_RESID>), grid, block, 0, st, b);
+        else if (epi == EPI_QKV) TSN_LAUNCH((gemm_fixup_kernel<EPI_QKV>), grid, block, 0, st, b);
+        else TSN_LAUNCH((gemm_fixup_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
+        TSN_HIP_CHECK(hipGetLastError());
+        return TSN_OK;
+    }
     long long red = 0;
     for (int i = 0; i < b.nprob; ++i)
         if (b.p[i].splits > 1) red += (long long)b.p[i].M * b.p[i].N / 4;
@@ -739,9 +865,17 @@ int launch_gemm_reduce(const GemmBatch &b, int epi, hipStream_t st) {
 }
 
 bool gemm_needs_reduce(const GemmBatch &b) {
+    if (b.sk) return true;
     for (int i = 0; i < b.nprob; ++i)
         if (b.p[i].splits > 1) return true;
     return false;
+}
+
+const char *gemm_reduce_name(const GemmBatch &b, int epi) {
+    if (b.sk)
+        return epi == EPI_STORE ? "gemm_fixup_kernel<0>" : epi == EPI_RESID ? "gemm_fixup_kernel<1>"
+               : epi == EPI_QKV ? "gemm_fixup_kernel<2>" : "gemm_fixup_kernel<3>";
+    return epi == EPI_RESID ? "splitk_reduce_kernel<1>" : "splitk_reduce_kernel<0>";
 }
 
 void gemm_problem_init(GemmProblem &p) {
@@ -765,6 +899,9 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         TSN_REQUIRE(p.amap.L > 0 && p.a_T > 0, "gemm: row map");
         TSN_REQUIRE((((uintptr_t)p.A) & 15) == 0 && (((uintptr_t)p.W) & 15) == 0, "gemm: A and W must be 16-byte aligned");
         if (epi == EPI_STORE) TSN_REQUIRE(p.Y && p.ymap.L > 0, "gemm: output");
+        if (p.w_half)
+            TSN_REQUIRE(p.Kc % (2 * BK) == 0 && p.ldw >= p.taps * (p.Kc / 2),
+                        "gemm: half-width W needs Kc a multiple of 128 and ldw >= taps*Kc/2");
         if (p.y_lo) {
             const int wout = epi == EPI_SWIGLU ? p.N / 2 : p.N;
             TSN_REQUIRE((epi == EPI_STORE || epi == EPI_SWIGLU) && p.y_f16 && p.y_lo % 8 == 0 && p.y_lo >= wout &&
@@ -818,7 +955,10 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         b.p[i].ws = nullptr;
         any_lo = any_lo || b.p[i].y_lo;
     }
+    bool any_half = false;
+    for (int i = 0; i < b.nprob; ++i) any_half = any_half || b.p[i].w_half;
     TSN_REQUIRE(pipe || !any_lo, "gemm: hi|lo output needs the pipelined kernel (f16 A, 16-byte aligned rows)");
+    TSN_REQUIRE(pipe || !any_half, "gemm: half-width W needs the pipelined kernel (f16 A, 16-byte aligned rows)");
     if (pipe && (epi == EPI_RESID || epi == EPI_STORE) && b.ws && !any_lo) {
         int nkmin = 1 << 30;
         for (int i = 0; i < b.nprob; ++i) nkmin = std::min(nkmin, b.p[i].K / BK);
@@ -861,9 +1001,46 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
             }
         }
     }
+    // Stream-K when the grid chosen above leaves CUs idle. Estimated critical path in K tiles:
+    // that grid = waves * longest K range per workgroup (+2 for a split-K reduce); stream-K = units
+    // per workgroup + pipeline fill, partial store and fixup.
+    b.sk = 0;
+    if (pipe && b.ws) {
+        long long units = 0, cur = 0;
+        int nkmax = 0, split = 0;
+        for (int i = 0; i < b.nprob; ++i) {
+            b.p[i].unit_start = units;
+            units += (long long)b.p[i].tiles_m * b.p[i].tiles_n * (b.p[i].K / BK);
+            nkmax = std::max(nkmax, b.p[i].K / BK / b.p[i].splits);
+            split = split || b.p[i].splits > 1;
+        }
+        cur = (long long)((b.total_tiles + NCU - 1) / NCU) * nkmax + (split ? 2 : 0);
+        const long long g = std::min<long long>(NCU, std::max<long long>(1, units / SK_MIN_UNITS));
+        const long long skt = (units + g - 1) / g + SK_OVERHEAD;
+        const size_t need = (size_t)g * 2 * BM * BN * sizeof(float);
+        if (g > 1 && skt * 10 < cur * 8 && need <= b.ws_bytes) {
+            b.sk = 1;
+            b.sk_g = (int)g;
+            b.sk_units = units;
+            int tiles = 0;
+            for (int i = 0; i < b.nprob; ++i) {   // back to one tile per (m, n): no classic split
+                GemmProblem &p = b.p[i];
+                p.splits = 1;
+                p.ws = nullptr;
+                p.tile_start = tiles;
+                tiles += p.tiles_m * p.tiles_n;
+            }
+            b.total_tiles = tiles;
+        }
+    }
     TSN_REQUIRE(pipe || epi != EPI_SWIGLU, "gemm swiglu: needs K and row strides the pipelined kernel takes");
     b.pipe = pipe ? 1 : 0;
-    b.kname = pipe ? (epi == EPI_STORE ? "gemm_pipe_kernel<0>" : epi == EPI_RESID ? "gemm_pipe_kernel<1>"
+    b.hl = any_half ? 1 : 0;
+    b.kname = b.sk ? (epi == EPI_STORE ? "gemm_sk_kernel<0>" : epi == EPI_RESID ? "gemm_sk_kernel<1>"
+                      : epi == EPI_QKV ? "gemm_sk_kernel<2>" : "gemm_sk_kernel<3>")
+            : pipe && b.hl ? (epi == EPI_STORE ? "gemm_pipe_hl_kernel<0>" : epi == EPI_RESID ? "gemm_pipe_hl_kernel<1>"
+                              : epi == EPI_QKV ? "gemm_pipe_hl_kernel<2>" : "gemm_pipe_hl_kernel<3>")
+            : pipe ? (epi == EPI_STORE ? "gemm_pipe_kernel<0>" : epi == EPI_RESID ? "gemm_pipe_kernel<1>"
                       : epi == EPI_QKV ? "gemm_pipe_kernel<2>" : "gemm_pipe_kernel<3>")
                    : a_f32 ? "gemm_f16_kernel<true, 0>"
                    : (epi == EPI_STORE ? "gemm_f16_kernel<false, 0>" : epi == EPI_RESID ? "gemm_f16_kernel<false, 1>"
@@ -874,9 +1051,21 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
 }
 
 int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
-    dim3 grid(b.total_tiles), block(b.pipe ? 512 : 256);
+    dim3 grid(b.sk ? b.sk_g : b.total_tiles), block(b.pipe ? 512 : 256);
     if (b.pipe) {
-        if (epi == EPI_STORE) TSN_LAUNCH((gemm_pipe_kernel<EPI_STORE>), grid, block, 0, st, b);
+        if (b.sk) {
+            if (epi == EPI_STORE) TSN_LAUNCH((gemm_sk_kernel<EPI_STORE>), grid, block, 0, st, b);
+            else if (epi == EPI_RESID) TSN_LAUNCH((gemm_sk_kernel<EPI_RESID>), grid, block, 0, st, b);
+            else if (epi == EPI_QKV) TSN_LAUNCH((gemm_sk_kernel<EPI_QKV>), grid, block, 0, st, b);
+            else if (epi == EPI_SWIGLU) TSN_LAUNCH((gemm_sk_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
+            else { set_error("gemm: unknown epilogue"); return TSN_ERR_ARG; }
+        } else if (b.hl) {
+            if (epi == EPI_STORE) TSN_LAUNCH((gemm_pipe_hl_kernel<EPI_STORE>), grid, block, 0, st, b);
+            else if (epi == EPI_RESID) TSN_LAUNCH((gemm_pipe_hl_kernel<EPI_RESID>), grid, block, 0, st, b);
+            else if (epi == EPI_QKV) TSN_LAUNCH((gemm_pipe_hl_kernel<EPI_QKV>), grid, block, 0, st, b);
+            else if (epi == EPI_SWIGLU) TSN_LAUNCH((gemm_pipe_hl_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
+            else { set_error("gemm: unknown epilogue"); return TSN_ERR_ARG; }
+        } else if (epi == EPI_STORE) TSN_LAUNCH((gemm_pipe_kernel<EPI_STORE>), grid, block, 0, st, b);
         else if (epi == EPI_RESID) TSN_LAUNCH((gemm_pipe_kernel<EPI_RESID>), grid, block, 0, st, b);
         else if (epi == EPI_QKV) TSN_LAUNCH((gemm_pipe_kernel<EPI_QKV>), grid, block, 0, st, b);
         else if (epi == EPI_SWIGLU) TSN_LAUNCH((gemm_pipe_kernel<EPI_SWIGLU>), grid, block, 0, st, b);

@@ -88,8 +88,8 @@ int GraphRunner::gemm_run(GemmBatch &b, int epi) {
     double red = 0;
     for (int i = 0; i < b.nprob; ++i)
         if (b.p[i].splits > 1) red += (4.0 * b.p[i].splits + (epi == EPI_RESID ? 8.0 : 4.0)) * b.p[i].M * (double)b.p[i].N;
-    return run(epi == EPI_RESID ? "splitk_reduce_kernel<1>" : "splitk_reduce_kernel<0>", 0, red,
-               [&] { return launch_gemm_reduce(b, epi, st); });
+    if (b.sk) red = 2.0 * b.sk_g * 128 * 128 * 4.0;   // every partial slot read once (upper bound)
+    return run(gemm_reduce_name(b, epi), 0, red, [&] { return launch_gemm_reduce(b, epi, st); });
 }
 
 // Residual GEMM batch followed by one reduce kernel that finishes the split-K sum into X
@@ -100,6 +100,9 @@ int GraphRunner::resid_ln(GemmBatch &b, RedLnArgs &r, int H, float eps) {
     const hipStream_t st = rt->dev.stream();
     TSN_TRY(gemm_plan(b, EPI_RESID, false));
     TSN_TRY(run(b.kname, gemm_flops(b), gemm_bytes(b, EPI_RESID), [&] { return gemm_launch_planned(b, EPI_RESID, false, st); }));
+    if (b.sk)   // stream-K: the fixup applies the residual epilogue to the cut tiles
+        TSN_TRY(run(gemm_reduce_name(b, EPI_RESID), 0, 2.0 * b.sk_g * 128 * 128 * 4.0,
+                    [&] { return launch_gemm_reduce(b, EPI_RESID, st); }));
     r.nseg = b.nprob;
     r.H = H;
     r.eps = eps;
@@ -121,19 +124,20 @@ int GraphRunner::resid_ln(GemmBatch &b, RedLnArgs &r, int H, float eps) {
 
 double gemm_flops(const GemmBatch &b) {
     double f = 0;
-    for (int i = 0; i < b.nprob; ++i) f += 2.0 * b.p[i].M * (double)b.p[i].N * b.p[i].K;
+    for (int i = 0; i < b.nprob; ++i) f += 2.0 * b.p[i].M * (double)b.p[i].N * b.p[i].K / (b.p[i].w_half ? 2 : 1);
     return f;
 }
 
 // A once (conv taps re-read the same rows), W once, output at its storage type (residual: read +
-// write f32; SwiGLU: half the columns)
+// write f32; SwiGLU: half the columns). Flops of a hi|lo operand against half-width W count the
+// model's K (half the K the MFMAs run).
 double gemm_bytes(const GemmBatch &b, int epi) {
     double x = 0;
     for (int i = 0; i < b.nprob; ++i) {
         const GemmProblem &p = b.p[i];
         double out = epi == EPI_RESID ? 8.0 : epi == EPI_SWIGLU ? 1.0 : (p.y_f16 || epi == EPI_QKV ? 2.0 : 4.0);
         if (p.y_lo) out *= 2.0;
-        x += 2.0 * p.M * (double)p.Kc + 2.0 * p.N * (double)p.K + out * p.M * (double)p.N;
+        x += 2.0 * p.M * (double)p.Kc + 2.0 * p.N * (double)p.K / (p.w_half ? 2 : 1) + out * p.M * (double)p.N;
     }
     return x;
 }

@@ -18,6 +18,9 @@ struct GemmProblem {
     // t - pad + k / Kc of the same sample, zero outside [0, a_T). taps = 1, pad = 0 is a GEMM.
     int taps, Kc, pad, a_T;
     const half_t *W; int ldw;          // [N][K] row-major
+    // w_half: the A operand is an f16 hi|lo pair per tap (Kc = 2*IC: hi channels, then lo) and W
+    // holds IC channels per tap ([N][taps][IC], ldw >= taps*IC); both halves read the same W columns
+    int w_half;
     const float *bias;                 // [N] or null
     int M, N, K;
     // EPI_STORE: Y[ymap(m)*ldy + n] = act(acc + bias), f16 or f32
@@ -38,6 +41,7 @@ struct GemmProblem {
     const float *rope;                 // [pos][32][2] (cos, sin)
     // filled by the launcher
     int tile_start, tiles_m, tiles_n;
+    long long unit_start;              // stream-K: first (tile, K tile) unit of this problem
     // split-K (filled by the launcher): splits > 1 writes f32 partials [splits][M][N] at ws, and a
     // second kernel sums them in split order and applies the epilogue
     int splits;
@@ -48,12 +52,19 @@ struct GemmBatch {
     GemmProblem p[3];
     int nprob = 0;
     int total_tiles = 0;
-    // optional f32 workspace for split-K partials (EPI_RESID / EPI_STORE); null disables split-K
+    // optional f32 workspace for split-K partials (EPI_RESID / EPI_STORE) and stream-K partial
+    // tiles (any epilogue); null disables both
     float *ws = nullptr;
     size_t ws_bytes = 0;
     // set by gemm_plan: pipelined kernel chosen, and the symbol of the kernel that will run
     int pipe = 0;
     const char *kname = nullptr;
+    // stream-K schedule (gemm_plan, pipelined kernel with a workspace): sk_g workgroups share the
+    // sk_units (tile, K tile) units evenly; partial tiles go to ws and launch_gemm_reduce finishes
+    // them (gemm_fixup_kernel)
+    int sk = 0, sk_g = 0;
+    long long sk_units = 0;
+    int hl = 0;   // some problem reads half-width W (selects the kernel variant)
 };
 
 // a_f32: A operand is f32 (converted to f16 on load). All problems share the epilogue kind.
@@ -66,6 +77,8 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32);
 int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st);
 int launch_gemm_reduce(const GemmBatch &b, int epi, hipStream_t st);
 bool gemm_needs_reduce(const GemmBatch &b);
+// symbol of the kernel launch_gemm_reduce runs for this batch
+const char *gemm_reduce_name(const GemmBatch &b, int epi);
 void gemm_problem_init(GemmProblem &p);
 
 /* ------------------------------------------------------------------ attention */

@@ -15,6 +15,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 
 namespace tsn {
@@ -105,6 +106,11 @@ std::vector<float> rope_table(int n, float fscale, float base) {
         }
     return tab;
 }
+// A operand as f16 hi|lo pairs against W with half the channels per tap (f32-accurate operand)
+void half_w(GemmProblem &p) {
+    p.w_half = 1;
+    p.ldw = p.taps * p.Kc / 2;
+}
 } // namespace
 
 int RefDitModel::create(Runtime *r, const RefDitSpec &sp) {
@@ -143,7 +149,7 @@ int RefDitModel::create(Runtime *r, const RefDitSpec &sp) {
     TSN_TRY(af(&Vv_, B * T * s.latent));
     TSN_TRY(af(&x2_, B * T * s.latent));
     // split-K partials: up to 8 splits of the largest residual output (B*S x H f32)
-    ws_bytes_ = (size_t)8 * B * S * H * sizeof(float);
+    ws_bytes_ = std::max((size_t)8 * B * S * H * sizeof(float), (size_t)40 << 20);   // split-K / stream-K
     TSN_TRY(alloc(ws_bytes_, (void **)&ws_));
     // latent positions 0..T-1 (fscale 1); clip positions 0..C-1 scaled by T/C (src/dit_fwd.cpp:167-178)
     const std::vector<float> tl = rope_table(s.T, 1.0f, s.rope_theta);
@@ -177,11 +183,11 @@ int RefDitModel::upload_weights(const uint16_t *host, size_t numel) {
     };
     auto new_f16 = [&](size_t n, half_t **p) { return alloc(n * 2, (void **)p); };
     auto new_f32 = [&](size_t n, float **p) { return alloc(n * 4, (void **)p); };
-    // plain copies: f16 [OC][IC] (or tap-major conv; [w | w] per tap when dup), f32 vectors
-    auto f16w = [&](const std::string &n, int OC, int IC, int KT, int dup, const half_t **out) -> int {
+    // plain copies: f16 [OC][IC] (or tap-major conv [OC][KT][IC]), f32 vectors
+    auto f16w = [&](const std::string &n, int OC, int IC, int KT, const half_t **out) -> int {
         half_t *p;
-        TSN_TRY(new_f16((size_t)OC * IC * KT * (dup ? 2 : 1), &p));
-        TSN_TRY(prep(n, OC, IC, KT, dup, 1, 0, 1, 0, p, OC, 0));
+        TSN_TRY(new_f16((size_t)OC * IC * KT, &p));
+        TSN_TRY(prep(n, OC, IC, KT, 0, 1, 0, 1, 0, p, OC, 0));
         *out = p;
         return TSN_OK;
     };
@@ -192,32 +198,31 @@ int RefDitModel::upload_weights(const uint16_t *host, size_t numel) {
         *out = p;
         return TSN_OK;
     };
-    // SwiGLU pair: w1 and w3 [F][IC][KT] -> [2F][KT][IC] ([2F][KT][2IC] = [w | w] when dup),
-    // 64-row blocks w1 j, w3 j
-    auto swiglu_w = [&](const std::string &p, int IC, int KT, int dup, const half_t **out) -> int {
+    // SwiGLU pair: w1 and w3 [F][IC][KT] -> [2F][KT][IC], 64-row blocks w1 j, w3 j
+    auto swiglu_w = [&](const std::string &p, int IC, int KT, const half_t **out) -> int {
         half_t *w;
-        TSN_TRY(new_f16((size_t)2 * F * IC * KT * (dup ? 2 : 1), &w));
-        TSN_TRY(prep(p + ".w1.weight", F, IC, KT, dup, 64, 1, 128, 0, w, 2LL * F, 0));
-        TSN_TRY(prep(p + ".w3.weight", F, IC, KT, dup, 64, 1, 128, 64, w, 2LL * F, 0));
+        TSN_TRY(new_f16((size_t)2 * F * IC * KT, &w));
+        TSN_TRY(prep(p + ".w1.weight", F, IC, KT, 0, 64, 1, 128, 0, w, 2LL * F, 0));
+        TSN_TRY(prep(p + ".w3.weight", F, IC, KT, 0, 64, 1, 128, 64, w, 2LL * F, 0));
         *out = w;
         return TSN_OK;
     };
     half_t *wmodl;
     float *bmodl, *bmodg;
     uint16_t *wmodg;
-    TSN_TRY(new_f16((size_t)NMODL * 2 * H, &wmodl));
+    TSN_TRY(new_f16((size_t)NMODL * H, &wmodl));
     TSN_TRY(new_f32(NMODL, &bmodl));
     TSN_TRY(alloc((size_t)NMODG * H * 2, (void **)&wmodg));
     TSN_TRY(new_f32(NMODG, &bmodg));
     int rowl = 0, rowg = 0;
-    // per-row modulation weights gathered as f16 [W | W] rows of one GEMM over the hi|lo operand;
-    // per-sample ones as bf16 GEMV rows
+    // per-row modulation weights gathered as f16 rows of one GEMM (read by both halves of the hi|lo
+    // operand); per-sample ones as bf16 GEMV rows
     auto mod_rows = [&](const std::string &p, int chunks, bool per_row, int *off) -> int {
         const std::string wn = p + ".adaLN_modulation.1.weight", bn = p + ".adaLN_modulation.1.bias";
         TSN_REQUIRE(idx.at(wn)->numel == (int64_t)chunks * H * H, "refdit: adaLN size: " + p);
         if (per_row) {
             *off = rowl;
-            TSN_TRY(prep(wn, chunks * H, H, 1, 1, 1, 0, 1, rowl, wmodl, NMODL, 0));
+            TSN_TRY(prep(wn, chunks * H, H, 1, 0, 1, 0, 1, rowl, wmodl, NMODL, 0));
             TSN_TRY(prep(bn, chunks * H, 1, 1, 0, 1, 0, 1, rowl, bmodl, NMODL, 1));
             rowl += chunks * H;
         } else {
@@ -245,10 +250,10 @@ int RefDitModel::upload_weights(const uint16_t *host, size_t numel) {
         w.post = post ? 1 : 0;
         w.hl = per_row ? 1 : 0;   // latent rows: out-proj and FFN over hi|lo operands
         if (!post) return TSN_OK;
-        TSN_TRY(f16w(p + ".linear1.weight", H, H, taps, w.hl, &w.Wo));
+        TSN_TRY(f16w(p + ".linear1.weight", H, H, taps, &w.Wo));
         TSN_TRY(f32v(p + ".linear1.bias", H, &w.bo));
-        TSN_TRY(swiglu_w(p + ".ffn", H, taps, w.hl, &w.W13));
-        TSN_TRY(f16w(p + ".ffn.w2.weight", H, F, taps, w.hl, &w.W2));
+        TSN_TRY(swiglu_w(p + ".ffn", H, taps, &w.W13));
+        TSN_TRY(f16w(p + ".ffn.w2.weight", H, F, taps, &w.W2));
         return TSN_OK;
     };
     jl_.assign(s.n_joint, StreamW{});
@@ -273,20 +278,13 @@ int RefDitModel::upload_weights(const uint16_t *host, size_t numel) {
     Wt2_ = raw("t_embed.mlp.2.weight");
     TSN_TRY(f32v("t_embed.mlp.0.bias", H, &bt0_));
     TSN_TRY(f32v("t_embed.mlp.2.bias", H, &bt2_));
-    // input conv [H][L][3] and final conv [L][H][7] as tap-major [w | w] for hi|lo operands
-    {
-        half_t *w;
-        TSN_TRY(new_f16((size_t)H * 3 * 2 * L, &w));
-        TSN_TRY(prep("audio_input_proj.0.weight", H, L, 3, 1, 1, 0, 1, 0, w, H, 0));
-        Win_ = w;
-        TSN_TRY(new_f16((size_t)L * 7 * 2 * H, &w));
-        TSN_TRY(prep("final_layer.conv.weight", L, H, 7, 1, 1, 0, 1, 0, w, L, 0));
-        Wfin_ = w;
-    }
+    // input conv [H][L][3] and final conv [L][H][7], tap-major
+    TSN_TRY(f16w("audio_input_proj.0.weight", H, L, 3, &Win_));
+    TSN_TRY(f16w("final_layer.conv.weight", L, H, 7, &Wfin_));
     TSN_TRY(f32v("audio_input_proj.0.bias", H, &bin_));
     TSN_TRY(f32v("final_layer.conv.bias", L, &bfin_));
-    TSN_TRY(swiglu_w("audio_input_proj.2", H, 3, 1, &W13in_));
-    TSN_TRY(f16w("audio_input_proj.2.w2.weight", H, F, 3, 1, &W2in_));
+    TSN_TRY(swiglu_w("audio_input_proj.2", H, 3, &W13in_));
+    TSN_TRY(f16w("audio_input_proj.2.w2.weight", H, F, 3, &W2in_));
     TSN_TRY(rt->dev.sync());
     ready_ = true;
     return TSN_OK;
@@ -361,6 +359,8 @@ int RefDitModel::block_joint(int i, bool ln1, Next next) {
                     m.L, soff[k], rlen[k], rope[k], s.rms_eps);
         qb.p[k].lda = 2 * H;   // hi halves of the XN rows
     }
+    qb.ws = ws_;
+    qb.ws_bytes = ws_bytes_;
     TSN_TRY(gemm_run(qb, EPI_QKV));
 
     AttnArgs at;
@@ -383,6 +383,7 @@ int RefDitModel::block_joint(int i, bool ln1, Next next) {
         resid_problem(ob.p[k], AO_, 2 * H, m, w[k]->taps, w[k]->hl ? 2 * H : H, B * m.L, H, w[k]->Wo, w[k]->bo, X_, H,
                       (lat ? MODL_ : modg_) + w[k]->mod_off + 2 * H, lat ? NMODL : NMODG);
         if (lat) ob.p[k].gate_L = 1;   // gate per latent row
+        if (w[k]->hl) half_w(ob.p[k]);
     }
     RedLnArgs r;
     next_ln(r, Next{NEXT_JOINT, i}, kinds, np, true);   // LN2 of this block
@@ -395,7 +396,10 @@ int RefDitModel::block_joint(int i, bool ln1, Next next) {
         store_problem(f1.p[k], XN_, 2 * H, m, w[k]->taps, w[k]->hl ? 2 * H : H, B * m.L, 2 * s.F, w[k]->W13, HF_,
                       2 * s.F, 0);
         f1.p[k].y_lo = w[k]->hl ? s.F : 0;
+        if (w[k]->hl) half_w(f1.p[k]);
     }
+    f1.ws = ws_;
+    f1.ws_bytes = ws_bytes_;
     TSN_TRY(gemm_run(f1, EPI_SWIGLU));
 
     GemmBatch f2;
@@ -408,6 +412,7 @@ int RefDitModel::block_joint(int i, bool ln1, Next next) {
         resid_problem(f2.p[k], HF_, 2 * s.F, m, w[k]->taps, w[k]->hl ? 2 * s.F : s.F, B * m.L, H, w[k]->W2, nullptr,
                       X_, H, (lat ? MODL_ : modg_) + w[k]->mod_off + 5 * H, lat ? NMODL : NMODG);
         if (lat) f2.p[k].gate_L = 1;
+        if (w[k]->hl) half_w(f2.p[k]);
     }
     next_ln(r, next, kinds, np);
     return resid_ln(f2, r, H, s.ln_eps);
@@ -432,6 +437,8 @@ int RefDitModel::block_fused(int i, bool ln1, Next next) {
     qkv_problem(qb.p[0], XN_, Lm, M, w.Wqkv, w.bqkv, w.qn, w.kn, H, s.NH, Q_, K_, VtF_, T, SpF, T, 0, T, rope_l_,
                 s.rms_eps);
     qb.p[0].lda = 2 * H;
+    qb.ws = ws_;
+    qb.ws_bytes = ws_bytes_;
     TSN_TRY(gemm_run(qb, EPI_QKV));
 
     AttnArgs at;
@@ -448,6 +455,7 @@ int RefDitModel::block_fused(int i, bool ln1, Next next) {
     ob.ws_bytes = ws_bytes_;
     resid_problem(ob.p[0], AO_, 2 * H, Lm, w.taps, 2 * H, M, H, w.Wo, w.bo, X_, H, MODL_ + w.mod_off + 2 * H, NMODL);
     ob.p[0].gate_L = 1;
+    half_w(ob.p[0]);
     RedLnArgs r;
     next_ln(r, Next{NEXT_FUSED, i}, kinds, 1, true);   // LN2 of this block
     TSN_TRY(resid_ln(ob, r, H, s.ln_eps));
@@ -456,6 +464,9 @@ int RefDitModel::block_fused(int i, bool ln1, Next next) {
     f1.nprob = 1;
     store_problem(f1.p[0], XN_, 2 * H, Lm, w.taps, 2 * H, M, 2 * s.F, w.W13, HF_, 2 * s.F, 0);
     f1.p[0].y_lo = s.F;
+    half_w(f1.p[0]);
+    f1.ws = ws_;
+    f1.ws_bytes = ws_bytes_;
     TSN_TRY(gemm_run(f1, EPI_SWIGLU));
 
     GemmBatch f2;
@@ -465,6 +476,7 @@ int RefDitModel::block_fused(int i, bool ln1, Next next) {
     resid_problem(f2.p[0], HF_, 2 * s.F, Lm, w.taps, 2 * s.F, M, H, w.W2, nullptr, X_, H, MODL_ + w.mod_off + 5 * H,
                   NMODL);
     f2.p[0].gate_L = 1;
+    half_w(f2.p[0]);
     next_ln(r, next, kinds, 1);
     return resid_ln(f2, r, H, s.ln_eps);
 }
@@ -540,8 +552,11 @@ int RefDitModel::enqueue_eval(const float *x, const float *t, const float *clip_
         GemmProblem &p = mb.p[0];
         gemm_problem_init(p);
         p.A = XE_; p.lda = 2 * H; p.amap = rowmap_dense(B * T); p.taps = 1; p.Kc = 2 * H; p.a_T = B * T;
-        p.W = WmodL_; p.ldw = 2 * H; p.bias = bmodL_; p.M = B * T; p.N = NMODL; p.K = 2 * H;
+        p.W = WmodL_; p.bias = bmodL_; p.M = B * T; p.N = NMODL; p.K = 2 * H;
         p.Y = MODL_; p.ldy = NMODL; p.ymap = rowmap_dense(B * T); p.y_f16 = 0;
+        half_w(p);
+        mb.ws = ws_;
+        mb.ws_bytes = ws_bytes_;
         TSN_TRY(gemm_run(mb, EPI_STORE));
     }
     // input projection (src/dit_fwd.cpp:142-149): conv k3 over x as f16 hi|lo against [W|W]
@@ -555,11 +570,17 @@ int RefDitModel::enqueue_eval(const float *x, const float *t, const float *clip_
         store_problem(ib.p[0], Z2_, 2 * L, D, 3, 2 * L, B * T, H, Win_, XN_, 2 * H, 1);
         ib.p[0].bias = bin_;
         ib.p[0].y_lo = H;
+        half_w(ib.p[0]);
+        ib.ws = ws_;
+        ib.ws_bytes = ws_bytes_;
         TSN_TRY(gemm_run(ib, EPI_STORE));
         GemmBatch sb;
         sb.nprob = 1;
         store_problem(sb.p[0], XN_, 2 * H, D, 3, 2 * H, B * T, 2 * s.F, W13in_, HF_, 2 * s.F, 0);
         sb.p[0].y_lo = s.F;
+        half_w(sb.p[0]);
+        sb.ws = ws_;
+        sb.ws_bytes = ws_bytes_;
         TSN_TRY(gemm_run(sb, EPI_SWIGLU));
         GemmBatch ob;
         ob.nprob = 1;
@@ -567,6 +588,7 @@ int RefDitModel::enqueue_eval(const float *x, const float *t, const float *clip_
         ob.ws_bytes = ws_bytes_;
         store_problem(ob.p[0], HF_, 2 * s.F, D, 3, 2 * s.F, B * T, H, W2in_, nullptr, 0, 0);
         ob.p[0].Y = X_; ob.p[0].ldy = H; ob.p[0].ymap = stream_map(ST_LAT); ob.p[0].y_f16 = 0;
+        half_w(ob.p[0]);
         TSN_TRY(gemm_run(ob, EPI_STORE));
     }
     // clip and text streams start from the prepared features every evaluation (src/dit_fwd.cpp:162-163)
@@ -609,6 +631,7 @@ int RefDitModel::enqueue_eval(const float *x, const float *t, const float *clip_
     store_problem(fb.p[0], XF2_, 2 * H, D, 7, 2 * H, B * T, L, Wfin_, nullptr, 0, 0);
     fb.p[0].bias = bfin_;
     fb.p[0].Y = v; fb.p[0].ldy = L; fb.p[0].ymap = D; fb.p[0].y_f16 = 0;
+    half_w(fb.p[0]);
     return gemm_run(fb, EPI_STORE);
 }
 

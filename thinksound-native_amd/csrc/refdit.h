@@ -20,8 +20,8 @@
 //   Q,K  f16 [B][NH][S][64], Vt f16 [B][NH][64][Sp] (joint); VtF [B][NH][64][SpF] (fused, S = T)
 //   AO   f16 [B][S][2H]      attention output as hi|lo
 //   HF   f16 [B][S][2F]      SwiGLU hidden, hi|lo for latent rows
-// The latent stream's out-proj and FFN GEMMs read hi|lo operands against [w | w] weights (f32-
-// accurate operands); the clip and text streams read the hi halves only.
+// The latent stream's out-proj and FFN GEMMs read hi|lo operands, each half against the same
+// weight columns (f32-accurate operands); the clip and text streams read the hi halves only.
 #pragma once
 #include <vector>
 
@@ -80,7 +80,7 @@ private:
         int taps = 1;      // 3: conv k3 out-proj and FFN, 1: linear
         int post = 1;      // 0: pre-only stream (no out-proj, no FFN)
         int mod_off = 0;   // first modulation column (MODL for latent/fused, MODG for clip/text)
-        int hl = 0;        // out-proj / FFN weights as [w | w] per tap for hi|lo operands (latent rows)
+        int hl = 0;        // out-proj / FFN GEMMs over hi|lo operands (latent rows), half-width W
     };
     enum { NEXT_NONE = 0, NEXT_JOINT = 1, NEXT_FUSED = 2, NEXT_FINAL = 3 };
     enum { ST_LAT = 0, ST_CLIP = 1, ST_TEXT = 2 };
@@ -98,7 +98,7 @@ private:
     void next_ln(RedLnArgs &r, Next next, const int *kinds, int nseg, bool ln2 = false);
 
     std::vector<StreamW> jl_, jc_, jt_, fu_;
-    const half_t *WmodL_ = nullptr;                       // [NMODL][2H] f16 [W | W]
+    const half_t *WmodL_ = nullptr;                       // [NMODL][H] f16
     const uint16_t *WmodG_ = nullptr, *Wt0_ = nullptr, *Wt2_ = nullptr;   // bf16 GEMV weights
     const float *bmodL_ = nullptr, *bmodG_ = nullptr, *bt0_ = nullptr, *bt2_ = nullptr;
     const half_t *Win_ = nullptr, *W13in_ = nullptr, *W2in_ = nullptr, *Wfin_ = nullptr;

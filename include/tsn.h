@@ -198,6 +198,15 @@ int tsn_refdit_destroy(tsn_refdit *dit);
  * qkv row de-interleave (replaces qkv_split3, src/dit_fwd.cpp:33-36), conv [OC][IC][K] -> [OC][K][IC],
  * BF16 -> FP16 */
 int tsn_refdit_upload_weights(tsn_refdit *dit, const uint16_t *weights_host, size_t numel);
+/* the same from an f32 buffer (dequantized checkpoint tensors, manifest order) */
+int tsn_refdit_upload_weights_f32(tsn_refdit *dit, const float *weights_host, size_t numel);
+/* DitModel::load (src/dit.cpp:29-47) + WeightSet::load (src/net.mm:126-173): every tensor of the
+ * manifest looked up by name in a GGUF file, dequantized on the host (F32, F16, BF16, Q8_0), GEMM and
+ * GEMV weights converted to f16 with the reference's rounding (src/net.mm:144-164) */
+int tsn_refdit_load_gguf(tsn_refdit *dit, const char *path);
+/* hyperparameters from the checkpoint's dit.* metadata and the SwiGLU width from the first latent
+ * FFN weight (src/dit.cpp:32-43); B, T, C, TS are the caller's geometry */
+int tsn_refdit_spec_from_gguf(const char *path, int B, int T, int C, int TS, tsn_refdit_spec *out);
 /* DitModel::forward (src/models.h:83-84, src/dit_fwd.cpp:104-304) with the arms batched:
  * x [B][T][latent], clip_pp [B][C][H], text_pp [B][TS][H], gcmlp [B][H], sync_gather [B][T][H]
  * -> flow [B][T][latent]; every sample at flow time t. Enqueued; tsn_sync before reading flow. */
@@ -219,6 +228,20 @@ int tsn_refdit_replay(tsn_refdit *dit);
 int tsn_refdit_profile_forward(tsn_refdit *dit, const float *x, const float *t, const float *clip_pp,
                                const float *text_pp, const float *gcmlp, const float *sync_gather, float *flow,
                                tsn_kernel_stat *stats, int cap, int *n_stats);
+
+/* ---------------- GGUF checkpoint reader: tn::GgufFile / tn::to_f32 (src/gguf.h:42-86) ----------------
+ * mmap, GGUF v2/v3, typed metadata, tensor infos with ne[0] fastest, data at general.alignment. */
+typedef struct tsn_gguf tsn_gguf;
+int tsn_gguf_open(const char *path, tsn_gguf **out);                 /* GgufFile::open src/gguf.h:48 */
+int tsn_gguf_close(tsn_gguf *g);                                     /* GgufFile::~GgufFile src/gguf.h:47 */
+int tsn_gguf_tensor_count(const tsn_gguf *g);                        /* GgufFile::n_tensors src/gguf.h:59 */
+/* name, GGML type (0 F32, 1 F16, 8 Q8_0, 30 BF16), n_dims, ne[4] (GgufTensor, src/gguf.h:32-40) */
+int tsn_gguf_tensor_info(const tsn_gguf *g, int idx, char *name, int name_cap, uint32_t *type, uint32_t *n_dims,
+                         uint64_t *ne4);
+/* to_f32 (src/gguf.h:85): F16 and Q8_0 scales with subnormals flushed to zero, as the reference */
+int tsn_gguf_tensor_to_f32(const tsn_gguf *g, const char *name, float *out_host, size_t cap);
+int64_t tsn_gguf_get_i64(const tsn_gguf *g, const char *key, int64_t def);   /* GgufFile::get_i64 src/gguf.h:53 */
+double tsn_gguf_get_f64(const tsn_gguf *g, const char *key, double def);    /* GgufFile::get_f64 src/gguf.h:54 */
 
 /* ---------------- synthetic data (specified generator; see thinksound-native_amd/csrc/synth.cpp) ---------------- */
 int tsn_synth_normal_f32(uint64_t seed, uint64_t index, double mean, double std, size_t n, float *out_host);

@@ -7,7 +7,9 @@ TS = 154 text rows, H = 1024, SwiGLU F = 2816, 7 joint + 14 fused blocks):
   * structure, bit-exact: the pre-only last joint block and the fused blocks leave the clip and
     text rows untouched; samples do not mix;
   * bit-identical reruns, eager and hipGraph replay (with eager work between replays);
-  * the CFG Euler sampler (2 steps): displacement x - x0 rel-L2 <= 2e-3, graph replay bit-identical.
+  * the CFG Euler sampler (2 steps): displacement x - x0 rel-L2 <= 2e-3, graph replay bit-identical;
+  * real-weight mode: a small GGUF checkpoint with F32, F16, BF16 and Q8_0 tensors loads by name
+    and its velocity matches the oracle on the decoded weights (rel-L2 <= 1e-3).
 
 Tolerances are the north-star bars (f16 MFMA operands, f32 accumulation and residual streams).
 """
@@ -118,3 +120,50 @@ def test_ref_sampler_two_steps(tsn, rt, orc, ref):
     m.replay()
     rt.sync()
     assert np.array_equal(out.view(np.uint32), x2.numpy().view(np.uint32))
+
+
+def test_ref_gguf_checkpoint(tsn, rt, orc, tmp_path):
+    """A small checkpoint written as GGUF with every tensor type the reader takes (F32 vectors, F16,
+    BF16 and Q8_0 matrices, conv weights as (K, IC, OC) dims) goes through tsn_refdit_spec_from_gguf
+    and tsn_refdit_load_gguf; the velocity matches the oracle run on the reader's own decoded
+    weights (rel-L2 <= 1e-3), so names, shapes, dequantization and every upload-time layout agree."""
+    import gguf_writer as gw
+    from conftest import rng
+    geo = dict(B=2, T=20, C=8, TS=12)
+    spec_d = dict(geo, H=256, NH=4, HD=64, F=128, latent=64, n_joint=2, n_fused=1, rope_theta=10000.0,
+                  t_max_period=1.0, ln_eps=1e-5, rms_eps=1e-6)
+    man = orc.ref_manifest(spec_d)
+    r = rng(11)
+    tensors = []
+    for i, (name, n, _) in enumerate(man):
+        ne = gw.ref_ne(name, n, spec_d)
+        vals = ((1.0 if "norm.weight" in name else 0.0) + 0.05 * r.standard_normal(n)).astype(np.float32)
+        if len(ne) == 1:
+            ty = gw.F32
+        elif ne[0] % 32 == 0 and i % 3 == 0:
+            ty = gw.Q8_0
+        else:
+            ty = (gw.F16, gw.BF16)[i % 2]
+        tensors.append((name, ne, ty, vals))
+    meta = [("dit.hidden_dim", gw.KV_U32, 256), ("dit.num_heads", gw.KV_U32, 4), ("dit.depth", gw.KV_U32, 3),
+            ("dit.fused_depth", gw.KV_U32, 1), ("dit.latent_dim", gw.KV_U32, 64)]
+    path = str(tmp_path / "tiny.gguf")
+    dec = gw.write(path, tensors, meta)
+    assert {t for _, _, t, _ in tensors} == {gw.F32, gw.F16, gw.BF16, gw.Q8_0}
+    spec = tsn.ref_spec_from_gguf(path, **geo)
+    assert spec.as_dict() == pytest.approx(spec_d)
+    m = tsn.RefDitModel(rt, spec)
+    try:
+        m.load_gguf(path)
+        w32 = np.concatenate([dec[name] for name, _, _ in man])
+        inp = tsn.ref_synth_inputs(spec, 4242)
+        dev = {k: rt.array(v) for k, v in inp.items()}
+        v = rt.empty((spec.B, spec.T, spec.latent))
+        m.forward_ex(dev["x"], dev["t"], dev["clip_pp"], dev["text_pp"], dev["gcmlp"], dev["sync_gather"], v)
+        rt.sync()
+        vr = orc.ref_dit_forward(spec_d, w32, **inp)
+        err = rel_l2(v.numpy(), vr)
+        print("gguf checkpoint velocity rel-L2 %.3g" % err)
+        assert err <= 1e-3
+    finally:
+        m.close()

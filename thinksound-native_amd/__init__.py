@@ -140,10 +140,21 @@ _SIGS = {
     "tsn_refdit_profile_forward": [_P, _P, _P, _P, _P, _P, _P, _P, ctypes.POINTER(KernelStat), _I,
                                    ctypes.POINTER(_I)],
     "tsn_refdit_synth_weights": [ctypes.POINTER(RefDitSpec), ctypes.c_uint64, ctypes.c_double, _P],
+    "tsn_refdit_upload_weights_f32": [_P, _P, _SZ],
+    "tsn_refdit_load_gguf": [_P, ctypes.c_char_p],
+    "tsn_refdit_spec_from_gguf": [ctypes.c_char_p, _I, _I, _I, _I, ctypes.POINTER(RefDitSpec)],
+    "tsn_gguf_open": [ctypes.c_char_p, ctypes.POINTER(_P)],
+    "tsn_gguf_close": [_P],
+    "tsn_gguf_tensor_count": [_P],
+    "tsn_gguf_tensor_info": [_P, _I, ctypes.c_char_p, _I, ctypes.POINTER(ctypes.c_uint32),
+                             ctypes.POINTER(ctypes.c_uint32), ctypes.POINTER(ctypes.c_uint64)],
+    "tsn_gguf_tensor_to_f32": [_P, ctypes.c_char_p, _P, _SZ],
+    "tsn_gguf_get_i64": [_P, ctypes.c_char_p, ctypes.c_int64],
+    "tsn_gguf_get_f64": [_P, ctypes.c_char_p, ctypes.c_double],
 }
 _RESTYPES = {"tsn_last_error": ctypes.c_char_p, "tsn_last_gpu_ms": ctypes.c_double,
              "tsn_dit_manifest_total": ctypes.c_int64, "tsn_refdit_manifest_total": ctypes.c_int64,
-             "tsn_version": _I}
+             "tsn_gguf_get_i64": ctypes.c_int64, "tsn_gguf_get_f64": ctypes.c_double, "tsn_version": _I}
 
 
 def lib():
@@ -253,6 +264,47 @@ def ref_synth_weights(spec, seed=4242, norm_mean=0.0):
     w = np.empty(ref_manifest_total(spec), np.uint16)
     call("tsn_refdit_synth_weights", ctypes.byref(spec), seed, norm_mean, ptr(w))
     return w
+
+
+def ref_spec_from_gguf(path, B=2, T=172, C=64, TS=154):
+    """tsn_refdit_spec_from_gguf: hyperparameters from a checkpoint, geometry from the caller."""
+    s = RefDitSpec()
+    call("tsn_refdit_spec_from_gguf", os.fsencode(path), B, T, C, TS, ctypes.byref(s))
+    return s
+
+
+class Gguf:
+    """tsn_gguf_* reader: tensors (name, type, shape ne[0] fastest), metadata, host dequantization."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        call("tsn_gguf_open", os.fsencode(path), ctypes.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().tsn_gguf_close(self.h)
+            self.h = None
+
+    def tensors(self):
+        L = lib()
+        out, buf = [], ctypes.create_string_buffer(256)
+        ty, nd, ne = ctypes.c_uint32(), ctypes.c_uint32(), (ctypes.c_uint64 * 4)()
+        for i in range(L.tsn_gguf_tensor_count(self.h)):
+            call("tsn_gguf_tensor_info", self.h, i, buf, 256, ctypes.byref(ty), ctypes.byref(nd), ne)
+            out.append((buf.value.decode(), ty.value, tuple(ne[d] for d in range(nd.value))))
+        return out
+
+    def to_f32(self, name, numel):
+        a = np.empty(numel, np.float32)
+        call("tsn_gguf_tensor_to_f32", self.h, name.encode(), ptr(a), a.size)
+        return a
+
+    def get_i64(self, key, default=0):
+        return int(lib().tsn_gguf_get_i64(self.h, key.encode(), default))
+
+    def get_f64(self, key, default=0.0):
+        return float(lib().tsn_gguf_get_f64(self.h, key.encode(), default))
 
 
 def bf16_to_f32(u16):
@@ -459,6 +511,13 @@ class RefDitModel:
     def upload_weights(self, w_bf16):
         w_bf16 = np.ascontiguousarray(w_bf16, dtype=np.uint16)
         call("tsn_refdit_upload_weights", self.h, ptr(w_bf16), w_bf16.size)
+
+    def upload_weights_f32(self, w):
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        call("tsn_refdit_upload_weights_f32", self.h, ptr(w), w.size)
+
+    def load_gguf(self, path):
+        call("tsn_refdit_load_gguf", self.h, os.fsencode(path))
 
     def forward(self, x, t, clip_pp, text_pp, gcmlp, sync_gather, flow):
         call("tsn_refdit_forward", self.h, x.p, float(t), _p(clip_pp), _p(text_pp), gcmlp.p, sync_gather.p, flow.p)

@@ -6,6 +6,7 @@
 #include <new>
 
 #include "dit.h"
+#include "gguf.h"
 #include "refdit.h"
 
 namespace tsn {
@@ -22,6 +23,9 @@ struct tsn_dit {
 };
 struct tsn_refdit {
     tsn::RefDitModel m;
+};
+struct tsn_gguf {
+    tsn::GgufReader r;
 };
 
 #define RT_CHECK(r)                                                 \
@@ -293,6 +297,68 @@ int tsn_refdit_upload_weights(tsn_refdit *d, const uint16_t *w, size_t numel) {
     REF_CHECK(d);
     return d->m.upload_weights(w, numel);
 }
+int tsn_refdit_upload_weights_f32(tsn_refdit *d, const float *w, size_t numel) {
+    REF_CHECK(d);
+    return d->m.upload_weights_f32(w, numel);
+}
+int tsn_refdit_load_gguf(tsn_refdit *d, const char *path) {
+    REF_CHECK(d);
+    if (!path) { tsn::set_error("null path"); return TSN_ERR_ARG; }
+    return d->m.load_gguf(path);
+}
+int tsn_refdit_spec_from_gguf(const char *path, int B, int T, int C, int TS, tsn_refdit_spec *out) {
+    if (!path || !out) { tsn::set_error("null path or spec"); return TSN_ERR_ARG; }
+    tsn::RefDitSpec s;
+    TSN_TRY(tsn::refdit_spec_from_gguf(path, B, T, C, TS, &s));
+    out->B = s.B; out->T = s.T; out->C = s.C; out->TS = s.TS; out->H = s.H; out->NH = s.NH; out->HD = s.HD;
+    out->F = s.F; out->latent = s.latent; out->n_joint = s.n_joint; out->n_fused = s.n_fused;
+    out->rope_theta = s.rope_theta; out->t_max_period = s.t_max_period; out->ln_eps = s.ln_eps; out->rms_eps = s.rms_eps;
+    return TSN_OK;
+}
+
+/* ---------------- GGUF reader ---------------- */
+int tsn_gguf_open(const char *path, tsn_gguf **out) {
+    if (!path || !out) { tsn::set_error("null path or out pointer"); return TSN_ERR_ARG; }
+    *out = nullptr;
+    tsn_gguf *g = new (std::nothrow) tsn_gguf();
+    if (!g) { tsn::set_error("out of host memory"); return TSN_ERR_OOM; }
+    const int rc = g->r.open(path);
+    if (rc != TSN_OK) { delete g; return rc; }
+    *out = g;
+    return TSN_OK;
+}
+int tsn_gguf_close(tsn_gguf *g) { delete g; return TSN_OK; }
+int tsn_gguf_tensor_count(const tsn_gguf *g) {
+    if (!g) { tsn::set_error("null gguf handle"); return -1; }
+    return (int)g->r.tensors().size();
+}
+int tsn_gguf_tensor_info(const tsn_gguf *g, int idx, char *name, int name_cap, uint32_t *type, uint32_t *n_dims,
+                         uint64_t *ne4) {
+    if (!g) { tsn::set_error("null gguf handle"); return TSN_ERR_ARG; }
+    const auto &v = g->r.tensors();
+    if (idx < 0 || idx >= (int)v.size()) { tsn::set_error("tensor index out of range"); return TSN_ERR_ARG; }
+    const tsn::GgufTensorInfo &t = v[idx];
+    if (name && name_cap > 0) snprintf(name, (size_t)name_cap, "%s", t.name.c_str());
+    if (type) *type = t.type;
+    if (n_dims) *n_dims = t.n_dims;
+    if (ne4)
+        for (int d = 0; d < 4; ++d) ne4[d] = t.ne[d];
+    return TSN_OK;
+}
+int tsn_gguf_tensor_to_f32(const tsn_gguf *g, const char *name, float *out, size_t cap) {
+    if (!g || !name || !out) { tsn::set_error("null argument"); return TSN_ERR_ARG; }
+    const tsn::GgufTensorInfo *t = g->r.find(name);
+    if (!t) { tsn::set_error(std::string("gguf: no tensor ") + name); return TSN_ERR_ARG; }
+    if (cap < t->numel()) { tsn::set_error("gguf: output too small"); return TSN_ERR_ARG; }
+    return g->r.to_f32(*t, out);
+}
+int64_t tsn_gguf_get_i64(const tsn_gguf *g, const char *key, int64_t def) {
+    return g && key ? g->r.get_i64(key, def) : def;
+}
+double tsn_gguf_get_f64(const tsn_gguf *g, const char *key, double def) {
+    return g && key ? g->r.get_f64(key, def) : def;
+}
+
 int tsn_refdit_forward(tsn_refdit *d, const float *x, float t, const float *clip_pp, const float *text_pp,
                        const float *gcmlp, const float *sync_gather, float *flow) {
     REF_CHECK(d);

@@ -1,0 +1,220 @@
+// gguf.cpp — GgufReader: mmap, header / metadata / tensor-info parse, host dequantization.
+#include "gguf.h"
+
+#include <fcntl.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include "tsn_common.h"
+
+namespace tsn {
+
+namespace {
+
+constexpr uint32_t MAGIC = 0x46554747u;   // "GGUF" read as little-endian u32
+
+// metadata value types of the GGUF format
+enum : uint32_t {
+    KV_U8 = 0, KV_I8 = 1, KV_U16 = 2, KV_I16 = 3, KV_U32 = 4, KV_I32 = 5, KV_F32 = 6, KV_BOOL = 7,
+    KV_STRING = 8, KV_ARRAY = 9, KV_U64 = 10, KV_I64 = 11, KV_F64 = 12
+};
+
+// bounds-checked little-endian cursor over the mapping
+struct Cursor {
+    const uint8_t *p, *end;
+    bool ok = true;
+    bool take(void *dst, size_t n) {
+        if (!ok || (size_t)(end - p) < n) return ok = false;
+        if (dst) memcpy(dst, p, n);
+        p += n;
+        return true;
+    }
+    template <typename T>
+    T get() {
+        T v{};
+        take(&v, sizeof v);
+        return v;
+    }
+    std::string str() {
+        const uint64_t n = get<uint64_t>();
+        if (!ok || n > (uint64_t)(end - p)) { ok = false; return {}; }
+        std::string s((const char *)p, (size_t)n);
+        p += n;
+        return s;
+    }
+};
+
+size_t scalar_size(uint32_t t) {
+    switch (t) {
+    case KV_U8: case KV_I8: case KV_BOOL: return 1;
+    case KV_U16: case KV_I16: return 2;
+    case KV_U32: case KV_I32: case KV_F32: return 4;
+    case KV_U64: case KV_I64: case KV_F64: return 8;
+    default: return 0;
+    }
+}
+
+} // namespace
+
+float f16_bits_to_f32_ftz(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1F, m = h & 0x3FF;
+    uint32_t f;
+    if (e == 0) f = sign;                                  // zero and subnormals -> signed zero
+    else if (e == 31) f = sign | 0x7F800000u | (m << 13);  // inf / nan
+    else f = sign | ((e + 112) << 23) | (m << 13);        // rebias 15 -> 127
+    float out;
+    memcpy(&out, &f, 4);
+    return out;
+}
+
+GgufReader::~GgufReader() {
+    if (map_) munmap(map_, len_);
+    if (fd_ >= 0) close(fd_);
+}
+
+int GgufReader::open(const char *path) {
+    TSN_REQUIRE(path && !map_, "gguf: null path or already open");
+    fd_ = ::open(path, O_RDONLY);
+    TSN_REQUIRE(fd_ >= 0, std::string("gguf: cannot open ") + path);
+    struct stat st;
+    TSN_REQUIRE(fstat(fd_, &st) == 0 && st.st_size > 24, std::string("gguf: not a GGUF file: ") + path);
+    len_ = (size_t)st.st_size;
+    void *m = mmap(nullptr, len_, PROT_READ, MAP_PRIVATE, fd_, 0);
+    TSN_REQUIRE(m != MAP_FAILED, std::string("gguf: mmap failed: ") + path);
+    map_ = m;
+    return parse();
+}
+
+int GgufReader::parse() {
+    Cursor c{(const uint8_t *)map_, (const uint8_t *)map_ + len_};
+    TSN_REQUIRE(c.get<uint32_t>() == MAGIC, "gguf: bad magic");
+    version_ = c.get<uint32_t>();
+    TSN_REQUIRE(version_ == 2 || version_ == 3, "gguf: only versions 2 and 3 are read");
+    const uint64_t n_tensors = c.get<uint64_t>(), n_kv = c.get<uint64_t>();
+    TSN_REQUIRE(c.ok && n_tensors < (1u << 24) && n_kv < (1u << 24), "gguf: truncated header");
+    for (uint64_t i = 0; i < n_kv; ++i) {
+        const std::string key = c.str();
+        Kv v;
+        v.type = c.get<uint32_t>();
+        switch (v.type) {
+        case KV_U8: v.i = c.get<uint8_t>(); break;
+        case KV_I8: v.i = c.get<int8_t>(); break;
+        case KV_BOOL: v.i = c.get<uint8_t>() != 0; break;
+        case KV_U16: v.i = c.get<uint16_t>(); break;
+        case KV_I16: v.i = c.get<int16_t>(); break;
+        case KV_U32: v.i = c.get<uint32_t>(); break;
+        case KV_I32: v.i = c.get<int32_t>(); break;
+        case KV_U64: v.i = (int64_t)c.get<uint64_t>(); break;
+        case KV_I64: v.i = c.get<int64_t>(); break;
+        case KV_F32: v.f = c.get<float>(); break;
+        case KV_F64: v.f = c.get<double>(); break;
+        case KV_STRING: v.s = c.str(); break;
+        case KV_ARRAY: {   // kept only as skipped bytes: the DiT reads no array metadata
+            const uint32_t et = c.get<uint32_t>();
+            const uint64_t n = c.get<uint64_t>();
+            if (et == KV_STRING) {
+                for (uint64_t k = 0; k < n && c.ok; ++k) c.str();
+            } else {
+                const size_t es = scalar_size(et);
+                TSN_REQUIRE(es > 0 && n <= (uint64_t)(c.end - c.p) / es, "gguf: bad array in metadata " + key);
+                c.take(nullptr, (size_t)(n * es));
+            }
+            break;
+        }
+        default: TSN_REQUIRE(false, "gguf: unknown metadata type for " + key);
+        }
+        TSN_REQUIRE(c.ok, "gguf: truncated metadata at " + key);
+        kv_[key] = v;
+    }
+    const uint64_t align = has("general.alignment") ? (uint64_t)get_i64("general.alignment", 32) : 32;
+    TSN_REQUIRE(align > 0 && (align & (align - 1)) == 0, "gguf: alignment must be a power of two");
+    for (uint64_t i = 0; i < n_tensors; ++i) {
+        GgufTensorInfo t;
+        t.name = c.str();
+        t.n_dims = c.get<uint32_t>();
+        TSN_REQUIRE(c.ok && t.n_dims >= 1 && t.n_dims <= 4, "gguf: bad tensor info " + t.name);
+        for (uint32_t d = 0; d < t.n_dims; ++d) t.ne[d] = c.get<uint64_t>();
+        t.type = c.get<uint32_t>();
+        t.offset = c.get<uint64_t>();
+        TSN_REQUIRE(c.ok, "gguf: truncated tensor info " + t.name);
+        const uint64_t n = t.numel();
+        switch (t.type) {
+        case GGUF_T_F32: t.nbytes = n * 4; break;
+        case GGUF_T_F16: case GGUF_T_BF16: t.nbytes = n * 2; break;
+        case GGUF_T_Q8_0:
+            TSN_REQUIRE(t.ne[0] % 32 == 0, "gguf: Q8_0 rows must be whole 32-element blocks: " + t.name);
+            t.nbytes = n / 32 * 34;
+            break;
+        default: t.nbytes = 0; break;   // unsupported: rejected when read
+        }
+        index_[t.name] = list_.size();
+        list_.push_back(t);
+    }
+    const uint64_t hdr = (uint64_t)(c.p - (const uint8_t *)map_);
+    const uint64_t data = (hdr + align - 1) & ~(align - 1);
+    for (auto &t : list_) {
+        TSN_REQUIRE(data + t.offset + t.nbytes <= len_ && data + t.offset >= data, "gguf: tensor past end of file: " + t.name);
+        t.data = (const uint8_t *)map_ + data + t.offset;
+    }
+    return TSN_OK;
+}
+
+int64_t GgufReader::get_i64(const std::string &key, int64_t def) const {
+    const auto it = kv_.find(key);
+    if (it == kv_.end()) return def;
+    return it->second.type == KV_F32 || it->second.type == KV_F64 ? (int64_t)it->second.f : it->second.i;
+}
+
+double GgufReader::get_f64(const std::string &key, double def) const {
+    const auto it = kv_.find(key);
+    if (it == kv_.end()) return def;
+    return it->second.type == KV_F32 || it->second.type == KV_F64 ? it->second.f : (double)it->second.i;
+}
+
+std::string GgufReader::get_str(const std::string &key, const std::string &def) const {
+    const auto it = kv_.find(key);
+    return it == kv_.end() || it->second.type != KV_STRING ? def : it->second.s;
+}
+
+const GgufTensorInfo *GgufReader::find(const std::string &name) const {
+    const auto it = index_.find(name);
+    return it == index_.end() ? nullptr : &list_[it->second];
+}
+
+int GgufReader::to_f32(const GgufTensorInfo &t, float *out) const {
+    TSN_REQUIRE(out && t.data, "gguf: null output or tensor");
+    const uint64_t n = t.numel();
+    switch (t.type) {
+    case GGUF_T_F32: memcpy(out, t.data, n * 4); break;
+    case GGUF_T_BF16:
+        for (uint64_t i = 0; i < n; ++i) {
+            uint16_t h;
+            memcpy(&h, t.data + 2 * i, 2);
+            const uint32_t f = (uint32_t)h << 16;
+            memcpy(out + i, &f, 4);
+        }
+        break;
+    case GGUF_T_F16:
+        for (uint64_t i = 0; i < n; ++i) {
+            uint16_t h;
+            memcpy(&h, t.data + 2 * i, 2);
+            out[i] = f16_bits_to_f32_ftz(h);
+        }
+        break;
+    case GGUF_T_Q8_0:
+        for (uint64_t b = 0; b < n / 32; ++b) {
+            const uint8_t *blk = t.data + b * 34;
+            uint16_t sh;
+            memcpy(&sh, blk, 2);
+            const float scale = f16_bits_to_f32_ftz(sh);
+            for (int k = 0; k < 32; ++k) out[b * 32 + k] = scale * (float)(int8_t)blk[2 + k];
+        }
+        break;
+    default: TSN_REQUIRE(false, "gguf: unsupported tensor type " + std::to_string(t.type) + " for " + t.name);
+    }
+    return TSN_OK;
+}
+
+} // namespace tsn

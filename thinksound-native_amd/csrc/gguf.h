@@ -1,0 +1,66 @@
+// gguf.h — read-only GGUF checkpoint reader (host C++, mmap).
+//
+// Replaces tn::GgufFile / tn::to_f32 (src/gguf.h:42-86, src/gguf.cpp): GGUF v2/v3 header, typed
+// key-value metadata, tensor infos (ne[0] fastest), data section at the file's alignment
+// (general.alignment, default 32). Tensor payloads are read in place from the mapping and
+// dequantized on the host to f32 with the reference's semantics: F32 as is, BF16 exact, F16 and
+// the Q8_0 block scale with subnormals flushed to zero, Q8_0 = scale * int8.
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+namespace tsn {
+
+enum GgufTensorType : uint32_t { GGUF_T_F32 = 0, GGUF_T_F16 = 1, GGUF_T_Q8_0 = 8, GGUF_T_BF16 = 30 };
+
+struct GgufTensorInfo {
+    std::string name;
+    uint32_t n_dims = 0;
+    uint64_t ne[4] = {1, 1, 1, 1};   // ne[0] fastest
+    uint32_t type = GGUF_T_F32;
+    uint64_t offset = 0;             // from the start of the data section
+    uint64_t nbytes = 0;
+    const uint8_t *data = nullptr;
+    uint64_t numel() const { return ne[0] * ne[1] * ne[2] * ne[3]; }
+};
+
+class GgufReader {
+public:
+    ~GgufReader();
+    // map and parse; TSN_* status, message in last_error
+    int open(const char *path);
+    bool has(const std::string &key) const { return kv_.count(key) != 0; }
+    int64_t get_i64(const std::string &key, int64_t def) const;
+    double get_f64(const std::string &key, double def) const;
+    std::string get_str(const std::string &key, const std::string &def) const;
+    const GgufTensorInfo *find(const std::string &name) const;
+    const std::vector<GgufTensorInfo> &tensors() const { return list_; }
+    uint32_t version() const { return version_; }
+    // dequantize to f32 (out holds numel floats)
+    int to_f32(const GgufTensorInfo &t, float *out) const;
+
+private:
+    struct Kv {
+        uint32_t type = 0;
+        int64_t i = 0;
+        double f = 0;
+        std::string s;
+    };
+    int fd_ = -1;
+    void *map_ = nullptr;
+    size_t len_ = 0;
+    uint32_t version_ = 0;
+    std::map<std::string, Kv> kv_;
+    std::vector<GgufTensorInfo> list_;
+    std::map<std::string, size_t> index_;
+    int parse();
+};
+
+// f16 bits -> f32 with subnormals flushed to signed zero (the reference's host conversion)
+float f16_bits_to_f32_ftz(uint16_t h);
+
+} // namespace tsn

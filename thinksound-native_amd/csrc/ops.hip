@@ -361,17 +361,46 @@ __global__ void conv_reorder_kernel(const void *src, int src_bf16, half_t *dst, 
     dst[i] = src_bf16 ? (half_t)bf16_to_f32(((const uint16_t *)src)[si]) : ((const half_t *)src)[si];
 }
 
-// Upload-time weight layout: src bf16 [OC][IC][KT] -> dst row r(oc) = (oc % ra)*rb + (oc / ra)*rc + rd,
-// tap-major [KT][IC] within the row, each tap's IC channels written twice ([w | w]) when dup.
-__global__ void weight_prep_kernel(const uint16_t *src, void *dst, int out_f32, int OC, int IC, int KT, int dup,
-                                   int ra, int rb, int rc, int rd) {
+// f32 -> f16 bits as the reference's weight upload converts (src/net.mm:144-164): round to nearest
+// even in the normal range, f32 zero/denormal inputs -> signed zero, results below the f16 normal
+// range truncated to a subnormal (or zero), overflow -> infinity, NaN -> quiet NaN
+__device__ inline half_t f32_to_f16_upload(float f) {
+    const unsigned x = __float_as_uint(f);
+    const unsigned short sign = (unsigned short)((x >> 16) & 0x8000u);
+    const unsigned e8 = (x >> 23) & 0xFFu, man = x & 0x7FFFFFu;
+    unsigned short h;
+    if (e8 == 0xFFu) {
+        h = sign | 0x7C00u | (man ? 0x200u : 0u);
+    } else if (e8 == 0u) {
+        h = sign;
+    } else {
+        const int e = (int)e8 - 112;   // f16 biased exponent
+        if (e >= 31) {
+            h = sign | 0x7C00u;
+        } else if (e <= 0) {
+            h = e < -10 ? sign : (unsigned short)(sign | ((man | 0x800000u) >> (14 - e)));
+        } else {
+            h = (unsigned short)(sign | ((unsigned)e << 10) | (man >> 13));
+            const unsigned rest = man & 0x1FFFu;
+            if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h = (unsigned short)(h + 1u);
+        }
+    }
+    return __builtin_bit_cast(half_t, h);
+}
+
+// Upload-time weight layout: src [OC][IC][KT] (bf16, or f32 when src_f32) -> dst row
+// r(oc) = (oc % ra)*rb + (oc / ra)*rc + rd, tap-major [KT][IC] within the row, each tap's IC channels
+// written twice ([w | w]) when dup; f16 (reference upload rounding) or f32 when out_f32.
+__global__ void weight_prep_kernel(const void *src, int src_f32, void *dst, int out_f32, int OC, int IC, int KT,
+                                   int dup, int ra, int rb, int rc, int rd) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long long)OC * IC * KT) return;
     const int ic = (int)(i % IC);
     const long long q = i / IC;
     const int k = (int)(q % KT);
     const int oc = (int)(q / KT);
-    const float w = bf16_to_f32(src[((long long)oc * IC + ic) * KT + k]);
+    const long long si = ((long long)oc * IC + ic) * KT + k;
+    const float w = src_f32 ? ((const float *)src)[si] : bf16_to_f32(((const uint16_t *)src)[si]);
     const long long row = (long long)(oc % ra) * rb + (long long)(oc / ra) * rc + rd;
     const int w_ic = IC * (dup ? 2 : 1);
     const long long d = row * KT * w_ic + (long long)k * w_ic + ic;
@@ -379,8 +408,9 @@ __global__ void weight_prep_kernel(const uint16_t *src, void *dst, int out_f32, 
         ((float *)dst)[d] = w;
         if (dup) ((float *)dst)[d + IC] = w;
     } else {
-        ((half_t *)dst)[d] = (half_t)w;
-        if (dup) ((half_t *)dst)[d + IC] = (half_t)w;
+        const half_t h = f32_to_f16_upload(w);
+        ((half_t *)dst)[d] = h;
+        if (dup) ((half_t *)dst)[d + IC] = h;
     }
 }
 
@@ -637,16 +667,16 @@ int launch_conv_weight_reorder(const void *src, int src_bf16, half_t *dst, int O
     return TSN_OK;
 }
 
-int launch_weight_prep(const uint16_t *src, void *dst, int out_f32, int OC, int IC, int KT, int dup, int ra, int rb,
-                       int rc, int rd, long long dst_rows, hipStream_t st) {
+int launch_weight_prep(const void *src, int src_f32, void *dst, int out_f32, int OC, int IC, int KT, int dup, int ra,
+                       int rb, int rc, int rd, long long dst_rows, hipStream_t st) {
     TSN_REQUIRE(src && dst && OC > 0 && IC > 0 && KT > 0 && ra > 0 && dst_rows > 0, "weight_prep: arguments");
     for (int oc = 0; oc < OC; ++oc) {   // every destination row inside the destination
         const long long row = (long long)(oc % ra) * rb + (long long)(oc / ra) * rc + rd;
         TSN_REQUIRE(row >= 0 && row < dst_rows, "weight_prep: row map leaves the destination");
     }
     const size_t n = (size_t)OC * IC * KT;
-    TSN_LAUNCH(weight_prep_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, dst, out_f32, OC, IC, KT, dup, ra, rb,
-               rc, rd);
+    TSN_LAUNCH(weight_prep_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, src_f32, dst, out_f32, OC, IC, KT, dup,
+               ra, rb, rc, rd);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }

@@ -12,6 +12,8 @@
 //   final: per-row adaLN (f16 hi|lo) fused into the last reduce, conv k7 pad 3 -> v
 #include "refdit.h"
 
+#include "gguf.h"
+
 #include <math.h>
 #include <string.h>
 
@@ -75,7 +77,7 @@ int refdit_spec_check(const RefDitSpec &s) {
     TSN_REQUIRE(s.HD == 64, "refdit spec: head dim must be 64");
     TSN_REQUIRE(s.H == s.NH * s.HD && s.H % 256 == 0 && s.H <= 2048, "refdit spec: H = NH*64, multiple of 256, <= 2048");
     TSN_REQUIRE(s.F % 64 == 0 && s.F > 0, "refdit spec: F must be a multiple of 64");
-    TSN_REQUIRE(s.latent > 0 && s.latent % 32 == 0, "refdit spec: latent must be a multiple of 32");
+    TSN_REQUIRE(s.latent > 0 && s.latent % 64 == 0, "refdit spec: latent must be a multiple of 64");
     TSN_REQUIRE(s.n_joint >= 0 && s.n_fused >= 0, "refdit spec: block counts");
     return TSN_OK;
 }
@@ -163,23 +165,31 @@ int RefDitModel::create(Runtime *r, const RefDitSpec &sp) {
     return TSN_OK;
 }
 
-int RefDitModel::upload_weights(const uint16_t *host, size_t numel) {
+int RefDitModel::upload_weights(const uint16_t *host, size_t numel) { return upload(host, false, numel); }
+
+int RefDitModel::upload_weights_f32(const float *host, size_t numel) { return upload(host, true, numel); }
+
+// The flat buffer (bf16 or f32, manifest order) goes to the device once; every tensor is laid out
+// and converted from there, then the staging buffer is freed.
+int RefDitModel::upload(const void *host, bool src_f32, size_t numel) {
     TSN_REQUIRE(rt && host, "refdit: not created / null weights");
+    TSN_REQUIRE(!ready_, "refdit: weights already uploaded");
     const auto man = refdit_manifest(s);
     const size_t total = (size_t)(man.back().offset + man.back().numel);
     TSN_REQUIRE(numel == total, "refdit: weight count does not match the manifest (" + std::to_string(total) + ")");
-    TSN_TRY(alloc(total * 2, &wraw_));
-    TSN_TRY(rt->dev.upload(wraw_, host, total * 2));
+    const size_t esz = src_f32 ? 4 : 2;
+    TSN_TRY(alloc(total * esz, &wraw_));
+    TSN_TRY(rt->dev.upload(wraw_, host, total * esz));
     std::map<std::string, const ManifestEntry *> idx;
     for (const auto &e : man) idx[e.name] = &e;
     const hipStream_t st = rt->dev.stream();
     const int H = s.H, F = s.F, L = s.latent;
-    auto raw = [&](const std::string &n) -> const uint16_t * { return (const uint16_t *)wraw_ + idx.at(n)->offset; };
+    auto raw = [&](const std::string &n) -> const void * { return (const char *)wraw_ + idx.at(n)->offset * esz; };
     // prep(name, OC, IC, KT, dup, row map ra/rb/rc/rd, dst, dst_rows, f32 out)
     auto prep = [&](const std::string &n, int OC, int IC, int KT, int dup, int ra, int rb, int rc, int rd, void *dst,
                     long long dst_rows, int out_f32) -> int {
         TSN_REQUIRE(idx.at(n)->numel == (int64_t)OC * IC * KT, "refdit: tensor size mismatch: " + n);
-        return launch_weight_prep(raw(n), dst, out_f32, OC, IC, KT, dup, ra, rb, rc, rd, dst_rows, st);
+        return launch_weight_prep(raw(n), src_f32 ? 1 : 0, dst, out_f32, OC, IC, KT, dup, ra, rb, rc, rd, dst_rows, st);
     };
     auto new_f16 = [&](size_t n, half_t **p) { return alloc(n * 2, (void **)p); };
     auto new_f32 = [&](size_t n, float **p) { return alloc(n * 4, (void **)p); };
@@ -207,16 +217,15 @@ int RefDitModel::upload_weights(const uint16_t *host, size_t numel) {
         *out = w;
         return TSN_OK;
     };
-    half_t *wmodl;
+    half_t *wmodl, *wmodg;
     float *bmodl, *bmodg;
-    uint16_t *wmodg;
     TSN_TRY(new_f16((size_t)NMODL * H, &wmodl));
     TSN_TRY(new_f32(NMODL, &bmodl));
-    TSN_TRY(alloc((size_t)NMODG * H * 2, (void **)&wmodg));
+    TSN_TRY(new_f16((size_t)NMODG * H, &wmodg));
     TSN_TRY(new_f32(NMODG, &bmodg));
     int rowl = 0, rowg = 0;
     // per-row modulation weights gathered as f16 rows of one GEMM (read by both halves of the hi|lo
-    // operand); per-sample ones as bf16 GEMV rows
+    // operand); per-sample ones as f16 rows of one GEMV
     auto mod_rows = [&](const std::string &p, int chunks, bool per_row, int *off) -> int {
         const std::string wn = p + ".adaLN_modulation.1.weight", bn = p + ".adaLN_modulation.1.bias";
         TSN_REQUIRE(idx.at(wn)->numel == (int64_t)chunks * H * H, "refdit: adaLN size: " + p);
@@ -227,7 +236,7 @@ int RefDitModel::upload_weights(const uint16_t *host, size_t numel) {
             rowl += chunks * H;
         } else {
             *off = rowg;
-            TSN_TRY(rt->dev.copy_d2d(wmodg + (size_t)rowg * H, raw(wn), (size_t)chunks * H * H * 2));
+            TSN_TRY(prep(wn, chunks * H, H, 1, 0, 1, 0, 1, rowg, wmodg, NMODG, 0));
             TSN_TRY(prep(bn, chunks * H, 1, 1, 0, 1, 0, 1, rowg, bmodg, NMODG, 1));
             rowg += chunks * H;
         }
@@ -273,9 +282,8 @@ int RefDitModel::upload_weights(const uint16_t *host, size_t numel) {
     bmodL_ = bmodl;
     WmodG_ = wmodg;
     bmodG_ = bmodg;
-    // t-MLP weights are read as bf16 straight from the uploaded buffer by the GEMV
-    Wt0_ = raw("t_embed.mlp.0.weight");
-    Wt2_ = raw("t_embed.mlp.2.weight");
+    TSN_TRY(f16w("t_embed.mlp.0.weight", H, H, 1, &Wt0_));
+    TSN_TRY(f16w("t_embed.mlp.2.weight", H, H, 1, &Wt2_));
     TSN_TRY(f32v("t_embed.mlp.0.bias", H, &bt0_));
     TSN_TRY(f32v("t_embed.mlp.2.bias", H, &bt2_));
     // input conv [H][L][3] and final conv [L][H][7], tap-major
@@ -286,7 +294,54 @@ int RefDitModel::upload_weights(const uint16_t *host, size_t numel) {
     TSN_TRY(swiglu_w("audio_input_proj.2", H, 3, &W13in_));
     TSN_TRY(f16w("audio_input_proj.2.w2.weight", H, F, 3, &W2in_));
     TSN_TRY(rt->dev.sync());
+    TSN_TRY(release(wraw_));
+    wraw_ = nullptr;
     ready_ = true;
+    return TSN_OK;
+}
+
+// WeightSet::load + DitModel::load (src/net.mm:126-173, src/dit.cpp:29-47): every tensor the graph
+// needs is looked up by name, dequantized to f32 on the host (F32, F16, BF16, Q8_0) and uploaded;
+// GEMM and GEMV weights become f16 with the reference's rounding, vectors stay f32.
+int RefDitModel::load_gguf(const char *path) {
+    GgufReader g;
+    TSN_TRY(g.open(path));
+    const auto man = refdit_manifest(s);
+    const size_t total = (size_t)(man.back().offset + man.back().numel);
+    std::vector<float> host(total);
+    for (const auto &e : man) {
+        const GgufTensorInfo *t = g.find(e.name);
+        TSN_REQUIRE(t, std::string("refdit gguf: missing tensor ") + e.name);
+        TSN_REQUIRE((int64_t)t->numel() == e.numel, "refdit gguf: " + e.name + " has " + std::to_string(t->numel()) +
+                                                        " elements, the graph needs " + std::to_string(e.numel));
+        TSN_TRY(g.to_f32(*t, host.data() + e.offset));
+    }
+    return upload(host.data(), true, total);
+}
+
+int refdit_spec_from_gguf(const char *path, int B, int T, int C, int TS, RefDitSpec *out) {
+    TSN_REQUIRE(out, "refdit gguf: null spec");
+    GgufReader g;
+    TSN_TRY(g.open(path));
+    RefDitSpec s{};
+    s.B = B; s.T = T; s.C = C; s.TS = TS;
+    s.H = (int)g.get_i64("dit.hidden_dim", 1024);
+    s.NH = (int)g.get_i64("dit.num_heads", 16);
+    TSN_REQUIRE(s.NH > 0 && s.H % s.NH == 0, "refdit gguf: hidden_dim must be a multiple of num_heads");
+    s.HD = s.H / s.NH;
+    const int depth = (int)g.get_i64("dit.depth", 21);
+    s.n_fused = (int)g.get_i64("dit.fused_depth", 14);
+    s.n_joint = depth - s.n_fused;
+    s.latent = (int)g.get_i64("dit.latent_dim", 64);
+    s.rope_theta = (float)g.get_f64("dit.rope_theta", 10000.0);
+    s.t_max_period = (float)g.get_f64("dit.t_embed_max_period", 1.0);
+    // SwiGLU width from the first latent FFN conv weight, ne = [3, H, F]
+    const GgufTensorInfo *w1 = g.find("joint_blocks.0.latent_block.ffn.w1.weight");
+    s.F = w1 && w1->n_dims >= 3 ? (int)w1->ne[2] : 2816;
+    s.ln_eps = 1e-5f;
+    s.rms_eps = 1e-6f;
+    TSN_TRY(refdit_spec_check(s));
+    *out = s;
     return TSN_OK;
 }
 
@@ -495,19 +550,19 @@ int RefDitModel::enqueue_conditioning(const float *t, int rows, const float *gcm
         const int nb = rem >= 16 ? 16 : rem > 8 ? 16 : rem > 4 ? 8 : rem > 2 ? 4 : rem;   // rows past `rows` are padding
         GemvArgs g1;
         memset(&g1, 0, sizeof g1);
-        g1.W = Wt0_; g1.ldw = H; g1.wdt = DT_BF16; g1.X = temb + (size_t)r0 * H; g1.ldx = H;
+        g1.W = Wt0_; g1.ldw = H; g1.wdt = DT_F16; g1.X = temb + (size_t)r0 * H; g1.ldx = H;
         g1.Y = h1 + (size_t)r0 * H; g1.ldy = H; g1.bias = bt0_; g1.N = H; g1.K = H; g1.nb = nb; g1.silu = 1;
         TSN_TRY(run(K_GEMV, 2.0 * nb * H * H, 2.0 * H * H, [&] { return launch_gemv(g1, st); }));
         GemvArgs g2;
         memset(&g2, 0, sizeof g2);
-        g2.W = Wt2_; g2.ldw = H; g2.wdt = DT_BF16; g2.X = h1 + (size_t)r0 * H; g2.ldx = H;
+        g2.W = Wt2_; g2.ldw = H; g2.wdt = DT_F16; g2.X = h1 + (size_t)r0 * H; g2.ldx = H;
         g2.Y = gc + (size_t)r0 * H; g2.ldy = H; g2.bias = bt2_; g2.addv = gcmlp; g2.ld_add = H;
         g2.Y2 = gs + (size_t)r0 * H; g2.ldy2 = H; g2.N = H; g2.K = H; g2.nb = nb;
         TSN_TRY(run(K_GEMV, 2.0 * nb * H * H, 2.0 * H * H, [&] { return launch_gemv(g2, st); }));
         if (s.n_joint == 0) continue;
         GemvArgs m;
         memset(&m, 0, sizeof m);
-        m.W = WmodG_; m.ldw = H; m.wdt = DT_BF16;
+        m.W = WmodG_; m.ldw = H; m.wdt = DT_F16;
         m.X = gs + (size_t)r0 * H; m.ldx = H;
         m.Y = modg + (size_t)r0 * NMODG; m.ldy = NMODG;
         m.bias = bmodG_; m.N = NMODG; m.K = H; m.nb = nb;

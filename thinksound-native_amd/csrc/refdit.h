@@ -41,6 +41,9 @@ std::vector<ManifestEntry> refdit_manifest(const RefDitSpec &s);
 int refdit_spec_check(const RefDitSpec &s);
 // geometry of a generation of dur seconds (src/models.h:14-22, src/pipeline.cpp:81-83)
 RefDitSpec refdit_spec_for_duration(int dur_s, int B);
+// hyperparameters from a checkpoint's dit.* metadata and the SwiGLU width from its first latent
+// FFN weight (src/dit.cpp:29-47); geometry B, T, C, TS from the caller
+int refdit_spec_from_gguf(const char *path, int B, int T, int C, int TS, RefDitSpec *out);
 
 class RefDitModel : public GraphRunner {
 public:
@@ -50,6 +53,10 @@ public:
     // [OC][K][IC], w1/w3 interleaved in 64-row blocks for the SwiGLU epilogue, input and final conv
     // weights duplicated as [w | w] for f32-accurate hi|lo operands, all GEMM weights f16.
     int upload_weights(const uint16_t *host_bf16, size_t numel);
+    // the same from an f32 buffer (dequantized checkpoint tensors)
+    int upload_weights_f32(const float *host_f32, size_t numel);
+    // every tensor of the manifest from a GGUF checkpoint (any of F32, F16, BF16, Q8_0)
+    int load_gguf(const char *path);
 
     // one velocity evaluation, device pointers: x [B][T][latent], t [B], clip_pp [B][C][H],
     // text_pp [B][TS][H], gcmlp [B][H], sync_gather [B][T][H] -> v [B][T][latent].
@@ -87,6 +94,7 @@ private:
     struct Next {
         int kind, idx;
     };
+    int upload(const void *host, bool src_f32, size_t numel);
     int enqueue_conditioning(const float *t, int rows, const float *gcmlp, float *temb, float *h1, float *gc,
                              float *gs, float *modg);
     int enqueue_eval(const float *x, const float *t, const float *clip_pp, const float *text_pp, const float *gcmlp,
@@ -99,7 +107,7 @@ private:
 
     std::vector<StreamW> jl_, jc_, jt_, fu_;
     const half_t *WmodL_ = nullptr;                       // [NMODL][H] f16
-    const uint16_t *WmodG_ = nullptr, *Wt0_ = nullptr, *Wt2_ = nullptr;   // bf16 GEMV weights
+    const half_t *WmodG_ = nullptr, *Wt0_ = nullptr, *Wt2_ = nullptr;   // f16 GEMV weights
     const float *bmodL_ = nullptr, *bmodG_ = nullptr, *bt0_ = nullptr, *bt2_ = nullptr;
     const half_t *Win_ = nullptr, *W13in_ = nullptr, *W2in_ = nullptr, *Wfin_ = nullptr;
     const float *bin_ = nullptr, *bfin_ = nullptr;

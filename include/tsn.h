@@ -229,6 +229,37 @@ int tsn_refdit_profile_forward(tsn_refdit *dit, const float *x, const float *t, 
                                const float *text_pp, const float *gcmlp, const float *sync_gather, float *flow,
                                tsn_kernel_stat *stats, int cap, int *n_stats);
 
+/* ---------------- conditioning prep: DitModel::prep_conditioning / prep_text_arm (src/dit.cpp:55-191) ----------------
+ * Once per generation (sync and clip streams) and once per CFG arm (text): the inputs of
+ * tsn_refdit_forward. All GEMMs read f32-accurate f16 hi|lo operands. */
+typedef struct {
+    int H, F;           /* hidden 1024, SwiGLU width 2816 */
+    int T, C, sync_S;   /* latent rows, clip rows (8/s), sync rows (24/s: src/pipeline.cpp:81-83) */
+    int TS;             /* text rows (154) */
+    int sync_dim, clip_dim, text_dim, gtext_dim;   /* input widths 768, 1024, 2048, 1024 */
+} tsn_refcond_spec;
+typedef struct tsn_refcond tsn_refcond;
+int tsn_refcond_spec_for_duration(int dur_s, tsn_refcond_spec *out);
+/* widths from a checkpoint (dit.hidden_dim; F and the input widths from the projections' shapes) */
+int tsn_refcond_spec_from_gguf(const char *path, int T, int C, int sync_S, int TS, tsn_refcond_spec *out);
+int tsn_refcond_manifest_count(const tsn_refcond_spec *spec);
+int tsn_refcond_manifest_entry(const tsn_refcond_spec *spec, int idx, char *name, int name_cap, int64_t *numel,
+                               int64_t *offset);
+int64_t tsn_refcond_manifest_total(const tsn_refcond_spec *spec);
+int tsn_refcond_create(tsn_runtime *rt, const tsn_refcond_spec *spec, tsn_refcond **out);
+int tsn_refcond_destroy(tsn_refcond *c);
+int tsn_refcond_upload_weights(tsn_refcond *c, const uint16_t *weights_host, size_t numel);   /* flat BF16 */
+int tsn_refcond_upload_weights_f32(tsn_refcond *c, const float *weights_host, size_t numel);
+int tsn_refcond_load_gguf(tsn_refcond *c, const char *path);   /* WeightSet::load, src/net.mm:126-173 */
+/* DitModel::prep_conditioning (src/dit.cpp:55-135): clip_f [C][clip_dim], sync_f [sync_S][sync_dim]
+ * -> clip_pp [C][H], sync_gather [T][H], clip_fc [H] (device pointers) */
+int tsn_refcond_prep_conditioning(tsn_refcond *c, const float *clip_f, const float *sync_f, float *clip_pp,
+                                  float *sync_gather, float *clip_fc);
+/* DitModel::prep_text_arm (src/dit.cpp:137-191): text_cat [TS][text_dim], gtext [gtext_dim], clip_fc [H]
+ * -> text_pp [TS][H], gcmlp [H] */
+int tsn_refcond_prep_text_arm(tsn_refcond *c, const float *text_cat, const float *gtext, const float *clip_fc,
+                              float *text_pp, float *gcmlp);
+
 /* ---------------- GGUF checkpoint reader: tn::GgufFile / tn::to_f32 (src/gguf.h:42-86) ----------------
  * mmap, GGUF v2/v3, typed metadata, tensor infos with ne[0] fastest, data at general.alignment. */
 typedef struct tsn_gguf tsn_gguf;
@@ -250,6 +281,7 @@ int tsn_synth_uniform_f32(uint64_t seed, uint64_t index, double lo, double hi, s
 /* all weights of a spec, flat BF16 in manifest order: N(0, 0.02); q/k norm weights N(norm_mean, 0.02) */
 int tsn_dit_synth_weights(const tsn_dit_spec *spec, uint64_t seed, double norm_mean, uint16_t *out_host);
 int tsn_refdit_synth_weights(const tsn_refdit_spec *spec, uint64_t seed, double norm_mean, uint16_t *out_host);
+int tsn_refcond_synth_weights(const tsn_refcond_spec *spec, uint64_t seed, uint16_t *out_host);
 
 #ifdef __cplusplus
 }

@@ -143,6 +143,28 @@ void orc_ref_dit_sample(const orc_ref_spec *s, const float *weights, float *x, c
                         const float *text_pp, const float *gcmlp, const float *sync_gather, int steps,
                         float cfg);
 
+/* ---------------- the reference's conditioning prep (oracle_cond.cpp) ---------------- */
+
+// H hidden, F SwiGLU width, T latent rows, C clip rows, sync_S sync rows, TS text rows; feature
+// widths of the sync (768), clip (1024), text (2048) and pooled-text (1024) inputs
+typedef struct {
+    int H, F, T, C, sync_S, TS;
+    int sync_dim, clip_dim, text_dim, gtext_dim;
+} orc_refcond_spec;
+
+int orc_refcond_manifest_count(const orc_refcond_spec *s);
+int64_t orc_refcond_manifest_numel(const orc_refcond_spec *s, int idx);
+void orc_refcond_manifest_name(const orc_refcond_spec *s, int idx, char *buf, int cap);
+
+// DitModel::prep_conditioning (src/dit.cpp:55-135): clip_f [C, clip_dim], sync_f [sync_S, sync_dim]
+//   -> clip_pp [C, H], sync_gather [T, H], clip_fc [H]
+void orc_ref_prep_conditioning(const orc_refcond_spec *s, const float *weights, const float *clip_f,
+                               const float *sync_f, float *clip_pp, float *sync_gather, float *clip_fc);
+// DitModel::prep_text_arm (src/dit.cpp:137-191): text_cat [TS, text_dim], gtext [gtext_dim], clip_fc [H]
+//   -> text_pp [TS, H], gcmlp [H]
+void orc_ref_prep_text_arm(const orc_refcond_spec *s, const float *weights, const float *text_cat,
+                           const float *gtext, const float *clip_fc, float *text_pp, float *gcmlp);
+
 // number of OpenMP threads the oracle uses (for the CPU-baseline report)
 int orc_num_threads(void);
 

@@ -31,6 +31,12 @@ class RefSpec(ctypes.Structure):
                 ("rope_theta", _F), ("t_max_period", _F), ("ln_eps", _F), ("rms_eps", _F)]
 
 
+class CondSpec(ctypes.Structure):
+    """orc_refcond_spec: the reference's conditioning prep"""
+    _fields_ = [("H", _I), ("F", _I), ("T", _I), ("C", _I), ("sync_S", _I), ("TS", _I),
+                ("sync_dim", _I), ("clip_dim", _I), ("text_dim", _I), ("gtext_dim", _I)]
+
+
 _SIGS = {
     "orc_gemm": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
     "orc_gemv": [_P, _P, _P, _P, _I, _I, _I],
@@ -61,9 +67,15 @@ _SIGS = {
     "orc_ref_manifest_name": [ctypes.POINTER(RefSpec), _I, ctypes.c_char_p, _I],
     "orc_ref_dit_forward": [ctypes.POINTER(RefSpec), _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "orc_ref_dit_sample": [ctypes.POINTER(RefSpec), _P, _P, _P, _P, _P, _P, _I, _F],
+    "orc_refcond_manifest_count": [ctypes.POINTER(CondSpec)],
+    "orc_refcond_manifest_numel": [ctypes.POINTER(CondSpec), _I],
+    "orc_refcond_manifest_name": [ctypes.POINTER(CondSpec), _I, ctypes.c_char_p, _I],
+    "orc_ref_prep_conditioning": [ctypes.POINTER(CondSpec), _P, _P, _P, _P, _P, _P],
+    "orc_ref_prep_text_arm": [ctypes.POINTER(CondSpec), _P, _P, _P, _P, _P, _P],
 }
 _RES = {"orc_manifest_count": _I, "orc_manifest_numel": ctypes.c_int64, "orc_manifest_total": ctypes.c_int64,
-        "orc_num_threads": _I, "orc_ref_manifest_count": _I, "orc_ref_manifest_numel": ctypes.c_int64}
+        "orc_num_threads": _I, "orc_ref_manifest_count": _I, "orc_ref_manifest_numel": ctypes.c_int64,
+        "orc_refcond_manifest_count": _I, "orc_refcond_manifest_numel": ctypes.c_int64}
 
 _lib = None
 
@@ -298,3 +310,45 @@ def ref_dit_sample(spec, W, x, clip_pp, text_pp, gcmlp, sync_gather, steps, cfg)
     lib().orc_ref_dit_sample(ctypes.byref(s), p(W), p(x), p(f32(clip_pp)), p(f32(text_pp)), p(f32(gcmlp)),
                              p(f32(sync_gather)), steps, cfg)
     return x
+
+
+# ---------------- the reference's conditioning prep ----------------
+def cond_spec_from(spec):
+    if isinstance(spec, CondSpec):
+        return spec
+    d = spec if isinstance(spec, dict) else {k: getattr(spec, k) for k, _ in CondSpec._fields_}
+    return CondSpec(**{k: d[k] for k, _ in CondSpec._fields_})
+
+
+def cond_manifest(spec):
+    s = cond_spec_from(spec)
+    L = lib()
+    out, buf = [], ctypes.create_string_buffer(256)
+    off = 0
+    for i in range(L.orc_refcond_manifest_count(ctypes.byref(s))):
+        L.orc_refcond_manifest_name(ctypes.byref(s), i, buf, 256)
+        n = L.orc_refcond_manifest_numel(ctypes.byref(s), i)
+        out.append((buf.value.decode(), n, off))
+        off += n
+    return out
+
+
+def ref_prep_conditioning(spec, W, clip_f, sync_f):
+    """-> clip_pp [C, H], sync_gather [T, H], clip_fc [H]"""
+    s = cond_spec_from(spec)
+    clip_pp = np.empty((s.C, s.H), np.float32)
+    sync_gather = np.empty((s.T, s.H), np.float32)
+    clip_fc = np.empty(s.H, np.float32)
+    lib().orc_ref_prep_conditioning(ctypes.byref(s), p(W), p(f32(clip_f)), p(f32(sync_f)), p(clip_pp),
+                                    p(sync_gather), p(clip_fc))
+    return clip_pp, sync_gather, clip_fc
+
+
+def ref_prep_text_arm(spec, W, text_cat, gtext, clip_fc):
+    """-> text_pp [TS, H], gcmlp [H]"""
+    s = cond_spec_from(spec)
+    text_pp = np.empty((s.TS, s.H), np.float32)
+    gcmlp = np.empty(s.H, np.float32)
+    lib().orc_ref_prep_text_arm(ctypes.byref(s), p(W), p(f32(text_cat)), p(f32(gtext)), p(f32(clip_fc)),
+                                p(text_pp), p(gcmlp))
+    return text_pp, gcmlp

@@ -146,3 +146,12 @@ def test_ref_spec_errors(tsn):
     h = ctypes.c_void_p()
     assert tsn.lib().tsn_refdit_create(rt_null, ctypes.byref(spec), ctypes.byref(h)) == 1
     assert tsn.lib().tsn_refdit_replay(None) == 1
+
+
+def test_cond_manifest_matches_oracle(tsn, orc):
+    spec = tsn.cond_spec_for_duration(8)
+    assert (spec.H, spec.F, spec.T, spec.C, spec.sync_S, spec.TS) == (1024, 2816, 172, 64, 192, 154)
+    assert (spec.sync_dim, spec.clip_dim, spec.text_dim, spec.gtext_dim) == (768, 1024, 2048, 1024)
+    assert tsn.cond_manifest(spec) == orc.cond_manifest(spec.as_dict())
+    small = spec.copy(H=256, F=128, sync_dim=64, clip_dim=128, text_dim=192, gtext_dim=32)
+    assert tsn.cond_manifest(small) == orc.cond_manifest(small.as_dict())

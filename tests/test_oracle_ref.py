@@ -1,4 +1,5 @@
-"""Pinning of the oracle's reference-graph restatement (oracle/oracle_ref.cpp) — CPU only.
+"""Pinning of the oracle's reference-graph restatement (oracle/oracle_ref.cpp) and conditioning
+prep (oracle/oracle_cond.cpp) — CPU only.
 
 Checked against:
   * a float64 NumPy restatement of the three-stream graph written here from the reference forward
@@ -6,7 +7,9 @@ Checked against:
     clip RoPE scaled by T/C, pre-only last joint block, conv-k7 final layer);
   * structure: the pre-only block leaves the clip and text rows untouched, fused blocks never touch
     them, samples do not mix;
-  * closed form: a zero final conv makes the velocity its bias and the sampler moves x by -bias.
+  * closed form: a zero final conv makes the velocity its bias and the sampler moves x by -bias;
+  * conditioning prep (src/dit.cpp:55-191) against a float64 NumPy restatement, with the sync
+    gather's row choice as a known answer.
 """
 import numpy as np
 import pytest
@@ -199,3 +202,73 @@ def test_ref_sampler_closed_form(orc):
     x0 = inp["x"][:1]
     x = orc.ref_dit_sample(spec, w, x0, inp["clip_pp"], inp["text_pp"], inp["gcmlp"], inp["sync_gather"], 4, 5.0)
     assert np.allclose(x, x0 - bias, atol=1e-6)
+
+
+# ---------------- conditioning prep (oracle/oracle_cond.cpp) ----------------
+def tiny_cond_spec():
+    return dict(H=128, F=64, T=10, C=4, sync_S=12, TS=5, sync_dim=64, clip_dim=96, text_dim=160, gtext_dim=32)
+
+
+def cond_weights(orc, spec, seed=3):
+    man = orc.cond_manifest(spec)
+    r = rng(seed)
+    w = (0.05 * r.standard_normal(sum(n for _, n, _ in man))).astype(np.float32)
+    return w, {name: (off, n) for name, n, off in man}
+
+
+def np_prep(spec, w, idx, clip_f, sync_f, text_cat, gtext):
+    """float64 restatement of src/dit.cpp:55-191 written from the reference's steps"""
+    H, F = spec["H"], spec["F"]
+
+    def get(n, shape):
+        o, k = idx[n]
+        return w[o:o + k].astype(np.float64).reshape(shape)
+
+    def convmlp(p, x):
+        h = _silu(_conv(x, get(p + ".w1.weight", (F, H, 3)), None, 1)) * _conv(x, get(p + ".w3.weight", (F, H, 3)), None, 1)
+        return _conv(h, get(p + ".w2.weight", (H, F, 3)), None, 1)
+
+    def mlp(p, x):
+        h = _silu(x @ get(p + ".w1.weight", (F, H)).T) * (x @ get(p + ".w3.weight", (F, H)).T)
+        return h @ get(p + ".w2.weight", (H, F)).T
+
+    SS, T = spec["sync_S"], spec["T"]
+    pe = get("sync_pos_emb", (8, spec["sync_dim"]))
+    sb = sync_f.astype(np.float64) + pe[np.arange(SS) % 8]
+    smid = convmlp("sync_input_proj.2", _silu(_conv(sb, get("sync_input_proj.0.weight", (H, spec["sync_dim"], 7)),
+                                                    get("sync_input_proj.0.bias", (H,)), 3)))
+    f = np.float32   # the row index is computed in f32: floorf(((float)i + 0.5f) * (float)S / (float)T)
+    rows = [int(np.floor((f(i) + f(0.5)) * f(SS) / f(T))) for i in range(T)]
+    sync_gather = smid[rows]
+    clip = _silu(clip_f.astype(np.float64) @ get("clip_input_proj.0.weight", (H, spec["clip_dim"])).T
+                 + get("clip_input_proj.0.bias", (H,)))
+    clip_pp = convmlp("clip_input_proj.2", clip)
+    clip_fc = get("clip_cond_proj.weight", (H, H)) @ clip_pp.mean(0) + get("clip_cond_proj.bias", (H,))
+    text = _silu(text_cat.astype(np.float64) @ get("text_input_proj.0.weight", (H, spec["text_dim"])).T
+                 + get("text_input_proj.0.bias", (H,)))
+    text_pp = mlp("text_input_proj.2", text)
+    fc = get("text_cond_proj.weight", (H, spec["gtext_dim"])) @ gtext.astype(np.float64) + \
+        get("text_cond_proj.bias", (H,)) + clip_fc
+    gcmlp = mlp("global_cond_mlp", fc[None, :])[0]
+    return clip_pp, sync_gather, clip_fc, text_pp, gcmlp, rows
+
+
+def test_cond_prep_vs_numpy(orc):
+    spec = tiny_cond_spec()
+    w, idx = cond_weights(orc, spec)
+    r = rng(4)
+    clip_f = r.standard_normal((spec["C"], spec["clip_dim"])).astype(np.float32)
+    sync_f = r.standard_normal((spec["sync_S"], spec["sync_dim"])).astype(np.float32)
+    text_cat = r.standard_normal((spec["TS"], spec["text_dim"])).astype(np.float32)
+    gtext = r.standard_normal(spec["gtext_dim"]).astype(np.float32)
+    clip_pp, sg, clip_fc = orc.ref_prep_conditioning(spec, w, clip_f, sync_f)
+    text_pp, gcmlp = orc.ref_prep_text_arm(spec, w, text_cat, gtext, clip_fc)
+    e = np_prep(spec, w, idx, clip_f, sync_f, text_cat, gtext)
+    for got, ref in zip((clip_pp, sg, clip_fc, text_pp, gcmlp), e[:5]):
+        assert rel_l2(got, ref) < 1e-5
+    # the gather picks rows floor((i + 0.5) * sync_S / T): for 12 -> 10 rows that is row 0, 1, 3, ...
+    assert e[5] == [0, 1, 3, 4, 5, 6, 7, 9, 10, 11]
+    # upsampling (sync_S < T) repeats rows: 12 -> 20 takes each sync row for 5/3 latent rows
+    up = dict(spec, T=20)
+    _, sg_up, _ = orc.ref_prep_conditioning(up, w, clip_f, sync_f)
+    assert np.array_equal(sg_up[0], sg_up[1]) and not np.array_equal(sg_up[1], sg_up[2])

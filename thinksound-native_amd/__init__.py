@@ -65,6 +65,22 @@ class RefDitSpec(ctypes.Structure):
         return s
 
 
+class RefCondSpec(ctypes.Structure):
+    """tsn_refcond_spec (include/tsn.h): the reference's conditioning prep."""
+    _fields_ = [("H", ctypes.c_int), ("F", ctypes.c_int), ("T", ctypes.c_int), ("C", ctypes.c_int),
+                ("sync_S", ctypes.c_int), ("TS", ctypes.c_int), ("sync_dim", ctypes.c_int),
+                ("clip_dim", ctypes.c_int), ("text_dim", ctypes.c_int), ("gtext_dim", ctypes.c_int)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+    def copy(self, **kw):
+        s = RefCondSpec()
+        for k, _ in self._fields_:
+            setattr(s, k, kw.get(k, getattr(self, k)))
+        return s
+
+
 class KernelStat(ctypes.Structure):
     """tsn_kernel_stat (include/tsn.h)."""
     _fields_ = [("name", ctypes.c_char * 64), ("launches", ctypes.c_int), ("total_ms", ctypes.c_double),
@@ -143,6 +159,20 @@ _SIGS = {
     "tsn_refdit_upload_weights_f32": [_P, _P, _SZ],
     "tsn_refdit_load_gguf": [_P, ctypes.c_char_p],
     "tsn_refdit_spec_from_gguf": [ctypes.c_char_p, _I, _I, _I, _I, ctypes.POINTER(RefDitSpec)],
+    "tsn_refcond_spec_for_duration": [_I, ctypes.POINTER(RefCondSpec)],
+    "tsn_refcond_spec_from_gguf": [ctypes.c_char_p, _I, _I, _I, _I, ctypes.POINTER(RefCondSpec)],
+    "tsn_refcond_manifest_count": [ctypes.POINTER(RefCondSpec)],
+    "tsn_refcond_manifest_entry": [ctypes.POINTER(RefCondSpec), _I, ctypes.c_char_p, _I,
+                                   ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)],
+    "tsn_refcond_manifest_total": [ctypes.POINTER(RefCondSpec)],
+    "tsn_refcond_create": [_P, ctypes.POINTER(RefCondSpec), ctypes.POINTER(_P)],
+    "tsn_refcond_destroy": [_P],
+    "tsn_refcond_upload_weights": [_P, _P, _SZ],
+    "tsn_refcond_upload_weights_f32": [_P, _P, _SZ],
+    "tsn_refcond_load_gguf": [_P, ctypes.c_char_p],
+    "tsn_refcond_prep_conditioning": [_P, _P, _P, _P, _P, _P],
+    "tsn_refcond_prep_text_arm": [_P, _P, _P, _P, _P, _P],
+    "tsn_refcond_synth_weights": [ctypes.POINTER(RefCondSpec), ctypes.c_uint64, _P],
     "tsn_gguf_open": [ctypes.c_char_p, ctypes.POINTER(_P)],
     "tsn_gguf_close": [_P],
     "tsn_gguf_tensor_count": [_P],
@@ -154,7 +184,8 @@ _SIGS = {
 }
 _RESTYPES = {"tsn_last_error": ctypes.c_char_p, "tsn_last_gpu_ms": ctypes.c_double,
              "tsn_dit_manifest_total": ctypes.c_int64, "tsn_refdit_manifest_total": ctypes.c_int64,
-             "tsn_gguf_get_i64": ctypes.c_int64, "tsn_gguf_get_f64": ctypes.c_double, "tsn_version": _I}
+             "tsn_gguf_get_i64": ctypes.c_int64, "tsn_gguf_get_f64": ctypes.c_double,
+             "tsn_refcond_manifest_total": ctypes.c_int64, "tsn_version": _I}
 
 
 def lib():
@@ -271,6 +302,66 @@ def ref_spec_from_gguf(path, B=2, T=172, C=64, TS=154):
     s = RefDitSpec()
     call("tsn_refdit_spec_from_gguf", os.fsencode(path), B, T, C, TS, ctypes.byref(s))
     return s
+
+
+def cond_spec_for_duration(dur_s):
+    s = RefCondSpec()
+    call("tsn_refcond_spec_for_duration", dur_s, ctypes.byref(s))
+    return s
+
+
+def cond_spec_from_gguf(path, T=172, C=64, sync_S=192, TS=154):
+    s = RefCondSpec()
+    call("tsn_refcond_spec_from_gguf", os.fsencode(path), T, C, sync_S, TS, ctypes.byref(s))
+    return s
+
+
+def cond_manifest(spec):
+    L = lib()
+    out, buf = [], ctypes.create_string_buffer(256)
+    for i in range(L.tsn_refcond_manifest_count(ctypes.byref(spec))):
+        numel, off = ctypes.c_int64(), ctypes.c_int64()
+        call("tsn_refcond_manifest_entry", ctypes.byref(spec), i, buf, 256, ctypes.byref(numel), ctypes.byref(off))
+        out.append((buf.value.decode(), numel.value, off.value))
+    return out
+
+
+def cond_synth_weights(spec, seed=4242):
+    w = np.empty(int(lib().tsn_refcond_manifest_total(ctypes.byref(spec))), np.uint16)
+    call("tsn_refcond_synth_weights", ctypes.byref(spec), seed, ptr(w))
+    return w
+
+
+class RefCondModel:
+    """DitModel::prep_conditioning / prep_text_arm mirror (src/dit.cpp:55-191)."""
+
+    def __init__(self, rt, spec):
+        self.rt, self.spec = rt, spec
+        h = ctypes.c_void_p()
+        call("tsn_refcond_create", rt.h, ctypes.byref(spec), ctypes.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().tsn_refcond_destroy(self.h)
+            self.h = None
+
+    def upload_weights(self, w_bf16):
+        w_bf16 = np.ascontiguousarray(w_bf16, dtype=np.uint16)
+        call("tsn_refcond_upload_weights", self.h, ptr(w_bf16), w_bf16.size)
+
+    def upload_weights_f32(self, w):
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        call("tsn_refcond_upload_weights_f32", self.h, ptr(w), w.size)
+
+    def load_gguf(self, path):
+        call("tsn_refcond_load_gguf", self.h, os.fsencode(path))
+
+    def prep_conditioning(self, clip_f, sync_f, clip_pp, sync_gather, clip_fc):
+        call("tsn_refcond_prep_conditioning", self.h, clip_f.p, sync_f.p, clip_pp.p, sync_gather.p, clip_fc.p)
+
+    def prep_text_arm(self, text_cat, gtext, clip_fc, text_pp, gcmlp):
+        call("tsn_refcond_prep_text_arm", self.h, text_cat.p, gtext.p, clip_fc.p, text_pp.p, gcmlp.p)
 
 
 class Gguf:

@@ -7,6 +7,7 @@
 
 #include "dit.h"
 #include "gguf.h"
+#include "refcond.h"
 #include "refdit.h"
 
 namespace tsn {
@@ -26,6 +27,9 @@ struct tsn_refdit {
 };
 struct tsn_gguf {
     tsn::GgufReader r;
+};
+struct tsn_refcond {
+    tsn::RefCondModel m;
 };
 
 #define RT_CHECK(r)                                                 \
@@ -48,6 +52,17 @@ static tsn::RefDitSpec to_ref_spec(const tsn_refdit_spec *c) {
     s.latent = c->latent; s.n_joint = c->n_joint; s.n_fused = c->n_fused; s.rope_theta = c->rope_theta;
     s.t_max_period = c->t_max_period; s.ln_eps = c->ln_eps; s.rms_eps = c->rms_eps;
     return s;
+}
+
+static tsn::RefCondSpec to_cond_spec(const tsn_refcond_spec *c) {
+    tsn::RefCondSpec s;
+    s.H = c->H; s.F = c->F; s.T = c->T; s.C = c->C; s.sync_S = c->sync_S; s.TS = c->TS;
+    s.sync_dim = c->sync_dim; s.clip_dim = c->clip_dim; s.text_dim = c->text_dim; s.gtext_dim = c->gtext_dim;
+    return s;
+}
+static void from_cond_spec(const tsn::RefCondSpec &s, tsn_refcond_spec *c) {
+    c->H = s.H; c->F = s.F; c->T = s.T; c->C = s.C; c->sync_S = s.sync_S; c->TS = s.TS;
+    c->sync_dim = s.sync_dim; c->clip_dim = s.clip_dim; c->text_dim = s.text_dim; c->gtext_dim = s.gtext_dim;
 }
 
 static int copy_stats(const std::vector<tsn::KernelStat> &ks, tsn_kernel_stat *stats, int cap, int *n_stats) {
@@ -316,6 +331,79 @@ int tsn_refdit_spec_from_gguf(const char *path, int B, int T, int C, int TS, tsn
     return TSN_OK;
 }
 
+/* ---------------- conditioning prep ---------------- */
+#define COND_CHECK(d)                                                             \
+    do {                                                                          \
+        if (!(d)) { tsn::set_error("null refcond handle"); return TSN_ERR_ARG; }  \
+    } while (0)
+
+int tsn_refcond_spec_for_duration(int dur_s, tsn_refcond_spec *out) {
+    if (!out || dur_s <= 0) { tsn::set_error("refcond spec: null out pointer or non-positive duration"); return TSN_ERR_ARG; }
+    from_cond_spec(tsn::refcond_spec_for_duration(dur_s), out);
+    return TSN_OK;
+}
+int tsn_refcond_spec_from_gguf(const char *path, int T, int C, int sync_S, int TS, tsn_refcond_spec *out) {
+    if (!path || !out) { tsn::set_error("null path or spec"); return TSN_ERR_ARG; }
+    tsn::RefCondSpec s;
+    TSN_TRY(tsn::refcond_spec_from_gguf(path, T, C, sync_S, TS, &s));
+    from_cond_spec(s, out);
+    return TSN_OK;
+}
+int tsn_refcond_manifest_count(const tsn_refcond_spec *spec) {
+    if (!spec) { tsn::set_error("null spec"); return -1; }
+    return (int)tsn::refcond_manifest(to_cond_spec(spec)).size();
+}
+int tsn_refcond_manifest_entry(const tsn_refcond_spec *spec, int idx, char *name, int name_cap, int64_t *numel,
+                               int64_t *offset) {
+    if (!spec) { tsn::set_error("null spec"); return TSN_ERR_ARG; }
+    const auto m = tsn::refcond_manifest(to_cond_spec(spec));
+    if (idx < 0 || idx >= (int)m.size()) { tsn::set_error("manifest index out of range"); return TSN_ERR_ARG; }
+    if (name && name_cap > 0) snprintf(name, (size_t)name_cap, "%s", m[idx].name.c_str());
+    if (numel) *numel = m[idx].numel;
+    if (offset) *offset = m[idx].offset;
+    return TSN_OK;
+}
+int64_t tsn_refcond_manifest_total(const tsn_refcond_spec *spec) {
+    if (!spec) { tsn::set_error("null spec"); return -1; }
+    const auto m = tsn::refcond_manifest(to_cond_spec(spec));
+    return m.back().offset + m.back().numel;
+}
+int tsn_refcond_create(tsn_runtime *rt, const tsn_refcond_spec *spec, tsn_refcond **out) {
+    RT_CHECK(rt);
+    if (!spec || !out) { tsn::set_error("null spec or out pointer"); return TSN_ERR_ARG; }
+    *out = nullptr;
+    tsn_refcond *d = new (std::nothrow) tsn_refcond();
+    if (!d) { tsn::set_error("out of host memory"); return TSN_ERR_OOM; }
+    const int rc = d->m.create(&rt->rt, to_cond_spec(spec));
+    if (rc != TSN_OK) { delete d; return rc; }
+    *out = d;
+    return TSN_OK;
+}
+int tsn_refcond_destroy(tsn_refcond *d) { delete d; return TSN_OK; }
+int tsn_refcond_upload_weights(tsn_refcond *d, const uint16_t *w, size_t numel) {
+    COND_CHECK(d);
+    return d->m.upload_weights(w, numel);
+}
+int tsn_refcond_upload_weights_f32(tsn_refcond *d, const float *w, size_t numel) {
+    COND_CHECK(d);
+    return d->m.upload_weights_f32(w, numel);
+}
+int tsn_refcond_load_gguf(tsn_refcond *d, const char *path) {
+    COND_CHECK(d);
+    if (!path) { tsn::set_error("null path"); return TSN_ERR_ARG; }
+    return d->m.load_gguf(path);
+}
+int tsn_refcond_prep_conditioning(tsn_refcond *d, const float *clip_f, const float *sync_f, float *clip_pp,
+                                  float *sync_gather, float *clip_fc) {
+    COND_CHECK(d);
+    return d->m.enqueue_prep_conditioning(clip_f, sync_f, clip_pp, sync_gather, clip_fc);
+}
+int tsn_refcond_prep_text_arm(tsn_refcond *d, const float *text_cat, const float *gtext, const float *clip_fc,
+                              float *text_pp, float *gcmlp) {
+    COND_CHECK(d);
+    return d->m.enqueue_prep_text_arm(text_cat, gtext, clip_fc, text_pp, gcmlp);
+}
+
 /* ---------------- GGUF reader ---------------- */
 int tsn_gguf_open(const char *path, tsn_gguf **out) {
     if (!path || !out) { tsn::set_error("null path or out pointer"); return TSN_ERR_ARG; }
@@ -424,6 +512,13 @@ int tsn_refdit_synth_weights(const tsn_refdit_spec *spec, uint64_t seed, double 
         const bool is_norm = m[i].name.find("norm.weight") != std::string::npos;
         tsn::synth_normal_bf16(seed, (uint64_t)i, is_norm ? norm_mean : 0.0, 0.02, (size_t)m[i].numel, out + m[i].offset);
     }
+    return TSN_OK;
+}
+int tsn_refcond_synth_weights(const tsn_refcond_spec *spec, uint64_t seed, uint16_t *out) {
+    if (!spec || !out) { tsn::set_error("null spec or output"); return TSN_ERR_ARG; }
+    const auto m = tsn::refcond_manifest(to_cond_spec(spec));
+    for (size_t i = 0; i < m.size(); ++i)
+        tsn::synth_normal_bf16(seed, (uint64_t)i, 0.0, 0.02, (size_t)m[i].numel, out + m[i].offset);
     return TSN_OK;
 }
 int tsn_dit_synth_weights(const tsn_dit_spec *spec, uint64_t seed, double norm_mean, uint16_t *out) {

@@ -7,6 +7,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include "graph.h"
 #include "tsn_common.h"
 
 namespace tsn {
@@ -213,6 +214,19 @@ int GgufReader::to_f32(const GgufTensorInfo &t, float *out) const {
         }
         break;
     default: TSN_REQUIRE(false, "gguf: unsupported tensor type " + std::to_string(t.type) + " for " + t.name);
+    }
+    return TSN_OK;
+}
+
+int gguf_read_manifest(const GgufReader &g, const std::vector<ManifestEntry> &man, std::vector<float> &out) {
+    TSN_REQUIRE(!man.empty(), "gguf: empty manifest");
+    out.assign((size_t)(man.back().offset + man.back().numel), 0.0f);
+    for (const auto &e : man) {
+        const GgufTensorInfo *t = g.find(e.name);
+        TSN_REQUIRE(t, "gguf: missing tensor " + e.name);
+        TSN_REQUIRE((int64_t)t->numel() == e.numel, "gguf: " + e.name + " has " + std::to_string(t->numel()) +
+                                                        " elements, the graph needs " + std::to_string(e.numel));
+        TSN_TRY(g.to_f32(*t, out.data() + e.offset));
     }
     return TSN_OK;
 }

@@ -63,4 +63,9 @@ private:
 // f16 bits -> f32 with subnormals flushed to signed zero (the reference's host conversion)
 float f16_bits_to_f32_ftz(uint16_t h);
 
+struct ManifestEntry;
+// every tensor of a manifest looked up by name in the file, its element count checked, dequantized
+// to f32 into out at the manifest offsets (WeightSet::load's name map, src/net.mm:126-140)
+int gguf_read_manifest(const GgufReader &g, const std::vector<ManifestEntry> &man, std::vector<float> &out);
+
 } // namespace tsn

@@ -202,6 +202,13 @@ int launch_weight_prep(const void *src, int src_f32, void *dst, int out_f32, int
 // y = silu(x[m] + v[m / L]) (x [M][H], v [M/L][H] f32) as f16 hi|lo rows [M][2H] (LN_F16_HILO layout)
 int launch_bcast_add_silu_f16(const float *x, const float *v, half_t *y, int L, int M, int H, hipStream_t st);
 
+// out [M][2K] f16 hi|lo of x[m][k] + pe[m % P][k] (pe null: x alone)
+int launch_add_period_hilo(const float *x, const float *pe, int P, half_t *out, int M, int K, hipStream_t st);
+// dst[i][:] = src[idx[i]][:] for rows x H floats (idx on the device, every entry a valid src row)
+int launch_gather_rows(const float *src, const int32_t *idx, float *dst, int rows, int H, hipStream_t st);
+// out[c] = mean over rows of x[r][c], rows summed in order (src/net.mm Runtime::mean_cols)
+int launch_mean_rows(const float *x, int rows, int H, float *out, hipStream_t st);
+
 // reference-surface elementwise ops (f32)
 int launch_silu(float *x, size_t n, hipStream_t st);
 int launch_copy(const float *x, float *y, size_t n, hipStream_t st);

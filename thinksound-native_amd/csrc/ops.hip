@@ -428,6 +428,36 @@ __global__ void bcast_add_silu_kernel(const float *x, const float *v, half_t *y,
     y[(long long)m * 2 * H + H + c] = (half_t)(s - (float)hi);
 }
 
+// out [M][2K] f16 hi|lo of x[m][k] + pe[m % P][k] (pe may be null): the sync features plus their
+// 8-periodic positional embedding (src/dit.cpp:93-99), as the operand of the following conv
+__global__ void add_period_hilo_kernel(const float *x, const float *pe, int P, half_t *out, int M, int K) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)M * K) return;
+    const int m = (int)(i / K), k = (int)(i - (long long)m * K);
+    const float v = x[i] + (pe ? pe[(long long)(m % P) * K + k] : 0.0f);
+    const half_t hi = (half_t)v;
+    out[(long long)m * 2 * K + k] = hi;
+    out[(long long)m * 2 * K + K + k] = (half_t)(v - (float)hi);
+}
+
+// dst[i] = src[idx[i]], rows of H floats
+__global__ void gather_rows_kernel(const float *src, const int32_t *idx, float *dst, int rows, int H) {
+    const int r = blockIdx.x;
+    if (r >= rows) return;
+    const float *s = src + (long long)idx[r] * H;
+    float *d = dst + (long long)r * H;
+    for (int c = threadIdx.x; c < H; c += blockDim.x) d[c] = s[c];
+}
+
+// out[c] = (sum over rows r in order of x[r][c]) / rows: one thread per column, fixed order
+__global__ void mean_rows_kernel(const float *x, int rows, int H, float *out) {
+    const int c = blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= H) return;
+    float acc = 0.0f;
+    for (int r = 0; r < rows; ++r) acc += x[(long long)r * H + c];
+    out[c] = acc / (float)rows;
+}
+
 // reference-surface elementwise kernels (shaders/ops_conv.metal:9-57,146-169,193-201)
 __global__ void silu_kernel(float *x, size_t n) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -683,6 +713,24 @@ int launch_weight_prep(const void *src, int src_f32, void *dst, int out_f32, int
 int launch_bcast_add_silu_f16(const float *x, const float *v, half_t *y, int L, int M, int H, hipStream_t st) {
     TSN_REQUIRE(x && v && y && L > 0 && M > 0 && H > 0, "bcast_add_silu: arguments");
     TSN_LAUNCH(bcast_add_silu_kernel, dim3(blocks_for((size_t)M * H)), dim3(256), 0, st, x, v, y, L, M, H);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_add_period_hilo(const float *x, const float *pe, int P, half_t *out, int M, int K, hipStream_t st) {
+    TSN_REQUIRE(x && out && M > 0 && K > 0 && (!pe || P > 0), "add_period_hilo: arguments");
+    TSN_LAUNCH(add_period_hilo_kernel, dim3(blocks_for((size_t)M * K)), dim3(256), 0, st, x, pe, P, out, M, K);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_gather_rows(const float *src, const int32_t *idx, float *dst, int rows, int H, hipStream_t st) {
+    TSN_REQUIRE(src && idx && dst && rows > 0 && H > 0, "gather_rows: arguments");
+    TSN_LAUNCH(gather_rows_kernel, dim3(rows), dim3(256), 0, st, src, idx, dst, rows, H);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+int launch_mean_rows(const float *x, int rows, int H, float *out, hipStream_t st) {
+    TSN_REQUIRE(x && out && rows > 0 && H > 0, "mean_rows: arguments");
+    TSN_LAUNCH(mean_rows_kernel, dim3((H + 255) / 256), dim3(256), 0, st, x, rows, H, out);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }

@@ -306,17 +306,9 @@ int RefDitModel::upload(const void *host, bool src_f32, size_t numel) {
 int RefDitModel::load_gguf(const char *path) {
     GgufReader g;
     TSN_TRY(g.open(path));
-    const auto man = refdit_manifest(s);
-    const size_t total = (size_t)(man.back().offset + man.back().numel);
-    std::vector<float> host(total);
-    for (const auto &e : man) {
-        const GgufTensorInfo *t = g.find(e.name);
-        TSN_REQUIRE(t, std::string("refdit gguf: missing tensor ") + e.name);
-        TSN_REQUIRE((int64_t)t->numel() == e.numel, "refdit gguf: " + e.name + " has " + std::to_string(t->numel()) +
-                                                        " elements, the graph needs " + std::to_string(e.numel));
-        TSN_TRY(g.to_f32(*t, host.data() + e.offset));
-    }
-    return upload(host.data(), true, total);
+    std::vector<float> host;
+    TSN_TRY(gguf_read_manifest(g, refdit_manifest(s), host));
+    return upload(host.data(), true, host.size());
 }
 
 int refdit_spec_from_gguf(const char *path, int B, int T, int C, int TS, RefDitSpec *out) {
@@ -361,8 +353,9 @@ void RefDitModel::ln1_seg(LnSeg &g, int kind, const StreamW &w) {
 
 // Fill the LN part of r's segments (one per stream of the residual GEMM) for the adaLN that runs
 // next: LN1 of the next joint block (every stream) or fused block (latent), or the final layer's
-// (latent rows as f16 hi|lo into XF2). ln2: the LN2 of block next.idx instead of its LN1 (chunks
-// 3, 4), latent rows as f16 hi|lo (the FFN operand).
+// (latent rows as f16 hi|lo into XF2). LN1 output is f16 hi|lo in every stream (the QKV operand).
+// ln2: the LN2 of block next.idx instead of its LN1 (chunks 3, 4), f16 hi|lo for latent rows (the
+// FFN operand), hi only for clip and text rows.
 void RefDitModel::next_ln(RedLnArgs &r, Next next, const int *kinds, int nseg, bool ln2) {
     memset(&r, 0, sizeof r);
     r.ymode = next.kind == NEXT_FINAL ? LN_F16_HILO : LN_F16;
@@ -371,7 +364,7 @@ void RefDitModel::next_ln(RedLnArgs &r, Next next, const int *kinds, int nseg, b
         const int k = kinds[i];
         const RowMap m = stream_map(k);
         g.Y = XN_; g.ldy = 2 * s.H; g.ymap = m;
-        g.hilo = ln2 && k == ST_LAT;
+        g.hilo = !ln2 || k == ST_LAT;   // LN1 (QKV operand) in every stream, LN2 (FFN operand) for latent rows
         if (k == ST_LAT) { g.mod = MODL_; g.mod_ld = NMODL; g.mod_L = 1; g.ln_len = 1; }
         else { g.mod = modg_; g.mod_ld = NMODG; g.mod_L = m.L; g.ln_len = m.L; }
         switch (next.kind) {
@@ -400,7 +393,7 @@ int RefDitModel::block_joint(int i, bool ln1, Next next) {
         memset(&ln, 0, sizeof ln);
         ln.nseg = 3; ln.H = H; ln.eps = s.ln_eps;
         for (int k = 0; k < 3; ++k) ln1_seg(ln.seg[k], kinds[k], *w[k]);
-        TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16, st); }));
+        TSN_TRY(run(K_LNHL, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16_HILO, st); }));
     }
     // q|k|v with per-head RMS; RoPE on latent (positions 0..T-1) and clip (scaled by T/C) rows
     GemmBatch qb;
@@ -412,7 +405,8 @@ int RefDitModel::block_joint(int i, bool ln1, Next next) {
         const RowMap m = stream_map(kinds[k]);
         qkv_problem(qb.p[k], XN_, m, B * m.L, w[k]->Wqkv, w[k]->bqkv, w[k]->qn, w[k]->kn, H, s.NH, Q_, K_, Vt_, S, Sp,
                     m.L, soff[k], rlen[k], rope[k], s.rms_eps);
-        qb.p[k].lda = 2 * H;   // hi halves of the XN rows
+        qb.p[k].lda = qb.p[k].Kc = qb.p[k].K = 2 * H;   // XN rows as hi|lo
+        half_w(qb.p[k]);
     }
     qb.ws = ws_;
     qb.ws_bytes = ws_bytes_;
@@ -485,13 +479,14 @@ int RefDitModel::block_fused(int i, bool ln1, Next next) {
         memset(&ln, 0, sizeof ln);
         ln.nseg = 1; ln.H = H; ln.eps = s.ln_eps;
         ln1_seg(ln.seg[0], ST_LAT, w);
-        TSN_TRY(run(K_LN16, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16, st); }));
+        TSN_TRY(run(K_LNHL, 0, ln_bytes(ln, true), [&] { return launch_ln_mod(ln, LN_F16_HILO, st); }));
     }
     GemmBatch qb;
     qb.nprob = 1;
     qkv_problem(qb.p[0], XN_, Lm, M, w.Wqkv, w.bqkv, w.qn, w.kn, H, s.NH, Q_, K_, VtF_, T, SpF, T, 0, T, rope_l_,
                 s.rms_eps);
-    qb.p[0].lda = 2 * H;
+    qb.p[0].lda = qb.p[0].Kc = qb.p[0].K = 2 * H;   // XN rows as hi|lo
+    half_w(qb.p[0]);
     qb.ws = ws_;
     qb.ws_bytes = ws_bytes_;
     TSN_TRY(gemm_run(qb, EPI_QKV));

@@ -11,17 +11,18 @@
 //
 // HBM layout (B samples, S rows per sample: latent, then clip, then text):
 //   X    f32 [B][S][H]       residual streams, updated in place by GEMM epilogues
-//   XN   f16 [B][S][2H]      adaLN output (GEMM A operand), hi at [0, H), lo at [H, 2H) for the
-//                            latent LN2 rows (FFN operand); rows [0, B*T) double as the input
-//                            projection's hidden (hi|lo)
+//   XN   f16 [B][S][2H]      adaLN output (GEMM A operand), hi at [0, H), lo at [H, 2H): LN1 of
+//                            every stream (QKV operand), LN2 of the latent rows (FFN operand); rows
+//                            [0, B*T) double as the input projection's hidden (hi|lo)
 //   XE   f16 [B*T][2H]       silu(extended_c) as hi|lo, A operand of the per-row modulation GEMM
 //   MODL f32 [B*T][NMODL]    per-row modulation: every latent and fused block (6 chunks), final (2)
 //   MODG f32 [B][NMODG]      per-sample modulation of the clip and text streams (6, or 2 when pre-only)
 //   Q,K  f16 [B][NH][S][64], Vt f16 [B][NH][64][Sp] (joint); VtF [B][NH][64][SpF] (fused, S = T)
 //   AO   f16 [B][S][2H]      attention output as hi|lo
 //   HF   f16 [B][S][2F]      SwiGLU hidden, hi|lo for latent rows
-// The latent stream's out-proj and FFN GEMMs read hi|lo operands, each half against the same
-// weight columns (f32-accurate operands); the clip and text streams read the hi halves only.
+// Every QKV GEMM and the latent stream's out-proj and FFN GEMMs read hi|lo operands, each half
+// against the same weight columns (f32-accurate operands); the clip and text out-proj and FFN read
+// the hi halves only.
 #pragma once
 #include <vector>
 

@@ -226,6 +226,71 @@ def bench_ref(tsn, rt, args):
             "launch": "hipGraph replay"}
 
 
+def bench_vae(tsn, rt, args):
+    """The reference's VAE decoder at 8 s (T = 172 latent rows -> 352,256 stereo samples): graph
+    replays of one decode, per-kernel statistics, and the oracle timed on a 4-row latent."""
+    spec = tsn.vae_spec_for_duration(8)
+    w = tsn.vae_synth_weights(spec, 4242)
+    m = tsn.VaeModel(rt, spec)
+    m.upload_weights(w)
+    latent = tsn.synth_normal_f32(4242, 2000, 0.0, 1.0, (spec.T, spec.latent))
+    z = rt.array(latent)
+    n_audio = tsn.vae_audio_len(spec)
+    audio = rt.empty((n_audio, spec.out_ch))
+    m.capture_decode(z, audio)
+    for _ in range(3):
+        m.replay()
+    rt.sync()
+    n = 10
+    rt.begin()
+    for _ in range(n):
+        m.replay()
+    ms = rt.commit() / n
+    stats = None
+    for _ in range(2):
+        stats = m.profile_decode(z, audio)
+    stats.sort(key=lambda k: -k["ms"])
+    tot = sum(k["ms"] for k in stats)
+    flops = sum(k["flops"] for k in stats)
+    for k in stats[:6]:
+        log("  vae %-28s %4d launches %8.3f ms  %7.1f TFLOP/s (f32 GEMM)  %7.1f GB/s"
+            % (k["name"], k["launches"], k["ms"], k["flops"] / (k["ms"] * 1e9) if k["ms"] else 0,
+               k["bytes"] / (k["ms"] * 1e6) if k["ms"] else 0))
+    dom = stats[0]
+    dom_tf = dom["flops"] / (dom["ms"] * 1e9) if dom["ms"] else 0.0
+    log("bench vae: %.3f ms per 8 s decode (%.0fx real time), %.1f GFLOP (f32 GEMM)" % (ms, 8e3 / ms, flops / 1e9))
+    cpu = None
+    if not args.no_cpu:
+        import pyoracle
+        cspec = spec.copy(T=4)
+        cw = w   # the manifest does not depend on T
+        cl = latent[:4].copy()
+        k, c0 = 0, time.perf_counter()
+        while True:
+            pyoracle.vae_decode(cspec.as_dict(), cw, cl)
+            k += 1
+            cs = time.perf_counter() - c0
+            if cs >= CPU_SAMPLE_S / 2:
+                break
+        cpu = {"value": round(k * 4 * 2048 / cs, 1), "unit": "audio samples/s", "cores": pyoracle.num_threads(),
+               "kind": "port", "sample": "%d decodes of a 4-row latent (8192 samples), f32 host C++ oracle, %.2f s"
+                                         % (k, cs)}
+        log("bench vae: CPU oracle %d decodes of 4 rows in %.2f s" % (k, cs))
+    m.close()
+    return {"workload": "VAE decode of an 8 s latent (T=172 -> 352256 samples x 2 channels)",
+            "T": spec.T, "widths": list(spec.width), "strides": list(spec.stride),
+            "ms_per_decode": round(ms, 4), "audio_samples_per_s": round(n_audio / (ms * 1e-3), 1),
+            "realtime_factor": round(8e3 / ms, 1), "gflop_f32": round(flops / 1e9, 2),
+            "f32_tflops": round(flops / (ms * 1e-3) / 1e12, 2),
+            "mfma_frac_f16_executed": round(3 * flops / (ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4),
+            "dominant": {"kernel": dom["name"], "f32_tflops": round(dom_tf, 2),
+                         "mfma_frac_f16_executed": round(3 * dom_tf / PEAK_F16_TFLOPS, 4)},
+            "kernels": [{"name": k["name"], "launches": k["launches"], "ms": round(k["ms"], 4),
+                         "share": round(k["ms"] / tot, 4)} for k in stats[:8]],
+            "arithmetic": "f32-accurate: three f16 MFMA products per term (hi/lo split of both operands)",
+            "cpu_baseline": cpu, "launch": "hipGraph replay"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -234,6 +299,7 @@ def main():
     ap.add_argument("--sampler-reps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-ref", action="store_true", help="skip the reference checkpoint graph section")
+    ap.add_argument("--no-vae", action="store_true", help="skip the VAE decoder section")
     ap.add_argument("--eager", action="store_true",
                     help="launch kernel by kernel instead of replaying hipGraphs (for profilers that do not follow graphs)")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -347,13 +413,19 @@ def main():
     if not args.no_ref and not args.eager:
         ref = bench_ref(tsn, rt, args)
 
-    # ---------------- CPU baseline: the oracle, one full evaluation ----------------
-    cpu = None
     if not args.no_cpu:
         sys.path.insert(0, os.path.join(ROOT, "oracle"))
         import pyoracle
         if not os.path.exists(pyoracle.LIB_PATH):
             pyoracle.build()
+    vae = None
+    if not args.no_vae and not args.eager:
+        vae = bench_vae(tsn, rt, args)
+
+    # ---------------- CPU baseline: the oracle, one full evaluation ----------------
+    cpu = None
+    if not args.no_cpu:
+        import pyoracle
         w32 = tsn.bf16_to_f32(w16)
         n_ev = 0
         c0 = time.perf_counter()
@@ -397,6 +469,7 @@ def main():
                      "share": round(k["ms"] / tot_ms, 4)} for k in stats],
         "cpu_baseline": cpu,
         "reference_graph": ref,
+        "vae_decoder": vae,
         "accumulate": "f32 (f16 MFMA operands from BF16 weights; f32 residual stream)",
         "launch": "eager" if args.eager else "hipGraph replay",
     }

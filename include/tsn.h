@@ -260,6 +260,39 @@ int tsn_refcond_prep_conditioning(tsn_refcond *c, const float *clip_f, const flo
 int tsn_refcond_prep_text_arm(tsn_refcond *c, const float *text_cat, const float *gtext, const float *clip_fc,
                               float *text_pp, float *gcmlp);
 
+/* ---------------- VAE decoder: tn::VaeModel (src/models.h:87-94, src/vae.cpp:17-86) ----------------
+ * latent [T][64] -> conv k7 (+b) -> 5 stages { snake -> transposed conv (stride s, kernel 2s, +b)
+ * -> 3 residual units (dilation 1, 3, 9) } -> snake -> conv k7 (no bias) -> audio [T*prod(s)][2].
+ * f32 in the reference (src/vae.cpp:12); here every GEMM is f32-accurate on f16 MFMA (three products
+ * of a hi/lo split of both operands), the residual stream f32. */
+typedef struct {
+    int T, latent;   /* latent rows (llround(44100/2048*dur), src/models.h:16-21) and width 64 */
+    int width[6];    /* input conv output width, then each stage's output width: 2048,1024,512,256,128,128 */
+    int stride[5];   /* upsampling factors 8, 8, 4, 4, 2 (src/vae.cpp:20) */
+    int kt[5];       /* transposed-conv kernel sizes (2*stride in the checkpoint) */
+    int out_ch;      /* audio channels (2) */
+} tsn_vae_spec;
+typedef struct tsn_vae tsn_vae;
+int tsn_vae_spec_for_duration(int dur_s, tsn_vae_spec *out);
+/* widths and kernel sizes from a checkpoint's tensor shapes (vae-f32.gguf); T from the caller */
+int tsn_vae_spec_from_gguf(const char *path, int T, tsn_vae_spec *out);
+int64_t tsn_vae_audio_len(const tsn_vae_spec *spec);   /* T_audio = T * prod(stride) */
+int tsn_vae_manifest_count(const tsn_vae_spec *spec);
+int tsn_vae_manifest_entry(const tsn_vae_spec *spec, int idx, char *name, int name_cap, int64_t *numel,
+                           int64_t *offset);
+int64_t tsn_vae_manifest_total(const tsn_vae_spec *spec);
+int tsn_vae_create(tsn_runtime *rt, const tsn_vae_spec *spec, tsn_vae **out);   /* VaeModel::load src/vae.cpp:10-15 */
+int tsn_vae_destroy(tsn_vae *v);
+int tsn_vae_upload_weights(tsn_vae *v, const float *weights_host, size_t numel);   /* flat f32, manifest order */
+int tsn_vae_load_gguf(tsn_vae *v, const char *path);   /* WeightSet::load(keep_f32), src/net.mm:126-173 */
+/* VaeModel::decode (src/vae.cpp:17-86): latent [T][latent] -> audio [T_audio][out_ch], device pointers,
+ * enqueued on the runtime's stream (the reference returns host audio; download it with tsn_download) */
+int tsn_vae_decode(tsn_vae *v, const float *latent, float *audio);
+int tsn_vae_capture_decode(tsn_vae *v, const float *latent, float *audio);   /* hipGraph of one decode */
+int tsn_vae_replay(tsn_vae *v);
+int tsn_vae_profile_decode(tsn_vae *v, const float *latent, float *audio, tsn_kernel_stat *stats, int cap,
+                           int *n_stats);
+
 /* ---------------- GGUF checkpoint reader: tn::GgufFile / tn::to_f32 (src/gguf.h:42-86) ----------------
  * mmap, GGUF v2/v3, typed metadata, tensor infos with ne[0] fastest, data at general.alignment. */
 typedef struct tsn_gguf tsn_gguf;
@@ -282,6 +315,9 @@ int tsn_synth_uniform_f32(uint64_t seed, uint64_t index, double lo, double hi, s
 int tsn_dit_synth_weights(const tsn_dit_spec *spec, uint64_t seed, double norm_mean, uint16_t *out_host);
 int tsn_refdit_synth_weights(const tsn_refdit_spec *spec, uint64_t seed, double norm_mean, uint16_t *out_host);
 int tsn_refcond_synth_weights(const tsn_refcond_spec *spec, uint64_t seed, uint16_t *out_host);
+/* VAE: conv weights N(0, 1/(IC*K)) (residual-branch k1 convs N(0, 0.25/IC)), biases N(0, 0.02), snake
+ * alpha and beta N(0, 0.1); f32 */
+int tsn_vae_synth_weights(const tsn_vae_spec *spec, uint64_t seed, float *out_host);
 
 #ifdef __cplusplus
 }

@@ -165,6 +165,34 @@ void orc_ref_prep_conditioning(const orc_refcond_spec *s, const float *weights, 
 void orc_ref_prep_text_arm(const orc_refcond_spec *s, const float *weights, const float *text_cat,
                            const float *gtext, const float *clip_fc, float *text_pp, float *gcmlp);
 
+/* ---------------- the reference's VAE decoder (oracle_vae.cpp) ---------------- */
+
+// T latent frames of `latent` channels; width[0] is the input conv's output width, width[n+1] the
+// output width of upsampling stage n; stride[n] and kt[n] the stage's transposed-conv stride and
+// kernel size; out_ch audio channels
+typedef struct {
+    int T, latent;
+    int width[6];
+    int stride[5];
+    int kt[5];
+    int out_ch;
+} orc_vae_spec;
+
+int orc_vae_manifest_count(const orc_vae_spec *s);
+int64_t orc_vae_manifest_numel(const orc_vae_spec *s, int idx);
+void orc_vae_manifest_name(const orc_vae_spec *s, int idx, char *buf, int cap);
+int64_t orc_vae_audio_len(const orc_vae_spec *s);
+
+// snake: y = x + sin(x*exp(alpha[c]))^2 * exp(-beta[c]), x and y [S, C] (shaders/ops_conv.metal:204-213)
+void orc_snake(const float *x, float *y, const float *alpha, const float *beta, int S, int C);
+// transposed conv in the reference's gather form (src/net.mm:36-48, shaders/ops_conv.metal:262-283):
+// y[t, oc] = b[oc] + sum_{ic,k} x[(t-pad+k)/stride, ic] * W[oc][ic][k] over taps where t-pad+k >= 0
+// is a multiple of stride and the row is inside [0, T)
+void orc_conv1d_t(const float *W, const float *bias, const float *x, float *y, int T, int OL, int IC, int OC,
+                  int K, int stride, int pad);
+// VaeModel::decode (src/vae.cpp:17-86): latent [T, latent] -> audio [T*prod(stride), out_ch]
+void orc_vae_decode(const orc_vae_spec *s, const float *weights, const float *latent, float *audio);
+
 // number of OpenMP threads the oracle uses (for the CPU-baseline report)
 int orc_num_threads(void);
 

@@ -37,6 +37,11 @@ class CondSpec(ctypes.Structure):
                 ("sync_dim", _I), ("clip_dim", _I), ("text_dim", _I), ("gtext_dim", _I)]
 
 
+class VaeSpec(ctypes.Structure):
+    """orc_vae_spec: the reference's VAE decoder"""
+    _fields_ = [("T", _I), ("latent", _I), ("width", _I * 6), ("stride", _I * 5), ("kt", _I * 5), ("out_ch", _I)]
+
+
 _SIGS = {
     "orc_gemm": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
     "orc_gemv": [_P, _P, _P, _P, _I, _I, _I],
@@ -72,10 +77,18 @@ _SIGS = {
     "orc_refcond_manifest_name": [ctypes.POINTER(CondSpec), _I, ctypes.c_char_p, _I],
     "orc_ref_prep_conditioning": [ctypes.POINTER(CondSpec), _P, _P, _P, _P, _P, _P],
     "orc_ref_prep_text_arm": [ctypes.POINTER(CondSpec), _P, _P, _P, _P, _P, _P],
+    "orc_vae_manifest_count": [ctypes.POINTER(VaeSpec)],
+    "orc_vae_manifest_numel": [ctypes.POINTER(VaeSpec), _I],
+    "orc_vae_manifest_name": [ctypes.POINTER(VaeSpec), _I, ctypes.c_char_p, _I],
+    "orc_vae_audio_len": [ctypes.POINTER(VaeSpec)],
+    "orc_snake": [_P, _P, _P, _P, _I, _I],
+    "orc_conv1d_t": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I],
+    "orc_vae_decode": [ctypes.POINTER(VaeSpec), _P, _P, _P],
 }
 _RES = {"orc_manifest_count": _I, "orc_manifest_numel": ctypes.c_int64, "orc_manifest_total": ctypes.c_int64,
         "orc_num_threads": _I, "orc_ref_manifest_count": _I, "orc_ref_manifest_numel": ctypes.c_int64,
-        "orc_refcond_manifest_count": _I, "orc_refcond_manifest_numel": ctypes.c_int64}
+        "orc_refcond_manifest_count": _I, "orc_refcond_manifest_numel": ctypes.c_int64,
+        "orc_vae_manifest_count": _I, "orc_vae_manifest_numel": ctypes.c_int64, "orc_vae_audio_len": ctypes.c_int64}
 
 _lib = None
 
@@ -352,3 +365,65 @@ def ref_prep_text_arm(spec, W, text_cat, gtext, clip_fc):
     lib().orc_ref_prep_text_arm(ctypes.byref(s), p(W), p(f32(text_cat)), p(f32(gtext)), p(f32(clip_fc)),
                                 p(text_pp), p(gcmlp))
     return text_pp, gcmlp
+
+
+# ---------------- the reference's VAE decoder ----------------
+def vae_spec_from(spec):
+    """VaeSpec from a VaeSpec, a dict or an object with T, latent, width[6], stride[5], kt[5], out_ch"""
+    if isinstance(spec, VaeSpec):
+        return spec
+    d = spec if isinstance(spec, dict) else {k: getattr(spec, k) for k, _ in VaeSpec._fields_}
+    s = VaeSpec()
+    s.T, s.latent, s.out_ch = d["T"], d["latent"], d["out_ch"]
+    for i in range(6):
+        s.width[i] = d["width"][i]
+    for i in range(5):
+        s.stride[i] = d["stride"][i]
+        s.kt[i] = d["kt"][i]
+    return s
+
+
+def vae_manifest(spec):
+    s = vae_spec_from(spec)
+    L = lib()
+    out, buf = [], ctypes.create_string_buffer(256)
+    off = 0
+    for i in range(L.orc_vae_manifest_count(ctypes.byref(s))):
+        L.orc_vae_manifest_name(ctypes.byref(s), i, buf, 256)
+        n = L.orc_vae_manifest_numel(ctypes.byref(s), i)
+        out.append((buf.value.decode(), n, off))
+        off += n
+    return out
+
+
+def vae_audio_len(spec):
+    s = vae_spec_from(spec)
+    return lib().orc_vae_audio_len(ctypes.byref(s))
+
+
+def snake(x, alpha, beta):
+    """x [S, C] -> x + sin(x*exp(alpha))^2 * exp(-beta)"""
+    x = f32(x)
+    S, C = x.shape
+    y = np.empty_like(x)
+    lib().orc_snake(p(x), p(y), p(f32(alpha)), p(f32(beta)), S, C)
+    return y
+
+
+def conv1d_t(W, bias, x, stride, pad):
+    """reference-form transposed conv: W [OC][IC][K], x [T, IC] -> y [T*stride, OC]"""
+    W, x = f32(W), f32(x)
+    OC, IC, K = W.shape
+    T = x.shape[0]
+    y = np.empty((T * stride, OC), np.float32)
+    lib().orc_conv1d_t(p(W), p(f32(bias)) if bias is not None else None, p(x), p(y), T, T * stride, IC, OC, K,
+                       stride, pad)
+    return y
+
+
+def vae_decode(spec, W, latent):
+    """latent [T, latent] -> audio [T_audio, out_ch]"""
+    s = vae_spec_from(spec)
+    audio = np.empty((vae_audio_len(s), s.out_ch), np.float32)
+    lib().orc_vae_decode(ctypes.byref(s), p(f32(W)), p(f32(latent)), p(audio))
+    return audio

@@ -155,3 +155,62 @@ def test_cond_manifest_matches_oracle(tsn, orc):
     assert tsn.cond_manifest(spec) == orc.cond_manifest(spec.as_dict())
     small = spec.copy(H=256, F=128, sync_dim=64, clip_dim=128, text_dim=192, gtext_dim=32)
     assert tsn.cond_manifest(small) == orc.cond_manifest(small.as_dict())
+
+
+def test_vae_manifest_matches_oracle(tsn, orc):
+    spec = tsn.vae_spec_for_duration(8)
+    # src/models.h:16-21 and src/vae.cpp:20 at 8 s: T = 172 latent rows, hop 2048
+    d = spec.as_dict()
+    assert (d["T"], d["latent"], d["width"], d["stride"], d["kt"], d["out_ch"]) == \
+        (172, 64, [2048, 1024, 512, 256, 128, 128], [8, 8, 4, 4, 2], [16, 16, 8, 8, 4], 2)
+    assert tsn.vae_audio_len(spec) == 172 * 2048 == orc.vae_audio_len(d)
+    assert tsn.vae_manifest(spec) == orc.vae_manifest(d)
+    small = spec.copy(T=5, width=[128, 64, 64, 64, 64, 64], stride=[2, 4, 2, 2, 2], kt=[4, 8, 4, 4, 4])
+    assert tsn.vae_manifest(small) == orc.vae_manifest(small.as_dict())
+
+
+def test_vae_synth_weights_layout(tsn):
+    spec = tsn.vae_spec_for_duration(1).copy(width=[256, 128, 128, 64, 64, 64])
+    w = tsn.vae_synth_weights(spec, 7)
+    man = tsn.vae_manifest(spec)
+    assert w.size == man[-1][1] + man[-1][2]
+    for name, n, off in man:
+        x = w[off:off + n].astype(np.float64)
+        if name.endswith(".alpha") or name.endswith(".beta"):
+            want = 0.1
+        elif name.endswith(".bias"):
+            want = 0.02
+        else:
+            layer = int(name.split(".")[2])
+            oc = spec.width[0] if layer == 0 else spec.out_ch if layer == 7 else spec.width[layer]
+            want = 1.0 / np.sqrt(n / oc) * (0.5 if name.endswith(".layers.3.weight") else 1.0)
+        if n >= 1000:
+            assert abs(x.std() / want - 1) < 0.1, name
+    # each tensor is its own stream of the generator: the same seed reproduces it alone
+    name, n, off = man[4]
+    assert name == "decoder.layers.1.layers.1.weight"
+    alone = np.empty(n, np.float32)
+    tsn.call("tsn_synth_normal_f32", 7, 4, 0.0, 1.0 / np.sqrt(n / spec.width[1]), n, tsn.ptr(alone))
+    assert np.array_equal(alone, w[off:off + n])
+
+
+def test_vae_spec_from_gguf(tsn, tmp_path):
+    """widths from the conv shapes (ne = K, IC, OC), transposed-conv kernels from ne[0]"""
+    from gguf_writer import F32, write
+    path = str(tmp_path / "v.gguf")
+    w = [128, 64, 64, 64, 64, 64]
+    kt = [16, 16, 8, 8, 6]
+    tensors = [("decoder.layers.0.weight", (7, 64, w[0]), F32, np.zeros(7 * 64 * w[0], np.float32))]
+    for n in range(5):
+        shape = (kt[n], w[n], w[n + 1])
+        tensors.append(("decoder.layers.%d.layers.1.weight" % (n + 1), shape, F32,
+                        np.zeros(int(np.prod(shape)), np.float32)))
+    tensors.append(("decoder.layers.7.weight", (7, 64, 2), F32, np.zeros(7 * 64 * 2, np.float32)))
+    write(path, tensors)
+    s = tsn.vae_spec_from_gguf(path, T=11)
+    assert s.as_dict() == dict(T=11, latent=64, width=w, stride=[8, 8, 4, 4, 2], kt=kt, out_ch=2)
+    # a transposed-conv kernel that is not a multiple of its stride is rejected
+    tensors[1] = ("decoder.layers.1.layers.1.weight", (20, w[0], w[1]), F32, np.zeros(20 * w[0] * w[1], np.float32))
+    write(path, tensors)
+    with pytest.raises(RuntimeError):
+        tsn.vae_spec_from_gguf(path, T=11)

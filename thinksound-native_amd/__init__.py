@@ -65,6 +65,27 @@ class RefDitSpec(ctypes.Structure):
         return s
 
 
+class VaeSpec(ctypes.Structure):
+    """tsn_vae_spec (include/tsn.h): the reference's VAE decoder."""
+    _fields_ = [("T", ctypes.c_int), ("latent", ctypes.c_int), ("width", ctypes.c_int * 6),
+                ("stride", ctypes.c_int * 5), ("kt", ctypes.c_int * 5), ("out_ch", ctypes.c_int)]
+
+    def as_dict(self):
+        return {"T": self.T, "latent": self.latent, "width": list(self.width), "stride": list(self.stride),
+                "kt": list(self.kt), "out_ch": self.out_ch}
+
+    def copy(self, **kw):
+        d = self.as_dict()
+        d.update(kw)
+        s = VaeSpec()
+        s.T, s.latent, s.out_ch = d["T"], d["latent"], d["out_ch"]
+        for i in range(6):
+            s.width[i] = d["width"][i]
+        for i in range(5):
+            s.stride[i], s.kt[i] = d["stride"][i], d["kt"][i]
+        return s
+
+
 class RefCondSpec(ctypes.Structure):
     """tsn_refcond_spec (include/tsn.h): the reference's conditioning prep."""
     _fields_ = [("H", ctypes.c_int), ("F", ctypes.c_int), ("T", ctypes.c_int), ("C", ctypes.c_int),
@@ -173,6 +194,22 @@ _SIGS = {
     "tsn_refcond_prep_conditioning": [_P, _P, _P, _P, _P, _P],
     "tsn_refcond_prep_text_arm": [_P, _P, _P, _P, _P, _P],
     "tsn_refcond_synth_weights": [ctypes.POINTER(RefCondSpec), ctypes.c_uint64, _P],
+    "tsn_vae_spec_for_duration": [_I, ctypes.POINTER(VaeSpec)],
+    "tsn_vae_spec_from_gguf": [ctypes.c_char_p, _I, ctypes.POINTER(VaeSpec)],
+    "tsn_vae_audio_len": [ctypes.POINTER(VaeSpec)],
+    "tsn_vae_manifest_count": [ctypes.POINTER(VaeSpec)],
+    "tsn_vae_manifest_entry": [ctypes.POINTER(VaeSpec), _I, ctypes.c_char_p, _I,
+                               ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)],
+    "tsn_vae_manifest_total": [ctypes.POINTER(VaeSpec)],
+    "tsn_vae_create": [_P, ctypes.POINTER(VaeSpec), ctypes.POINTER(_P)],
+    "tsn_vae_destroy": [_P],
+    "tsn_vae_upload_weights": [_P, _P, _SZ],
+    "tsn_vae_load_gguf": [_P, ctypes.c_char_p],
+    "tsn_vae_decode": [_P, _P, _P],
+    "tsn_vae_capture_decode": [_P, _P, _P],
+    "tsn_vae_replay": [_P],
+    "tsn_vae_profile_decode": [_P, _P, _P, _P, _I, ctypes.POINTER(_I)],
+    "tsn_vae_synth_weights": [ctypes.POINTER(VaeSpec), ctypes.c_uint64, _P],
     "tsn_gguf_open": [ctypes.c_char_p, ctypes.POINTER(_P)],
     "tsn_gguf_close": [_P],
     "tsn_gguf_tensor_count": [_P],
@@ -185,7 +222,8 @@ _SIGS = {
 _RESTYPES = {"tsn_last_error": ctypes.c_char_p, "tsn_last_gpu_ms": ctypes.c_double,
              "tsn_dit_manifest_total": ctypes.c_int64, "tsn_refdit_manifest_total": ctypes.c_int64,
              "tsn_gguf_get_i64": ctypes.c_int64, "tsn_gguf_get_f64": ctypes.c_double,
-             "tsn_refcond_manifest_total": ctypes.c_int64, "tsn_version": _I}
+             "tsn_refcond_manifest_total": ctypes.c_int64, "tsn_version": _I,
+             "tsn_vae_manifest_total": ctypes.c_int64, "tsn_vae_audio_len": ctypes.c_int64}
 
 
 def lib():
@@ -362,6 +400,79 @@ class RefCondModel:
 
     def prep_text_arm(self, text_cat, gtext, clip_fc, text_pp, gcmlp):
         call("tsn_refcond_prep_text_arm", self.h, text_cat.p, gtext.p, clip_fc.p, text_pp.p, gcmlp.p)
+
+
+def vae_spec_for_duration(dur_s):
+    s = VaeSpec()
+    call("tsn_vae_spec_for_duration", dur_s, ctypes.byref(s))
+    return s
+
+
+def vae_spec_from_gguf(path, T=172):
+    """tsn_vae_spec_from_gguf: widths and kernel sizes from a checkpoint, T from the caller."""
+    s = VaeSpec()
+    call("tsn_vae_spec_from_gguf", os.fsencode(path), T, ctypes.byref(s))
+    return s
+
+
+def vae_audio_len(spec):
+    return int(lib().tsn_vae_audio_len(ctypes.byref(spec)))
+
+
+def vae_manifest(spec):
+    L = lib()
+    out, buf = [], ctypes.create_string_buffer(256)
+    for i in range(L.tsn_vae_manifest_count(ctypes.byref(spec))):
+        numel, off = ctypes.c_int64(), ctypes.c_int64()
+        call("tsn_vae_manifest_entry", ctypes.byref(spec), i, buf, 256, ctypes.byref(numel), ctypes.byref(off))
+        out.append((buf.value.decode(), numel.value, off.value))
+    return out
+
+
+def vae_synth_weights(spec, seed=4242):
+    w = np.empty(int(lib().tsn_vae_manifest_total(ctypes.byref(spec))), np.float32)
+    call("tsn_vae_synth_weights", ctypes.byref(spec), seed, ptr(w))
+    return w
+
+
+class VaeModel:
+    """tn::VaeModel mirror (src/models.h:87-94): load, then decode latent -> audio on the device."""
+
+    def __init__(self, rt, spec):
+        self.rt, self.spec = rt, spec
+        h = ctypes.c_void_p()
+        call("tsn_vae_create", rt.h, ctypes.byref(spec), ctypes.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().tsn_vae_destroy(self.h)
+            self.h = None
+
+    def upload_weights(self, w):
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        call("tsn_vae_upload_weights", self.h, ptr(w), w.size)
+
+    def load_gguf(self, path):
+        call("tsn_vae_load_gguf", self.h, os.fsencode(path))
+
+    def decode(self, latent, audio):
+        """latent [T][latent] -> audio [T_audio][out_ch], device arrays, enqueued on the runtime's stream"""
+        call("tsn_vae_decode", self.h, latent.p, audio.p)
+
+    def capture_decode(self, latent, audio):
+        call("tsn_vae_capture_decode", self.h, latent.p, audio.p)
+
+    def replay(self):
+        call("tsn_vae_replay", self.h)
+
+    def profile_decode(self, latent, audio):
+        cap = 64
+        arr = (KernelStat * cap)()
+        n = ctypes.c_int()
+        call("tsn_vae_profile_decode", self.h, latent.p, audio.p, arr, cap, ctypes.byref(n))
+        return [{"name": arr[i].name.decode(), "launches": arr[i].launches, "ms": arr[i].total_ms,
+                 "flops": arr[i].flops, "bytes": arr[i].bytes} for i in range(n.value)]
 
 
 class Gguf:

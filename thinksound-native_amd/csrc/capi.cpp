@@ -1,6 +1,8 @@
 // capi.cpp — extern "C" boundary of libtsn (declarations and reference citations in include/tsn.h).
 #include "../../include/tsn.h"
 
+#include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <new>
@@ -9,6 +11,7 @@
 #include "gguf.h"
 #include "refcond.h"
 #include "refdit.h"
+#include "vae.h"
 
 namespace tsn {
 void synth_normal_f32(uint64_t seed, uint64_t idx, double mean, double std, size_t n, float *out);
@@ -30,6 +33,9 @@ struct tsn_gguf {
 };
 struct tsn_refcond {
     tsn::RefCondModel m;
+};
+struct tsn_vae {
+    tsn::VaeModel m;
 };
 
 #define RT_CHECK(r)                                                 \
@@ -63,6 +69,19 @@ static tsn::RefCondSpec to_cond_spec(const tsn_refcond_spec *c) {
 static void from_cond_spec(const tsn::RefCondSpec &s, tsn_refcond_spec *c) {
     c->H = s.H; c->F = s.F; c->T = s.T; c->C = s.C; c->sync_S = s.sync_S; c->TS = s.TS;
     c->sync_dim = s.sync_dim; c->clip_dim = s.clip_dim; c->text_dim = s.text_dim; c->gtext_dim = s.gtext_dim;
+}
+
+static tsn::VaeSpec to_vae_spec(const tsn_vae_spec *c) {
+    tsn::VaeSpec s;
+    s.T = c->T; s.latent = c->latent; s.out_ch = c->out_ch;
+    for (int i = 0; i < 6; ++i) s.width[i] = c->width[i];
+    for (int i = 0; i < 5; ++i) { s.stride[i] = c->stride[i]; s.kt[i] = c->kt[i]; }
+    return s;
+}
+static void from_vae_spec(const tsn::VaeSpec &s, tsn_vae_spec *c) {
+    c->T = s.T; c->latent = s.latent; c->out_ch = s.out_ch;
+    for (int i = 0; i < 6; ++i) c->width[i] = s.width[i];
+    for (int i = 0; i < 5; ++i) { c->stride[i] = s.stride[i]; c->kt[i] = s.kt[i]; }
 }
 
 static int copy_stats(const std::vector<tsn::KernelStat> &ks, tsn_kernel_stat *stats, int cap, int *n_stats) {
@@ -404,6 +423,89 @@ int tsn_refcond_prep_text_arm(tsn_refcond *d, const float *text_cat, const float
     return d->m.enqueue_prep_text_arm(text_cat, gtext, clip_fc, text_pp, gcmlp);
 }
 
+/* ---------------- VAE decoder ---------------- */
+#define VAE_CHECK(d)                                                          \
+    do {                                                                      \
+        if (!(d)) { tsn::set_error("null vae handle"); return TSN_ERR_ARG; }  \
+    } while (0)
+
+int tsn_vae_spec_for_duration(int dur_s, tsn_vae_spec *out) {
+    if (!out || dur_s <= 0) { tsn::set_error("vae spec: null out pointer or non-positive duration"); return TSN_ERR_ARG; }
+    from_vae_spec(tsn::vae_spec_for_duration(dur_s), out);
+    return TSN_OK;
+}
+int tsn_vae_spec_from_gguf(const char *path, int T, tsn_vae_spec *out) {
+    if (!path || !out) { tsn::set_error("null path or spec"); return TSN_ERR_ARG; }
+    tsn::VaeSpec s;
+    TSN_TRY(tsn::vae_spec_from_gguf(path, T, &s));
+    from_vae_spec(s, out);
+    return TSN_OK;
+}
+int64_t tsn_vae_audio_len(const tsn_vae_spec *spec) {
+    if (!spec) { tsn::set_error("null spec"); return -1; }
+    return tsn::vae_audio_len(to_vae_spec(spec));
+}
+int tsn_vae_manifest_count(const tsn_vae_spec *spec) {
+    if (!spec) { tsn::set_error("null spec"); return -1; }
+    return (int)tsn::vae_manifest(to_vae_spec(spec)).size();
+}
+int tsn_vae_manifest_entry(const tsn_vae_spec *spec, int idx, char *name, int name_cap, int64_t *numel,
+                           int64_t *offset) {
+    if (!spec) { tsn::set_error("null spec"); return TSN_ERR_ARG; }
+    const auto m = tsn::vae_manifest(to_vae_spec(spec));
+    if (idx < 0 || idx >= (int)m.size()) { tsn::set_error("manifest index out of range"); return TSN_ERR_ARG; }
+    if (name && name_cap > 0) snprintf(name, (size_t)name_cap, "%s", m[idx].name.c_str());
+    if (numel) *numel = m[idx].numel;
+    if (offset) *offset = m[idx].offset;
+    return TSN_OK;
+}
+int64_t tsn_vae_manifest_total(const tsn_vae_spec *spec) {
+    if (!spec) { tsn::set_error("null spec"); return -1; }
+    const auto m = tsn::vae_manifest(to_vae_spec(spec));
+    return m.back().offset + m.back().numel;
+}
+int tsn_vae_create(tsn_runtime *rt, const tsn_vae_spec *spec, tsn_vae **out) {
+    RT_CHECK(rt);
+    if (!spec || !out) { tsn::set_error("null spec or out pointer"); return TSN_ERR_ARG; }
+    *out = nullptr;
+    tsn_vae *d = new (std::nothrow) tsn_vae();
+    if (!d) { tsn::set_error("out of host memory"); return TSN_ERR_OOM; }
+    const int rc = d->m.create(&rt->rt, to_vae_spec(spec));
+    if (rc != TSN_OK) { delete d; return rc; }
+    *out = d;
+    return TSN_OK;
+}
+int tsn_vae_destroy(tsn_vae *d) { delete d; return TSN_OK; }
+int tsn_vae_upload_weights(tsn_vae *d, const float *w, size_t numel) {
+    VAE_CHECK(d);
+    return d->m.upload_weights(w, numel);
+}
+int tsn_vae_load_gguf(tsn_vae *d, const char *path) {
+    VAE_CHECK(d);
+    if (!path) { tsn::set_error("null path"); return TSN_ERR_ARG; }
+    return d->m.load_gguf(path);
+}
+int tsn_vae_decode(tsn_vae *d, const float *latent, float *audio) {
+    VAE_CHECK(d);
+    return d->m.enqueue_decode(latent, audio);
+}
+int tsn_vae_capture_decode(tsn_vae *d, const float *latent, float *audio) {
+    VAE_CHECK(d);
+    return d->m.capture([&] { return d->m.enqueue_decode(latent, audio); });
+}
+int tsn_vae_replay(tsn_vae *d) {
+    VAE_CHECK(d);
+    return d->m.replay();
+}
+int tsn_vae_profile_decode(tsn_vae *d, const float *latent, float *audio, tsn_kernel_stat *stats, int cap,
+                           int *n_stats) {
+    if (!d || !stats || !n_stats || cap <= 0) { tsn::set_error("profile: null argument"); return TSN_ERR_ARG; }
+    std::vector<tsn::KernelStat> ks;
+    const int rc = d->m.profile([&] { return d->m.enqueue_decode(latent, audio); }, ks);
+    if (rc != TSN_OK) return rc;
+    return copy_stats(ks, stats, cap, n_stats);
+}
+
 /* ---------------- GGUF reader ---------------- */
 int tsn_gguf_open(const char *path, tsn_gguf **out) {
     if (!path || !out) { tsn::set_error("null path or out pointer"); return TSN_ERR_ARG; }
@@ -519,6 +621,28 @@ int tsn_refcond_synth_weights(const tsn_refcond_spec *spec, uint64_t seed, uint1
     const auto m = tsn::refcond_manifest(to_cond_spec(spec));
     for (size_t i = 0; i < m.size(); ++i)
         tsn::synth_normal_bf16(seed, (uint64_t)i, 0.0, 0.02, (size_t)m[i].numel, out + m[i].offset);
+    return TSN_OK;
+}
+int tsn_vae_synth_weights(const tsn_vae_spec *spec, uint64_t seed, float *out) {
+    if (!spec || !out) { tsn::set_error("null spec or output"); return TSN_ERR_ARG; }
+    const tsn::VaeSpec vs = to_vae_spec(spec);
+    const auto m = tsn::vae_manifest(vs);
+    for (size_t i = 0; i < m.size(); ++i) {
+        const std::string &n = m[i].name;
+        const bool snake = n.size() > 6 && (n.compare(n.size() - 6, 6, ".alpha") == 0 || n.compare(n.size() - 5, 5, ".beta") == 0);
+        const bool bias = n.size() > 5 && n.compare(n.size() - 5, 5, ".bias") == 0;
+        double std = 0.02;
+        if (snake) std = 0.1;
+        else if (!bias) {   // conv weight [OC][IC][K]: fan-in IC*K = numel / OC
+            const int layer = atoi(n.c_str() + strlen("decoder.layers."));
+            const int oc = layer == 0 ? vs.width[0] : layer == 7 ? vs.out_ch : vs.width[layer];
+            std = 1.0 / sqrt((double)m[i].numel / oc);
+            // the residual branch's closing k1 conv at half gain keeps the stream's scale bounded
+            // over the 15 residual units (audio RMS near 1 instead of growing 2x per unit)
+            if (n.size() > 16 && n.compare(n.size() - 16, 16, ".layers.3.weight") == 0) std *= 0.5;
+        }
+        tsn::synth_normal_f32(seed, (uint64_t)i, 0.0, std, (size_t)m[i].numel, out + m[i].offset);
+    }
     return TSN_OK;
 }
 int tsn_dit_synth_weights(const tsn_dit_spec *spec, uint64_t seed, double norm_mean, uint16_t *out) {

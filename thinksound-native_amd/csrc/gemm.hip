@@ -341,6 +341,19 @@ __device__ __forceinline__ void add8(float (&v)[8], const float *p) {
     v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w; v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
 }
 
+// snake activation (shaders/ops_conv.metal:204-213) with exp(alpha) and exp(-beta) precomputed per column
+__device__ __forceinline__ void snake8(float (&v)[8], const float *ea, const float *eb) {
+    const float4 a0 = *(const float4 *)ea, a1 = *(const float4 *)(ea + 4);
+    const float4 b0 = *(const float4 *)eb, b1 = *(const float4 *)(eb + 4);
+    const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const float b[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const float sn = sinf(v[e] * a[e]);
+        v[e] = v[e] + sn * sn * b[e];
+    }
+}
+
 template <int EPI>
 __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float *tile, int m0, int n0, int ks, int tid) {
     const int M = P.M, N = P.N;
@@ -416,6 +429,27 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
                 for (int e = 0; e < 8; ++e) lo[e] = (half_t)(y[e] - (float)o[e]);
                 *(half8 *)(dst + P.y_lo) = lo;
             }
+        }
+    } else if constexpr (EPI == EPI_SNAKE) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int c = tid + 512 * p, row = c >> 4, col = (c & 15) * 8;
+            const int m = m0 + row, n = n0 + col;
+            if (m >= M || n >= N) continue;
+            float v[8];
+            ldsum8(tile, row * TP + col, v);
+            if (P.bias) add8(v, P.bias + n);
+            snake8(v, P.snake + n, P.snake + N + n);
+            half8 hi, lo;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                hi[e] = (half_t)v[e];
+                lo[e] = (half_t)(v[e] - (float)hi[e]);
+            }
+            half_t *y = (half_t *)P.Y + rowmap_phys(P.ymap, m) * (long long)P.ldy + n;
+            *(half8 *)y = hi;
+            *(half8 *)(y + P.y_lo) = lo;
+            *(half8 *)(y + P.y_hi2) = hi;
         }
     } else if constexpr (EPI == EPI_RESID) {
 #pragma unroll
@@ -568,14 +602,17 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
         b_off[i] = n < N ? (n * ldw + lc * 8) * 2 : -1;
     }
     const int lda2 = lda * 2;
-    // K tiles are issued in order kbeg, kbeg + 1, ...: the tap, the offset inside it and the W
-    // column of the next one are carried from call to call (no division in the loop)
-    int nt_tap = kbeg * BK / Kc;
-    int nt_kin = kbeg * BK - nt_tap * Kc;
-    int nt_kw = hl ? nt_tap * hc + ((nt_kin >> 7) << 6) : kbeg * BK;
+    // K tiles are issued in order kbeg, kbeg + 1, ...: the source-row offset of the tap (tap*dil),
+    // the offset inside it and the W column of the next one are carried from call to call (no
+    // division in the loop)
+    const int dil = EPI == EPI_SNAKE ? P.dil : 1;   // dilated taps only in the snake-conv kernels
+    const int tap0 = kbeg * BK / Kc;
+    int nt_trow = tap0 * dil;
+    int nt_kin = kbeg * BK - tap0 * Kc;
+    int nt_kw = hl ? tap0 * hc + ((nt_kin >> 7) << 6) : kbeg * BK;
     auto issue = [&](int kt, int stage) {
         (void)kt;   // = the previous call's kt + 1
-        const int tap = nt_tap, kin = nt_kin, kw = nt_kw;
+        const int trow = nt_trow, kin = nt_kin, kw = nt_kw;
         // hi|lo: K tile j of the tap is chunk j >> 1 of the hi (j even) or lo (j odd) half
         const int odd = (kin >> 6) & 1;
         const int acol = hl ? odd * hc + ((kin >> 7) << 6) : kin;
@@ -583,14 +620,14 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
         nt_kin += BK;
         if (nt_kin == Kc) {
             nt_kin = 0;
-            ++nt_tap;
+            nt_trow += dil;
         }
-        const int kc2 = acol * 2 + tap * lda2;
+        const int kc2 = acol * 2 + trow * lda2;
         lds_char *sa = (lds_char *)(smem + stage * STAGE) + wave * 2048;
         lds_char *sb = (lds_char *)(smem + (NS + stage) * STAGE) + wave * 2048;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int ts = a_ts0[i] + tap;
+            const int ts = a_ts0[i] + trow;
             const unsigned vo = (ts >= 0 && ts < aT) ? (unsigned)(a_base[i] + kc2) : 0x80000000u;
             dma16(rsa, vo, sa + i * 1024);
         }
@@ -848,6 +885,7 @@ int launch_gemm_reduce(const GemmBatch &b, int epi, hipStream_t st) {
         if (epi == EPI_STORE) TSN_LAUNCH((gemm_fixup_kernel<EPI_STORE>), grid, block, 0, st, b);
         else if (epi == EPI_RESID) TSN_LAUNCH((gemm_fixup_kernel<EPI_RESID>), grid, block, 0, st, b);
         else if (epi == EPI_QKV) TSN_LAUNCH((gemm_fixup_kernel<EPI_QKV>), grid, block, 0, st, b);
+        else if (epi == EPI_SNAKE) TSN_LAUNCH((gemm_fixup_kernel<EPI_SNAKE>), grid, block, 0, st, b);
         else TSN_LAUNCH((gemm_fixup_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
         TSN_HIP_CHECK(hipGetLastError());
         return TSN_OK;
@@ -874,13 +912,15 @@ bool gemm_needs_reduce(const GemmBatch &b) {
 const char *gemm_reduce_name(const GemmBatch &b, int epi) {
     if (b.sk)
         return epi == EPI_STORE ? "gemm_fixup_kernel<0>" : epi == EPI_RESID ? "gemm_fixup_kernel<1>"
-               : epi == EPI_QKV ? "gemm_fixup_kernel<2>" : "gemm_fixup_kernel<3>";
+               : epi == EPI_QKV ? "gemm_fixup_kernel<2>" : epi == EPI_SNAKE ? "gemm_fixup_kernel<4>"
+                                                                          : "gemm_fixup_kernel<3>";
     return epi == EPI_RESID ? "splitk_reduce_kernel<1>" : "splitk_reduce_kernel<0>";
 }
 
 void gemm_problem_init(GemmProblem &p) {
     memset(&p, 0, sizeof p);
     p.taps = 1;
+    p.dil = 1;
     p.gate_L = 1;
     p.q_L = 1;
     p.q_scale = 1.0f;
@@ -897,17 +937,26 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         TSN_REQUIRE(p.taps >= 1 && p.Kc * p.taps == p.K, "gemm: K must equal taps*Kc");
         TSN_REQUIRE(p.taps == 1 || p.Kc % BK == 0, "gemm: conv channels must be a multiple of 64");
         TSN_REQUIRE(p.amap.L > 0 && p.a_T > 0, "gemm: row map");
+        if (p.dil < 1) p.dil = 1;
+        TSN_REQUIRE(p.dil == 1 || epi == EPI_SNAKE, "gemm: dilated taps only with the snake epilogue");
         TSN_REQUIRE((((uintptr_t)p.A) & 15) == 0 && (((uintptr_t)p.W) & 15) == 0, "gemm: A and W must be 16-byte aligned");
         if (epi == EPI_STORE) TSN_REQUIRE(p.Y && p.ymap.L > 0, "gemm: output");
         if (p.w_half)
             TSN_REQUIRE(p.Kc % (2 * BK) == 0 && p.ldw >= p.taps * (p.Kc / 2),
                         "gemm: half-width W needs Kc a multiple of 128 and ldw >= taps*Kc/2");
-        if (p.y_lo) {
+        if (p.y_lo && epi != EPI_SNAKE) {
             const int wout = epi == EPI_SWIGLU ? p.N / 2 : p.N;
             TSN_REQUIRE((epi == EPI_STORE || epi == EPI_SWIGLU) && p.y_f16 && p.y_lo % 8 == 0 && p.y_lo >= wout &&
                             p.ldy >= p.y_lo + wout,
                         "gemm: hi|lo output needs f16 Y, lo offset a multiple of 8 past the hi columns, ldy >= y_lo + width");
         }
+        if (epi == EPI_SNAKE)
+            TSN_REQUIRE(p.Y && p.ymap.L > 0 && p.snake && (((uintptr_t)p.snake) & 15) == 0 && p.N % 8 == 0 &&
+                            p.y_lo % 8 == 0 && p.y_hi2 % 8 == 0 && p.y_lo >= p.N && p.y_hi2 >= p.y_lo + p.N &&
+                            p.ldy >= p.y_hi2 + p.N && p.ldy % 8 == 0 && !p.w_half,
+                        "gemm snake: table, three 8-aligned N-wide parts (hi, lo at y_lo, hi at y_hi2) inside ldy");
+        else
+            TSN_REQUIRE(!p.snake && !p.y_hi2, "gemm: snake table and second hi part only with the snake epilogue");
         if (epi == EPI_SWIGLU)
             TSN_REQUIRE(p.Y && p.ymap.L > 0 && p.y_f16 && p.N % BN == 0 && p.ldy % 8 == 0 &&
                             (((uintptr_t)p.Y) & 15) == 0,
@@ -937,6 +986,7 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
                (((uintptr_t)p.bias) & 15) == 0;
         // the C-tile epilogue writes 8 columns with 16-byte accesses
         if (epi == EPI_STORE) pipe = pipe && (((uintptr_t)p.Y) & 15) == 0 && p.ldy % (p.y_f16 ? 8 : 4) == 0;
+        if (epi == EPI_SNAKE) pipe = pipe && (((uintptr_t)p.Y) & 15) == 0;
         if (epi == EPI_RESID)
             pipe = pipe && (((uintptr_t)p.R) & 15) == 0 && (((uintptr_t)p.gate) & 15) == 0 && p.ldr % 4 == 0 &&
                    p.gate_ld % 4 == 0;
@@ -958,6 +1008,7 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     bool any_half = false;
     for (int i = 0; i < b.nprob; ++i) any_half = any_half || b.p[i].w_half;
     TSN_REQUIRE(pipe || !any_lo, "gemm: hi|lo output needs the pipelined kernel (f16 A, 16-byte aligned rows)");
+    TSN_REQUIRE(pipe || epi != EPI_SNAKE, "gemm snake: needs the pipelined kernel (f16 A, 16-byte aligned rows)");
     TSN_REQUIRE(pipe || !any_half, "gemm: half-width W needs the pipelined kernel (f16 A, 16-byte aligned rows)");
     if (pipe && (epi == EPI_RESID || epi == EPI_STORE) && b.ws && !any_lo) {
         int nkmin = 1 << 30;
@@ -1036,17 +1087,21 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     TSN_REQUIRE(pipe || epi != EPI_SWIGLU, "gemm swiglu: needs K and row strides the pipelined kernel takes");
     b.pipe = pipe ? 1 : 0;
     b.hl = any_half ? 1 : 0;
+    TSN_REQUIRE(epi != EPI_SNAKE || !b.hl, "gemm snake: no half-width W");
     b.kname = b.sk ? (epi == EPI_STORE ? "gemm_sk_kernel<0>" : epi == EPI_RESID ? "gemm_sk_kernel<1>"
-                      : epi == EPI_QKV ? "gemm_sk_kernel<2>" : "gemm_sk_kernel<3>")
+                      : epi == EPI_QKV ? "gemm_sk_kernel<2>" : epi == EPI_SNAKE ? "gemm_sk_kernel<4>"
+                                                                                : "gemm_sk_kernel<3>")
             : pipe && b.hl ? (epi == EPI_STORE ? "gemm_pipe_hl_kernel<0>" : epi == EPI_RESID ? "gemm_pipe_hl_kernel<1>"
                               : epi == EPI_QKV ? "gemm_pipe_hl_kernel<2>" : "gemm_pipe_hl_kernel<3>")
             : pipe ? (epi == EPI_STORE ? "gemm_pipe_kernel<0>" : epi == EPI_RESID ? "gemm_pipe_kernel<1>"
-                      : epi == EPI_QKV ? "gemm_pipe_kernel<2>" : "gemm_pipe_kernel<3>")
+                      : epi == EPI_QKV ? "gemm_pipe_kernel<2>" : epi == EPI_SNAKE ? "gemm_pipe_kernel<4>"
+                                                                                  : "gemm_pipe_kernel<3>")
                    : a_f32 ? "gemm_f16_kernel<true, 0>"
                    : (epi == EPI_STORE ? "gemm_f16_kernel<false, 0>" : epi == EPI_RESID ? "gemm_f16_kernel<false, 1>"
                                                                         : "gemm_f16_kernel<false, 2>");
     if (a_f32) TSN_REQUIRE(epi == EPI_STORE, "gemm: f32 A operand only with a plain store epilogue");
-    TSN_REQUIRE(epi == EPI_STORE || epi == EPI_RESID || epi == EPI_QKV || epi == EPI_SWIGLU, "gemm: unknown epilogue");
+    TSN_REQUIRE(epi == EPI_STORE || epi == EPI_RESID || epi == EPI_QKV || epi == EPI_SWIGLU || epi == EPI_SNAKE,
+                "gemm: unknown epilogue");
     return TSN_OK;
 }
 
@@ -1058,6 +1113,7 @@ int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st)
             else if (epi == EPI_RESID) TSN_LAUNCH((gemm_sk_kernel<EPI_RESID>), grid, block, 0, st, b);
             else if (epi == EPI_QKV) TSN_LAUNCH((gemm_sk_kernel<EPI_QKV>), grid, block, 0, st, b);
             else if (epi == EPI_SWIGLU) TSN_LAUNCH((gemm_sk_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
+            else if (epi == EPI_SNAKE) TSN_LAUNCH((gemm_sk_kernel<EPI_SNAKE>), grid, block, 0, st, b);
             else { set_error("gemm: unknown epilogue"); return TSN_ERR_ARG; }
         } else if (b.hl) {
             if (epi == EPI_STORE) TSN_LAUNCH((gemm_pipe_hl_kernel<EPI_STORE>), grid, block, 0, st, b);
@@ -1069,6 +1125,7 @@ int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st)
         else if (epi == EPI_RESID) TSN_LAUNCH((gemm_pipe_kernel<EPI_RESID>), grid, block, 0, st, b);
         else if (epi == EPI_QKV) TSN_LAUNCH((gemm_pipe_kernel<EPI_QKV>), grid, block, 0, st, b);
         else if (epi == EPI_SWIGLU) TSN_LAUNCH((gemm_pipe_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
+        else if (epi == EPI_SNAKE) TSN_LAUNCH((gemm_pipe_kernel<EPI_SNAKE>), grid, block, 0, st, b);
         else { set_error("gemm: unknown epilogue"); return TSN_ERR_ARG; }
     } else if (a_f32) {
         TSN_LAUNCH((gemm_f16_kernel<true, EPI_STORE>), grid, block, 0, st, b);

@@ -80,10 +80,11 @@ int GraphRunner::profile(const std::function<int()> &enqueue, std::vector<Kernel
     return rc2;
 }
 
-int GraphRunner::gemm_run(GemmBatch &b, int epi) {
+int GraphRunner::gemm_run(GemmBatch &b, int epi, double flop_scale) {
     const hipStream_t st = rt->dev.stream();
     TSN_TRY(gemm_plan(b, epi, false));
-    TSN_TRY(run(b.kname, gemm_flops(b), gemm_bytes(b, epi), [&] { return gemm_launch_planned(b, epi, false, st); }));
+    TSN_TRY(run(b.kname, gemm_flops(b) * flop_scale, gemm_bytes(b, epi),
+                [&] { return gemm_launch_planned(b, epi, false, st); }));
     if (!gemm_needs_reduce(b)) return TSN_OK;
     double red = 0;
     for (int i = 0; i < b.nprob; ++i)
@@ -135,7 +136,8 @@ double gemm_bytes(const GemmBatch &b, int epi) {
     double x = 0;
     for (int i = 0; i < b.nprob; ++i) {
         const GemmProblem &p = b.p[i];
-        double out = epi == EPI_RESID ? 8.0 : epi == EPI_SWIGLU ? 1.0 : (p.y_f16 || epi == EPI_QKV ? 2.0 : 4.0);
+        double out = epi == EPI_RESID ? 8.0 : epi == EPI_SWIGLU ? 1.0 : epi == EPI_SNAKE ? 6.0
+                   : (p.y_f16 || epi == EPI_QKV ? 2.0 : 4.0);
         if (p.y_lo) out *= 2.0;
         x += 2.0 * p.M * (double)p.Kc + 2.0 * p.N * (double)p.K / (p.w_half ? 2 : 1) + out * p.M * (double)p.N;
     }

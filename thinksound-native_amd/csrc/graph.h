@@ -79,8 +79,9 @@ protected:
         prof_->push_back(r);
         return rc;
     }
-    // plan, launch (timed under the kernel's own symbol) and, when K was split, reduce
-    int gemm_run(GemmBatch &b, int epi);
+    // plan, launch (timed under the kernel's own symbol) and, when K was split, reduce; the
+    // profiled algorithmic flops are gemm_flops(b) * flop_scale
+    int gemm_run(GemmBatch &b, int epi, double flop_scale = 1.0);
     // residual GEMM batch + one reduce kernel that finishes the split-K sum into X and applies
     // the adaLN set up in r (segment i covers problem i's rows)
     int resid_ln(GemmBatch &b, RedLnArgs &r, int H, float eps);

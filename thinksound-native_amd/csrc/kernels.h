@@ -9,14 +9,15 @@ namespace tsn {
 /* ------------------------------------------------------------------ GEMM (MFMA) */
 // C[M,N] = A[M,K] · W[N,K]ᵀ with f16 operands and f32 accumulation; 128x128x64 tiles,
 // v_mfma_f32_16x16x32_f16 (pipelined kernel: 8 waves, 5 direct-to-LDS stages).
-enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_SWIGLU = 3 };
+enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_SWIGLU = 3, EPI_SNAKE = 4 };
 
 struct GemmProblem {
     // A operand rows (f16, or f32 converted on load): row m -> rowmap_phys(amap, m).
     const void *A; int lda; RowMap amap;
     // Convolution view of K: K = taps*Kc; column k reads channel k % Kc of source row
-    // t - pad + k / Kc of the same sample, zero outside [0, a_T). taps = 1, pad = 0 is a GEMM.
-    int taps, Kc, pad, a_T;
+    // t - pad + (k / Kc)*dil of the same sample, zero outside [0, a_T). taps = 1, pad = 0 is a GEMM.
+    // dil > 1 (dilated taps) only with EPI_SNAKE.
+    int taps, Kc, pad, a_T, dil;
     const half_t *W; int ldw;          // [N][K] row-major
     // w_half: the A operand is an f16 hi|lo pair per tap (Kc = 2*IC: hi channels, then lo) and W
     // holds IC channels per tap ([N][taps][IC], ldw >= taps*IC); both halves read the same W columns
@@ -30,6 +31,12 @@ struct GemmProblem {
     // f16 Y (EPI_STORE, EPI_SWIGLU): nonzero also writes lo = f16(y - f16(y)) at column offset y_lo
     // of the same row (hi|lo operand of a following GEMM against [W | W]); K is then never split
     int y_lo;
+    // EPI_SNAKE: y = snake(acc + bias) = v + sin(v*ea[n])^2 * eb[n] with snake = [ea (N) | eb (N)],
+    // stored f16 as a three-part row: hi at column n, lo = f16(y - hi) at n + y_lo, hi again at
+    // n + y_hi2 ([hi | lo | hi], the operand of a following GEMM against [W_hi | W_hi | W_lo]);
+    // K is never split
+    int y_hi2;
+    const float *snake;
     // EPI_RESID: R[rmap(m)*ldr + n] += gate[(m / gate_L)*gate_ld + n] * (acc + bias)
     float *R; int ldr; RowMap rmap; const float *gate; int gate_ld; int gate_L;
     // EPI_QKV: columns [0,Hq) q, [Hq,2Hq) k, [2Hq,3Hq) v; heads of hd = 64 columns.
@@ -204,6 +211,13 @@ int launch_bcast_add_silu_f16(const float *x, const float *v, half_t *y, int L, 
 
 // out [M][2K] f16 hi|lo of x[m][k] + pe[m % P][k] (pe null: x alone)
 int launch_add_period_hilo(const float *x, const float *pe, int P, half_t *out, int M, int K, hipStream_t st);
+// VAE decoder (vae.hip). split3: f32 rows [rows][C] (C % 8 == 0) -> f16 [rows][3C], v = x or, with a
+// table ab = [exp(alpha) (C) | exp(-beta) (C)], snake(x) = x + sin(x*ea)^2*eb; parts [hi | lo | hi]
+// (lo_part 1, activation operand) or [hi | hi | lo] (lo_part 2, weight operand)
+int launch_split3(const float *x, long long rows, int C, const float *ab, int lo_part, half_t *out, hipStream_t st);
+// y [T][OC] = conv(snake(x), W [OC][C][KK], pad), no bias; x [T][C] f32, OC in {1, 2, 4}, C % 64 == 0
+int launch_conv_out(const float *x, const float *ab, const float *W, float *y, int T, int C, int OC, int KK, int pad,
+                    hipStream_t st);
 // dst[i][:] = src[idx[i]][:] for rows x H floats (idx on the device, every entry a valid src row)
 int launch_gather_rows(const float *src, const int32_t *idx, float *dst, int rows, int H, hipStream_t st);
 // out[c] = mean over rows of x[r][c], rows summed in order (src/net.mm Runtime::mean_cols)

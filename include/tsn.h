@@ -293,6 +293,66 @@ int tsn_vae_replay(tsn_vae *v);
 int tsn_vae_profile_decode(tsn_vae *v, const float *latent, float *audio, tsn_kernel_stat *stats, int cap,
                            int *n_stats);
 
+/* ---------------- text encoders: tn::ClipModel, tn::T5Model (src/models.h:24-52) ----------------
+ * f32 throughout, as the reference loads both (src/clip.cpp:7, src/t5.cpp:22): f32 MFMA GEMMs, f32
+ * attention over the 77-token context. ids are host arrays (the reference's std::vector<int32_t>);
+ * outputs are device pointers enqueued on the runtime's stream. */
+typedef struct {
+    int H, NL, NH, ctx, vocab;   /* 1024, 24 layers, 16 heads, 77 tokens, 49408 (clip.* metadata) */
+    float eps;                   /* LayerNorm eps 1e-5 */
+} tsn_clip_spec;
+typedef struct {
+    int d, d_ff, NL, NH, ctx, vocab;   /* 2048, 5120, 24 layers, 32 heads, 77, 32128 (t5.* metadata) */
+    int n_bucket, max_dist;            /* relative-position buckets 32, max distance 128 */
+    float eps;                         /* RMSNorm eps 1e-6 */
+} tsn_t5_spec;
+typedef struct tsn_clip tsn_clip;
+typedef struct tsn_t5 tsn_t5;
+int tsn_clip_spec_default(tsn_clip_spec *out);
+int tsn_clip_spec_from_gguf(const char *path, tsn_clip_spec *out);   /* ClipModel::load src/clip.cpp:6-32 */
+int tsn_clip_manifest_count(const tsn_clip_spec *spec);
+int tsn_clip_manifest_entry(const tsn_clip_spec *spec, int idx, char *name, int name_cap, int64_t *numel,
+                            int64_t *offset);
+int64_t tsn_clip_manifest_total(const tsn_clip_spec *spec);
+int tsn_clip_create(tsn_runtime *rt, const tsn_clip_spec *spec, tsn_clip **out);
+int tsn_clip_destroy(tsn_clip *c);
+int tsn_clip_upload_weights(tsn_clip *c, const float *weights_host, size_t numel);   /* flat f32, manifest order */
+int tsn_clip_load_gguf(tsn_clip *c, const char *path);
+/* ClipModel::encode (src/clip.cpp:34-92): ids [ctx] -> per_token [ctx][H], global [H] */
+int tsn_clip_encode(tsn_clip *c, const int32_t *ids_host, float *per_token, float *global);
+int tsn_clip_profile_encode(tsn_clip *c, const int32_t *ids_host, float *per_token, float *global,
+                            tsn_kernel_stat *stats, int cap, int *n_stats);
+int tsn_t5_spec_default(tsn_t5_spec *out);
+int tsn_t5_spec_from_gguf(const char *path, tsn_t5_spec *out);   /* T5Model::load src/t5.cpp:21-55 */
+int tsn_t5_manifest_count(const tsn_t5_spec *spec);
+int tsn_t5_manifest_entry(const tsn_t5_spec *spec, int idx, char *name, int name_cap, int64_t *numel,
+                          int64_t *offset);
+int64_t tsn_t5_manifest_total(const tsn_t5_spec *spec);
+int tsn_t5_create(tsn_runtime *rt, const tsn_t5_spec *spec, tsn_t5 **out);
+int tsn_t5_destroy(tsn_t5 *t);
+int tsn_t5_upload_weights(tsn_t5 *t, const float *weights_host, size_t numel);
+int tsn_t5_load_gguf(tsn_t5 *t, const char *path);   /* Q8_0 / F16 / F32 tensors dequantized to f32 */
+/* T5Model::encode (src/t5.cpp:88-131): ids [ctx] -> out [ctx][d] */
+int tsn_t5_encode(tsn_t5 *t, const int32_t *ids_host, float *out);
+int tsn_t5_profile_encode(tsn_t5 *t, const int32_t *ids_host, float *out, tsn_kernel_stat *stats, int cap,
+                          int *n_stats);
+/* the relative-position bucket of rel = key - query (t5_bucket, src/t5.cpp:6-19) */
+int tsn_t5_bucket(int rel, int n_bucket, int max_dist);
+
+/* ---------------- tokenizers: tn::ClipTokenizer, tn::T5Tokenizer (src/tokenizers.h:12-31) ----------------
+ * Host only. Vocabularies come from the tokenizer GGUFs' array metadata. */
+typedef struct tsn_clip_tokenizer tsn_clip_tokenizer;
+typedef struct tsn_t5_tokenizer tsn_t5_tokenizer;
+int tsn_clip_tokenizer_load(const char *path, tsn_clip_tokenizer **out);   /* ClipTokenizer::load */
+int tsn_clip_tokenizer_destroy(tsn_clip_tokenizer *t);
+/* ClipTokenizer::encode: writes exactly ctx ids (bos, BPE tokens, eos, eos padding) */
+int tsn_clip_tokenizer_encode(const tsn_clip_tokenizer *t, const char *text, int ctx, int32_t *ids);
+int tsn_t5_tokenizer_load(const char *path, tsn_t5_tokenizer **out);   /* T5Tokenizer::load */
+int tsn_t5_tokenizer_destroy(tsn_t5_tokenizer *t);
+/* T5Tokenizer::encode: up to ctx ids (pad != 0 pads with pad_id to ctx); *n_ids = count written */
+int tsn_t5_tokenizer_encode(const tsn_t5_tokenizer *t, const char *text, int ctx, int pad, int32_t *ids,
+                            int *n_ids);
+
 /* ---------------- GGUF checkpoint reader: tn::GgufFile / tn::to_f32 (src/gguf.h:42-86) ----------------
  * mmap, GGUF v2/v3, typed metadata, tensor infos with ne[0] fastest, data at general.alignment. */
 typedef struct tsn_gguf tsn_gguf;
@@ -318,6 +378,10 @@ int tsn_refcond_synth_weights(const tsn_refcond_spec *spec, uint64_t seed, uint1
 /* VAE: conv weights N(0, 1/(IC*K)) (residual-branch k1 convs N(0, 0.25/IC)), biases N(0, 0.02), snake
  * alpha and beta N(0, 0.1); f32 */
 int tsn_vae_synth_weights(const tsn_vae_spec *spec, uint64_t seed, float *out_host);
+/* text encoders: embeddings N(0, 1), norm weights 1 + N(0, 0.1), biases N(0, 0.02), projections into the
+ * residual stream N(0, 0.25/fan_in), other linear weights N(0, 1/fan_in), T5 relative bias N(0, 0.25); f32 */
+int tsn_clip_synth_weights(const tsn_clip_spec *spec, uint64_t seed, float *out_host);
+int tsn_t5_synth_weights(const tsn_t5_spec *spec, uint64_t seed, float *out_host);
 
 #ifdef __cplusplus
 }

@@ -193,6 +193,33 @@ void orc_conv1d_t(const float *W, const float *bias, const float *x, float *y, i
 // VaeModel::decode (src/vae.cpp:17-86): latent [T, latent] -> audio [T*prod(stride), out_ch]
 void orc_vae_decode(const orc_vae_spec *s, const float *weights, const float *latent, float *audio);
 
+/* ---------------- the reference's text encoders (oracle_enc.cpp) ---------------- */
+
+typedef struct { int H, NL, NH, ctx, vocab; float eps; } orc_clip_spec;
+typedef struct { int d, d_ff, NL, NH, ctx, vocab, n_bucket, max_dist; float eps; } orc_t5_spec;
+
+int orc_clip_manifest_count(const orc_clip_spec *s);
+int64_t orc_clip_manifest_numel(const orc_clip_spec *s, int idx);
+void orc_clip_manifest_name(const orc_clip_spec *s, int idx, char *buf, int cap);
+int orc_t5_manifest_count(const orc_t5_spec *s);
+int64_t orc_t5_manifest_numel(const orc_t5_spec *s, int idx);
+void orc_t5_manifest_name(const orc_t5_spec *s, int idx, char *buf, int cap);
+// LayerNorm with weight and bias (shaders/ops_conv.metal:90-103), RMSNorm with weight (:104-113)
+void orc_ln_wb(const float *x, float *y, const float *w, const float *b, int rows, int H, float eps);
+void orc_rms_w(const float *x, float *y, const float *w, int rows, int H, float eps);
+// bidirectional relative-position bucket of rel = key - query (src/t5.cpp:6-19)
+int orc_t5_bucket(int rel, int num_buckets, int max_dist);
+// attention with the reference's bias modes (shaders/gemm_attn.metal:84-202): 1 T5 (pad keys
+// masked, bucketed bias rel[bucket*nh + h]), 2 CLIP (k <= q and k <= eot), 0 none
+void orc_enc_attention(const float *qkv, float *out, int S, int nh, int hd, int ld, int q_off, int k_off, int v_off,
+                       int ldo, float scale, int mode, const int32_t *bucket, const float *rel, const int32_t *pad,
+                       int eot);
+// ClipModel::encode (src/clip.cpp:34-92): ids [ctx] -> per_token [ctx, H], global [H]
+void orc_clip_encode(const orc_clip_spec *s, const float *weights, const int32_t *ids, float *per_token,
+                     float *global);
+// T5Model::encode (src/t5.cpp:88-131): ids [ctx] -> out [ctx, d]
+void orc_t5_encode(const orc_t5_spec *s, const float *weights, const int32_t *ids, float *out);
+
 // number of OpenMP threads the oracle uses (for the CPU-baseline report)
 int orc_num_threads(void);
 

@@ -42,6 +42,17 @@ class VaeSpec(ctypes.Structure):
     _fields_ = [("T", _I), ("latent", _I), ("width", _I * 6), ("stride", _I * 5), ("kt", _I * 5), ("out_ch", _I)]
 
 
+class ClipSpec(ctypes.Structure):
+    """orc_clip_spec: the reference's CLIP text encoder"""
+    _fields_ = [("H", _I), ("NL", _I), ("NH", _I), ("ctx", _I), ("vocab", _I), ("eps", _F)]
+
+
+class T5Spec(ctypes.Structure):
+    """orc_t5_spec: the reference's T5 v1.1 encoder"""
+    _fields_ = [("d", _I), ("d_ff", _I), ("NL", _I), ("NH", _I), ("ctx", _I), ("vocab", _I), ("n_bucket", _I),
+                ("max_dist", _I), ("eps", _F)]
+
+
 _SIGS = {
     "orc_gemm": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I],
     "orc_gemv": [_P, _P, _P, _P, _I, _I, _I],
@@ -84,11 +95,25 @@ _SIGS = {
     "orc_snake": [_P, _P, _P, _P, _I, _I],
     "orc_conv1d_t": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I],
     "orc_vae_decode": [ctypes.POINTER(VaeSpec), _P, _P, _P],
+    "orc_clip_manifest_count": [ctypes.POINTER(ClipSpec)],
+    "orc_clip_manifest_numel": [ctypes.POINTER(ClipSpec), _I],
+    "orc_clip_manifest_name": [ctypes.POINTER(ClipSpec), _I, ctypes.c_char_p, _I],
+    "orc_t5_manifest_count": [ctypes.POINTER(T5Spec)],
+    "orc_t5_manifest_numel": [ctypes.POINTER(T5Spec), _I],
+    "orc_t5_manifest_name": [ctypes.POINTER(T5Spec), _I, ctypes.c_char_p, _I],
+    "orc_ln_wb": [_P, _P, _P, _P, _I, _I, _F],
+    "orc_rms_w": [_P, _P, _P, _I, _I, _F],
+    "orc_t5_bucket": [_I, _I, _I],
+    "orc_enc_attention": [_P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _I, _P, _P, _P, _I],
+    "orc_clip_encode": [ctypes.POINTER(ClipSpec), _P, _P, _P, _P],
+    "orc_t5_encode": [ctypes.POINTER(T5Spec), _P, _P, _P],
 }
 _RES = {"orc_manifest_count": _I, "orc_manifest_numel": ctypes.c_int64, "orc_manifest_total": ctypes.c_int64,
         "orc_num_threads": _I, "orc_ref_manifest_count": _I, "orc_ref_manifest_numel": ctypes.c_int64,
         "orc_refcond_manifest_count": _I, "orc_refcond_manifest_numel": ctypes.c_int64,
-        "orc_vae_manifest_count": _I, "orc_vae_manifest_numel": ctypes.c_int64, "orc_vae_audio_len": ctypes.c_int64}
+        "orc_vae_manifest_count": _I, "orc_vae_manifest_numel": ctypes.c_int64, "orc_vae_audio_len": ctypes.c_int64,
+        "orc_clip_manifest_count": _I, "orc_clip_manifest_numel": ctypes.c_int64,
+        "orc_t5_manifest_count": _I, "orc_t5_manifest_numel": ctypes.c_int64, "orc_t5_bucket": _I}
 
 _lib = None
 
@@ -115,7 +140,8 @@ def p(a):
     if a is None:
         return None
     assert a.dtype in (np.float32, np.int32) and a.flags["C_CONTIGUOUS"], (a.dtype, a.flags)
-    return ctypes.c_void_p(a.ctypes.data)
+    # data_as keeps a reference to the array, so a temporary made by f32() lives through the call
+    return a.ctypes.data_as(ctypes.c_void_p)
 
 
 def f32(a):
@@ -403,27 +429,202 @@ def vae_audio_len(spec):
 
 def snake(x, alpha, beta):
     """x [S, C] -> x + sin(x*exp(alpha))^2 * exp(-beta)"""
-    x = f32(x)
+    x, alpha, beta = f32(x), f32(alpha), f32(beta)
     S, C = x.shape
     y = np.empty_like(x)
-    lib().orc_snake(p(x), p(y), p(f32(alpha)), p(f32(beta)), S, C)
+    lib().orc_snake(p(x), p(y), p(alpha), p(beta), S, C)
     return y
 
 
 def conv1d_t(W, bias, x, stride, pad):
     """reference-form transposed conv: W [OC][IC][K], x [T, IC] -> y [T*stride, OC]"""
     W, x = f32(W), f32(x)
+    bias = None if bias is None else f32(bias)
     OC, IC, K = W.shape
     T = x.shape[0]
     y = np.empty((T * stride, OC), np.float32)
-    lib().orc_conv1d_t(p(W), p(f32(bias)) if bias is not None else None, p(x), p(y), T, T * stride, IC, OC, K,
-                       stride, pad)
+    lib().orc_conv1d_t(p(W), p(bias), p(x), p(y), T, T * stride, IC, OC, K, stride, pad)
     return y
 
 
 def vae_decode(spec, W, latent):
     """latent [T, latent] -> audio [T_audio, out_ch]"""
     s = vae_spec_from(spec)
+    W, latent = f32(W), f32(latent)
     audio = np.empty((vae_audio_len(s), s.out_ch), np.float32)
-    lib().orc_vae_decode(ctypes.byref(s), p(f32(W)), p(f32(latent)), p(audio))
+    lib().orc_vae_decode(ctypes.byref(s), p(W), p(latent), p(audio))
     return audio
+
+
+# ---------------- the reference's text encoders ----------------
+def _spec(cls, spec):
+    if isinstance(spec, cls):
+        return spec
+    d = spec if isinstance(spec, dict) else {k: getattr(spec, k) for k, _ in cls._fields_}
+    return cls(**{k: d[k] for k, _ in cls._fields_})
+
+
+def _manifest(prefix, cls, spec):
+    s = _spec(cls, spec)
+    L = lib()
+    out, buf = [], ctypes.create_string_buffer(256)
+    off = 0
+    for i in range(getattr(L, prefix + "_manifest_count")(ctypes.byref(s))):
+        getattr(L, prefix + "_manifest_name")(ctypes.byref(s), i, buf, 256)
+        n = getattr(L, prefix + "_manifest_numel")(ctypes.byref(s), i)
+        out.append((buf.value.decode(), n, off))
+        off += n
+    return out
+
+
+def clip_manifest(spec):
+    return _manifest("orc_clip", ClipSpec, spec)
+
+
+def t5_manifest(spec):
+    return _manifest("orc_t5", T5Spec, spec)
+
+
+def ln_wb(x, w, b, eps):
+    x, w, b = f32(x), f32(w), f32(b)
+    y = np.empty_like(x)
+    lib().orc_ln_wb(p(x), p(y), p(w), p(b), x.shape[0], x.shape[1], eps)
+    return y
+
+
+def rms_w(x, w, eps):
+    x, w = f32(x), f32(w)
+    y = np.empty_like(x)
+    lib().orc_rms_w(p(x), p(y), p(w), x.shape[0], x.shape[1], eps)
+    return y
+
+
+def t5_bucket(rel, n_bucket=32, max_dist=128):
+    return lib().orc_t5_bucket(rel, n_bucket, max_dist)
+
+
+def enc_attention(qkv, nh, scale, mode, bucket=None, rel=None, pad=None, eot=0, hd=64):
+    """qkv [S, 3*nh*hd] (q | k | v) -> out [S, nh*hd]"""
+    qkv = f32(qkv)
+    S = qkv.shape[0]
+    H = nh * hd
+    out = np.empty((S, H), np.float32)
+    bucket = None if bucket is None else np.ascontiguousarray(bucket, np.int32)
+    pad = None if pad is None else np.ascontiguousarray(pad, np.int32)
+    rel = None if rel is None else f32(rel)
+    lib().orc_enc_attention(p(qkv), p(out), S, nh, hd, 3 * H, 0, H, 2 * H, H, scale, mode, p(bucket), p(rel), p(pad),
+                            eot)
+    return out
+
+
+def clip_encode(spec, W, ids):
+    """ids [ctx] -> per_token [ctx, H], global [H]"""
+    s = _spec(ClipSpec, spec)
+    ids, W = np.ascontiguousarray(ids, np.int32), f32(W)
+    per_token = np.empty((s.ctx, s.H), np.float32)
+    glob = np.empty(s.H, np.float32)
+    lib().orc_clip_encode(ctypes.byref(s), p(W), p(ids), p(per_token), p(glob))
+    return per_token, glob
+
+
+def t5_encode(spec, W, ids):
+    """ids [ctx] -> out [ctx, d]"""
+    s = _spec(T5Spec, spec)
+    ids, W = np.ascontiguousarray(ids, np.int32), f32(W)
+    out = np.empty((s.ctx, s.d), np.float32)
+    lib().orc_t5_encode(ctypes.byref(s), p(W), p(ids), p(out))
+    return out
+
+
+# ---------------- tokenizers: pure-Python restatement (src/tokenizers.cpp) ----------------
+def _byte_symbols():
+    """GPT-2 byte alphabet: printable bytes map to themselves, the rest to U+0100.. in byte order"""
+    keep = set(range(ord("!"), ord("~") + 1)) | set(range(0xA1, 0xAD)) | set(range(0xAE, 0x100))
+    out, nxt = {}, 256
+    for b in range(256):
+        if b in keep:
+            out[b] = chr(b)
+        else:
+            out[b] = chr(nxt)
+            nxt += 1
+    return out
+
+
+def clip_bpe_encode(vocab, merges, text, ctx, bos=49406, eos=49407):
+    """ClipTokenizer::encode (src/tokenizers.cpp:61-96): ASCII-lowercased, split on C-locale
+    whitespace, bytes -> symbols, '</w>' on the last, repeatedly merge the lowest-ranked adjacent
+    pair (leftmost among equal ranks), look up (unknown symbols dropped), bos ... eos, cut / pad"""
+    ids_of = {}
+    for i, v in enumerate(vocab):
+        ids_of[v] = i
+    rank = {}
+    for i, m in enumerate(merges):
+        rank[m] = i
+    bsym = _byte_symbols()
+    low = "".join(chr(ord(c) + 32) if "A" <= c <= "Z" else c for c in text)
+    words = [w for w in "".join(" " if c in " \t\n\v\f\r" else c for c in low).split(" ") if w]
+    ids = [bos]
+    for w in words:
+        sym = [bsym[b] for b in w.encode("utf-8", "surrogateescape")]
+        sym[-1] += "</w>"
+        while len(sym) > 1:
+            best, at = None, None
+            for i in range(len(sym) - 1):
+                r = rank.get(sym[i] + " " + sym[i + 1])
+                if r is not None and (best is None or r < best):
+                    best, at = r, i
+            if best is None:
+                break
+            sym[at:at + 2] = [sym[at] + sym[at + 1]]
+        ids += [ids_of[t] for t in sym if t in ids_of]
+    ids.append(eos)
+    if len(ids) > ctx:
+        ids = ids[:ctx]
+        ids[-1] = eos
+    return ids + [eos] * (ctx - len(ids))
+
+
+def t5_unigram_encode(pieces, scores, text, ctx, pad, unk_id=2, eos_id=1, pad_id=0):
+    """T5Tokenizer::encode (src/tokenizers.cpp:98-140): trimmed, U+2581 for spaces and at the start,
+    Viterbi over pieces (strictly better replaces; unknown chars at min(min score, 0) - 10), eos"""
+    idx = {}
+    for i, pc in enumerate(pieces):
+        idx[pc] = i
+    sc = list(scores) + [0.0] * (len(pieces) - len(scores))
+    unk = min([0.0] + [float(x) for x in sc]) - 10.0
+    t = "\u2581" + text.strip(" \t\n").replace(" ", "\u2581")
+    chars = list(t)
+    L = len(chars)
+    best = [-1e18] * (L + 1)
+    frm = [-1] * (L + 1)
+    tok = [-1] * (L + 1)
+    best[0] = 0.0
+    for i in range(L):
+        if best[i] <= -1e17:
+            continue
+        piece = ""
+        for j in range(i, L):
+            piece += chars[j]
+            if piece in idx:
+                v = best[i] + float(sc[idx[piece]])
+                if v > best[j + 1]:
+                    best[j + 1], frm[j + 1], tok[j + 1] = v, i, idx[piece]
+            if len(piece.encode("utf-8")) > 64:
+                break
+        v = best[i] + unk
+        if v > best[i + 1]:
+            best[i + 1], frm[i + 1], tok[i + 1] = v, i, unk_id
+    ids = []
+    i = L
+    while i > 0:
+        ids.append(tok[i])
+        if frm[i] < 0:
+            break
+        i = frm[i]
+    ids = ids[::-1] + [eos_id]
+    if len(ids) > ctx:
+        ids = ids[:ctx]
+        ids[-1] = eos_id
+    if pad:
+        ids += [pad_id] * (ctx - len(ids))
+    return ids

@@ -86,6 +86,37 @@ class VaeSpec(ctypes.Structure):
         return s
 
 
+class ClipSpec(ctypes.Structure):
+    """tsn_clip_spec (include/tsn.h): the reference's CLIP text encoder."""
+    _fields_ = [("H", ctypes.c_int), ("NL", ctypes.c_int), ("NH", ctypes.c_int), ("ctx", ctypes.c_int),
+                ("vocab", ctypes.c_int), ("eps", ctypes.c_float)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+    def copy(self, **kw):
+        s = ClipSpec()
+        for k, _ in self._fields_:
+            setattr(s, k, kw.get(k, getattr(self, k)))
+        return s
+
+
+class T5Spec(ctypes.Structure):
+    """tsn_t5_spec (include/tsn.h): the reference's T5 v1.1 encoder."""
+    _fields_ = [("d", ctypes.c_int), ("d_ff", ctypes.c_int), ("NL", ctypes.c_int), ("NH", ctypes.c_int),
+                ("ctx", ctypes.c_int), ("vocab", ctypes.c_int), ("n_bucket", ctypes.c_int),
+                ("max_dist", ctypes.c_int), ("eps", ctypes.c_float)]
+
+    def as_dict(self):
+        return {k: getattr(self, k) for k, _ in self._fields_}
+
+    def copy(self, **kw):
+        s = T5Spec()
+        for k, _ in self._fields_:
+            setattr(s, k, kw.get(k, getattr(self, k)))
+        return s
+
+
 class RefCondSpec(ctypes.Structure):
     """tsn_refcond_spec (include/tsn.h): the reference's conditioning prep."""
     _fields_ = [("H", ctypes.c_int), ("F", ctypes.c_int), ("T", ctypes.c_int), ("C", ctypes.c_int),
@@ -210,6 +241,39 @@ _SIGS = {
     "tsn_vae_replay": [_P],
     "tsn_vae_profile_decode": [_P, _P, _P, _P, _I, ctypes.POINTER(_I)],
     "tsn_vae_synth_weights": [ctypes.POINTER(VaeSpec), ctypes.c_uint64, _P],
+    "tsn_clip_spec_default": [ctypes.POINTER(ClipSpec)],
+    "tsn_clip_spec_from_gguf": [ctypes.c_char_p, ctypes.POINTER(ClipSpec)],
+    "tsn_clip_manifest_count": [ctypes.POINTER(ClipSpec)],
+    "tsn_clip_manifest_entry": [ctypes.POINTER(ClipSpec), _I, ctypes.c_char_p, _I,
+                                ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)],
+    "tsn_clip_manifest_total": [ctypes.POINTER(ClipSpec)],
+    "tsn_clip_create": [_P, ctypes.POINTER(ClipSpec), ctypes.POINTER(_P)],
+    "tsn_clip_destroy": [_P],
+    "tsn_clip_upload_weights": [_P, _P, _SZ],
+    "tsn_clip_load_gguf": [_P, ctypes.c_char_p],
+    "tsn_clip_encode": [_P, _P, _P, _P],
+    "tsn_clip_profile_encode": [_P, _P, _P, _P, _P, _I, ctypes.POINTER(_I)],
+    "tsn_clip_synth_weights": [ctypes.POINTER(ClipSpec), ctypes.c_uint64, _P],
+    "tsn_t5_spec_default": [ctypes.POINTER(T5Spec)],
+    "tsn_t5_spec_from_gguf": [ctypes.c_char_p, ctypes.POINTER(T5Spec)],
+    "tsn_t5_manifest_count": [ctypes.POINTER(T5Spec)],
+    "tsn_t5_manifest_entry": [ctypes.POINTER(T5Spec), _I, ctypes.c_char_p, _I,
+                              ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)],
+    "tsn_t5_manifest_total": [ctypes.POINTER(T5Spec)],
+    "tsn_t5_create": [_P, ctypes.POINTER(T5Spec), ctypes.POINTER(_P)],
+    "tsn_t5_destroy": [_P],
+    "tsn_t5_upload_weights": [_P, _P, _SZ],
+    "tsn_t5_load_gguf": [_P, ctypes.c_char_p],
+    "tsn_t5_encode": [_P, _P, _P],
+    "tsn_t5_profile_encode": [_P, _P, _P, _P, _I, ctypes.POINTER(_I)],
+    "tsn_t5_synth_weights": [ctypes.POINTER(T5Spec), ctypes.c_uint64, _P],
+    "tsn_t5_bucket": [_I, _I, _I],
+    "tsn_clip_tokenizer_load": [ctypes.c_char_p, ctypes.POINTER(_P)],
+    "tsn_clip_tokenizer_destroy": [_P],
+    "tsn_clip_tokenizer_encode": [_P, ctypes.c_char_p, _I, _P],
+    "tsn_t5_tokenizer_load": [ctypes.c_char_p, ctypes.POINTER(_P)],
+    "tsn_t5_tokenizer_destroy": [_P],
+    "tsn_t5_tokenizer_encode": [_P, ctypes.c_char_p, _I, _I, _P, ctypes.POINTER(_I)],
     "tsn_gguf_open": [ctypes.c_char_p, ctypes.POINTER(_P)],
     "tsn_gguf_close": [_P],
     "tsn_gguf_tensor_count": [_P],
@@ -223,7 +287,8 @@ _RESTYPES = {"tsn_last_error": ctypes.c_char_p, "tsn_last_gpu_ms": ctypes.c_doub
              "tsn_dit_manifest_total": ctypes.c_int64, "tsn_refdit_manifest_total": ctypes.c_int64,
              "tsn_gguf_get_i64": ctypes.c_int64, "tsn_gguf_get_f64": ctypes.c_double,
              "tsn_refcond_manifest_total": ctypes.c_int64, "tsn_version": _I,
-             "tsn_vae_manifest_total": ctypes.c_int64, "tsn_vae_audio_len": ctypes.c_int64}
+             "tsn_vae_manifest_total": ctypes.c_int64, "tsn_vae_audio_len": ctypes.c_int64,
+             "tsn_clip_manifest_total": ctypes.c_int64, "tsn_t5_manifest_total": ctypes.c_int64, "tsn_t5_bucket": _I}
 
 
 def lib():
@@ -255,9 +320,9 @@ def call(name, *args):
 
 
 def ptr(a):
-    """Host pointer of a contiguous numpy array."""
+    """Host pointer of a contiguous numpy array (keeps a reference to the array)."""
     assert a.flags["C_CONTIGUOUS"]
-    return ctypes.c_void_p(a.ctypes.data)
+    return a.ctypes.data_as(ctypes.c_void_p)
 
 
 def default_spec(workload):
@@ -473,6 +538,184 @@ class VaeModel:
         call("tsn_vae_profile_decode", self.h, latent.p, audio.p, arr, cap, ctypes.byref(n))
         return [{"name": arr[i].name.decode(), "launches": arr[i].launches, "ms": arr[i].total_ms,
                  "flops": arr[i].flops, "bytes": arr[i].bytes} for i in range(n.value)]
+
+
+def clip_spec_default():
+    s = ClipSpec()
+    call("tsn_clip_spec_default", ctypes.byref(s))
+    return s
+
+
+def t5_spec_default():
+    s = T5Spec()
+    call("tsn_t5_spec_default", ctypes.byref(s))
+    return s
+
+
+def clip_spec_from_gguf(path):
+    s = ClipSpec()
+    call("tsn_clip_spec_from_gguf", os.fsencode(path), ctypes.byref(s))
+    return s
+
+
+def t5_spec_from_gguf(path):
+    s = T5Spec()
+    call("tsn_t5_spec_from_gguf", os.fsencode(path), ctypes.byref(s))
+    return s
+
+
+def _enc_manifest(prefix, spec):
+    L = lib()
+    out, buf = [], ctypes.create_string_buffer(256)
+    for i in range(getattr(L, prefix + "_manifest_count")(ctypes.byref(spec))):
+        numel, off = ctypes.c_int64(), ctypes.c_int64()
+        call(prefix + "_manifest_entry", ctypes.byref(spec), i, buf, 256, ctypes.byref(numel), ctypes.byref(off))
+        out.append((buf.value.decode(), numel.value, off.value))
+    return out
+
+
+def clip_manifest(spec):
+    return _enc_manifest("tsn_clip", spec)
+
+
+def t5_manifest(spec):
+    return _enc_manifest("tsn_t5", spec)
+
+
+def clip_synth_weights(spec, seed=4242):
+    w = np.empty(int(lib().tsn_clip_manifest_total(ctypes.byref(spec))), np.float32)
+    call("tsn_clip_synth_weights", ctypes.byref(spec), seed, ptr(w))
+    return w
+
+
+def t5_synth_weights(spec, seed=4242):
+    w = np.empty(int(lib().tsn_t5_manifest_total(ctypes.byref(spec))), np.float32)
+    call("tsn_t5_synth_weights", ctypes.byref(spec), seed, ptr(w))
+    return w
+
+
+def t5_bucket(rel, n_bucket=32, max_dist=128):
+    return int(lib().tsn_t5_bucket(rel, n_bucket, max_dist))
+
+
+def _stats(arr, n):
+    return [{"name": arr[i].name.decode(), "launches": arr[i].launches, "ms": arr[i].total_ms,
+             "flops": arr[i].flops, "bytes": arr[i].bytes} for i in range(n.value)]
+
+
+class ClipModel:
+    """tn::ClipModel mirror (src/models.h:24-38): encode host ids -> per-token features and pooled vector."""
+
+    def __init__(self, rt, spec):
+        self.rt, self.spec = rt, spec
+        h = ctypes.c_void_p()
+        call("tsn_clip_create", rt.h, ctypes.byref(spec), ctypes.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().tsn_clip_destroy(self.h)
+            self.h = None
+
+    def upload_weights(self, w):
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        call("tsn_clip_upload_weights", self.h, ptr(w), w.size)
+
+    def load_gguf(self, path):
+        call("tsn_clip_load_gguf", self.h, os.fsencode(path))
+
+    def _ids(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        if ids.shape != (self.spec.ctx,):
+            raise ValueError("clip: %d ids expected, got shape %s" % (self.spec.ctx, ids.shape))
+        return ids
+
+    def encode(self, ids, per_token, glob):
+        ids = self._ids(ids)
+        call("tsn_clip_encode", self.h, ptr(ids), per_token.p, glob.p)
+
+    def profile_encode(self, ids, per_token, glob):
+        ids = self._ids(ids)
+        arr, n = (KernelStat * 64)(), ctypes.c_int()
+        call("tsn_clip_profile_encode", self.h, ptr(ids), per_token.p, glob.p, arr, 64, ctypes.byref(n))
+        return _stats(arr, n)
+
+
+class T5Model:
+    """tn::T5Model mirror (src/models.h:40-52): encode host ids -> per-token features."""
+
+    def __init__(self, rt, spec):
+        self.rt, self.spec = rt, spec
+        h = ctypes.c_void_p()
+        call("tsn_t5_create", rt.h, ctypes.byref(spec), ctypes.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().tsn_t5_destroy(self.h)
+            self.h = None
+
+    def upload_weights(self, w):
+        w = np.ascontiguousarray(w, dtype=np.float32)
+        call("tsn_t5_upload_weights", self.h, ptr(w), w.size)
+
+    def load_gguf(self, path):
+        call("tsn_t5_load_gguf", self.h, os.fsencode(path))
+
+    def _ids(self, ids):
+        ids = np.ascontiguousarray(ids, np.int32)
+        if ids.shape != (self.spec.ctx,):
+            raise ValueError("t5: %d ids expected, got shape %s" % (self.spec.ctx, ids.shape))
+        return ids
+
+    def encode(self, ids, out):
+        ids = self._ids(ids)
+        call("tsn_t5_encode", self.h, ptr(ids), out.p)
+
+    def profile_encode(self, ids, out):
+        ids = self._ids(ids)
+        arr, n = (KernelStat * 64)(), ctypes.c_int()
+        call("tsn_t5_profile_encode", self.h, ptr(ids), out.p, arr, 64, ctypes.byref(n))
+        return _stats(arr, n)
+
+
+class ClipTokenizer:
+    """tn::ClipTokenizer mirror (src/tokenizers.h:12-21), host only."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        call("tsn_clip_tokenizer_load", os.fsencode(path), ctypes.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().tsn_clip_tokenizer_destroy(self.h)
+            self.h = None
+
+    def encode(self, text, ctx=77):
+        ids = np.empty(ctx, np.int32)
+        call("tsn_clip_tokenizer_encode", self.h, text.encode("utf-8", "surrogateescape"), ctx, ptr(ids))
+        return ids.tolist()
+
+
+class T5Tokenizer:
+    """tn::T5Tokenizer mirror (src/tokenizers.h:23-31), host only."""
+
+    def __init__(self, path):
+        h = ctypes.c_void_p()
+        call("tsn_t5_tokenizer_load", os.fsencode(path), ctypes.byref(h))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib().tsn_t5_tokenizer_destroy(self.h)
+            self.h = None
+
+    def encode(self, text, ctx=77, pad=True):
+        ids, n = np.empty(ctx, np.int32), ctypes.c_int()
+        call("tsn_t5_tokenizer_encode", self.h, text.encode("utf-8", "surrogateescape"), ctx, 1 if pad else 0, ptr(ids),
+             ctypes.byref(n))
+        return ids[:n.value].tolist()
 
 
 class Gguf:

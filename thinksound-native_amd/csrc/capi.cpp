@@ -5,12 +5,15 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <functional>
 #include <new>
 
 #include "dit.h"
+#include "encoders.h"
 #include "gguf.h"
 #include "refcond.h"
 #include "refdit.h"
+#include "tokenizers.h"
 #include "vae.h"
 
 namespace tsn {
@@ -36,6 +39,18 @@ struct tsn_refcond {
 };
 struct tsn_vae {
     tsn::VaeModel m;
+};
+struct tsn_clip {
+    tsn::ClipModel m;
+};
+struct tsn_t5 {
+    tsn::T5Model m;
+};
+struct tsn_clip_tokenizer {
+    tsn::ClipBpe t;
+};
+struct tsn_t5_tokenizer {
+    tsn::T5Unigram t;
 };
 
 #define RT_CHECK(r)                                                 \
@@ -82,6 +97,28 @@ static void from_vae_spec(const tsn::VaeSpec &s, tsn_vae_spec *c) {
     c->T = s.T; c->latent = s.latent; c->out_ch = s.out_ch;
     for (int i = 0; i < 6; ++i) c->width[i] = s.width[i];
     for (int i = 0; i < 5; ++i) { c->stride[i] = s.stride[i]; c->kt[i] = s.kt[i]; }
+}
+
+static tsn::ClipSpec to_clip_spec(const tsn_clip_spec *c) {
+    return tsn::ClipSpec{c->H, c->NL, c->NH, c->ctx, c->vocab, c->eps};
+}
+static void from_clip_spec(const tsn::ClipSpec &s, tsn_clip_spec *c) {
+    c->H = s.H; c->NL = s.NL; c->NH = s.NH; c->ctx = s.ctx; c->vocab = s.vocab; c->eps = s.eps;
+}
+static tsn::T5Spec to_t5_spec(const tsn_t5_spec *c) {
+    return tsn::T5Spec{c->d, c->d_ff, c->NL, c->NH, c->ctx, c->vocab, c->n_bucket, c->max_dist, c->eps};
+}
+static void from_t5_spec(const tsn::T5Spec &s, tsn_t5_spec *c) {
+    c->d = s.d; c->d_ff = s.d_ff; c->NL = s.NL; c->NH = s.NH; c->ctx = s.ctx; c->vocab = s.vocab;
+    c->n_bucket = s.n_bucket; c->max_dist = s.max_dist; c->eps = s.eps;
+}
+static int manifest_entry(const std::vector<tsn::ManifestEntry> &m, int idx, char *name, int name_cap,
+                          int64_t *numel, int64_t *offset) {
+    if (idx < 0 || idx >= (int)m.size()) { tsn::set_error("manifest index out of range"); return TSN_ERR_ARG; }
+    if (name && name_cap > 0) snprintf(name, (size_t)name_cap, "%s", m[idx].name.c_str());
+    if (numel) *numel = m[idx].numel;
+    if (offset) *offset = m[idx].offset;
+    return TSN_OK;
 }
 
 static int copy_stats(const std::vector<tsn::KernelStat> &ks, tsn_kernel_stat *stats, int cap, int *n_stats) {
@@ -506,6 +543,174 @@ int tsn_vae_profile_decode(tsn_vae *d, const float *latent, float *audio, tsn_ke
     return copy_stats(ks, stats, cap, n_stats);
 }
 
+/* ---------------- text encoders ---------------- */
+#define ENC_CHECK(d, what)                                                              \
+    do {                                                                                \
+        if (!(d)) { tsn::set_error("null " what " handle"); return TSN_ERR_ARG; }       \
+    } while (0)
+
+int tsn_clip_spec_default(tsn_clip_spec *out) {
+    if (!out) { tsn::set_error("null spec"); return TSN_ERR_ARG; }
+    from_clip_spec(tsn::clip_spec_default(), out);
+    return TSN_OK;
+}
+int tsn_clip_spec_from_gguf(const char *path, tsn_clip_spec *out) {
+    if (!path || !out) { tsn::set_error("null path or spec"); return TSN_ERR_ARG; }
+    tsn::ClipSpec s;
+    TSN_TRY(tsn::clip_spec_from_gguf(path, &s));
+    from_clip_spec(s, out);
+    return TSN_OK;
+}
+int tsn_clip_manifest_count(const tsn_clip_spec *spec) {
+    if (!spec) { tsn::set_error("null spec"); return -1; }
+    return (int)tsn::clip_manifest(to_clip_spec(spec)).size();
+}
+int tsn_clip_manifest_entry(const tsn_clip_spec *spec, int idx, char *name, int name_cap, int64_t *numel,
+                            int64_t *offset) {
+    if (!spec) { tsn::set_error("null spec"); return TSN_ERR_ARG; }
+    return manifest_entry(tsn::clip_manifest(to_clip_spec(spec)), idx, name, name_cap, numel, offset);
+}
+int64_t tsn_clip_manifest_total(const tsn_clip_spec *spec) {
+    if (!spec) { tsn::set_error("null spec"); return -1; }
+    const auto m = tsn::clip_manifest(to_clip_spec(spec));
+    return m.back().offset + m.back().numel;
+}
+int tsn_clip_create(tsn_runtime *rt, const tsn_clip_spec *spec, tsn_clip **out) {
+    RT_CHECK(rt);
+    if (!spec || !out) { tsn::set_error("null spec or out pointer"); return TSN_ERR_ARG; }
+    *out = nullptr;
+    tsn_clip *d = new (std::nothrow) tsn_clip();
+    if (!d) { tsn::set_error("out of host memory"); return TSN_ERR_OOM; }
+    const int rc = d->m.create(&rt->rt, to_clip_spec(spec));
+    if (rc != TSN_OK) { delete d; return rc; }
+    *out = d;
+    return TSN_OK;
+}
+int tsn_clip_destroy(tsn_clip *d) { delete d; return TSN_OK; }
+int tsn_clip_upload_weights(tsn_clip *d, const float *w, size_t numel) {
+    ENC_CHECK(d, "clip");
+    return d->m.upload_weights(w, numel);
+}
+int tsn_clip_load_gguf(tsn_clip *d, const char *path) {
+    ENC_CHECK(d, "clip");
+    if (!path) { tsn::set_error("null path"); return TSN_ERR_ARG; }
+    return d->m.load_gguf(path);
+}
+int tsn_clip_encode(tsn_clip *d, const int32_t *ids, float *per_token, float *global) {
+    ENC_CHECK(d, "clip");
+    return d->m.encode(ids, per_token, global);
+}
+int tsn_clip_profile_encode(tsn_clip *d, const int32_t *ids, float *per_token, float *global, tsn_kernel_stat *stats,
+                            int cap, int *n_stats) {
+    if (!d || !stats || !n_stats || cap <= 0) { tsn::set_error("profile: null argument"); return TSN_ERR_ARG; }
+    std::vector<tsn::KernelStat> ks;
+    const int rc = d->m.profile([&] { return d->m.encode(ids, per_token, global); }, ks);
+    if (rc != TSN_OK) return rc;
+    return copy_stats(ks, stats, cap, n_stats);
+}
+int tsn_t5_spec_default(tsn_t5_spec *out) {
+    if (!out) { tsn::set_error("null spec"); return TSN_ERR_ARG; }
+    from_t5_spec(tsn::t5_spec_default(), out);
+    return TSN_OK;
+}
+int tsn_t5_spec_from_gguf(const char *path, tsn_t5_spec *out) {
+    if (!path || !out) { tsn::set_error("null path or spec"); return TSN_ERR_ARG; }
+    tsn::T5Spec s;
+    TSN_TRY(tsn::t5_spec_from_gguf(path, &s));
+    from_t5_spec(s, out);
+    return TSN_OK;
+}
+int tsn_t5_manifest_count(const tsn_t5_spec *spec) {
+    if (!spec) { tsn::set_error("null spec"); return -1; }
+    return (int)tsn::t5_manifest(to_t5_spec(spec)).size();
+}
+int tsn_t5_manifest_entry(const tsn_t5_spec *spec, int idx, char *name, int name_cap, int64_t *numel,
+                          int64_t *offset) {
+    if (!spec) { tsn::set_error("null spec"); return TSN_ERR_ARG; }
+    return manifest_entry(tsn::t5_manifest(to_t5_spec(spec)), idx, name, name_cap, numel, offset);
+}
+int64_t tsn_t5_manifest_total(const tsn_t5_spec *spec) {
+    if (!spec) { tsn::set_error("null spec"); return -1; }
+    const auto m = tsn::t5_manifest(to_t5_spec(spec));
+    return m.back().offset + m.back().numel;
+}
+int tsn_t5_create(tsn_runtime *rt, const tsn_t5_spec *spec, tsn_t5 **out) {
+    RT_CHECK(rt);
+    if (!spec || !out) { tsn::set_error("null spec or out pointer"); return TSN_ERR_ARG; }
+    *out = nullptr;
+    tsn_t5 *d = new (std::nothrow) tsn_t5();
+    if (!d) { tsn::set_error("out of host memory"); return TSN_ERR_OOM; }
+    const int rc = d->m.create(&rt->rt, to_t5_spec(spec));
+    if (rc != TSN_OK) { delete d; return rc; }
+    *out = d;
+    return TSN_OK;
+}
+int tsn_t5_destroy(tsn_t5 *d) { delete d; return TSN_OK; }
+int tsn_t5_upload_weights(tsn_t5 *d, const float *w, size_t numel) {
+    ENC_CHECK(d, "t5");
+    return d->m.upload_weights(w, numel);
+}
+int tsn_t5_load_gguf(tsn_t5 *d, const char *path) {
+    ENC_CHECK(d, "t5");
+    if (!path) { tsn::set_error("null path"); return TSN_ERR_ARG; }
+    return d->m.load_gguf(path);
+}
+int tsn_t5_encode(tsn_t5 *d, const int32_t *ids, float *out) {
+    ENC_CHECK(d, "t5");
+    return d->m.encode(ids, out);
+}
+int tsn_t5_profile_encode(tsn_t5 *d, const int32_t *ids, float *out, tsn_kernel_stat *stats, int cap, int *n_stats) {
+    if (!d || !stats || !n_stats || cap <= 0) { tsn::set_error("profile: null argument"); return TSN_ERR_ARG; }
+    std::vector<tsn::KernelStat> ks;
+    const int rc = d->m.profile([&] { return d->m.encode(ids, out); }, ks);
+    if (rc != TSN_OK) return rc;
+    return copy_stats(ks, stats, cap, n_stats);
+}
+int tsn_t5_bucket(int rel, int n_bucket, int max_dist) {
+    if (n_bucket < 4 || n_bucket % 4 || max_dist <= n_bucket / 4) {
+        tsn::set_error("t5 bucket: n_bucket a multiple of 4, max_dist past the exact range");
+        return -1;
+    }
+    return tsn::t5_bucket(rel, n_bucket, max_dist);
+}
+
+/* ---------------- tokenizers ---------------- */
+int tsn_clip_tokenizer_load(const char *path, tsn_clip_tokenizer **out) {
+    if (!path || !out) { tsn::set_error("null path or out pointer"); return TSN_ERR_ARG; }
+    *out = nullptr;
+    tsn_clip_tokenizer *t = new (std::nothrow) tsn_clip_tokenizer();
+    if (!t) { tsn::set_error("out of host memory"); return TSN_ERR_OOM; }
+    const int rc = t->t.load(path);
+    if (rc != TSN_OK) { delete t; return rc; }
+    *out = t;
+    return TSN_OK;
+}
+int tsn_clip_tokenizer_destroy(tsn_clip_tokenizer *t) { delete t; return TSN_OK; }
+int tsn_clip_tokenizer_encode(const tsn_clip_tokenizer *t, const char *text, int ctx, int32_t *ids) {
+    if (!t || !text || !ids || ctx < 2) { tsn::set_error("clip tokenizer: null argument or ctx < 2"); return TSN_ERR_ARG; }
+    const auto v = t->t.encode(text, ctx);
+    memcpy(ids, v.data(), v.size() * sizeof(int32_t));
+    return TSN_OK;
+}
+int tsn_t5_tokenizer_load(const char *path, tsn_t5_tokenizer **out) {
+    if (!path || !out) { tsn::set_error("null path or out pointer"); return TSN_ERR_ARG; }
+    *out = nullptr;
+    tsn_t5_tokenizer *t = new (std::nothrow) tsn_t5_tokenizer();
+    if (!t) { tsn::set_error("out of host memory"); return TSN_ERR_OOM; }
+    const int rc = t->t.load(path);
+    if (rc != TSN_OK) { delete t; return rc; }
+    *out = t;
+    return TSN_OK;
+}
+int tsn_t5_tokenizer_destroy(tsn_t5_tokenizer *t) { delete t; return TSN_OK; }
+int tsn_t5_tokenizer_encode(const tsn_t5_tokenizer *t, const char *text, int ctx, int pad, int32_t *ids, int *n_ids) {
+    if (!t || !text || !ids || !n_ids || ctx < 1) { tsn::set_error("t5 tokenizer: null argument or ctx < 1"); return TSN_ERR_ARG; }
+    const auto v = t->t.encode(text, ctx, pad != 0);
+    memcpy(ids, v.data(), v.size() * sizeof(int32_t));
+    *n_ids = (int)v.size();
+    return TSN_OK;
+}
+
 /* ---------------- GGUF reader ---------------- */
 int tsn_gguf_open(const char *path, tsn_gguf **out) {
     if (!path || !out) { tsn::set_error("null path or out pointer"); return TSN_ERR_ARG; }
@@ -643,6 +848,46 @@ int tsn_vae_synth_weights(const tsn_vae_spec *spec, uint64_t seed, float *out) {
         }
         tsn::synth_normal_f32(seed, (uint64_t)i, 0.0, std, (size_t)m[i].numel, out + m[i].offset);
     }
+    return TSN_OK;
+}
+// per-tensor std of the encoders' synthetic weights (include/tsn.h): embeddings 1, norm weights 1 + 0.1,
+// biases 0.02, residual-stream projections 0.5/sqrt(fan_in), other linears 1/sqrt(fan_in), rel bias 0.5
+static void enc_synth(const std::vector<tsn::ManifestEntry> &m, uint64_t seed, float *out,
+                      const std::function<int(const std::string &)> &fan_in) {
+    for (size_t i = 0; i < m.size(); ++i) {
+        const std::string &n = m[i].name;
+        auto ends = [&](const char *suf) {
+            const size_t k = strlen(suf);
+            return n.size() >= k && n.compare(n.size() - k, k, suf) == 0;
+        };
+        double mean = 0.0, std = 0.02;
+        if (n == "tok_emb" || n == "pos_emb") std = 1.0;
+        else if (n == "rel_bias") std = 0.5;
+        else if (ends("norm") || ends("ln1.w") || ends("ln2.w") || ends("out_ln.w")) { mean = 1.0; std = 0.1; }
+        else if (ends(".b")) std = 0.02;
+        else {
+            const bool into_stream = ends(".out.w") || ends(".fc2.w") || ends(".o") || ends(".wo");
+            std = (into_stream ? 0.5 : 1.0) / sqrt((double)fan_in(n));
+        }
+        tsn::synth_normal_f32(seed, (uint64_t)i, mean, std, (size_t)m[i].numel, out + m[i].offset);
+    }
+}
+int tsn_clip_synth_weights(const tsn_clip_spec *spec, uint64_t seed, float *out) {
+    if (!spec || !out) { tsn::set_error("null spec or output"); return TSN_ERR_ARG; }
+    const tsn::ClipSpec s = to_clip_spec(spec);
+    enc_synth(tsn::clip_manifest(s), seed, out, [&](const std::string &n) {
+        const size_t k = n.size();
+        return k >= 6 && n.compare(k - 6, 6, ".fc2.w") == 0 ? 4 * s.H : s.H;
+    });
+    return TSN_OK;
+}
+int tsn_t5_synth_weights(const tsn_t5_spec *spec, uint64_t seed, float *out) {
+    if (!spec || !out) { tsn::set_error("null spec or output"); return TSN_ERR_ARG; }
+    const tsn::T5Spec s = to_t5_spec(spec);
+    enc_synth(tsn::t5_manifest(s), seed, out, [&](const std::string &n) {
+        const size_t k = n.size();
+        return k >= 3 && n.compare(k - 3, 3, ".wo") == 0 ? s.d_ff : s.d;
+    });
     return TSN_OK;
 }
 int tsn_dit_synth_weights(const tsn_dit_spec *spec, uint64_t seed, double norm_mean, uint16_t *out) {

@@ -112,15 +112,33 @@ int GgufReader::parse() {
         case KV_F32: v.f = c.get<float>(); break;
         case KV_F64: v.f = c.get<double>(); break;
         case KV_STRING: v.s = c.str(); break;
-        case KV_ARRAY: {   // kept only as skipped bytes: the DiT reads no array metadata
+        case KV_ARRAY: {   // tokenizer vocabularies, merges and scores
             const uint32_t et = c.get<uint32_t>();
             const uint64_t n = c.get<uint64_t>();
+            v.elem = et;
             if (et == KV_STRING) {
-                for (uint64_t k = 0; k < n && c.ok; ++k) c.str();
+                TSN_REQUIRE(n <= (uint64_t)(c.end - c.p) / 8, "gguf: bad string array in metadata " + key);
+                v.sa.reserve((size_t)n);
+                for (uint64_t k = 0; k < n && c.ok; ++k) v.sa.push_back(c.str());
             } else {
                 const size_t es = scalar_size(et);
                 TSN_REQUIRE(es > 0 && n <= (uint64_t)(c.end - c.p) / es, "gguf: bad array in metadata " + key);
-                c.take(nullptr, (size_t)(n * es));
+                v.na.reserve((size_t)n);
+                for (uint64_t k = 0; k < n && c.ok; ++k) {
+                    switch (et) {
+                    case KV_U8: v.na.push_back(c.get<uint8_t>()); break;
+                    case KV_I8: v.na.push_back(c.get<int8_t>()); break;
+                    case KV_BOOL: v.na.push_back(c.get<uint8_t>() != 0); break;
+                    case KV_U16: v.na.push_back(c.get<uint16_t>()); break;
+                    case KV_I16: v.na.push_back(c.get<int16_t>()); break;
+                    case KV_U32: v.na.push_back(c.get<uint32_t>()); break;
+                    case KV_I32: v.na.push_back(c.get<int32_t>()); break;
+                    case KV_F32: v.na.push_back(c.get<float>()); break;
+                    case KV_U64: v.na.push_back((double)c.get<uint64_t>()); break;
+                    case KV_I64: v.na.push_back((double)c.get<int64_t>()); break;
+                    default: v.na.push_back(c.get<double>()); break;
+                    }
+                }
             }
             break;
         }
@@ -177,6 +195,18 @@ double GgufReader::get_f64(const std::string &key, double def) const {
 std::string GgufReader::get_str(const std::string &key, const std::string &def) const {
     const auto it = kv_.find(key);
     return it == kv_.end() || it->second.type != KV_STRING ? def : it->second.s;
+}
+
+const std::vector<std::string> &GgufReader::get_arr_str(const std::string &key) const {
+    static const std::vector<std::string> empty;
+    const auto it = kv_.find(key);
+    return it == kv_.end() || it->second.type != KV_ARRAY || it->second.elem != KV_STRING ? empty : it->second.sa;
+}
+
+std::vector<double> GgufReader::get_arr_num(const std::string &key) const {
+    const auto it = kv_.find(key);
+    if (it == kv_.end() || it->second.type != KV_ARRAY || it->second.elem == KV_STRING) return {};
+    return it->second.na;
 }
 
 const GgufTensorInfo *GgufReader::find(const std::string &name) const {

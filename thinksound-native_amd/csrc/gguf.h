@@ -37,6 +37,10 @@ public:
     int64_t get_i64(const std::string &key, int64_t def) const;
     double get_f64(const std::string &key, double def) const;
     std::string get_str(const std::string &key, const std::string &def) const;
+    // array metadata (empty when absent or of another element type): strings, and any numeric
+    // element type widened to double
+    const std::vector<std::string> &get_arr_str(const std::string &key) const;
+    std::vector<double> get_arr_num(const std::string &key) const;
     const GgufTensorInfo *find(const std::string &name) const;
     const std::vector<GgufTensorInfo> &tensors() const { return list_; }
     uint32_t version() const { return version_; }
@@ -49,6 +53,9 @@ private:
         int64_t i = 0;
         double f = 0;
         std::string s;
+        uint32_t elem = 0;                // array element type
+        std::vector<std::string> sa;      // string array
+        std::vector<double> na;           // numeric array
     };
     int fd_ = -1;
     void *map_ = nullptr;

@@ -218,6 +218,39 @@ int launch_split3(const float *x, long long rows, int C, const float *ab, int lo
 // y [T][OC] = conv(snake(x), W [OC][C][KK], pad), no bias; x [T][C] f32, OC in {1, 2, 4}, C % 64 == 0
 int launch_conv_out(const float *x, const float *ab, const float *W, float *y, int T, int C, int OC, int KK, int pad,
                     hipStream_t st);
+// Text encoders (enc.hip), all f32.
+// gemm_f32: Y[m*ldy + n] = act(sum_k A[m*lda + k] W[n*ldw + k] + bias[n]) (act 1: quick GELU), or with
+// resid set Y[m*ldy + n] += sum + bias[n]; K % 32 == 0, f32 MFMA
+struct EncGemmArgs {
+    const float *A; int lda;
+    const float *W; int ldw;
+    const float *bias;
+    float *Y; int ldy;
+    int M, N, K;
+    int resid, act;
+};
+int launch_gemm_f32(const EncGemmArgs &g, hipStream_t st);
+// LayerNorm with weight and bias (ln) or RMSNorm with weight, rows of H floats
+int launch_enc_norm(const float *x, float *y, const float *w, const float *b, int rows, int H, float eps, bool ln,
+                    hipStream_t st);
+// attention over one context of S <= 128 rows, heads of 64: q, k, v at column offsets q_off/k_off/v_off
+// + 64h of qkv rows (stride ld), output at column 64h of out rows (stride ldo);
+// mode 0 none, 1 T5 (keys with pad[k] == 0 masked, else + rel[bucket[q*S + k]*nh + h]),
+// 2 CLIP (keys k > q or k > eot masked)
+struct EncAttnArgs {
+    const float *qkv; int ld, q_off, k_off, v_off;
+    float *out; int ldo;
+    int S, nh, hd;
+    float scale;
+    int mode;
+    const int32_t *bucket; const float *rel; const int32_t *pad;
+    int eot;
+};
+int launch_enc_attention(const EncAttnArgs &a, hipStream_t st);
+// y[r][c] = gelu_tanh(u[r][c]) * u[r][F + c], u rows of 2F
+int launch_geglu_rows(const float *u, float *y, int rows, int F, hipStream_t st);
+// x[s][:] = tok[ids[s]][:] (+ pos[s][:]); ids on the device, each inside tok's rows
+int launch_embed_rows(const int32_t *ids, const float *tok, const float *pos, float *x, int S, int H, hipStream_t st);
 // dst[i][:] = src[idx[i]][:] for rows x H floats (idx on the device, every entry a valid src row)
 int launch_gather_rows(const float *src, const int32_t *idx, float *dst, int rows, int H, hipStream_t st);
 // out[c] = mean over rows of x[r][c], rows summed in order (src/net.mm Runtime::mean_cols)

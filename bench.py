@@ -20,11 +20,14 @@ import statistics
 import sys
 import time
 
+import numpy as np
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_F16_TFLOPS = 2500.0      # MI355X dense FP16/BF16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
+PEAK_F32_TFLOPS = 157.3       # MI355X dense FP32 MFMA
 CAL_COPY_FLOATS = 16 << 20    # calibration copy: 64 MiB read + 64 MiB written
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_dit_eval_b2_la256.txt")
 CPU_SAMPLE_S = 10.0           # CPU baseline: whole evaluations until this much time has passed
@@ -291,6 +294,52 @@ def bench_vae(tsn, rt, args):
             "cpu_baseline": cpu, "launch": "hipGraph replay"}
 
 
+def bench_encoders(tsn, rt, args):
+    """The reference's text encoders, once per prompt: CLIP (24 layers, H 1024) and T5 v1.1 XL (24 layers,
+    d 2048, d_ff 5120) over 77 tokens, f32 synthetic weights; eager launches, median of 5."""
+    out = {}
+    for name, spec, synth, cls in (("clip", tsn.clip_spec_default(), tsn.clip_synth_weights, tsn.ClipModel),
+                                   ("t5", tsn.t5_spec_default(), tsn.t5_synth_weights, tsn.T5Model)):
+        w = synth(spec, 4242)
+        m = cls(rt, spec)
+        m.upload_weights(w)
+        del w
+        ids = np.arange(spec.ctx, dtype=np.int32) % (spec.vocab - 1) + 1
+        width = spec.H if name == "clip" else spec.d
+        a = rt.empty((spec.ctx, width))
+        g = rt.empty((width,))
+        run = (lambda: m.encode(ids, a, g)) if name == "clip" else (lambda: m.encode(ids, a))
+        for _ in range(2):
+            run()
+        rt.sync()
+        ts = []
+        for _ in range(5):
+            rt.begin()
+            run()
+            ts.append(rt.commit())
+        stats = m.profile_encode(ids, a, g) if name == "clip" else m.profile_encode(ids, a)
+        flops = sum(k["flops"] for k in stats)
+        wbytes = 4.0 * (int(lib_total(tsn, name, spec)))
+        ms = statistics.median(ts)
+        gemm = [k for k in stats if k["name"] == "gemm_f32_kernel"][0]
+        log("bench %s: %.3f ms per prompt, %.1f GFLOP, gemm_f32 %.3f ms (%d launches, %.1f TFLOP/s)"
+            % (name, ms, flops / 1e9, gemm["ms"], gemm["launches"], gemm["flops"] / (gemm["ms"] * 1e9)))
+        out[name] = {"ms_per_prompt": round(ms, 4), "gflop": round(flops / 1e9, 2), "weights_gb_f32": round(wbytes / 1e9, 3),
+                     "weight_read_gbs": round(wbytes / (ms * 1e-3) / 1e9, 1),
+                     "gemm_f32": {"launches": gemm["launches"], "ms": round(gemm["ms"], 4),
+                                  "tflops": round(gemm["flops"] / (gemm["ms"] * 1e9), 2),
+                                  "frac_fp32_mfma_peak": round(gemm["flops"] / (gemm["ms"] * 1e9) / PEAK_F32_TFLOPS, 4)}}
+        m.close()
+    out["workload"] = "CLIP and T5 text encoders over 77 tokens, one prompt each, f32"
+    out["launch"] = "eager"
+    return out
+
+
+def lib_total(tsn, name, spec):
+    man = tsn.clip_manifest(spec) if name == "clip" else tsn.t5_manifest(spec)
+    return man[-1][1] + man[-1][2]
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -300,6 +349,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-ref", action="store_true", help="skip the reference checkpoint graph section")
     ap.add_argument("--no-vae", action="store_true", help="skip the VAE decoder section")
+    ap.add_argument("--no-enc", action="store_true", help="skip the text-encoder section")
     ap.add_argument("--eager", action="store_true",
                     help="launch kernel by kernel instead of replaying hipGraphs (for profilers that do not follow graphs)")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -421,6 +471,9 @@ def main():
     vae = None
     if not args.no_vae and not args.eager:
         vae = bench_vae(tsn, rt, args)
+    enc = None
+    if not args.no_enc and not args.eager:
+        enc = bench_encoders(tsn, rt, args)
 
     # ---------------- CPU baseline: the oracle, one full evaluation ----------------
     cpu = None
@@ -470,6 +523,7 @@ def main():
         "cpu_baseline": cpu,
         "reference_graph": ref,
         "vae_decoder": vae,
+        "text_encoders": enc,
         "accumulate": "f32 (f16 MFMA operands from BF16 weights; f32 residual stream)",
         "launch": "eager" if args.eager else "hipGraph replay",
     }

@@ -322,6 +322,8 @@ def bench_encoders(tsn, rt, args):
         wbytes = 4.0 * (int(lib_total(tsn, name, spec)))
         ms = statistics.median(ts)
         gemm = [k for k in stats if k["name"] == "gemm_f32_kernel"][0]
+        for k in sorted(stats, key=lambda k: -k["ms"]):
+            log("  %s %-24s %4d launches %8.3f ms" % (name, k["name"], k["launches"], k["ms"]))
         log("bench %s: %.3f ms per prompt, %.1f GFLOP, gemm_f32 %.3f ms (%d launches, %.1f TFLOP/s)"
             % (name, ms, flops / 1e9, gemm["ms"], gemm["launches"], gemm["flops"] / (gemm["ms"] * 1e9)))
         out[name] = {"ms_per_prompt": round(ms, 4), "gflop": round(flops / 1e9, 2), "weights_gb_f32": round(wbytes / 1e9, 3),

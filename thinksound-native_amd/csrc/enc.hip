@@ -12,80 +12,108 @@ namespace {
 
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
-constexpr int FB_M = 32, FB_N = 64, FB_K = 32, FB_LD = FB_K + 1;
+constexpr int FB_M = 32, FB_N = 64, FB_K = 64, FB_LD = FB_K + 1;
 
-// Y = act(A·Wᵀ + bias) or Y += A·Wᵀ + bias. 4 waves; wave w owns columns 16w..16w+15 of a 32x64
-// tile (two 16x16 blocks of v_mfma_f32_16x16x4_f32 per 4-wide K slice). A and W tiles are staged
-// through LDS, the next K tile is held in registers while the current one is multiplied.
+// The epilogue of one output element: v = sum + bias, then Y = act(v) or Y += v.
+__device__ __forceinline__ void enc_epi(const EncGemmArgs &g, int m, int n, float v) {
+    if (g.bias) v += g.bias[n];
+    float *y = g.Y + (long long)m * g.ldy + n;
+    if (g.resid) {
+        *y = *y + v;
+    } else {
+        if (g.act == 1) v = v / (1.0f + expf(-1.702f * v));   // quick GELU (shaders/ops_conv.metal:25-29)
+        *y = v;
+    }
+}
+
+// 4 waves; wave w owns columns 16w..16w+15 of a 32x64 tile (two 16x16 blocks of v_mfma_f32_16x16x4_f32
+// per 4-wide K slice). A and W reach LDS in 64-wide K stages; the next stage is loaded into registers
+// while the current one is multiplied. blockIdx.z = split: K tiles [z*kps, (z+1)*kps); with more than
+// one split the raw sums go to ws[z][M][N] and enc_gemm_reduce_kernel adds them in split order.
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const EncGemmArgs g) {
     __shared__ float As[2][FB_M * FB_LD];
     __shared__ float Ws[2][FB_N * FB_LD];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n0 = blockIdx.x * FB_N, m0 = blockIdx.y * FB_M;
+    const int n0 = blockIdx.x * FB_N, m0 = blockIdx.y * FB_M, z = blockIdx.z;
     const int M = g.M, N = g.N, K = g.K;
-    // loader: A row tid/8 (32 rows), W rows tid/8 and 32 + tid/8; 4 floats at column (tid%8)*4
-    const int lr = tid >> 3, lc = (tid & 7) * 4;
-    const bool a_ok = m0 + lr < M, w0_ok = n0 + lr < N, w1_ok = n0 + 32 + lr < N;
-    const float *ap = g.A + (long long)(a_ok ? m0 + lr : 0) * g.lda + lc;
-    const float *wp0 = g.W + (long long)(w0_ok ? n0 + lr : 0) * g.ldw + lc;
-    const float *wp1 = g.W + (long long)(w1_ok ? n0 + 32 + lr : 0) * g.ldw + lc;
+    const int nkt = (K + FB_K - 1) / FB_K;
+    const int kt0 = z * g.kps, kt1 = min(nkt, kt0 + g.kps);
+    // loader: 16 lanes per 64-wide row (4 floats each); A rows lr + 16i (i < 2), W rows lr + 16i (i < 4)
+    const int lr = tid >> 4, lc = (tid & 15) * 4;
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 ra, rw0, rw1;
-    auto fetch = [&](int k0) {
-        ra = a_ok ? *(const float4 *)(ap + k0) : z4;
-        rw0 = w0_ok ? *(const float4 *)(wp0 + k0) : z4;
-        rw1 = w1_ok ? *(const float4 *)(wp1 + k0) : z4;
+    float4 ra[2], rw[4];
+    auto fetch = [&](int kt) {
+        const int k = kt * FB_K + lc;
+        const bool kin = k < K;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int m = m0 + lr + 16 * i;
+            ra[i] = (kin && m < M) ? *(const float4 *)(g.A + (long long)m * g.lda + k) : z4;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int n = n0 + lr + 16 * i;
+            rw[i] = (kin && n < N) ? *(const float4 *)(g.W + (long long)n * g.ldw + k) : z4;
+        }
     };
     auto stash = [&](int b) {
-        float *a = &As[b][lr * FB_LD + lc];
-        a[0] = ra.x; a[1] = ra.y; a[2] = ra.z; a[3] = ra.w;
-        float *w = &Ws[b][lr * FB_LD + lc];
-        w[0] = rw0.x; w[1] = rw0.y; w[2] = rw0.z; w[3] = rw0.w;
-        float *w1 = &Ws[b][(32 + lr) * FB_LD + lc];
-        w1[0] = rw1.x; w1[1] = rw1.y; w1[2] = rw1.z; w1[3] = rw1.w;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            float *a = &As[b][(lr + 16 * i) * FB_LD + lc];
+            a[0] = ra[i].x; a[1] = ra[i].y; a[2] = ra[i].z; a[3] = ra[i].w;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float *w = &Ws[b][(lr + 16 * i) * FB_LD + lc];
+            w[0] = rw[i].x; w[1] = rw[i].y; w[2] = rw[i].z; w[3] = rw[i].w;
+        }
     };
     floatx4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
     const int r16 = lane & 15, kq = lane >> 4;   // operand lane: row / column r16, k offset kq
-    const int nk = K / FB_K;
-    fetch(0);
-    stash(0);
-    __syncthreads();
-    for (int kt = 0; kt < nk; ++kt) {
-        const int b = kt & 1;
-        if (kt + 1 < nk) fetch((kt + 1) * FB_K);
-        const float *as = As[b], *ws = Ws[b];
+    if (kt0 < kt1) {
+        fetch(kt0);
+        stash(0);
+        __syncthreads();
+        for (int kt = kt0; kt < kt1; ++kt) {
+            const int b = (kt - kt0) & 1;
+            if (kt + 1 < kt1) fetch(kt + 1);
+            const float *as = As[b], *ws = Ws[b];
 #pragma unroll
-        for (int kk = 0; kk < FB_K; kk += 4) {
-            const float bv = ws[(wave * 16 + r16) * FB_LD + kk + kq];
-            const float a0 = as[r16 * FB_LD + kk + kq];
-            const float a1 = as[(16 + r16) * FB_LD + kk + kq];
-            acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, bv, acc[0], 0, 0, 0);
-            acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, bv, acc[1], 0, 0, 0);
-        }
-        if (kt + 1 < nk) {
-            stash(b ^ 1);
-            __syncthreads();
+            for (int kk = 0; kk < FB_K; kk += 4) {
+                const float bv = ws[(wave * 16 + r16) * FB_LD + kk + kq];
+                const float a0 = as[r16 * FB_LD + kk + kq];
+                const float a1 = as[(16 + r16) * FB_LD + kk + kq];
+                acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, bv, acc[0], 0, 0, 0);
+                acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, bv, acc[1], 0, 0, 0);
+            }
+            if (kt + 1 < kt1) {
+                stash(b ^ 1);
+                __syncthreads();
+            }
         }
     }
     // lane holds rows 16i + 4*(lane/16) + r, column lane%16 of the wave's 16 columns
     const int n = n0 + wave * 16 + r16;
     if (n >= N) return;
-    const float bn = g.bias ? g.bias[n] : 0.0f;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int m = m0 + 16 * i + 4 * kq + r;
             if (m >= M) continue;
-            float v = acc[i][r] + bn;
-            float *y = g.Y + (long long)m * g.ldy + n;
-            if (g.resid) {
-                *y = *y + v;
-            } else {
-                if (g.act == 1) v = v / (1.0f + expf(-1.702f * v));   // quick GELU (shaders/ops_conv.metal:25-29)
-                *y = v;
-            }
+            if (g.splits > 1) g.ws[((long long)z * M + m) * N + n] = acc[i][r];
+            else enc_epi(g, m, n, acc[i][r]);
         }
+}
+
+// split-K finish: sum the partials in split order, then the epilogue
+__global__ void enc_gemm_reduce_kernel(const EncGemmArgs g) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)g.M * g.N) return;
+    const int m = (int)(i / g.N), n = (int)(i - (long long)m * g.N);
+    float v = 0.0f;
+    for (int z = 0; z < g.splits; ++z) v += g.ws[(long long)z * g.M * g.N + i];
+    enc_epi(g, m, n, v);
 }
 
 // one wave per row: LayerNorm (w, b; mean then variance of the centred row) or RMSNorm (w)
@@ -204,14 +232,30 @@ __global__ void embed_rows_kernel(const int32_t *__restrict__ ids, const float *
 
 } // namespace
 
-int launch_gemm_f32(const EncGemmArgs &g, hipStream_t st) {
+int launch_gemm_f32(const EncGemmArgs &gin, hipStream_t st) {
+    EncGemmArgs g = gin;
     TSN_REQUIRE(g.A && g.W && g.Y && g.M > 0 && g.N > 0 && g.K > 0, "gemm_f32: null operand or empty shape");
-    TSN_REQUIRE(g.K % FB_K == 0 && g.lda % 4 == 0 && g.ldw % 4 == 0 && g.lda >= g.K && g.ldw >= g.K && g.ldy >= g.N,
-                "gemm_f32: K a multiple of 32, row strides multiples of 4 covering the rows");
+    TSN_REQUIRE(g.K % 4 == 0 && g.lda % 4 == 0 && g.ldw % 4 == 0 && g.lda >= g.K && g.ldw >= g.K && g.ldy >= g.N,
+                "gemm_f32: K and row strides multiples of 4, strides covering the rows");
     TSN_REQUIRE((((uintptr_t)g.A) & 15) == 0 && (((uintptr_t)g.W) & 15) == 0, "gemm_f32: 16-byte aligned A and W");
     TSN_REQUIRE(g.act == 0 || g.act == 1, "gemm_f32: activation 0 (none) or 1 (quick GELU)");
-    TSN_LAUNCH(gemm_f32_kernel, dim3((g.N + FB_N - 1) / FB_N, (g.M + FB_M - 1) / FB_M), dim3(256), 0, st, g);
+    // split K until about 200 workgroups run, while the workspace holds the partials and every
+    // split keeps at least 4 K tiles
+    const int tiles = ((g.N + FB_N - 1) / FB_N) * ((g.M + FB_M - 1) / FB_M);
+    const int nkt = (g.K + FB_K - 1) / FB_K;
+    int splits = 1;
+    while (g.ws && tiles * splits < 200 && nkt / (splits * 2) >= 4 &&
+           (size_t)(splits * 2) * g.M * g.N * sizeof(float) <= g.ws_bytes)
+        splits *= 2;
+    g.kps = (nkt + splits - 1) / splits;
+    g.splits = (nkt + g.kps - 1) / g.kps;
+    TSN_LAUNCH(gemm_f32_kernel, dim3((g.N + FB_N - 1) / FB_N, (g.M + FB_M - 1) / FB_M, g.splits), dim3(256), 0, st, g);
     TSN_HIP_CHECK(hipGetLastError());
+    if (g.splits > 1) {
+        const long long n = (long long)g.M * g.N;
+        TSN_LAUNCH(enc_gemm_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, g);
+        TSN_HIP_CHECK(hipGetLastError());
+    }
     return TSN_OK;
 }
 

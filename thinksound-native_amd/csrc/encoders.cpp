@@ -165,6 +165,7 @@ int ClipModel::create(Runtime *r, const ClipSpec &sp) {
     TSN_TRY(alloc(n * H * 4, (void **)&ATT_));
     TSN_TRY(alloc(n * 4 * H * 4, (void **)&FF_));
     TSN_TRY(alloc(n * 4, (void **)&ids_));
+    TSN_TRY(alloc(ENC_WS_BYTES, (void **)&ws_));
     return TSN_OK;
 }
 
@@ -236,7 +237,7 @@ int ClipModel::encode(const int32_t *ids, float *per_token, float *global) {
     const hipStream_t st = rt->dev.stream();
     auto gemm = [&](const float *A, int lda, const float *W, const float *b, float *Y, int ldy, int M, int N, int K,
                     int resid, int act) {
-        EncGemmArgs g{A, lda, W, K, b, Y, ldy, M, N, K, resid, act};
+        EncGemmArgs g{A, lda, W, K, b, Y, ldy, M, N, K, resid, act, ws_, ENC_WS_BYTES, 1, 0};
         return run("gemm_f32_kernel", 2.0 * M * N * K, 4.0 * ((double)N * K + (double)M * K + M * (double)N),
                    [&] { return launch_gemm_f32(g, st); });
     };
@@ -277,6 +278,7 @@ int T5Model::create(Runtime *r, const T5Spec &sp) {
     TSN_TRY(alloc(n * F * 4, (void **)&G_));
     TSN_TRY(alloc(n * 4, (void **)&ids_));
     TSN_TRY(alloc(n * 4, (void **)&pad_));
+    TSN_TRY(alloc(ENC_WS_BYTES, (void **)&ws_));
     // bucket of (q, k) = bucket(k - q) (src/t5.cpp:47-53)
     std::vector<int32_t> bk(n * n);
     for (size_t q = 0; q < n; ++q)
@@ -350,7 +352,7 @@ int T5Model::encode(const int32_t *ids, float *out) {
     TSN_TRY(rt->dev.upload(pad_, pad.data(), (size_t)n * 4));
     const hipStream_t st = rt->dev.stream();
     auto gemm = [&](const float *A, int lda, const float *W, float *Y, int ldy, int M, int N, int K, int resid) {
-        EncGemmArgs g{A, lda, W, K, nullptr, Y, ldy, M, N, K, resid, 0};
+        EncGemmArgs g{A, lda, W, K, nullptr, Y, ldy, M, N, K, resid, 0, ws_, ENC_WS_BYTES, 1, 0};
         return run("gemm_f32_kernel", 2.0 * M * N * K, 4.0 * ((double)N * K + (double)M * K + M * (double)N),
                    [&] { return launch_gemm_f32(g, st); });
     };

@@ -16,6 +16,8 @@
 
 namespace tsn {
 
+constexpr size_t ENC_WS_BYTES = (size_t)16 << 20;   // split-K partials of the f32 GEMMs
+
 struct ClipSpec {   // field meaning documented in include/tsn.h (tsn_clip_spec)
     int H, NL, NH, ctx, vocab;
     float eps;
@@ -52,7 +54,7 @@ private:
     };
     std::vector<Layer> L_;
     const float *tok_ = nullptr, *pos_ = nullptr, *lnw_ = nullptr, *lnb_ = nullptr, *proj_ = nullptr;
-    float *X_ = nullptr, *R_ = nullptr, *QKV_ = nullptr, *ATT_ = nullptr, *FF_ = nullptr;
+    float *X_ = nullptr, *R_ = nullptr, *QKV_ = nullptr, *ATT_ = nullptr, *FF_ = nullptr, *ws_ = nullptr;
     int32_t *ids_ = nullptr;
     bool ready_ = false;
     int upload(const float *host, size_t numel);
@@ -74,7 +76,7 @@ private:
     };
     std::vector<Layer> L_;
     const float *tok_ = nullptr, *rel_ = nullptr, *on_ = nullptr;
-    float *X_ = nullptr, *R_ = nullptr, *QKV_ = nullptr, *ATT_ = nullptr, *U_ = nullptr, *G_ = nullptr;
+    float *X_ = nullptr, *R_ = nullptr, *QKV_ = nullptr, *ATT_ = nullptr, *U_ = nullptr, *G_ = nullptr, *ws_ = nullptr;
     int32_t *ids_ = nullptr, *pad_ = nullptr, *bucket_ = nullptr;
     bool ready_ = false;
     int upload(const float *host, size_t numel);

@@ -220,7 +220,8 @@ int launch_conv_out(const float *x, const float *ab, const float *W, float *y, i
                     hipStream_t st);
 // Text encoders (enc.hip), all f32.
 // gemm_f32: Y[m*ldy + n] = act(sum_k A[m*lda + k] W[n*ldw + k] + bias[n]) (act 1: quick GELU), or with
-// resid set Y[m*ldy + n] += sum + bias[n]; K % 32 == 0, f32 MFMA
+// resid set Y[m*ldy + n] += sum + bias[n]; K % 4 == 0, f32 MFMA. With a workspace the launcher may
+// split K (partials reduced in split order by a second kernel it launches); splits and kps are its own.
 struct EncGemmArgs {
     const float *A; int lda;
     const float *W; int ldw;
@@ -228,6 +229,8 @@ struct EncGemmArgs {
     float *Y; int ldy;
     int M, N, K;
     int resid, act;
+    float *ws; size_t ws_bytes;
+    int splits, kps;
 };
 int launch_gemm_f32(const EncGemmArgs &g, hipStream_t st);
 // LayerNorm with weight and bias (ln) or RMSNorm with weight, rows of H floats

@@ -451,6 +451,36 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             *(half8 *)(y + P.y_lo) = lo;
             *(half8 *)(y + P.y_hi2) = hi;
         }
+    } else if constexpr (EPI == EPI_RSNAKE) {
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int c = tid + 512 * p, row = c >> 4, col = (c & 15) * 8;
+            const int m = m0 + row, n = n0 + col;
+            if (m >= M || n >= N) continue;
+            float v[8];
+            ldsum8(tile, row * TP + col, v);
+            if (P.bias) add8(v, P.bias + n);
+            float *x = P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n;
+            if (P.r_add) {
+                const float4 x0 = *(const float4 *)x, x1 = *(const float4 *)(x + 4);
+                v[0] += x0.x; v[1] += x0.y; v[2] += x0.z; v[3] += x0.w;
+                v[4] += x1.x; v[5] += x1.y; v[6] += x1.z; v[7] += x1.w;
+            }
+            *(float4 *)x = make_float4(v[0], v[1], v[2], v[3]);
+            *(float4 *)(x + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            snake8(v, P.snake + n, P.snake + N + n);
+            half8 hi, lo;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                hi[e] = (half_t)v[e];
+                lo[e] = (half_t)(v[e] - (float)hi[e]);
+            }
+            const int C = P.y_lo;
+            half_t *y = (half_t *)P.Y + rowmap_phys(P.ymap, m) * (long long)P.ldy + n + 2 * C * (n / C);
+            *(half8 *)y = hi;
+            *(half8 *)(y + C) = lo;
+            *(half8 *)(y + 2 * C) = hi;
+        }
     } else if constexpr (EPI == EPI_RESID) {
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
@@ -858,7 +888,28 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmBatch bt) 
         const float4 b = *(const float4 *)(P.bias + n);
         v.x += b.x; v.y += b.y; v.z += b.z; v.w += b.w;
     }
-    if constexpr (EPI == EPI_RESID) {
+    if constexpr (EPI == EPI_RSNAKE) {
+        float4 *xr = (float4 *)(P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n);
+        if (P.r_add) {
+            const float4 x = *xr;
+            v.x += x.x; v.y += x.y; v.z += x.z; v.w += x.w;
+        }
+        *xr = v;
+        float e[4] = {v.x, v.y, v.z, v.w};
+        half4 hi, lo;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float sn = sinf(e[j] * P.snake[n + j]);
+            e[j] = e[j] + sn * sn * P.snake[P.N + n + j];
+            hi[j] = (half_t)e[j];
+            lo[j] = (half_t)(e[j] - (float)hi[j]);
+        }
+        const int C = P.y_lo;
+        half_t *y = (half_t *)P.Y + rowmap_phys(P.ymap, m) * (long long)P.ldy + n + 2 * C * (n / C);
+        *(half4 *)y = hi;
+        *(half4 *)(y + C) = lo;
+        *(half4 *)(y + 2 * C) = hi;
+    } else if constexpr (EPI == EPI_RESID) {
         const float4 g = *(const float4 *)(P.gate + (long long)(m / P.gate_L) * P.gate_ld + n);
         float4 *xr = (float4 *)(P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n);
         float4 x = *xr;
@@ -886,6 +937,7 @@ int launch_gemm_reduce(const GemmBatch &b, int epi, hipStream_t st) {
         else if (epi == EPI_RESID) TSN_LAUNCH((gemm_fixup_kernel<EPI_RESID>), grid, block, 0, st, b);
         else if (epi == EPI_QKV) TSN_LAUNCH((gemm_fixup_kernel<EPI_QKV>), grid, block, 0, st, b);
         else if (epi == EPI_SNAKE) TSN_LAUNCH((gemm_fixup_kernel<EPI_SNAKE>), grid, block, 0, st, b);
+        else if (epi == EPI_RSNAKE) TSN_LAUNCH((gemm_fixup_kernel<EPI_RSNAKE>), grid, block, 0, st, b);
         else TSN_LAUNCH((gemm_fixup_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
         TSN_HIP_CHECK(hipGetLastError());
         return TSN_OK;
@@ -897,6 +949,7 @@ int launch_gemm_reduce(const GemmBatch &b, int epi, hipStream_t st) {
     const dim3 grid((unsigned)((red + 255) / 256)), block(256);
     if (epi == EPI_RESID) TSN_LAUNCH(splitk_reduce_kernel<EPI_RESID>, grid, block, 0, st, b);
     else if (epi == EPI_STORE) TSN_LAUNCH(splitk_reduce_kernel<EPI_STORE>, grid, block, 0, st, b);
+    else if (epi == EPI_RSNAKE) TSN_LAUNCH(splitk_reduce_kernel<EPI_RSNAKE>, grid, block, 0, st, b);
     else { set_error("gemm reduce: epilogue without split-K support"); return TSN_ERR_ARG; }
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
@@ -913,8 +966,9 @@ const char *gemm_reduce_name(const GemmBatch &b, int epi) {
     if (b.sk)
         return epi == EPI_STORE ? "gemm_fixup_kernel<0>" : epi == EPI_RESID ? "gemm_fixup_kernel<1>"
                : epi == EPI_QKV ? "gemm_fixup_kernel<2>" : epi == EPI_SNAKE ? "gemm_fixup_kernel<4>"
-                                                                          : "gemm_fixup_kernel<3>";
-    return epi == EPI_RESID ? "splitk_reduce_kernel<1>" : "splitk_reduce_kernel<0>";
+               : epi == EPI_RSNAKE ? "gemm_fixup_kernel<5>" : "gemm_fixup_kernel<3>";
+    return epi == EPI_RESID ? "splitk_reduce_kernel<1>" : epi == EPI_RSNAKE ? "splitk_reduce_kernel<5>"
+                                                                            : "splitk_reduce_kernel<0>";
 }
 
 void gemm_problem_init(GemmProblem &p) {
@@ -944,7 +998,7 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         if (p.w_half)
             TSN_REQUIRE(p.Kc % (2 * BK) == 0 && p.ldw >= p.taps * (p.Kc / 2),
                         "gemm: half-width W needs Kc a multiple of 128 and ldw >= taps*Kc/2");
-        if (p.y_lo && epi != EPI_SNAKE) {
+        if (p.y_lo && epi != EPI_SNAKE && epi != EPI_RSNAKE) {
             const int wout = epi == EPI_SWIGLU ? p.N / 2 : p.N;
             TSN_REQUIRE((epi == EPI_STORE || epi == EPI_SWIGLU) && p.y_f16 && p.y_lo % 8 == 0 && p.y_lo >= wout &&
                             p.ldy >= p.y_lo + wout,
@@ -955,8 +1009,13 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
                             p.y_lo % 8 == 0 && p.y_hi2 % 8 == 0 && p.y_lo >= p.N && p.y_hi2 >= p.y_lo + p.N &&
                             p.ldy >= p.y_hi2 + p.N && p.ldy % 8 == 0 && !p.w_half,
                         "gemm snake: table, three 8-aligned N-wide parts (hi, lo at y_lo, hi at y_hi2) inside ldy");
+        else if (epi == EPI_RSNAKE)
+            TSN_REQUIRE(p.R && p.rmap.L > 0 && p.Y && p.ymap.L > 0 && p.snake && (((uintptr_t)p.snake) & 15) == 0 &&
+                            p.y_lo > 0 && p.y_lo % 8 == 0 && p.N % p.y_lo == 0 && p.ldr % 4 == 0 && p.ldy % 8 == 0 &&
+                            !p.w_half,
+                        "gemm residual snake: stream R, table, phases of y_lo (a multiple of 8) columns");
         else
-            TSN_REQUIRE(!p.snake && !p.y_hi2, "gemm: snake table and second hi part only with the snake epilogue");
+            TSN_REQUIRE(!p.snake && !p.y_hi2, "gemm: snake table and second hi part only with the snake epilogues");
         if (epi == EPI_SWIGLU)
             TSN_REQUIRE(p.Y && p.ymap.L > 0 && p.y_f16 && p.N % BN == 0 && p.ldy % 8 == 0 &&
                             (((uintptr_t)p.Y) & 15) == 0,
@@ -987,6 +1046,7 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         // the C-tile epilogue writes 8 columns with 16-byte accesses
         if (epi == EPI_STORE) pipe = pipe && (((uintptr_t)p.Y) & 15) == 0 && p.ldy % (p.y_f16 ? 8 : 4) == 0;
         if (epi == EPI_SNAKE) pipe = pipe && (((uintptr_t)p.Y) & 15) == 0;
+        if (epi == EPI_RSNAKE) pipe = pipe && ((((uintptr_t)p.Y) | ((uintptr_t)p.R)) & 15) == 0;
         if (epi == EPI_RESID)
             pipe = pipe && (((uintptr_t)p.R) & 15) == 0 && (((uintptr_t)p.gate) & 15) == 0 && p.ldr % 4 == 0 &&
                    p.gate_ld % 4 == 0;
@@ -1008,9 +1068,10 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     bool any_half = false;
     for (int i = 0; i < b.nprob; ++i) any_half = any_half || b.p[i].w_half;
     TSN_REQUIRE(pipe || !any_lo, "gemm: hi|lo output needs the pipelined kernel (f16 A, 16-byte aligned rows)");
-    TSN_REQUIRE(pipe || epi != EPI_SNAKE, "gemm snake: needs the pipelined kernel (f16 A, 16-byte aligned rows)");
+    TSN_REQUIRE(pipe || (epi != EPI_SNAKE && epi != EPI_RSNAKE),
+                "gemm snake: needs the pipelined kernel (f16 A, 16-byte aligned rows)");
     TSN_REQUIRE(pipe || !any_half, "gemm: half-width W needs the pipelined kernel (f16 A, 16-byte aligned rows)");
-    if (pipe && (epi == EPI_RESID || epi == EPI_STORE) && b.ws && !any_lo) {
+    if (pipe && (epi == EPI_RESID || epi == EPI_STORE || epi == EPI_RSNAKE) && b.ws && (!any_lo || epi == EPI_RSNAKE)) {
         int nkmin = 1 << 30;
         for (int i = 0; i < b.nprob; ++i) nkmin = std::min(nkmin, b.p[i].K / BK);
         int best = 0;
@@ -1087,20 +1148,21 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     TSN_REQUIRE(pipe || epi != EPI_SWIGLU, "gemm swiglu: needs K and row strides the pipelined kernel takes");
     b.pipe = pipe ? 1 : 0;
     b.hl = any_half ? 1 : 0;
-    TSN_REQUIRE(epi != EPI_SNAKE || !b.hl, "gemm snake: no half-width W");
+    TSN_REQUIRE((epi != EPI_SNAKE && epi != EPI_RSNAKE) || !b.hl, "gemm snake: no half-width W");
     b.kname = b.sk ? (epi == EPI_STORE ? "gemm_sk_kernel<0>" : epi == EPI_RESID ? "gemm_sk_kernel<1>"
                       : epi == EPI_QKV ? "gemm_sk_kernel<2>" : epi == EPI_SNAKE ? "gemm_sk_kernel<4>"
-                                                                                : "gemm_sk_kernel<3>")
+                      : epi == EPI_RSNAKE ? "gemm_sk_kernel<5>" : "gemm_sk_kernel<3>")
             : pipe && b.hl ? (epi == EPI_STORE ? "gemm_pipe_hl_kernel<0>" : epi == EPI_RESID ? "gemm_pipe_hl_kernel<1>"
                               : epi == EPI_QKV ? "gemm_pipe_hl_kernel<2>" : "gemm_pipe_hl_kernel<3>")
             : pipe ? (epi == EPI_STORE ? "gemm_pipe_kernel<0>" : epi == EPI_RESID ? "gemm_pipe_kernel<1>"
                       : epi == EPI_QKV ? "gemm_pipe_kernel<2>" : epi == EPI_SNAKE ? "gemm_pipe_kernel<4>"
-                                                                                  : "gemm_pipe_kernel<3>")
+                      : epi == EPI_RSNAKE ? "gemm_pipe_kernel<5>" : "gemm_pipe_kernel<3>")
                    : a_f32 ? "gemm_f16_kernel<true, 0>"
                    : (epi == EPI_STORE ? "gemm_f16_kernel<false, 0>" : epi == EPI_RESID ? "gemm_f16_kernel<false, 1>"
                                                                         : "gemm_f16_kernel<false, 2>");
     if (a_f32) TSN_REQUIRE(epi == EPI_STORE, "gemm: f32 A operand only with a plain store epilogue");
-    TSN_REQUIRE(epi == EPI_STORE || epi == EPI_RESID || epi == EPI_QKV || epi == EPI_SWIGLU || epi == EPI_SNAKE,
+    TSN_REQUIRE(epi == EPI_STORE || epi == EPI_RESID || epi == EPI_QKV || epi == EPI_SWIGLU || epi == EPI_SNAKE ||
+                    epi == EPI_RSNAKE,
                 "gemm: unknown epilogue");
     return TSN_OK;
 }
@@ -1114,6 +1176,7 @@ int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st)
             else if (epi == EPI_QKV) TSN_LAUNCH((gemm_sk_kernel<EPI_QKV>), grid, block, 0, st, b);
             else if (epi == EPI_SWIGLU) TSN_LAUNCH((gemm_sk_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
             else if (epi == EPI_SNAKE) TSN_LAUNCH((gemm_sk_kernel<EPI_SNAKE>), grid, block, 0, st, b);
+            else if (epi == EPI_RSNAKE) TSN_LAUNCH((gemm_sk_kernel<EPI_RSNAKE>), grid, block, 0, st, b);
             else { set_error("gemm: unknown epilogue"); return TSN_ERR_ARG; }
         } else if (b.hl) {
             if (epi == EPI_STORE) TSN_LAUNCH((gemm_pipe_hl_kernel<EPI_STORE>), grid, block, 0, st, b);
@@ -1126,6 +1189,7 @@ int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st)
         else if (epi == EPI_QKV) TSN_LAUNCH((gemm_pipe_kernel<EPI_QKV>), grid, block, 0, st, b);
         else if (epi == EPI_SWIGLU) TSN_LAUNCH((gemm_pipe_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
         else if (epi == EPI_SNAKE) TSN_LAUNCH((gemm_pipe_kernel<EPI_SNAKE>), grid, block, 0, st, b);
+        else if (epi == EPI_RSNAKE) TSN_LAUNCH((gemm_pipe_kernel<EPI_RSNAKE>), grid, block, 0, st, b);
         else { set_error("gemm: unknown epilogue"); return TSN_ERR_ARG; }
     } else if (a_f32) {
         TSN_LAUNCH((gemm_f16_kernel<true, EPI_STORE>), grid, block, 0, st, b);

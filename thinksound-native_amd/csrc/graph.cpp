@@ -137,8 +137,8 @@ double gemm_bytes(const GemmBatch &b, int epi) {
     for (int i = 0; i < b.nprob; ++i) {
         const GemmProblem &p = b.p[i];
         double out = epi == EPI_RESID ? 8.0 : epi == EPI_SWIGLU ? 1.0 : epi == EPI_SNAKE ? 6.0
-                   : (p.y_f16 || epi == EPI_QKV ? 2.0 : 4.0);
-        if (p.y_lo) out *= 2.0;
+                   : epi == EPI_RSNAKE ? (p.r_add ? 14.0 : 10.0) : (p.y_f16 || epi == EPI_QKV ? 2.0 : 4.0);
+        if (p.y_lo && (epi == EPI_STORE || epi == EPI_SWIGLU)) out *= 2.0;
         x += 2.0 * p.M * (double)p.Kc + 2.0 * p.N * (double)p.K / (p.w_half ? 2 : 1) + out * p.M * (double)p.N;
     }
     return x;

@@ -9,7 +9,7 @@ namespace tsn {
 /* ------------------------------------------------------------------ GEMM (MFMA) */
 // C[M,N] = A[M,K] · W[N,K]ᵀ with f16 operands and f32 accumulation; 128x128x64 tiles,
 // v_mfma_f32_16x16x32_f16 (pipelined kernel: 8 waves, 5 direct-to-LDS stages).
-enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_SWIGLU = 3, EPI_SNAKE = 4 };
+enum GemmEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_QKV = 2, EPI_SWIGLU = 3, EPI_SNAKE = 4, EPI_RSNAKE = 5 };
 
 struct GemmProblem {
     // A operand rows (f16, or f32 converted on load): row m -> rowmap_phys(amap, m).
@@ -37,6 +37,10 @@ struct GemmProblem {
     // K is never split
     int y_hi2;
     const float *snake;
+    // EPI_RSNAKE: x = (r_add ? R[rmap(m)*ldr + n] : 0) + acc + bias[n] is stored to R, and snake(x) (table
+    // as EPI_SNAKE) as a three-part f16 row: columns come in phases of C = y_lo, and column n of phase
+    // n / C lands at n + 2C*(n / C) (hi), + C (lo), + 2C (hi) of Y row ymap(m)*ldy
+    int r_add;
     // EPI_RESID: R[rmap(m)*ldr + n] += gate[(m / gate_L)*gate_ld + n] * (acc + bias)
     float *R; int ldr; RowMap rmap; const float *gate; int gate_ld; int gate_L;
     // EPI_QKV: columns [0,Hq) q, [Hq,2Hq) k, [2Hq,3Hq) v; heads of hd = 64 columns.

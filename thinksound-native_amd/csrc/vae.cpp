@@ -237,6 +237,7 @@ int VaeModel::upload(const float *host, size_t numel) {
             ++g.ngroups;
         }
         const float *w = src(bp + ".layers.1.weight"), *b = src(bp + ".layers.1.bias");
+        const float *a0 = src(bp + ".layers.2.layers.0.alpha"), *b0 = src(bp + ".layers.2.layers.0.beta");
         for (int q = 0; q < g.ngroups; ++q) {
             const size_t off = wconv.size();
             const int rows = g.nph[q] * co;
@@ -254,6 +255,14 @@ int VaeModel::upload(const float *host, size_t numel) {
             std::vector<float> brep((size_t)rows);
             for (int p = 0; p < g.nph[q]; ++p) memcpy(brep.data() + (size_t)p * co, b, (size_t)co * sizeof(float));
             vec(brep.data(), rows, &g.bt[q]);
+            // the first residual unit's snake, applied in this conv's epilogue: table per output column
+            std::vector<float> tab(2 * (size_t)rows);
+            for (int p = 0; p < g.nph[q]; ++p)
+                for (int c = 0; c < co; ++c) {
+                    tab[(size_t)p * co + c] = (float)exp((double)a0[c]);
+                    tab[(size_t)rows + (size_t)p * co + c] = (float)exp(-(double)b0[c]);
+                }
+            vec(tab.data(), 2 * rows, &g.abt[q]);
         }
         for (int r = 0; r < 3; ++r) {
             Unit &u = g.u[r];
@@ -300,10 +309,9 @@ int VaeModel::enqueue_decode(const float *latent, float *audio) {
     TSN_REQUIRE((((uintptr_t)latent) & 15) == 0, "vae: latent must be 16-byte aligned");
     const hipStream_t stq = rt->dev.stream();
     const double third = 1.0 / 3.0;   // profiled flops: the f32 GEMM's 2*M*N*K, not the three f16 products
-    auto split = [&](const float *x, long long rows, int C, const float *ab) {
-        return run("split3_kernel", 0, rows * (double)C * (4.0 + 6.0),
-                   [&] { return launch_split3(x, rows, C, ab, 1, A1_, stq); });
-    };
+    // three-part operands ping-pong between A1 and A2: each GEMM reads `in` and writes `out`
+    half_t *in = A1_, *out = A2_;
+    auto flip = [&]() { std::swap(in, out); };
     // conv GEMM over the three-part operand A (lda = 3 IC); taps of width 3 IC
     auto conv = [&](GemmProblem &p, const half_t *A, int M, int IC, int taps, int pad, int dil, const half_t *W,
                     const float *bias, int N) {
@@ -313,61 +321,76 @@ int VaeModel::enqueue_decode(const float *latent, float *audio) {
         p.W = W; p.ldw = taps * 3 * IC; p.bias = bias;
         p.M = M; p.N = N; p.K = taps * 3 * IC;
     };
+    auto batch = [&](GemmBatch &b, int n) {
+        b.nprob = n;
+        b.ws = ws_;
+        b.ws_bytes = ws_bytes_;
+    };
 
     int T = s.T, C = s.width[0];
-    // input conv k7 pad 3: latent [T][latent] -> X [T][width0]
+    // input conv k7 pad 3 + b, then the first stage's snake: latent -> snake(x0) three-part
     TSN_TRY(run("split3_kernel", 0, (double)T * s.latent * 10.0,
-                [&] { return launch_split3(latent, T, s.latent, nullptr, 1, A1_, stq); }));
+                [&] { return launch_split3(latent, T, s.latent, nullptr, 1, in, stq); }));
     {
         GemmBatch b;
-        b.nprob = 1;
-        b.ws = ws_; b.ws_bytes = ws_bytes_;
+        batch(b, 1);
         GemmProblem &p = b.p[0];
-        conv(p, A1_, T, s.latent, KRES, 3, 1, W0_, b0_, C);
-        p.Y = X_; p.ldy = C; p.ymap = rowmap_dense(T);
-        TSN_TRY(gemm_run(b, EPI_STORE, third));
+        conv(p, in, T, s.latent, KRES, 3, 1, W0_, b0_, C);
+        p.Y = out; p.ldy = 3 * C; p.ymap = rowmap_dense(T);
+        p.y_f16 = 1; p.y_lo = C; p.y_hi2 = 2 * C; p.snake = st_[0].ab_in;
+        TSN_TRY(gemm_run(b, EPI_SNAKE, third));
+        flip();
     }
     for (int n = 0; n < 5; ++n) {
         const Stage &g = st_[n];
         const int stv = s.stride[n], co = s.width[n + 1];
-        // snake -> transposed conv as phase-group convs; output rows interleave straight into X
-        TSN_TRY(split(X_, T, C, g.ab_in));
+        // transposed conv as phase-group convs: x rows interleave straight into X, and the first
+        // residual unit's snake(x) into the three-part rows of `out`
         {
             GemmBatch b;
-            b.nprob = g.ngroups;
-            b.ws = ws_; b.ws_bytes = ws_bytes_;
+            batch(b, g.ngroups);
             for (int q = 0; q < g.ngroups; ++q) {
                 GemmProblem &p = b.p[q];
-                conv(p, A1_, T, C, g.taps, g.pad[q], 1, g.Wt[q], g.bt[q], g.nph[q] * co);
-                p.Y = X_ + (size_t)g.r0[q] * co; p.ldy = stv * co; p.ymap = rowmap_dense(T);
+                conv(p, in, T, C, g.taps, g.pad[q], 1, g.Wt[q], g.bt[q], g.nph[q] * co);
+                p.R = X_ + (size_t)g.r0[q] * co; p.ldr = stv * co; p.rmap = rowmap_dense(T); p.r_add = 0;
+                p.Y = out + (size_t)g.r0[q] * 3 * co; p.ldy = stv * 3 * co; p.ymap = rowmap_dense(T);
+                p.y_lo = co; p.snake = g.abt[q];
             }
-            TSN_TRY(gemm_run(b, EPI_STORE, third));
+            TSN_TRY(gemm_run(b, EPI_RSNAKE, third));
+            flip();
         }
         T *= stv;
         C = co;
         for (int r = 0; r < 3; ++r) {
             const Unit &u = g.u[r];
             const int d = DILS[r];
-            TSN_TRY(split(X_, T, C, u.ab1));
-            {   // conv k7, dilation d, + bias -> snake -> three-part f16 A2
+            {   // conv k7, dilation d, + bias -> snake -> three-part f16
                 GemmBatch b;
-                b.nprob = 1;
-                b.ws = ws_; b.ws_bytes = ws_bytes_;
+                batch(b, 1);
                 GemmProblem &p = b.p[0];
-                conv(p, A1_, T, C, KRES, 3 * d, d, u.W7, u.b7, C);
-                p.Y = A2_; p.ldy = 3 * C; p.ymap = rowmap_dense(T);
+                conv(p, in, T, C, KRES, 3 * d, d, u.W7, u.b7, C);
+                p.Y = out; p.ldy = 3 * C; p.ymap = rowmap_dense(T);
                 p.y_f16 = 1; p.y_lo = C; p.y_hi2 = 2 * C; p.snake = u.ab2;
                 TSN_TRY(gemm_run(b, EPI_SNAKE, third));
+                flip();
             }
-            {   // conv k1 + bias, added to the residual stream
+            {   // conv k1 + bias added to x; the next snake (next unit, or next stage's input) from the new x
+                const float *next = r < 2 ? g.u[r + 1].ab1 : n < 4 ? st_[n + 1].ab_in : nullptr;
                 GemmBatch b;
-                b.nprob = 1;
-                b.ws = ws_; b.ws_bytes = ws_bytes_;
+                batch(b, 1);
                 GemmProblem &p = b.p[0];
-                conv(p, A2_, T, C, 1, 0, 1, u.W1, u.b1, C);
+                conv(p, in, T, C, 1, 0, 1, u.W1, u.b1, C);
                 p.R = X_; p.ldr = C; p.rmap = rowmap_dense(T);
-                p.gate = ones_; p.gate_ld = 0; p.gate_L = T;
-                TSN_TRY(gemm_run(b, EPI_RESID, third));
+                if (next) {
+                    p.r_add = 1;
+                    p.Y = out; p.ldy = 3 * C; p.ymap = rowmap_dense(T);
+                    p.y_lo = C; p.snake = next;
+                    TSN_TRY(gemm_run(b, EPI_RSNAKE, third));
+                    flip();
+                } else {   // the final snake belongs to the output conv
+                    p.gate = ones_; p.gate_ld = 0; p.gate_L = T;
+                    TSN_TRY(gemm_run(b, EPI_RESID, third));
+                }
             }
         }
     }

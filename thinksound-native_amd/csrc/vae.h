@@ -9,6 +9,9 @@
 // weight row [W_hi | W_hi | W_lo], so one f16 GEMM over K = 3*IC sums hi*W_hi + lo*W_hi + hi*W_lo
 // (the dropped lo*W_lo term is below 2^-22 relative). The residual stream x stays f32.
 //
+// Every snake runs in the epilogue of the GEMM that produces its input (the residual units' closing
+// k1 conv writes x and snake(x) for the next unit or stage), so x is read once per GEMM.
+//
 // Transposed convs are decomposed by output phase: output row s*q + r reads input rows q + c_r + j
 // (j < K/s) with weight taps k0(r) + j*s, k0(r) = (pad - r) mod s, c_r = -floor((pad - r)/s). Phases
 // with the same c_r form one conv GEMM whose N stacks the phases (N = phases*OC); written with row
@@ -59,6 +62,7 @@ private:
         int r0[2] = {0, 0}, nph[2] = {0, 0}, pad[2] = {0, 0};   // phase group: first phase, phases, row pad
         const half_t *Wt[2] = {nullptr, nullptr};               // [nph*C_out][taps][3 C_in]
         const float *bt[2] = {nullptr, nullptr};                // bias repeated per phase
+        const float *abt[2] = {nullptr, nullptr};               // first unit's snake table, per phase
         Unit u[3];
     };
     Stage st_[5];

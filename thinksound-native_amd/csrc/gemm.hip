@@ -888,7 +888,21 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmBatch bt) 
         const float4 b = *(const float4 *)(P.bias + n);
         v.x += b.x; v.y += b.y; v.z += b.z; v.w += b.w;
     }
-    if constexpr (EPI == EPI_RSNAKE) {
+    if constexpr (EPI == EPI_SNAKE) {
+        float e[4] = {v.x, v.y, v.z, v.w};
+        half4 hi, lo;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float sn = sinf(e[j] * P.snake[n + j]);
+            e[j] = e[j] + sn * sn * P.snake[P.N + n + j];
+            hi[j] = (half_t)e[j];
+            lo[j] = (half_t)(e[j] - (float)hi[j]);
+        }
+        half_t *y = (half_t *)P.Y + rowmap_phys(P.ymap, m) * (long long)P.ldy + n;
+        *(half4 *)y = hi;
+        *(half4 *)(y + P.y_lo) = lo;
+        *(half4 *)(y + P.y_hi2) = hi;
+    } else if constexpr (EPI == EPI_RSNAKE) {
         float4 *xr = (float4 *)(P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n);
         if (P.r_add) {
             const float4 x = *xr;
@@ -950,6 +964,7 @@ int launch_gemm_reduce(const GemmBatch &b, int epi, hipStream_t st) {
     if (epi == EPI_RESID) TSN_LAUNCH(splitk_reduce_kernel<EPI_RESID>, grid, block, 0, st, b);
     else if (epi == EPI_STORE) TSN_LAUNCH(splitk_reduce_kernel<EPI_STORE>, grid, block, 0, st, b);
     else if (epi == EPI_RSNAKE) TSN_LAUNCH(splitk_reduce_kernel<EPI_RSNAKE>, grid, block, 0, st, b);
+    else if (epi == EPI_SNAKE) TSN_LAUNCH(splitk_reduce_kernel<EPI_SNAKE>, grid, block, 0, st, b);
     else { set_error("gemm reduce: epilogue without split-K support"); return TSN_ERR_ARG; }
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
@@ -968,7 +983,7 @@ const char *gemm_reduce_name(const GemmBatch &b, int epi) {
                : epi == EPI_QKV ? "gemm_fixup_kernel<2>" : epi == EPI_SNAKE ? "gemm_fixup_kernel<4>"
                : epi == EPI_RSNAKE ? "gemm_fixup_kernel<5>" : "gemm_fixup_kernel<3>";
     return epi == EPI_RESID ? "splitk_reduce_kernel<1>" : epi == EPI_RSNAKE ? "splitk_reduce_kernel<5>"
-                                                                            : "splitk_reduce_kernel<0>";
+           : epi == EPI_SNAKE ? "splitk_reduce_kernel<4>" : "splitk_reduce_kernel<0>";
 }
 
 void gemm_problem_init(GemmProblem &p) {
@@ -1071,21 +1086,46 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     TSN_REQUIRE(pipe || (epi != EPI_SNAKE && epi != EPI_RSNAKE),
                 "gemm snake: needs the pipelined kernel (f16 A, 16-byte aligned rows)");
     TSN_REQUIRE(pipe || !any_half, "gemm: half-width W needs the pipelined kernel (f16 A, 16-byte aligned rows)");
-    if (pipe && (epi == EPI_RESID || epi == EPI_STORE || epi == EPI_RSNAKE) && b.ws && (!any_lo || epi == EPI_RSNAKE)) {
+    const bool snake_epi = epi == EPI_SNAKE || epi == EPI_RSNAKE;
+    if (pipe && (epi == EPI_RESID || epi == EPI_STORE || snake_epi) && b.ws && (!any_lo || snake_epi)) {
         int nkmin = 1 << 30;
         for (int i = 0; i < b.nprob; ++i) nkmin = std::min(nkmin, b.p[i].K / BK);
         int best = 0;
-        for (int kc = nkmin; kc >= 4; --kc) {
-            bool divides = true;
-            long long wg = 0;
-            for (int i = 0; i < b.nprob; ++i) {
-                const int nkp = b.p[i].K / BK;
-                divides = divides && nkp % kc == 0;
-                wg += (long long)b.p[i].tiles_m * b.p[i].tiles_n * (nkp / kc);
+        if (b.split_waves) {
+            // estimated time in K tiles: waves x tiles per split, plus the partial sums written and read
+            // (about 2.15 MB per K-tile time) when split
+            double best_cost = 1e30;
+            for (int kc = nkmin; kc >= 2; --kc) {
+                bool divides = true;
+                long long wg = 0;
+                double part = 0;
+                for (int i = 0; i < b.nprob; ++i) {
+                    const int nkp = b.p[i].K / BK;
+                    divides = divides && nkp % kc == 0;
+                    wg += (long long)b.p[i].tiles_m * b.p[i].tiles_n * (nkp / kc);
+                    part += 8.0 * (nkp / kc) * b.p[i].M * (double)b.p[i].N;
+                }
+                if (!divides) continue;
+                const bool split = kc < nkmin || wg > b.total_tiles;
+                const double cost = (double)((wg + NCU - 1) / NCU) * kc + (split ? 2.0 + part / 2.15e6 : 0.0);
+                if (cost < best_cost) {
+                    best_cost = cost;
+                    best = kc;
+                }
             }
-            if (!divides) continue;
-            best = kc;
-            if (wg >= 224) break;
+        } else {
+            for (int kc = nkmin; kc >= 4; --kc) {
+                bool divides = true;
+                long long wg = 0;
+                for (int i = 0; i < b.nprob; ++i) {
+                    const int nkp = b.p[i].K / BK;
+                    divides = divides && nkp % kc == 0;
+                    wg += (long long)b.p[i].tiles_m * b.p[i].tiles_n * (nkp / kc);
+                }
+                if (!divides) continue;
+                best = kc;
+                if (wg >= 224) break;
+            }
         }
         if (best > 0 && best < nkmin + 1) {
             size_t need = 0;
@@ -1100,8 +1140,9 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
                     GemmProblem &p = b.p[i];
                     p.splits = p.K / BK / best;
                     if (p.splits > 1) {
-                        TSN_REQUIRE(p.N % 4 == 0 && (epi == EPI_STORE ? p.ldy % 4 == 0
-                                                                      : p.ldr % 4 == 0 && p.gate_ld % 4 == 0),
+                        TSN_REQUIRE(p.N % 4 == 0 && ((epi == EPI_STORE || epi == EPI_SNAKE)
+                                                         ? p.ldy % 4 == 0
+                                                         : p.ldr % 4 == 0 && p.gate_ld % 4 == 0),
                                     "gemm split-K: N and output strides must be multiples of 4");
                         p.ws = b.ws + off / sizeof(float);
                         off += (size_t)p.splits * p.M * p.N * sizeof(float);
@@ -1117,7 +1158,7 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     // that grid = waves * longest K range per workgroup (+2 for a split-K reduce); stream-K = units
     // per workgroup + pipeline fill, partial store and fixup.
     b.sk = 0;
-    if (pipe && b.ws) {
+    if (pipe && b.ws && !b.split_waves) {
         long long units = 0, cur = 0;
         int nkmax = 0, split = 0;
         for (int i = 0; i < b.nprob; ++i) {

@@ -76,6 +76,10 @@ struct GemmBatch {
     int sk = 0, sk_g = 0;
     long long sk_units = 0;
     int hl = 0;   // some problem reads half-width W (selects the kernel variant)
+    // nonzero: never stream-K, and choose the classic K split by the estimated time (waves x K tiles
+    // per split, plus the partial-sum traffic). For long-K GEMMs with few tiles, whose A and W tiles
+    // would not be shared in L2 under stream-K's staggered K ranges.
+    int split_waves = 0;
 };
 
 // a_f32: A operand is f32 (converted to f16 on load). All problems share the epilogue kind.

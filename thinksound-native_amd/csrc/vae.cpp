@@ -325,6 +325,7 @@ int VaeModel::enqueue_decode(const float *latent, float *audio) {
         b.nprob = n;
         b.ws = ws_;
         b.ws_bytes = ws_bytes_;
+        b.split_waves = 1;   // long-K stages: classic split-K, which keeps W and A tiles shared in L2
     };
 
     int T = s.T, C = s.width[0];

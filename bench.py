@@ -132,7 +132,7 @@ def read_traffic(kernel):
     return None
 
 
-def stats_summary(stats_csv, cmd):
+def stats_summary(stats_csv, cmd, title="eager launches of the DiT evaluation (B=2, La=256, Lt=141, S=397)"):
     """Text summary of a rocprofv3 --kernel-trace --stats kernel_stats.csv"""
     import csv
     rows = []
@@ -141,12 +141,48 @@ def stats_summary(stats_csv, cmd):
             rows.append((short_kernel_name(r["Name"]), int(r["Calls"]), float(r["TotalDurationNs"]) / 1e6,
                          float(r["AverageNs"]) / 1e3, float(r["MinNs"]) / 1e3, float(r["MaxNs"]) / 1e3,
                          float(r["Percentage"])))
-    lines = ["# rocprofv3 kernel statistics, eager launches of the DiT evaluation (B=2, La=256, Lt=141, S=397)",
+    lines = ["# rocprofv3 kernel statistics, " + title,
              "# command: " + cmd,
              "%-28s %8s %12s %10s %10s %10s %7s" % ("kernel", "calls", "total ms", "avg us", "min us", "max us", "%")]
     for r in sorted(rows, key=lambda r: -r[2]):
         lines.append("%-28s %8d %12.3f %10.3f %10.3f %10.3f %7.2f" % r)
     return "\n".join(lines) + "\n"
+
+
+def profile_pass(which):
+    """workload for rocprofv3 --kernel-trace: eager launches only. vae: five 8 s decodes (T=172);
+    enc: five CLIP and five T5 encodes of 77 tokens at the reference sizes"""
+    tsn = importlib.import_module("thinksound-native_amd")
+    rt = tsn.Runtime(0)
+    if which == "vae":
+        spec = tsn.vae_spec_for_duration(8)
+        m = tsn.VaeModel(rt, spec)
+        m.upload_weights(tsn.vae_synth_weights(spec, 4242))
+        z = rt.array(tsn.synth_normal_f32(4242, 2000, 0.0, 1.0, (spec.T, spec.latent)))
+        a = rt.empty((tsn.vae_audio_len(spec), spec.out_ch))
+        for i in range(5):
+            m.decode(z, a)
+            rt.sync()
+            log("profile pass: vae decode %d done" % i)
+        m.close()
+    else:
+        for name, spec, synth, cls in (("clip", tsn.clip_spec_default(), tsn.clip_synth_weights, tsn.ClipModel),
+                                       ("t5", tsn.t5_spec_default(), tsn.t5_synth_weights, tsn.T5Model)):
+            m = cls(rt, spec)
+            m.upload_weights(synth(spec, 4242))
+            ids = np.arange(spec.ctx, dtype=np.int32) % (spec.vocab - 1) + 1
+            width = spec.H if name == "clip" else spec.d
+            a, g = rt.empty((spec.ctx, width)), rt.empty((width,))
+            for i in range(5):
+                if name == "clip":
+                    m.encode(ids, a, g)
+                else:
+                    m.encode(ids, a)
+                rt.sync()
+                log("profile pass: %s encode %d done" % (name, i))
+            m.close()
+    rt.close()
+    return 0
 
 
 def pmc_pass():
@@ -360,12 +396,18 @@ def main():
                     help="print the traffic summary of two counter-collection CSVs (no GPU use)")
     ap.add_argument("--stats-summary", nargs=2, metavar=("STATS_CSV", "CMD"),
                     help="print the summary of a rocprofv3 kernel_stats.csv (no GPU use)")
+    ap.add_argument("--stats-title", default=None, help="workload line of --stats-summary")
+    ap.add_argument("--profile-pass", choices=["vae", "enc"],
+                    help="only run eager VAE decodes or text-encoder passes (workload for rocprofv3 --kernel-trace)")
     args = ap.parse_args()
     if args.pmc_summary:
         sys.stdout.write(pmc_summary(*args.pmc_summary))
         return 0
     if args.stats_summary:
-        sys.stdout.write(stats_summary(*args.stats_summary))
+        if args.stats_title:
+            sys.stdout.write(stats_summary(*args.stats_summary, title=args.stats_title))
+        else:
+            sys.stdout.write(stats_summary(*args.stats_summary))
         return 0
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (one process, one MI355X); --gpus %d is not supported"
@@ -374,6 +416,8 @@ def main():
 
     if args.pmc_pass:
         return pmc_pass()
+    if args.profile_pass:
+        return profile_pass(args.profile_pass)
 
     tsn = importlib.import_module("thinksound-native_amd")
     spec = tsn.default_spec(1)

@@ -116,32 +116,40 @@ __global__ void enc_gemm_reduce_kernel(const EncGemmArgs g) {
     enc_epi(g, m, n, v);
 }
 
-// one wave per row: LayerNorm (w, b; mean then variance of the centred row) or RMSNorm (w)
+// one 256-thread workgroup per row: LayerNorm (w, b; mean then variance of the centred row) or
+// RMSNorm (w); sums reduced per wave, then across the 4 waves in wave order through LDS
 template <bool LN>
 __global__ __launch_bounds__(256) void enc_norm_kernel(const float *__restrict__ x, float *__restrict__ y,
                                                        const float *__restrict__ w, const float *__restrict__ b,
                                                        int rows, int H, float eps) {
-    const int row = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (row >= rows) return;
+    __shared__ float part[4];
+    const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *xr = x + (long long)row * H;
+    auto block_sum = [&](float v) {
+        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+        __syncthreads();   // part[] free from the previous reduction
+        if (lane == 0) part[wave] = v;
+        __syncthreads();
+        return ((part[0] + part[1]) + part[2]) + part[3];
+    };
     float s = 0.0f;
-    for (int c = lane; c < H; c += 64) s += LN ? xr[c] : xr[c] * xr[c];
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
+    for (int c = tid; c < H; c += 256) s += LN ? xr[c] : xr[c] * xr[c];
+    s = block_sum(s);
     float mean = 0.0f, inv;
     if (LN) {
         mean = s / (float)H;
         float v = 0.0f;
-        for (int c = lane; c < H; c += 64) {
+        for (int c = tid; c < H; c += 256) {
             const float d = xr[c] - mean;
             v += d * d;
         }
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+        v = block_sum(v);
         inv = 1.0f / sqrtf(v / (float)H + eps);
     } else {
         inv = 1.0f / sqrtf(s / (float)H + eps);
     }
     float *yr = y + (long long)row * H;
-    for (int c = lane; c < H; c += 64) yr[c] = LN ? (xr[c] - mean) * inv * w[c] + b[c] : xr[c] * inv * w[c];
+    for (int c = tid; c < H; c += 256) yr[c] = LN ? (xr[c] - mean) * inv * w[c] + b[c] : xr[c] * inv * w[c];
 }
 
 constexpr int EA_Q = 16;      // queries per workgroup
@@ -262,8 +270,8 @@ int launch_gemm_f32(const EncGemmArgs &gin, hipStream_t st) {
 int launch_enc_norm(const float *x, float *y, const float *w, const float *b, int rows, int H, float eps, bool ln,
                     hipStream_t st) {
     TSN_REQUIRE(x && y && w && rows > 0 && H > 0 && (!ln || b), "enc_norm: arguments");
-    if (ln) TSN_LAUNCH(enc_norm_kernel<true>, dim3((rows + 3) / 4), dim3(256), 0, st, x, y, w, b, rows, H, eps);
-    else TSN_LAUNCH(enc_norm_kernel<false>, dim3((rows + 3) / 4), dim3(256), 0, st, x, y, w, b, rows, H, eps);
+    if (ln) TSN_LAUNCH(enc_norm_kernel<true>, dim3(rows), dim3(256), 0, st, x, y, w, b, rows, H, eps);
+    else TSN_LAUNCH(enc_norm_kernel<false>, dim3(rows), dim3(256), 0, st, x, y, w, b, rows, H, eps);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }

@@ -330,6 +330,54 @@ def bench_vae(tsn, rt, args):
             "cpu_baseline": cpu, "launch": "hipGraph replay"}
 
 
+def bench_workloads(tsn, rt, args):
+    """The other configured workloads, reported beside the metric: the 30 s clip (La=960, S=1101) as
+    one evaluation and the 24-step sampler, and the 16-sample batch (8 prompts x CFG) as one
+    evaluation; graph replays, synthetic BF16 weights."""
+    out = {}
+    for wl, name in ((3, "clip_30s"), (4, "batch16")):
+        spec = tsn.default_spec(wl)
+        m = tsn.DitModel(rt, spec)
+        m.upload_weights(tsn.synth_weights(spec, 4242, 0.0))
+        inp = tsn.synth_inputs(spec, 4242, cfg_pairs=True)
+        z, tt, text, pooled = (rt.array(inp[k]) for k in ("z", "t", "text", "pooled"))
+        v = rt.empty((spec.B, spec.La, spec.latent))
+        m.capture_forward(z, tt, text, pooled, v)
+        for _ in range(5):
+            m.replay()
+        rt.sync()
+        n = 20
+        rt.begin()
+        for _ in range(n):
+            m.replay()
+        ms = rt.commit() / n
+        stats = m.profile_forward(z, tt, text, pooled, v)
+        flops = sum(k["flops"] for k in stats)
+        for k in sorted(stats, key=lambda k: -k["ms"])[:6]:
+            log("  %s %-28s %4d launches %8.3f ms  %7.1f TFLOP/s  %7.1f GB/s"
+                % (name, k["name"], k["launches"], k["ms"], k["flops"] / (k["ms"] * 1e9) if k["ms"] else 0,
+                   k["bytes"] / (k["ms"] * 1e6) if k["ms"] else 0))
+        r = {"B": spec.B, "La": spec.La, "Lt": spec.Lt, "ms_per_eval": round(ms, 4),
+             "evals_per_s": round(1e3 / ms, 2), "eval_gflop": round(flops / 1e9, 1),
+             "mfma_frac_eval": round(flops / (ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4)}
+        if wl == 3:
+            x0 = inp["z"][0::2].copy()
+            x = rt.array(x0)
+            m.capture_sample(x, text, pooled, 24, 5.0)
+            m.replay()
+            rt.sync()
+            x.upload(x0)
+            rt.begin()
+            m.replay()
+            r["sampler_ms"] = round(rt.commit(), 3)
+        log("bench %s: %.4f ms/eval, %.1f GFLOP, %.1f%% of the f16 MFMA peak%s"
+            % (name, ms, flops / 1e9, 100 * r["mfma_frac_eval"],
+               (", 24-step sampler %.2f ms" % r["sampler_ms"]) if "sampler_ms" in r else ""))
+        out[name] = r
+        m.close()
+    return out
+
+
 def bench_encoders(tsn, rt, args):
     """The reference's text encoders, once per prompt: CLIP (24 layers, H 1024) and T5 v1.1 XL (24 layers,
     d 2048, d_ff 5120) over 77 tokens, f32 synthetic weights; eager launches, median of 5."""
@@ -388,6 +436,7 @@ def main():
     ap.add_argument("--no-ref", action="store_true", help="skip the reference checkpoint graph section")
     ap.add_argument("--no-vae", action="store_true", help="skip the VAE decoder section")
     ap.add_argument("--no-enc", action="store_true", help="skip the text-encoder section")
+    ap.add_argument("--no-wl", action="store_true", help="skip the 30 s and batch-16 workload section")
     ap.add_argument("--eager", action="store_true",
                     help="launch kernel by kernel instead of replaying hipGraphs (for profilers that do not follow graphs)")
     ap.add_argument("--pmc-pass", action="store_true",
@@ -520,6 +569,9 @@ def main():
     enc = None
     if not args.no_enc and not args.eager:
         enc = bench_encoders(tsn, rt, args)
+    wls = None
+    if not args.no_wl and not args.eager:
+        wls = bench_workloads(tsn, rt, args)
 
     # ---------------- CPU baseline: the oracle, one full evaluation ----------------
     cpu = None
@@ -570,6 +622,7 @@ def main():
         "reference_graph": ref,
         "vae_decoder": vae,
         "text_encoders": enc,
+        "other_workloads": wls,
         "accumulate": "f32 (f16 MFMA operands from BF16 weights; f32 residual stream)",
         "launch": "eager" if args.eager else "hipGraph replay",
     }

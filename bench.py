@@ -378,6 +378,27 @@ def bench_workloads(tsn, rt, args):
     return out
 
 
+def bench_hbm(tsn, rt, args):
+    """The HBM-bound norm kernel on a large shape: adaLN (LayerNorm + broadcast shift/scale) over
+    65536 rows x 1024, f32 in, f16 out; algorithmic bytes = rows*H*(4 + 2) + modulation, 20 launches"""
+    rows, H = 65536, 1024
+    x = rt.array(tsn.synth_normal_f32(4242, 3000, 0.0, 1.0, (rows, H)))
+    mod = rt.array(tsn.synth_normal_f32(4242, 3001, 0.0, 0.1, (6 * H,)))
+    y = rt.empty((rows, H), np.float16)
+    for _ in range(3):
+        rt.adaln_ln(x, mod, y, 1, rows, H, 0, 6, 0, 1e-5)
+    rt.sync()
+    n = 20
+    rt.begin()
+    for _ in range(n):
+        rt.adaln_ln(x, mod, y, 1, rows, H, 0, 6, 0, 1e-5)
+    ms = rt.commit() / n
+    gbs = (rows * H * 6.0 + 2 * H * 4.0) / (ms * 1e-3) / 1e9
+    log("bench hbm: adaLN 65536 x 1024 %.1f us, %.0f GB/s (%.1f%% of 8 TB/s)" % (ms * 1e3, gbs, gbs / 80.0))
+    return {"adaln_ln_65536x1024_f16": {"us": round(ms * 1e3, 2), "gbs": round(gbs, 1),
+                                         "frac_hbm_peak": round(gbs / PEAK_HBM_GBS, 4)}}
+
+
 def bench_encoders(tsn, rt, args):
     """The reference's text encoders, once per prompt: CLIP (24 layers, H 1024) and T5 v1.1 XL (24 layers,
     d 2048, d_ff 5120) over 77 tokens, f32 synthetic weights; eager launches, median of 5."""
@@ -572,6 +593,7 @@ def main():
     wls = None
     if not args.no_wl and not args.eager:
         wls = bench_workloads(tsn, rt, args)
+        wls["hbm_kernels"] = bench_hbm(tsn, rt, args)
 
     # ---------------- CPU baseline: the oracle, one full evaluation ----------------
     cpu = None

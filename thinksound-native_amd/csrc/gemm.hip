@@ -166,6 +166,20 @@ __device__ __forceinline__ void gemm_epilogue(const GemmProblem &P, floatx4 (&ac
 }
 
 
+// tile index -> (m tile, n tile). Tiles come in groups of up to 8 m tiles; inside a group n is the
+// slow index and m the fast one. Consecutive workgroups land on one XCD (xcd_remap), so the tiles an
+// XCD runs together share the group's A rows and a few W columns in its L2. With 8 or fewer m tiles
+// this is the plain m-fastest order.
+__device__ __forceinline__ void tile_mn(int t, int tiles_m, int tiles_n, int &tm, int &tn) {
+    constexpr int GM = 8;
+    const int grp = t / (GM * tiles_n);
+    const int m_first = grp * GM;
+    const int gm = min(GM, tiles_m - m_first);
+    const int r = t - grp * GM * tiles_n;
+    tn = r / gm;
+    tm = m_first + (r - tn * gm);
+}
+
 template <bool A_F32, int EPI>
 __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const GemmBatch bt) {
     __shared__ __attribute__((aligned(16))) half_t sA[2][BM * LDSW];
@@ -177,7 +191,8 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const GemmBatch bt) {
     const GemmProblem &P = bt.p[pi];
 
     const int local = tile - P.tile_start;
-    const int tn = local / P.tiles_m, tm = local - tn * P.tiles_m;
+    int tm, tn;
+    tile_mn(local, P.tiles_m, P.tiles_n, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int M = P.M, N = P.N, K = P.K;
 
@@ -786,7 +801,8 @@ __device__ __forceinline__ void pipe_dp(const GemmBatch &bt) {
     const int per_split = P.tiles_m * P.tiles_n;
     const int ks = local / per_split;
     const int rem = local - ks * per_split;
-    const int tn = rem / P.tiles_m, tm = rem - tn * P.tiles_m;
+    int tm, tn;
+    tile_mn(rem, P.tiles_m, P.tiles_n, tm, tn);
     const int nk = P.K / BK / P.splits;
     pipe_tile<EPI, HL, false>(P, tm * BM, tn * BN, ks * nk, nk, nullptr, ks, tid);
 }
@@ -815,7 +831,8 @@ __global__ __launch_bounds__(512, 1) void gemm_sk_kernel(const GemmBatch bt) {
         const int tile = (int)(lu / nkp);
         const int kbeg = (int)(lu - (long long)tile * nkp);
         const int nk = (int)min((long long)(nkp - kbeg), ue - u);
-        const int tn = tile / P.tiles_m, tm = tile - tn * P.tiles_m;
+        int tm, tn;
+        tile_mn(tile, P.tiles_m, P.tiles_n, tm, tn);
         float *part = (kbeg == 0 && nk == nkp) ? nullptr : bt.ws + ((long long)wg * 2 + (seg == 0 ? 0 : 1)) * (BM * BN);
         pipe_tile<EPI, true, true>(P, tm * BM, tn * BN, kbeg, nk, part, 0, tid);
         u += nk;
@@ -857,7 +874,8 @@ __global__ __launch_bounds__(512) void gemm_fixup_kernel(const GemmBatch bt) {
         *(float4 *)(tile + row * TP + col) = make_float4(v[p][0], v[p][1], v[p][2], v[p][3]);
     }
     __syncthreads();
-    const int tn = local / P.tiles_m, tm = local - tn * P.tiles_m;
+    int tm, tn;
+    tile_mn(local, P.tiles_m, P.tiles_n, tm, tn);
     tile_epilogue<EPI>(P, tile, tm * BM, tn * BN, 0, tid);
 }
 

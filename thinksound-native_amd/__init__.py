@@ -521,17 +521,27 @@ class VaeModel:
     def load_gguf(self, path):
         call("tsn_vae_load_gguf", self.h, os.fsencode(path))
 
+    def _check(self, latent, audio):
+        s = self.spec
+        want_l, want_a = (s.T, s.latent), (vae_audio_len(s), s.out_ch)
+        if int(np.prod(latent.shape)) != want_l[0] * want_l[1] or int(np.prod(audio.shape)) != want_a[0] * want_a[1]:
+            raise ValueError("vae: latent %s and audio %s expected, got %s and %s"
+                             % (want_l, want_a, latent.shape, audio.shape))
+
     def decode(self, latent, audio):
         """latent [T][latent] -> audio [T_audio][out_ch], device arrays, enqueued on the runtime's stream"""
+        self._check(latent, audio)
         call("tsn_vae_decode", self.h, latent.p, audio.p)
 
     def capture_decode(self, latent, audio):
+        self._check(latent, audio)
         call("tsn_vae_capture_decode", self.h, latent.p, audio.p)
 
     def replay(self):
         call("tsn_vae_replay", self.h)
 
     def profile_decode(self, latent, audio):
+        self._check(latent, audio)
         cap = 64
         arr = (KernelStat * cap)()
         n = ctypes.c_int()
@@ -630,12 +640,19 @@ class ClipModel:
             raise ValueError("clip: %d ids expected, got shape %s" % (self.spec.ctx, ids.shape))
         return ids
 
+    def _outs(self, per_token, glob):
+        s = self.spec
+        if int(np.prod(per_token.shape)) != s.ctx * s.H or int(np.prod(glob.shape)) != s.H:
+            raise ValueError("clip: per_token [%d, %d] and global [%d] expected" % (s.ctx, s.H, s.H))
+
     def encode(self, ids, per_token, glob):
         ids = self._ids(ids)
+        self._outs(per_token, glob)
         call("tsn_clip_encode", self.h, ptr(ids), per_token.p, glob.p)
 
     def profile_encode(self, ids, per_token, glob):
         ids = self._ids(ids)
+        self._outs(per_token, glob)
         arr, n = (KernelStat * 64)(), ctypes.c_int()
         call("tsn_clip_profile_encode", self.h, ptr(ids), per_token.p, glob.p, arr, 64, ctypes.byref(n))
         return _stats(arr, n)
@@ -668,12 +685,18 @@ class T5Model:
             raise ValueError("t5: %d ids expected, got shape %s" % (self.spec.ctx, ids.shape))
         return ids
 
+    def _out(self, out):
+        if int(np.prod(out.shape)) != self.spec.ctx * self.spec.d:
+            raise ValueError("t5: out [%d, %d] expected, got %s" % (self.spec.ctx, self.spec.d, out.shape))
+
     def encode(self, ids, out):
         ids = self._ids(ids)
+        self._out(out)
         call("tsn_t5_encode", self.h, ptr(ids), out.p)
 
     def profile_encode(self, ids, out):
         ids = self._ids(ids)
+        self._out(out)
         arr, n = (KernelStat * 64)(), ctypes.c_int()
         call("tsn_t5_profile_encode", self.h, ptr(ids), out.p, arr, 64, ctypes.byref(n))
         return _stats(arr, n)

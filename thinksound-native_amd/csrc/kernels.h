@@ -223,7 +223,7 @@ int launch_add_period_hilo(const float *x, const float *pe, int P, half_t *out, 
 // table ab = [exp(alpha) (C) | exp(-beta) (C)], snake(x) = x + sin(x*ea)^2*eb; parts [hi | lo | hi]
 // (lo_part 1, activation operand) or [hi | hi | lo] (lo_part 2, weight operand)
 int launch_split3(const float *x, long long rows, int C, const float *ab, int lo_part, half_t *out, hipStream_t st);
-// y [T][OC] = conv(snake(x), W [OC][C][KK], pad), no bias; x [T][C] f32, OC in {1, 2, 4}, C % 64 == 0
+// y [T][OC] = conv(snake(x), W [OC][C][KK], pad), no bias; x [T][C] f32, OC in {1, 2, 4}, KK == 7, C % 8 == 0
 int launch_conv_out(const float *x, const float *ab, const float *W, float *y, int T, int C, int OC, int KK, int pad,
                     hipStream_t st);
 // Text encoders (enc.hip), all f32.

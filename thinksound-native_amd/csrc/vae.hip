@@ -41,57 +41,94 @@ __global__ void split3_kernel(const float *__restrict__ x, long long rows, int C
     *(half8 *)(o + 2 * C) = lo_part == 1 ? hi : lo;
 }
 
-constexpr int CO_TB = 64;   // output rows per workgroup
-constexpr int CO_CH = 64;   // channels per LDS chunk
-constexpr int CO_KMAX = 15; // largest kernel width
+constexpr int CO_TB = 64;    // output rows per workgroup (16 per wave)
+constexpr int CO_CH = 128;   // channels per LDS chunk (2 per lane)
+constexpr int CO_K = 7;      // kernel width
+constexpr int CO_ROWS = CO_TB + CO_K - 1;
+constexpr int CO_PER = (CO_ROWS * CO_CH + 255) / 256;   // staged elements per thread and chunk
 
-// y[t][c] = sum_{i,k} snake(x)[t - pad + k][i] * W[c][i][k], zero rows outside [0, T); OC in {1, 2, 4}.
-// 256 threads: output (row r, channel c) is summed by 4/OC adjacent lanes, each over its share of
-// every channel chunk, then combined in lane order.
+// y[t][c] = sum_{i,k} snake(x)[t - pad + k][i] * W[c][i][k], zero rows outside [0, T), k < 7, OC in {1, 2, 4}.
+// The workgroup stages snake(x) rows of a 128-channel chunk in LDS; lane l of wave w holds channels
+// 2l, 2l+1 and accumulates all 16 x OC outputs of the wave's rows from them (each staged row read
+// once, feeding up to 7 outputs). The lanes' partial sums are then added by an xor butterfly, the
+// same order for every output.
+template <int OC>
 __global__ void __launch_bounds__(256) conv_out_kernel(const float *__restrict__ x, const float *__restrict__ ab,
                                                        const float *__restrict__ W, float *__restrict__ y, int T, int C,
-                                                       int OC, int KK, int pad) {
-    __shared__ float xs[(CO_TB + CO_KMAX - 1) * (CO_CH + 1)];
-    __shared__ float ws[4 * CO_CH * CO_KMAX];
-    const int tid = threadIdx.x;
+                                                       int pad) {
+    __shared__ float xs[CO_ROWS * CO_CH];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int t0 = blockIdx.x * CO_TB;
-    const int tpo = 4 / OC;
-    const int o = tid / tpo, h = tid - o * tpo;
-    const int r = o / OC, c = o - r * OC;
-    const int share = CO_CH / tpo;
-    const int rows = CO_TB + KK - 1;
-    float acc = 0.0f;
+    float acc[16][OC];
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int c = 0; c < OC; ++c) acc[r][c] = 0.0f;
     for (int c0 = 0; c0 < C; c0 += CO_CH) {
-        for (int e = tid; e < rows * CO_CH; e += 256) {
+        const int cw = min(CO_CH, C - c0);   // channels of this chunk; the rest stay zero
+        float v[CO_PER];
+#pragma unroll
+        for (int j = 0; j < CO_PER; ++j) {
+            const int e = tid + 256 * j;
             const int rr = e / CO_CH, i = e - rr * CO_CH;
             const int t = t0 - pad + rr;
-            float v = 0.0f;
-            if (t >= 0 && t < T) {
-                const float u = x[(long long)t * C + c0 + i];
-                const float sn = sinf(u * ab[c0 + i]);
-                v = u + sn * sn * ab[C + c0 + i];
+            v[j] = (rr < CO_ROWS && i < cw && t >= 0 && t < T) ? x[(long long)t * C + c0 + i] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < CO_PER; ++j) {
+            const int e = tid + 256 * j;
+            const int rr = e / CO_CH, i = e - rr * CO_CH;
+            if (rr < CO_ROWS) {
+                float u = 0.0f;   // snake(0) = 0: padding rows and channels past the chunk stay zero
+                if (i < cw) {
+                    const float sn = sinf(v[j] * ab[c0 + i]);
+                    u = v[j] + sn * sn * ab[C + c0 + i];
+                }
+                xs[e] = u;
             }
-            xs[rr * (CO_CH + 1) + i] = v;
         }
-        for (int e = tid; e < OC * CO_CH * KK; e += 256) {
-            const int cc = e / (CO_CH * KK), rem = e - cc * CO_CH * KK;
-            const int i = rem / KK, k = rem - i * KK;
-            ws[e] = W[((long long)cc * C + c0 + i) * KK + k];
+        // this lane's weights: w[c][j][k] for channels c0 + 2*lane + j
+        float w[OC][2][CO_K];
+#pragma unroll
+        for (int c = 0; c < OC; ++c)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int i = 2 * lane + j;
+#pragma unroll
+                for (int k = 0; k < CO_K; ++k) w[c][j][k] = i < cw ? W[((long long)c * C + c0 + i) * CO_K + k] : 0.0f;
+            }
+        __syncthreads();
+#pragma unroll
+        for (int jr = 0; jr < 16 + CO_K - 1; ++jr) {   // staged row 16*wave + jr feeds outputs r = jr - k
+            const float2 xv = *(const float2 *)&xs[(16 * wave + jr) * CO_CH + 2 * lane];
+#pragma unroll
+            for (int k = 0; k < CO_K; ++k) {
+                const int r = jr - k;
+                if (r < 0 || r >= 16) continue;
+#pragma unroll
+                for (int c = 0; c < OC; ++c) acc[r][c] = fmaf(xv.y, w[c][1][k], fmaf(xv.x, w[c][0][k], acc[r][c]));
+            }
         }
         __syncthreads();
-        const float *wc = ws + c * CO_CH * KK;
-        for (int i = h * share; i < (h + 1) * share; ++i)
-            for (int k = 0; k < KK; ++k) acc = fmaf(xs[(r + k) * (CO_CH + 1) + i], wc[i * KK + k], acc);
-        __syncthreads();
     }
-    // combine the tpo partial sums of one output (adjacent lanes) in lane order
-    if (tpo == 4) {
-        const float a1 = __shfl_down(acc, 1, 4), a2 = __shfl_down(acc, 2, 4), a3 = __shfl_down(acc, 3, 4);
-        acc = ((acc + a1) + a2) + a3;
-    } else if (tpo == 2) {
-        acc = acc + __shfl_down(acc, 1, 2);
-    }
-    if (h == 0 && t0 + r < T) y[(long long)(t0 + r) * OC + c] = acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int c = 0; c < OC; ++c) {
+            float a = acc[r][c];
+#pragma unroll
+            for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
+            acc[r][c] = a;
+        }
+    // lane r*OC + c writes output (row r, channel c) of the wave's 16 rows
+    float mine = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int c = 0; c < OC; ++c)
+            if (lane == r * OC + c) mine = acc[r][c];
+    const int t = t0 + 16 * wave + lane / OC;
+    if (lane < 16 * OC && t < T) y[(long long)t * OC + (lane % OC)] = mine;
 }
 
 } // namespace
@@ -110,10 +147,12 @@ int launch_conv_out(const float *x, const float *ab, const float *W, float *y, i
                     hipStream_t st) {
     TSN_REQUIRE(x && ab && W && y && T > 0, "conv_out: arguments");
     TSN_REQUIRE(OC == 1 || OC == 2 || OC == 4, "conv_out: 1, 2 or 4 output channels");
-    TSN_REQUIRE(C > 0 && C % CO_CH == 0, "conv_out: input channels must be a multiple of 64");
-    TSN_REQUIRE(KK >= 1 && KK <= CO_KMAX && pad >= 0 && pad < KK, "conv_out: kernel width 1..15, pad < width");
-    TSN_LAUNCH(conv_out_kernel, dim3((unsigned)((T + CO_TB - 1) / CO_TB)), dim3(256), 0, st, x, ab, W, y, T, C, OC,
-               KK, pad);
+    TSN_REQUIRE(C > 0 && C % 8 == 0, "conv_out: input channels must be a multiple of 8");
+    TSN_REQUIRE(KK == CO_K && pad >= 0 && pad < KK, "conv_out: kernel width 7, pad < width");
+    const dim3 grid((unsigned)((T + CO_TB - 1) / CO_TB)), block(256);
+    if (OC == 1) TSN_LAUNCH(conv_out_kernel<1>, grid, block, 0, st, x, ab, W, y, T, C, pad);
+    else if (OC == 2) TSN_LAUNCH(conv_out_kernel<2>, grid, block, 0, st, x, ab, W, y, T, C, pad);
+    else TSN_LAUNCH(conv_out_kernel<4>, grid, block, 0, st, x, ab, W, y, T, C, pad);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }

@@ -81,18 +81,29 @@ __device__ __forceinline__ float rows_max(float v) {
 // 16 rows one operand read touches (K rows 8 apart, see below) fall in distinct banks.
 __device__ __forceinline__ int sw(int r) { return (r & 7) ^ ((r >> 3) & 7); }
 
+__device__ inline int attn_xcd_remap(int bid, int nwg) {
+    const int xcd = bid & 7, idx = bid >> 3;
+    const int base = nwg >> 3, rem = nwg & 7;
+    return (xcd < rem ? xcd * (base + 1) : rem * (base + 1) + (xcd - rem) * base) + idx;
+}
+
 __global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
     __shared__ __attribute__((aligned(1024))) half_t smem[ANS * ASTAGE];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar DMA choices
     const int half = wave >> 2, wq = wave & 3;
-    const int bh = blockIdx.y;
+    // workgroup -> (head, 64-query tile), the query tiles of one head consecutive; consecutive
+    // workgroups run on one XCD (dispatch is round-robin over the 8 XCDs), so a head's K and Vt
+    // come from HBM once into that XCD's L2
+    const int nqt = (a.S + 63) >> 6;
+    const int wg = attn_xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = wg / nqt, qt = wg - bh * nqt;
     const int S = a.S, Sp = a.Sp;
     const half_t *Qp = a.Q + (long long)bh * S * 64;
     const i32x4 rk = make_rsrc(a.K + (long long)bh * S * 64);
     const i32x4 rv = make_rsrc(a.Vt + (long long)bh * 64 * Sp);
 
-    const int q = blockIdx.x * 64 + wq * 16 + (lane & 15);
+    const int q = qt * 64 + wq * 16 + (lane & 15);
     const int g = lane >> 4;
     half8 qf[2];
 #pragma unroll
@@ -294,7 +305,8 @@ int launch_attention(const AttnArgs &a, hipStream_t st) {
                 "attention: 16-byte aligned Q/K/Vt");
     TSN_REQUIRE((long long)a.S * 64 * 2 < (1LL << 31) && (long long)a.Sp * 64 * 2 < (1LL << 31),
                 "attention: per-head K/Vt extent must stay below 2 GB (buffer addressing)");
-    dim3 grid((a.S + 63) / 64, a.BH), block(512);
+    TSN_REQUIRE((long long)((a.S + 63) / 64) * a.BH < (1LL << 31), "attention: too many query tiles");
+    dim3 grid((unsigned)((a.S + 63) / 64 * a.BH)), block(512);
     TSN_LAUNCH(flash_attn_kernel, grid, block, 0, st, a);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;

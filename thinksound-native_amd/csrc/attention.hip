@@ -60,8 +60,13 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
     else if (n >= 4) __builtin_amdgcn_s_waitcnt(4 | (7 << 4) | (0xF << 8));
     else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0xF << 8));
 }
+// s_waitcnt lgkmcnt(0), then s_barrier: this wave's LDS reads have completed before any wave
+// passes, so a stage refilled by direct-to-LDS DMA after the barrier is never still being read
+// (s_barrier alone does not wait for them, and the compiler issues the next MFMAs' operand reads
+// ahead of it)
 __device__ __forceinline__ void block_barrier() {
     asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // vmcnt 63, expcnt 7: no wait; lgkmcnt 0
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 }

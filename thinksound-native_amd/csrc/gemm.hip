@@ -330,8 +330,13 @@ __device__ __forceinline__ void wait_vmcnt(int n) {
     else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0xF << 8));
 }
 
+// s_waitcnt lgkmcnt(0), then s_barrier: this wave's LDS reads have completed before any wave
+// passes, so a stage refilled by direct-to-LDS DMA after the barrier is never still being read
+// (s_barrier alone does not wait for them, and the compiler issues the next MFMAs' operand reads
+// ahead of it)
 __device__ __forceinline__ void block_barrier() {
     asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // vmcnt 63, expcnt 7: no wait; lgkmcnt 0
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
 }
@@ -816,6 +821,172 @@ __global__ __launch_bounds__(512, 1) void gemm_pipe_hl_kernel(const GemmBatch bt
     pipe_dp<EPI, true>(bt);
 }
 
+// gemm_small_kernel: 64x64 C tiles over the full K, 4 waves of 32x32 (2 x 2 MFMA blocks of 16x16),
+// the same swizzled direct-to-LDS ring as pipe_tile (5 stages of 16 KB, two workgroups per CU) and
+// the residual epilogue in place. For GEMMs whose 128x128 grid would need a K split to fill the
+// chip (M ~ 800, N = 1024, K = 1024): 64x64 tiles give four times the workgroups with no f32
+// partials to write and sum.
+constexpr int SB = 64;              // tile rows and columns
+constexpr int SSTAGE = SB * BK;     // halves per operand tile of one stage (8 KB)
+constexpr int STP = 68;             // pitch (floats) of the staged f32 C tile: 4 rows = 16 banks apart
+
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) {
+    static_assert(EPI == EPI_RESID, "gemm_small_kernel: residual epilogue only");
+    __shared__ __attribute__((aligned(1024))) half_t smem[2 * NS * SSTAGE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wg = xcd_remap(blockIdx.x, gridDim.x);
+    const int pi = (bt.nprob > 2 && wg >= bt.p[2].tile_start) ? 2 : (bt.nprob > 1 && wg >= bt.p[1].tile_start) ? 1 : 0;
+    const GemmProblem &P = bt.p[pi];
+    int tm, tn;
+    tile_mn(wg - P.tile_start, P.tiles_m, P.tiles_n, tm, tn);
+    const int m0 = tm * SB, n0 = tn * SB;
+    const int M = P.M, N = P.N, lda = P.lda, Kc = P.Kc, pad = P.pad, aT = P.a_T, ldw = P.ldw;
+    const RowMap am = P.amap;
+    const i32x4 rsa = make_rsrc(P.A);
+    const i32x4 rsb = make_rsrc(P.W);
+
+    // loader rows of this lane: wave*16 + i*8 + (lane >> 3), 16-byte chunk (lane & 7) ^ (lane >> 3)
+    const int lr = lane >> 3, lc = (lane & 7) ^ lr;
+    int a_base[2], a_ts0[2], b_off[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = wave * 16 + i * 8 + lr;
+        const int m = m0 + r;
+        const int mm = m < M ? m : 0;
+        const int b = mm / am.L;
+        const int t = mm - b * am.L;
+        a_ts0[i] = m < M ? t - pad : -(1 << 29);
+        a_base[i] = ((b * am.seg + am.off + t - pad) * lda + lc * 8) * 2;
+        const int n = n0 + r;
+        b_off[i] = n < N ? (n * ldw + lc * 8) * 2 : -1;
+    }
+    const int lda2 = lda * 2;
+    int nt_trow = 0, nt_kin = 0, nt_kw = 0;   // tap, offset inside it, W column of the next K tile
+    auto issue = [&](int stage) {
+        const int trow = nt_trow, kin = nt_kin, kw = nt_kw;
+        nt_kw += BK;
+        nt_kin += BK;
+        if (nt_kin == Kc) {
+            nt_kin = 0;
+            ++nt_trow;
+        }
+        const int kc2 = kin * 2 + trow * lda2;
+        lds_char *sa = (lds_char *)(smem + stage * SSTAGE) + wave * 2048;
+        lds_char *sb = (lds_char *)(smem + (NS + stage) * SSTAGE) + wave * 2048;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int ts = a_ts0[i] + trow;
+            const unsigned vo = (ts >= 0 && ts < aT) ? (unsigned)(a_base[i] + kc2) : 0x80000000u;
+            dma16(rsa, vo, sa + i * 1024);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const unsigned vo = b_off[i] >= 0 ? (unsigned)(b_off[i] + kw * 2) : 0x80000000u;
+            dma16(rsb, vo, sb + i * 1024);
+        }
+    };
+
+    floatx4 acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const int wm = wave >> 1, wn = wave & 1;
+    int a_rd[2][2], b_rd[2][2];
+#pragma unroll
+    for (int kh = 0; kh < 2; ++kh) {
+        const int slot = (kh * 4 + (lane >> 4)) ^ (lane & 7);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            a_rd[kh][i] = (wm * 32 + i * 16 + (lane & 15)) * BK + slot * 8;
+            b_rd[kh][i] = (wn * 32 + i * 16 + (lane & 15)) * BK + slot * 8;
+        }
+    }
+    auto compute = [&](int stage) {
+        const half_t *sa = smem + stage * SSTAGE, *sb = smem + (NS + stage) * SSTAGE;
+#pragma unroll
+        for (int kh = 0; kh < 2; ++kh) {
+            half8 af[2], bf[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                af[i] = *(const half8 *)(sa + a_rd[kh][i]);
+                bf[i] = *(const half8 *)(sb + b_rd[kh][i]);
+            }
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
+    };
+
+    // the K loop of pipe_tile: tile kt landed in stage kt%NS, tiles kt+1..kt+NS-1 in flight
+    const int nk = P.K / BK;
+    issue(0);
+#pragma unroll
+    for (int j = 1; j < NS - 1; ++j)
+        if (nk > j) issue(j);
+    wait_vmcnt(4 * min(nk - 1, NS - 2));
+    block_barrier();
+    if (nk > NS - 1) issue(NS - 1);
+#define TSN_SMALL_STEP(S)                                                                       \
+    {                                                                                           \
+        compute(S);                                                                             \
+        wait_vmcnt(4 * (NS - 2));                                                               \
+        block_barrier();                                                                        \
+        issue(S);                                                                               \
+    }
+    int kt = 0;
+    for (; kt + 2 * NS <= nk; kt += NS) {
+        TSN_SMALL_STEP(0)
+        TSN_SMALL_STEP(1)
+        TSN_SMALL_STEP(2)
+        TSN_SMALL_STEP(3)
+        TSN_SMALL_STEP(4)
+    }
+#undef TSN_SMALL_STEP
+    for (; kt < nk; ++kt) {
+        const int st = kt % NS;
+        compute(st);
+        if (kt + 1 < nk) {
+            wait_vmcnt(4 * min(nk - 2 - kt, NS - 2));
+            block_barrier();
+            if (kt + NS < nk) issue(st);
+        }
+    }
+    // C tile through LDS, then 16-byte residual updates: x += gate * (acc + bias)
+    block_barrier();
+    float *tile = (float *)smem;
+    {
+        const int rb = wm * 32 + (lane >> 4) * 4, cb = wn * 32 + (lane & 15);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) tile[(rb + i * 16 + r) * STP + cb + j * 16] = acc[i][j][r];
+    }
+    block_barrier();
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int c = tid + 256 * p, row = c >> 3, col = (c & 7) * 8;
+        const int m = m0 + row, n = n0 + col;
+        if (m >= M || n >= N) continue;
+        float v[8];
+        load8(tile + row * STP + col, v);
+        if (P.bias) add8(v, P.bias + n);
+        const float *g = P.gate + (long long)(m / P.gate_L) * P.gate_ld + n;
+        float *x = P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n;
+        const float4 g0 = *(const float4 *)g, g1 = *(const float4 *)(g + 4);
+        float4 x0 = *(float4 *)x, x1 = *(float4 *)(x + 4);
+        x0.x = x0.x + v[0] * g0.x; x0.y = x0.y + v[1] * g0.y; x0.z = x0.z + v[2] * g0.z; x0.w = x0.w + v[3] * g0.w;
+        x1.x = x1.x + v[4] * g1.x; x1.y = x1.y + v[5] * g1.y; x1.z = x1.z + v[6] * g1.z; x1.w = x1.w + v[7] * g1.w;
+        *(float4 *)x = x0;
+        *(float4 *)(x + 4) = x1;
+    }
+}
+
 template <int EPI>
 __global__ __launch_bounds__(512, 1) void gemm_sk_kernel(const GemmBatch bt) {
     const int tid = threadIdx.x;
@@ -1104,6 +1275,26 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     TSN_REQUIRE(pipe || (epi != EPI_SNAKE && epi != EPI_RSNAKE),
                 "gemm snake: needs the pipelined kernel (f16 A, 16-byte aligned rows)");
     TSN_REQUIRE(pipe || !any_half, "gemm: half-width W needs the pipelined kernel (f16 A, 16-byte aligned rows)");
+    // small tiles when asked for and the 128x128 grid would fill under half the chip
+    b.small = b.small && tiles < NCU / 2 ? 1 : 0;
+    if (b.small) {
+        TSN_REQUIRE(epi == EPI_RESID && pipe && !any_half,
+                    "gemm small tiles: residual epilogue, f16 A and 16-byte aligned operands, no half-width W");
+        tiles = 0;
+        for (int i = 0; i < b.nprob; ++i) {
+            GemmProblem &p = b.p[i];
+            p.tiles_m = (p.M + SB - 1) / SB;
+            p.tiles_n = (p.N + SB - 1) / SB;
+            p.tile_start = tiles;
+            tiles += p.tiles_m * p.tiles_n;
+        }
+        b.total_tiles = tiles;
+        b.sk = 0;
+        b.pipe = 1;
+        b.hl = 0;
+        b.kname = "gemm_small_kernel<1>";
+        return TSN_OK;
+    }
     const bool snake_epi = epi == EPI_SNAKE || epi == EPI_RSNAKE;
     if (pipe && (epi == EPI_RESID || epi == EPI_STORE || snake_epi) && b.ws && (!any_lo || snake_epi)) {
         int nkmin = 1 << 30;
@@ -1227,6 +1418,12 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
 }
 
 int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
+    if (b.small) {
+        TSN_REQUIRE(epi == EPI_RESID, "gemm small tiles: residual epilogue only");
+        TSN_LAUNCH((gemm_small_kernel<EPI_RESID>), dim3(b.total_tiles), dim3(256), 0, st, b);
+        TSN_HIP_CHECK(hipGetLastError());
+        return TSN_OK;
+    }
     dim3 grid(b.sk ? b.sk_g : b.total_tiles), block(b.pipe ? 512 : 256);
     if (b.pipe) {
         if (b.sk) {

@@ -80,6 +80,10 @@ struct GemmBatch {
     // per split, plus the partial-sum traffic). For long-K GEMMs with few tiles, whose A and W tiles
     // would not be shared in L2 under stream-K's staggered K ranges.
     int split_waves = 0;
+    // nonzero (EPI_RESID, pipelined-kernel operands, no half-width W): 64x64 tiles over the full K
+    // (gemm_small_kernel), no split and no stream-K, when the 128x128 grid has fewer than 128 tiles;
+    // gemm_plan clears it otherwise (the workspace then serves the usual split-K / stream-K choice)
+    int small = 0;
 };
 
 // a_f32: A operand is f32 (converted to f16 on load). All problems share the epilogue kind.

@@ -12,7 +12,8 @@ namespace {
 
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
-constexpr int FB_M = 32, FB_N = 64, FB_K = 64, FB_LD = FB_K + 1;
+constexpr int FB_MT = 5;                 // 16-row MFMA blocks per tile: 80 rows hold a 77-token prompt
+constexpr int FB_M = 16 * FB_MT, FB_N = 64, FB_K = 64, FB_LD = FB_K + 1;
 
 // The epilogue of one output element: v = sum + bias, then Y = act(v) or Y += v.
 __device__ __forceinline__ void enc_epi(const EncGemmArgs &g, int m, int n, float v) {
@@ -26,10 +27,12 @@ __device__ __forceinline__ void enc_epi(const EncGemmArgs &g, int m, int n, floa
     }
 }
 
-// 4 waves; wave w owns columns 16w..16w+15 of a 32x64 tile (two 16x16 blocks of v_mfma_f32_16x16x4_f32
-// per 4-wide K slice). A and W reach LDS in 64-wide K stages; the next stage is loaded into registers
-// while the current one is multiplied. blockIdx.z = split: K tiles [z*kps, (z+1)*kps); with more than
-// one split the raw sums go to ws[z][M][N] and enc_gemm_reduce_kernel adds them in split order.
+// 4 waves; wave w owns columns 16w..16w+15 of an 80x64 tile (five 16x16 blocks of
+// v_mfma_f32_16x16x4_f32 per 4-wide K slice). With 80 rows a whole prompt is one row tile, so each
+// weight is read from HBM once. A and W reach LDS in 64-wide K stages; the next stage is loaded into
+// registers while the current one is multiplied. blockIdx.z = split: K tiles [z*kps, (z+1)*kps);
+// with more than one split the raw sums go to ws[z][M][N] and enc_gemm_reduce_kernel adds them in
+// split order.
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const EncGemmArgs g) {
     __shared__ float As[2][FB_M * FB_LD];
     __shared__ float Ws[2][FB_N * FB_LD];
@@ -38,15 +41,15 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const EncGemmArgs g) {
     const int M = g.M, N = g.N, K = g.K;
     const int nkt = (K + FB_K - 1) / FB_K;
     const int kt0 = z * g.kps, kt1 = min(nkt, kt0 + g.kps);
-    // loader: 16 lanes per 64-wide row (4 floats each); A rows lr + 16i (i < 2), W rows lr + 16i (i < 4)
+    // loader: 16 lanes per 64-wide row (4 floats each); A rows lr + 16i (i < 5), W rows lr + 16i (i < 4)
     const int lr = tid >> 4, lc = (tid & 15) * 4;
-    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 ra[2], rw[4];
+    float4 ra[FB_MT], rw[4];
     auto fetch = [&](int kt) {
         const int k = kt * FB_K + lc;
         const bool kin = k < K;
+        const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < FB_MT; ++i) {
             const int m = m0 + lr + 16 * i;
             ra[i] = (kin && m < M) ? *(const float4 *)(g.A + (long long)m * g.lda + k) : z4;
         }
@@ -58,7 +61,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const EncGemmArgs g) {
     };
     auto stash = [&](int b) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < FB_MT; ++i) {
             float *a = &As[b][(lr + 16 * i) * FB_LD + lc];
             a[0] = ra[i].x; a[1] = ra[i].y; a[2] = ra[i].z; a[3] = ra[i].w;
         }
@@ -68,7 +71,9 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const EncGemmArgs g) {
             w[0] = rw[i].x; w[1] = rw[i].y; w[2] = rw[i].z; w[3] = rw[i].w;
         }
     };
-    floatx4_t acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    floatx4_t acc[FB_MT];
+#pragma unroll
+    for (int i = 0; i < FB_MT; ++i) acc[i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
     const int r16 = lane & 15, kq = lane >> 4;   // operand lane: row / column r16, k offset kq
     if (kt0 < kt1) {
         fetch(kt0);
@@ -81,10 +86,10 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const EncGemmArgs g) {
 #pragma unroll
             for (int kk = 0; kk < FB_K; kk += 4) {
                 const float bv = ws[(wave * 16 + r16) * FB_LD + kk + kq];
-                const float a0 = as[r16 * FB_LD + kk + kq];
-                const float a1 = as[(16 + r16) * FB_LD + kk + kq];
-                acc[0] = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, bv, acc[0], 0, 0, 0);
-                acc[1] = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, bv, acc[1], 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < FB_MT; ++i)
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(as[(16 * i + r16) * FB_LD + kk + kq], bv, acc[i], 0,
+                                                                  0, 0);
             }
             if (kt + 1 < kt1) {
                 stash(b ^ 1);
@@ -96,7 +101,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const EncGemmArgs g) {
     const int n = n0 + wave * 16 + r16;
     if (n >= N) return;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < FB_MT; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int m = m0 + 16 * i + 4 * kq + r;
@@ -247,14 +252,22 @@ int launch_gemm_f32(const EncGemmArgs &gin, hipStream_t st) {
                 "gemm_f32: K and row strides multiples of 4, strides covering the rows");
     TSN_REQUIRE((((uintptr_t)g.A) & 15) == 0 && (((uintptr_t)g.W) & 15) == 0, "gemm_f32: 16-byte aligned A and W");
     TSN_REQUIRE(g.act == 0 || g.act == 1, "gemm_f32: activation 0 (none) or 1 (quick GELU)");
-    // split K until about 200 workgroups run, while the workspace holds the partials and every
-    // split keeps at least 4 K tiles
+    // The f32 MFMA bounds these GEMMs, so the K split balances K tiles per CU: estimated time in K
+    // tiles = rounds of 256 workgroups x K tiles per split, plus the partial sums written and read
+    // (about 8 MB per K-tile time) and a reduce launch. Splits are powers of two with at least 2 K
+    // tiles each, and the workspace must hold the partials.
     const int tiles = ((g.N + FB_N - 1) / FB_N) * ((g.M + FB_M - 1) / FB_M);
     const int nkt = (g.K + FB_K - 1) / FB_K;
     int splits = 1;
-    while (g.ws && tiles * splits < 200 && nkt / (splits * 2) >= 4 &&
-           (size_t)(splits * 2) * g.M * g.N * sizeof(float) <= g.ws_bytes)
-        splits *= 2;
+    double best = (double)((tiles + 255) / 256) * nkt;
+    for (int s = 2; g.ws && nkt / s >= 2 && (size_t)s * g.M * g.N * sizeof(float) <= g.ws_bytes; s *= 2) {
+        const double cost = (double)((tiles * s + 255) / 256) * ((nkt + s - 1) / s) + 1.0 +
+                            2.0 * s * g.M * (double)g.N * sizeof(float) / 8e6;
+        if (cost < best) {
+            best = cost;
+            splits = s;
+        }
+    }
     g.kps = (nkt + splits - 1) / splits;
     g.splits = (nkt + g.kps - 1) / g.kps;
     TSN_LAUNCH(gemm_f32_kernel, dim3((g.N + FB_N - 1) / FB_N, (g.M + FB_M - 1) / FB_M, g.splits), dim3(256), 0, st, g);

@@ -16,7 +16,7 @@
 
 namespace tsn {
 
-constexpr size_t ENC_WS_BYTES = (size_t)16 << 20;   // split-K partials of the f32 GEMMs
+constexpr size_t ENC_WS_BYTES = (size_t)32 << 20;   // split-K partials of the f32 GEMMs
 
 struct ClipSpec {   // field meaning documented in include/tsn.h (tsn_clip_spec)
     int H, NL, NH, ctx, vocab;

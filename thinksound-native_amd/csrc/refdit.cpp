@@ -426,6 +426,7 @@ int RefDitModel::block_joint(int i, bool ln1, Next next) {
     ob.nprob = np;
     ob.ws = ws_;
     ob.ws_bytes = ws_bytes_;
+    ob.split_waves = 1;
     for (int k = 0; k < np; ++k) {
         const RowMap m = stream_map(kinds[k]);
         const bool lat = kinds[k] == ST_LAT;
@@ -455,6 +456,7 @@ int RefDitModel::block_joint(int i, bool ln1, Next next) {
     f2.nprob = np;
     f2.ws = ws_;
     f2.ws_bytes = ws_bytes_;
+    f2.split_waves = 1;   // long K over few tiles: a classic split keeps each W tile's readers together
     for (int k = 0; k < np; ++k) {
         const RowMap m = stream_map(kinds[k]);
         const bool lat = kinds[k] == ST_LAT;
@@ -503,6 +505,7 @@ int RefDitModel::block_fused(int i, bool ln1, Next next) {
     ob.nprob = 1;
     ob.ws = ws_;
     ob.ws_bytes = ws_bytes_;
+    ob.split_waves = 1;
     resid_problem(ob.p[0], AO_, 2 * H, Lm, w.taps, 2 * H, M, H, w.Wo, w.bo, X_, H, MODL_ + w.mod_off + 2 * H, NMODL);
     ob.p[0].gate_L = 1;
     half_w(ob.p[0]);
@@ -523,6 +526,7 @@ int RefDitModel::block_fused(int i, bool ln1, Next next) {
     f2.nprob = 1;
     f2.ws = ws_;
     f2.ws_bytes = ws_bytes_;
+    f2.split_waves = 1;   // long K over few tiles: a classic split keeps each W tile's readers together
     resid_problem(f2.p[0], HF_, 2 * s.F, Lm, w.taps, 2 * s.F, M, H, w.W2, nullptr, X_, H, MODL_ + w.mod_off + 5 * H,
                   NMODL);
     f2.p[0].gate_L = 1;

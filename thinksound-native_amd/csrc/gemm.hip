@@ -1053,52 +1053,19 @@ __global__ __launch_bounds__(512) void gemm_fixup_kernel(const GemmBatch bt) {
 // split-K reduction + epilogue, one thread per 4 columns; partials summed in split order
 // (deterministic). EPI_RESID: R[rmap(m)][n] += gate[m/gate_L][n] * (sum + bias[n]);
 // EPI_STORE: Y[ymap(m)][n] = act(sum + bias[n]) as f16 or f32.
-// threads of the split-K reduce for one split problem: one per 4 output columns (SwiGLU: N/2 columns)
-__host__ __device__ inline long long splitk_reduce_threads(const GemmProblem &p, int epi) {
-    return (long long)p.M * (epi == EPI_SWIGLU ? p.N / 2 : p.N) / 4;
-}
-
 template <int EPI>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmBatch bt) {
     long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    // problems with a split come one after the other, one thread per 4 output columns each
+    // problems with a split come one after the other, M*N/4 threads each
     int pi = -1;
     for (int q = 0; q < bt.nprob; ++q) {
         if (bt.p[q].splits <= 1) continue;
-        const long long nq = splitk_reduce_threads(bt.p[q], EPI);
+        const long long nq = (long long)bt.p[q].M * bt.p[q].N / 4;
         if (idx < nq) { pi = q; break; }
         idx -= nq;
     }
     if (pi < 0) return;
     const GemmProblem &P = bt.p[pi];
-    if constexpr (EPI == EPI_SWIGLU) {
-        // output columns c..c+3 of F = N/2: w1 rows 128j + e and w3 rows 128j + 64 + e (j = c / 64,
-        // e = c % 64) of the interleaved W; y = silu(a) * b as f16 (+ lo at y_lo)
-        const int f4 = P.N / 8;
-        const int m = (int)(idx / f4), c = (int)(idx - (long long)m * f4) * 4;
-        const int na = (c >> 6) * 128 + (c & 63);
-        float4 a = *(const float4 *)(P.ws + (long long)m * P.N + na);
-        float4 b = *(const float4 *)(P.ws + (long long)m * P.N + na + 64);
-        for (int k = 1; k < P.splits; ++k) {
-            const float *w = P.ws + ((long long)k * P.M + m) * P.N + na;
-            const float4 u = *(const float4 *)w, t = *(const float4 *)(w + 64);
-            a.x += u.x; a.y += u.y; a.z += u.z; a.w += u.w;
-            b.x += t.x; b.y += t.y; b.z += t.z; b.w += t.w;
-        }
-        const float y[4] = {silu_f(a.x) * b.x, silu_f(a.y) * b.y, silu_f(a.z) * b.z, silu_f(a.w) * b.w};
-        half4 hi;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) hi[j] = (half_t)y[j];
-        half_t *o = (half_t *)P.Y + rowmap_phys(P.ymap, m) * (long long)P.ldy + c;
-        *(half4 *)o = hi;
-        if (P.y_lo) {
-            half4 lo;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) lo[j] = (half_t)(y[j] - (float)hi[j]);
-            *(half4 *)(o + P.y_lo) = lo;
-        }
-        return;
-    }
     const int n4 = P.N / 4;
     const int m = (int)(idx / n4), n = (int)(idx - (long long)m * n4) * 4;
     float4 v = *(const float4 *)(P.ws + (long long)m * P.N + n);
@@ -1180,12 +1147,11 @@ int launch_gemm_reduce(const GemmBatch &b, int epi, hipStream_t st) {
     }
     long long red = 0;
     for (int i = 0; i < b.nprob; ++i)
-        if (b.p[i].splits > 1) red += splitk_reduce_threads(b.p[i], epi);
+        if (b.p[i].splits > 1) red += (long long)b.p[i].M * b.p[i].N / 4;
     if (red == 0) return TSN_OK;
     const dim3 grid((unsigned)((red + 255) / 256)), block(256);
     if (epi == EPI_RESID) TSN_LAUNCH(splitk_reduce_kernel<EPI_RESID>, grid, block, 0, st, b);
     else if (epi == EPI_STORE) TSN_LAUNCH(splitk_reduce_kernel<EPI_STORE>, grid, block, 0, st, b);
-    else if (epi == EPI_SWIGLU) TSN_LAUNCH(splitk_reduce_kernel<EPI_SWIGLU>, grid, block, 0, st, b);
     else if (epi == EPI_RSNAKE) TSN_LAUNCH(splitk_reduce_kernel<EPI_RSNAKE>, grid, block, 0, st, b);
     else if (epi == EPI_SNAKE) TSN_LAUNCH(splitk_reduce_kernel<EPI_SNAKE>, grid, block, 0, st, b);
     else { set_error("gemm reduce: epilogue without split-K support"); return TSN_ERR_ARG; }
@@ -1206,8 +1172,7 @@ const char *gemm_reduce_name(const GemmBatch &b, int epi) {
                : epi == EPI_QKV ? "gemm_fixup_kernel<2>" : epi == EPI_SNAKE ? "gemm_fixup_kernel<4>"
                : epi == EPI_RSNAKE ? "gemm_fixup_kernel<5>" : "gemm_fixup_kernel<3>";
     return epi == EPI_RESID ? "splitk_reduce_kernel<1>" : epi == EPI_RSNAKE ? "splitk_reduce_kernel<5>"
-           : epi == EPI_SNAKE ? "splitk_reduce_kernel<4>" : epi == EPI_SWIGLU ? "splitk_reduce_kernel<3>"
-           : "splitk_reduce_kernel<0>";
+           : epi == EPI_SNAKE ? "splitk_reduce_kernel<4>" : "splitk_reduce_kernel<0>";
 }
 
 void gemm_problem_init(GemmProblem &p) {
@@ -1331,10 +1296,7 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         return TSN_OK;
     }
     const bool snake_epi = epi == EPI_SNAKE || epi == EPI_RSNAKE;
-    // SwiGLU splits only by estimated time (split_waves); its reduce writes the hi|lo output too
-    const bool swiglu_split = epi == EPI_SWIGLU && b.split_waves;
-    if (pipe && (epi == EPI_RESID || epi == EPI_STORE || snake_epi || swiglu_split) && b.ws &&
-        (!any_lo || snake_epi || swiglu_split)) {
+    if (pipe && (epi == EPI_RESID || epi == EPI_STORE || snake_epi) && b.ws && (!any_lo || snake_epi)) {
         int nkmin = 1 << 30;
         for (int i = 0; i < b.nprob; ++i) nkmin = std::min(nkmin, b.p[i].K / BK);
         int best = 0;
@@ -1387,7 +1349,7 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
                     GemmProblem &p = b.p[i];
                     p.splits = p.K / BK / best;
                     if (p.splits > 1) {
-                        TSN_REQUIRE(p.N % 4 == 0 && ((epi == EPI_STORE || epi == EPI_SNAKE || epi == EPI_SWIGLU)
+                        TSN_REQUIRE(p.N % 4 == 0 && ((epi == EPI_STORE || epi == EPI_SNAKE)
                                                          ? p.ldy % 4 == 0
                                                          : p.ldr % 4 == 0 && p.gate_ld % 4 == 0),
                                     "gemm split-K: N and output strides must be multiples of 4");

@@ -534,6 +534,15 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
 #pragma unroll
                 for (int e = 0; e < 8; ++e) bw[e] = 0.0f;
             load8(nw + d0, nwv);
+            // the RoPE rows of all four passes, loaded before any store: a store to Q/K may alias
+            // the table, so a load left inside the loop would wait for the previous pass's store
+            float cs4[4][8];
+#pragma unroll
+            for (int p = 0; p < 4; ++p) {
+                const int m = m0 + (tid >> 4) + 32 * p;
+                const int t = m < M ? m % P.q_L : P.rope_len;
+                if (t < P.rope_len) load8(P.rope + (t * 32 + (d0 >> 1)) * 2, cs4[p]);
+            }
 #pragma unroll
             for (int p = 0; p < 4; ++p) {
                 const int row = (tid >> 4) + 32 * p, m = m0 + row;
@@ -554,9 +563,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
                 if (m >= M) continue;
                 const int b = m / P.q_L, t = m - b * P.q_L, s = P.q_soff + t;
                 if (t < P.rope_len) {
-                    const float *cs = P.rope + (t * 32 + (d0 >> 1)) * 2;
-                    float cv[8];
-                    load8(cs, cv);
+                    const float *cv = cs4[p];
 #pragma unroll
                     for (int e = 0; e < 8; e += 2) {
                         const float x0 = v[e], x1 = v[e + 1];

@@ -41,10 +41,12 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const EncGemmArgs g) {
     const int M = g.M, N = g.N, K = g.K;
     const int nkt = (K + FB_K - 1) / FB_K;
     const int kt0 = z * g.kps, kt1 = min(nkt, kt0 + g.kps);
-    // loader: 16 lanes per 64-wide row (4 floats each); A rows lr + 16i (i < 5), W rows lr + 16i (i < 4)
+    // loader: 16 lanes per 64-wide row (4 floats each); A rows lr + 16i (i < 5), W rows lr + 16i (i < 4).
+    // Two register sets: K tile kt + 2 is fetched while kt is multiplied and kt + 1 waits in the
+    // other set, so a tile has two K steps of MFMA work to arrive from HBM.
     const int lr = tid >> 4, lc = (tid & 15) * 4;
-    float4 ra[FB_MT], rw[4];
-    auto fetch = [&](int kt) {
+    float4 ra0[FB_MT], rw0[4], ra1[FB_MT], rw1[4];
+    auto fetch = [&](int kt, float4 (&ra)[FB_MT], float4 (&rw)[4]) {
         const int k = kt * FB_K + lc;
         const bool kin = k < K;
         const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -59,7 +61,7 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const EncGemmArgs g) {
             rw[i] = (kin && n < N) ? *(const float4 *)(g.W + (long long)n * g.ldw + k) : z4;
         }
     };
-    auto stash = [&](int b) {
+    auto stash = [&](int b, const float4 (&ra)[FB_MT], const float4 (&rw)[4]) {
 #pragma unroll
         for (int i = 0; i < FB_MT; ++i) {
             float *a = &As[b][(lr + 16 * i) * FB_LD + lc];
@@ -75,26 +77,35 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const EncGemmArgs g) {
 #pragma unroll
     for (int i = 0; i < FB_MT; ++i) acc[i] = floatx4_t{0.f, 0.f, 0.f, 0.f};
     const int r16 = lane & 15, kq = lane >> 4;   // operand lane: row / column r16, k offset kq
+    auto compute = [&](int b) {
+        const float *as = As[b], *ws = Ws[b];
+#pragma unroll
+        for (int kk = 0; kk < FB_K; kk += 4) {
+            const float bv = ws[(wave * 16 + r16) * FB_LD + kk + kq];
+#pragma unroll
+            for (int i = 0; i < FB_MT; ++i)
+                acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(as[(16 * i + r16) * FB_LD + kk + kq], bv, acc[i], 0, 0, 0);
+        }
+    };
+    // K tile kt0 + r lives in LDS buffer r & 1 and, before that, in register set r & 1
     if (kt0 < kt1) {
-        fetch(kt0);
-        stash(0);
+        fetch(kt0, ra0, rw0);
+        stash(0, ra0, rw0);
+        if (kt0 + 1 < kt1) fetch(kt0 + 1, ra1, rw1);
         __syncthreads();
-        for (int kt = kt0; kt < kt1; ++kt) {
-            const int b = (kt - kt0) & 1;
-            if (kt + 1 < kt1) fetch(kt + 1);
-            const float *as = As[b], *ws = Ws[b];
-#pragma unroll
-            for (int kk = 0; kk < FB_K; kk += 4) {
-                const float bv = ws[(wave * 16 + r16) * FB_LD + kk + kq];
-#pragma unroll
-                for (int i = 0; i < FB_MT; ++i)
-                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(as[(16 * i + r16) * FB_LD + kk + kq], bv, acc[i], 0,
-                                                                  0, 0);
-            }
-            if (kt + 1 < kt1) {
-                stash(b ^ 1);
-                __syncthreads();
-            }
+        for (int kt = kt0; kt < kt1; kt += 2) {
+            // even step: tile kt in buffer 0; set 0 is free, set 1 holds kt + 1
+            if (kt + 2 < kt1) fetch(kt + 2, ra0, rw0);
+            compute(0);
+            if (kt + 1 >= kt1) break;
+            stash(1, ra1, rw1);
+            __syncthreads();
+            // odd step: tile kt + 1 in buffer 1; set 1 is free, set 0 holds kt + 2
+            if (kt + 3 < kt1) fetch(kt + 3, ra1, rw1);
+            compute(1);
+            if (kt + 2 >= kt1) break;
+            stash(0, ra0, rw0);
+            __syncthreads();
         }
     }
     // lane holds rows 16i + 4*(lane/16) + r, column lane%16 of the wave's 16 columns

@@ -171,43 +171,62 @@ __global__ __launch_bounds__(256) void enc_norm_kernel(const float *__restrict__
 constexpr int EA_Q = 16;      // queries per workgroup
 constexpr int EA_SMAX = 128;  // longest context
 constexpr int EA_HD = 64;
+constexpr int EA_KP = EA_HD + 4;   // K row pitch (floats): 16-byte rows, 16 consecutive keys in distinct banks
+constexpr int EA_PP = EA_SMAX + 1;
 
-// one workgroup per (16 queries, head): scores, mask / bias, softmax and P·V in f32
+// one workgroup per (16 queries, head): scores, mask / bias, softmax and P·V in f32. Thread t
+// serves query t / 16: its scores are keys t % 16 + 16j (query row in registers, K rows read as
+// float4), its outputs columns 4 (t % 16) .. + 3 (V rows read as float4).
 __global__ __launch_bounds__(256) void enc_attn_kernel(const EncAttnArgs a) {
-    __shared__ float Ks[EA_SMAX * (EA_HD + 1)];
-    __shared__ float Vs[EA_SMAX * EA_HD];
-    __shared__ float Qs[EA_Q * EA_HD];
-    __shared__ float P[EA_Q * (EA_SMAX + 1)];
+    __shared__ __attribute__((aligned(16))) float Ks[EA_SMAX * EA_KP];
+    __shared__ __attribute__((aligned(16))) float Vs[EA_SMAX * EA_HD];
+    __shared__ __attribute__((aligned(16))) float Qs[EA_Q * EA_HD];
+    __shared__ float P[EA_Q * EA_PP];
     const int tid = threadIdx.x, h = blockIdx.y, q0 = blockIdx.x * EA_Q, S = a.S;
-    for (int e = tid; e < S * EA_HD; e += 256) {
-        const int k = e >> 6, d = e & 63;
+    for (int e = tid; e < S * (EA_HD / 4); e += 256) {
+        const int k = e >> 4, d = (e & 15) * 4;
         const float *row = a.qkv + (long long)k * a.ld + h * EA_HD + d;
-        Ks[k * (EA_HD + 1) + d] = row[a.k_off];
-        Vs[k * EA_HD + d] = row[a.v_off];
+        *(float4 *)&Ks[k * EA_KP + d] = *(const float4 *)(row + a.k_off);
+        *(float4 *)&Vs[k * EA_HD + d] = *(const float4 *)(row + a.v_off);
     }
-    for (int e = tid; e < EA_Q * EA_HD; e += 256) {
-        const int q = e >> 6, d = e & 63;
-        Qs[e] = q0 + q < S ? a.qkv[(long long)(q0 + q) * a.ld + a.q_off + h * EA_HD + d] : 0.0f;
+    {
+        const int q = tid >> 4, d = (tid & 15) * 4;
+        *(float4 *)&Qs[q * EA_HD + d] = q0 + q < S
+            ? *(const float4 *)(a.qkv + (long long)(q0 + q) * a.ld + a.q_off + h * EA_HD + d)
+            : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     __syncthreads();
-    for (int e = tid; e < EA_Q * S; e += 256) {
-        const int q = e / S, k = e - q * S, qg = q0 + q;
-        float s = 0.0f;
-        for (int d = 0; d < EA_HD; ++d) s += Qs[q * EA_HD + d] * Ks[k * (EA_HD + 1) + d];
-        s *= a.scale;
-        if (a.mode == 1) {   // T5: padded keys masked, else the head's bias for the bucket of (q, k)
-            if (a.pad && a.pad[k] == 0) s = -INFINITY;
-            else if (qg < S) s += a.rel[a.bucket[qg * S + k] * a.nh + h];
-        } else if (a.mode == 2) {   // CLIP: causal, and nothing past the end-of-text token
-            if (!(k <= qg && k <= a.eot)) s = -INFINITY;
+    const int q = tid >> 4, t16 = tid & 15, qg = q0 + q;
+    {
+        float4 qv[EA_HD / 4];
+#pragma unroll
+        for (int i = 0; i < EA_HD / 4; ++i) qv[i] = *(const float4 *)&Qs[q * EA_HD + 4 * i];
+        for (int k = t16; k < S; k += 16) {
+            const float *kr = &Ks[k * EA_KP];
+            float s = 0.0f;
+#pragma unroll
+            for (int i = 0; i < EA_HD / 4; ++i) {
+                const float4 kv = *(const float4 *)(kr + 4 * i);
+                s += qv[i].x * kv.x;
+                s += qv[i].y * kv.y;
+                s += qv[i].z * kv.z;
+                s += qv[i].w * kv.w;
+            }
+            s *= a.scale;
+            if (a.mode == 1) {   // T5: padded keys masked, else the head's bias for the bucket of (q, k)
+                if (a.pad && a.pad[k] == 0) s = -INFINITY;
+                else if (qg < S) s += a.rel[a.bucket[qg * S + k] * a.nh + h];
+            } else if (a.mode == 2) {   // CLIP: causal, and nothing past the end-of-text token
+                if (!(k <= qg && k <= a.eot)) s = -INFINITY;
+            }
+            P[q * EA_PP + k] = s;
         }
-        P[q * (EA_SMAX + 1) + k] = s;
     }
     __syncthreads();
     {   // softmax: wave w takes rows w, w+4, w+8, w+12
         const int lane = tid & 63, wave = tid >> 6;
-        for (int q = wave; q < EA_Q; q += 4) {
-            float *pr = P + q * (EA_SMAX + 1);
+        for (int r = wave; r < EA_Q; r += 4) {
+            float *pr = P + r * EA_PP;
             float mx = -INFINITY;
             for (int k = lane; k < S; k += 64) mx = fmaxf(mx, pr[k]);
             for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
@@ -223,13 +242,18 @@ __global__ __launch_bounds__(256) void enc_attn_kernel(const EncAttnArgs a) {
         }
     }
     __syncthreads();
-    for (int e = tid; e < EA_Q * EA_HD; e += 256) {
-        const int q = e >> 6, d = e & 63;
-        if (q0 + q >= S) continue;
-        float o = 0.0f;
-        for (int k = 0; k < S; ++k) o += P[q * (EA_SMAX + 1) + k] * Vs[k * EA_HD + d];
-        a.out[(long long)(q0 + q) * a.ldo + h * EA_HD + d] = o;
+    if (qg >= S) return;
+    const int d = t16 * 4;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < S; ++k) {
+        const float pk = P[q * EA_PP + k];
+        const float4 v = *(const float4 *)&Vs[k * EA_HD + d];
+        o.x += pk * v.x;
+        o.y += pk * v.y;
+        o.z += pk * v.z;
+        o.w += pk * v.w;
     }
+    *(float4 *)(a.out + (long long)qg * a.ldo + h * EA_HD + d) = o;
 }
 
 // y[r][c] = gelu_tanh(u[r][c]) * u[r][F + c] (tanh form, argument clamped to +-10: shaders/ops_conv.metal:15-24)
@@ -304,6 +328,9 @@ int launch_enc_attention(const EncAttnArgs &a, hipStream_t st) {
     TSN_REQUIRE(a.qkv && a.out && a.S > 0 && a.S <= EA_SMAX && a.nh > 0 && a.hd == EA_HD,
                 "enc_attention: context 1..128, head width 64");
     TSN_REQUIRE(a.mode == 0 || a.mode == 2 || (a.mode == 1 && a.rel && a.bucket), "enc_attention: mode and tables");
+    TSN_REQUIRE((((uintptr_t)a.qkv | (uintptr_t)a.out) & 15) == 0 && a.ld % 4 == 0 && a.ldo % 4 == 0 &&
+                    a.q_off % 4 == 0 && a.k_off % 4 == 0 && a.v_off % 4 == 0,
+                "enc_attention: 16-byte aligned rows (qkv, out, strides and offsets multiples of 4 floats)");
     TSN_LAUNCH(enc_attn_kernel, dim3((a.S + EA_Q - 1) / EA_Q, a.nh), dim3(256), 0, st, a);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;

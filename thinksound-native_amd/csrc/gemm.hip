@@ -853,9 +853,10 @@ __global__ __launch_bounds__(512, 1) void gemm_pipe_hl_kernel(const GemmBatch bt
     pipe_dp<EPI, true>(bt);
 }
 
-// gemm_small_kernel: 64x64 C tiles over the full K, 4 waves of 32x32 (2 x 2 MFMA blocks of 16x16),
-// the same swizzled direct-to-LDS ring as pipe_tile (5 stages of 16 KB, two workgroups per CU) and
-// the residual epilogue in place. For GEMMs whose 128x128 grid would need a K split to fill the
+// gemm_small_kernel: plain GEMMs (one tap), 64x64 C tiles over the full K, 4 waves of 32x32
+// (2 x 2 MFMA blocks of 16x16), the same swizzled direct-to-LDS ring as pipe_tile (5 stages of
+// 16 KB, two workgroups per CU) and the residual epilogue in place. For GEMMs whose 128x128 grid
+// would need a K split to fill the
 // chip (M ~ 800, N = 1024, K = 1024): 64x64 tiles give four times the workgroups with no f32
 // partials to write and sum.
 constexpr int SB = 64;              // tile rows and columns
@@ -873,7 +874,7 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
     int tm, tn;
     tile_mn(wg - P.tile_start, P.tiles_m, P.tiles_n, tm, tn);
     const int m0 = tm * SB, n0 = tn * SB;
-    const int M = P.M, N = P.N, lda = P.lda, Kc = P.Kc, pad = P.pad, aT = P.a_T, ldw = P.ldw;
+    const int M = P.M, N = P.N, lda = P.lda, pad = P.pad, aT = P.a_T, ldw = P.ldw;
     const RowMap am = P.amap;
     const i32x4 rsa = make_rsrc(P.A);
     const i32x4 rsb = make_rsrc(P.W);
@@ -893,28 +894,21 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
         const int n = n0 + r;
         b_off[i] = n < N ? (n * ldw + lc * 8) * 2 : -1;
     }
-    const int lda2 = lda * 2;
-    int nt_trow = 0, nt_kin = 0, nt_kw = 0;   // tap, offset inside it, W column of the next K tile
+    int nt_k = 0;   // K column of the next K tile (plain GEMM: one tap, so A and W share it)
     auto issue = [&](int stage) {
-        const int trow = nt_trow, kin = nt_kin, kw = nt_kw;
-        nt_kw += BK;
-        nt_kin += BK;
-        if (nt_kin == Kc) {
-            nt_kin = 0;
-            ++nt_trow;
-        }
-        const int kc2 = kin * 2 + trow * lda2;
+        const int k = nt_k;
+        nt_k += BK;
         lds_char *sa = (lds_char *)(smem + stage * SSTAGE) + wave * 2048;
         lds_char *sb = (lds_char *)(smem + (NS + stage) * SSTAGE) + wave * 2048;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const int ts = a_ts0[i] + trow;
-            const unsigned vo = (ts >= 0 && ts < aT) ? (unsigned)(a_base[i] + kc2) : 0x80000000u;
+            const int ts = a_ts0[i];
+            const unsigned vo = (ts >= 0 && ts < aT) ? (unsigned)(a_base[i] + k * 2) : 0x80000000u;
             dma16(rsa, vo, sa + i * 1024);
         }
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
-            const unsigned vo = b_off[i] >= 0 ? (unsigned)(b_off[i] + kw * 2) : 0x80000000u;
+            const unsigned vo = b_off[i] >= 0 ? (unsigned)(b_off[i] + k * 2) : 0x80000000u;
             dma16(rsb, vo, sb + i * 1024);
         }
     };
@@ -1307,8 +1301,11 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     TSN_REQUIRE(pipe || (epi != EPI_SNAKE && epi != EPI_RSNAKE),
                 "gemm snake: needs the pipelined kernel (f16 A, 16-byte aligned rows)");
     TSN_REQUIRE(pipe || !any_half, "gemm: half-width W needs the pipelined kernel (f16 A, 16-byte aligned rows)");
-    // small tiles when asked for and the 128x128 grid would fill under half the chip
-    b.small = b.small && tiles < NCU / 2 ? 1 : 0;
+    // small tiles when asked for, for plain GEMMs (one tap), when the 128x128 grid would fill under
+    // half the chip
+    bool one_tap = true;
+    for (int i = 0; i < b.nprob; ++i) one_tap = one_tap && b.p[i].taps == 1;
+    b.small = b.small && one_tap && tiles < NCU / 2 ? 1 : 0;
     if (b.small) {
         TSN_REQUIRE(epi == EPI_RESID && pipe && !any_half,
                     "gemm small tiles: residual epilogue, f16 A and 16-byte aligned operands, no half-width W");

@@ -856,9 +856,8 @@ __global__ __launch_bounds__(512, 1) void gemm_pipe_hl_kernel(const GemmBatch bt
 // gemm_small_kernel: plain GEMMs (one tap), 64x64 C tiles over the full K, 4 waves of 32x32
 // (2 x 2 MFMA blocks of 16x16), the same swizzled direct-to-LDS ring as pipe_tile (5 stages of
 // 16 KB, two workgroups per CU) and the residual epilogue in place. For GEMMs whose 128x128 grid
-// would need a K split to fill the
-// chip (M ~ 800, N = 1024, K = 1024): 64x64 tiles give four times the workgroups with no f32
-// partials to write and sum.
+// would need a K split to fill the chip (M ~ 800, N = 1024, K = 1024): 64x64 tiles give four times
+// the workgroups with no f32 partials to write and sum.
 constexpr int SB = 64;              // tile rows and columns
 constexpr int SSTAGE = SB * BK;     // halves per operand tile of one stage (8 KB)
 constexpr int STP = 68;             // pitch (floats) of the staged f32 C tile: 4 rows = 16 banks apart

@@ -27,8 +27,9 @@ namespace {
 
 constexpr int BM = 128, BN = 128, BK = 64, LDSW = BK + 8;
 // stream-K: workgroups of one grid (one per CU of an MI355X), the fewest K tiles one takes, and
-// the per-workgroup cost of pipeline fill, partial store and fixup in K-tile units
-constexpr int NCU = 256, SK_MIN_UNITS = 8, SK_OVERHEAD = 6;
+// the per-workgroup cost of pipeline fill, partial store and the fixup launch in K-tile units
+// (the fixup kernel alone takes 8-10 us, about 20 K tiles)
+constexpr int NCU = 256, SK_MIN_UNITS = 8, SK_OVERHEAD = 20;
 
 __device__ inline int xcd_remap(int bid, int nwg) {
     const int xcd = bid & 7, idx = bid >> 3;

@@ -16,6 +16,7 @@
 // workgroup ID) receives one contiguous range of tiles, and tiles are numbered n-major, so the
 // workgroups of one XCD share W column blocks in that XCD's L2.
 #include "kernels.h"
+#include "snake.h"
 
 #include <string.h>
 
@@ -370,8 +371,7 @@ __device__ __forceinline__ void snake8(float (&v)[8], const float *ea, const flo
     const float b[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-        const float sn = sinf(v[e] * a[e]);
-        v[e] = v[e] + sn * sn * b[e];
+        v[e] = v[e] + snake_sin2(v[e] * a[e]) * b[e];
     }
 }
 
@@ -1108,8 +1108,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmBatch bt) 
         half4 hi, lo;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float sn = sinf(e[j] * P.snake[n + j]);
-            e[j] = e[j] + sn * sn * P.snake[P.N + n + j];
+            e[j] = e[j] + snake_sin2(e[j] * P.snake[n + j]) * P.snake[P.N + n + j];
             hi[j] = (half_t)e[j];
             lo[j] = (half_t)(e[j] - (float)hi[j]);
         }
@@ -1128,8 +1127,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const GemmBatch bt) 
         half4 hi, lo;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            const float sn = sinf(e[j] * P.snake[n + j]);
-            e[j] = e[j] + sn * sn * P.snake[P.N + n + j];
+            e[j] = e[j] + snake_sin2(e[j] * P.snake[n + j]) * P.snake[P.N + n + j];
             hi[j] = (half_t)e[j];
             lo[j] = (half_t)(e[j] - (float)hi[j]);
         }

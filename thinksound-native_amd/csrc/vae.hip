@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include "kernels.h"
+#include "snake.h"
 
 namespace tsn {
 
@@ -25,8 +26,7 @@ __global__ void split3_kernel(const float *__restrict__ x, long long rows, int C
     if (ab) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            const float sn = sinf(v[e] * ab[c + e]);
-            v[e] = v[e] + sn * sn * ab[C + c + e];
+            v[e] = v[e] + snake_sin2(v[e] * ab[c + e]) * ab[C + c + e];
         }
     }
     half8 hi, lo;
@@ -81,8 +81,7 @@ __global__ void __launch_bounds__(256) conv_out_kernel(const float *__restrict__
             if (rr < CO_ROWS) {
                 float u = 0.0f;   // snake(0) = 0: padding rows and channels past the chunk stay zero
                 if (i < cw) {
-                    const float sn = sinf(v[j] * ab[c0 + i]);
-                    u = v[j] + sn * sn * ab[C + c0 + i];
+                    u = v[j] + snake_sin2(v[j] * ab[c0 + i]) * ab[C + c0 + i];
                 }
                 xs[e] = u;
             }

@@ -286,7 +286,7 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
 
     GemmBatch ob;
     ob.nprob = 2;
-    ob.small = 1;   // 64x64 tiles over the full K when the 128x128 grid is small: no split-K partials
+    ob.small = 1;   // 64x64 tiles over the full K while 128x128 tiles would fill under half the chip
     ob.ws = ws_;
     ob.ws_bytes = ws_bytes_;
     resid_problem(ob.p[0], AO_, H, Sa, 1, H, B * La, H, a.Wo, a.bo, X_, H, mod_ + a.mod_off + 2 * H, NMOD);
@@ -343,7 +343,7 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
 
     GemmBatch ob;
     ob.nprob = 1;
-    ob.small = 1;   // 64x64 tiles over the full K when the 128x128 grid is small: no split-K partials
+    ob.small = 1;   // 64x64 tiles over the full K while 128x128 tiles would fill under half the chip
     ob.ws = ws_;
     ob.ws_bytes = ws_bytes_;
     resid_problem(ob.p[0], AO_, H, D, 1, H, M, H, w.Wo, w.bo, X_, H, mod_ + w.mod_off + 2 * H, NMOD);

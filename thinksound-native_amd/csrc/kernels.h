@@ -82,8 +82,8 @@ struct GemmBatch {
     int split_waves = 0;
     // nonzero (EPI_RESID, pipelined-kernel operands, no half-width W): 64x64 tiles over the full K
     // (gemm_small_kernel), no split and no stream-K, for one-tap problems when the 128x128 grid has
-    // fewer than 128 tiles;
-    // gemm_plan clears it otherwise (the workspace then serves the usual split-K / stream-K choice)
+    // fewer than 128 tiles. gemm_plan clears it otherwise, and the workspace then serves the usual
+    // split-K / stream-K choice.
     int small = 0;
 };
 

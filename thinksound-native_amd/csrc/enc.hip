@@ -148,24 +148,48 @@ __global__ __launch_bounds__(256) void enc_norm_kernel(const float *__restrict__
         __syncthreads();
         return ((part[0] + part[1]) + part[2]) + part[3];
     };
+    // the row in registers: columns 4*tid + 1024*j .. + 3 (H % 4 == 0, H <= 2048)
+    float4 v[2];
     float s = 0.0f;
-    for (int c = tid; c < H; c += 256) s += LN ? xr[c] : xr[c] * xr[c];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int c = 4 * tid + 1024 * j;
+        v[j] = c < H ? *(const float4 *)(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        s += LN ? (v[j].x + v[j].y) + (v[j].z + v[j].w)
+                : (v[j].x * v[j].x + v[j].y * v[j].y) + (v[j].z * v[j].z + v[j].w * v[j].w);
+    }
     s = block_sum(s);
     float mean = 0.0f, inv;
     if (LN) {
         mean = s / (float)H;
-        float v = 0.0f;
-        for (int c = tid; c < H; c += 256) {
-            const float d = xr[c] - mean;
-            v += d * d;
-        }
-        v = block_sum(v);
-        inv = 1.0f / sqrtf(v / (float)H + eps);
+        float q = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+            if (4 * tid + 1024 * j < H) {
+                const float d0 = v[j].x - mean, d1 = v[j].y - mean, d2 = v[j].z - mean, d3 = v[j].w - mean;
+                q += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+            }
+        q = block_sum(q);
+        inv = 1.0f / sqrtf(q / (float)H + eps);
     } else {
         inv = 1.0f / sqrtf(s / (float)H + eps);
     }
     float *yr = y + (long long)row * H;
-    for (int c = tid; c < H; c += 256) yr[c] = LN ? (xr[c] - mean) * inv * w[c] + b[c] : xr[c] * inv * w[c];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int c = 4 * tid + 1024 * j;
+        if (c >= H) continue;
+        const float4 wv = *(const float4 *)(w + c);
+        float4 o;
+        if (LN) {
+            const float4 bv = *(const float4 *)(b + c);
+            o = make_float4((v[j].x - mean) * inv * wv.x + bv.x, (v[j].y - mean) * inv * wv.y + bv.y,
+                            (v[j].z - mean) * inv * wv.z + bv.z, (v[j].w - mean) * inv * wv.w + bv.w);
+        } else {
+            o = make_float4(v[j].x * inv * wv.x, v[j].y * inv * wv.y, v[j].z * inv * wv.z, v[j].w * inv * wv.w);
+        }
+        *(float4 *)(yr + c) = o;
+    }
 }
 
 constexpr int EA_Q = 16;      // queries per workgroup
@@ -318,6 +342,8 @@ int launch_gemm_f32(const EncGemmArgs &gin, hipStream_t st) {
 int launch_enc_norm(const float *x, float *y, const float *w, const float *b, int rows, int H, float eps, bool ln,
                     hipStream_t st) {
     TSN_REQUIRE(x && y && w && rows > 0 && H > 0 && (!ln || b), "enc_norm: arguments");
+    TSN_REQUIRE(H % 4 == 0 && H <= 2048 && ((((uintptr_t)x) | ((uintptr_t)y) | ((uintptr_t)w) | ((uintptr_t)b)) & 15) == 0,
+                "enc_norm: rows of at most 2048 floats, a multiple of 4, 16-byte aligned");
     if (ln) TSN_LAUNCH(enc_norm_kernel<true>, dim3(rows), dim3(256), 0, st, x, y, w, b, rows, H, eps);
     else TSN_LAUNCH(enc_norm_kernel<false>, dim3(rows), dim3(256), 0, st, x, y, w, b, rows, H, eps);
     TSN_HIP_CHECK(hipGetLastError());

@@ -217,20 +217,38 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
                 for (int e = 0; e < 8; ++e) acc[rr][b] += w[rr][e] * xs[e];
         }
     }
+    // Reduce-scatter of the V = GEMV_ROWS*NB partial sums over the wave: at the xor step of lane
+    // bit 32, 16, ... each lane keeps half of its values (the upper half when its bit is set) and
+    // adds the partner's copy of that half, so V values cost V - 1 shuffles; a butterfly over the
+    // remaining low lane bits finishes the sum. Lane l then holds value index
+    // sum_j bit_j(l) * V / 2^(j+1) over the scatter bits (fixed order: deterministic).
+    constexpr int V = GEMV_ROWS * NB;
+    float vals[V];
 #pragma unroll
-    for (int rr = 0; rr < GEMV_ROWS; ++rr) {
-        const int n = n0 + rr;
+    for (int rr = 0; rr < GEMV_ROWS; ++rr)
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            float v = wave_sum(acc[rr][b]);
-            if (lane == b && n < a.N) {
-                if (a.bias) v += a.bias[n];
-                if (a.addv) v += a.addv[(long long)b * a.ld_add + n];
-                if (a.silu) v = silu_f(v);
-                a.Y[(long long)b * a.ldy + n] = v;
-                if (a.Y2) a.Y2[(long long)b * a.ldy2 + n] = silu_f(v);
-            }
+        for (int b = 0; b < NB; ++b) vals[rr * NB + b] = acc[rr][b];
+    int idx = 0;
+#pragma unroll
+    for (int h = V / 2, bit = 32; h >= 1; h >>= 1, bit >>= 1) {
+        const bool upper = (lane & bit) != 0;
+#pragma unroll
+        for (int i = 0; i < h; ++i) {
+            const float lo = vals[i], hi = vals[i + h];
+            vals[i] = (upper ? hi : lo) + __shfl_xor(upper ? lo : hi, bit);
         }
+        idx += upper ? h : 0;
+    }
+#pragma unroll
+    for (int bit = 32 / V; bit >= 1; bit >>= 1) vals[0] += __shfl_xor(vals[0], bit);
+    const int rr = idx / NB, b = idx - rr * NB, n = n0 + rr;
+    if ((lane & (64 / V - 1)) == 0 && n < a.N) {
+        float v = vals[0];
+        if (a.bias) v += a.bias[n];
+        if (a.addv) v += a.addv[(long long)b * a.ld_add + n];
+        if (a.silu) v = silu_f(v);
+        a.Y[(long long)b * a.ldy + n] = v;
+        if (a.Y2) a.Y2[(long long)b * a.ldy2 + n] = silu_f(v);
     }
 }
 

@@ -120,6 +120,27 @@ int GraphRunner::resid_ln(GemmBatch &b, RedLnArgs &r, int H, float eps) {
         if (g.ln) bytes += (double)g.ln_len * (p.M / g.mod_L) * p.N * (r.ymode == LN_F16_HILO || g.hilo ? 4.0 : 2.0);
     }
     if (!work) return TSN_OK;
+    // nothing to sum (no split) and a plain f16 LN of every row of each segment: the one-wave-per-row
+    // LN kernel does the same job with less synchronization
+    bool plain_ln = r.ymode == LN_F16;
+    for (int i = 0; i < r.nseg; ++i) {
+        const RedLnSeg &g = r.seg[i];
+        plain_ln = plain_ln && g.splits <= 1 && g.ln && g.ln_len == g.mod_L && !g.hilo;
+    }
+    if (plain_ln) {
+        LnArgs ln;
+        memset(&ln, 0, sizeof ln);
+        ln.nseg = r.nseg; ln.H = H; ln.eps = eps;
+        for (int i = 0; i < r.nseg; ++i) {
+            const RedLnSeg &g = r.seg[i];
+            LnSeg &l = ln.seg[i];
+            l.X = g.X; l.ldx = g.ldx; l.xmap = g.xmap;
+            l.Y = g.Y; l.ldy = g.ldy; l.ymap = g.ymap;
+            l.mod = g.mod; l.mod_ld = g.mod_ld; l.mod_L = g.mod_L; l.shift_off = g.shift_off; l.scale_off = g.scale_off;
+            l.rows = g.M;
+        }
+        return run(K_LN16, 0, bytes, [&] { return launch_ln_mod(ln, LN_F16, st); });
+    }
     return run(r.ymode == LN_F16_HILO ? K_RLNHL : K_RLN16, 0, bytes, [&] { return launch_reduce_ln(r, st); });
 }
 

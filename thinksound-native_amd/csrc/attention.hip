@@ -31,7 +31,6 @@ namespace tsn {
 namespace {
 
 constexpr int AKB = 64;       // keys per block
-constexpr int ANS = 4;        // ring stages, each two key blocks: K 2 x 8 KB + Vt 2 x 8 KB
 constexpr int ASTAGE = 16384; // halves per stage
 
 typedef __attribute__((address_space(3))) char lds_char;
@@ -92,8 +91,12 @@ __device__ inline int attn_xcd_remap(int bid, int nwg) {
     return (xcd < rem ? xcd * (base + 1) : rem * (base + 1) + (xcd - rem) * base) + idx;
 }
 
-__global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
-    __shared__ __attribute__((aligned(1024))) half_t smem[ANS * ASTAGE];
+// NSTG ring stages of two key blocks each: 4 (128 KB, one workgroup per CU; up to 512 keys load
+// at once) or 2 (64 KB, two workgroups per CU, one pair of key blocks in flight while the other is
+// multiplied; for longer contexts, where the second workgroup covers the load latency)
+template <int NSTG>
+__global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(const AttnArgs a) {
+    __shared__ __attribute__((aligned(1024))) half_t smem[NSTG * ASTAGE];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar DMA choices
     const int half = wave >> 2, wq = wave & 3;
@@ -203,15 +206,31 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
         }
     };
 
-    if (npair <= ANS) {
+    if (npair <= NSTG) {
         // every key block fits the ring: load all, one wait, no barrier inside the loop
         for (int p = 0; p < npair; ++p) issue(p, p);
         wait_vmcnt(0);
         block_barrier();
         for (int p = 0; p < npair; ++p)
             if (2 * p + half < nkb) compute(p, 2 * p + half);
+    } else if constexpr (NSTG == 2) {
+        // two stages: pair p + 1 lands while pair p is multiplied
+        issue(0, 0);
+        wait_vmcnt(0);
+        block_barrier();
+        issue(1, 1);
+        for (int p = 0; p < npair; ++p) {
+            const int st = p & 1;
+            if (2 * p + half < nkb) compute(st, 2 * p + half);
+            if (p + 1 < npair) {
+                wait_vmcnt(0);      // pair p + 1, the only one in flight, has landed
+                block_barrier();    // and every wave is done with stage st
+                if (p + 2 < npair) issue(p + 2, st);
+            }
+        }
     } else {
-        // ring over pairs of key blocks, as in the GEMM: pair p in stage p % ANS
+        // ring over pairs of key blocks, as in the GEMM: pair p in stage p % NSTG
+        static_assert(NSTG == 4, "four-stage ring");
         issue(0, 0);
         issue(1, 1);
         issue(2, 2);
@@ -219,12 +238,12 @@ __global__ __launch_bounds__(512, 1) void flash_attn_kernel(const AttnArgs a) {
         block_barrier();
         issue(3, 3);
         for (int p = 0; p < npair; ++p) {
-            const int st = p % ANS;
+            const int st = p % NSTG;
             if (2 * p + half < nkb) compute(st, 2 * p + half);
             if (p + 1 < npair) {
                 wait_vmcnt(4 * min(npair - 2 - p, 2));
                 block_barrier();
-                if (p + ANS < npair) issue(p + ANS, st);
+                if (p + NSTG < npair) issue(p + NSTG, st);
             }
         }
     }
@@ -312,7 +331,9 @@ int launch_attention(const AttnArgs &a, hipStream_t st) {
                 "attention: per-head K/Vt extent must stay below 2 GB (buffer addressing)");
     TSN_REQUIRE((long long)((a.S + 63) / 64) * a.BH < (1LL << 31), "attention: too many query tiles");
     dim3 grid((unsigned)((a.S + 63) / 64 * a.BH)), block(512);
-    TSN_LAUNCH(flash_attn_kernel, grid, block, 0, st, a);
+    // up to 512 keys: all key blocks in LDS at once; longer: the two-stage ring, two workgroups per CU
+    if (a.S <= 4 * 2 * AKB) TSN_LAUNCH(flash_attn_kernel<4>, grid, block, 0, st, a);
+    else TSN_LAUNCH(flash_attn_kernel<2>, grid, block, 0, st, a);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }

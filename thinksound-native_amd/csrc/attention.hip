@@ -331,8 +331,9 @@ int launch_attention(const AttnArgs &a, hipStream_t st) {
                 "attention: per-head K/Vt extent must stay below 2 GB (buffer addressing)");
     TSN_REQUIRE((long long)((a.S + 63) / 64) * a.BH < (1LL << 31), "attention: too many query tiles");
     dim3 grid((unsigned)((a.S + 63) / 64 * a.BH)), block(512);
-    // up to 512 keys: all key blocks in LDS at once; longer: the two-stage ring, two workgroups per CU
-    if (a.S <= 4 * 2 * AKB) TSN_LAUNCH(flash_attn_kernel<4>, grid, block, 0, st, a);
+    // up to 512 keys and at most one workgroup per CU: all key blocks in LDS at once; otherwise the
+    // two-stage ring, two workgroups per CU
+    if (a.S <= 4 * 2 * AKB && grid.x <= 256) TSN_LAUNCH(flash_attn_kernel<4>, grid, block, 0, st, a);
     else TSN_LAUNCH(flash_attn_kernel<2>, grid, block, 0, st, a);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;

@@ -625,11 +625,14 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
 // f32 [BM][BN] store of the accumulators to part (a stream-K segment, finished by the fixup kernel).
 // HL: problems may read half-width W (hi|lo A operand); SEG: more tiles follow in this workgroup
 // (stream-K), so the LDS C tile is released with a barrier at the end.
-template <int EPI, bool HL, bool SEG>
+// NSX: LDS stages (5: 160 KB, one workgroup per CU; 2: 68 KB, two workgroups per CU, for grids
+// of several rounds where the second workgroup covers the first's barrier and load waits).
+template <int EPI, bool HL, bool SEG, int NSX = NS>
 __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, int kbeg, int nk, float *part, int ks,
                                           int tid) {
-    // stage s: A tile at smem + s*STAGE, W tile at smem + (NS + s)*STAGE; reused for the C tile
-    __shared__ __attribute__((aligned(1024))) half_t smem[2 * NS * STAGE];
+    // stage s: A tile at smem + s*STAGE, W tile at smem + (NSX + s)*STAGE; reused for the C tile
+    constexpr int SMEM = 2 * NSX * STAGE > BM * TP * 2 ? 2 * NSX * STAGE : BM * TP * 2;
+    __shared__ __attribute__((aligned(1024))) half_t smem[SMEM];
 
     const int lane = tid & 63, wave = tid >> 6;
     const int M = P.M, N = P.N, lda = P.lda, Kc = P.Kc, pad = P.pad, aT = P.a_T;
@@ -707,7 +710,7 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
         }
         const int kc2 = acol * 2 + trow * lda2;
         lds_char *sa = (lds_char *)(smem + stage * STAGE) + wave * 2048;
-        lds_char *sb = (lds_char *)(smem + (NS + stage) * STAGE) + wave * 2048;
+        lds_char *sb = (lds_char *)(smem + (NSX + stage) * STAGE) + wave * 2048;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int ts = a_ts0[i] + trow;
@@ -741,7 +744,7 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
         for (int j = 0; j < 4; ++j) b_rd[kh][j] = (wn * 64 + j * 16 + (lane & 15)) * BK + slot * 8;
     }
     auto compute = [&](int stage) {
-        const half_t *sa = smem + stage * STAGE, *sb = smem + (NS + stage) * STAGE;
+        const half_t *sa = smem + stage * STAGE, *sb = smem + (NSX + stage) * STAGE;
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
             half8 af[2], bf[4];
@@ -763,35 +766,42 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
     // is now free) and refills that stage NS tiles ahead.
     issue(0, 0);
 #pragma unroll
-    for (int j = 1; j < NS - 1; ++j)
+    for (int j = 1; j < NSX - 1; ++j)
         if (nk > j) issue(j, j);
-    wait_vmcnt(4 * min(nk - 1, NS - 2));
+    wait_vmcnt(4 * min(nk - 1, NSX - 2));
     block_barrier();
-    if (nk > NS - 1) issue(NS - 1, NS - 1);
+    if (nk > NSX - 1) issue(NSX - 1, NSX - 1);
 #define TSN_GEMM_STEP(NEXT, S)                                                                  \
     {                                                                                           \
         compute(S);                                                                             \
-        wait_vmcnt(4 * (NS - 2));                                                               \
+        wait_vmcnt(4 * (NSX - 2));                                                              \
         block_barrier();                                                                        \
         issue(NEXT, S);                                                                         \
     }
     int kt = 0;
-    for (; kt + 2 * NS <= nk; kt += NS) {
-        TSN_GEMM_STEP(kt + NS + 0, 0)
-        TSN_GEMM_STEP(kt + NS + 1, 1)
-        TSN_GEMM_STEP(kt + NS + 2, 2)
-        TSN_GEMM_STEP(kt + NS + 3, 3)
-        TSN_GEMM_STEP(kt + NS + 4, 4)
+    if constexpr (NSX == 5) {
+        for (; kt + 2 * NSX <= nk; kt += NSX) {
+            TSN_GEMM_STEP(kt + NSX + 0, 0)
+            TSN_GEMM_STEP(kt + NSX + 1, 1)
+            TSN_GEMM_STEP(kt + NSX + 2, 2)
+            TSN_GEMM_STEP(kt + NSX + 3, 3)
+            TSN_GEMM_STEP(kt + NSX + 4, 4)
+        }
+    } else {
+        for (; kt + 2 * NSX <= nk; kt += NSX) {
+#pragma unroll
+            for (int s2 = 0; s2 < NSX; ++s2) TSN_GEMM_STEP(kt + NSX + s2, s2)
+        }
     }
 #undef TSN_GEMM_STEP
-    // tail: the last < 2*NS tiles; tile kt is visible, kt+1..min(kt+NS-1, nk-1) in flight
+    // tail: the last < 2*NSX tiles; tile kt is visible, kt+1..min(kt+NSX-1, nk-1) in flight
     for (; kt < nk; ++kt) {
-        const int st = kt % NS;
+        const int st = kt % NSX;
         compute(st);
         if (kt + 1 < nk) {
-            wait_vmcnt(4 * min(nk - 2 - kt, NS - 2));
+            wait_vmcnt(4 * min(nk - 2 - kt, NSX - 2));
             block_barrier();
-            if (kt + NS < nk) issue(kt + NS, st);
+            if (kt + NSX < nk) issue(kt + NSX, st);
         }
     }
     // Every DMA has landed (the last tile was waited for). The waves store their accumulators as a
@@ -829,7 +839,7 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
 // touches over its part of K. A tile covered whole gets the epilogue here; a tile cut by a
 // workgroup boundary leaves f32 partials in bt.ws slot (w, 0) for the first tile of w or (w, 1) for
 // its last, which gemm_fixup_kernel sums in K order (deterministic for a given G) and finishes.
-template <int EPI, bool HL>
+template <int EPI, bool HL, int NSX = NS>
 __device__ __forceinline__ void pipe_dp(const GemmBatch &bt) {
     const int tid = threadIdx.x;
     const int wg = xcd_remap(blockIdx.x, gridDim.x);
@@ -842,7 +852,7 @@ __device__ __forceinline__ void pipe_dp(const GemmBatch &bt) {
     int tm, tn;
     tile_mn(rem, P.tiles_m, P.tiles_n, tm, tn);
     const int nk = P.K / BK / P.splits;
-    pipe_tile<EPI, HL, false>(P, tm * BM, tn * BN, ks * nk, nk, nullptr, ks, tid);
+    pipe_tile<EPI, HL, false, NSX>(P, tm * BM, tn * BN, ks * nk, nk, nullptr, ks, tid);
 }
 template <int EPI>
 __global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
@@ -852,6 +862,11 @@ __global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
 template <int EPI>
 __global__ __launch_bounds__(512, 1) void gemm_pipe_hl_kernel(const GemmBatch bt) {
     pipe_dp<EPI, true>(bt);
+}
+// two LDS stages, two workgroups per CU (grids of several rounds)
+template <int EPI>
+__global__ __launch_bounds__(512, 2) void gemm_pipe2_kernel(const GemmBatch bt) {
+    pipe_dp<EPI, false, 2>(bt);
 }
 
 // gemm_small_kernel: plain GEMMs (one tap), 64x64 C tiles over the full K, 4 waves of 32x32
@@ -1437,6 +1452,13 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
                    : a_f32 ? "gemm_f16_kernel<true, 0>"
                    : (epi == EPI_STORE ? "gemm_f16_kernel<false, 0>" : epi == EPI_RESID ? "gemm_f16_kernel<false, 1>"
                                                                         : "gemm_f16_kernel<false, 2>");
+    // two LDS stages and two workgroups per CU once the data-parallel grid takes two rounds or more
+    // (the QKV epilogue needs more registers than two workgroups per CU leave)
+    b.ns2 = pipe && !b.sk && !b.hl && epi != EPI_QKV && b.total_tiles >= 2 * NCU ? 1 : 0;
+    if (b.ns2)
+        b.kname = epi == EPI_STORE ? "gemm_pipe2_kernel<0>" : epi == EPI_RESID ? "gemm_pipe2_kernel<1>"
+                  : epi == EPI_SNAKE ? "gemm_pipe2_kernel<4>" : epi == EPI_RSNAKE ? "gemm_pipe2_kernel<5>"
+                  : "gemm_pipe2_kernel<3>";
     if (a_f32) TSN_REQUIRE(epi == EPI_STORE, "gemm: f32 A operand only with a plain store epilogue");
     TSN_REQUIRE(epi == EPI_STORE || epi == EPI_RESID || epi == EPI_QKV || epi == EPI_SWIGLU || epi == EPI_SNAKE ||
                     epi == EPI_RSNAKE,
@@ -1467,6 +1489,13 @@ int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st)
             else if (epi == EPI_QKV) TSN_LAUNCH((gemm_pipe_hl_kernel<EPI_QKV>), grid, block, 0, st, b);
             else if (epi == EPI_SWIGLU) TSN_LAUNCH((gemm_pipe_hl_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
             else { set_error("gemm: unknown epilogue"); return TSN_ERR_ARG; }
+        } else if (b.ns2) {
+            if (epi == EPI_STORE) TSN_LAUNCH((gemm_pipe2_kernel<EPI_STORE>), grid, block, 0, st, b);
+            else if (epi == EPI_RESID) TSN_LAUNCH((gemm_pipe2_kernel<EPI_RESID>), grid, block, 0, st, b);
+            else if (epi == EPI_SWIGLU) TSN_LAUNCH((gemm_pipe2_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
+            else if (epi == EPI_SNAKE) TSN_LAUNCH((gemm_pipe2_kernel<EPI_SNAKE>), grid, block, 0, st, b);
+            else if (epi == EPI_RSNAKE) TSN_LAUNCH((gemm_pipe2_kernel<EPI_RSNAKE>), grid, block, 0, st, b);
+            else { set_error("gemm: no two-stage kernel for this epilogue"); return TSN_ERR_ARG; }
         } else if (epi == EPI_STORE) TSN_LAUNCH((gemm_pipe_kernel<EPI_STORE>), grid, block, 0, st, b);
         else if (epi == EPI_RESID) TSN_LAUNCH((gemm_pipe_kernel<EPI_RESID>), grid, block, 0, st, b);
         else if (epi == EPI_QKV) TSN_LAUNCH((gemm_pipe_kernel<EPI_QKV>), grid, block, 0, st, b);

@@ -85,6 +85,9 @@ struct GemmBatch {
     // fewer than 128 tiles. gemm_plan clears it otherwise, and the workspace then serves the usual
     // split-K / stream-K choice.
     int small = 0;
+    // set by gemm_plan: the two-stage kernel (gemm_pipe2_kernel, two workgroups per CU) for
+    // data-parallel grids of at least two rounds
+    int ns2 = 0;
 };
 
 // a_f32: A operand is f32 (converted to f16 on load). All problems share the epilogue kind.

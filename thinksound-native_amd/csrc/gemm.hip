@@ -1452,9 +1452,9 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
                    : a_f32 ? "gemm_f16_kernel<true, 0>"
                    : (epi == EPI_STORE ? "gemm_f16_kernel<false, 0>" : epi == EPI_RESID ? "gemm_f16_kernel<false, 1>"
                                                                         : "gemm_f16_kernel<false, 2>");
-    // two LDS stages and two workgroups per CU once the data-parallel grid takes two rounds or more
-    // (the QKV epilogue needs more registers than two workgroups per CU leave)
-    b.ns2 = pipe && !b.sk && !b.hl && epi != EPI_QKV && b.total_tiles >= 2 * NCU ? 1 : 0;
+    // two LDS stages and two workgroups per CU once the data-parallel grid exceeds one round (the
+    // QKV epilogue needs more registers than two workgroups per CU leave)
+    b.ns2 = pipe && !b.sk && !b.hl && epi != EPI_QKV && b.total_tiles > NCU ? 1 : 0;
     if (b.ns2)
         b.kname = epi == EPI_STORE ? "gemm_pipe2_kernel<0>" : epi == EPI_RESID ? "gemm_pipe2_kernel<1>"
                   : epi == EPI_SNAKE ? "gemm_pipe2_kernel<4>" : epi == EPI_RSNAKE ? "gemm_pipe2_kernel<5>"

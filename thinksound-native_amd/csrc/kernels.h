@@ -86,7 +86,7 @@ struct GemmBatch {
     // split-K / stream-K choice.
     int small = 0;
     // set by gemm_plan: the two-stage kernel (gemm_pipe2_kernel, two workgroups per CU) for
-    // data-parallel grids of at least two rounds
+    // data-parallel grids of more than one round (256 tiles)
     int ns2 = 0;
 };
 

@@ -1452,13 +1452,12 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
                    : a_f32 ? "gemm_f16_kernel<true, 0>"
                    : (epi == EPI_STORE ? "gemm_f16_kernel<false, 0>" : epi == EPI_RESID ? "gemm_f16_kernel<false, 1>"
                                                                         : "gemm_f16_kernel<false, 2>");
-    // two LDS stages and two workgroups per CU once the data-parallel grid exceeds one round (the
-    // QKV epilogue needs more registers than two workgroups per CU leave)
-    b.ns2 = pipe && !b.sk && !b.hl && epi != EPI_QKV && b.total_tiles > NCU ? 1 : 0;
+    // two LDS stages and two workgroups per CU once the data-parallel grid exceeds one round
+    b.ns2 = pipe && !b.sk && !b.hl && b.total_tiles > NCU ? 1 : 0;
     if (b.ns2)
         b.kname = epi == EPI_STORE ? "gemm_pipe2_kernel<0>" : epi == EPI_RESID ? "gemm_pipe2_kernel<1>"
-                  : epi == EPI_SNAKE ? "gemm_pipe2_kernel<4>" : epi == EPI_RSNAKE ? "gemm_pipe2_kernel<5>"
-                  : "gemm_pipe2_kernel<3>";
+                  : epi == EPI_QKV ? "gemm_pipe2_kernel<2>" : epi == EPI_SNAKE ? "gemm_pipe2_kernel<4>"
+                  : epi == EPI_RSNAKE ? "gemm_pipe2_kernel<5>" : "gemm_pipe2_kernel<3>";
     if (a_f32) TSN_REQUIRE(epi == EPI_STORE, "gemm: f32 A operand only with a plain store epilogue");
     TSN_REQUIRE(epi == EPI_STORE || epi == EPI_RESID || epi == EPI_QKV || epi == EPI_SWIGLU || epi == EPI_SNAKE ||
                     epi == EPI_RSNAKE,
@@ -1495,6 +1494,7 @@ int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st)
             else if (epi == EPI_SWIGLU) TSN_LAUNCH((gemm_pipe2_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
             else if (epi == EPI_SNAKE) TSN_LAUNCH((gemm_pipe2_kernel<EPI_SNAKE>), grid, block, 0, st, b);
             else if (epi == EPI_RSNAKE) TSN_LAUNCH((gemm_pipe2_kernel<EPI_RSNAKE>), grid, block, 0, st, b);
+            else if (epi == EPI_QKV) TSN_LAUNCH((gemm_pipe2_kernel<EPI_QKV>), grid, block, 0, st, b);
             else { set_error("gemm: no two-stage kernel for this epilogue"); return TSN_ERR_ARG; }
         } else if (epi == EPI_STORE) TSN_LAUNCH((gemm_pipe_kernel<EPI_STORE>), grid, block, 0, st, b);
         else if (epi == EPI_RESID) TSN_LAUNCH((gemm_pipe_kernel<EPI_RESID>), grid, block, 0, st, b);

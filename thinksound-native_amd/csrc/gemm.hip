@@ -868,6 +868,10 @@ template <int EPI>
 __global__ __launch_bounds__(512, 2) void gemm_pipe2_kernel(const GemmBatch bt) {
     pipe_dp<EPI, false, 2>(bt);
 }
+template <int EPI>
+__global__ __launch_bounds__(512, 2) void gemm_pipe2_hl_kernel(const GemmBatch bt) {
+    pipe_dp<EPI, true, 2>(bt);
+}
 
 // gemm_small_kernel: plain GEMMs (one tap), 64x64 C tiles over the full K, 4 waves of 32x32
 // (2 x 2 MFMA blocks of 16x16), the same swizzled direct-to-LDS ring as pipe_tile (5 stages of
@@ -1453,8 +1457,11 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
                    : (epi == EPI_STORE ? "gemm_f16_kernel<false, 0>" : epi == EPI_RESID ? "gemm_f16_kernel<false, 1>"
                                                                         : "gemm_f16_kernel<false, 2>");
     // two LDS stages and two workgroups per CU once the data-parallel grid exceeds one round
-    b.ns2 = pipe && !b.sk && !b.hl && b.total_tiles > NCU ? 1 : 0;
-    if (b.ns2)
+    b.ns2 = pipe && !b.sk && b.total_tiles > NCU ? 1 : 0;
+    if (b.ns2 && b.hl)
+        b.kname = epi == EPI_STORE ? "gemm_pipe2_hl_kernel<0>" : epi == EPI_RESID ? "gemm_pipe2_hl_kernel<1>"
+                  : epi == EPI_QKV ? "gemm_pipe2_hl_kernel<2>" : "gemm_pipe2_hl_kernel<3>";
+    else if (b.ns2)
         b.kname = epi == EPI_STORE ? "gemm_pipe2_kernel<0>" : epi == EPI_RESID ? "gemm_pipe2_kernel<1>"
                   : epi == EPI_QKV ? "gemm_pipe2_kernel<2>" : epi == EPI_SNAKE ? "gemm_pipe2_kernel<4>"
                   : epi == EPI_RSNAKE ? "gemm_pipe2_kernel<5>" : "gemm_pipe2_kernel<3>";
@@ -1481,6 +1488,12 @@ int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st)
             else if (epi == EPI_SWIGLU) TSN_LAUNCH((gemm_sk_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
             else if (epi == EPI_SNAKE) TSN_LAUNCH((gemm_sk_kernel<EPI_SNAKE>), grid, block, 0, st, b);
             else if (epi == EPI_RSNAKE) TSN_LAUNCH((gemm_sk_kernel<EPI_RSNAKE>), grid, block, 0, st, b);
+            else { set_error("gemm: unknown epilogue"); return TSN_ERR_ARG; }
+        } else if (b.hl && b.ns2) {
+            if (epi == EPI_STORE) TSN_LAUNCH((gemm_pipe2_hl_kernel<EPI_STORE>), grid, block, 0, st, b);
+            else if (epi == EPI_RESID) TSN_LAUNCH((gemm_pipe2_hl_kernel<EPI_RESID>), grid, block, 0, st, b);
+            else if (epi == EPI_QKV) TSN_LAUNCH((gemm_pipe2_hl_kernel<EPI_QKV>), grid, block, 0, st, b);
+            else if (epi == EPI_SWIGLU) TSN_LAUNCH((gemm_pipe2_hl_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
             else { set_error("gemm: unknown epilogue"); return TSN_ERR_ARG; }
         } else if (b.hl) {
             if (epi == EPI_STORE) TSN_LAUNCH((gemm_pipe_hl_kernel<EPI_STORE>), grid, block, 0, st, b);

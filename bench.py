@@ -151,10 +151,23 @@ def stats_summary(stats_csv, cmd, title="eager launches of the DiT evaluation (B
 
 def profile_pass(which):
     """workload for rocprofv3 --kernel-trace: eager launches only. vae: five 8 s decodes (T=172);
-    enc: five CLIP and five T5 encodes of 77 tokens at the reference sizes"""
+    enc: five CLIP and five T5 encodes of 77 tokens at the reference sizes; ref: five evaluations
+    of the reference checkpoint's graph at 8 s, B = 2 (one CFG pair)"""
     tsn = importlib.import_module("thinksound-native_amd")
     rt = tsn.Runtime(0)
-    if which == "vae":
+    if which == "ref":
+        spec = tsn.ref_spec_for_duration(8, 2)
+        m = tsn.RefDitModel(rt, spec)
+        m.upload_weights(tsn.ref_synth_weights(spec, 4242, 0.0))
+        inp = tsn.ref_synth_inputs(spec, 4242, cfg_pairs=True)
+        d = {k: rt.array(v) for k, v in inp.items()}
+        v = rt.empty((spec.B, spec.T, spec.latent))
+        for i in range(5):
+            m.forward_ex(d["x"], d["t"], d["clip_pp"], d["text_pp"], d["gcmlp"], d["sync_gather"], v)
+            rt.sync()
+            log("profile pass: reference graph eval %d done" % i)
+        m.close()
+    elif which == "vae":
         spec = tsn.vae_spec_for_duration(8)
         m = tsn.VaeModel(rt, spec)
         m.upload_weights(tsn.vae_synth_weights(spec, 4242))
@@ -467,8 +480,9 @@ def main():
     ap.add_argument("--stats-summary", nargs=2, metavar=("STATS_CSV", "CMD"),
                     help="print the summary of a rocprofv3 kernel_stats.csv (no GPU use)")
     ap.add_argument("--stats-title", default=None, help="workload line of --stats-summary")
-    ap.add_argument("--profile-pass", choices=["vae", "enc"],
-                    help="only run eager VAE decodes or text-encoder passes (workload for rocprofv3 --kernel-trace)")
+    ap.add_argument("--profile-pass", choices=["vae", "enc", "ref"],
+                    help="only run eager VAE decodes, text-encoder passes or reference-graph evaluations "
+                         "(workload for rocprofv3 --kernel-trace)")
     args = ap.parse_args()
     if args.pmc_summary:
         sys.stdout.write(pmc_summary(*args.pmc_summary))

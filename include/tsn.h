@@ -55,22 +55,37 @@ int tsn_sync(tsn_runtime *rt);
 
 /* ---------------- launcher runtime: tn::Runtime (src/net.h:18-51) ---------------- */
 /* Y[M,N] = X[M,K]·W[N,K]^T (+bias[N], f32). Runtime::gemm src/net.h:24-26, src/net.mm:14-23.
- * wdtype TSN_F16 runs on MFMA (X f32 or f16, converted to f16 on load; Y f32 or f16);
- * TSN_F32 / TSN_BF16 weights run an f32 path (X, Y f32). ld* = 0 means packed.
- * MFMA path needs K, ldx, ldw multiples of 8 and 16-byte aligned X and W. */
+ * wdtype TSN_F16 with f32 X keeps the reference's f32-activation contract (gemm_mpp_h,
+ * shaders/gemm_mpp.metal:19-25): X is split into an f16 hi|lo pair on the device and multiplied
+ * against [W | W] on MFMA with f32 accumulation, so the product is f32-accurate (relative error
+ * about 2^-22 of the operand, against 2^-11 for an f16-rounded X). Y f32, or f16 on request. Shapes
+ * the MFMA tiling does not take (K % 64, N % 8, unaligned W/bias/Y) run exact f32 products on the
+ * SIMT path (f32 Y only). wdtype TSN_F16 with f16 X is the plain f16 product (opt-in, f16 operands
+ * as given). TSN_F32 / TSN_BF16 weights run the f32 SIMT path (X, Y f32). ld* = 0 means packed.
+ * Uses the runtime's grow-on-demand scratch (2*M*K halves). */
 int tsn_gemm(tsn_runtime *rt, int wdtype, const void *W, const void *X, int xdtype, void *Y, int ydtype,
              const float *bias, uint32_t M, uint32_t N, uint32_t K, uint32_t ldx, uint32_t ldw, uint32_t ldy);
 /* y[n] = bias[n] + W[n,:]·x. Runtime::gemv src/net.h:27-28, src/net.mm:51-56 (wdtype f16/bf16/f32). */
 int tsn_gemv(tsn_runtime *rt, const void *W, int wdtype, const float *x, float *y, const float *bias,
              uint32_t N, uint32_t K, uint32_t ldw);
-/* Upload-time conv weight transform [OC][IC][K] -> [OC][K][IC] f16 (W f16, or bf16 when w_bf16).
- * The reference converts at load (src/net.mm:141-168); this adds the tap-major reorder that lets
- * tsn_conv1d run as an implicit GEMM. Wp holds OC*IC*K halves. */
-int tsn_conv1d_prepare(tsn_runtime *rt, const void *W, int w_bf16, void *Wp, uint32_t OC, uint32_t IC, uint32_t K);
-/* conv1d, x [T,IC] f32, y [OL,OC] f32 (+bias). Runtime::conv src/net.h:29-34, src/net.mm:25-49.
- * Implemented: stride 1, dil 1, OL = T + 2*pad - K + 1, IC % 64 == 0 (K > 1); else TSN_ERR_UNSUPPORTED. */
-int tsn_conv1d(tsn_runtime *rt, const void *Wp, const float *bias, const float *x, float *y, uint32_t T,
-               uint32_t OL, uint32_t IC, uint32_t OC, uint32_t K, uint32_t stride, uint32_t pad, uint32_t dil);
+/* Upload-time conv weight transform, W [OC][IC][K] in the reference's layout (wdtype TSN_F16, TSN_BF16
+ * or TSN_F32; the reference converts at load, src/net.mm:141-168) -> Wp, tap-major f16 rows that
+ * tsn_conv1d reads as an implicit GEMM: f16/bf16 weights one f16 per element (bf16 with the
+ * reference upload's rounding), f32 weights [hi | hi | lo] f16 parts per tap (f32-accurate
+ * products). Wp must hold tsn_conv1d_prepared_bytes(wdtype, OC, IC, K) bytes. */
+size_t tsn_conv1d_prepared_bytes(int wdtype, uint32_t OC, uint32_t IC, uint32_t K);
+int tsn_conv1d_prepare(tsn_runtime *rt, const void *W, int wdtype, void *Wp, uint32_t OC, uint32_t IC, uint32_t K);
+/* conv1d, x [T,IC] f32, y [OL,OC] f32 (+bias). Runtime::conv src/net.h:29-34, src/net.mm:25-49, with
+ * the im2col semantics of shaders/ops_conv.metal:226-236,266-283: tap k of output row t reads row
+ * t*stride - pad + k*dil, or, when convt, row (t - pad + k)/stride of the zero-stuffed input where
+ * t - pad + k is a non-negative multiple of stride; zero outside [0, T). Wp is the output of
+ * tsn_conv1d_prepare for the same wdtype (wf16 true: TSN_F16/TSN_BF16; false: TSN_F32). f32-accurate
+ * for every weight dtype. Stride 1, dilation 1 and IC % 64 == 0 run as an implicit GEMM (taps in K);
+ * other geometries gather the operand in chunks of at most 64 MB of scratch; OC % 8 != 0 runs a
+ * direct conv. */
+int tsn_conv1d(tsn_runtime *rt, int wdtype, const void *Wp, const float *bias, const float *x, float *y, uint32_t T,
+               uint32_t OL, uint32_t IC, uint32_t OC, uint32_t K, uint32_t stride, uint32_t pad, uint32_t dil,
+               int convt);
 /* elementwise, f32 (src/net.h:37-49; shaders/ops_conv.metal:9-57,193-201) */
 int tsn_silu(tsn_runtime *rt, float *x, size_t n);
 int tsn_copy(tsn_runtime *rt, const float *x, float *y, size_t n);
@@ -78,7 +93,18 @@ int tsn_swiglu(tsn_runtime *rt, const float *a, const float *b, float *y, size_t
 int tsn_add(tsn_runtime *rt, const float *a, const float *b, float *y, size_t n);
 int tsn_add_bcast_col(tsn_runtime *rt, const float *x, const float *v, float *y, uint32_t S, uint32_t H);
 int tsn_cfg_euler(tsn_runtime *rt, const float *fc, const float *fu, float *x, size_t n, float cfg, float dt);
-/* named kernels dispatched by dit_fwd.cpp (src/dit_fwd.cpp:16-22), on net.h as the north star asks:
+int tsn_geglu(tsn_runtime *rt, const float *a, const float *b, float *y, size_t n);   /* gelu_tanh(a)·b  :15-24 */
+int tsn_gelu_quick(tsn_runtime *rt, float *x, size_t n);                              /* in place       :25-29 */
+/* norms over rows of H floats, biased variance (shaders/ops_conv.metal:77-113). ln_wb and rms_w take
+ * H % 4 == 0, H <= 2048 and 16-byte aligned rows. */
+int tsn_ln_plain(tsn_runtime *rt, const float *x, float *y, uint32_t S, uint32_t H, float eps);
+int tsn_ln_wb(tsn_runtime *rt, const float *x, float *y, const float *w, const float *b, uint32_t S, uint32_t H,
+              float eps);
+int tsn_rms_w(tsn_runtime *rt, const float *x, float *y, const float *w, uint32_t S, uint32_t H, float eps);
+/* y[c] = mean over the S rows of x[:, c], rows summed in order. Runtime::mean_cols src/net.h:50,
+ * shaders/ops_conv.metal:171-193 */
+int tsn_mean_cols(tsn_runtime *rt, const float *x, float *y, uint32_t S, uint32_t H);
+/* named kernels dispatched by dit_fwd.cpp (src/dit_fwd.cpp:16-22), as runtime launchers here:
  * adaln_ln  — AD{H,per_row,chunks,base,eps}  shaders/ops_conv.metal:127-144 (y f32 or f16)
  * gate_add  — GA{H,per_row,chunks,gate_idx}  shaders/ops_conv.metal:146-154
  * rms_head  — RH{ld,hd,col_off,row_off,eps}  shaders/ops_conv.metal:115-125 (in place)
@@ -88,6 +114,9 @@ int tsn_adaln_ln(tsn_runtime *rt, const float *x, const float *mod, void *y, int
                  uint32_t per_row, uint32_t chunks, uint32_t base, float eps);
 int tsn_gate_add(tsn_runtime *rt, const float *x, const float *f, const float *mod, float *y, uint32_t rows,
                  uint32_t H, uint32_t per_row, uint32_t chunks, uint32_t gate_idx);
+/* qkv_split3 — QS3{H,row_off}  shaders/ops_conv.metal:60-74: the element-interleaved projection rows
+ * [rows][3H] (column 3c + j) -> block q|k|v rows row_off.. of dst [.][3H] (src/dit_fwd.cpp:33-36) */
+int tsn_qkv_split3(tsn_runtime *rt, const float *src, float *dst, uint32_t rows, uint32_t H, uint32_t row_off);
 int tsn_rms_head(tsn_runtime *rt, float *x, const float *w, uint32_t rows, uint32_t nh, uint32_t ld, uint32_t hd,
                  uint32_t col_off, uint32_t row_off, float eps);
 int tsn_rope_pairs(tsn_runtime *rt, float *x, const int32_t *pos, uint32_t rows, uint32_t nh, uint32_t ld,

@@ -69,6 +69,15 @@ void orc_add(const float *a, const float *b, float *y, size_t n);
 void orc_add_bcast_col(const float *x, const float *v, float *y, int S, int H);
 void orc_cfg_euler(const float *fc, const float *fu, float *x, size_t n, float cfg, float dt);
 
+// the rest of the reference's launcher surface (src/net.h:37-50; shaders/ops_conv.metal:15-29,60-89,171-193):
+// gated tanh-GELU y = gelu_tanh(a)*b (argument clamped to [-10, 10]); quick GELU in place; LayerNorm
+// without affine over rows of H; column means over S rows; qkv de-interleave into rows row_off..
+void orc_geglu(const float *a, const float *b, float *y, size_t n);
+void orc_gelu_quick(float *x, size_t n);
+void orc_ln_plain(const float *x, float *y, int S, int H, float eps);
+void orc_mean_cols(const float *x, float *y, int S, int H);
+void orc_qkv_split3(const float *src, float *dst, int rows, int H, int row_off);
+
 // sinusoidal timestep embedding, cos half then sin half:
 // fr_k = (10000/max_period) * 10000^(-2k/D); out[k] = cos(t*fr_k), out[D/2+k] = sin(t*fr_k)
 // (src/dit_fwd.cpp:111-119)

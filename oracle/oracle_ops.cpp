@@ -256,6 +256,46 @@ extern "C" void orc_cfg_euler(const float *fc, const float *fu, float *x, size_t
         x[i] += dt * v;
     }
 }
+// shaders/ops_conv.metal:15-24: y = 0.5 v (1 + tanh(clamp(0.7978845608 (v + 0.044715 v^3), -10, 10))) b
+extern "C" void orc_geglu(const float *a, const float *b, float *y, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        const float v = a[i];
+        const float arg = 0.7978845608f * (v + 0.044715f * v * v * v);
+        y[i] = 0.5f * v * (1.0f + tanhf(fminf(fmaxf(arg, -10.0f), 10.0f))) * b[i];
+    }
+}
+// shaders/ops_conv.metal:25-29: x = x / (1 + exp(-1.702 x))
+extern "C" void orc_gelu_quick(float *x, size_t n) {
+    for (size_t i = 0; i < n; ++i) x[i] = x[i] / (1.0f + expf(-1.702f * x[i]));
+}
+// shaders/ops_conv.metal:77-89: per row, mean then the biased variance of the centred row, no affine
+extern "C" void orc_ln_plain(const float *x, float *y, int S, int H, float eps) {
+    for (int r = 0; r < S; ++r) {
+        const float *xr = x + (size_t)r * H;
+        float mean = 0.0f, var = 0.0f;
+        for (int i = 0; i < H; ++i) mean += xr[i];
+        mean /= (float)H;
+        for (int i = 0; i < H; ++i) { const float d = xr[i] - mean; var += d * d; }
+        var /= (float)H;
+        const float inv = 1.0f / sqrtf(var + eps);
+        for (int i = 0; i < H; ++i) y[(size_t)r * H + i] = (xr[i] - mean) * inv;
+    }
+}
+// shaders/ops_conv.metal:171-193 (Runtime::mean_cols, src/net.mm:103-106): y[c] = sum_s x[s][c] / S
+extern "C" void orc_mean_cols(const float *x, float *y, int S, int H) {
+    for (int c = 0; c < H; ++c) {
+        float acc = 0.0f;
+        for (int s = 0; s < S; ++s) acc += x[(size_t)s * H + c];
+        y[c] = acc / (float)S;
+    }
+}
+// shaders/ops_conv.metal:60-74: src row r column 3c + j -> dst row row_off + r column j*H + c
+extern "C" void orc_qkv_split3(const float *src, float *dst, int rows, int H, int row_off) {
+    for (int r = 0; r < rows; ++r)
+        for (int c = 0; c < H; ++c)
+            for (int j = 0; j < 3; ++j)
+                dst[(size_t)(row_off + r) * 3 * H + (size_t)j * H + c] = src[(size_t)r * 3 * H + 3 * c + j];
+}
 // src/dit_fwd.cpp:111-119
 extern "C" void orc_timestep_embedding(float t, int D, float max_period, float *out) {
     const int half = D / 2;

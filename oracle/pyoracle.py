@@ -69,6 +69,11 @@ _SIGS = {
     "orc_add_bcast_col": [_P, _P, _P, _I, _I],
     "orc_cfg_euler": [_P, _P, _P, _SZ, _F, _F],
     "orc_timestep_embedding": [_F, _I, _F, _P],
+    "orc_geglu": [_P, _P, _P, _SZ],
+    "orc_gelu_quick": [_P, _SZ],
+    "orc_ln_plain": [_P, _P, _I, _I, _F],
+    "orc_mean_cols": [_P, _P, _I, _I],
+    "orc_qkv_split3": [_P, _P, _I, _I, _I],
     "orc_manifest_count": [ctypes.POINTER(OrcSpec)],
     "orc_manifest_numel": [ctypes.POINTER(OrcSpec), _I],
     "orc_manifest_total": [ctypes.POINTER(OrcSpec)],
@@ -253,6 +258,42 @@ def cfg_euler(fc, fu, x, cfg, dt):
     x = f32(x).copy()
     lib().orc_cfg_euler(p(f32(fc)), p(f32(fu)), p(x), x.size, cfg, dt)
     return x
+
+
+def geglu(a, b):
+    a, b = f32(a), f32(b)
+    y = np.empty_like(a)
+    lib().orc_geglu(p(a), p(b), p(y), a.size)
+    return y
+
+
+def gelu_quick(x):
+    x = f32(x).copy()
+    lib().orc_gelu_quick(p(x), x.size)
+    return x
+
+
+def ln_plain(x, eps=1e-5):
+    x = f32(x)
+    y = np.empty_like(x)
+    lib().orc_ln_plain(p(x), p(y), x.shape[0], x.shape[1], eps)
+    return y
+
+
+def mean_cols(x):
+    x = f32(x)
+    y = np.empty(x.shape[1], np.float32)
+    lib().orc_mean_cols(p(x), p(y), x.shape[0], x.shape[1])
+    return y
+
+
+def qkv_split3(src, dst, row_off):
+    """src [rows, 3H] element-interleaved -> copy of dst [., 3H] with rows row_off.. in q|k|v blocks"""
+    src = f32(src)
+    dst = f32(dst).copy()
+    rows, H3 = src.shape
+    lib().orc_qkv_split3(p(src), p(dst), rows, H3 // 3, row_off)
+    return dst
 
 
 def timestep_embedding(t, D, max_period=1.0):

@@ -214,3 +214,51 @@ def test_vae_spec_from_gguf(tsn, tmp_path):
     write(path, tensors)
     with pytest.raises(RuntimeError):
         tsn.vae_spec_from_gguf(path, T=11)
+
+
+def test_model_wrappers_check_array_sizes(tsn):
+    """DitModel / RefDitModel refuse device arrays shorter than the spec needs before calling the
+    library (a short buffer would otherwise be an out-of-bounds device access)"""
+    class Fake:
+        def __init__(self, n, itemsize=4):
+            self.nbytes, self.p = n * itemsize, None
+
+    spec = tsn.default_spec(1)
+    m = tsn.DitModel.__new__(tsn.DitModel)
+    m.spec, m.h = spec, None
+    B, La, Lt, H, L = spec.B, spec.La, spec.Lt, spec.H, spec.latent
+    ok = dict(z=Fake(B * La * L), text=Fake(B * Lt * H), pooled=Fake(B * H), v=Fake(B * La * L))
+    for k in ok:
+        bad = dict(ok, **{k: Fake(1)})
+        with pytest.raises(ValueError):
+            m.forward(bad["z"], 0.5, bad["text"], bad["pooled"], bad["v"])
+    with pytest.raises(ValueError):
+        m.sample(Fake(B * La * L // 2 - 1), ok["text"], ok["pooled"], 2, 5.0)
+    with pytest.raises(ValueError):
+        m.joint_block(0, Fake(B * (La + Lt) * H - 1), Fake(B * H))
+    with pytest.raises(TypeError):
+        m.forward(np.zeros(4), 0.5, ok["text"], ok["pooled"], ok["v"])
+    rs = tsn.ref_spec_for_duration(8, 2)
+    r = tsn.RefDitModel.__new__(tsn.RefDitModel)
+    r.spec, r.h = rs, None
+    good = dict(x=Fake(rs.B * rs.T * rs.latent), clip_pp=Fake(rs.B * rs.C * rs.H), text_pp=Fake(rs.B * rs.TS * rs.H),
+                gcmlp=Fake(rs.B * rs.H), sync_gather=Fake(rs.B * rs.T * rs.H), flow=Fake(rs.B * rs.T * rs.latent))
+    for k in good:
+        bad = dict(good, **{k: Fake(3)})
+        with pytest.raises(ValueError):
+            r.forward(bad["x"], 0.5, bad["clip_pp"], bad["text_pp"], bad["gcmlp"], bad["sync_gather"], bad["flow"])
+
+
+def test_sampler_fixture_inputs(tsn):
+    """tests/golden/sampler_8s_24steps.npz still describes what the generator produces (the GPU test
+    compares the 24-step sampler with it)"""
+    g = np.load(os.path.join(ROOT, "tests", "golden", "sampler_8s_24steps.npz"))
+    spec = tsn.default_spec(2)
+    seed, steps = (int(v) for v in g["seeds"])
+    inp = tsn.synth_inputs(spec, seed, cfg_pairs=True)
+    assert np.array_equal(inp["z"][0::2], g["x0"])
+    assert np.isclose(inp["text"].astype(np.float64).sum(), float(g["text_checksum"]), rtol=0, atol=1e-6)
+    assert np.isclose(inp["pooled"].astype(np.float64).sum(), float(g["pooled_checksum"]), rtol=0, atol=1e-9)
+    w = tsn.bf16_to_f32(tsn.synth_weights(spec, seed, float(g["norm_mean"])))
+    assert np.isclose(w.astype(np.float64).sum(), float(g["w_checksum"]), rtol=0, atol=1e-6)
+    assert steps == 24 and g["x"].shape == (1, spec.La, spec.latent) and np.isfinite(g["x"]).all()

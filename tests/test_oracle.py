@@ -393,3 +393,35 @@ def test_forward_taps_and_batch_independence(orc):
         ln = (x - x.mean(1, keepdims=True)) / np.sqrt(x.var(1, keepdims=True) + 1e-5)
         ref = (ln * (1 + mod[H:]) + mod[:H]) @ get("final_layer.linear.weight").reshape(8, H).T + get("final_layer.linear.bias")
         assert rel_l2(v[b], ref) < 1e-5
+
+
+def test_launcher_surface_ops(orc):
+    """The rest of the net.h surface, each against an independent library routine or a known answer:
+    geglu against torch's tanh-GELU (the clamp at |arg| = 10 changes tanh by < 5e-9), gelu_quick
+    against x·sigmoid(1.702 x), ln_plain against torch's layer_norm without affine (biased variance),
+    mean_cols against a float64 mean, and qkv_split3 on values that encode their own (row, channel,
+    part): a swapped part or a shifted channel is visible element by element."""
+    import torch
+    r = rng(41)
+    a = (3.0 * r.standard_normal(4099)).astype(np.float32)
+    a[:3] = [30.0, -30.0, 0.0]                               # deep in the clamp, and zero
+    b = r.standard_normal(4099).astype(np.float32)
+    ta = torch.from_numpy(a.astype(np.float64))
+    ref = torch.nn.functional.gelu(ta, approximate="tanh").numpy() * b
+    assert rel_l2(orc.geglu(a, b), ref) < 1e-6
+    assert rel_l2(orc.gelu_quick(a), (ta * torch.sigmoid(1.702 * ta)).numpy()) < 1e-6
+    x = (2.0 + r.standard_normal((37, 1000))).astype(np.float32)
+    ln = torch.nn.functional.layer_norm(torch.from_numpy(x.astype(np.float64)), (1000,), eps=1e-5).numpy()
+    assert rel_l2(orc.ln_plain(x, 1e-5), ln) < 1e-6
+    assert rel_l2(orc.mean_cols(x), x.astype(np.float64).mean(axis=0)) < 1e-6
+    rows, H, off = 5, 6, 2
+    src = np.zeros((rows, 3 * H), np.float32)
+    for rr in range(rows):
+        for c in range(H):
+            for j in range(3):
+                src[rr, 3 * c + j] = 1000 * rr + 10 * c + j
+    out = orc.qkv_split3(src, np.full((rows + 4, 3 * H), -1.0, np.float32), off)
+    assert (out[:off] == -1).all() and (out[off + rows:] == -1).all()
+    for j in range(3):
+        assert np.array_equal(out[off:off + rows, j * H:(j + 1) * H],
+                              1000 * np.arange(rows)[:, None] + 10 * np.arange(H)[None, :] + j)

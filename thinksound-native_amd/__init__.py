@@ -156,8 +156,16 @@ _SIGS = {
     "tsn_sync": [_P],
     "tsn_gemm": [_P, _I, _P, _P, _I, _P, _I, _P, _U32, _U32, _U32, _U32, _U32, _U32],
     "tsn_gemv": [_P, _P, _I, _P, _P, _P, _U32, _U32, _U32],
+    "tsn_conv1d_prepared_bytes": [_I, _U32, _U32, _U32],
     "tsn_conv1d_prepare": [_P, _P, _I, _P, _U32, _U32, _U32],
-    "tsn_conv1d": [_P, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _U32, _U32],
+    "tsn_conv1d": [_P, _I, _P, _P, _P, _P, _U32, _U32, _U32, _U32, _U32, _U32, _U32, _U32, _I],
+    "tsn_geglu": [_P, _P, _P, _P, _SZ],
+    "tsn_gelu_quick": [_P, _P, _SZ],
+    "tsn_ln_plain": [_P, _P, _P, _U32, _U32, _FL],
+    "tsn_ln_wb": [_P, _P, _P, _P, _P, _U32, _U32, _FL],
+    "tsn_rms_w": [_P, _P, _P, _P, _U32, _U32, _FL],
+    "tsn_mean_cols": [_P, _P, _P, _U32, _U32],
+    "tsn_qkv_split3": [_P, _P, _P, _U32, _U32, _U32],
     "tsn_silu": [_P, _P, _SZ],
     "tsn_copy": [_P, _P, _P, _SZ],
     "tsn_swiglu": [_P, _P, _P, _P, _SZ],
@@ -288,7 +296,7 @@ _RESTYPES = {"tsn_last_error": ctypes.c_char_p, "tsn_last_gpu_ms": ctypes.c_doub
              "tsn_gguf_get_i64": ctypes.c_int64, "tsn_gguf_get_f64": ctypes.c_double,
              "tsn_refcond_manifest_total": ctypes.c_int64, "tsn_version": _I,
              "tsn_vae_manifest_total": ctypes.c_int64, "tsn_vae_audio_len": ctypes.c_int64,
-             "tsn_clip_manifest_total": ctypes.c_int64, "tsn_t5_manifest_total": ctypes.c_int64, "tsn_t5_bucket": _I}
+             "tsn_clip_manifest_total": ctypes.c_int64, "tsn_conv1d_prepared_bytes": _SZ, "tsn_t5_manifest_total": ctypes.c_int64, "tsn_t5_bucket": _I}
 
 
 def lib():
@@ -857,12 +865,37 @@ class Runtime:
     def gemv(self, W, wdtype, x, y, bias, N, K, ldw=0):
         call("tsn_gemv", self.h, W.p, wdtype, x.p, y.p, bias.p if bias is not None else None, N, K, ldw)
 
-    def conv1d_prepare(self, W, w_bf16, Wp, OC, IC, K):
-        call("tsn_conv1d_prepare", self.h, W.p, int(w_bf16), Wp.p, OC, IC, K)
+    @staticmethod
+    def conv1d_prepared_bytes(wdtype, OC, IC, K):
+        return int(lib().tsn_conv1d_prepared_bytes(wdtype, OC, IC, K))
 
-    def conv1d(self, Wp, bias, x, y, T, OL, IC, OC, K, stride, pad, dil):
-        call("tsn_conv1d", self.h, Wp.p, bias.p if bias is not None else None, x.p, y.p, T, OL, IC, OC, K,
-             stride, pad, dil)
+    def conv1d_prepare(self, W, wdtype, Wp, OC, IC, K):
+        call("tsn_conv1d_prepare", self.h, W.p, int(wdtype), Wp.p, OC, IC, K)
+
+    def conv1d(self, wdtype, Wp, bias, x, y, T, OL, IC, OC, K, stride, pad, dil, convt=False):
+        call("tsn_conv1d", self.h, int(wdtype), Wp.p, bias.p if bias is not None else None, x.p, y.p, T, OL, IC,
+             OC, K, stride, pad, dil, int(bool(convt)))
+
+    def geglu(self, a, b, y, n):
+        call("tsn_geglu", self.h, a.p, b.p, y.p, n)
+
+    def gelu_quick(self, x, n):
+        call("tsn_gelu_quick", self.h, x.p, n)
+
+    def ln_plain(self, x, y, S, H, eps):
+        call("tsn_ln_plain", self.h, x.p, y.p, S, H, eps)
+
+    def ln_wb(self, x, y, w, b, S, H, eps):
+        call("tsn_ln_wb", self.h, x.p, y.p, w.p, b.p, S, H, eps)
+
+    def rms_w(self, x, y, w, S, H, eps):
+        call("tsn_rms_w", self.h, x.p, y.p, w.p, S, H, eps)
+
+    def mean_cols(self, x, y, S, H):
+        call("tsn_mean_cols", self.h, x.p, y.p, S, H)
+
+    def qkv_split3(self, src, dst, rows, H, row_off):
+        call("tsn_qkv_split3", self.h, src.p, dst.p, rows, H, row_off)
 
     def adaln_ln(self, x, mod, y, ydtype, rows, H, per_row, chunks, base, eps):
         call("tsn_adaln_ln", self.h, x.p, mod.p, y.p, ydtype, rows, H, per_row, chunks, base, eps)
@@ -905,6 +938,20 @@ class Runtime:
         return t.value, g.value
 
 
+def _need(what, arr, numel, itemsize=4, optional=False):
+    """A device array must hold at least numel elements of itemsize bytes: a short buffer would
+    otherwise become an out-of-bounds device access instead of an error."""
+    if arr is None:
+        if optional:
+            return
+        raise ValueError("%s: a device array is required" % what)
+    have = getattr(arr, "nbytes", None)
+    if have is None or not hasattr(arr, "p"):
+        raise TypeError("%s: expected a DeviceArray, got %r" % (what, type(arr)))
+    if have < numel * itemsize:
+        raise ValueError("%s: %d bytes needed, the array holds %d" % (what, numel * itemsize, have))
+
+
 class DitModel:
     """tn::DitModel mirror (src/models.h:55-85) for the batched two-stream graph."""
 
@@ -923,33 +970,60 @@ class DitModel:
         w_bf16 = np.ascontiguousarray(w_bf16, dtype=np.uint16)
         call("tsn_dit_upload_weights", self.h, ptr(w_bf16), w_bf16.size)
 
+    def _io(self, z=None, t_dev=None, text=None, pooled=None, v=None, taps=None, x=None, X=None, g=None):
+        s = self.spec
+        S = s.La + s.Lt
+        if z is not None or v is not None:
+            _need("dit z", z, s.B * s.La * s.latent)
+            _need("dit v", v, s.B * s.La * s.latent)
+            _need("dit pooled", pooled, s.B * s.H)
+            _need("dit text", text, s.B * s.Lt * s.H, optional=s.Lt == 0)
+        if t_dev is not None:
+            _need("dit t", t_dev, s.B)
+        _need("dit taps", taps, (s.n_joint + s.n_fused) * s.B * S * s.H, optional=True)
+        if x is not None:
+            _need("dit x", x, (s.B // 2) * s.La * s.latent)
+            _need("dit pooled", pooled, s.B * s.H)
+            _need("dit text", text, s.B * s.Lt * s.H, optional=s.Lt == 0)
+        if X is not None:
+            _need("dit X", X, s.B * S * s.H)
+            _need("dit g", g, s.B * s.H)
+
     def forward(self, z, t, text, pooled, v):
+        self._io(z=z, text=text, pooled=pooled, v=v)
         call("tsn_dit_forward", self.h, z.p, float(t), text.p if text is not None else None, pooled.p, v.p)
 
     def forward_ex(self, z, t_dev, text, pooled, v, taps=None):
+        self._io(z=z, t_dev=t_dev, text=text, pooled=pooled, v=v, taps=taps)
         call("tsn_dit_forward_ex", self.h, z.p, t_dev.p, text.p if text is not None else None, pooled.p, v.p,
              taps.p if taps is not None else None)
 
     def joint_block(self, block, X, g):
+        self._io(X=X, g=g)
         call("tsn_dit_joint_block", self.h, block, X.p, g.p)
 
     def fused_block(self, block, X, g):
+        self._io(X=X, g=g)
         call("tsn_dit_fused_block", self.h, block, X.p, g.p)
 
     def sample(self, x, text, pooled, steps, cfg):
-        call("tsn_dit_sample", self.h, x.p, text.p, pooled.p, steps, cfg)
+        self._io(x=x, text=text, pooled=pooled)
+        call("tsn_dit_sample", self.h, x.p, _p(text), pooled.p, steps, cfg)
 
     def capture_forward(self, z, t_dev, text, pooled, v):
-        call("tsn_dit_capture_forward", self.h, z.p, t_dev.p, text.p, pooled.p, v.p)
+        self._io(z=z, t_dev=t_dev, text=text, pooled=pooled, v=v)
+        call("tsn_dit_capture_forward", self.h, z.p, t_dev.p, _p(text), pooled.p, v.p)
 
     def capture_sample(self, x, text, pooled, steps, cfg):
-        call("tsn_dit_capture_sample", self.h, x.p, text.p, pooled.p, steps, cfg)
+        self._io(x=x, text=text, pooled=pooled)
+        call("tsn_dit_capture_sample", self.h, x.p, _p(text), pooled.p, steps, cfg)
 
     def replay(self):
         call("tsn_dit_replay", self.h)
 
     def profile_forward(self, z, t_dev, text, pooled, v):
         """Per-kernel stats of one eager evaluation: list of dicts (name, launches, ms, flops, bytes)."""
+        self._io(z=z, t_dev=t_dev, text=text, pooled=pooled, v=v)
         cap = 64
         arr = (KernelStat * cap)()
         n = ctypes.c_int()
@@ -987,27 +1061,45 @@ class RefDitModel:
     def load_gguf(self, path):
         call("tsn_refdit_load_gguf", self.h, os.fsencode(path))
 
+    def _io(self, x, clip_pp, text_pp, gcmlp, sync_gather, flow=None, t_dev=None, taps=None, sampler=False):
+        s = self.spec
+        rows = s.B // 2 if sampler else s.B
+        _need("refdit x", x, rows * s.T * s.latent)
+        _need("refdit flow", flow, s.B * s.T * s.latent, optional=sampler)
+        _need("refdit t", t_dev, s.B, optional=True)
+        _need("refdit clip_pp", clip_pp, s.B * s.C * s.H, optional=s.C == 0)
+        _need("refdit text_pp", text_pp, s.B * s.TS * s.H, optional=s.TS == 0)
+        _need("refdit gcmlp", gcmlp, s.B * s.H)
+        _need("refdit sync_gather", sync_gather, s.B * s.T * s.H)
+        _need("refdit taps", taps, (s.n_joint + s.n_fused) * s.B * (s.T + s.C + s.TS) * s.H, optional=True)
+
     def forward(self, x, t, clip_pp, text_pp, gcmlp, sync_gather, flow):
+        self._io(x, clip_pp, text_pp, gcmlp, sync_gather, flow)
         call("tsn_refdit_forward", self.h, x.p, float(t), _p(clip_pp), _p(text_pp), gcmlp.p, sync_gather.p, flow.p)
 
     def forward_ex(self, x, t_dev, clip_pp, text_pp, gcmlp, sync_gather, flow, taps=None):
+        self._io(x, clip_pp, text_pp, gcmlp, sync_gather, flow, t_dev, taps)
         call("tsn_refdit_forward_ex", self.h, x.p, t_dev.p, _p(clip_pp), _p(text_pp), gcmlp.p, sync_gather.p,
              flow.p, _p(taps))
 
     def sample(self, x, clip_pp, text_pp, gcmlp, sync_gather, steps, cfg):
+        self._io(x, clip_pp, text_pp, gcmlp, sync_gather, sampler=True)
         call("tsn_refdit_sample", self.h, x.p, _p(clip_pp), _p(text_pp), gcmlp.p, sync_gather.p, steps, cfg)
 
     def capture_forward(self, x, t_dev, clip_pp, text_pp, gcmlp, sync_gather, flow):
+        self._io(x, clip_pp, text_pp, gcmlp, sync_gather, flow, t_dev)
         call("tsn_refdit_capture_forward", self.h, x.p, t_dev.p, _p(clip_pp), _p(text_pp), gcmlp.p,
              sync_gather.p, flow.p)
 
     def capture_sample(self, x, clip_pp, text_pp, gcmlp, sync_gather, steps, cfg):
+        self._io(x, clip_pp, text_pp, gcmlp, sync_gather, sampler=True)
         call("tsn_refdit_capture_sample", self.h, x.p, _p(clip_pp), _p(text_pp), gcmlp.p, sync_gather.p, steps, cfg)
 
     def replay(self):
         call("tsn_refdit_replay", self.h)
 
     def profile_forward(self, x, t_dev, clip_pp, text_pp, gcmlp, sync_gather, flow):
+        self._io(x, clip_pp, text_pp, gcmlp, sync_gather, flow, t_dev)
         cap = 64
         arr = (KernelStat * cap)()
         n = ctypes.c_int()

@@ -169,14 +169,19 @@ int tsn_gemv(tsn_runtime *rt, const void *W, int wdtype, const float *x, float *
     RT_CHECK(rt);
     return rt->rt.gemv(W, x, y, bias, N, K, ldw, wdtype);
 }
-int tsn_conv1d_prepare(tsn_runtime *rt, const void *W, int w_bf16, void *Wp, uint32_t OC, uint32_t IC, uint32_t K) {
-    RT_CHECK(rt);
-    return rt->rt.conv_prepare(W, w_bf16, Wp, OC, IC, K);
+size_t tsn_conv1d_prepared_bytes(int wdtype, uint32_t OC, uint32_t IC, uint32_t K) {
+    if (wdtype != TSN_F32 && wdtype != TSN_F16 && wdtype != TSN_BF16) return 0;
+    return (size_t)OC * (size_t)tsn::conv_prep_cols(wdtype, (int)IC, (int)K) * sizeof(tsn::half_t);
 }
-int tsn_conv1d(tsn_runtime *rt, const void *Wp, const float *bias, const float *x, float *y, uint32_t T, uint32_t OL,
-               uint32_t IC, uint32_t OC, uint32_t K, uint32_t stride, uint32_t pad, uint32_t dil) {
+int tsn_conv1d_prepare(tsn_runtime *rt, const void *W, int wdtype, void *Wp, uint32_t OC, uint32_t IC, uint32_t K) {
     RT_CHECK(rt);
-    return rt->rt.conv(Wp, bias, x, y, T, OL, IC, OC, K, stride, pad, dil);
+    return rt->rt.conv_prepare(W, wdtype, Wp, OC, IC, K);
+}
+int tsn_conv1d(tsn_runtime *rt, int wdtype, const void *Wp, const float *bias, const float *x, float *y, uint32_t T,
+               uint32_t OL, uint32_t IC, uint32_t OC, uint32_t K, uint32_t stride, uint32_t pad, uint32_t dil,
+               int convt) {
+    RT_CHECK(rt);
+    return rt->rt.conv(wdtype, Wp, bias, x, y, T, OL, IC, OC, K, stride, pad, dil, convt ? 1u : 0u);
 }
 int tsn_silu(tsn_runtime *rt, float *x, size_t n) { RT_CHECK(rt); return rt->rt.silu(x, n); }
 int tsn_copy(tsn_runtime *rt, const float *x, float *y, size_t n) { RT_CHECK(rt); return rt->rt.copy(x, y, n); }
@@ -189,6 +194,29 @@ int tsn_add_bcast_col(tsn_runtime *rt, const float *x, const float *v, float *y,
 int tsn_cfg_euler(tsn_runtime *rt, const float *fc, const float *fu, float *x, size_t n, float cfg, float dt) {
     RT_CHECK(rt);
     return rt->rt.cfg_euler(fc, fu, x, n, cfg, dt);
+}
+int tsn_geglu(tsn_runtime *rt, const float *a, const float *b, float *y, size_t n) { RT_CHECK(rt); return rt->rt.geglu(a, b, y, n); }
+int tsn_gelu_quick(tsn_runtime *rt, float *x, size_t n) { RT_CHECK(rt); return rt->rt.gelu_quick(x, n); }
+int tsn_ln_plain(tsn_runtime *rt, const float *x, float *y, uint32_t S, uint32_t H, float eps) {
+    RT_CHECK(rt);
+    return rt->rt.ln_plain(x, y, S, H, eps);
+}
+int tsn_ln_wb(tsn_runtime *rt, const float *x, float *y, const float *w, const float *b, uint32_t S, uint32_t H,
+              float eps) {
+    RT_CHECK(rt);
+    return rt->rt.ln_wb(x, y, w, b, S, H, eps);
+}
+int tsn_rms_w(tsn_runtime *rt, const float *x, float *y, const float *w, uint32_t S, uint32_t H, float eps) {
+    RT_CHECK(rt);
+    return rt->rt.rms_w(x, y, w, S, H, eps);
+}
+int tsn_mean_cols(tsn_runtime *rt, const float *x, float *y, uint32_t S, uint32_t H) {
+    RT_CHECK(rt);
+    return rt->rt.mean_cols(x, y, S, H);
+}
+int tsn_qkv_split3(tsn_runtime *rt, const float *src, float *dst, uint32_t rows, uint32_t H, uint32_t row_off) {
+    RT_CHECK(rt);
+    return rt->rt.qkv_split3(src, dst, rows, H, row_off);
 }
 int tsn_adaln_ln(tsn_runtime *rt, const float *x, const float *mod, void *y, int ydtype, uint32_t rows, uint32_t H,
                  uint32_t per_row, uint32_t chunks, uint32_t base, float eps) {

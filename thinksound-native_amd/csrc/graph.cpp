@@ -21,16 +21,22 @@ int GraphRunner::alloc(size_t bytes, void **p) {
 int GraphRunner::release(void *p) {
     for (auto it = owned_.begin(); it != owned_.end(); ++it)
         if (*it == p) {
+            // a captured graph may hold this buffer's address: it is no longer replayable
+            drop_graph();
             owned_.erase(it);
             return rt->dev.free(p);
         }
     TSN_REQUIRE(false, "release: not an allocation of this model");
 }
 
-int GraphRunner::capture(const std::function<int()> &enqueue) {
-    TSN_TRY(rt->dev.make_current());
+void GraphRunner::drop_graph() {
     if (gexec_) { hipGraphExecDestroy(gexec_); gexec_ = nullptr; }
     if (graph_) { hipGraphDestroy(graph_); graph_ = nullptr; }
+}
+
+int GraphRunner::capture(const std::function<int()> &enqueue) {
+    TSN_TRY(rt->dev.make_current());
+    drop_graph();
     const hipStream_t st = rt->dev.stream();
     TSN_HIP_CHECK(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
     const int rc = enqueue();
@@ -44,7 +50,10 @@ int GraphRunner::capture(const std::function<int()> &enqueue) {
 }
 
 int GraphRunner::replay() {
-    TSN_REQUIRE(gexec_, "no captured graph");
+    if (!gexec_) {
+        set_error("no captured graph (none was captured, or a buffer it used has been reallocated since)");
+        return TSN_ERR_STATE;
+    }
     TSN_TRY(rt->dev.make_current());
     TSN_HIP_CHECK(hipGraphLaunch(gexec_, rt->dev.stream()));
     return TSN_OK;

@@ -57,7 +57,9 @@ protected:
     hipGraphExec_t gexec_ = nullptr;
 
     int alloc(size_t bytes, void **p);   // zero-filled, freed with the runner
-    int release(void *p);                // frees one allocation made by alloc()
+    // frees one allocation made by alloc(); drops the captured graph, which may address it
+    int release(void *p);
+    void drop_graph();
     // launch() under the profiler when profiling (one record per launched kernel)
     template <typename F>
     int run(const char *name, double flops, double bytes, F &&launch) {

@@ -275,6 +275,33 @@ int launch_gather_rows(const float *src, const int32_t *idx, float *dst, int row
 // out[c] = mean over rows of x[r][c], rows summed in order (src/net.mm Runtime::mean_cols)
 int launch_mean_rows(const float *x, int rows, int H, float *out, hipStream_t st);
 
+/* ------------------------------------------------------------------ net.h conv surface (netops.hip) */
+// Geometry of Runtime::conv (src/net.h:29-34): x [T][IC] rows of stride ldx -> y [OL][OC].
+struct ConvGeom {
+    int T, OL, IC, OC, K, stride, pad, dil, convt, ldx;
+};
+// Columns of a prepared conv weight row: K*IC (f16/bf16 source) or 3*K*IC (f32 source, three
+// parts per tap) rounded up to a multiple of 64.
+int conv_prep_cols(int sdt, int IC, int K);
+// W [OC][IC][K] (sdt f16, bf16 or f32) -> Wp [OC][conv_prep_cols] f16, tap-major, zero padded:
+// f16/bf16 sources one channel per column (bf16 with the reference upload's rounding), f32
+// sources [hi | hi | lo] of each tap's channels (the weight of a three-part product)
+int launch_conv_prepare(const void *W, int sdt, half_t *Wp, int OC, int IC, int K, hipStream_t st);
+// gathered operand rows [t0, t0 + rows) of the conv (the reference's im2col, src/net.mm:36-48):
+// parts 1 -> [rows][2*Kp] f16 hi|lo halves; parts 3 -> [rows][Kp] with [hi | lo | hi] per tap
+int launch_conv_gather(const float *x, const ConvGeom &g, int t0, int rows, int parts, int Kp, half_t *out,
+                       hipStream_t st);
+// direct f32 conv on a prepared weight (outputs too narrow for a GEMM tile)
+int launch_conv_direct(const float *x, const ConvGeom &g, const half_t *Wp, int parts, int Kp, const float *bias,
+                       float *y, hipStream_t st);
+// LayerNorm without affine, rows of H floats (shaders/ops_conv.metal:77-89)
+int launch_ln_plain(const float *x, float *y, int S, int H, float eps, hipStream_t st);
+// y = gelu_tanh(a) * b (shaders/ops_conv.metal:15-24); x = gelu_quick(x) (:25-29)
+int launch_geglu(const float *a, const float *b, float *y, size_t n, hipStream_t st);
+int launch_gelu_quick(float *x, size_t n, hipStream_t st);
+// element-interleaved qkv rows [rows][3H] -> block q|k|v rows [row_off + r][3H] (shaders/ops_conv.metal:60-74)
+int launch_qkv_split3(const float *src, float *dst, int rows, int H, int row_off, hipStream_t st);
+
 // reference-surface elementwise ops (f32)
 int launch_silu(float *x, size_t n, hipStream_t st);
 int launch_copy(const float *x, float *y, size_t n, hipStream_t st);

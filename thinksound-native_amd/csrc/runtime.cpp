@@ -145,35 +145,83 @@ int Runtime::scratch(size_t bytes, void **p) {
     return TSN_OK;
 }
 
+namespace {
+bool aligned16(const void *p) { return (((uintptr_t)p) & 15) == 0; }
+}
+
+bool gemm_hilo_ok(const void *W, uint32_t ldw, const void *Y, int ydt, uint32_t ldy, const float *bias,
+                  uint32_t M, uint32_t N, uint32_t K) {
+    // what the pipelined kernel takes for a hi|lo operand (gemm_plan): K a multiple of 64, 8-aligned
+    // strides, 16-byte aligned W, bias and Y, operand offsets below 2^31 bytes
+    return M > 0 && N > 0 && K > 0 && K % 64 == 0 && ldw % 8 == 0 && ldw >= K && N % 8 == 0 && aligned16(W) &&
+           aligned16(bias) && aligned16(Y) && ldy >= N && ldy % (ydt == DT_F16 ? 8 : 4) == 0 &&
+           (unsigned long long)N * ldw * 2 < (1ULL << 31) && 4ULL * M * K * 2 < (1ULL << 31);
+}
+
+size_t gemm_hilo_bytes(uint32_t M, uint32_t K) { return (size_t)M * 2 * K * sizeof(half_t); }
+
+int gemm_hilo(const half_t *W, uint32_t ldw, const float *X, uint32_t ldx, void *Y, int ydt, uint32_t ldy,
+              const float *bias, uint32_t M, uint32_t N, uint32_t K, half_t *hl, hipStream_t st) {
+    TSN_REQUIRE(W && X && Y && hl && aligned16(hl), "gemm: null operand or unaligned operand buffer");
+    TSN_REQUIRE(ydt == DT_F32 || ydt == DT_F16, "gemm: Y must be f32 or f16");
+    TSN_REQUIRE(gemm_hilo_ok(W, ldw, Y, ydt, ldy, bias, M, N, K), "gemm: shape outside the hi|lo MFMA path");
+    TSN_TRY(launch_split_hilo(X, (int)ldx, rowmap_dense((int)M), hl, (int)M, (int)K, st));
+    GemmBatch b;
+    gemm_problem_init(b.p[0]);
+    GemmProblem &q = b.p[0];
+    q.A = hl; q.lda = (int)(2 * K); q.amap = rowmap_dense((int)M);
+    q.taps = 1; q.Kc = (int)(2 * K); q.pad = 0; q.a_T = (int)M;
+    q.W = W; q.ldw = (int)ldw; q.w_half = 1; q.bias = bias;
+    q.M = (int)M; q.N = (int)N; q.K = (int)(2 * K);
+    q.Y = Y; q.ldy = (int)ldy; q.ymap = rowmap_dense((int)M); q.y_f16 = ydt == DT_F16;
+    b.nprob = 1;
+    return launch_gemm(b, EPI_STORE, false, st);
+}
+
 int Runtime::gemm(int wdt, const void *W, const void *X, int xdt, void *Y, int ydt, const float *bias,
                   const GemmParams &p) {
     TSN_REQUIRE(W && X && Y, "gemm: null operand");
     TSN_REQUIRE(p.M > 0 && p.N > 0 && p.K > 0, "gemm: empty shape");
-    const int ldx = p.ldx ? (int)p.ldx : (int)p.K, ldw = p.ldw ? (int)p.ldw : (int)p.K;
-    const int ldy = p.ldy ? (int)p.ldy : (int)p.N;
+    const uint32_t ldx = p.ldx ? p.ldx : p.K, ldw = p.ldw ? p.ldw : p.K, ldy = p.ldy ? p.ldy : p.N;
+    TSN_REQUIRE(ldx >= p.K && ldw >= p.K && ldy >= p.N, "gemm: leading dimension below the row width");
     TSN_TRY(dev.make_current());
-    if (wdt == DT_F16) {
-        TSN_REQUIRE(xdt == DT_F32 || xdt == DT_F16, "gemm: X must be f32 or f16");
+    const hipStream_t st = dev.stream();
+    if (wdt == DT_F16 && xdt == DT_F32) {
+        // the reference's f32-activation contract (shaders/gemm_mpp.metal:19-25: X stays f32)
+        if (gemm_hilo_ok(W, ldw, Y, ydt, ldy, bias, p.M, p.N, p.K)) {
+            void *hl = nullptr;
+            TSN_TRY(scratch(gemm_hilo_bytes(p.M, p.K), &hl));
+            return gemm_hilo((const half_t *)W, ldw, (const float *)X, ldx, Y, ydt, ldy, bias, p.M, p.N, p.K,
+                             (half_t *)hl, st);
+        }
+        if (ydt != DT_F32) {
+            set_error("gemm: f32 X with f16 Y needs K % 64 == 0, N % 8 == 0 and 16-byte aligned W, bias and Y");
+            return TSN_ERR_UNSUPPORTED;
+        }
+        // shapes outside the MFMA tiling: exact f32 products on the SIMT path
+    } else if (wdt == DT_F16) {
+        TSN_REQUIRE(xdt == DT_F16, "gemm: X must be f32 or f16");
         TSN_REQUIRE(ydt == DT_F32 || ydt == DT_F16, "gemm: Y must be f32 or f16");
         GemmBatch b;
         gemm_problem_init(b.p[0]);
         GemmProblem &q = b.p[0];
-        q.A = X; q.lda = ldx; q.amap = rowmap_dense((int)p.M);
+        q.A = X; q.lda = (int)ldx; q.amap = rowmap_dense((int)p.M);
         q.taps = 1; q.Kc = (int)p.K; q.pad = 0; q.a_T = (int)p.M;
-        q.W = (const half_t *)W; q.ldw = ldw; q.bias = bias;
+        q.W = (const half_t *)W; q.ldw = (int)ldw; q.bias = bias;
         q.M = (int)p.M; q.N = (int)p.N; q.K = (int)p.K;
-        q.Y = Y; q.ldy = ldy; q.ymap = rowmap_dense((int)p.M); q.y_f16 = ydt == DT_F16;
+        q.Y = Y; q.ldy = (int)ldy; q.ymap = rowmap_dense((int)p.M); q.y_f16 = ydt == DT_F16;
         b.nprob = 1;
-        return launch_gemm(b, EPI_STORE, xdt == DT_F32, dev.stream());
+        return launch_gemm(b, EPI_STORE, false, st);
+    } else {
+        TSN_REQUIRE(wdt == DT_F32 || wdt == DT_BF16, "gemm: weight dtype");
+        TSN_REQUIRE(xdt == DT_F32 && ydt == DT_F32, "gemm: f32/bf16 weights take f32 X and Y");
     }
-    TSN_REQUIRE(wdt == DT_F32 || wdt == DT_BF16, "gemm: weight dtype");
-    TSN_REQUIRE(xdt == DT_F32 && ydt == DT_F32, "gemm: f32/bf16 weights take f32 X and Y");
     LinArgs a;
-    a.X = (const float *)X; a.ldx = ldx; a.xmap = rowmap_dense((int)p.M);
-    a.W = W; a.ldw = ldw; a.wdt = wdt; a.bias = bias;
-    a.Y = (float *)Y; a.ldy = ldy; a.ymap = rowmap_dense((int)p.M);
+    a.X = (const float *)X; a.ldx = (int)ldx; a.xmap = rowmap_dense((int)p.M);
+    a.W = W; a.ldw = (int)ldw; a.wdt = wdt; a.bias = bias;
+    a.Y = (float *)Y; a.ldy = (int)ldy; a.ymap = rowmap_dense((int)p.M);
     a.M = (int)p.M; a.N = (int)p.N; a.K = (int)p.K;
-    return launch_linear_f32(a, dev.stream());
+    return launch_linear_f32(a, st);
 }
 
 int Runtime::gemv(const void *W, const float *X, float *Y, const float *bias, uint32_t N, uint32_t K,
@@ -187,31 +235,69 @@ int Runtime::gemv(const void *W, const float *X, float *Y, const float *bias, ui
     return launch_gemv(a, dev.stream());
 }
 
-int Runtime::conv_prepare(const void *W, int w_bf16, void *Wp, uint32_t OC, uint32_t IC, uint32_t K) {
+int Runtime::conv_prepare(const void *W, int wdt, void *Wp, uint32_t OC, uint32_t IC, uint32_t K) {
     TSN_TRY(dev.make_current());
-    return launch_conv_weight_reorder(W, w_bf16, (half_t *)Wp, (int)OC, (int)IC, (int)K, dev.stream());
+    return launch_conv_prepare(W, wdt, (half_t *)Wp, (int)OC, (int)IC, (int)K, dev.stream());
 }
 
-int Runtime::conv(const void *Wp, const float *bias, const float *x, float *y, uint32_t T, uint32_t OL,
-                  uint32_t IC, uint32_t OC, uint32_t K, uint32_t stride, uint32_t pad, uint32_t dil) {
+// Three routes, all f32-accurate (f16 weights: x as hi|lo against [W | W]; f32 weights: three-part
+// products against [W_hi | W_hi | W_lo]):
+//   * stride 1, dilation 1, IC % 64 == 0: implicit GEMM over the split input, taps in K (no im2col);
+//   * other strides, dilations, transposed convs and channel counts: the gathered operand (the
+//     reference's im2col, src/net.mm:36-48) in chunks of at most 64 MB, one GEMM per chunk;
+//   * outputs too narrow for a GEMM tile (OC % 8 != 0) or unaligned: a direct f32 conv.
+int Runtime::conv(int wdt, const void *Wp, const float *bias, const float *x, float *y, uint32_t T, uint32_t OL,
+                  uint32_t IC, uint32_t OC, uint32_t K, uint32_t stride, uint32_t pad, uint32_t dil, uint32_t convt) {
     TSN_REQUIRE(Wp && x && y, "conv: null operand");
-    if (stride != 1 || dil != 1) {
-        set_error("conv: only stride 1, dilation 1 (the DiT convs) are implemented");
-        return TSN_ERR_UNSUPPORTED;
-    }
-    TSN_REQUIRE((int)OL == (int)T + 2 * (int)pad - (int)K + 1, "conv: OL must equal T + 2*pad - K + 1");
-    TSN_REQUIRE(K == 1 || IC % 64 == 0, "conv: IC must be a multiple of 64 for K > 1");
+    TSN_REQUIRE(wdt == DT_F16 || wdt == DT_BF16 || wdt == DT_F32, "conv: weight dtype f16, bf16 or f32");
+    TSN_REQUIRE(T > 0 && OL > 0 && IC > 0 && OC > 0 && K > 0 && stride > 0 && dil > 0,
+                "conv: empty shape, or zero stride or dilation");
+    TSN_REQUIRE((unsigned long long)OL * OC < (1ULL << 31) && (unsigned long long)T * IC < (1ULL << 31) &&
+                    (unsigned long long)K * IC * 3 < (1ULL << 30) && pad < (1u << 30),
+                "conv: sizes beyond 32-bit indexing");
     TSN_TRY(dev.make_current());
+    const hipStream_t st = dev.stream();
+    const int parts = wdt == DT_F32 ? 3 : 1;
+    const int Kp = conv_prep_cols(wdt, (int)IC, (int)K);
+    const ConvGeom g{(int)T, (int)OL, (int)IC, (int)OC, (int)K, (int)stride, (int)pad, (int)dil, convt ? 1 : 0,
+                     (int)IC};
+    if (OC % 8 != 0 || !aligned16(y) || !aligned16(bias) || !aligned16(Wp) ||
+        (unsigned long long)OC * Kp * 2 >= (1ULL << 31))
+        return launch_conv_direct(x, g, (const half_t *)Wp, parts, Kp, bias, y, st);
     GemmBatch b;
     gemm_problem_init(b.p[0]);
     GemmProblem &q = b.p[0];
-    q.A = x; q.lda = (int)IC; q.amap = rowmap_dense((int)OL);
-    q.taps = (int)K; q.Kc = (int)IC; q.pad = (int)pad; q.a_T = (int)T;
-    q.W = (const half_t *)Wp; q.ldw = (int)(IC * K); q.bias = bias;
-    q.M = (int)OL; q.N = (int)OC; q.K = (int)(IC * K);
-    q.Y = y; q.ldy = (int)OC; q.ymap = rowmap_dense((int)OL); q.y_f16 = 0;
+    q.W = (const half_t *)Wp; q.ldw = Kp; q.bias = bias; q.w_half = parts == 1;
+    q.N = (int)OC; q.ldy = (int)OC; q.y_f16 = 0;
     b.nprob = 1;
-    return launch_gemm(b, EPI_STORE, true, dev.stream());
+    const int ich = (int)IC * (parts == 1 ? 2 : 3);   // split input row: [hi | lo] or [hi | lo | hi]
+    if (stride == 1 && dil == 1 && !convt && IC % 64 == 0 && aligned16(x) &&
+        2ULL * (OL + T) * ich * 2 < (1ULL << 31)) {
+        void *buf = nullptr;
+        TSN_TRY(scratch((size_t)T * ich * sizeof(half_t), &buf));
+        if (parts == 1) TSN_TRY(launch_split_hilo(x, (int)IC, rowmap_dense((int)T), (half_t *)buf, (int)T, (int)IC, st));
+        else TSN_TRY(launch_split3(x, (long long)T, (int)IC, nullptr, 1, (half_t *)buf, st));
+        q.A = buf; q.lda = ich; q.amap = rowmap_dense((int)OL);
+        q.taps = (int)K; q.Kc = ich; q.pad = (int)pad; q.a_T = (int)T;
+        q.M = (int)OL; q.K = (int)K * ich;
+        q.Y = y; q.ymap = rowmap_dense((int)OL);
+        return launch_gemm(b, EPI_STORE, false, st);
+    }
+    const int width = parts == 1 ? 2 * Kp : Kp;
+    const size_t row_bytes = (size_t)width * sizeof(half_t);
+    const uint32_t rows = (uint32_t)std::max<size_t>(1, std::min<size_t>(OL, ((size_t)64 << 20) / row_bytes));
+    void *buf = nullptr;
+    TSN_TRY(scratch((size_t)rows * row_bytes, &buf));
+    for (uint32_t t0 = 0; t0 < OL; t0 += rows) {
+        const uint32_t n = std::min(rows, OL - t0);
+        TSN_TRY(launch_conv_gather(x, g, (int)t0, (int)n, parts, Kp, (half_t *)buf, st));
+        q.A = buf; q.lda = width; q.amap = rowmap_dense((int)n);
+        q.taps = 1; q.Kc = width; q.pad = 0; q.a_T = (int)n;
+        q.M = (int)n; q.K = width;
+        q.Y = y + (size_t)t0 * OC; q.ymap = rowmap_dense((int)n);
+        TSN_TRY(launch_gemm(b, EPI_STORE, false, st));
+    }
+    return TSN_OK;
 }
 
 int Runtime::silu(float *x, size_t n) { TSN_TRY(dev.make_current()); return launch_silu(x, n, dev.stream()); }
@@ -231,6 +317,37 @@ int Runtime::add_bcast_col(const float *x, const float *v, float *y, uint32_t S,
 int Runtime::cfg_euler(const float *fc, const float *fu, float *x, size_t n, float cfg, float dt) {
     TSN_TRY(dev.make_current());
     return launch_cfg_euler(fc, fu, x, n, cfg, dt, dev.stream());
+}
+
+int Runtime::geglu(const float *a, const float *b, float *y, size_t n) {
+    TSN_TRY(dev.make_current());
+    return launch_geglu(a, b, y, n, dev.stream());
+}
+int Runtime::gelu_quick(float *x, size_t n) {
+    TSN_TRY(dev.make_current());
+    return launch_gelu_quick(x, n, dev.stream());
+}
+int Runtime::ln_plain(const float *x, float *y, uint32_t S, uint32_t H, float eps) {
+    TSN_TRY(dev.make_current());
+    return launch_ln_plain(x, y, (int)S, (int)H, eps, dev.stream());
+}
+int Runtime::ln_wb(const float *x, float *y, const float *w, const float *b, uint32_t S, uint32_t H, float eps) {
+    TSN_REQUIRE(b, "ln_wb: null bias");
+    TSN_TRY(dev.make_current());
+    return launch_enc_norm(x, y, w, b, (int)S, (int)H, eps, true, dev.stream());
+}
+int Runtime::rms_w(const float *x, float *y, const float *w, uint32_t S, uint32_t H, float eps) {
+    TSN_TRY(dev.make_current());
+    return launch_enc_norm(x, y, w, nullptr, (int)S, (int)H, eps, false, dev.stream());
+}
+int Runtime::mean_cols(const float *x, float *y, uint32_t S, uint32_t H) {
+    TSN_TRY(dev.make_current());
+    return launch_mean_rows(x, (int)S, (int)H, y, dev.stream());
+}
+int Runtime::qkv_split3(const float *src, float *dst, uint32_t rows, uint32_t H, uint32_t row_off) {
+    TSN_REQUIRE(src != dst, "qkv_split3: source and destination must differ");
+    TSN_TRY(dev.make_current());
+    return launch_qkv_split3(src, dst, (int)rows, (int)H, (int)row_off, dev.stream());
 }
 
 int Runtime::adaln_ln(const float *x, const float *mod, void *y, int ydt, uint32_t rows, uint32_t H,

@@ -24,6 +24,16 @@ struct GemmParams {  // src/net.h:13-16; a zero ld means the packed default
     uint32_t ldx, ldw, ldy;
 };
 
+// Y = X·Wᵀ (+bias) with f32 X and f16 W as an f32-accurate MFMA product: X is split into an f16
+// hi|lo pair in hl (M x 2K halves) and multiplied against [W | W]. gemm_hilo_ok tells whether the
+// pipelined kernel takes the shape; hl needs gemm_hilo_bytes(M, K) bytes, 16-byte aligned. No
+// split-K or stream-K (no workspace), so the result depends only on the operands.
+bool gemm_hilo_ok(const void *W, uint32_t ldw, const void *Y, int ydt, uint32_t ldy, const float *bias,
+                  uint32_t M, uint32_t N, uint32_t K);
+size_t gemm_hilo_bytes(uint32_t M, uint32_t K);
+int gemm_hilo(const half_t *W, uint32_t ldw, const float *X, uint32_t ldx, void *Y, int ydt, uint32_t ldy,
+              const float *bias, uint32_t M, uint32_t N, uint32_t K, half_t *hl, hipStream_t st);
+
 class Device {
 public:
     ~Device();
@@ -55,19 +65,23 @@ public:
     Device dev;
     int init(int device) { return dev.init(device); }
 
-    // Y[M,N] = X[M,K]·W[N,K]ᵀ (+bias). wdt F16: MFMA path, X f32 or f16, Y f32 or f16.
-    // wdt F32 / BF16: f32 SIMT path (X, Y f32).                    (src/net.h:24-26)
+    // Y[M,N] = X[M,K]·W[N,K]ᵀ (+bias)                              (src/net.h:24-26)
+    // wdt F16, X f32: f32-accurate MFMA product (X as an f16 hi|lo pair against [W | W]), Y f32 or f16;
+    //   shapes the pipelined kernel does not take run the f32 SIMT path (Y f32 only).
+    // wdt F16, X f16: plain f16 MFMA product. wdt F32 / BF16: f32 SIMT path (X, Y f32).
     int gemm(int wdt, const void *W, const void *X, int xdt, void *Y, int ydt, const float *bias,
              const GemmParams &p);
     // y[n] = bias[n] + W[n,:]·x                                      (src/net.h:27-28)
     int gemv(const void *W, const float *X, float *Y, const float *bias, uint32_t N, uint32_t K,
              uint32_t ldw, int wdt);
-    // Upload-time weight transform for conv: [OC][IC][K] f16 -> [OC][K][IC] f16.
-    int conv_prepare(const void *W, int w_bf16, void *Wp, uint32_t OC, uint32_t IC, uint32_t K);
-    // conv1d on a prepared weight; x [T,IC] f32, y [OL,OC] f32 (+bias). stride = dil = 1,
-    // OL = T + 2*pad - K + 1, IC % 64 == 0 unless K == 1.            (src/net.h:29-34)
-    int conv(const void *Wp, const float *bias, const float *x, float *y, uint32_t T, uint32_t OL,
-             uint32_t IC, uint32_t OC, uint32_t K, uint32_t stride, uint32_t pad, uint32_t dil);
+    // Upload-time conv weight transform: W [OC][IC][K] (f16, bf16 or f32) -> Wp [OC][conv_prep_cols]
+    // f16, tap-major (three parts per tap for f32 weights), zero padded.
+    int conv_prepare(const void *W, int wdt, void *Wp, uint32_t OC, uint32_t IC, uint32_t K);
+    // conv1d on a prepared weight (wdt = the dtype it was prepared from); x [T,IC] f32, y [OL,OC]
+    // f32 (+bias); strided, dilated or transposed (convt) as the reference's im2col defines them.
+    // f32-accurate for every weight dtype.                           (src/net.h:29-34)
+    int conv(int wdt, const void *Wp, const float *bias, const float *x, float *y, uint32_t T, uint32_t OL,
+             uint32_t IC, uint32_t OC, uint32_t K, uint32_t stride, uint32_t pad, uint32_t dil, uint32_t convt);
     // elementwise (src/net.h:37-49)
     int silu(float *x, size_t n);
     int copy(const float *x, float *y, size_t n);
@@ -75,11 +89,18 @@ public:
     int add_(const float *a, const float *b, float *y, size_t n);
     int add_bcast_col(const float *x, const float *v, float *y, uint32_t S, uint32_t H);
     int cfg_euler(const float *fc, const float *fu, float *x, size_t n, float cfg, float dt);
+    int geglu(const float *a, const float *b, float *y, size_t n);
+    int gelu_quick(float *x, size_t n);
+    int ln_plain(const float *x, float *y, uint32_t S, uint32_t H, float eps);
+    int ln_wb(const float *x, float *y, const float *w, const float *b, uint32_t S, uint32_t H, float eps);
+    int rms_w(const float *x, float *y, const float *w, uint32_t S, uint32_t H, float eps);
+    int mean_cols(const float *x, float *y, uint32_t S, uint32_t H);
     // named kernels of src/dit_fwd.cpp:16-22,83-102
     int adaln_ln(const float *x, const float *mod, void *y, int ydt, uint32_t rows, uint32_t H,
                  uint32_t per_row, uint32_t chunks, uint32_t base, float eps);
     int gate_add(const float *x, const float *f, const float *mod, float *y, uint32_t rows, uint32_t H,
                  uint32_t per_row, uint32_t chunks, uint32_t gate_idx);
+    int qkv_split3(const float *src, float *dst, uint32_t rows, uint32_t H, uint32_t row_off);
     int rms_head(float *x, const float *w, uint32_t rows, uint32_t nh, uint32_t ld, uint32_t hd,
                  uint32_t col_off, uint32_t row_off, float eps);
     int rope_pairs(float *x, const int32_t *pos, uint32_t rows, uint32_t nh, uint32_t ld, uint32_t hd,

@@ -90,4 +90,31 @@ __host__ __device__ inline float bf16_to_f32(uint16_t b) {
     return c.f;
 }
 
+// f32 -> f16 bits as the reference's weight upload converts (src/net.mm:144-164): round to nearest
+// even in the normal range, f32 zero/denormal inputs -> signed zero, results below the f16 normal
+// range truncated to a subnormal (or zero), overflow -> infinity, NaN -> quiet NaN
+__device__ inline half_t f32_to_f16_upload(float f) {
+    const unsigned x = __float_as_uint(f);
+    const unsigned short sign = (unsigned short)((x >> 16) & 0x8000u);
+    const unsigned e8 = (x >> 23) & 0xFFu, man = x & 0x7FFFFFu;
+    unsigned short h;
+    if (e8 == 0xFFu) {
+        h = sign | 0x7C00u | (man ? 0x200u : 0u);
+    } else if (e8 == 0u) {
+        h = sign;
+    } else {
+        const int e = (int)e8 - 112;   // f16 biased exponent
+        if (e >= 31) {
+            h = sign | 0x7C00u;
+        } else if (e <= 0) {
+            h = e < -10 ? sign : (unsigned short)(sign | ((man | 0x800000u) >> (14 - e)));
+        } else {
+            h = (unsigned short)(sign | ((unsigned)e << 10) | (man >> 13));
+            const unsigned rest = man & 0x1FFFu;
+            if (rest > 0x1000u || (rest == 0x1000u && (h & 1u))) h = (unsigned short)(h + 1u);
+        }
+    }
+    return __builtin_bit_cast(half_t, h);
+}
+
 } // namespace tsn

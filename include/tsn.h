@@ -65,6 +65,16 @@ int tsn_sync(tsn_runtime *rt);
  * Uses the runtime's grow-on-demand scratch (2*M*K halves). */
 int tsn_gemm(tsn_runtime *rt, int wdtype, const void *W, const void *X, int xdtype, void *Y, int ydtype,
              const float *bias, uint32_t M, uint32_t N, uint32_t K, uint32_t ldx, uint32_t ldw, uint32_t ldy);
+/* tsn_gemm without any device allocation. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under hipGraph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). Same arguments, kernels and results as tsn_gemm (bit-identical); the f16 hi|lo
+ * split of an f32 X goes to a fixed 32 MiB device array per GPU instead of the runtime's scratch, so
+ * with f16 W and f32 X it needs M*K <= tsn_gemm_noalloc_max_elems() (TSN_ERR_ARG beyond). The array
+ * is shared by every call on one GPU and keeps the last call's contents (nothing in it needs to
+ * start at zero); calls that overlap on one GPU race. */
+int tsn_gemm_noalloc(tsn_runtime *rt, int wdtype, const void *W, const void *X, int xdtype, void *Y, int ydtype,
+                     const float *bias, uint32_t M, uint32_t N, uint32_t K, uint32_t ldx, uint32_t ldw, uint32_t ldy);
+size_t tsn_gemm_noalloc_max_elems(void);
 /* y[n] = bias[n] + W[n,:]·x. Runtime::gemv src/net.h:27-28, src/net.mm:51-56 (wdtype f16/bf16/f32). */
 int tsn_gemv(tsn_runtime *rt, const void *W, int wdtype, const float *x, float *y, const float *bias,
              uint32_t N, uint32_t K, uint32_t ldw);

@@ -155,6 +155,8 @@ _SIGS = {
     "tsn_commit": [_P],
     "tsn_sync": [_P],
     "tsn_gemm": [_P, _I, _P, _P, _I, _P, _I, _P, _U32, _U32, _U32, _U32, _U32, _U32],
+    "tsn_gemm_noalloc": [_P, _I, _P, _P, _I, _P, _I, _P, _U32, _U32, _U32, _U32, _U32, _U32],
+    "tsn_gemm_noalloc_max_elems": [],
     "tsn_gemv": [_P, _P, _I, _P, _P, _P, _U32, _U32, _U32],
     "tsn_conv1d_prepared_bytes": [_I, _U32, _U32, _U32],
     "tsn_conv1d_prepare": [_P, _P, _I, _P, _U32, _U32, _U32],
@@ -296,7 +298,8 @@ _RESTYPES = {"tsn_last_error": ctypes.c_char_p, "tsn_last_gpu_ms": ctypes.c_doub
              "tsn_gguf_get_i64": ctypes.c_int64, "tsn_gguf_get_f64": ctypes.c_double,
              "tsn_refcond_manifest_total": ctypes.c_int64, "tsn_version": _I,
              "tsn_vae_manifest_total": ctypes.c_int64, "tsn_vae_audio_len": ctypes.c_int64,
-             "tsn_clip_manifest_total": ctypes.c_int64, "tsn_conv1d_prepared_bytes": _SZ, "tsn_t5_manifest_total": ctypes.c_int64, "tsn_t5_bucket": _I}
+             "tsn_clip_manifest_total": ctypes.c_int64, "tsn_conv1d_prepared_bytes": _SZ,
+             "tsn_gemm_noalloc_max_elems": _SZ, "tsn_t5_manifest_total": ctypes.c_int64, "tsn_t5_bucket": _I}
 
 
 def lib():
@@ -861,6 +864,15 @@ class Runtime:
     def gemm(self, wdtype, W, X, xdtype, Y, ydtype, bias, M, N, K, ldx=0, ldw=0, ldy=0):
         call("tsn_gemm", self.h, wdtype, W.p, X.p, xdtype, Y.p, ydtype, bias.p if bias is not None else None,
              M, N, K, ldx, ldw, ldy)
+
+    def gemm_noalloc(self, wdtype, W, X, xdtype, Y, ydtype, bias, M, N, K, ldx=0, ldw=0, ldy=0):
+        """tsn_gemm on a fixed per-GPU device array instead of the runtime's scratch (allocates nothing)"""
+        call("tsn_gemm_noalloc", self.h, wdtype, W.p, X.p, xdtype, Y.p, ydtype, bias.p if bias is not None else None,
+             M, N, K, ldx, ldw, ldy)
+
+    @staticmethod
+    def gemm_noalloc_max_elems():
+        return int(lib().tsn_gemm_noalloc_max_elems())
 
     def gemv(self, W, wdtype, x, y, bias, N, K, ldw=0):
         call("tsn_gemv", self.h, W.p, wdtype, x.p, y.p, bias.p if bias is not None else None, N, K, ldw)

@@ -14,7 +14,7 @@ OUT_DIR = os.path.join(HERE, "lib")
 OBJ_DIR = os.path.join(HERE, "_build")
 LIB = os.path.join(OUT_DIR, "libtsn.so")
 
-SOURCES = ["gemm.hip", "attention.hip", "ops.hip", "vae.hip", "enc.hip", "netops.hip", "runtime.cpp", "graph.cpp", "gguf.cpp", "dit.cpp", "refdit.cpp", "refcond.cpp", "vae.cpp", "encoders.cpp", "tokenizers.cpp", "synth.cpp", "capi.cpp"]
+SOURCES = ["gemm.hip", "attention.hip", "ops.hip", "vae.hip", "enc.hip", "netops.hip", "noalloc.hip", "runtime.cpp", "graph.cpp", "gguf.cpp", "dit.cpp", "refdit.cpp", "refcond.cpp", "vae.cpp", "encoders.cpp", "tokenizers.cpp", "synth.cpp", "capi.cpp"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 COMMON = ["-std=c++17", "-O3", "-fPIC", "-Wall", "-Wno-unused-function",

@@ -164,6 +164,12 @@ int tsn_gemm(tsn_runtime *rt, int wdtype, const void *W, const void *X, int xdty
     RT_CHECK(rt);
     return rt->rt.gemm(wdtype, W, X, xdtype, Y, ydtype, bias, tsn::GemmParams{M, N, K, ldx, ldw, ldy});
 }
+int tsn_gemm_noalloc(tsn_runtime *rt, int wdtype, const void *W, const void *X, int xdtype, void *Y, int ydtype,
+                     const float *bias, uint32_t M, uint32_t N, uint32_t K, uint32_t ldx, uint32_t ldw, uint32_t ldy) {
+    RT_CHECK(rt);
+    return tsn::gemm_noalloc(rt->rt, wdtype, W, X, xdtype, Y, ydtype, bias, tsn::GemmParams{M, N, K, ldx, ldw, ldy});
+}
+size_t tsn_gemm_noalloc_max_elems(void) { return tsn::noalloc_scratch_bytes() / 4; }
 int tsn_gemv(tsn_runtime *rt, const void *W, int wdtype, const float *x, float *y, const float *bias, uint32_t N,
              uint32_t K, uint32_t ldw) {
     RT_CHECK(rt);

@@ -40,7 +40,8 @@ int Device::init(int device) {
     TSN_HIP_CHECK(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
     TSN_HIP_CHECK(hipEventCreate(&ev0_));
     TSN_HIP_CHECK(hipEventCreate(&ev1_));
-    return TSN_OK;
+    // device address of the allocation-free GEMM's static scratch on this GPU
+    return noalloc_init(dev_);
 }
 
 int Device::make_current() const {

@@ -34,6 +34,16 @@ size_t gemm_hilo_bytes(uint32_t M, uint32_t K);
 int gemm_hilo(const half_t *W, uint32_t ldw, const float *X, uint32_t ldx, void *Y, int ydt, uint32_t ldy,
               const float *bias, uint32_t M, uint32_t N, uint32_t K, half_t *hl, hipStream_t st);
 
+// The allocation-free GEMM (noalloc.hip): a fixed device array per GPU replaces the runtime scratch.
+// noalloc_init takes that array's device address on `device` (which must be current); Device::init
+// calls it once per runtime.
+int noalloc_init(int device);
+size_t noalloc_scratch_bytes();
+class Runtime;
+struct GemmParams;
+int gemm_noalloc(Runtime &rt, int wdt, const void *W, const void *X, int xdt, void *Y, int ydt, const float *bias,
+                 const GemmParams &p);
+
 class Device {
 public:
     ~Device();

@@ -28,6 +28,7 @@ sys.path.insert(0, ROOT)
 PEAK_F16_TFLOPS = 2500.0      # MI355X dense FP16/BF16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 PEAK_F32_TFLOPS = 157.3       # MI355X dense FP32 MFMA
+PEAK_CLK_GHZ = 2.4            # MI355X peak engine clock (2.5 PF = 256 CUs x 4096 flop/clock x 2.4 GHz)
 CAL_COPY_FLOATS = 16 << 20    # calibration copy: 64 MiB read + 64 MiB written
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_dit_eval_b2_la256.txt")
 CPU_SAMPLE_S = 10.0           # CPU baseline: whole evaluations until this much time has passed
@@ -198,11 +199,15 @@ def profile_pass(which):
     return 0
 
 
-def pmc_pass():
-    """workload for counter runs: three eager evaluations and three calibration copies"""
+PMC_WORKLOADS = {"8s": 1, "b16": 4, "30s": 3}   # counter-pass workload -> tsn_dit_default_spec index
+
+
+def pmc_pass(which="8s"):
+    """workload for counter runs: three eager evaluations of the 8 s (B = 2), batch-16 or 30 s
+    workload, each followed by a calibration copy of 64 MiB"""
     import numpy as np
     tsn = importlib.import_module("thinksound-native_amd")
-    spec = tsn.default_spec(1)
+    spec = tsn.default_spec(PMC_WORKLOADS[which])
     rt = tsn.Runtime(0)
     m = tsn.DitModel(rt, spec)
     m.upload_weights(tsn.synth_weights(spec, 4242, 0.0))
@@ -215,10 +220,95 @@ def pmc_pass():
         m.forward_ex(z, tt, text, pooled, v)
         rt.copy(a, b, CAL_COPY_FLOATS)
         rt.sync()
-        log("pmc pass: eval %d done" % i)
+        log("pmc pass %s: eval %d done" % (which, i))
     m.close()
     rt.close()
     return 0
+
+
+N_SIMD = 1024   # 256 CUs x 4 SIMDs
+N_XCC = 8
+
+
+def read_counter_rows(path):
+    """{kernel: {counter: [values per dispatch]}, plus '__dur_ns': [durations]} from a counter CSV"""
+    import csv
+    out = {}
+    seen = set()
+    with open(path, newline="") as f:
+        for row in csv.DictReader(f):
+            k = short_kernel_name(row["Kernel_Name"])
+            d = out.setdefault(k, {})
+            d.setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+            key = (row["Dispatch_Id"], k)
+            if key not in seen:
+                seen.add(key)
+                d.setdefault("__dur_ns", []).append(float(row["End_Timestamp"]) - float(row["Start_Timestamp"]))
+    return out
+
+
+def pmc_util_summary(sq_csv, dram_csv, title, cmd):
+    """Per-kernel MFMA utilisation (SQ_VALU_MFMA_BUSY_CYCLES over GRBM_GUI_ACTIVE x 1024 SIMDs, the
+    MfmaUtil metric), executed f16 MFMA flops (SQ_INSTS_VALU_MFMA_MOPS_F16 x 512), instruction mix, and
+    memory-side traffic (TCC_EA0_RDREQ_DRAM / WRREQ_DRAM requests, scaled to bytes by the 64 MiB
+    calibration copy) per dispatch."""
+    sq, dr = read_counter_rows(sq_csv), read_counter_rows(dram_csv)
+    mean = statistics.mean
+    cal_bytes = CAL_COPY_FLOATS * 4.0
+    rd_b = cal_bytes / mean(dr["copy_kernel"]["TCC_EA0_RDREQ_DRAM_sum"])
+    wr_b = cal_bytes / mean(dr["copy_kernel"]["TCC_EA0_WRREQ_DRAM_sum"])
+    lines = ["# rocprofv3 counters per dispatch, " + title,
+             "# commands (two counter passes):",
+             "#   " + cmd.replace("{P}", "SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CU_CYCLES SQ_INSTS_VALU SQ_INSTS_MFMA "
+                                          "SQ_INSTS_VALU_MFMA_MOPS_F16 SQ_INSTS_LDS SQ_WAVES GRBM_GUI_ACTIVE"),
+             "#   " + cmd.replace("{P}", "TCC_EA0_RDREQ_DRAM_sum TCC_EA0_WRREQ_DRAM_sum"),
+             "# mfma_util = SQ_VALU_MFMA_BUSY_CYCLES / (%d SIMDs x GRBM_GUI_ACTIVE / %d XCCs) (rocprofv3's MfmaUtil; its"
+             " GRBM_GUI_ACTIVE window holds about 6 us more than the dispatch, see clk)" % (N_SIMD, N_XCC),
+             "# mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (%d SIMDs x dispatch duration x %.1f GHz peak clock): the"
+             " fraction of the dispatch's peak MFMA cycles spent busy" % (N_SIMD, PEAK_CLK_GHZ),
+             "# clk = GRBM_GUI_ACTIVE / %d / dispatch duration (GHz-equivalent)" % N_XCC,
+             "# exec TF/s = SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 flops / dispatch duration (executed MFMA work, hi|lo"
+             " operands counted twice)",
+             "# valu/wave, mfma/wave, lds/wave = SQ_INSTS_VALU, SQ_INSTS_MFMA, SQ_INSTS_LDS over SQ_WAVES",
+             "# DRAM MB = TCC_EA0_RDREQ_DRAM x %.1f B + TCC_EA0_WRREQ_DRAM x %.1f B (bytes per request from the 64 MiB"
+             " calibration copy; memory-side requests past L2, MALL hits included)" % (rd_b, wr_b),
+             "%-26s %5s %8s %6s %9s %9s %9s %9s %8s %9s %9s %7s" % (
+                 "kernel", "disp", "avg us", "clk", "mfma_util", "mfma_busy", "exec TF/s", "valu/wave", "mfma/wv",
+                 "lds/wave", "DRAM MB", "GB/s")]
+    rows = []
+    for k, d in sq.items():
+        if "SQ_VALU_MFMA_BUSY_CYCLES" not in d:
+            continue
+        dur = mean(d["__dur_ns"])
+        gui = mean(d["GRBM_GUI_ACTIVE"]) / N_XCC
+        util = mean(d["SQ_VALU_MFMA_BUSY_CYCLES"]) / (N_SIMD * gui) if gui > 0 else 0.0
+        busy = mean(d["SQ_VALU_MFMA_BUSY_CYCLES"]) / (N_SIMD * dur * PEAK_CLK_GHZ)
+        flops = mean(d["SQ_INSTS_VALU_MFMA_MOPS_F16"]) * 512
+        waves = max(mean(d["SQ_WAVES"]), 1.0)
+        dm = dr.get(k, {})
+        dram = (mean(dm["TCC_EA0_RDREQ_DRAM_sum"]) * rd_b + mean(dm["TCC_EA0_WRREQ_DRAM_sum"]) * wr_b) if dm else 0.0
+        rows.append((k, len(d["__dur_ns"]), dur / 1e3, gui / dur, util, busy, flops / dur / 1e3,
+                     mean(d["SQ_INSTS_VALU"]) / waves, mean(d["SQ_INSTS_MFMA"]) / waves,
+                     mean(d["SQ_INSTS_LDS"]) / waves, dram / 1e6, dram / dur))
+    for r in sorted(rows, key=lambda r: -r[1] * r[2]):
+        lines.append("%-26s %5d %8.2f %6.2f %9.3f %9.3f %9.1f %9.0f %8.0f %9.0f %9.2f %7.0f" % r)
+    return "\n".join(lines) + "\n"
+
+
+UTIL_FILE = os.path.join(ROOT, "profiles", "mfma_util_dit_eval_b2_la256.txt")
+
+
+def read_util_row(kernel, path=UTIL_FILE):
+    """(mfma_busy, DRAM bytes per dispatch) of a kernel from a committed counter summary, or None"""
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.rsplit(None, 11)
+                if not line.startswith("#") and len(parts) == 12 and parts[0] == kernel:
+                    return float(parts[5]), float(parts[10]) * 1e6
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def bench_ref(tsn, rt, args):
@@ -373,7 +463,7 @@ def bench_workloads(tsn, rt, args):
         r = {"B": spec.B, "La": spec.La, "Lt": spec.Lt, "ms_per_eval": round(ms, 4),
              "evals_per_s": round(1e3 / ms, 2), "eval_gflop": round(flops / 1e9, 1),
              "mfma_frac_eval": round(flops / (ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4)}
-        if wl == 3:
+        if wl in (3, 4):
             x0 = inp["z"][0::2].copy()
             x = rt.array(x0)
             m.capture_sample(x, text, pooled, 24, 5.0)
@@ -388,6 +478,80 @@ def bench_workloads(tsn, rt, args):
                (", 24-step sampler %.2f ms" % r["sampler_ms"]) if "sampler_ms" in r else ""))
         out[name] = r
         m.close()
+    return out
+
+
+def bench_joint_block(tsn, rt, args):
+    """One joint block at 8 s (B=2, La=256, Lt=141) on the stream rows X [B, S, H]: its adaLN
+    modulation GEMV, LN, QKV, attention, out-projection, FFNs and gated residuals, eager launches
+    timed by events (the entry point copies X in and out)."""
+    spec = tsn.default_spec(0)
+    m = tsn.DitModel(rt, spec)
+    m.upload_weights(tsn.synth_weights(spec, 4242, 0.0))
+    S = spec.La + spec.Lt
+    X = rt.array(tsn.synth_normal_f32(4242, tsn.IDX_X, 0.0, 1.0, (spec.B, S, spec.H)))
+    g = rt.array(tsn.synth_normal_f32(4242, tsn.IDX_G, 0.0, 1.0, (spec.B, spec.H)))
+    for _ in range(5):
+        m.joint_block(0, X, g)
+    rt.sync()
+    n = 50
+    rt.begin()
+    for _ in range(n):
+        m.joint_block(0, X, g)
+    ms = rt.commit() / n
+    B, La, Lt, H, F = spec.B, spec.La, spec.Lt, spec.H, spec.F
+    flops = 2.0 * B * (La * 3 * H * H + Lt * 3 * H * H + La * H * H + Lt * H * H + La * F * 3 * H + La * H * 3 * F
+                       + Lt * F * H * 2) + 4.0 * B * spec.NH * S * S * 64
+    m.close()
+    log("bench joint block: %.4f ms, %.2f GFLOP, %.1f%% of the f16 MFMA peak"
+        % (ms, flops / 1e9, flops / (ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS * 100))
+    return {"B": B, "La": La, "Lt": Lt, "ms": round(ms, 4), "gflop": round(flops / 1e9, 2),
+            "mfma_frac": round(flops / (ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4), "launch": "eager"}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baselines(tsn, pyoracle):
+    """The CPU oracle on every configured workload, on this host's cores: the single joint block and
+    the 24-step 8 s sampler in full; the 30 s clip and the 16-sample batch as one evaluation each, the
+    24-step sampler projected as 24 x that (the oracle's cost per step does not depend on the step)."""
+    out = {"cores": pyoracle.num_threads(), "cpu": cpu_model(), "kind": "port"}
+    spec = tsn.default_spec(0)
+    w32 = tsn.bf16_to_f32(tsn.synth_weights(spec, 4242, 0.0))
+    S = spec.La + spec.Lt
+    X = tsn.synth_normal_f32(4242, tsn.IDX_X, 0.0, 1.0, (spec.B, S, spec.H))
+    g = tsn.synth_normal_f32(4242, tsn.IDX_G, 0.0, 1.0, (spec.B, spec.H))
+    c0 = time.perf_counter()
+    pyoracle.joint_block(spec, w32, 0, X, g)
+    out["joint_block_8s_b2"] = {"ms": round((time.perf_counter() - c0) * 1e3, 1), "measured": "full"}
+    del w32
+    spec = tsn.default_spec(2)
+    w32 = tsn.bf16_to_f32(tsn.synth_weights(spec, 4242, 0.0))
+    inp = tsn.synth_inputs(spec, 4242, cfg_pairs=True)
+    c0 = time.perf_counter()
+    pyoracle.dit_sample(spec, w32, inp["z"][0::2].copy(), inp["text"], inp["pooled"], 24, 5.0)
+    out["sampler_8s_24steps"] = {"ms": round((time.perf_counter() - c0) * 1e3, 1), "measured": "full"}
+    del w32
+    for wl, name in ((3, "clip_30s"), (4, "batch16")):
+        spec = tsn.default_spec(wl)
+        w32 = tsn.bf16_to_f32(tsn.synth_weights(spec, 4242, 0.0))
+        inp = tsn.synth_inputs(spec, 4242, cfg_pairs=True)
+        c0 = time.perf_counter()
+        pyoracle.dit_forward(spec, w32, inp["z"], inp["t"], inp["text"], inp["pooled"])
+        ms = (time.perf_counter() - c0) * 1e3
+        out[name] = {"eval_ms": round(ms, 1), "measured": "one evaluation",
+                     "sampler_24steps_ms_projected": round(24 * ms, 1)}
+        del w32
+    log("bench: CPU oracle baselines %s" % json.dumps(out))
     return out
 
 
@@ -467,14 +631,19 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sampler-reps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--cpu-quick", action="store_true",
+                    help="time the CPU oracle on the metric's workload only (skip the other workloads, about 80 s)")
     ap.add_argument("--no-ref", action="store_true", help="skip the reference checkpoint graph section")
     ap.add_argument("--no-vae", action="store_true", help="skip the VAE decoder section")
     ap.add_argument("--no-enc", action="store_true", help="skip the text-encoder section")
     ap.add_argument("--no-wl", action="store_true", help="skip the 30 s and batch-16 workload section")
     ap.add_argument("--eager", action="store_true",
                     help="launch kernel by kernel instead of replaying hipGraphs (for profilers that do not follow graphs)")
-    ap.add_argument("--pmc-pass", action="store_true",
-                    help="only run three eager evaluations and a 64 MiB calibration copy (workload for rocprofv3 --pmc)")
+    ap.add_argument("--pmc-pass", nargs="?", const="8s", choices=sorted(PMC_WORKLOADS),
+                    help="only run three eager evaluations (8 s B=2, batch 16 or 30 s) and 64 MiB calibration "
+                         "copies (workload for rocprofv3 --pmc)")
+    ap.add_argument("--pmc-util-summary", nargs=4, metavar=("SQ_CSV", "DRAM_CSV", "TITLE", "CMD"),
+                    help="print the MFMA-utilisation and DRAM summary of two counter CSVs (no GPU use)")
     ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "CMD"),
                     help="print the traffic summary of two counter-collection CSVs (no GPU use)")
     ap.add_argument("--stats-summary", nargs=2, metavar=("STATS_CSV", "CMD"),
@@ -486,6 +655,9 @@ def main():
     args = ap.parse_args()
     if args.pmc_summary:
         sys.stdout.write(pmc_summary(*args.pmc_summary))
+        return 0
+    if args.pmc_util_summary:
+        sys.stdout.write(pmc_util_summary(*args.pmc_util_summary))
         return 0
     if args.stats_summary:
         if args.stats_title:
@@ -499,7 +671,7 @@ def main():
         return 2
 
     if args.pmc_pass:
-        return pmc_pass()
+        return pmc_pass(args.pmc_pass)
     if args.profile_pass:
         return profile_pass(args.profile_pass)
 
@@ -564,6 +736,7 @@ def main():
     log("bench: measured peaks %.0f TFLOP/s dense f16 MFMA, %.0f GB/s device copy" % (meas_tflops, meas_gbs))
     meas_peak = meas_tflops if bound == "mfma" else meas_gbs
     traffic = read_traffic(dom["name"])
+    util = read_util_row(dom["name"])
     if traffic is not None:
         log("bench: %s HBM traffic %.0f B/dispatch (counters), algorithmic %.0f B/dispatch"
             % (dom["name"], traffic, dom["bytes"] / dom["launches"]))
@@ -607,10 +780,12 @@ def main():
     wls = None
     if not args.no_wl and not args.eager:
         wls = bench_workloads(tsn, rt, args)
+        wls["joint_block"] = bench_joint_block(tsn, rt, args)
         wls["hbm_kernels"] = bench_hbm(tsn, rt, args)
 
     # ---------------- CPU baseline: the oracle, one full evaluation ----------------
     cpu = None
+    cpu_all = None
     if not args.no_cpu:
         import pyoracle
         w32 = tsn.bf16_to_f32(w16)
@@ -623,9 +798,12 @@ def main():
             if cpu_s >= CPU_SAMPLE_S:
                 break
         cpu = {"value": round(n_ev / cpu_s, 4), "unit": "evals/s", "cores": pyoracle.num_threads(), "kind": "port",
+               "cpu": cpu_model(),
                "sample": "%d full 21-block evaluations of the timed workload (B=2, La=256, Lt=141), f32 host C++ "
                          "oracle, %.2f s" % (n_ev, cpu_s)}
         log("bench: CPU oracle %d evals in %.2f s on %d threads" % (n_ev, cpu_s, pyoracle.num_threads()))
+        if not args.cpu_quick:
+            cpu_all = cpu_baselines(tsn, pyoracle)
 
     out = {
         "metric": "DiT evals/s (8 s, CFG batch 2); 24-step sampler ms; % BF16 MFMA peak",
@@ -650,11 +828,14 @@ def main():
         "measured_peaks": {"mfma_f16_tflops": round(meas_tflops, 1), "copy_gbs": round(meas_gbs, 1)},
         "roofline": {"kernel": dom["name"], "bound": bound, "achieved": round(achieved, 2), "peak": peak,
                      "unit": unit, "frac": round(achieved / peak, 4), "traffic": traffic,
+                     "mfma_busy_counter": util[0] if util else None,
+                     "traffic_dram_requests": round(util[1]) if util else None,
                      "peak_measured": round(meas_peak, 1), "frac_of_measured": round(achieved / meas_peak, 4),
                      "launches_per_eval": dom["launches"], "avg_launch_us": round(avg_launch_ms * 1e3, 3)},
         "kernels": [{"name": k["name"], "launches": k["launches"], "ms": round(k["ms"], 4),
                      "share": round(k["ms"] / tot_ms, 4)} for k in stats],
         "cpu_baseline": cpu,
+        "cpu_baselines_other_workloads": cpu_all,
         "reference_graph": ref,
         "vae_decoder": vae,
         "text_encoders": enc,

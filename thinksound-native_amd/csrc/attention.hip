@@ -54,8 +54,10 @@ __device__ __forceinline__ void dma16(i32x4 rs, unsigned voff, lds_char *lds) {
                  : "v"(voff), "s"(rs), "s"(l)
                  : "memory");
 }
+// s_waitcnt vmcnt(n) (n in {0, 4, 8, 12}), expcnt/lgkmcnt left at their maxima
 __device__ __forceinline__ void wait_vmcnt(int n) {
-    if (n >= 8) __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (0xF << 8));
+    if (n >= 12) __builtin_amdgcn_s_waitcnt(12 | (7 << 4) | (0xF << 8));
+    else if (n >= 8) __builtin_amdgcn_s_waitcnt(8 | (7 << 4) | (0xF << 8));
     else if (n >= 4) __builtin_amdgcn_s_waitcnt(4 | (7 << 4) | (0xF << 8));
     else __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0xF << 8));
 }
@@ -84,6 +86,23 @@ __device__ __forceinline__ float rows_max(float v) {
 // LDS slot of 16-byte chunk c of row r: c ^ sw(r). Rows 8 apart get different slots too, so the
 // 16 rows one operand read touches (K rows 8 apart, see below) fall in distinct banks.
 __device__ __forceinline__ int sw(int r) { return (r & 7) ^ ((r >> 3) & 7); }
+
+// Online-softmax reference value with a slack of 2^8: the running reference m (log2 units) moves
+// only when a block's row maximum exceeds it by more than 8, so the probabilities exp2(s - m) stay
+// below 2^8 (well inside f16) and most blocks skip the rescale of O and the row sum. The wave
+// branches on whether any of its lanes moves; a lane that does not keeps alpha = 1. The result is
+// the softmax of the same scores: numerator and denominator share every factor.
+__device__ __forceinline__ void lazy_max(float &m_i, float m_blk, floatx4 (&o)[4], floatx4 &lsum) {
+    const bool up = m_blk > m_i + 8.0f;
+    if (__builtin_amdgcn_ballot_w64(up) != 0) {
+        const float m_new = up ? m_blk : m_i;
+        const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
+        m_i = m_new;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+        lsum *= alpha;
+    }
+}
 
 __device__ inline int attn_xcd_remap(int bid, int nwg) {
     const int xcd = bid & 7, idx = bid >> 3;
@@ -180,17 +199,12 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
         float mx = -INFINITY;
 #pragma unroll
         for (int j = 0; j < 4; ++j) mx = fmaxf(fmaxf(mx, fmaxf(sc[j][0], sc[j][1])), fmaxf(sc[j][2], sc[j][3]));
-        const float m_new = fmaxf(m_i, rows_max(mx) * scale);   // scale > 0: max commutes with it
-        const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
-        m_i = m_new;
+        lazy_max(m_i, rows_max(mx) * scale, o, lsum);   // scale > 0: max commutes with it
         half_t ph[4][4];
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) ph[j][r] = (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r], scale, -m_new));
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
-        lsum *= alpha;
+            for (int r = 0; r < 4; ++r) ph[j][r] = (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r], scale, -m_i));
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const half8 pf = half8{ph[2 * c][0], ph[2 * c][1], ph[2 * c][2], ph[2 * c][3],
@@ -295,6 +309,146 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
     }
 }
 
+// Four-wave variant for grids beyond one round of the eight-wave kernel (long contexts, large
+// batches): 64 queries per workgroup, wave w serves queries 16w..16w+15 over every key block (no
+// key split, no merge), and a three-stage ring of single key blocks (K 8 KB + Vt 8 KB per stage),
+// 48 KB of LDS and at most 128 VGPRs, so three workgroups share a CU. At 30 s (S = 1101, 576
+// workgroups) the whole grid is resident at once instead of running in two rounds. The MFMA
+// formulation, the online softmax and the probability rounding are the eight-wave kernel's.
+__global__ __launch_bounds__(256, 3) void flash_attn4_kernel(const AttnArgs a) {
+    constexpr int STG = 8192;   // halves per stage: K block (64 keys x 64) then Vt block (64 d x 64 keys)
+    constexpr int NST = 3;      // ring stages: two key blocks in flight while one is multiplied
+    __shared__ __attribute__((aligned(1024))) half_t smem[NST * STG];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nqt = (a.S + 63) >> 6;
+    const int wg = attn_xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = wg / nqt, qt = wg - bh * nqt;
+    const int S = a.S, Sp = a.Sp;
+    const half_t *Qp = a.Q + (long long)bh * S * 64;
+    // K rows past S read as zero through the buffer range (num_records = the head's S rows)
+    const unsigned long long ka = (unsigned long long)(a.K + (long long)bh * S * 64);
+    const i32x4 rk = i32x4{(int)(unsigned)ka, (int)((ka >> 32) & 0xFFFF), S * 128, 0x00020000};
+    const i32x4 rv = make_rsrc(a.Vt + (long long)bh * 64 * Sp);
+
+    const int q = qt * 64 + wave * 16 + (lane & 15);
+    const int g = lane >> 4;
+    half8 qf[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+        qf[ks] = q < S ? *(const half8 *)(Qp + (long long)q * 64 + ks * 32 + g * 8) : zero_h8();
+
+    const int nkb = (S + AKB - 1) / AKB;
+    // DMA of key block b: 16 chunks of 1 KB (K rows 8sub.., then Vt rows 8sub..); wave w issues
+    // chunks 4w..4w+3. Lane l writes slot l & 7 of row lr = l >> 3 (source chunk lc = (l & 7) ^ sw(row)).
+    // The lane's byte offsets inside a block are fixed; a block adds 8 KB (K) or 128 B (Vt).
+    const int lr = lane >> 3;
+    unsigned voff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int d = wave * 4 + i, part = d >> 3, sub = d & 7;
+        const int lc = (lane & 7) ^ lr ^ sub;
+        voff[i] = part == 0 ? (unsigned)(((sub * 8 + lr) * 64 + lc * 8) * 2)
+                            : (unsigned)(((sub * 8 + lr) * Sp + lc * 8) * 2);
+    }
+    auto issue = [&](int b, int st) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int d = wave * 4 + i, part = d >> 3, sub = d & 7;
+            const unsigned vo = voff[i] + (part == 0 ? (unsigned)b * 8192u : (unsigned)b * 128u);
+            dma16(part == 0 ? rk : rv, vo, (lds_char *)(smem + st * STG + part * 4096 + sub * 512));
+        }
+    };
+
+    float m_i = -INFINITY;
+    floatx4 o[4], lsum = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    const half8 ones = half8{1, 1, 1, 1, 1, 1, 1, 1};
+    const float scale = a.scale_log2;
+
+    auto compute = [&](int st, int blk) {
+        const half_t *sK = smem + st * STG;
+        const half_t *sV = sK + 4096;
+        floatx4 sc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            sc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            const int i = lane & 15;
+            const int r = 32 * (j >> 1) + 8 * (i >> 2) + 4 * (j & 1) + (i & 3);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const half8 kf = *(const half8 *)(sK + r * 64 + (((ks * 4 + g) ^ sw(r)) * 8));
+                sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], sc[j], 0, 0, 0);
+            }
+        }
+        if (blk * AKB + AKB > S) {   // the last, partial key block only (wave-uniform)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    if (blk * AKB + 32 * (j >> 1) + 8 * g + 4 * (j & 1) + r >= S) sc[j][r] = -INFINITY;
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mx = fmaxf(fmaxf(mx, fmaxf(sc[j][0], sc[j][1])), fmaxf(sc[j][2], sc[j][3]));
+        lazy_max(m_i, rows_max(mx) * scale, o, lsum);
+        half_t ph[4][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ph[j][r] = (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r], scale, -m_i));
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const half8 pf = half8{ph[2 * c][0], ph[2 * c][1], ph[2 * c][2], ph[2 * c][3],
+                                   ph[2 * c + 1][0], ph[2 * c + 1][1], ph[2 * c + 1][2], ph[2 * c + 1][3]};
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const int d = dt * 16 + (lane & 15);
+                const half8 vf = *(const half8 *)(sV + d * 64 + (((c * 4 + g) ^ sw(d)) * 8));
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[dt], 0, 0, 0);
+            }
+            lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lsum, 0, 0, 0);
+        }
+    };
+
+    // ring: block b in stage b % 3; blocks b + 1 and b + 2 land while b is multiplied
+    issue(0, 0);
+    if (nkb > 1) issue(1, 1);
+    wait_vmcnt(nkb > 1 ? 4 : 0);
+    block_barrier();
+    if (nkb > 2) issue(2, 2);
+    for (int b = 0; b < nkb; ++b) {
+        compute(b % NST, b);
+        if (b + 1 < nkb) {
+            wait_vmcnt(b + 2 < nkb ? 4 : 0);   // block b + 1 has landed (b + 2 may still be in flight)
+            block_barrier();                    // and every wave is done with stage b % 3
+            if (b + NST < nkb) issue(b + NST, b % NST);
+        }
+    }
+    if (q < S) {
+        const float inv = 1.0f / lsum[0];   // every row of the ones product holds the same sum
+        const int b = bh / a.nh, h = bh - b * a.nh;
+        const long long orow = rowmap_phys(a.omap, b * S + q) * (long long)a.ldo + h * 64;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            const int d0 = dt * 16 + g * 4;
+            if (a.o_f32) {
+                float *op = (float *)a.O + orow + d0;
+                *(float4 *)op = make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+            } else {
+                half_t *op = (half_t *)a.O + orow + d0;
+                const float y0 = o[dt][0] * inv, y1 = o[dt][1] * inv, y2 = o[dt][2] * inv, y3 = o[dt][3] * inv;
+                const half4 hi = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
+                *(half4 *)op = hi;
+                if (a.o_lo)
+                    *(half4 *)(op + a.o_lo) = half4{(half_t)(y0 - (float)hi[0]), (half_t)(y1 - (float)hi[1]),
+                                                    (half_t)(y2 - (float)hi[2]), (half_t)(y3 - (float)hi[3])};
+            }
+        }
+    }
+}
+
 // f32 [S, ld] q/k/v slices -> Q/K [nh][S][64], Vt [nh][64][Sp] (f16), one thread per element
 __global__ void attn_pack_kernel(const float *qkv, int S, int nh, int ld, int q_off, int k_off, int v_off,
                                  half_t *Q, half_t *K, half_t *Vt, int Sp) {
@@ -330,10 +484,12 @@ int launch_attention(const AttnArgs &a, hipStream_t st) {
     TSN_REQUIRE((long long)a.S * 64 * 2 < (1LL << 31) && (long long)a.Sp * 64 * 2 < (1LL << 31),
                 "attention: per-head K/Vt extent must stay below 2 GB (buffer addressing)");
     TSN_REQUIRE((long long)((a.S + 63) / 64) * a.BH < (1LL << 31), "attention: too many query tiles");
+    TSN_REQUIRE((long long)a.S * 128 < (1LL << 31), "attention: K extent per head below 2 GB");
     dim3 grid((unsigned)((a.S + 63) / 64 * a.BH)), block(512);
-    // up to 512 keys and at most one workgroup per CU: all key blocks in LDS at once; otherwise the
-    // two-stage ring, two workgroups per CU
+    // up to 512 keys and at most one workgroup per CU: all key blocks in LDS at once; grids beyond
+    // one round (256 workgroups): the four-wave kernel, up to four workgroups per CU
     if (a.S <= 4 * 2 * AKB && grid.x <= 256) TSN_LAUNCH(flash_attn_kernel<4>, grid, block, 0, st, a);
+    else if (grid.x > 256) TSN_LAUNCH(flash_attn4_kernel, grid, dim3(256), 0, st, a);
     else TSN_LAUNCH(flash_attn_kernel<2>, grid, block, 0, st, a);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;

@@ -631,8 +631,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sampler-reps", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--cpu-quick", action="store_true",
-                    help="time the CPU oracle on the metric's workload only (skip the other workloads, about 80 s)")
+    ap.add_argument("--cpu-all", action="store_true",
+                    help="also time the CPU oracle on the other workloads: the joint block and the 24-step 8 s "
+                         "sampler in full, the 30 s and batch-16 evaluations once (about 3 minutes)")
     ap.add_argument("--no-ref", action="store_true", help="skip the reference checkpoint graph section")
     ap.add_argument("--no-vae", action="store_true", help="skip the VAE decoder section")
     ap.add_argument("--no-enc", action="store_true", help="skip the text-encoder section")
@@ -802,7 +803,7 @@ def main():
                "sample": "%d full 21-block evaluations of the timed workload (B=2, La=256, Lt=141), f32 host C++ "
                          "oracle, %.2f s" % (n_ev, cpu_s)}
         log("bench: CPU oracle %d evals in %.2f s on %d threads" % (n_ev, cpu_s, pyoracle.num_threads()))
-        if not args.cpu_quick:
+        if args.cpu_all:
             cpu_all = cpu_baselines(tsn, pyoracle)
 
     out = {

@@ -100,6 +100,7 @@ int DitModel::create(Runtime *r, const DitSpec &sp) {
     // split-K partials: up to 8 splits of the largest residual GEMM output (B*S x H f32)
     ws_bytes_ = (size_t)8 * B * S * H * sizeof(float);
     TSN_TRY(alloc(ws_bytes_, (void **)&ws_));
+    TSN_TRY(alloc_skcnt());
     // RoPE table: same expression as shaders/ops_conv.metal:162-164 with fscale 1 (audio rows)
     std::vector<float> tab((size_t)s.La * 32 * 2);
     for (int p = 0; p < s.La; ++p)

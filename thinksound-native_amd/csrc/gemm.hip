@@ -31,6 +31,11 @@ constexpr int BM = 128, BN = 128, BK = 64, LDSW = BK + 8;
 // the per-workgroup cost of pipeline fill, partial store and the fixup launch in K-tile units
 // (the fixup kernel alone takes 8-10 us, about 20 K tiles)
 constexpr int NCU = 256, SK_MIN_UNITS = 8, SK_OVERHEAD = 20;
+// with the fixup inside the stream-K kernel (GemmBatch::sk_cnt): partial store written through,
+// arrival, and the last contributor's sum of the slots. Measured about as long as the fixup launch
+// it replaces (3.345 -> 3.324 ms per reference-graph evaluation with the same plans; a charge of 8
+// K tiles picked stream-K for more GEMMs and measured 3.369 -> 3.411 ms)
+constexpr int SK_OVERHEAD_IN = 20;
 
 __device__ inline int xcd_remap(int bid, int nwg) {
     const int xcd = bid & 7, idx = bid >> 3;
@@ -304,12 +309,19 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const GemmBatch bt) {
 // ---------------------------------------------------------------------------------------------
 typedef __attribute__((address_space(3))) char lds_char;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+constexpr int CPOL_SC1 = 16;   // cache-policy bit sc1 of a buffer access: device-coherent (written through / read past L1)
 
 // raw buffer descriptor: base, stride 0, num_records 2^31-1, 32-bit data format; an offset at or
 // above 0x80000000 is out of range and reads as zero
 __device__ __forceinline__ i32x4 make_rsrc(const void *p) {
     const unsigned long long a = (unsigned long long)p;
     return i32x4{(int)(unsigned)a, (int)((a >> 32) & 0xFFFF), 0x7FFFFFFF, 0x00020000};
+}
+
+// the same descriptor as the buffer type of the compiler's buffer builtins
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_brsrc(const void *p) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(p), (short)0, 0x7FFFFFFF, 0x00020000);
 }
 
 // 16 bytes per lane, global -> LDS slot (lane) of the 1 KB block at lds. Issued from inline asm so
@@ -620,6 +632,21 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
     }
 }
 
+// In-kernel stream-K fixup of one cut tile: its arrival counter (zero before the first arrival,
+// reset by the last), and its contributors, workgroups w0 .. w0 + nc - 1 of G over U units, whose
+// partial slots in ws follow the slot rule of gemm_sk_kernel (slot 0 when the tile is the
+// workgroup's first segment, i.e. the workgroup starts at or after the tile's first unit a)
+struct SkFix {
+    unsigned *cnt;
+    const float *ws;
+    long long U, G, a, w0;
+    int nc;
+    __device__ const float *slot(int j) const {
+        const long long ww = w0 + j;
+        return ws + (ww * 2 + (ww * U / G >= a ? 0 : 1)) * (long long)(BM * BN);
+    }
+};
+
 // One C tile (rows m0.., columns n0..) over the K tiles [kbeg, kbeg + nk): the pipelined K loop,
 // then either the epilogue (part == null; ks = split index for a classic split-K partial) or a raw
 // f32 [BM][BN] store of the accumulators to part (a stream-K segment, finished by the fixup kernel).
@@ -629,7 +656,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
 // of several rounds where the second workgroup covers the first's barrier and load waits).
 template <int EPI, bool HL, bool SEG, int NSX = NS>
 __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, int kbeg, int nk, float *part, int ks,
-                                          int tid) {
+                                          int tid, const SkFix *fx = nullptr) {
     // stage s: A tile at smem + s*STAGE, W tile at smem + (NSX + s)*STAGE; reused for the C tile
     constexpr int SMEM = 2 * NSX * STAGE > BM * TP * 2 ? 2 * NSX * STAGE : BM * TP * 2;
     __shared__ __attribute__((aligned(1024))) half_t smem[SMEM];
@@ -819,7 +846,50 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
                 for (int r = 0; r < 4; ++r) tile[(rb + i * 16 + r) * TP + cb + j * 16] = acc[i][j][r];
         block_barrier();
     }
-    if (SEG && part) {
+    if (SEG && part && fx) {
+        // raw partial tile written through to memory (sc1), so the tile's last contributor reads
+        // it from any XCD; then the arrival. The last of the tile's contributors sums every
+        // contributor's slot in K order into the LDS C tile and runs the epilogue.
+        const __amdgpu_buffer_rsrc_t rp = make_brsrc(part);
+#pragma unroll 1
+        for (int p = 0; p < 8; ++p) {
+            const int c = tid + 512 * p, row = c >> 5, col = (c & 31) * 4;
+            const floatx4 v = *(const floatx4 *)(tile + row * TP + col);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp, (row * BN + col) * 4, 0, CPOL_SC1);
+        }
+        __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (0xF << 8));   // this thread's partial stores are done
+        int *s_last = (int *)(tile + BM * TP);   // LDS word past the C tile
+        block_barrier();
+        if (tid == 0) {
+            const unsigned old = __hip_atomic_fetch_add(fx->cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            *s_last = old + 1 == (unsigned)fx->nc;
+        }
+        block_barrier();
+        if (*s_last) {
+            float v[8][4];
+#pragma unroll
+            for (int p = 0; p < 8; ++p) v[p][0] = v[p][1] = v[p][2] = v[p][3] = 0.0f;
+            for (int j = 0; j < fx->nc; ++j) {
+                const __amdgpu_buffer_rsrc_t rs = make_brsrc(fx->slot(j));
+                u32x4 x[8];
+#pragma unroll
+                for (int p = 0; p < 8; ++p) x[p] = __builtin_amdgcn_raw_buffer_load_b128(rs, (tid + 512 * p) * 16, 0, CPOL_SC1);
+#pragma unroll
+                for (int p = 0; p < 8; ++p) {
+                    v[p][0] += __uint_as_float(x[p][0]); v[p][1] += __uint_as_float(x[p][1]);
+                    v[p][2] += __uint_as_float(x[p][2]); v[p][3] += __uint_as_float(x[p][3]);
+                }
+            }
+#pragma unroll
+            for (int p = 0; p < 8; ++p) {
+                const int c = tid + 512 * p, row = c >> 5, col = (c & 31) * 4;
+                *(floatx4 *)(tile + row * TP + col) = floatx4{v[p][0], v[p][1], v[p][2], v[p][3]};
+            }
+            block_barrier();
+            tile_epilogue<EPI>(P, tile, m0, n0, 0, tid);
+            if (tid == 0) __hip_atomic_store(fx->cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    } else if (SEG && part) {
         // raw partial tile, row-major [BM][BN], 16-byte stores (not unrolled: keeps registers free)
 #pragma unroll 1
         for (int p = 0; p < 8; ++p) {
@@ -838,7 +908,9 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
 // tile-major, K innermost; workgroup w of G takes units [w*U/G, (w+1)*U/G) and computes each tile it
 // touches over its part of K. A tile covered whole gets the epilogue here; a tile cut by a
 // workgroup boundary leaves f32 partials in bt.ws slot (w, 0) for the first tile of w or (w, 1) for
-// its last, which gemm_fixup_kernel sums in K order (deterministic for a given G) and finishes.
+// its last. With bt.sk_cnt the last contributor to arrive (per-tile counter) sums the slots in K
+// order and finishes the tile in this kernel; otherwise gemm_fixup_kernel does, in the same order
+// (deterministic for a given G either way: the sum does not depend on who arrives last).
 template <int EPI, bool HL, int NSX = NS>
 __device__ __forceinline__ void pipe_dp(const GemmBatch &bt) {
     const int tid = threadIdx.x;
@@ -1032,6 +1104,14 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
     }
 }
 
+// the workgroup w of G holding unit u: w*U/G <= u < (w + 1)*U/G
+__device__ __forceinline__ long long sk_owner(long long u, long long U, long long G) {
+    long long w = u * G / U;
+    while (w + 1 < G && (w + 1) * U / G <= u) ++w;
+    while (w > 0 && w * U / G > u) --w;
+    return w;
+}
+
 template <int EPI>
 __global__ __launch_bounds__(512, 1) void gemm_sk_kernel(const GemmBatch bt) {
     const int tid = threadIdx.x;
@@ -1050,7 +1130,22 @@ __global__ __launch_bounds__(512, 1) void gemm_sk_kernel(const GemmBatch bt) {
         int tm, tn;
         tile_mn(tile, P.tiles_m, P.tiles_n, tm, tn);
         float *part = (kbeg == 0 && nk == nkp) ? nullptr : bt.ws + ((long long)wg * 2 + (seg == 0 ? 0 : 1)) * (BM * BN);
-        pipe_tile<EPI, true, true>(P, tm * BM, tn * BN, kbeg, nk, part, 0, tid);
+        if (part && bt.sk_cnt) {
+            // cut tile finished here by its last contributor: contributors are the workgroups
+            // holding units a .. a + nkp - 1 of the tile
+            SkFix fx;
+            const long long a = P.unit_start + (long long)tile * nkp, b = a + nkp;
+            fx.cnt = bt.sk_cnt + P.tile_start + tile;
+            fx.ws = bt.ws;
+            fx.U = U;
+            fx.G = G;
+            fx.a = a;
+            fx.w0 = sk_owner(a, U, G);
+            fx.nc = (int)(sk_owner(b - 1, U, G) - fx.w0 + 1);
+            pipe_tile<EPI, true, true>(P, tm * BM, tn * BN, kbeg, nk, part, 0, tid, &fx);
+        } else {
+            pipe_tile<EPI, true, true>(P, tm * BM, tn * BN, kbeg, nk, part, 0, tid);
+        }
         u += nk;
     }
 }
@@ -1177,6 +1272,7 @@ int launch_gemm(GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
 }
 
 int launch_gemm_reduce(const GemmBatch &b, int epi, hipStream_t st) {
+    if (b.sk && b.sk_cnt) return TSN_OK;   // finished inside the stream-K kernel
     if (b.sk) {
         const dim3 grid(b.total_tiles), block(512);
         if (epi == EPI_STORE) TSN_LAUNCH((gemm_fixup_kernel<EPI_STORE>), grid, block, 0, st, b);
@@ -1203,7 +1299,7 @@ int launch_gemm_reduce(const GemmBatch &b, int epi, hipStream_t st) {
 }
 
 bool gemm_needs_reduce(const GemmBatch &b) {
-    if (b.sk) return true;
+    if (b.sk) return b.sk_cnt == nullptr;
     for (int i = 0; i < b.nprob; ++i)
         if (b.p[i].splits > 1) return true;
     return false;
@@ -1424,7 +1520,8 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         }
         cur = (long long)((b.total_tiles + NCU - 1) / NCU) * nkmax + (split ? 2 : 0);
         const long long g = std::min<long long>(NCU, std::max<long long>(1, units / SK_MIN_UNITS));
-        const long long skt = (units + g - 1) / g + SK_OVERHEAD;
+        const bool fix_in = b.sk_cnt && b.sk_cnt_n >= b.total_tiles;
+        const long long skt = (units + g - 1) / g + (fix_in ? SK_OVERHEAD_IN : SK_OVERHEAD);
         const size_t need = (size_t)g * 2 * BM * BN * sizeof(float);
         if (g > 1 && skt * 10 < cur * 8 && need <= b.ws_bytes) {
             b.sk = 1;
@@ -1439,8 +1536,10 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
                 tiles += p.tiles_m * p.tiles_n;
             }
             b.total_tiles = tiles;
+            if (!fix_in) b.sk_cnt = nullptr;   // the fixup kernel finishes the cut tiles
         }
     }
+    if (!b.sk) b.sk_cnt = nullptr;
     TSN_REQUIRE(pipe || epi != EPI_SWIGLU, "gemm swiglu: needs K and row strides the pipelined kernel takes");
     b.pipe = pipe ? 1 : 0;
     b.hl = any_half ? 1 : 0;

@@ -89,8 +89,19 @@ int GraphRunner::profile(const std::function<int()> &enqueue, std::vector<Kernel
     return rc2;
 }
 
+int GraphRunner::alloc_skcnt() {
+    void *p = nullptr;
+    TSN_TRY(alloc(SK_COUNTERS * sizeof(unsigned), &p));
+    skcnt_ = (unsigned *)p;
+    return TSN_OK;
+}
+
 int GraphRunner::gemm_run(GemmBatch &b, int epi, double flop_scale) {
     const hipStream_t st = rt->dev.stream();
+    if (!b.sk_cnt && skcnt_) {
+        b.sk_cnt = skcnt_;
+        b.sk_cnt_n = SK_COUNTERS;
+    }
     TSN_TRY(gemm_plan(b, epi, false));
     TSN_TRY(run(b.kname, gemm_flops(b) * flop_scale, gemm_bytes(b, epi),
                 [&] { return gemm_launch_planned(b, epi, false, st); }));
@@ -108,6 +119,10 @@ int GraphRunner::gemm_run(GemmBatch &b, int epi, double flop_scale) {
 // kernel is skipped (the GEMM epilogue already updated X).
 int GraphRunner::resid_ln(GemmBatch &b, RedLnArgs &r, int H, float eps) {
     const hipStream_t st = rt->dev.stream();
+    if (!b.sk_cnt && skcnt_) {
+        b.sk_cnt = skcnt_;
+        b.sk_cnt_n = SK_COUNTERS;
+    }
     TSN_TRY(gemm_plan(b, EPI_RESID, false));
     TSN_TRY(run(b.kname, gemm_flops(b), gemm_bytes(b, EPI_RESID), [&] { return gemm_launch_planned(b, EPI_RESID, false, st); }));
     if (b.sk)   // stream-K: the fixup applies the residual epilogue to the cut tiles

@@ -57,6 +57,11 @@ protected:
     hipGraphExec_t gexec_ = nullptr;
 
     int alloc(size_t bytes, void **p);   // zero-filled, freed with the runner
+    // zero-initialised per-tile arrival counters for the stream-K kernel's own fixup
+    // (GemmBatch::sk_cnt); gemm_run and resid_ln hand them to every batch once allocated
+    static constexpr int SK_COUNTERS = 16384;
+    int alloc_skcnt();
+    unsigned *skcnt_ = nullptr;
     // frees one allocation made by alloc(); drops the captured graph, which may address it
     int release(void *p);
     void drop_graph();

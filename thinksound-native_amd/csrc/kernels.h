@@ -71,10 +71,14 @@ struct GemmBatch {
     int pipe = 0;
     const char *kname = nullptr;
     // stream-K schedule (gemm_plan, pipelined kernel with a workspace): sk_g workgroups share the
-    // sk_units (tile, K tile) units evenly; partial tiles go to ws and launch_gemm_reduce finishes
-    // them (gemm_fixup_kernel)
+    // sk_units (tile, K tile) units evenly; partial tiles go to ws. With sk_cnt (zero-initialised
+    // arrival counters, sk_cnt_n >= total tiles; every launch leaves them at zero) the last
+    // contributor of a cut tile finishes it inside the kernel; otherwise launch_gemm_reduce does
+    // (gemm_fixup_kernel)
     int sk = 0, sk_g = 0;
     long long sk_units = 0;
+    unsigned *sk_cnt = nullptr;
+    int sk_cnt_n = 0;
     int hl = 0;   // some problem reads half-width W (selects the kernel variant)
     // nonzero: never stream-K, and choose the classic K split by the estimated time (waves x K tiles
     // per split, plus the partial-sum traffic). For long-K GEMMs with few tiles, whose A and W tiles

@@ -103,6 +103,7 @@ int RefCondModel::create(Runtime *r, const RefCondSpec &sp) {
     TSN_TRY(alloc(F * sizeof(float), (void **)&gb_));
     ws_bytes_ = (size_t)40 << 20;
     TSN_TRY(alloc(ws_bytes_, (void **)&ws_));
+    TSN_TRY(alloc_skcnt());
     // latent row i takes sync row floor((i + 0.5) * sync_S / T), computed in f32 as src/dit.cpp:112
     std::vector<int32_t> idx(s.T);
     for (int i = 0; i < s.T; ++i) {

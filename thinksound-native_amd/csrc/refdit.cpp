@@ -153,6 +153,7 @@ int RefDitModel::create(Runtime *r, const RefDitSpec &sp) {
     // split-K partials: up to 8 splits of the largest residual output (B*S x H f32)
     ws_bytes_ = std::max((size_t)8 * B * S * H * sizeof(float), (size_t)40 << 20);   // split-K / stream-K
     TSN_TRY(alloc(ws_bytes_, (void **)&ws_));
+    TSN_TRY(alloc_skcnt());
     // latent positions 0..T-1 (fscale 1); clip positions 0..C-1 scaled by T/C (src/dit_fwd.cpp:167-178)
     const std::vector<float> tl = rope_table(s.T, 1.0f, s.rope_theta);
     TSN_TRY(af(&rope_l_, tl.size()));

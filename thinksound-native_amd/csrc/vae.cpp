@@ -156,6 +156,7 @@ int VaeModel::create(Runtime *r, const VaeSpec &sp) {
     TSN_TRY(rt->dev.upload(ones_, ones.data(), ones.size() * sizeof(float)));
     ws_bytes_ = (size_t)64 << 20;
     TSN_TRY(alloc(ws_bytes_, (void **)&ws_));
+    TSN_TRY(alloc_skcnt());
     return TSN_OK;
 }
 

@@ -555,6 +555,44 @@ def cpu_baselines(tsn, pyoracle):
     return out
 
 
+def f32_to_bf16(x):
+    """round-to-nearest-even f32 -> bf16 bits (uint16)"""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bench_bf16_gemm(tsn, rt, args):
+    """The bf16-operand mode beside f16: tsn_gemm on the same pipelined kernel and tiles, f16 X and W
+    against bf16 X and W (f32 Y), at the 8 s evaluation's FFN1 and QKV shapes and the batch-16 FFN1
+    shape; eager launches timed by events, 20 each"""
+    out = {}
+    for name, (M, N, K) in (("ffn1_8s_794x4096x1024", (794, 4096, 1024)), ("qkv_8s_794x3072x1024", (794, 3072, 1024)),
+                            ("ffn1_b16_6352x4096x1024", (6352, 4096, 1024))):
+        xf = tsn.synth_normal_f32(4242, 3100, 0.0, 1.0, (M, K))
+        wf = tsn.synth_normal_f32(4242, 3101, 0.0, 0.02, (N, K))
+        y = rt.empty((M, N))
+        row = {}
+        for tag, dt, conv in (("f16", tsn.F16, lambda a: a.astype(np.float16)), ("bf16", tsn.BF16, f32_to_bf16)):
+            X, W = rt.array(conv(xf)), rt.array(conv(wf))
+            for _ in range(3):
+                rt.gemm(dt, W, X, dt, y, tsn.F32, None, M, N, K)
+            rt.sync()
+            n = 20
+            rt.begin()
+            for _ in range(n):
+                rt.gemm(dt, W, X, dt, y, tsn.F32, None, M, N, K)
+            ms = rt.commit() / n
+            tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+            row[tag] = {"us": round(ms * 1e3, 2), "tflops": round(tf, 1), "frac_peak": round(tf / PEAK_F16_TFLOPS, 4)}
+            X.free()
+            W.free()
+        y.free()
+        row["bf16_over_f16"] = round(row["bf16"]["tflops"] / row["f16"]["tflops"], 3)
+        out[name] = row
+    log("bench bf16 gemm: %s" % json.dumps(out))
+    return out
+
+
 def bench_hbm(tsn, rt, args):
     """The HBM-bound norm kernel on a large shape: adaLN (LayerNorm + broadcast shift/scale) over
     65536 rows x 1024, f32 in, f16 out; algorithmic bytes = rows*H*(4 + 2) + modulation, 20 launches"""
@@ -783,6 +821,7 @@ def main():
         wls = bench_workloads(tsn, rt, args)
         wls["joint_block"] = bench_joint_block(tsn, rt, args)
         wls["hbm_kernels"] = bench_hbm(tsn, rt, args)
+        wls["bf16_gemm"] = bench_bf16_gemm(tsn, rt, args)
 
     # ---------------- CPU baseline: the oracle, one full evaluation ----------------
     cpu = None

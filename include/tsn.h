@@ -61,7 +61,9 @@ int tsn_sync(tsn_runtime *rt);
  * about 2^-22 of the operand, against 2^-11 for an f16-rounded X). Y f32, or f16 on request. Shapes
  * the MFMA tiling does not take (K % 64, N % 8, unaligned W/bias/Y) run exact f32 products on the
  * SIMT path (f32 Y only). wdtype TSN_F16 with f16 X is the plain f16 product (opt-in, f16 operands
- * as given). TSN_F32 / TSN_BF16 weights run the f32 SIMT path (X, Y f32). ld* = 0 means packed.
+ * as given). TSN_F32 / TSN_BF16 weights run the f32 SIMT path (X, Y f32). TSN_BF16 weights with
+ * TSN_BF16 X run bf16 products on MFMA (f32 accumulation, f32 Y; K % 64 == 0, N % 8 == 0, 16-byte
+ * aligned rows, else TSN_ERR_UNSUPPORTED): the bf16-operand mode, beside the f16 one. ld* = 0 means packed.
  * Uses the runtime's grow-on-demand scratch (2*M*K halves). */
 int tsn_gemm(tsn_runtime *rt, int wdtype, const void *W, const void *X, int xdtype, void *Y, int ydtype,
              const float *bias, uint32_t M, uint32_t N, uint32_t K, uint32_t ldx, uint32_t ldw, uint32_t ldy);

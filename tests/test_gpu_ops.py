@@ -88,6 +88,50 @@ def test_gemm_f32_weights(tsn, rt, orc):
     assert rel_l2(Y.numpy(), orc.gemm(W, X, b)) < 1e-5
 
 
+def _bf16(x):
+    """round-to-nearest-even f32 -> bf16 bits, and the f32 value those bits hold"""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    b = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return b, (b.astype(np.uint32) << 16).view(np.float32)
+
+
+@pytest.mark.parametrize("M,N,K", [(794, 4096, 1024), (1100, 4096, 256), (130, 200, 128), (1, 64, 64)])
+def test_gemm_bf16_operands(tsn, rt, M, N, K):
+    """bf16 X and W on MFMA (1100 x 4096: more than one round of tiles, the two-stage kernel): each
+    bf16 x bf16 product is exact in f32, so against the float64
+    product of the same bf16 values only the f32 accumulation differs (rel-L2 <= 1e-5); the bias
+    is added in f32"""
+    r = rng(11)
+    X = r.standard_normal((M, K)).astype(np.float32)
+    W = (r.standard_normal((N, K)) * 0.03).astype(np.float32)
+    b = r.standard_normal(N).astype(np.float32)
+    xb, xv = _bf16(X)
+    wb, wv = _bf16(W)
+    Y = rt.array(np.full((M, N), np.nan, np.float32))
+    rt.gemm(BF16, rt.array(wb), rt.array(xb), BF16, Y, F32, rt.array(b), M, N, K)
+    rt.sync()
+    ref = xv.astype(np.float64) @ wv.T.astype(np.float64) + b
+    y = Y.numpy()
+    assert not np.isnan(y).any()
+    assert rel_l2(y, ref) < 1e-5
+    # and it is a bf16 product, not a wider one: the product of the unrounded operands sits well
+    # above that (bias left out, it would mask the product at small K)
+    exact = X.astype(np.float64) @ W.T.astype(np.float64)
+    assert rel_l2(y - b, exact) > 1e-3
+
+
+def test_gemm_bf16_rejects_untiled_shape(tsn, rt):
+    """bf16 operands run only on the MFMA tiling: K % 64 != 0 is refused, not computed elsewhere"""
+    Wd, Xd, Yd = rt.empty((64, 72), np.uint16), rt.empty((4, 72), np.uint16), rt.empty((4, 64))
+    with pytest.raises(tsn.TsnError) as e:
+        rt.gemm(BF16, Wd, Xd, BF16, Yd, F32, None, 4, 64, 72)
+    assert e.value.code == 3
+    with pytest.raises(tsn.TsnError) as e:   # bf16 operands give f32 Y
+        rt.gemm(BF16, rt.empty((64, 64), np.uint16), rt.empty((4, 64), np.uint16), BF16, rt.empty((4, 64), np.float16),
+                F16, None, 4, 64, 64)
+    assert e.value.code == 1
+
+
 def test_gemm_rejects_bad_shape(tsn, rt):
     Wd, Xd, Yd = rt.empty((64, 12), np.float16), rt.empty((4, 12), np.float16), rt.empty((4, 64))
     with pytest.raises(tsn.TsnError) as e:

@@ -310,6 +310,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const GemmBatch bt) {
 typedef __attribute__((address_space(3))) char lds_char;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 constexpr int CPOL_SC1 = 16;   // cache-policy bit sc1 of a buffer access: device-coherent (written through / read past L1)
 
 // raw buffer descriptor: base, stride 0, num_records 2^31-1, 32-bit data format; an offset at or
@@ -654,7 +655,7 @@ struct SkFix {
 // (stream-K), so the LDS C tile is released with a barrier at the end.
 // NSX: LDS stages (5: 160 KB, one workgroup per CU; 2: 68 KB, two workgroups per CU, for grids
 // of several rounds where the second workgroup covers the first's barrier and load waits).
-template <int EPI, bool HL, bool SEG, int NSX = NS>
+template <int EPI, bool HL, bool SEG, int NSX = NS, bool BF = false>
 __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, int kbeg, int nk, float *part, int ks,
                                           int tid, const SkFix *fx = nullptr) {
     // stage s: A tile at smem + s*STAGE, W tile at smem + (NSX + s)*STAGE; reused for the C tile
@@ -782,8 +783,13 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
 #pragma unroll
             for (int i = 0; i < 2; ++i)
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                for (int j = 0; j < 4; ++j) {
+                    if constexpr (BF)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, af[i]),
+                                                                            __builtin_bit_cast(bf16x8, bf[j]), acc[i][j], 0, 0, 0);
+                    else
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                }
         }
     };
 
@@ -911,7 +917,7 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
 // its last. With bt.sk_cnt the last contributor to arrive (per-tile counter) sums the slots in K
 // order and finishes the tile in this kernel; otherwise gemm_fixup_kernel does, in the same order
 // (deterministic for a given G either way: the sum does not depend on who arrives last).
-template <int EPI, bool HL, int NSX = NS>
+template <int EPI, bool HL, int NSX = NS, bool BF = false>
 __device__ __forceinline__ void pipe_dp(const GemmBatch &bt) {
     const int tid = threadIdx.x;
     const int wg = xcd_remap(blockIdx.x, gridDim.x);
@@ -924,7 +930,7 @@ __device__ __forceinline__ void pipe_dp(const GemmBatch &bt) {
     int tm, tn;
     tile_mn(rem, P.tiles_m, P.tiles_n, tm, tn);
     const int nk = P.K / BK / P.splits;
-    pipe_tile<EPI, HL, false, NSX>(P, tm * BM, tn * BN, ks * nk, nk, nullptr, ks, tid);
+    pipe_tile<EPI, HL, false, NSX, BF>(P, tm * BM, tn * BN, ks * nk, nk, nullptr, ks, tid);
 }
 template <int EPI>
 __global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
@@ -934,6 +940,15 @@ __global__ __launch_bounds__(512, 1) void gemm_pipe_kernel(const GemmBatch bt) {
 template <int EPI>
 __global__ __launch_bounds__(512, 1) void gemm_pipe_hl_kernel(const GemmBatch bt) {
     pipe_dp<EPI, true>(bt);
+}
+// bf16 A and W: the same tiles and schedules with bf16 MFMA products
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void gemm_pipe_bf16_kernel(const GemmBatch bt) {
+    pipe_dp<EPI, false, NS, true>(bt);
+}
+template <int EPI>
+__global__ __launch_bounds__(512, 2) void gemm_pipe2_bf16_kernel(const GemmBatch bt) {
+    pipe_dp<EPI, false, 2, true>(bt);
 }
 // two LDS stages, two workgroups per CU (grids of several rounds)
 template <int EPI>
@@ -1326,6 +1341,14 @@ void gemm_problem_init(GemmProblem &p) {
 
 int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     TSN_REQUIRE(b.nprob >= 1 && b.nprob <= 3, "gemm: 1 to 3 problems");
+    if (b.bf16) {   // one data-parallel schedule: no workspace, so no split and no stream-K
+        TSN_REQUIRE(epi == EPI_STORE && !a_f32 && !b.small, "gemm bf16: plain store epilogue, bf16 A");
+        b.ws = nullptr;
+        b.ws_bytes = 0;
+        for (int i = 0; i < b.nprob; ++i)
+            TSN_REQUIRE(!b.p[i].y_f16 && !b.p[i].w_half && !b.p[i].y_lo && b.p[i].taps == 1,
+                        "gemm bf16: one tap, f32 Y, no hi|lo operands");
+    }
     int tiles = 0;
     for (int i = 0; i < b.nprob; ++i) {
         GemmProblem &p = b.p[i];
@@ -1557,6 +1580,10 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
                                                                         : "gemm_f16_kernel<false, 2>");
     // two LDS stages and two workgroups per CU once the data-parallel grid exceeds one round
     b.ns2 = pipe && !b.sk && b.total_tiles > NCU ? 1 : 0;
+    if (b.bf16) {
+        TSN_REQUIRE(pipe, "gemm bf16: needs K % 64 == 0, N % 8 == 0 and 16-byte aligned rows, W, bias and Y");
+        b.kname = b.ns2 ? "gemm_pipe2_bf16_kernel<0>" : "gemm_pipe_bf16_kernel<0>";
+    }
     if (b.ns2 && b.hl)
         b.kname = epi == EPI_STORE ? "gemm_pipe2_hl_kernel<0>" : epi == EPI_RESID ? "gemm_pipe2_hl_kernel<1>"
                   : epi == EPI_QKV ? "gemm_pipe2_hl_kernel<2>" : "gemm_pipe2_hl_kernel<3>";
@@ -1579,6 +1606,13 @@ int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st)
         return TSN_OK;
     }
     dim3 grid(b.sk ? b.sk_g : b.total_tiles), block(b.pipe ? 512 : 256);
+    if (b.bf16) {
+        TSN_REQUIRE(b.pipe && epi == EPI_STORE, "gemm bf16: pipelined store kernel only");
+        if (b.ns2) TSN_LAUNCH((gemm_pipe2_bf16_kernel<EPI_STORE>), grid, block, 0, st, b);
+        else TSN_LAUNCH((gemm_pipe_bf16_kernel<EPI_STORE>), grid, block, 0, st, b);
+        TSN_HIP_CHECK(hipGetLastError());
+        return TSN_OK;
+    }
     if (b.pipe) {
         if (b.sk) {
             if (epi == EPI_STORE) TSN_LAUNCH((gemm_sk_kernel<EPI_STORE>), grid, block, 0, st, b);

@@ -92,6 +92,9 @@ struct GemmBatch {
     // set by gemm_plan: the two-stage kernel (gemm_pipe2_kernel, two workgroups per CU) for
     // data-parallel grids of more than one round (256 tiles)
     int ns2 = 0;
+    // nonzero: A and W hold bf16 values and the MFMAs run bf16 products (gemm_pipe_bf16_kernel /
+    // gemm_pipe2_bf16_kernel: EPI_STORE with f32 Y, one tap, data-parallel, no split)
+    int bf16 = 0;
 };
 
 // a_f32: A operand is f32 (converted to f16 on load). All problems share the epilogue kind.

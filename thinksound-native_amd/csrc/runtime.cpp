@@ -213,9 +213,25 @@ int Runtime::gemm(int wdt, const void *W, const void *X, int xdt, void *Y, int y
         q.Y = Y; q.ldy = (int)ldy; q.ymap = rowmap_dense((int)p.M); q.y_f16 = ydt == DT_F16;
         b.nprob = 1;
         return launch_gemm(b, EPI_STORE, false, st);
+    } else if (wdt == DT_BF16 && xdt == DT_BF16) {
+        // bf16 operands on MFMA (bf16 products, f32 accumulation and Y)
+        TSN_REQUIRE(ydt == DT_F32, "gemm: bf16 X and W give f32 Y");
+        GemmBatch b;
+        gemm_problem_init(b.p[0]);
+        GemmProblem &q = b.p[0];
+        q.A = X; q.lda = (int)ldx; q.amap = rowmap_dense((int)p.M);
+        q.taps = 1; q.Kc = (int)p.K; q.pad = 0; q.a_T = (int)p.M;
+        q.W = (const half_t *)W; q.ldw = (int)ldw; q.bias = bias;
+        q.M = (int)p.M; q.N = (int)p.N; q.K = (int)p.K;
+        q.Y = Y; q.ldy = (int)ldy; q.ymap = rowmap_dense((int)p.M); q.y_f16 = 0;
+        b.nprob = 1;
+        b.bf16 = 1;
+        const int rc = gemm_plan(b, EPI_STORE, false);
+        if (rc != TSN_OK) return rc == TSN_ERR_ARG ? TSN_ERR_UNSUPPORTED : rc;
+        return gemm_launch_planned(b, EPI_STORE, false, st);
     } else {
         TSN_REQUIRE(wdt == DT_F32 || wdt == DT_BF16, "gemm: weight dtype");
-        TSN_REQUIRE(xdt == DT_F32 && ydt == DT_F32, "gemm: f32/bf16 weights take f32 X and Y");
+        TSN_REQUIRE(xdt == DT_F32 && ydt == DT_F32, "gemm: f32/bf16 weights take f32 X and Y (or bf16 X with bf16 W)");
     }
     LinArgs a;
     a.X = (const float *)X; a.ldx = (int)ldx; a.xmap = rowmap_dense((int)p.M);

@@ -78,7 +78,8 @@ public:
     // Y[M,N] = X[M,K]·W[N,K]ᵀ (+bias)                              (src/net.h:24-26)
     // wdt F16, X f32: f32-accurate MFMA product (X as an f16 hi|lo pair against [W | W]), Y f32 or f16;
     //   shapes the pipelined kernel does not take run the f32 SIMT path (Y f32 only).
-    // wdt F16, X f16: plain f16 MFMA product. wdt F32 / BF16: f32 SIMT path (X, Y f32).
+    // wdt F16, X f16: plain f16 MFMA product. wdt BF16, X bf16: bf16 MFMA product (f32 Y; MFMA
+    // tiling only). wdt F32 / BF16 with X f32: f32 SIMT path (X, Y f32).
     int gemm(int wdt, const void *W, const void *X, int xdt, void *Y, int ydt, const float *bias,
              const GemmParams &p);
     // y[n] = bias[n] + W[n,:]·x                                      (src/net.h:27-28)

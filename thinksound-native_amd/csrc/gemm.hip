@@ -296,7 +296,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const GemmBatch bt) {
 // per SIMD let one wave's LDS reads hide behind the other's MFMAs.
 //
 // Operands go global -> LDS with buffer_load_dwordx4 ... lds (no register staging, see dma16) into
-// NS = 5 stages of one 128x64 A tile + one 128x64 W tile each (160 KB): four K tiles are in flight
+// NS = 4 stages of one 128x64 A tile + one 128x64 W tile each (128 KB): three K tiles are in flight
 // while the fifth is multiplied, with one barrier per K tile. The C tile is staged through LDS for
 // the epilogue (f32, pitch TP).
 //
@@ -357,7 +357,10 @@ __device__ __forceinline__ void block_barrier() {
 }
 
 constexpr int STAGE = BM * BK;   // halves per operand tile of one stage
-constexpr int NS = 5;            // LDS stages (5 x 32 KB = 160 KB): NS-1 K tiles in flight
+constexpr int NS = 4;            // LDS stages (4 x 32 KB = 128 KB): NS-1 K tiles in flight.
+                                 // Measured per 8 s evaluation: 5 stages 2.026 ms, 4 stages 1.965,
+                                 // 3 stages 1.987 (same box); a fifth stage only adds L2 traffic in
+                                 // flight, the loop is bound by the L2 -> LDS rate and the LDS port
 constexpr int TP = 132;          // pitch (floats) of the f32 C tile staged in LDS for the epilogue:
                                  // 4 rows apart = 528 floats = 16 banks apart, so MFMA-layout writes
                                  // from the 4 lane groups of a wave never collide
@@ -653,7 +656,7 @@ struct SkFix {
 // f32 [BM][BN] store of the accumulators to part (a stream-K segment, finished by the fixup kernel).
 // HL: problems may read half-width W (hi|lo A operand); SEG: more tiles follow in this workgroup
 // (stream-K), so the LDS C tile is released with a barrier at the end.
-// NSX: LDS stages (5: 160 KB, one workgroup per CU; 2: 68 KB, two workgroups per CU, for grids
+// NSX: LDS stages (4: 128 KB, one workgroup per CU; 2: 68 KB, two workgroups per CU, for grids
 // of several rounds where the second workgroup covers the first's barrier and load waits).
 template <int EPI, bool HL, bool SEG, int NSX = NS, bool BF = false>
 __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, int kbeg, int nk, float *part, int ks,
@@ -812,19 +815,9 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
         issue(NEXT, S);                                                                         \
     }
     int kt = 0;
-    if constexpr (NSX == 5) {
-        for (; kt + 2 * NSX <= nk; kt += NSX) {
-            TSN_GEMM_STEP(kt + NSX + 0, 0)
-            TSN_GEMM_STEP(kt + NSX + 1, 1)
-            TSN_GEMM_STEP(kt + NSX + 2, 2)
-            TSN_GEMM_STEP(kt + NSX + 3, 3)
-            TSN_GEMM_STEP(kt + NSX + 4, 4)
-        }
-    } else {
-        for (; kt + 2 * NSX <= nk; kt += NSX) {
+    for (; kt + 2 * NSX <= nk; kt += NSX) {
 #pragma unroll
-            for (int s2 = 0; s2 < NSX; ++s2) TSN_GEMM_STEP(kt + NSX + s2, s2)
-        }
+        for (int s2 = 0; s2 < NSX; ++s2) TSN_GEMM_STEP(kt + NSX + s2, s2)
     }
 #undef TSN_GEMM_STEP
     // tail: the last < 2*NSX tiles; tile kt is visible, kt+1..min(kt+NSX-1, nk-1) in flight
@@ -967,12 +960,13 @@ __global__ __launch_bounds__(512, 2) void gemm_pipe2_hl_kernel(const GemmBatch b
 // the workgroups with no f32 partials to write and sum.
 constexpr int SB = 64;              // tile rows and columns
 constexpr int SSTAGE = SB * BK;     // halves per operand tile of one stage (8 KB)
+constexpr int SNS = 5;              // LDS stages of the small-tile ring (5 x 16 KB)
 constexpr int STP = 68;             // pitch (floats) of the staged f32 C tile: 4 rows = 16 banks apart
 
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) {
     static_assert(EPI == EPI_RESID, "gemm_small_kernel: residual epilogue only");
-    __shared__ __attribute__((aligned(1024))) half_t smem[2 * NS * SSTAGE];
+    __shared__ __attribute__((aligned(1024))) half_t smem[2 * SNS * SSTAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wg = xcd_remap(blockIdx.x, gridDim.x);
     const int pi = (bt.nprob > 2 && wg >= bt.p[2].tile_start) ? 2 : (bt.nprob > 1 && wg >= bt.p[1].tile_start) ? 1 : 0;
@@ -1005,7 +999,7 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
         const int k = nt_k;
         nt_k += BK;
         lds_char *sa = (lds_char *)(smem + stage * SSTAGE) + wave * 2048;
-        lds_char *sb = (lds_char *)(smem + (NS + stage) * SSTAGE) + wave * 2048;
+        lds_char *sb = (lds_char *)(smem + (SNS + stage) * SSTAGE) + wave * 2048;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int ts = a_ts0[i];
@@ -1036,7 +1030,7 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
         }
     }
     auto compute = [&](int stage) {
-        const half_t *sa = smem + stage * SSTAGE, *sb = smem + (NS + stage) * SSTAGE;
+        const half_t *sa = smem + stage * SSTAGE, *sb = smem + (SNS + stage) * SSTAGE;
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
             half8 af[2], bf[2];
@@ -1053,24 +1047,24 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
         }
     };
 
-    // the K loop of pipe_tile: tile kt landed in stage kt%NS, tiles kt+1..kt+NS-1 in flight
+    // the K loop of pipe_tile: tile kt landed in stage kt%SNS, tiles kt+1..kt+SNS-1 in flight
     const int nk = P.K / BK;
     issue(0);
 #pragma unroll
-    for (int j = 1; j < NS - 1; ++j)
+    for (int j = 1; j < SNS - 1; ++j)
         if (nk > j) issue(j);
-    wait_vmcnt(4 * min(nk - 1, NS - 2));
+    wait_vmcnt(4 * min(nk - 1, SNS - 2));
     block_barrier();
-    if (nk > NS - 1) issue(NS - 1);
+    if (nk > SNS - 1) issue(SNS - 1);
 #define TSN_SMALL_STEP(S)                                                                       \
     {                                                                                           \
         compute(S);                                                                             \
-        wait_vmcnt(4 * (NS - 2));                                                               \
+        wait_vmcnt(4 * (SNS - 2));                                                               \
         block_barrier();                                                                        \
         issue(S);                                                                               \
     }
     int kt = 0;
-    for (; kt + 2 * NS <= nk; kt += NS) {
+    for (; kt + 2 * SNS <= nk; kt += SNS) {
         TSN_SMALL_STEP(0)
         TSN_SMALL_STEP(1)
         TSN_SMALL_STEP(2)
@@ -1079,12 +1073,12 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
     }
 #undef TSN_SMALL_STEP
     for (; kt < nk; ++kt) {
-        const int st = kt % NS;
+        const int st = kt % SNS;
         compute(st);
         if (kt + 1 < nk) {
-            wait_vmcnt(4 * min(nk - 2 - kt, NS - 2));
+            wait_vmcnt(4 * min(nk - 2 - kt, SNS - 2));
             block_barrier();
-            if (kt + NS < nk) issue(st);
+            if (kt + SNS < nk) issue(st);
         }
     }
     // C tile through LDS, then 16-byte residual updates: x += gate * (acc + bias)

@@ -1065,11 +1065,8 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
     }
     int kt = 0;
     for (; kt + 2 * SNS <= nk; kt += SNS) {
-        TSN_SMALL_STEP(0)
-        TSN_SMALL_STEP(1)
-        TSN_SMALL_STEP(2)
-        TSN_SMALL_STEP(3)
-        TSN_SMALL_STEP(4)
+#pragma unroll
+        for (int s2 = 0; s2 < SNS; ++s2) TSN_SMALL_STEP(s2)
     }
 #undef TSN_SMALL_STEP
     for (; kt < nk; ++kt) {

@@ -1,15 +1,16 @@
 #!/usr/bin/env python3
-"""Writes tests/golden/sampler_8s_24steps.npz: the final latent of the full rectified-flow Euler
-sampler at 8 s (src/pipeline.cpp:141-155: 24 steps, t_s = 1 - s/24, CFG 5.0, v = v_u + 5 (v_c - v_u)),
-one prompt as a cond/uncond pair (B = 2, La = 256, Lt = 141, 7 joint + 14 fused blocks, H = 1024),
-computed by the CPU oracle (oracle/, orc_dit_sample) on exactly the weights and inputs the benchmark
-times: BF16 weights N(0, 0.02) from seed 4242 (q/k norm weights N(0, 0.02) too), z0, text and pooled
-features from seed 4242, the unconditional arm with zeroed text and pooled features.
+"""Writes tests/golden/sampler_8s_24steps.npz (default) or sampler_30s_24steps.npz (argument 30s):
+the final latent of the full rectified-flow Euler sampler (src/pipeline.cpp:141-155: 24 steps,
+t_s = 1 - s/24, CFG 5.0, v = v_u + 5 (v_c - v_u)), one prompt as a cond/uncond pair (B = 2,
+Lt = 141, 7 joint + 14 fused blocks, H = 1024; La = 256 at 8 s, 960 at 30 s), computed by the CPU
+oracle (oracle/, orc_dit_sample) on exactly the weights and inputs the benchmark times: BF16
+weights N(0, 0.02) from seed 4242 (q/k norm weights N(0, 0.02) too), z0, text and pooled features
+from seed 4242, the unconditional arm with zeroed text and pooled features.
 
-The oracle takes about 3.5 minutes on 8 cores for the 24 evaluations, too long for the GPU suite;
-the fixture holds the seeds, input checksums and the expected final latent (64 KB). Run from the
-repository root after building the oracle (make -C oracle):
-    python3 tests/golden/make_sampler_golden.py
+The oracle takes about 3.5 minutes (8 s) or 20 minutes (30 s) on 8 cores for the 24 evaluations,
+too long for the GPU suite; the fixture holds the seeds, input checksums and the expected final
+latent (64 KB / 240 KB). Run from the repository root after building the oracle (make -C oracle):
+    python3 tests/golden/make_sampler_golden.py [8s|30s]
 """
 import importlib
 import os
@@ -23,13 +24,16 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
 
 SEED, NORM_MEAN, STEPS, CFG = 4242, 0.0, 24, 5.0
-OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "sampler_8s_24steps.npz")
+WORKLOADS = {"8s": (2, "sampler_8s_24steps.npz"), "30s": (3, "sampler_30s_24steps.npz")}   # default_spec index
 
 
 def main():
     tsn = importlib.import_module("thinksound-native_amd")
     import pyoracle
-    spec = tsn.default_spec(2)
+    which = sys.argv[1] if len(sys.argv) > 1 else "8s"
+    idx, name = WORKLOADS[which]
+    OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), name)
+    spec = tsn.default_spec(idx)
     w16 = tsn.synth_weights(spec, SEED, NORM_MEAN)
     inp = tsn.synth_inputs(spec, SEED, cfg_pairs=True)
     x0 = inp["z"][0::2].copy()

@@ -4,8 +4,12 @@ specified synthetic generator:
 
   * CLIP at the reference's full size (24 layers, H = 1024, 16 heads, 77 tokens, vocabulary 49408):
     per-token features and the pooled vector within rel-L2 1e-4;
-  * T5 at the reference's widths (d = 2048, d_ff = 5120, 32 heads, 77 tokens, vocabulary 32128) with 4
-    of its 24 layers (the layers repeat the same kernels), padded ids: within 1e-4;
+  * T5 at the reference's widths (d = 2048, d_ff = 5120, 32 heads, 77 tokens, vocabulary 32128),
+    padded ids: with 4 of its 24 layers within 1e-4; at the full 24 layers (1.2 G f32 weights,
+    about 30 s of host work) within 2e-3. Random-init T5 amplifies rounding-level differences with
+    depth: perturbing every weight by 6e-8 relative (half an f32 ulp) moves the f32 oracle's own
+    output by 5.4e-6 at 4 layers, 5.6e-5 at 12 and 4.2e-4 at 24 (measured), so at full depth two
+    correct f32 implementations that only sum in different orders differ by that much;
   * small widths for both, with an end-of-text token in the middle of the context (CLIP) and
     padding (T5);
   * bit-identical reruns; a GGUF load (F32 tensors) encodes bit-identically to the flat upload.
@@ -60,11 +64,15 @@ def test_clip_parity(tsn, rt, orc, size):
         m.close()
 
 
-@pytest.mark.parametrize("size", ["full_width", "small"])
+@pytest.mark.parametrize("size", ["full", "full_width_4_layers", "small"])
 def test_t5_parity(tsn, rt, orc, size):
-    spec = tsn.t5_spec_default().copy(NL=4)
+    spec = tsn.t5_spec_default()
+    tol = 2e-3 if size == "full" else TOL
+    if size == "full_width_4_layers":
+        spec = spec.copy(NL=4)
     if size == "small":
         spec = spec.copy(d=256, d_ff=320, NL=3, NH=4, ctx=19, vocab=200)
+    print("t5 %s: synthesising %d layers of weights" % (size, spec.NL), flush=True)
     w = tsn.t5_synth_weights(spec, 22)
     m = tsn.T5Model(rt, spec)
     try:
@@ -73,10 +81,11 @@ def test_t5_parity(tsn, rt, orc, size):
         out = rt.empty((spec.ctx, spec.d))
         m.encode(ids, out)
         rt.sync()
+        print("t5 %s: oracle" % size, flush=True)
         ref = orc.t5_encode(spec.as_dict(), w, ids)
         e = rel_l2(out.numpy(), ref)
         print("t5 %s: rel-L2 %.3g, max |ref| %.3g" % (size, e, np.abs(ref).max()))
-        assert e <= TOL
+        assert e <= tol
         out2 = rt.empty((spec.ctx, spec.d))
         m.encode(ids, out2)
         rt.sync()

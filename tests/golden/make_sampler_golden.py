@@ -7,9 +7,9 @@ oracle (oracle/, orc_dit_sample) on exactly the weights and inputs the benchmark
 weights N(0, 0.02) from seed 4242 (q/k norm weights N(0, 0.02) too), z0, text and pooled features
 from seed 4242, the unconditional arm with zeroed text and pooled features.
 
-The oracle takes about 3.5 minutes (8 s) or 20 minutes (30 s) on 8 cores for the 24 evaluations,
+The oracle takes about 3.5 minutes (8 s) or 42 minutes (30 s) on 8 cores for the 24 evaluations,
 too long for the GPU suite; the fixture holds the seeds, input checksums and the expected final
-latent (64 KB / 240 KB). Run from the repository root after building the oracle (make -C oracle):
+latent and z0 (130 KB / 490 KB). Run from the repository root after building the oracle (make -C oracle):
     python3 tests/golden/make_sampler_golden.py [8s|30s]
 """
 import importlib

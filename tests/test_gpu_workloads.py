@@ -5,7 +5,8 @@ weights and inputs:
   * batch 16: 8 prompts x CFG at 8 s (La=256, Lt=141) — large-M GEMMs, 16-row GEMVs.
 
 Bars as for the 8 s evaluation: velocity rel-L2 <= 1e-3, every block output <= 2e-3; the batch-16
-sampler step (8 cond/uncond pairs) <= 2e-3 on the displacement.
+sampler step (8 cond/uncond pairs) and the whole 24-step 30 s sampler (against a committed oracle
+fixture) <= 2e-3 on the displacement.
 """
 import numpy as np
 import pytest
@@ -78,5 +79,40 @@ def test_batch16_sampler_step_and_graph_replays(tsn, rt, orc):
             assert np.array_equal(out.view(np.uint32), x2.numpy().view(np.uint32))
             m.forward_ex(dev["z"], dev["t"], dev["text"], dev["pooled"], scratch)
             rt.sync()
+    finally:
+        m.close()
+
+
+def test_sampler_30s_24_steps_against_fixture(tsn, rt):
+    """The whole 24-step CFG sampler on the 30 s workload (La=960, S=1101, one prompt as a
+    cond/uncond pair) on the benchmark's weights (every weight N(0, 0.02), seed 4242) against the
+    oracle's final latent (tests/golden/sampler_30s_24steps.npz, written by make_sampler_golden.py
+    30s; the oracle needs about 42 minutes for it): displacement x - z0 within rel-L2 2e-3, eager
+    and graph-captured runs bit-identical."""
+    import os
+    spec = tsn.default_spec(3)
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "sampler_30s_24steps.npz"))
+    assert int(g["seeds"][0]) == 4242 and int(g["seeds"][1]) == 24 and float(g["norm_mean"]) == 0.0
+    w16 = tsn.synth_weights(spec, 4242, 0.0)
+    assert np.isclose(tsn.bf16_to_f32(w16).astype(np.float64).sum(), float(g["w_checksum"]), rtol=0, atol=1e-6)
+    m = tsn.DitModel(rt, spec)
+    try:
+        m.upload_weights(w16)
+        inp = tsn.synth_inputs(spec, 4242, cfg_pairs=True)
+        dev = {k: rt.array(v) for k, v in inp.items()}
+        x0 = inp["z"][0::2].copy()
+        assert np.array_equal(x0, g["x0"])
+        x = rt.array(x0)
+        m.sample(x, dev["text"], dev["pooled"], 24, float(g["cfg"]))
+        rt.sync()
+        out = x.numpy()
+        err = rel_l2(out - x0, g["x"] - x0)
+        print("30 s 24-step sampler: displacement rel-L2 %.3g, final latent rel-L2 %.3g" % (err, rel_l2(out, g["x"])))
+        assert err <= 2e-3
+        x2 = rt.array(x0)
+        m.capture_sample(x2, dev["text"], dev["pooled"], 24, float(g["cfg"]))
+        m.replay()
+        rt.sync()
+        assert np.array_equal(out.view(np.uint32), x2.numpy().view(np.uint32))
     finally:
         m.close()

@@ -380,11 +380,7 @@ __device__ __forceinline__ void add8(float (&v)[8], const float *p) {
 }
 
 // snake activation (shaders/ops_conv.metal:204-213) with exp(alpha) and exp(-beta) precomputed per column
-__device__ __forceinline__ void snake8(float (&v)[8], const float *ea, const float *eb) {
-    const float4 a0 = *(const float4 *)ea, a1 = *(const float4 *)(ea + 4);
-    const float4 b0 = *(const float4 *)eb, b1 = *(const float4 *)(eb + 4);
-    const float a[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-    const float b[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+__device__ __forceinline__ void snake8(float (&v)[8], const float (&a)[8], const float (&b)[8]) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         v[e] = v[e] + snake_sin2(v[e] * a[e]) * b[e];
@@ -468,15 +464,27 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             }
         }
     } else if constexpr (EPI == EPI_SNAKE) {
+        // the thread's 8 columns are the same in every pass: bias and snake table loaded once, before
+        // any store (inside the loop each load would wait for the previous pass's store, which may
+        // alias it)
+        const int col = (tid & 15) * 8, n = n0 + col;
+        float bv[8], ea[8], eb[8];
+        if (n < N) {
+            if (P.bias) load8(P.bias + n, bv);
+            load8(P.snake + n, ea);
+            load8(P.snake + N + n, eb);
+        }
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-            const int c = tid + 512 * p, row = c >> 4, col = (c & 15) * 8;
-            const int m = m0 + row, n = n0 + col;
+            const int row = (tid >> 4) + 32 * p;
+            const int m = m0 + row;
             if (m >= M || n >= N) continue;
             float v[8];
             ldsum8(tile, row * TP + col, v);
-            if (P.bias) add8(v, P.bias + n);
-            snake8(v, P.snake + n, P.snake + N + n);
+            if (P.bias)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] += bv[e];
+            snake8(v, ea, eb);
             half8 hi, lo;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -489,23 +497,37 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             *(half8 *)(y + P.y_hi2) = hi;
         }
     } else if constexpr (EPI == EPI_RSNAKE) {
+        // bias and snake table as in EPI_SNAKE; the stream rows of all four passes are read before
+        // the first store
+        const int col = (tid & 15) * 8, n = n0 + col;
+        float bv[8], ea[8], eb[8], xr[4][8];
+        if (n < N) {
+            if (P.bias) load8(P.bias + n, bv);
+            load8(P.snake + n, ea);
+            load8(P.snake + N + n, eb);
+        }
 #pragma unroll
         for (int p = 0; p < 4; ++p) {
-            const int c = tid + 512 * p, row = c >> 4, col = (c & 15) * 8;
-            const int m = m0 + row, n = n0 + col;
+            const int m = m0 + (tid >> 4) + 32 * p;
+            if (P.r_add && m < M && n < N) load8(P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n, xr[p]);
+        }
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            const int row = (tid >> 4) + 32 * p;
+            const int m = m0 + row;
             if (m >= M || n >= N) continue;
             float v[8];
             ldsum8(tile, row * TP + col, v);
-            if (P.bias) add8(v, P.bias + n);
+            if (P.bias)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] += bv[e];
+            if (P.r_add)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] += xr[p][e];
             float *x = P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n;
-            if (P.r_add) {
-                const float4 x0 = *(const float4 *)x, x1 = *(const float4 *)(x + 4);
-                v[0] += x0.x; v[1] += x0.y; v[2] += x0.z; v[3] += x0.w;
-                v[4] += x1.x; v[5] += x1.y; v[6] += x1.z; v[7] += x1.w;
-            }
             *(float4 *)x = make_float4(v[0], v[1], v[2], v[3]);
             *(float4 *)(x + 4) = make_float4(v[4], v[5], v[6], v[7]);
-            snake8(v, P.snake + n, P.snake + N + n);
+            snake8(v, ea, eb);
             half8 hi, lo;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {

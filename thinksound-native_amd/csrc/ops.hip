@@ -32,13 +32,20 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const LnArgs a) {
     if (si >= a.nseg) return;
     const LnSeg &S = a.seg[si];
     const float *x = S.X + rowmap_phys(S.xmap, v) * (long long)S.ldx;
-    float4 xv[NV];
-    float sum = 0.0f;
+    float4 xv[NV], sh[NV], scl[NV];
+#pragma unroll
+    for (int c = 0; c < NV; ++c) xv[c] = *(const float4 *)(x + c * 256 + lane * 4);
+    // the modulation rows are loaded with the row, not after its statistics: one global latency
+    const int b = v / S.mod_L;
+    const float *mb = S.mod + (long long)b * S.mod_ld;
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
-        xv[c] = *(const float4 *)(x + c * 256 + lane * 4);
-        sum += (xv[c].x + xv[c].y) + (xv[c].z + xv[c].w);
+        sh[c] = *(const float4 *)(mb + S.shift_off + c * 256 + lane * 4);
+        scl[c] = *(const float4 *)(mb + S.scale_off + c * 256 + lane * 4);
     }
+    float sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NV; ++c) sum += (xv[c].x + xv[c].y) + (xv[c].z + xv[c].w);
     const float inv_h = 1.0f / (float)(NV * 256);
     const float mean = wave_sum(sum) * inv_h;
     float var = 0.0f;
@@ -49,18 +56,14 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const LnArgs a) {
     }
     var = wave_sum(var) * inv_h;
     const float inv = 1.0f / sqrtf(var + a.eps);
-    const int b = v / S.mod_L;
-    const float *mb = S.mod + (long long)b * S.mod_ld;
     const long long yrow = rowmap_phys(S.ymap, v) * (long long)S.ldy;
 #pragma unroll
     for (int c = 0; c < NV; ++c) {
         const int col = c * 256 + lane * 4;
-        const float4 sh = *(const float4 *)(mb + S.shift_off + col);
-        const float4 scl = *(const float4 *)(mb + S.scale_off + col);
-        const float y0 = (xv[c].x - mean) * inv * (1.0f + scl.x) + sh.x;
-        const float y1 = (xv[c].y - mean) * inv * (1.0f + scl.y) + sh.y;
-        const float y2 = (xv[c].z - mean) * inv * (1.0f + scl.z) + sh.z;
-        const float y3 = (xv[c].w - mean) * inv * (1.0f + scl.w) + sh.w;
+        const float y0 = (xv[c].x - mean) * inv * (1.0f + scl[c].x) + sh[c].x;
+        const float y1 = (xv[c].y - mean) * inv * (1.0f + scl[c].y) + sh[c].y;
+        const float y2 = (xv[c].z - mean) * inv * (1.0f + scl[c].z) + sh[c].z;
+        const float y3 = (xv[c].w - mean) * inv * (1.0f + scl[c].w) + sh[c].w;
         if constexpr (YMODE == LN_F16) {
             *(half4 *)((half_t *)S.Y + yrow + col) = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
         } else if constexpr (YMODE == LN_F16_HILO) {

@@ -1001,6 +1001,24 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
     const i32x4 rsa = make_rsrc(P.A);
     const i32x4 rsb = make_rsrc(P.W);
 
+    // The epilogue's operands (bias, gate rows and the stream rows this thread updates: columns
+    // (tid & 7)*8 .. +7 of rows (tid >> 3) and + 32) do not depend on the product: they are read
+    // here and arrive during the K loop. Read after it, each of the two passes would wait for a
+    // global load, the second behind the first pass's store (the pointers may alias).
+    const int ecol = (tid & 7) * 8, en = n0 + ecol;
+    float eb[8], eg[2][8], ex[2][8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) eb[e] = 0.0f;
+    if (P.bias && en < N) load8(P.bias + en, eb);
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int m = m0 + (tid >> 3) + 32 * p;
+        if (m < M && en < N) {
+            load8(P.gate + (long long)(m / P.gate_L) * P.gate_ld + en, eg[p]);
+            load8(P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + en, ex[p]);
+        }
+    }
+
     // loader rows of this lane: wave*16 + i*8 + (lane >> 3), 16-byte chunk (lane & 7) ^ (lane >> 3)
     const int lr = lane >> 3, lc = (lane & 7) ^ lr;
     int a_base[2], a_ts0[2], b_off[2];
@@ -1115,20 +1133,19 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
     block_barrier();
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
-        const int c = tid + 256 * p, row = c >> 3, col = (c & 7) * 8;
-        const int m = m0 + row, n = n0 + col;
+        const int row = (tid >> 3) + 32 * p, col = ecol;
+        const int m = m0 + row, n = en;
         if (m >= M || n >= N) continue;
         float v[8];
         load8(tile + row * STP + col, v);
-        if (P.bias) add8(v, P.bias + n);
-        const float *g = P.gate + (long long)(m / P.gate_L) * P.gate_ld + n;
+        if (P.bias)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] += eb[e];
         float *x = P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n;
-        const float4 g0 = *(const float4 *)g, g1 = *(const float4 *)(g + 4);
-        float4 x0 = *(float4 *)x, x1 = *(float4 *)(x + 4);
-        x0.x = x0.x + v[0] * g0.x; x0.y = x0.y + v[1] * g0.y; x0.z = x0.z + v[2] * g0.z; x0.w = x0.w + v[3] * g0.w;
-        x1.x = x1.x + v[4] * g1.x; x1.y = x1.y + v[5] * g1.y; x1.z = x1.z + v[6] * g1.z; x1.w = x1.w + v[7] * g1.w;
-        *(float4 *)x = x0;
-        *(float4 *)(x + 4) = x1;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ex[p][e] = ex[p][e] + v[e] * eg[p][e];
+        *(float4 *)x = make_float4(ex[p][0], ex[p][1], ex[p][2], ex[p][3]);
+        *(float4 *)(x + 4) = make_float4(ex[p][4], ex[p][5], ex[p][6], ex[p][7]);
     }
 }
 

@@ -297,7 +297,7 @@ __global__ __launch_bounds__(256, 2) void gemm_f16_kernel(const GemmBatch bt) {
 //
 // Operands go global -> LDS with buffer_load_dwordx4 ... lds (no register staging, see dma16) into
 // NS = 4 stages of one 128x64 A tile + one 128x64 W tile each (128 KB): three K tiles are in flight
-// while the fifth is multiplied, with one barrier per K tile. The C tile is staged through LDS for
+// while the fourth is multiplied, with one barrier per K tile. The C tile is staged through LDS for
 // the epilogue (f32, pitch TP).
 //
 // LDS layout of a stage: row r (128 B = 8 chunks of 8 halves) keeps chunk c at slot c ^ (r & 7).

@@ -332,7 +332,7 @@ def test_elementwise(tsn, rt, orc):
     assert np.array_equal(yy.numpy(), orc.add_bcast_col(X, v))
 
 
-@pytest.mark.parametrize("S", [397, 1101, 1, 64, 65])
+@pytest.mark.parametrize("S", [397, 1101, 1, 64, 65, 100, 500, 512])
 def test_attention(tsn, rt, orc, S):
     r = rng(61 + S)
     H, nh, hd = 1024, 16, 64

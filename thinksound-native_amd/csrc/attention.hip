@@ -7,10 +7,12 @@
 //
 // 8 waves: wave w serves queries 16*(w&3)..+15; waves 0-3 take the even 64-key blocks and waves
 // 4-7 the odd ones, each half keeping its own running max / sum / output, merged through LDS at
-// the end. K and Vᵀ blocks reach LDS by direct-to-LDS buffer loads (no register staging) into a
-// ring of 4 stages x 2 blocks (128 KB); at S <= 512 all of them are loaded at once and the key
-// loop runs without barriers. The running max is shared by the four lanes holding a query's keys
-// (row-swap permutes); the running sum is an MFMA product of the probabilities with ones.
+// the end. K and Vᵀ blocks reach LDS by direct-to-LDS buffer loads (no register staging). At
+// S <= 512 all of them (128 KB) are loaded at once, every K block before the Vᵀ blocks are needed,
+// and each half's key loop is software-pipelined (the next block's scores are multiplied before
+// this block's PV product); longer contexts use a two-stage ring. The running max is shared by the
+// four lanes holding a query's keys (row-swap permutes); the running sum is an MFMA product of the
+// probabilities with ones.
 //
 // MFMA formulation (v_mfma_f32_16x16x32_f16; A row = lane&15, B col = lane&15, K group = lane>>4,
 // D[4*(lane>>4)+r][lane&15]):
@@ -103,6 +105,18 @@ __device__ __forceinline__ void lazy_max(float &m_i, float m_blk, floatx4 (&o)[4
         lsum *= alpha;
     }
 }
+// The same reference update without the branch: a lane whose maximum does not move keeps
+// alpha = 1 exactly, so the values are those of lazy_max. One exp2 and 20 multiplies per block;
+// the block's instructions stay one basic block, so the next block's score products can be
+// scheduled among them.
+__device__ __forceinline__ void lazy_max_sel(float &m_i, float m_blk, floatx4 (&o)[4], floatx4 &lsum) {
+    const bool up = m_blk > m_i + 8.0f;
+    const float alpha = up ? __builtin_amdgcn_exp2f(m_i - m_blk) : 1.0f;
+    m_i = up ? m_blk : m_i;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+    lsum *= alpha;
+}
 
 __device__ inline int attn_xcd_remap(int bid, int nwg) {
     const int xcd = bid & 7, idx = bid >> 3;
@@ -110,12 +124,13 @@ __device__ inline int attn_xcd_remap(int bid, int nwg) {
     return (xcd < rem ? xcd * (base + 1) : rem * (base + 1) + (xcd - rem) * base) + idx;
 }
 
-// NSTG ring stages of two key blocks each: 4 (128 KB, one workgroup per CU; up to 512 keys load
-// at once) or 2 (64 KB, two workgroups per CU, one pair of key blocks in flight while the other is
-// multiplied; for longer contexts, where the second workgroup covers the load latency)
+// NSTG stages of two key blocks each: 4 (128 KB, one workgroup per CU; up to 512 keys, all loaded
+// at once) or 2 (a 64 KB ring, two workgroups per CU, one pair of key blocks in flight while the
+// other is multiplied; for longer contexts, where the second workgroup covers the load latency)
 template <int NSTG>
 __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(const AttnArgs a) {
-    __shared__ __attribute__((aligned(1024))) half_t smem[NSTG * ASTAGE];
+    // NSTG stages of two key blocks, then the 64-row query tile (resident path)
+    __shared__ __attribute__((aligned(1024))) half_t smem[NSTG * ASTAGE + 4096];
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar DMA choices
     const int half = wave >> 2, wq = wave & 3;
@@ -133,9 +148,6 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
     const int q = qt * 64 + wq * 16 + (lane & 15);
     const int g = lane >> 4;
     half8 qf[2];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-        qf[ks] = q < S ? *(const half8 *)(Qp + (long long)q * 64 + ks * 32 + g * 8) : zero_h8();
 
     const int nkb = (S + AKB - 1) / AKB;
     const int npair = (nkb + 1) / 2;
@@ -220,15 +232,144 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
         }
     };
 
-    if (npair <= NSTG) {
-        // every key block fits the ring: load all, one wait, no barrier inside the loop
-        for (int p = 0; p < npair; ++p) issue(p, p);
-        wait_vmcnt(0);
+    if constexpr (NSTG == 4) {
+        // Every key block fits (S <= 512; the launcher takes this kernel only then). Wave w loads rows 8w..8w+7 of the query tile, then
+        // the K rows of key block w, then its Vt columns (16 bytes per lane, the ring's layout:
+        // block b in stage b >> 1, K at part b & 1, Vt at part 2 + (b & 1)); blocks past the last
+        // read as zero, so every wave issues 17 loads. Waiting for all but the last 8 (vmcnt 8)
+        // covers the queries and the K blocks: each half multiplies its first key block and forms
+        // its probabilities while the Vt blocks still land.
+        half_t *sQ = smem + NSTG * ASTAGE;
+        {
+            const int qrow = qt * 64 + wave * 8 + lr;
+            const int lc = (lane & 7) ^ lr ^ wave;
+            dma16(make_rsrc(Qp), qrow < S ? (unsigned)((qrow * 64 + lc * 8) * 2) : 0x80000000u,
+                  (lds_char *)(sQ + wave * 512));
+        }
+        // (the ring holds 2*NSTG key blocks: waves past that load only their query rows)
+        const int kb = wave;
+        const bool kv = kb < 2 * NSTG;
+        if (kv) {
+#pragma unroll
+            for (int sub = 0; sub < 8; ++sub) {
+                const int lc = (lane & 7) ^ lr ^ sub, key = kb * AKB + sub * 8 + lr;
+                dma16(rk, key < S ? (unsigned)((key * 64 + lc * 8) * 2) : 0x80000000u,
+                      (lds_char *)(smem + (kb >> 1) * ASTAGE + (kb & 1) * 4096 + sub * 512));
+            }
+#pragma unroll
+            for (int sub = 0; sub < 8; ++sub) {
+                const int lc = (lane & 7) ^ lr ^ sub;
+                dma16(rv, kb < nkb ? (unsigned)(((sub * 8 + lr) * Sp + kb * AKB + lc * 8) * 2) : 0x80000000u,
+                      (lds_char *)(smem + (kb >> 1) * ASTAGE + (2 + (kb & 1)) * 4096 + sub * 512));
+            }
+        }
+        wait_vmcnt(kv ? 8 : 0);
         block_barrier();
-        for (int p = 0; p < npair; ++p)
-            if (2 * p + half < nkb) compute(p, 2 * p + half);
-    } else if constexpr (NSTG == 2) {
+        {
+            const int r = wq * 16 + (lane & 15);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) qf[ks] = *(const half8 *)(sQ + r * 64 + (((ks * 4 + g) ^ sw(r)) * 8));
+        }
+        // scores of key block blk for the first NJ 16-key MFMA blocks (NJ = 4: all 64 keys, 2: the
+        // first 32), layout as in compute()
+        auto qk = [&](int blk, int nj, floatx4 (&sc)[4]) {
+            const half_t *sK = smem + (blk >> 1) * ASTAGE + (blk & 1) * 4096;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                sc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                if (j < nj) {
+                    const int i = lane & 15;
+                    const int r = 32 * (j >> 1) + 8 * (i >> 2) + 4 * (j & 1) + (i & 3);
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        const half8 kf = *(const half8 *)(sK + r * 64 + (((ks * 4 + g) ^ sw(r)) * 8));
+                        sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], sc[j], 0, 0, 0);
+                    }
+                }
+            }
+        };
+        // probabilities of keys < lim (the block's valid keys) as the PV product's B operands
+        auto softmax = [&](floatx4 (&sc)[4], int nj, int lim, half8 (&pf)[2]) {
+            if (lim < AKB) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (32 * (j >> 1) + 8 * g + 4 * (j & 1) + r >= lim) sc[j][r] = -INFINITY;
+            }
+            float mx = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (j < nj) mx = fmaxf(fmaxf(mx, fmaxf(sc[j][0], sc[j][1])), fmaxf(sc[j][2], sc[j][3]));
+            lazy_max_sel(m_i, rows_max(mx) * scale, o, lsum);
+            half_t ph[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    ph[j][r] = j < nj ? (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r], scale, -m_i)) : (half_t)0.0f;
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+                pf[c] = half8{ph[2 * c][0], ph[2 * c][1], ph[2 * c][2], ph[2 * c][3],
+                              ph[2 * c + 1][0], ph[2 * c + 1][1], ph[2 * c + 1][2], ph[2 * c + 1][3]};
+        };
+        auto pv = [&](int blk, int nc, const half8 (&pf)[2]) {
+            const half_t *sV = smem + (blk >> 1) * ASTAGE + 8192 + (blk & 1) * 4096;
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                if (c < nc) {
+#pragma unroll
+                    for (int dt = 0; dt < 4; ++dt) {
+                        const int d = dt * 16 + (lane & 15);
+                        const half8 vf = *(const half8 *)(sV + d * 64 + (((c * 4 + g) ^ sw(d)) * 8));
+                        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[c], o[dt], 0, 0, 0);
+                    }
+                    lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[c], lsum, 0, 0, 0);
+                }
+            }
+        };
+        // full key blocks half, half + 2, ... < nfull; the partial last block (if any) goes to the
+        // half of its parity and runs after them, on 32 keys when it has no more
+        const int nfull = S / AKB, lim_t = S - nfull * AKB;
+        const int nf = (nfull - half + 1) >> 1;
+        const bool own_tail = lim_t > 0 && (nfull & 1) == half;
+        half8 pf[2];
+        if (nf > 0) {
+            floatx4 sc[4];
+            qk(half, 4, sc);
+            softmax(sc, 4, AKB, pf);
+        }
+        wait_vmcnt(0);
+        block_barrier();   // every Vt block visible
+        if (nf > 0) {
+            // the next block's score products are issued before this block's PV products; its
+            // probabilities (after the rescale that follows this block's PV) come last
+            for (int i = 0; i + 1 < nf; ++i) {
+                const int blk = half + 2 * i;
+                floatx4 sn[4];
+                qk(blk + 2, 4, sn);
+                pv(blk, 2, pf);
+                softmax(sn, 4, AKB, pf);
+            }
+            pv(half + 2 * (nf - 1), 2, pf);
+        }
+        if (own_tail) {
+            floatx4 sc[4];
+            if (lim_t <= 32) {
+                qk(nfull, 2, sc);
+                softmax(sc, 2, lim_t, pf);
+                pv(nfull, 1, pf);
+            } else {
+                qk(nfull, 4, sc);
+                softmax(sc, 4, lim_t, pf);
+                pv(nfull, 2, pf);
+            }
+        }
+    } else {
         // two stages: pair p + 1 lands while pair p is multiplied
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            qf[ks] = q < S ? *(const half8 *)(Qp + (long long)q * 64 + ks * 32 + g * 8) : zero_h8();
         issue(0, 0);
         wait_vmcnt(0);
         block_barrier();
@@ -240,24 +381,6 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
                 wait_vmcnt(0);      // pair p + 1, the only one in flight, has landed
                 block_barrier();    // and every wave is done with stage st
                 if (p + 2 < npair) issue(p + 2, st);
-            }
-        }
-    } else {
-        // ring over pairs of key blocks, as in the GEMM: pair p in stage p % NSTG
-        static_assert(NSTG == 4, "four-stage ring");
-        issue(0, 0);
-        issue(1, 1);
-        issue(2, 2);
-        wait_vmcnt(8);
-        block_barrier();
-        issue(3, 3);
-        for (int p = 0; p < npair; ++p) {
-            const int st = p % NSTG;
-            if (2 * p + half < nkb) compute(st, 2 * p + half);
-            if (p + 1 < npair) {
-                wait_vmcnt(4 * min(npair - 2 - p, 2));
-                block_barrier();
-                if (p + NSTG < npair) issue(p + NSTG, st);
             }
         }
     }

@@ -593,9 +593,10 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
                 float ss = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
-                ss += __shfl_xor(ss, 1);
-                ss += __shfl_xor(ss, 2);
-                ss += __shfl_xor(ss, 4);
+                // partners 1, 2 (quad permutes) and 4 (row half-mirror) apart, by DPP
+                ss += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(ss), 0xB1, 0xF, 0xF, true));
+                ss += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(ss), 0x4E, 0xF, 0xF, true));
+                ss += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(ss), 0x141, 0xF, 0xF, true));
                 const float inv = 1.0f / sqrtf(ss / 64.0f + P.rms_eps);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = v[e] * inv * nwv[e];

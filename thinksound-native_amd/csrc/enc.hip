@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include "kernels.h"
+#include "dpp.h"
 
 namespace tsn {
 
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(256) void enc_norm_kernel(const float *__restrict__
     const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float *xr = x + (long long)row * H;
     auto block_sum = [&](float v) {
-        for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+        v = wave_sum(v);
         __syncthreads();   // part[] free from the previous reduction
         if (lane == 0) part[wave] = v;
         __syncthreads();
@@ -253,14 +254,14 @@ __global__ __launch_bounds__(256) void enc_attn_kernel(const EncAttnArgs a) {
             float *pr = P + r * EA_PP;
             float mx = -INFINITY;
             for (int k = lane; k < S; k += 64) mx = fmaxf(mx, pr[k]);
-            for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+            mx = wave_max(mx);
             float sum = 0.0f;
             for (int k = lane; k < S; k += 64) {
                 const float e = expf(pr[k] - mx);
                 pr[k] = e;
                 sum += e;
             }
-            for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+            sum = wave_sum(sum);
             const float inv = 1.0f / sum;
             for (int k = lane; k < S; k += 64) pr[k] *= inv;
         }

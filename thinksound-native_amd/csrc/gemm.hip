@@ -16,6 +16,7 @@
 // workgroup ID) receives one contiguous range of tiles, and tiles are numbered n-major, so the
 // workgroups of one XCD share W column blocks in that XCD's L2.
 #include "kernels.h"
+#include "dpp.h"
 #include "snake.h"
 
 #include <string.h>
@@ -117,10 +118,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmProblem &P, floatx4 (&ac
                     float ss = 0.0f;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) ss += v[i][j][r] * v[i][j][r];
-                    ss += __shfl_xor(ss, 1);
-                    ss += __shfl_xor(ss, 2);
-                    ss += __shfl_xor(ss, 4);
-                    ss += __shfl_xor(ss, 8);
+                    ss = row16_sum(ss);
                     const float inv = 1.0f / sqrtf(ss / 64.0f + P.rms_eps);
 #pragma unroll
                     for (int j = 0; j < 4; ++j) v[i][j][r] = v[i][j][r] * inv * w[j];
@@ -135,7 +133,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmProblem &P, floatx4 (&ac
                     const bool rot = (m < M) && t < P.rope_len;
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
-                        const float partner = __shfl_xor(v[i][j][r], 1);
+                        const float partner = dpp_mov<DPP_XOR1>(v[i][j][r]);
                         if (rot) {
                             const int pj = (j * 16 + dl) >> 1;
                             const float cs = P.rope[(t * 32 + pj) * 2], sn = P.rope[(t * 32 + pj) * 2 + 1];
@@ -593,10 +591,10 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
                 float ss = 0.0f;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
-                // partners 1, 2 (quad permutes) and 4 (row half-mirror) apart, by DPP
-                ss += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(ss), 0xB1, 0xF, 0xF, true));
-                ss += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(ss), 0x4E, 0xF, 0xF, true));
-                ss += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(ss), 0x141, 0xF, 0xF, true));
+                // partners 1, 2 (quad permutes) and 4 (row half-mirror) lanes apart
+                ss += dpp_mov<DPP_XOR1>(ss);
+                ss += dpp_mov<DPP_XOR2>(ss);
+                ss += dpp_mov<DPP_HALF_MIRROR>(ss);
                 const float inv = 1.0f / sqrtf(ss / 64.0f + P.rms_eps);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = v[e] * inv * nwv[e];

@@ -8,6 +8,7 @@
 //   f32 weights: x as three parts [hi | lo | hi] against [W_hi | W_hi | W_lo]
 //   (hi·W_hi + lo·W_hi + hi·W_lo; the dropped lo·W_lo term is below 2^-22 relative).
 #include "kernels.h"
+#include "dpp.h"
 
 namespace tsn {
 
@@ -106,16 +107,14 @@ __global__ __launch_bounds__(256) void ln_plain_kernel(const float *x, float *y,
     const float *r = x + (long long)row * H;
     float s = 0.0f;
     for (int c = lane; c < H; c += 64) s += r[c];
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o);
+    s = wave_sum(s);
     const float mean = s / (float)H;
     float q = 0.0f;
     for (int c = lane; c < H; c += 64) {
         const float d = r[c] - mean;
         q += d * d;
     }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) q += __shfl_xor(q, o);
+    q = wave_sum(q);
     const float inv = 1.0f / sqrtf(q / (float)H + eps);
     float *o = y + (long long)row * H;
     for (int c = lane; c < H; c += 64) o[c] = (r[c] - mean) * inv;

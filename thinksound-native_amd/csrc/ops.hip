@@ -3,9 +3,11 @@
 // N=64 output projections, the sampler update, format conversions, and the reference-surface
 // elementwise ops.
 //
-// Reductions are wave-level butterflies (__shfl_xor), so every lane ends with the same value and
-// the order is fixed: reruns are bit-identical. No float atomics anywhere.
+// Reductions are wave-level butterflies (DPP and row-swap permutes, dpp.h; the GEMV's
+// reduce-scatter by __shfl_xor), so every lane ends with the same value and the order is fixed:
+// reruns are bit-identical. No float atomics anywhere.
 #include "kernels.h"
+#include "dpp.h"
 
 #include <string.h>
 
@@ -13,27 +15,6 @@ namespace tsn {
 
 namespace {
 
-// Sum over the wave, the same in every lane. Partners 1 and 2 apart by DPP quad permutes, then 4 and
-// 8 by the row half-mirror and mirror (each quad / half-row already holds one value), then across
-// the four 16-lane rows with the gfx950 row-swap permutes: VALU data movement only, no LDS round
-// trip. Every step adds two values, so the partner lanes compute the same sum and the order is
-// fixed: reruns are bit-identical.
-__device__ inline float dpp_add(float v, int ctrl_sel) {
-    int x;
-    if (ctrl_sel == 0) x = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true);        // quad_perm [1,0,3,2]
-    else if (ctrl_sel == 1) x = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true);   // quad_perm [2,3,0,1]
-    else if (ctrl_sel == 2) x = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true);  // row_half_mirror
-    else x = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true);                    // row_mirror
-    return v + __int_as_float(x);
-}
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) v = dpp_add(v, k);
-    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
-    const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return __uint_as_float(q[0]) + __uint_as_float(q[1]);
-}
 
 __device__ inline float silu_f(float v) { return v / (1.0f + __expf(-v)); }
 

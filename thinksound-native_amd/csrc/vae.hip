@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include "kernels.h"
+#include "dpp.h"
 #include "snake.h"
 
 namespace tsn {
@@ -114,10 +115,7 @@ __global__ void __launch_bounds__(256) conv_out_kernel(const float *__restrict__
     for (int r = 0; r < 16; ++r)
 #pragma unroll
         for (int c = 0; c < OC; ++c) {
-            float a = acc[r][c];
-#pragma unroll
-            for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
-            acc[r][c] = a;
+            acc[r][c] = wave_sum(acc[r][c]);
         }
     // lane r*OC + c writes output (row r, channel c) of the wave's 16 rows
     float mine = 0.0f;

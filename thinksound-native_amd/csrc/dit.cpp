@@ -255,6 +255,23 @@ void DitModel::next_ln(RedLnArgs &r, Next next, const RowMap *maps, int nseg) {
     }
 }
 
+// Weight prefetch from the LN kernels (PfRange): only when the LN kernel is long enough to hide
+// the extra workgroups' line fetches, i.e. at 4096 rows and more (batch 16 at 8 s: 7.56 -> 7.38 ms
+// per evaluation; at 794 rows (8 s, batch 2) and 2202 rows (30 s) the LN kernels lengthened by more
+// than the GEMMs gained).
+bool DitModel::ln_prefetch() const { return (long long)s.B * S >= 4096; }
+
+// The next block's QKV weights, touched by the reduce + LN kernel that runs before that GEMM.
+void DitModel::next_qkv_prefetch(RedLnArgs &r, Next next) const {
+    if (!ln_prefetch()) return;
+    if (next.kind == NEXT_JOINT) {
+        r.pf[0] = PfRange{ja_[next.idx].Wqkv, 3 * s.H, 2 * s.H, 2LL * s.H};
+        r.pf[1] = PfRange{jt_[next.idx].Wqkv, 3 * s.H, 2 * s.H, 2LL * s.H};
+    } else if (next.kind == NEXT_FUSED) {
+        r.pf[0] = PfRange{fu_[next.idx].Wqkv, 3 * s.H, 2 * s.H, 2LL * s.H};
+    }
+}
+
 // Joint block: src/dit_fwd.cpp:180-257 (pre_attn :24-49, attention :83-102, post_attn :51-81)
 int DitModel::block_joint(int i, bool ln1, Next next) {
     const hipStream_t st = rt->dev.stream();
@@ -292,13 +309,17 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
     ob.ws_bytes = ws_bytes_;
     resid_problem(ob.p[0], AO_, H, Sa, 1, H, B * La, H, a.Wo, a.bo, X_, H, mod_ + a.mod_off + 2 * H, NMOD);
     resid_problem(ob.p[1], AO_, H, St, 1, H, B * Lt, H, t.Wo, t.bo, X_, H, mod_ + t.mod_off + 2 * H, NMOD);
+    const int ta = a.conv ? 3 : 1;
     RedLnArgs r;
     next_ln(r, Next{NEXT_JOINT, i}, maps, 2);   // LN2 of this block: modulation chunks 3, 4
     r.seg[0].shift_off += 3 * H; r.seg[0].scale_off += 3 * H;
     r.seg[1].shift_off += 3 * H; r.seg[1].scale_off += 3 * H;
+    if (ln_prefetch()) {   // FFN1's weights, read next (the audio conv's first tap: the first third of its K)
+        r.pf[0] = PfRange{a.W1, s.F, H * 2, (long long)ta * H * 2};
+        r.pf[1] = PfRange{t.W1, s.F, H * 2, (long long)H * 2};
+    }
     TSN_TRY(resid_ln(ob, r, s.H, s.ln_eps));
 
-    const int ta = a.conv ? 3 : 1;
     GemmBatch f1;
     f1.nprob = 2;
     store_problem(f1.p[0], XN_, H, Sa, ta, H, B * La, s.F, a.W1, HF_, s.F, 1);
@@ -312,6 +333,7 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
     resid_problem(f2.p[0], HF_, s.F, Sa, ta, s.F, B * La, H, a.W2, nullptr, X_, H, mod_ + a.mod_off + 5 * H, NMOD);
     resid_problem(f2.p[1], HF_, s.F, St, 1, s.F, B * Lt, H, t.W2, nullptr, X_, H, mod_ + t.mod_off + 5 * H, NMOD);
     next_ln(r, next, maps, 2);
+    next_qkv_prefetch(r, next);
     return resid_ln(f2, r, s.H, s.ln_eps);
 }
 
@@ -351,6 +373,7 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
     RedLnArgs r;
     next_ln(r, Next{NEXT_FUSED, i}, &D, 1);   // LN2 of this block: modulation chunks 3, 4
     r.seg[0].shift_off += 3 * H; r.seg[0].scale_off += 3 * H;
+    if (ln_prefetch()) r.pf[0] = PfRange{w.W1, s.F, H * 2, (long long)H * 2};   // FFN1's weights, read next
     TSN_TRY(resid_ln(ob, r, s.H, s.ln_eps));
 
     GemmBatch f1;
@@ -364,6 +387,7 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
     f2.ws_bytes = ws_bytes_;
     resid_problem(f2.p[0], HF_, s.F, D, 1, s.F, M, H, w.W2, nullptr, X_, H, mod_ + w.mod_off + 5 * H, NMOD);
     next_ln(r, next, &D, 1);
+    next_qkv_prefetch(r, next);
     return resid_ln(f2, r, s.H, s.ln_eps);
 }
 

@@ -133,6 +133,19 @@ int launch_attn_pack(const float *qkv, int S, int nh, int ld, int q_off, int k_o
 // y = LN(x; eps, no affine) * (1 + scale) + shift, one wave per row, H % 256 == 0, H <= 2048.
 // Virtual row v of segment s: x row xmap(v), y row ymap(v), sample b = v / mod_L,
 // shift = mod[b*mod_ld + shift_off + c], scale = mod[b*mod_ld + scale_off + c].
+// Weight lines an LN kernel touches for the GEMM that follows it, so that GEMM's first reads of
+// them come from the last-level cache instead of HBM: the first row_bytes of each of `rows` rows,
+// ld bytes apart (row_bytes and ld multiples of 128; inside one allocation). Extra workgroups
+// appended to the LN grid load one dword per 128-byte line and do nothing else, so the LN waves
+// never wait for them. rows = 0: nothing.
+struct PfRange {
+    const void *p = nullptr;
+    int rows = 0, row_bytes = 0;
+    long long ld = 0;
+};
+constexpr int PF_PER_LANE = 2;
+constexpr int PF_LINES_PER_WG = 4 * 64 * PF_PER_LANE;   // 4 waves x 64 lanes x PF_PER_LANE loads
+int pf_workgroups(const PfRange (&pf)[2]);
 struct LnSeg {
     const float *X; int ldx; RowMap xmap;
     void *Y; int ldy; RowMap ymap;
@@ -143,6 +156,8 @@ struct LnArgs {
     LnSeg seg[3];
     int nseg, H;
     float eps;
+    PfRange pf[2];
+    int pf_wg0;   // set by the launcher: first prefetch workgroup
 };
 // ymode: 0 f32 output, 1 f16 output, 2 f16 hi|lo pair (y_hi at column c, y_lo = f16(y - y_hi) at
 // column H + c; ldy >= 2H): an f16 GEMM over [hi|lo] against a [W|W] weight reproduces the f32 y.
@@ -168,6 +183,8 @@ struct RedLnArgs {
     RedLnSeg seg[3];
     int nseg, H, ymode;
     float eps;
+    PfRange pf[2];
+    int pf_wg0;   // set by the launcher: first prefetch workgroup
 };
 int launch_reduce_ln(const RedLnArgs &a, hipStream_t st);
 

@@ -18,11 +18,39 @@ namespace {
 
 __device__ inline float silu_f(float v) { return v / (1.0f + __expf(-v)); }
 
+// Prefetch workgroup pw (4 waves): lines [PF_LINES_PER_WG*pw, +PF_LINES_PER_WG) of the two ranges
+// laid end to end, PF_PER_LANE per lane, issued together and waited for once at the end (these waves
+// do nothing else). Few lines per workgroup spread the requests over every CU.
+__device__ __forceinline__ void prefetch_wg(const PfRange (&pf)[2], int pw, int wave, int lane) {
+    const long long lpr0 = pf[0].row_bytes >> 7, lpr1 = pf[1].row_bytes >> 7;
+    const long long L0 = pf[0].rows * lpr0, L = L0 + pf[1].rows * lpr1;
+    const long long g0 = (long long)pw * PF_LINES_PER_WG + wave * (64 * PF_PER_LANE) + lane;
+    float v[PF_PER_LANE];
+#pragma unroll
+    for (int j = 0; j < PF_PER_LANE; ++j) {
+        const long long g = g0 + 64 * j;
+        v[j] = 0.0f;
+        if (g < L) {
+            const int ri = g < L0 ? 0 : 1;
+            const long long gl = ri ? g - L0 : g, lpr = ri ? lpr1 : lpr0;
+            const long long row = gl / lpr;
+            v[j] = *(const float *)((const char *)pf[ri].p + row * pf[ri].ld + (gl - row * lpr) * 128);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < PF_PER_LANE; ++j) asm volatile("" ::"v"(v[j]));
+}
+
 /* ---------------- LayerNorm + adaLN modulate (shaders/ops_conv.metal:127-144) ---------------- */
 // one wave per row; lane holds columns 4*lane + 256*c, c < NV (H = 256*NV)
 template <int YMODE, int NV>
 __global__ __launch_bounds__(256) void ln_mod_kernel(const LnArgs a) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // wave-uniform: the segment's fields come through scalar loads
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if ((int)blockIdx.x >= a.pf_wg0) {
+        prefetch_wg(a.pf, blockIdx.x - a.pf_wg0, wave, lane);
+        return;
+    }
     int v = blockIdx.x * 4 + wave;
     int si = 0;
     while (si < a.nseg && v >= a.seg[si].rows) v -= a.seg[si++].rows;
@@ -40,6 +68,7 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const LnArgs a) {
         sh[c] = *(const float4 *)(mb + S.shift_off + c * 256 + lane * 4);
         scl[c] = *(const float4 *)(mb + S.scale_off + c * 256 + lane * 4);
     }
+
     float sum = 0.0f;
 #pragma unroll
     for (int c = 0; c < NV; ++c) sum += (xv[c].x + xv[c].y) + (xv[c].z + xv[c].w);
@@ -92,6 +121,10 @@ __device__ __forceinline__ float block_sum(float v, float *red, int nw) {
 template <int YMODE>
 __global__ __launch_bounds__(512) void reduce_ln_kernel(const RedLnArgs a) {
     __shared__ float red[2][8];
+    if ((int)blockIdx.x >= a.pf_wg0) {
+        prefetch_wg(a.pf, blockIdx.x - a.pf_wg0, threadIdx.x >> 6, threadIdx.x & 63);
+        return;
+    }
     int v = blockIdx.x, si = 0;
     while (si < a.nseg && v >= a.seg[si].M) v -= a.seg[si++].M;
     if (si >= a.nseg) return;   // uniform over the workgroup
@@ -99,6 +132,7 @@ __global__ __launch_bounds__(512) void reduce_ln_kernel(const RedLnArgs a) {
     const int H = a.H, col = threadIdx.x * 4;
     float *x = S.X + rowmap_phys(S.xmap, v) * (long long)S.ldx + col;
     float4 xv = *(const float4 *)x;
+    const int nwv = blockDim.x >> 6;
     if (S.splits > 1) {
         const float *w = S.ws + (long long)v * H + col;
         const long long step = (long long)S.M * H;
@@ -119,11 +153,10 @@ __global__ __launch_bounds__(512) void reduce_ln_kernel(const RedLnArgs a) {
     if (!S.ln) return;   // uniform over the workgroup
     const int b = v / S.mod_L;
     if (v - b * S.mod_L >= S.ln_len) return;
-    const int nw = blockDim.x >> 6;
     const float inv_h = 1.0f / (float)H;
-    const float mean = block_sum((xv.x + xv.y) + (xv.z + xv.w), red[0], nw) * inv_h;
+    const float mean = block_sum((xv.x + xv.y) + (xv.z + xv.w), red[0], nwv) * inv_h;
     const float d0 = xv.x - mean, d1 = xv.y - mean, d2 = xv.z - mean, d3 = xv.w - mean;
-    const float var = block_sum((d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3), red[1], nw) * inv_h;
+    const float var = block_sum((d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3), red[1], nwv) * inv_h;
     const float inv = 1.0f / sqrtf(var + a.eps);
     const float *mb = S.mod + (long long)b * S.mod_ld;
     const float4 sh = *(const float4 *)(mb + S.shift_off + col);
@@ -517,6 +550,20 @@ inline unsigned blocks_for(size_t n, unsigned t = 256) { return (unsigned)((n + 
 
 } // namespace
 
+static bool pf_ranges_ok(const PfRange (&pf)[2]) {
+    for (int i = 0; i < 2; ++i)
+        if (pf[i].rows < 0 || (pf[i].rows > 0 && (!pf[i].p || pf[i].row_bytes <= 0 || pf[i].row_bytes % 128 ||
+                                                   pf[i].ld % 128 || pf[i].ld < pf[i].row_bytes)))
+            return false;
+    return true;
+}
+
+int pf_workgroups(const PfRange (&pf)[2]) {
+    long long lines = 0;
+    for (int i = 0; i < 2; ++i) lines += (long long)pf[i].rows * (pf[i].row_bytes >> 7);
+    return (int)((lines + PF_LINES_PER_WG - 1) / PF_LINES_PER_WG);
+}
+
 int launch_ln_mod(const LnArgs &a, int ymode, hipStream_t st) {
     TSN_REQUIRE(ymode == LN_F32 || ymode == LN_F16 || ymode == LN_F16_HILO, "ln: output mode");
     TSN_REQUIRE(a.nseg >= 1 && a.nseg <= 3, "ln: 1 to 3 segments");
@@ -530,14 +577,17 @@ int launch_ln_mod(const LnArgs &a, int ymode, hipStream_t st) {
         TSN_REQUIRE(ymode != LN_F16_HILO || s.ldy >= 2 * a.H, "ln: hi|lo output needs ldy >= 2H");
         total += s.rows;
     }
-    dim3 grid((total + 3) / 4), block(256);
+    TSN_REQUIRE(pf_ranges_ok(a.pf), "ln: prefetch ranges");
+    LnArgs b = a;
+    b.pf_wg0 = (total + 3) / 4;
+    dim3 grid(b.pf_wg0 + pf_workgroups(a.pf)), block(256);
     const int nv = a.H / 256;
 #define TSN_LN_CASE(NVV)                                                                           \
     case NVV:                                                                                      \
-        if (ymode == LN_F16) TSN_LAUNCH((ln_mod_kernel<LN_F16, NVV>), grid, block, 0, st, a); \
+        if (ymode == LN_F16) TSN_LAUNCH((ln_mod_kernel<LN_F16, NVV>), grid, block, 0, st, b); \
         else if (ymode == LN_F16_HILO)                                                             \
-            TSN_LAUNCH((ln_mod_kernel<LN_F16_HILO, NVV>), grid, block, 0, st, a);          \
-        else TSN_LAUNCH((ln_mod_kernel<LN_F32, NVV>), grid, block, 0, st, a);              \
+            TSN_LAUNCH((ln_mod_kernel<LN_F16_HILO, NVV>), grid, block, 0, st, b);          \
+        else TSN_LAUNCH((ln_mod_kernel<LN_F32, NVV>), grid, block, 0, st, b);              \
         break;
     switch (nv) {
         TSN_LN_CASE(1) TSN_LN_CASE(2) TSN_LN_CASE(3) TSN_LN_CASE(4)
@@ -565,9 +615,13 @@ int launch_reduce_ln(const RedLnArgs &a, hipStream_t st) {
                     "reduce_ln: hi|lo output needs ldy >= 2H");
         total += s.M;
     }
-    dim3 grid(total), block(a.H / 4);
-    if (a.ymode == LN_F16_HILO) TSN_LAUNCH((reduce_ln_kernel<LN_F16_HILO>), grid, block, 0, st, a);
-    else TSN_LAUNCH((reduce_ln_kernel<LN_F16>), grid, block, 0, st, a);
+    TSN_REQUIRE(pf_ranges_ok(a.pf) && ((a.pf[0].rows == 0 && a.pf[1].rows == 0) || a.H == 1024),
+                "reduce_ln: prefetch ranges (prefetch workgroups need 4 waves: H = 1024)");
+    RedLnArgs b = a;
+    b.pf_wg0 = total;
+    dim3 grid(total + pf_workgroups(a.pf)), block(a.H / 4);
+    if (a.ymode == LN_F16_HILO) TSN_LAUNCH((reduce_ln_kernel<LN_F16_HILO>), grid, block, 0, st, b);
+    else TSN_LAUNCH((reduce_ln_kernel<LN_F16>), grid, block, 0, st, b);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }

@@ -135,9 +135,9 @@ int launch_attn_pack(const float *qkv, int S, int nh, int ld, int q_off, int k_o
 // shift = mod[b*mod_ld + shift_off + c], scale = mod[b*mod_ld + scale_off + c].
 // Weight lines an LN kernel touches for the GEMM that follows it, so that GEMM's first reads of
 // them come from the last-level cache instead of HBM: the first row_bytes of each of `rows` rows,
-// ld bytes apart (row_bytes and ld multiples of 128; inside one allocation). Extra workgroups
-// appended to the LN grid load one dword per 128-byte line and do nothing else, so the LN waves
-// never wait for them. rows = 0: nothing.
+// ld bytes apart (row_bytes and ld multiples of 128; inside one allocation). Extra workgroups at
+// the front of the LN grid (dispatched first) load one dword per 128-byte line and do nothing
+// else, so the LN waves never wait for them. rows = 0: nothing.
 struct PfRange {
     const void *p = nullptr;
     int rows = 0, row_bytes = 0;
@@ -157,7 +157,7 @@ struct LnArgs {
     int nseg, H;
     float eps;
     PfRange pf[2];
-    int pf_wg0;   // set by the launcher: first prefetch workgroup
+    int pf_nwg;   // set by the launcher: prefetch workgroups, ahead of the row workgroups
 };
 // ymode: 0 f32 output, 1 f16 output, 2 f16 hi|lo pair (y_hi at column c, y_lo = f16(y - y_hi) at
 // column H + c; ldy >= 2H): an f16 GEMM over [hi|lo] against a [W|W] weight reproduces the f32 y.
@@ -184,7 +184,7 @@ struct RedLnArgs {
     int nseg, H, ymode;
     float eps;
     PfRange pf[2];
-    int pf_wg0;   // set by the launcher: first prefetch workgroup
+    int pf_nwg;   // set by the launcher: prefetch workgroups, ahead of the row workgroups
 };
 int launch_reduce_ln(const RedLnArgs &a, hipStream_t st);
 

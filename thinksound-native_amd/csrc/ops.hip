@@ -47,11 +47,11 @@ template <int YMODE, int NV>
 __global__ __launch_bounds__(256) void ln_mod_kernel(const LnArgs a) {
     // wave-uniform: the segment's fields come through scalar loads
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if ((int)blockIdx.x >= a.pf_wg0) {
-        prefetch_wg(a.pf, blockIdx.x - a.pf_wg0, wave, lane);
+    if ((int)blockIdx.x < a.pf_nwg) {
+        prefetch_wg(a.pf, blockIdx.x, wave, lane);
         return;
     }
-    int v = blockIdx.x * 4 + wave;
+    int v = ((int)blockIdx.x - a.pf_nwg) * 4 + wave;
     int si = 0;
     while (si < a.nseg && v >= a.seg[si].rows) v -= a.seg[si++].rows;
     if (si >= a.nseg) return;
@@ -121,11 +121,11 @@ __device__ __forceinline__ float block_sum(float v, float *red, int nw) {
 template <int YMODE>
 __global__ __launch_bounds__(512) void reduce_ln_kernel(const RedLnArgs a) {
     __shared__ float red[2][8];
-    if ((int)blockIdx.x >= a.pf_wg0) {
-        prefetch_wg(a.pf, blockIdx.x - a.pf_wg0, threadIdx.x >> 6, threadIdx.x & 63);
+    if ((int)blockIdx.x < a.pf_nwg) {
+        prefetch_wg(a.pf, blockIdx.x, threadIdx.x >> 6, threadIdx.x & 63);
         return;
     }
-    int v = blockIdx.x, si = 0;
+    int v = (int)blockIdx.x - a.pf_nwg, si = 0;
     while (si < a.nseg && v >= a.seg[si].M) v -= a.seg[si++].M;
     if (si >= a.nseg) return;   // uniform over the workgroup
     const RedLnSeg &S = a.seg[si];
@@ -579,8 +579,8 @@ int launch_ln_mod(const LnArgs &a, int ymode, hipStream_t st) {
     }
     TSN_REQUIRE(pf_ranges_ok(a.pf), "ln: prefetch ranges");
     LnArgs b = a;
-    b.pf_wg0 = (total + 3) / 4;
-    dim3 grid(b.pf_wg0 + pf_workgroups(a.pf)), block(256);
+    b.pf_nwg = pf_workgroups(a.pf);
+    dim3 grid(b.pf_nwg + (total + 3) / 4), block(256);
     const int nv = a.H / 256;
 #define TSN_LN_CASE(NVV)                                                                           \
     case NVV:                                                                                      \
@@ -618,8 +618,8 @@ int launch_reduce_ln(const RedLnArgs &a, hipStream_t st) {
     TSN_REQUIRE(pf_ranges_ok(a.pf) && ((a.pf[0].rows == 0 && a.pf[1].rows == 0) || a.H == 1024),
                 "reduce_ln: prefetch ranges (prefetch workgroups need 4 waves: H = 1024)");
     RedLnArgs b = a;
-    b.pf_wg0 = total;
-    dim3 grid(total + pf_workgroups(a.pf)), block(a.H / 4);
+    b.pf_nwg = pf_workgroups(a.pf);
+    dim3 grid(b.pf_nwg + total), block(a.H / 4);
     if (a.ymode == LN_F16_HILO) TSN_LAUNCH((reduce_ln_kernel<LN_F16_HILO>), grid, block, 0, st, b);
     else TSN_LAUNCH((reduce_ln_kernel<LN_F16>), grid, block, 0, st, b);
     TSN_HIP_CHECK(hipGetLastError());

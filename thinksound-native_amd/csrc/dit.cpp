@@ -324,6 +324,8 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
     f1.nprob = 2;
     store_problem(f1.p[0], XN_, H, Sa, ta, H, B * La, s.F, a.W1, HF_, s.F, 1);
     store_problem(f1.p[1], XN_, H, St, 1, H, B * Lt, s.F, t.W1, HF_, s.F, 1);
+    f1.pf[0] = PfRange{a.W2, H, ta * s.F * 2, (long long)ta * s.F * 2};   // FFN2's weights, read next
+    f1.pf[1] = PfRange{t.W2, H, s.F * 2, (long long)s.F * 2};
     TSN_TRY(gemm_run(f1, EPI_STORE));
 
     GemmBatch f2;
@@ -379,6 +381,7 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
     GemmBatch f1;
     f1.nprob = 1;
     store_problem(f1.p[0], XN_, H, D, 1, H, M, s.F, w.W1, HF_, s.F, 1);
+    f1.pf[0] = PfRange{w.W2, H, s.F * 2, (long long)s.F * 2};   // FFN2's weights, read next
     TSN_TRY(gemm_run(f1, EPI_STORE));
 
     GemmBatch f2;

@@ -17,6 +17,7 @@
 // workgroups of one XCD share W column blocks in that XCD's L2.
 #include "kernels.h"
 #include "dpp.h"
+#include "prefetch.h"
 #include "snake.h"
 
 #include <string.h>
@@ -934,7 +935,11 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
 template <int EPI, bool HL, int NSX = NS, bool BF = false>
 __device__ __forceinline__ void pipe_dp(const GemmBatch &bt) {
     const int tid = threadIdx.x;
-    const int wg = xcd_remap(blockIdx.x, gridDim.x);
+    if ((int)blockIdx.x >= bt.total_tiles) {   // prefetch workgroups after the tiles (GemmBatch::pf)
+        prefetch_wg<8>(bt.pf, blockIdx.x - bt.total_tiles, tid >> 6, tid & 63);
+        return;
+    }
+    const int wg = xcd_remap(blockIdx.x, bt.total_tiles);
     const int pi = (bt.nprob > 2 && wg >= bt.p[2].tile_start) ? 2 : (bt.nprob > 1 && wg >= bt.p[1].tile_start) ? 1 : 0;
     const GemmProblem &P = bt.p[pi];
     const int local = wg - P.tile_start;
@@ -1370,6 +1375,7 @@ void gemm_problem_init(GemmProblem &p) {
 
 int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     TSN_REQUIRE(b.nprob >= 1 && b.nprob <= 3, "gemm: 1 to 3 problems");
+    b.pf_nwg = 0;
     if (b.bf16) {   // one data-parallel schedule: no workspace, so no split and no stream-K
         TSN_REQUIRE(epi == EPI_STORE && !a_f32 && !b.small, "gemm bf16: plain store epilogue, bf16 A");
         b.ws = nullptr;
@@ -1609,6 +1615,9 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
                                                                         : "gemm_f16_kernel<false, 2>");
     // two LDS stages and two workgroups per CU once the data-parallel grid exceeds one round
     b.ns2 = pipe && !b.sk && b.total_tiles > NCU ? 1 : 0;
+    // weight prefetch workgroups after the tiles: data-parallel pipelined kernels only
+    TSN_REQUIRE(pf_ranges_ok(b.pf), "gemm: prefetch ranges");
+    b.pf_nwg = pipe && !b.sk ? pf_workgroups(b.pf, 8) : 0;
     if (b.bf16) {
         TSN_REQUIRE(pipe, "gemm bf16: needs K % 64 == 0, N % 8 == 0 and 16-byte aligned rows, W, bias and Y");
         b.kname = b.ns2 ? "gemm_pipe2_bf16_kernel<0>" : "gemm_pipe_bf16_kernel<0>";
@@ -1634,7 +1643,7 @@ int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st)
         TSN_HIP_CHECK(hipGetLastError());
         return TSN_OK;
     }
-    dim3 grid(b.sk ? b.sk_g : b.total_tiles), block(b.pipe ? 512 : 256);
+    dim3 grid(b.sk ? b.sk_g : b.total_tiles + b.pf_nwg), block(b.pipe ? 512 : 256);
     if (b.bf16) {
         TSN_REQUIRE(b.pipe && epi == EPI_STORE, "gemm bf16: pipelined store kernel only");
         if (b.ns2) TSN_LAUNCH((gemm_pipe2_bf16_kernel<EPI_STORE>), grid, block, 0, st, b);

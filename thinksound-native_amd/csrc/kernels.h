@@ -59,6 +59,22 @@ struct GemmProblem {
     float *ws;
 };
 
+// Weight lines a kernel touches for a GEMM that runs after it, so that GEMM's reads of them come
+// from the last-level cache instead of HBM: the first row_bytes of each of `rows` rows, ld bytes
+// apart (row_bytes and ld multiples of 128; inside one allocation). Extra workgroups of the
+// launch (prefetch.h) load one dword per 128-byte line and do nothing else, so the launch's other
+// workgroups never wait for them: at the front of an LN grid (dispatched first), after the tiles
+// of a data-parallel GEMM grid (on the CUs its last round leaves free). rows = 0: nothing.
+struct PfRange {
+    const void *p = nullptr;
+    int rows = 0, row_bytes = 0;
+    long long ld = 0;
+};
+constexpr int PF_PER_LANE = 2;   // loads per lane of a prefetch workgroup
+// prefetch workgroups of `waves` waves that cover both ranges; false if a range is malformed
+bool pf_ranges_ok(const PfRange (&pf)[2]);
+int pf_workgroups(const PfRange (&pf)[2], int waves);
+
 struct GemmBatch {
     GemmProblem p[3];
     int nprob = 0;
@@ -95,6 +111,11 @@ struct GemmBatch {
     // nonzero: A and W hold bf16 values and the MFMAs run bf16 products (gemm_pipe_bf16_kernel /
     // gemm_pipe2_bf16_kernel: EPI_STORE with f32 Y, one tap, data-parallel, no split)
     int bf16 = 0;
+    // weights of a following GEMM to touch from extra workgroups launched after the tiles (they
+    // take the CUs the last round leaves free); data-parallel pipelined kernels only, else ignored.
+    // pf_nwg is set by gemm_plan.
+    PfRange pf[2];
+    int pf_nwg = 0;
 };
 
 // a_f32: A operand is f32 (converted to f16 on load). All problems share the epilogue kind.
@@ -133,19 +154,6 @@ int launch_attn_pack(const float *qkv, int S, int nh, int ld, int q_off, int k_o
 // y = LN(x; eps, no affine) * (1 + scale) + shift, one wave per row, H % 256 == 0, H <= 2048.
 // Virtual row v of segment s: x row xmap(v), y row ymap(v), sample b = v / mod_L,
 // shift = mod[b*mod_ld + shift_off + c], scale = mod[b*mod_ld + scale_off + c].
-// Weight lines an LN kernel touches for the GEMM that follows it, so that GEMM's first reads of
-// them come from the last-level cache instead of HBM: the first row_bytes of each of `rows` rows,
-// ld bytes apart (row_bytes and ld multiples of 128; inside one allocation). Extra workgroups at
-// the front of the LN grid (dispatched first) load one dword per 128-byte line and do nothing
-// else, so the LN waves never wait for them. rows = 0: nothing.
-struct PfRange {
-    const void *p = nullptr;
-    int rows = 0, row_bytes = 0;
-    long long ld = 0;
-};
-constexpr int PF_PER_LANE = 2;
-constexpr int PF_LINES_PER_WG = 4 * 64 * PF_PER_LANE;   // 4 waves x 64 lanes x PF_PER_LANE loads
-int pf_workgroups(const PfRange (&pf)[2]);
 struct LnSeg {
     const float *X; int ldx; RowMap xmap;
     void *Y; int ldy; RowMap ymap;

@@ -8,6 +8,7 @@
 // reruns are bit-identical. No float atomics anywhere.
 #include "kernels.h"
 #include "dpp.h"
+#include "prefetch.h"
 
 #include <string.h>
 
@@ -18,29 +19,6 @@ namespace {
 
 __device__ inline float silu_f(float v) { return v / (1.0f + __expf(-v)); }
 
-// Prefetch workgroup pw (4 waves): lines [PF_LINES_PER_WG*pw, +PF_LINES_PER_WG) of the two ranges
-// laid end to end, PF_PER_LANE per lane, issued together and waited for once at the end (these waves
-// do nothing else). Few lines per workgroup spread the requests over every CU.
-__device__ __forceinline__ void prefetch_wg(const PfRange (&pf)[2], int pw, int wave, int lane) {
-    const long long lpr0 = pf[0].row_bytes >> 7, lpr1 = pf[1].row_bytes >> 7;
-    const long long L0 = pf[0].rows * lpr0, L = L0 + pf[1].rows * lpr1;
-    const long long g0 = (long long)pw * PF_LINES_PER_WG + wave * (64 * PF_PER_LANE) + lane;
-    float v[PF_PER_LANE];
-#pragma unroll
-    for (int j = 0; j < PF_PER_LANE; ++j) {
-        const long long g = g0 + 64 * j;
-        v[j] = 0.0f;
-        if (g < L) {
-            const int ri = g < L0 ? 0 : 1;
-            const long long gl = ri ? g - L0 : g, lpr = ri ? lpr1 : lpr0;
-            const long long row = gl / lpr;
-            v[j] = *(const float *)((const char *)pf[ri].p + row * pf[ri].ld + (gl - row * lpr) * 128);
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < PF_PER_LANE; ++j) asm volatile("" ::"v"(v[j]));
-}
-
 /* ---------------- LayerNorm + adaLN modulate (shaders/ops_conv.metal:127-144) ---------------- */
 // one wave per row; lane holds columns 4*lane + 256*c, c < NV (H = 256*NV)
 template <int YMODE, int NV>
@@ -48,7 +26,7 @@ __global__ __launch_bounds__(256) void ln_mod_kernel(const LnArgs a) {
     // wave-uniform: the segment's fields come through scalar loads
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     if ((int)blockIdx.x < a.pf_nwg) {
-        prefetch_wg(a.pf, blockIdx.x, wave, lane);
+        prefetch_wg<4>(a.pf, blockIdx.x, wave, lane);
         return;
     }
     int v = ((int)blockIdx.x - a.pf_nwg) * 4 + wave;
@@ -122,7 +100,7 @@ template <int YMODE>
 __global__ __launch_bounds__(512) void reduce_ln_kernel(const RedLnArgs a) {
     __shared__ float red[2][8];
     if ((int)blockIdx.x < a.pf_nwg) {
-        prefetch_wg(a.pf, blockIdx.x, threadIdx.x >> 6, threadIdx.x & 63);
+        prefetch_wg<4>(a.pf, blockIdx.x, threadIdx.x >> 6, threadIdx.x & 63);
         return;
     }
     int v = (int)blockIdx.x - a.pf_nwg, si = 0;
@@ -550,7 +528,7 @@ inline unsigned blocks_for(size_t n, unsigned t = 256) { return (unsigned)((n + 
 
 } // namespace
 
-static bool pf_ranges_ok(const PfRange (&pf)[2]) {
+bool pf_ranges_ok(const PfRange (&pf)[2]) {
     for (int i = 0; i < 2; ++i)
         if (pf[i].rows < 0 || (pf[i].rows > 0 && (!pf[i].p || pf[i].row_bytes <= 0 || pf[i].row_bytes % 128 ||
                                                    pf[i].ld % 128 || pf[i].ld < pf[i].row_bytes)))
@@ -558,10 +536,11 @@ static bool pf_ranges_ok(const PfRange (&pf)[2]) {
     return true;
 }
 
-int pf_workgroups(const PfRange (&pf)[2]) {
+int pf_workgroups(const PfRange (&pf)[2], int waves) {
     long long lines = 0;
     for (int i = 0; i < 2; ++i) lines += (long long)pf[i].rows * (pf[i].row_bytes >> 7);
-    return (int)((lines + PF_LINES_PER_WG - 1) / PF_LINES_PER_WG);
+    const long long per = (long long)waves * 64 * PF_PER_LANE;
+    return (int)((lines + per - 1) / per);
 }
 
 int launch_ln_mod(const LnArgs &a, int ymode, hipStream_t st) {
@@ -579,7 +558,7 @@ int launch_ln_mod(const LnArgs &a, int ymode, hipStream_t st) {
     }
     TSN_REQUIRE(pf_ranges_ok(a.pf), "ln: prefetch ranges");
     LnArgs b = a;
-    b.pf_nwg = pf_workgroups(a.pf);
+    b.pf_nwg = pf_workgroups(a.pf, 4);
     dim3 grid(b.pf_nwg + (total + 3) / 4), block(256);
     const int nv = a.H / 256;
 #define TSN_LN_CASE(NVV)                                                                           \
@@ -618,7 +597,7 @@ int launch_reduce_ln(const RedLnArgs &a, hipStream_t st) {
     TSN_REQUIRE(pf_ranges_ok(a.pf) && ((a.pf[0].rows == 0 && a.pf[1].rows == 0) || a.H == 1024),
                 "reduce_ln: prefetch ranges (prefetch workgroups need 4 waves: H = 1024)");
     RedLnArgs b = a;
-    b.pf_nwg = pf_workgroups(a.pf);
+    b.pf_nwg = pf_workgroups(a.pf, 4);
     dim3 grid(b.pf_nwg + total), block(a.H / 4);
     if (a.ymode == LN_F16_HILO) TSN_LAUNCH((reduce_ln_kernel<LN_F16_HILO>), grid, block, 0, st, b);
     else TSN_LAUNCH((reduce_ln_kernel<LN_F16>), grid, block, 0, st, b);

@@ -260,15 +260,22 @@ void DitModel::next_ln(RedLnArgs &r, Next next, const RowMap *maps, int nseg) {
 // per evaluation; at 794 rows (8 s, batch 2) and 2202 rows (30 s) the LN kernels lengthened by more
 // than the GEMMs gained).
 bool DitModel::ln_prefetch() const { return (long long)s.B * S >= 4096; }
+// FFN1's and the next QKV's weights from the spare CUs of the out-projection and FFN2 grids: above
+// 1024 rows, where those grids run two workgroups per CU with free slots (30 s: 3.978 -> 3.909 ms).
+// At 794 rows (8 s) the out-projection's small tiles share their CUs with the prefetch and FFN2's
+// single round leaves 16 CUs for it: 8 s 1.871 -> 1.886 ms, so not there.
+bool DitModel::grid_prefetch() const { return (long long)s.B * S > 1024 && !ln_prefetch(); }
 
-// The next block's QKV weights, touched by the reduce + LN kernel that runs before that GEMM.
-void DitModel::next_qkv_prefetch(RedLnArgs &r, Next next) const {
-    if (!ln_prefetch()) return;
+// The next block's QKV weights: touched by the reduce + LN kernel that runs before that GEMM, or
+// by the FFN2 GEMM's spare CUs (ln_prefetch, grid_prefetch).
+void DitModel::next_qkv_prefetch(RedLnArgs &r, GemmBatch &f2, Next next) const {
+    if (!ln_prefetch() && !grid_prefetch()) return;
+    PfRange (&pf)[2] = ln_prefetch() ? r.pf : f2.pf;
     if (next.kind == NEXT_JOINT) {
-        r.pf[0] = PfRange{ja_[next.idx].Wqkv, 3 * s.H, 2 * s.H, 2LL * s.H};
-        r.pf[1] = PfRange{jt_[next.idx].Wqkv, 3 * s.H, 2 * s.H, 2LL * s.H};
+        pf[0] = PfRange{ja_[next.idx].Wqkv, 3 * s.H, 2 * s.H, 2LL * s.H};
+        pf[1] = PfRange{jt_[next.idx].Wqkv, 3 * s.H, 2 * s.H, 2LL * s.H};
     } else if (next.kind == NEXT_FUSED) {
-        r.pf[0] = PfRange{fu_[next.idx].Wqkv, 3 * s.H, 2 * s.H, 2LL * s.H};
+        pf[0] = PfRange{fu_[next.idx].Wqkv, 3 * s.H, 2 * s.H, 2LL * s.H};
     }
 }
 
@@ -292,6 +299,8 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
     qb.nprob = 2;
     qkv_problem(qb.p[0], XN_, Sa, B * La, a.Wqkv, a.bqkv, a.qn, a.kn, H, s.NH, Q_, K_, Vt_, S, Sp, La, 0, La, rope_, s.rms_eps);
     qkv_problem(qb.p[1], XN_, St, B * Lt, t.Wqkv, t.bqkv, t.qn, t.kn, H, s.NH, Q_, K_, Vt_, S, Sp, Lt, La, 0, rope_, s.rms_eps);
+    qb.pf[0] = PfRange{a.Wo, H, H * 2, (long long)H * 2};   // the out-projection's weights
+    qb.pf[1] = PfRange{t.Wo, H, H * 2, (long long)H * 2};
     TSN_TRY(gemm_run(qb, EPI_QKV));
 
     AttnArgs at;
@@ -314,9 +323,11 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
     next_ln(r, Next{NEXT_JOINT, i}, maps, 2);   // LN2 of this block: modulation chunks 3, 4
     r.seg[0].shift_off += 3 * H; r.seg[0].scale_off += 3 * H;
     r.seg[1].shift_off += 3 * H; r.seg[1].scale_off += 3 * H;
-    if (ln_prefetch()) {   // FFN1's weights, read next (the audio conv's first tap: the first third of its K)
-        r.pf[0] = PfRange{a.W1, s.F, H * 2, (long long)ta * H * 2};
-        r.pf[1] = PfRange{t.W1, s.F, H * 2, (long long)H * 2};
+    if (ln_prefetch() || grid_prefetch()) {   // FFN1's weights, read next (the audio conv's first
+        // tap: the first third of its K), from the LN kernel or from the out-projection's spare CUs
+        PfRange (&pf)[2] = ln_prefetch() ? r.pf : ob.pf;
+        pf[0] = PfRange{a.W1, s.F, H * 2, (long long)ta * H * 2};
+        pf[1] = PfRange{t.W1, s.F, H * 2, (long long)H * 2};
     }
     TSN_TRY(resid_ln(ob, r, s.H, s.ln_eps));
 
@@ -335,7 +346,7 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
     resid_problem(f2.p[0], HF_, s.F, Sa, ta, s.F, B * La, H, a.W2, nullptr, X_, H, mod_ + a.mod_off + 5 * H, NMOD);
     resid_problem(f2.p[1], HF_, s.F, St, 1, s.F, B * Lt, H, t.W2, nullptr, X_, H, mod_ + t.mod_off + 5 * H, NMOD);
     next_ln(r, next, maps, 2);
-    next_qkv_prefetch(r, next);
+    next_qkv_prefetch(r, f2, next);
     return resid_ln(f2, r, s.H, s.ln_eps);
 }
 
@@ -356,6 +367,7 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
     GemmBatch qb;
     qb.nprob = 1;
     qkv_problem(qb.p[0], XN_, D, M, w.Wqkv, w.bqkv, w.qn, w.kn, H, s.NH, Q_, K_, Vt_, S, Sp, S, 0, s.La, rope_, s.rms_eps);
+    qb.pf[0] = PfRange{w.Wo, H, H * 2, (long long)H * 2};   // the out-projection's weights
     TSN_TRY(gemm_run(qb, EPI_QKV));
 
     AttnArgs at;
@@ -375,7 +387,9 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
     RedLnArgs r;
     next_ln(r, Next{NEXT_FUSED, i}, &D, 1);   // LN2 of this block: modulation chunks 3, 4
     r.seg[0].shift_off += 3 * H; r.seg[0].scale_off += 3 * H;
-    if (ln_prefetch()) r.pf[0] = PfRange{w.W1, s.F, H * 2, (long long)H * 2};   // FFN1's weights, read next
+    // FFN1's weights, read next, from the LN kernel or from the out-projection's spare CUs
+    if (ln_prefetch() || grid_prefetch())
+        (ln_prefetch() ? r.pf : ob.pf)[0] = PfRange{w.W1, s.F, H * 2, (long long)H * 2};
     TSN_TRY(resid_ln(ob, r, s.H, s.ln_eps));
 
     GemmBatch f1;
@@ -390,7 +404,7 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
     f2.ws_bytes = ws_bytes_;
     resid_problem(f2.p[0], HF_, s.F, D, 1, s.F, M, H, w.W2, nullptr, X_, H, mod_ + w.mod_off + 5 * H, NMOD);
     next_ln(r, next, &D, 1);
-    next_qkv_prefetch(r, next);
+    next_qkv_prefetch(r, f2, next);
     return resid_ln(f2, r, s.H, s.ln_eps);
 }
 

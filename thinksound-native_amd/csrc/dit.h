@@ -87,7 +87,8 @@ private:
     int enqueue_eval(const float *z, const float *t, const float *text, const float *pooled, float *v, float *taps,
                      const float *mod_pre);
     bool ln_prefetch() const;
-    void next_qkv_prefetch(RedLnArgs &r, Next next) const;
+    bool grid_prefetch() const;
+    void next_qkv_prefetch(RedLnArgs &r, GemmBatch &f2, Next next) const;
     int block_joint(int i, bool ln1, Next next);
     int block_fused(int i, bool ln1, Next next);
     void next_ln(RedLnArgs &r, Next next, const RowMap *maps, int nseg);

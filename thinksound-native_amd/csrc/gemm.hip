@@ -994,7 +994,11 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
     static_assert(EPI == EPI_RESID, "gemm_small_kernel: residual epilogue only");
     __shared__ __attribute__((aligned(1024))) half_t smem[2 * SNS * SSTAGE];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wg = xcd_remap(blockIdx.x, gridDim.x);
+    if ((int)blockIdx.x >= bt.total_tiles) {   // prefetch workgroups after the tiles (GemmBatch::pf)
+        prefetch_wg<4>(bt.pf, blockIdx.x - bt.total_tiles, wave, lane);
+        return;
+    }
+    const int wg = xcd_remap(blockIdx.x, bt.total_tiles);
     const int pi = (bt.nprob > 2 && wg >= bt.p[2].tile_start) ? 2 : (bt.nprob > 1 && wg >= bt.p[1].tile_start) ? 1 : 0;
     const GemmProblem &P = bt.p[pi];
     int tm, tn;
@@ -1493,6 +1497,8 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         b.pipe = 1;
         b.hl = 0;
         b.kname = "gemm_small_kernel<1>";
+        TSN_REQUIRE(pf_ranges_ok(b.pf), "gemm: prefetch ranges");
+        b.pf_nwg = pf_workgroups(b.pf, 4);
         return TSN_OK;
     }
     const bool snake_epi = epi == EPI_SNAKE || epi == EPI_RSNAKE;
@@ -1639,7 +1645,7 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
 int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
     if (b.small) {
         TSN_REQUIRE(epi == EPI_RESID, "gemm small tiles: residual epilogue only");
-        TSN_LAUNCH((gemm_small_kernel<EPI_RESID>), dim3(b.total_tiles), dim3(256), 0, st, b);
+        TSN_LAUNCH((gemm_small_kernel<EPI_RESID>), dim3(b.total_tiles + b.pf_nwg), dim3(256), 0, st, b);
         TSN_HIP_CHECK(hipGetLastError());
         return TSN_OK;
     }

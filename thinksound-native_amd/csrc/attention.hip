@@ -490,18 +490,33 @@ __global__ __launch_bounds__(256, 3) void flash_attn4_kernel(const AttnArgs a) {
     const half8 ones = half8{1, 1, 1, 1, 1, 1, 1, 1};
     const float scale = a.scale_log2;
 
+    // the lane's fragment offsets (halves) inside a stage, the same for every key block: K rows of
+    // MFMA block j, K half ks; Vt rows of d tile dt, key chunk c
+    unsigned k_off[4][2], v_off[2][4];   // unsigned: the stage offset folds into the reads
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = lane & 15;
+        const int r = 32 * (j >> 1) + 8 * (i >> 2) + 4 * (j & 1) + (i & 3);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) k_off[j][ks] = r * 64 + (((ks * 4 + g) ^ sw(r)) * 8);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            const int d = dt * 16 + (lane & 15);
+            v_off[c][dt] = 4096 + d * 64 + (((c * 4 + g) ^ sw(d)) * 8);
+        }
+
     auto compute = [&](int st, int blk) {
         const half_t *sK = smem + st * STG;
-        const half_t *sV = sK + 4096;
         floatx4 sc[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             sc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-            const int i = lane & 15;
-            const int r = 32 * (j >> 1) + 8 * (i >> 2) + 4 * (j & 1) + (i & 3);
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
-                const half8 kf = *(const half8 *)(sK + r * 64 + (((ks * 4 + g) ^ sw(r)) * 8));
+                const half8 kf = *(const half8 *)(sK + k_off[j][ks]);
                 sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], sc[j], 0, 0, 0);
             }
         }
@@ -527,8 +542,7 @@ __global__ __launch_bounds__(256, 3) void flash_attn4_kernel(const AttnArgs a) {
                                    ph[2 * c + 1][0], ph[2 * c + 1][1], ph[2 * c + 1][2], ph[2 * c + 1][3]};
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
-                const int d = dt * 16 + (lane & 15);
-                const half8 vf = *(const half8 *)(sV + d * 64 + (((c * 4 + g) ^ sw(d)) * 8));
+                const half8 vf = *(const half8 *)(sK + v_off[c][dt]);
                 o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[dt], 0, 0, 0);
             }
             lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lsum, 0, 0, 0);
@@ -541,12 +555,20 @@ __global__ __launch_bounds__(256, 3) void flash_attn4_kernel(const AttnArgs a) {
     wait_vmcnt(nkb > 1 ? 4 : 0);
     block_barrier();
     if (nkb > 2) issue(2, 2);
-    for (int b = 0; b < nkb; ++b) {
-        compute(b % NST, b);
-        if (b + 1 < nkb) {
-            wait_vmcnt(b + 2 < nkb ? 4 : 0);   // block b + 1 has landed (b + 2 may still be in flight)
-            block_barrier();                    // and every wave is done with stage b % 3
-            if (b + NST < nkb) issue(b + NST, b % NST);
+    // unrolled over the three stages, so each stage's LDS offset is a constant of the fragment reads
+    // and DMA targets (no per-block address arithmetic)
+    for (int b0 = 0; b0 < nkb; b0 += NST) {
+#pragma unroll
+        for (int u = 0; u < NST; ++u) {
+            const int b = b0 + u;
+            if (b < nkb) {
+                compute(u, b);
+                if (b + 1 < nkb) {
+                    wait_vmcnt(b + 2 < nkb ? 4 : 0);   // block b + 1 has landed (b + 2 may still be in flight)
+                    block_barrier();                    // and every wave is done with stage u = b % 3
+                    if (b + NST < nkb) issue(b + NST, u);
+                }
+            }
         }
     }
     if (q < S) {

@@ -233,10 +233,10 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
     };
 
     if constexpr (NSTG == 4) {
-        // Every key block fits (S <= 512; the launcher takes this kernel only then). Wave w loads rows 8w..8w+7 of the query tile, then
-        // the K rows of key block w, then its Vt columns (16 bytes per lane, the ring's layout:
-        // block b in stage b >> 1, K at part b & 1, Vt at part 2 + (b & 1)); blocks past the last
-        // read as zero, so every wave issues 17 loads. Waiting for all but the last 8 (vmcnt 8)
+        // Every key block fits (S <= 512; the launcher takes this kernel only then). Wave w loads
+        // rows 8w..8w+7 of the query tile, then the K rows of key block w, then its Vt columns (16
+        // bytes per lane; K of block b at b*8 KB, Vt of block b at 64 KB + b*8 KB); blocks past the
+        // last read as zero, so every wave issues 17 loads. Waiting for all but the last 8 (vmcnt 8)
         // covers the queries and the K blocks: each half multiplies its first key block and forms
         // its probabilities while the Vt blocks still land.
         half_t *sQ = smem + NSTG * ASTAGE;
@@ -254,13 +254,13 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
             for (int sub = 0; sub < 8; ++sub) {
                 const int lc = (lane & 7) ^ lr ^ sub, key = kb * AKB + sub * 8 + lr;
                 dma16(rk, key < S ? (unsigned)((key * 64 + lc * 8) * 2) : 0x80000000u,
-                      (lds_char *)(smem + (kb >> 1) * ASTAGE + (kb & 1) * 4096 + sub * 512));
+                      (lds_char *)(smem + kb * 4096 + sub * 512));
             }
 #pragma unroll
             for (int sub = 0; sub < 8; ++sub) {
                 const int lc = (lane & 7) ^ lr ^ sub;
                 dma16(rv, kb < nkb ? (unsigned)(((sub * 8 + lr) * Sp + kb * AKB + lc * 8) * 2) : 0x80000000u,
-                      (lds_char *)(smem + (kb >> 1) * ASTAGE + (2 + (kb & 1)) * 4096 + sub * 512));
+                      (lds_char *)(smem + 32768 + kb * 4096 + sub * 512));
             }
         }
         wait_vmcnt(kv ? 8 : 0);
@@ -270,19 +270,35 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) qf[ks] = *(const half8 *)(sQ + r * 64 + (((ks * 4 + g) ^ sw(r)) * 8));
         }
-        // scores of key block blk for the first NJ 16-key MFMA blocks (NJ = 4: all 64 keys, 2: the
-        // first 32), layout as in compute()
-        auto qk = [&](int blk, int nj, floatx4 (&sc)[4]) {
-            const half_t *sK = smem + (blk >> 1) * ASTAGE + (blk & 1) * 4096;
+        // The lane's fragment offsets (halves) for this half's blocks half, half + 2, ...: K block b
+        // at b*4096, Vt block b at 32768 + b*4096, so the half's i-th block adds i*8192 (16 KB), an
+        // immediate of the LDS reads once the loop below is unrolled (unsigned, so it folds).
+        unsigned k_off[4][2], v_off[2][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int i = lane & 15;
+            const int r = 32 * (j >> 1) + 8 * (i >> 2) + 4 * (j & 1) + (i & 3);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) k_off[j][ks] = half * 4096 + r * 64 + (((ks * 4 + g) ^ sw(r)) * 8);
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const int d = dt * 16 + (lane & 15);
+                v_off[c][dt] = 32768 + half * 4096 + d * 64 + (((c * 4 + g) ^ sw(d)) * 8);
+            }
+        // scores of this half's key block i (block half + 2i) for the first NJ 16-key MFMA blocks
+        // (NJ = 4: all 64 keys, 2: the first 32), layout as in compute()
+        auto qk = [&](int i, int nj, floatx4 (&sc)[4]) {
+            const half_t *sK = smem + i * 8192;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 sc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
                 if (j < nj) {
-                    const int i = lane & 15;
-                    const int r = 32 * (j >> 1) + 8 * (i >> 2) + 4 * (j & 1) + (i & 3);
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) {
-                        const half8 kf = *(const half8 *)(sK + r * 64 + (((ks * 4 + g) ^ sw(r)) * 8));
+                        const half8 kf = *(const half8 *)(sK + k_off[j][ks]);
                         sc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], sc[j], 0, 0, 0);
                     }
                 }
@@ -313,15 +329,14 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
                 pf[c] = half8{ph[2 * c][0], ph[2 * c][1], ph[2 * c][2], ph[2 * c][3],
                               ph[2 * c + 1][0], ph[2 * c + 1][1], ph[2 * c + 1][2], ph[2 * c + 1][3]};
         };
-        auto pv = [&](int blk, int nc, const half8 (&pf)[2]) {
-            const half_t *sV = smem + (blk >> 1) * ASTAGE + 8192 + (blk & 1) * 4096;
+        auto pv = [&](int i, int nc, const half8 (&pf)[2]) {
+            const half_t *sV = smem + i * 8192;
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
                 if (c < nc) {
 #pragma unroll
                     for (int dt = 0; dt < 4; ++dt) {
-                        const int d = dt * 16 + (lane & 15);
-                        const half8 vf = *(const half8 *)(sV + d * 64 + (((c * 4 + g) ^ sw(d)) * 8));
+                        const half8 vf = *(const half8 *)(sV + v_off[c][dt]);
                         o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[c], o[dt], 0, 0, 0);
                     }
                     lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[c], lsum, 0, 0, 0);
@@ -336,33 +351,36 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
         half8 pf[2];
         if (nf > 0) {
             floatx4 sc[4];
-            qk(half, 4, sc);
+            qk(0, 4, sc);
             softmax(sc, 4, AKB, pf);
         }
         wait_vmcnt(0);
         block_barrier();   // every Vt block visible
         if (nf > 0) {
             // the next block's score products are issued before this block's PV products; its
-            // probabilities (after the rescale that follows this block's PV) come last
-            for (int i = 0; i + 1 < nf; ++i) {
-                const int blk = half + 2 * i;
-                floatx4 sn[4];
-                qk(blk + 2, 4, sn);
-                pv(blk, 2, pf);
-                softmax(sn, 4, AKB, pf);
+            // probabilities (after the rescale that follows this block's PV) come last (at most
+            // four blocks per half: unrolled, so every block offset is a constant)
+#pragma unroll
+            for (int i = 0; i < 3; ++i) {
+                if (i + 1 < nf) {
+                    floatx4 sn[4];
+                    qk(i + 1, 4, sn);
+                    pv(i, 2, pf);
+                    softmax(sn, 4, AKB, pf);
+                }
             }
-            pv(half + 2 * (nf - 1), 2, pf);
+            pv(nf - 1, 2, pf);
         }
-        if (own_tail) {
+        if (own_tail) {   // block nfull = half + 2*nf
             floatx4 sc[4];
             if (lim_t <= 32) {
-                qk(nfull, 2, sc);
+                qk(nf, 2, sc);
                 softmax(sc, 2, lim_t, pf);
-                pv(nfull, 1, pf);
+                pv(nf, 1, pf);
             } else {
-                qk(nfull, 4, sc);
+                qk(nf, 4, sc);
                 softmax(sc, 4, lim_t, pf);
-                pv(nfull, 2, pf);
+                pv(nf, 2, pf);
             }
         }
     } else {

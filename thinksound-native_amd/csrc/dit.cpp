@@ -270,7 +270,7 @@ bool DitModel::grid_prefetch() const { return (long long)s.B * S > 1024 && !ln_p
 // by the FFN2 GEMM's spare CUs (ln_prefetch, grid_prefetch).
 void DitModel::next_qkv_prefetch(RedLnArgs &r, GemmBatch &f2, Next next) const {
     if (!ln_prefetch() && !grid_prefetch()) return;
-    PfRange (&pf)[2] = ln_prefetch() ? r.pf : f2.pf;
+    PfRange (&pf)[PF_RANGES] = ln_prefetch() ? r.pf : f2.pf;
     if (next.kind == NEXT_JOINT) {
         pf[0] = PfRange{ja_[next.idx].Wqkv, 3 * s.H, 2 * s.H, 2LL * s.H};
         pf[1] = PfRange{jt_[next.idx].Wqkv, 3 * s.H, 2 * s.H, 2LL * s.H};
@@ -301,6 +301,10 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
     qkv_problem(qb.p[1], XN_, St, B * Lt, t.Wqkv, t.bqkv, t.qn, t.kn, H, s.NH, Q_, K_, Vt_, S, Sp, Lt, La, 0, rope_, s.rms_eps);
     qb.pf[0] = PfRange{a.Wo, H, H * 2, (long long)H * 2};   // the out-projection's weights
     qb.pf[1] = PfRange{t.Wo, H, H * 2, (long long)H * 2};
+    if (!ln_prefetch() && !grid_prefetch()) {   // and FFN1's (first tap of the conv), read three launches later
+        qb.pf[2] = PfRange{a.W1, s.F, H * 2, (long long)(a.conv ? 3 : 1) * H * 2};
+        qb.pf[3] = PfRange{t.W1, s.F, H * 2, (long long)H * 2};
+    }
     TSN_TRY(gemm_run(qb, EPI_QKV));
 
     AttnArgs at;
@@ -325,7 +329,7 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
     r.seg[1].shift_off += 3 * H; r.seg[1].scale_off += 3 * H;
     if (ln_prefetch() || grid_prefetch()) {   // FFN1's weights, read next (the audio conv's first
         // tap: the first third of its K), from the LN kernel or from the out-projection's spare CUs
-        PfRange (&pf)[2] = ln_prefetch() ? r.pf : ob.pf;
+        PfRange (&pf)[PF_RANGES] = ln_prefetch() ? r.pf : ob.pf;
         pf[0] = PfRange{a.W1, s.F, H * 2, (long long)ta * H * 2};
         pf[1] = PfRange{t.W1, s.F, H * 2, (long long)H * 2};
     }
@@ -368,6 +372,8 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
     qb.nprob = 1;
     qkv_problem(qb.p[0], XN_, D, M, w.Wqkv, w.bqkv, w.qn, w.kn, H, s.NH, Q_, K_, Vt_, S, Sp, S, 0, s.La, rope_, s.rms_eps);
     qb.pf[0] = PfRange{w.Wo, H, H * 2, (long long)H * 2};   // the out-projection's weights
+    if (!ln_prefetch() && !grid_prefetch())   // and FFN1's, read three launches later
+        qb.pf[1] = PfRange{w.W1, s.F, H * 2, (long long)H * 2};
     TSN_TRY(gemm_run(qb, EPI_QKV));
 
     AttnArgs at;

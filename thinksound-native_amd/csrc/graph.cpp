@@ -155,8 +155,7 @@ int GraphRunner::resid_ln(GemmBatch &b, RedLnArgs &r, int H, float eps) {
         LnArgs ln;
         memset(&ln, 0, sizeof ln);
         ln.nseg = r.nseg; ln.H = H; ln.eps = eps;
-        ln.pf[0] = r.pf[0];
-        ln.pf[1] = r.pf[1];
+        for (int k = 0; k < PF_RANGES; ++k) ln.pf[k] = r.pf[k];
         for (int i = 0; i < r.nseg; ++i) {
             const RedLnSeg &g = r.seg[i];
             LnSeg &l = ln.seg[i];

@@ -71,9 +71,10 @@ struct PfRange {
     long long ld = 0;
 };
 constexpr int PF_PER_LANE = 2;   // loads per lane of a prefetch workgroup
-// prefetch workgroups of `waves` waves that cover both ranges; false if a range is malformed
-bool pf_ranges_ok(const PfRange (&pf)[2]);
-int pf_workgroups(const PfRange (&pf)[2], int waves);
+constexpr int PF_RANGES = 4;     // ranges per launch
+// prefetch workgroups of `waves` waves that cover every range; false if a range is malformed
+bool pf_ranges_ok(const PfRange (&pf)[PF_RANGES]);
+int pf_workgroups(const PfRange (&pf)[PF_RANGES], int waves);
 
 struct GemmBatch {
     GemmProblem p[3];
@@ -114,7 +115,7 @@ struct GemmBatch {
     // weights of a following GEMM to touch from extra workgroups launched after the tiles (they
     // take the CUs the last round leaves free); data-parallel pipelined kernels only, else ignored.
     // pf_nwg is set by gemm_plan.
-    PfRange pf[2];
+    PfRange pf[PF_RANGES];
     int pf_nwg = 0;
 };
 
@@ -164,7 +165,7 @@ struct LnArgs {
     LnSeg seg[3];
     int nseg, H;
     float eps;
-    PfRange pf[2];
+    PfRange pf[PF_RANGES];
     int pf_nwg;   // set by the launcher: prefetch workgroups, ahead of the row workgroups
 };
 // ymode: 0 f32 output, 1 f16 output, 2 f16 hi|lo pair (y_hi at column c, y_lo = f16(y - y_hi) at
@@ -191,7 +192,7 @@ struct RedLnArgs {
     RedLnSeg seg[3];
     int nseg, H, ymode;
     float eps;
-    PfRange pf[2];
+    PfRange pf[PF_RANGES];
     int pf_nwg;   // set by the launcher: prefetch workgroups, ahead of the row workgroups
 };
 int launch_reduce_ln(const RedLnArgs &a, hipStream_t st);

@@ -528,17 +528,17 @@ inline unsigned blocks_for(size_t n, unsigned t = 256) { return (unsigned)((n + 
 
 } // namespace
 
-bool pf_ranges_ok(const PfRange (&pf)[2]) {
-    for (int i = 0; i < 2; ++i)
+bool pf_ranges_ok(const PfRange (&pf)[PF_RANGES]) {
+    for (int i = 0; i < PF_RANGES; ++i)
         if (pf[i].rows < 0 || (pf[i].rows > 0 && (!pf[i].p || pf[i].row_bytes <= 0 || pf[i].row_bytes % 128 ||
                                                    pf[i].ld % 128 || pf[i].ld < pf[i].row_bytes)))
             return false;
     return true;
 }
 
-int pf_workgroups(const PfRange (&pf)[2], int waves) {
+int pf_workgroups(const PfRange (&pf)[PF_RANGES], int waves) {
     long long lines = 0;
-    for (int i = 0; i < 2; ++i) lines += (long long)pf[i].rows * (pf[i].row_bytes >> 7);
+    for (int i = 0; i < PF_RANGES; ++i) lines += (long long)pf[i].rows * (pf[i].row_bytes >> 7);
     const long long per = (long long)waves * 64 * PF_PER_LANE;
     return (int)((lines + per - 1) / per);
 }
@@ -594,7 +594,7 @@ int launch_reduce_ln(const RedLnArgs &a, hipStream_t st) {
                     "reduce_ln: hi|lo output needs ldy >= 2H");
         total += s.M;
     }
-    TSN_REQUIRE(pf_ranges_ok(a.pf) && ((a.pf[0].rows == 0 && a.pf[1].rows == 0) || a.H == 1024),
+    TSN_REQUIRE(pf_ranges_ok(a.pf) && (pf_workgroups(a.pf, 4) == 0 || a.H == 1024),
                 "reduce_ln: prefetch ranges (prefetch workgroups need 4 waves: H = 1024)");
     RedLnArgs b = a;
     b.pf_nwg = pf_workgroups(a.pf, 4);

@@ -6,9 +6,10 @@
 // (sample, head) and the softmax is online, so no score buffer exists.
 //
 // 8 waves: wave w serves queries 16*(w&3)..+15; waves 0-3 take the even 64-key blocks and waves
-// 4-7 the odd ones, each half keeping its own running max / sum / output, merged through LDS at
-// the end. K and Vᵀ blocks reach LDS by direct-to-LDS buffer loads (no register staging). At
-// S <= 512 all of them (128 KB) are loaded at once, every K block before the Vᵀ blocks are needed,
+// 4-7 the odd ones, each half keeping its own running max / sum / output; at the end each half
+// merges and stores 32 of the 64 output columns through LDS. K and Vᵀ blocks reach LDS by
+// direct-to-LDS buffer loads (no register staging). At S <= 512 all of them (128 KB) are loaded
+// at once, every K block before the Vᵀ blocks are needed,
 // and each half's key loop is software-pipelined (the next block's scores are multiplied before
 // this block's PV product); longer contexts use a two-stage ring. The running max is shared by the
 // four lanes holding a query's keys (row-swap permutes); the running sum is an MFMA product of the
@@ -404,42 +405,49 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
     }
     float l_i = lsum[0];   // every row of the ones product holds the same sum
 
-    // merge the two halves: waves 4-7 park (m, l, O) in LDS, waves 0-3 combine and store
+    // merge the two halves: half h combines and stores output columns 32h..32h+31 (dt = 2h, 2h+1).
+    // Each half parks its (m, l) and the two column groups the other half stores in LDS; the
+    // combination is the same per element whichever half forms it (o_0*f_0 + o_1*f_1, 1/l).
     block_barrier();
     float *red = (float *)smem;
-    float *slot = red + (wq * 64 + lane) * 18;
-    if (half == 1) {
-        slot[0] = m_i;
-        slot[1] = l_i;
+    float *mine = red + ((half * 4 + wq) * 64 + lane) * 10;
+    const float *other = red + (((half ^ 1) * 4 + wq) * 64 + lane) * 10;
+    mine[0] = m_i;
+    mine[1] = l_i;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) slot[2 + dt * 4 + r] = o[dt][r];
-    }
+        for (int r = 0; r < 4; ++r) mine[2 + j * 4 + r] = half ? o[j][r] : o[2 + j][r];   // selects: o stays in registers
     block_barrier();
-    if (half == 1) return;
-    const float m1 = slot[0], l1 = slot[1];
-    const float m = fmaxf(m_i, m1);
-    const float f0 = exp2f(m_i - m), f1 = exp2f(m1 - m);
-    const float l = l_i * f0 + l1 * f1;
+    const float m_o = other[0], l_o = other[1];
+    const float m = fmaxf(m_i, m_o);
+    const float f_s = exp2f(m_i - m), f_o = exp2f(m_o - m);
+    // half 0's terms first in both halves: l = l_0*f_0 + l_1*f_1
+    const float l = half == 0 ? l_i * f_s + l_o * f_o : l_o * f_o + l_i * f_s;
+    float om[2][4];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[dt][r] = o[dt][r] * f0 + slot[2 + dt * 4 + r] * f1;
+        for (int r = 0; r < 4; ++r) {
+            const float own = (half ? o[2 + j][r] : o[j][r]) * f_s, oth = other[2 + j * 4 + r] * f_o;
+            om[j][r] = half == 0 ? own + oth : oth + own;
+        }
 
     if (q < S) {
         const float inv = 1.0f / l;
         const int b = bh / a.nh, h = bh - b * a.nh;
         const long long orow = rowmap_phys(a.omap, b * S + q) * (long long)a.ldo + h * 64;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
+        for (int j = 0; j < 2; ++j) {
+            const int dt = 2 * half + j;
+            const float (&od)[4] = om[j];
             const int d0 = dt * 16 + g * 4;
             if (a.o_f32) {
                 float *op = (float *)a.O + orow + d0;
-                *(float4 *)op = make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
+                *(float4 *)op = make_float4(od[0] * inv, od[1] * inv, od[2] * inv, od[3] * inv);
             } else {
                 half_t *op = (half_t *)a.O + orow + d0;
-                const float y0 = o[dt][0] * inv, y1 = o[dt][1] * inv, y2 = o[dt][2] * inv, y3 = o[dt][3] * inv;
+                const float y0 = od[0] * inv, y1 = od[1] * inv, y2 = od[2] * inv, y3 = od[3] * inv;
                 const half4 hi = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
                 *(half4 *)op = hi;
                 if (a.o_lo)   // f16 remainder at column offset o_lo: hi + lo carries the f32 value

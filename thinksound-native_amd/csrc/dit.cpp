@@ -211,7 +211,7 @@ int DitModel::upload_weights(const uint16_t *host, size_t numel) {
     return TSN_OK;
 }
 
-int DitModel::modulation(const float *gs, int row0, int rows) {
+GemvArgs DitModel::mod_args(const float *gs, int row0, int rows) const {
     GemvArgs a;
     memset(&a, 0, sizeof a);
     a.W = Wmod_ + (size_t)row0 * s.H; a.ldw = s.H; a.wdt = DT_BF16;
@@ -219,7 +219,36 @@ int DitModel::modulation(const float *gs, int row0, int rows) {
     a.Y = MOD_ + row0; a.ldy = NMOD;
     a.bias = bmod_ + row0;
     a.N = rows; a.K = s.H; a.nb = s.B;
-    return launch_gemv(a, rt->dev.stream());
+    return a;
+}
+
+int DitModel::modulation(const float *gs, int row0, int rows) {
+    return launch_gemv(mod_args(gs, row0, rows), rt->dev.stream());
+}
+
+bool DitModel::mod_grid_ok() const {
+    if (s.B != 2 || s.H != 1024 || s.n_joint + s.n_fused == 0) return false;
+    const int tn = 3 * s.H / 128, spare = 32, ncu = 256;   // 128x128 QKV tiles
+    const int tj = ((s.B * s.La + 127) / 128 + (s.B * s.Lt + 127) / 128) * tn;
+    const int tf = (s.B * S + 127) / 128 * tn;
+    return (s.n_joint == 0 || tj <= ncu - spare) && (s.n_fused == 0 || tf <= ncu - spare);
+}
+
+// block 0's rows: both streams of joint block 0 (audio then text, adjacent), or fused block 0's
+int DitModel::first_mod_rows() const {
+    return s.n_joint > 0 ? jt_[0].mod_off + 6 * s.H : fu_[0].mod_off + 6 * s.H;
+}
+
+void DitModel::next_mod_gemv(GemmBatch &qb, Next next) const {
+    if (!mod_in_grid_) return;
+    int row0 = 0, rows = 0;
+    switch (next.kind) {
+        case NEXT_JOINT: row0 = ja_[next.idx].mod_off; rows = jt_[next.idx].mod_off + 6 * s.H - row0; break;
+        case NEXT_FUSED: row0 = fu_[next.idx].mod_off; rows = 6 * s.H; break;
+        case NEXT_FINAL: row0 = fin_mod_off_; rows = 2 * s.H; break;
+        default: return;
+    }
+    qb.gv = mod_args(gs_, row0, rows);
 }
 
 int DitModel::gs_from_g(const float *g) {
@@ -305,6 +334,7 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
         qb.pf[2] = PfRange{a.W1, s.F, H * 2, (long long)(a.conv ? 3 : 1) * H * 2};
         qb.pf[3] = PfRange{t.W1, s.F, H * 2, (long long)H * 2};
     }
+    next_mod_gemv(qb, next);
     TSN_TRY(gemm_run(qb, EPI_QKV));
 
     AttnArgs at;
@@ -374,6 +404,7 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
     qb.pf[0] = PfRange{w.Wo, H, H * 2, (long long)H * 2};   // the out-projection's weights
     if (!ln_prefetch() && !grid_prefetch())   // and FFN1's, read three launches later
         qb.pf[1] = PfRange{w.W1, s.F, H * 2, (long long)H * 2};
+    next_mod_gemv(qb, next);
     TSN_TRY(gemm_run(qb, EPI_QKV));
 
     AttnArgs at;
@@ -419,7 +450,7 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
 // processed in GEMV batches of up to 16 (the weights are read once per batch); pooled row r is
 // pooled[r % 16] (callers pass B rows for B <= 16 batches, or the 16-row repetition).
 int DitModel::enqueue_conditioning(const float *t, int rows, const float *pooled, float *temb, float *h1, float *g,
-                                   float *gs, float *mod) {
+                                   float *gs, float *mod, int mod_rows) {
     const hipStream_t st = rt->dev.stream();
     const int H = s.H;
     TSN_TRY(run("temb_kernel", 0, 0, [&] { return launch_temb_sinusoid(t, temb, rows, s.temb_dim, s.t_max_period, st); }));
@@ -442,8 +473,8 @@ int DitModel::enqueue_conditioning(const float *t, int rows, const float *pooled
         m.W = Wmod_; m.ldw = H; m.wdt = DT_BF16;
         m.X = gs + (size_t)r0 * H; m.ldx = H;
         m.Y = mod + (size_t)r0 * NMOD; m.ldy = NMOD;
-        m.bias = bmod_; m.N = NMOD; m.K = H; m.nb = nb;
-        TSN_TRY(run(K_GEMV, 2.0 * nb * (double)NMOD * H, 2.0 * (double)NMOD * H + 4.0 * nb * NMOD,
+        m.bias = bmod_; m.N = mod_rows; m.K = H; m.nb = nb;
+        TSN_TRY(run(K_GEMV, 2.0 * nb * (double)mod_rows * H, 2.0 * (double)mod_rows * H + 4.0 * nb * mod_rows,
                     [&] { return launch_gemv(m, st); }));
     }
     return TSN_OK;
@@ -463,10 +494,11 @@ int DitModel::enqueue_eval(const float *z, const float *t, const float *text, co
     TSN_TRY(rt->dev.make_current());
     const hipStream_t st = rt->dev.stream();
     const int B = s.B, H = s.H;
+    mod_in_grid_ = !mod_pre && mod_grid_ok();
     if (mod_pre) {
         mod_ = mod_pre;
     } else {
-        TSN_TRY(enqueue_conditioning(t, B, pooled, temb_, h1_, g_, gs_, MOD_));
+        TSN_TRY(enqueue_conditioning(t, B, pooled, temb_, h1_, g_, gs_, MOD_, mod_in_grid_ ? first_mod_rows() : NMOD));
         mod_ = MOD_;
     }
     // input projection (src/dit_fwd.cpp:142-149): z split into f16 hi|lo halves, one MFMA GEMM
@@ -567,7 +599,7 @@ int DitModel::enqueue_sample(float *x, const float *text, const float *pooled, i
     // per 16 rows, before the step loop (row st*B + b = step st, sample b)
     TSN_TRY(launch_copy_rows(pooled, s.H, RowMap{s.B, 0, 0}, pooled_rep_, s.H, rowmap_dense(16), 16, s.H,
                              rt->dev.stream()));
-    TSN_TRY(enqueue_conditioning(tsched_, steps * s.B, pooled_rep_, temb_all_, h1_all_, g_all_, gs_all_, mod_all_));
+    TSN_TRY(enqueue_conditioning(tsched_, steps * s.B, pooled_rep_, temb_all_, h1_all_, g_all_, gs_all_, mod_all_, NMOD));
     for (int st = 0; st < steps; ++st) {
         const float t_curr = 1.0f - (float)st / (float)steps;
         const float t_prev = 1.0f - (float)(st + 1) / (float)steps;

@@ -81,9 +81,9 @@ private:
     };
     // timestep embedding -> t-MLP (+ pooled) -> silu -> every adaLN modulation, for `rows` rows
     // (t [rows], pooled rows [rows][H] at ld H or repeated with period per, outputs [rows][.]),
-    // in GEMV batches of up to 16 rows
+    // in GEMV batches of up to 16 rows; modulation rows [0, mod_rows) only
     int enqueue_conditioning(const float *t, int rows, const float *pooled, float *temb, float *h1, float *g,
-                             float *gs, float *mod);
+                             float *gs, float *mod, int mod_rows);
     int enqueue_eval(const float *z, const float *t, const float *text, const float *pooled, float *v, float *taps,
                      const float *mod_pre);
     bool ln_prefetch() const;
@@ -93,6 +93,13 @@ private:
     int block_fused(int i, bool ln1, Next next);
     void next_ln(RedLnArgs &r, Next next, const RowMap *maps, int nseg);
     int modulation(const float *gs, int row0, int rows);
+    GemvArgs mod_args(const float *gs, int row0, int rows) const;
+    // an evaluation's modulation rows past block 0's are computed by the free CUs of the QKV grid
+    // of the block before the one that reads them (B = 2, every QKV grid a single round)
+    bool mod_grid_ok() const;
+    int first_mod_rows() const;
+    void next_mod_gemv(GemmBatch &qb, Next next) const;
+    bool mod_in_grid_ = false;
     int gs_from_g(const float *g);
 
     std::vector<StreamW> ja_, jt_, fu_;

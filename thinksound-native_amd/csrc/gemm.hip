@@ -18,6 +18,7 @@
 #include "kernels.h"
 #include "dpp.h"
 #include "prefetch.h"
+#include "gemv.h"
 #include "snake.h"
 
 #include <string.h>
@@ -935,8 +936,14 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
 template <int EPI, bool HL, int NSX = NS, bool BF = false>
 __device__ __forceinline__ void pipe_dp(const GemmBatch &bt) {
     const int tid = threadIdx.x;
-    if ((int)blockIdx.x >= bt.total_tiles) {   // prefetch workgroups after the tiles (GemmBatch::pf)
-        prefetch_wg<8>(bt.pf, blockIdx.x - bt.total_tiles, tid >> 6, tid & 63);
+    if ((int)blockIdx.x >= bt.total_tiles) {   // GEMV, then prefetch workgroups after the tiles
+        const int e = blockIdx.x - bt.total_tiles, wave = tid >> 6, lane = tid & 63;
+        if (e < bt.gv_nwg) {   // 4-row groups of the GEMV, strided over its workgroups' waves
+            for (int n0 = (e * 8 + wave) * GEMV_ROWS; n0 < bt.gv.N; n0 += bt.gv_nwg * 8 * GEMV_ROWS)
+                gemv_rows<uint16_t, 2>(bt.gv, n0, lane);
+            return;
+        }
+        prefetch_wg<8>(bt.pf, e - bt.gv_nwg, wave, lane);
         return;
     }
     const int wg = xcd_remap(blockIdx.x, bt.total_tiles);
@@ -1380,6 +1387,7 @@ void gemm_problem_init(GemmProblem &p) {
 int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     TSN_REQUIRE(b.nprob >= 1 && b.nprob <= 3, "gemm: 1 to 3 problems");
     b.pf_nwg = 0;
+    b.gv_nwg = 0;
     if (b.bf16) {   // one data-parallel schedule: no workspace, so no split and no stream-K
         TSN_REQUIRE(epi == EPI_STORE && !a_f32 && !b.small, "gemm bf16: plain store epilogue, bf16 A");
         b.ws = nullptr;
@@ -1624,6 +1632,19 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     // weight prefetch workgroups after the tiles: data-parallel pipelined kernels only
     TSN_REQUIRE(pf_ranges_ok(b.pf), "gemm: prefetch ranges");
     b.pf_nwg = pipe && !b.sk ? pf_workgroups(b.pf, 8) : 0;
+    // GEMV rows on the CUs a single-round grid leaves free (one pipelined workgroup per CU); they
+    // replace the prefetch workgroups
+    b.gv_nwg = 0;
+    if (b.gv.N > 0) {
+        const GemvArgs &g = b.gv;
+        TSN_REQUIRE(g.W && g.X && g.Y && g.wdt == DT_BF16 && g.nb == 2 && g.K == 1024 && g.ldw % 8 == 0 &&
+                        g.ldx % 4 == 0 && !g.addv && !g.Y2 && !g.silu,
+                    "gemm: grid GEMV needs BF16 W, two X rows, K = 1024, no addv / Y2 / SiLU");
+        if (pipe && !b.sk && !b.ns2 && !b.small && NCU - b.total_tiles >= 32) {
+            b.gv_nwg = NCU - b.total_tiles;
+            b.pf_nwg = 0;
+        }
+    }
     if (b.bf16) {
         TSN_REQUIRE(pipe, "gemm bf16: needs K % 64 == 0, N % 8 == 0 and 16-byte aligned rows, W, bias and Y");
         b.kname = b.ns2 ? "gemm_pipe2_bf16_kernel<0>" : "gemm_pipe_bf16_kernel<0>";
@@ -1643,13 +1664,14 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
 }
 
 int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
+    if (b.gv.N > 0 && b.gv_nwg == 0) TSN_TRY(launch_gemv(b.gv, st));   // no free CUs in this grid
     if (b.small) {
         TSN_REQUIRE(epi == EPI_RESID, "gemm small tiles: residual epilogue only");
         TSN_LAUNCH((gemm_small_kernel<EPI_RESID>), dim3(b.total_tiles + b.pf_nwg), dim3(256), 0, st, b);
         TSN_HIP_CHECK(hipGetLastError());
         return TSN_OK;
     }
-    dim3 grid(b.sk ? b.sk_g : b.total_tiles + b.pf_nwg), block(b.pipe ? 512 : 256);
+    dim3 grid(b.sk ? b.sk_g : b.total_tiles + b.gv_nwg + b.pf_nwg), block(b.pipe ? 512 : 256);
     if (b.bf16) {
         TSN_REQUIRE(b.pipe && epi == EPI_STORE, "gemm bf16: pipelined store kernel only");
         if (b.ns2) TSN_LAUNCH((gemm_pipe2_bf16_kernel<EPI_STORE>), grid, block, 0, st, b);

@@ -76,6 +76,19 @@ constexpr int PF_RANGES = 4;     // ranges per launch
 bool pf_ranges_ok(const PfRange (&pf)[PF_RANGES]);
 int pf_workgroups(const PfRange (&pf)[PF_RANGES], int waves);
 
+/* ------------------------------------------------------------------ GEMV */
+// Y[b*ldy + n] = sum_k W[n*ldw + k] X[b*ldx + k] (+ bias[n], + addv[b*ld_add + n], SiLU) for the
+// nb rows b of X; Y2 (optional) = silu of the value written to Y.
+struct GemvArgs {
+    const void *W; int ldw; int wdt;
+    const float *X; int ldx;
+    float *Y; int ldy;
+    const float *bias;
+    const float *addv; int ld_add;
+    float *Y2; int ldy2;
+    int N, K, nb, silu;
+};
+
 struct GemmBatch {
     GemmProblem p[3];
     int nprob = 0;
@@ -117,6 +130,12 @@ struct GemmBatch {
     // pf_nwg is set by gemm_plan.
     PfRange pf[PF_RANGES];
     int pf_nwg = 0;
+    // rows of an HBM-bound GEMV (gv.N > 0; BF16 W, two rows of X, K = 1024) for extra workgroups
+    // launched after the tiles, on the CUs a single-round data-parallel pipelined grid leaves free;
+    // they take the place of the prefetch workgroups. gemm_plan sets gv_nwg; where it stays 0 the
+    // launcher runs the GEMV as its own kernel just before the GEMM.
+    GemvArgs gv{};
+    int gv_nwg = 0;
 };
 
 // a_f32: A operand is f32 (converted to f16 on load). All problems share the epilogue kind.
@@ -207,15 +226,6 @@ int launch_copy_peak(const float *src, float *dst, size_t n4, hipStream_t st);
 /* ------------------------------------------------------------------ GEMV (small M) */
 // Y[b][n] = act(sum_k W[n][k] * X[b][k] + bias[n] + addv[b][n]); optional Y2 = silu(Y).
 // W is bf16, f16 or f32 (wdt); X, Y f32; nb <= 16 rows of X. HBM-bound: one wave per 4 rows of W.
-struct GemvArgs {
-    const void *W; int ldw; int wdt;
-    const float *X; int ldx;
-    float *Y; int ldy;
-    const float *bias;
-    const float *addv; int ld_add;
-    float *Y2; int ldy2;
-    int N, K, nb, silu;
-};
 int launch_gemv(const GemvArgs &a, hipStream_t st);
 
 /* ------------------------------------------------------------------ f32 SIMT linear */

@@ -941,9 +941,10 @@ __device__ __forceinline__ void pipe_dp(const GemmBatch &bt) {
         if (e < bt.gv_nwg) {   // 4-row groups of the GEMV, strided over its workgroups' waves
             for (int n0 = (e * 8 + wave) * GEMV_ROWS; n0 < bt.gv.N; n0 += bt.gv_nwg * 8 * GEMV_ROWS)
                 gemv_rows<uint16_t, 2>(bt.gv, n0, lane);
+            for (int c = e; c < bt.pf_nwg; c += bt.gv_nwg) prefetch_wg<8>(bt.pf, c, wave, lane);   // then the prefetch
             return;
         }
-        prefetch_wg<8>(bt.pf, e - bt.gv_nwg, wave, lane);
+        prefetch_wg<8>(bt.pf, e, wave, lane);   // gv_nwg == 0 here
         return;
     }
     const int wg = xcd_remap(blockIdx.x, bt.total_tiles);
@@ -1640,10 +1641,9 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         TSN_REQUIRE(g.W && g.X && g.Y && g.wdt == DT_BF16 && g.nb == 2 && g.K == 1024 && g.ldw % 8 == 0 &&
                         g.ldx % 4 == 0 && !g.addv && !g.Y2 && !g.silu,
                     "gemm: grid GEMV needs BF16 W, two X rows, K = 1024, no addv / Y2 / SiLU");
-        if (pipe && !b.sk && !b.ns2 && !b.small && NCU - b.total_tiles >= 32) {
-            b.gv_nwg = NCU - b.total_tiles;
-            b.pf_nwg = 0;
-        }
+        if (pipe && !b.sk && !b.ns2 && !b.small && NCU - b.total_tiles >= 32)
+            b.gv_nwg = NCU - b.total_tiles;   // the prefetch chunks then follow each one's GEMV rows
+
     }
     if (b.bf16) {
         TSN_REQUIRE(pipe, "gemm bf16: needs K % 64 == 0, N % 8 == 0 and 16-byte aligned rows, W, bias and Y");
@@ -1671,7 +1671,7 @@ int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st)
         TSN_HIP_CHECK(hipGetLastError());
         return TSN_OK;
     }
-    dim3 grid(b.sk ? b.sk_g : b.total_tiles + b.gv_nwg + b.pf_nwg), block(b.pipe ? 512 : 256);
+    dim3 grid(b.sk ? b.sk_g : b.total_tiles + (b.gv_nwg ? b.gv_nwg : b.pf_nwg)), block(b.pipe ? 512 : 256);
     if (b.bf16) {
         TSN_REQUIRE(b.pipe && epi == EPI_STORE, "gemm bf16: pipelined store kernel only");
         if (b.ns2) TSN_LAUNCH((gemm_pipe2_bf16_kernel<EPI_STORE>), grid, block, 0, st, b);

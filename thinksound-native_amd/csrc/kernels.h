@@ -132,8 +132,9 @@ struct GemmBatch {
     int pf_nwg = 0;
     // rows of an HBM-bound GEMV (gv.N > 0; BF16 W, two rows of X, K = 1024) for extra workgroups
     // launched after the tiles, on the CUs a single-round data-parallel pipelined grid leaves free;
-    // they take the place of the prefetch workgroups. gemm_plan sets gv_nwg; where it stays 0 the
-    // launcher runs the GEMV as its own kernel just before the GEMM.
+    // each then runs its share of the prefetch chunks (no prefetch workgroups of their own).
+    // gemm_plan sets gv_nwg; where it stays 0 the launcher runs the GEMV as its own kernel just
+    // before the GEMM.
     GemvArgs gv{};
     int gv_nwg = 0;
 };

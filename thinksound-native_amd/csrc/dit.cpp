@@ -474,8 +474,9 @@ int DitModel::enqueue_conditioning(const float *t, int rows, const float *pooled
         m.X = gs + (size_t)r0 * H; m.ldx = H;
         m.Y = mod + (size_t)r0 * NMOD; m.ldy = NMOD;
         m.bias = bmod_; m.N = mod_rows; m.K = H; m.nb = nb;
-        TSN_TRY(run(K_GEMV, 2.0 * nb * (double)mod_rows * H, 2.0 * (double)mod_rows * H + 4.0 * nb * mod_rows,
-                    [&] { return launch_gemv(m, st); }));
+        if (mod_rows > 0)
+            TSN_TRY(run(K_GEMV, 2.0 * nb * (double)mod_rows * H, 2.0 * (double)mod_rows * H + 4.0 * nb * mod_rows,
+                        [&] { return launch_gemv(m, st); }));
     }
     return TSN_OK;
 }
@@ -498,7 +499,7 @@ int DitModel::enqueue_eval(const float *z, const float *t, const float *text, co
     if (mod_pre) {
         mod_ = mod_pre;
     } else {
-        TSN_TRY(enqueue_conditioning(t, B, pooled, temb_, h1_, g_, gs_, MOD_, mod_in_grid_ ? first_mod_rows() : NMOD));
+        TSN_TRY(enqueue_conditioning(t, B, pooled, temb_, h1_, g_, gs_, MOD_, mod_in_grid_ ? 0 : NMOD));
         mod_ = MOD_;
     }
     // input projection (src/dit_fwd.cpp:142-149): z split into f16 hi|lo halves, one MFMA GEMM
@@ -515,6 +516,7 @@ int DitModel::enqueue_eval(const float *z, const float *t, const float *text, co
         p.a_T = B * s.La; p.W = Win2_; p.ldw = 2 * s.latent; p.bias = bin_;
         p.M = B * s.La; p.N = H; p.K = 2 * s.latent;
         p.Y = X_; p.ldy = H; p.ymap = RowMap{s.La, S, 0}; p.y_f16 = 0;
+        if (mod_in_grid_) ib.gv = mod_args(gs_, 0, first_mod_rows());   // block 0's modulation rows
         TSN_TRY(gemm_run(ib, EPI_STORE));
     }
     if (s.Lt > 0)

@@ -94,8 +94,9 @@ private:
     void next_ln(RedLnArgs &r, Next next, const RowMap *maps, int nseg);
     int modulation(const float *gs, int row0, int rows);
     GemvArgs mod_args(const float *gs, int row0, int rows) const;
-    // an evaluation's modulation rows past block 0's are computed by the free CUs of the QKV grid
-    // of the block before the one that reads them (B = 2, every QKV grid a single round)
+    // an evaluation's modulation rows are computed by free CUs of GEMM grids: block 0's by the
+    // input projection's, later blocks' (and the final layer's) by the QKV grid of the block
+    // before the one that reads them (B = 2, every QKV grid a single round)
     bool mod_grid_ok() const;
     int first_mod_rows() const;
     void next_mod_gemv(GemmBatch &qb, Next next) const;

@@ -52,6 +52,9 @@ int tsn_begin(tsn_runtime *rt);                                 /* Device::begin
 int tsn_commit(tsn_runtime *rt);                                /* Device::commit src/gpu.h:38 */
 double tsn_last_gpu_ms(tsn_runtime *rt);                        /* Device::last_gpu_ms src/gpu.h:40 */
 int tsn_sync(tsn_runtime *rt);
+/* Live device allocations this runtime owns: their number and bytes (as requested). No reference
+ * counterpart (Metal buffers are never freed); lets a caller check that a call allocated nothing. */
+int tsn_runtime_alloc_stats(tsn_runtime *rt, size_t *count, size_t *bytes);
 
 /* ---------------- launcher runtime: tn::Runtime (src/net.h:18-51) ---------------- */
 /* Y[M,N] = X[M,K]·W[N,K]^T (+bias[N], f32). Runtime::gemm src/net.h:24-26, src/net.mm:14-23.
@@ -73,7 +76,10 @@ int tsn_gemm(tsn_runtime *rt, int wdtype, const void *W, const void *X, int xdty
  * split of an f32 X goes to a fixed 32 MiB device array per GPU instead of the runtime's scratch, so
  * with f16 W and f32 X it needs M*K <= tsn_gemm_noalloc_max_elems() (TSN_ERR_ARG beyond). The array
  * is shared by every call on one GPU and keeps the last call's contents (nothing in it needs to
- * start at zero); calls that overlap on one GPU race. */
+ * start at zero). Calls on one GPU are ordered on the device: a call from another stream (another
+ * runtime) waits for the previous call's GEMM through a per-GPU event. Calls made while the stream
+ * is being captured into a graph are not ordered that way: the caller orders the graph's launches
+ * against other users of the array. */
 int tsn_gemm_noalloc(tsn_runtime *rt, int wdtype, const void *W, const void *X, int xdtype, void *Y, int ydtype,
                      const float *bias, uint32_t M, uint32_t N, uint32_t K, uint32_t ldx, uint32_t ldw, uint32_t ldy);
 size_t tsn_gemm_noalloc_max_elems(void);

@@ -1,16 +1,20 @@
 #!/usr/bin/env python3
-"""Writes tests/golden/sampler_8s_24steps.npz (default) or sampler_30s_24steps.npz (argument 30s):
-the final latent of the full rectified-flow Euler sampler (src/pipeline.cpp:141-155: 24 steps,
-t_s = 1 - s/24, CFG 5.0, v = v_u + 5 (v_c - v_u)), one prompt as a cond/uncond pair (B = 2,
-Lt = 141, 7 joint + 14 fused blocks, H = 1024; La = 256 at 8 s, 960 at 30 s), computed by the CPU
-oracle (oracle/, orc_dit_sample) on exactly the weights and inputs the benchmark times: BF16
-weights N(0, 0.02) from seed 4242 (q/k norm weights N(0, 0.02) too), z0, text and pooled features
-from seed 4242, the unconditional arm with zeroed text and pooled features.
+"""Writes tests/golden/sampler_8s_24steps.npz (default), sampler_30s_24steps.npz (argument 30s) or
+sampler_b16_24steps.npz (argument b16): the final latent of the full rectified-flow Euler sampler
+(src/pipeline.cpp:141-155: 24 steps, t_s = 1 - s/24, CFG 5.0, v = v_u + 5 (v_c - v_u)), computed by
+the CPU oracle (oracle/, orc_dit_sample) on exactly the weights and inputs the benchmark times:
+BF16 weights N(0, 0.02) from seed 4242 (q/k norm weights N(0, 0.02) too), Lt = 141, 7 joint + 14
+fused blocks, H = 1024, each prompt as a cond/uncond pair, the unconditional arm with zeroed text
+and pooled features.
+  8s:  one prompt, La = 256; z0, text and pooled features from seed 4242;
+  30s: one prompt, La = 960 (S = 1101); inputs from seed 4242;
+  b16: eight prompts (batch 16), La = 256; prompt p's z0, text and pooled features from seed p + 1.
 
-The oracle takes about 3.5 minutes (8 s) or 42 minutes (30 s) on 8 cores for the 24 evaluations,
-too long for the GPU suite; the fixture holds the seeds, input checksums and the expected final
-latent and z0 (130 KB / 490 KB). Run from the repository root after building the oracle (make -C oracle):
-    python3 tests/golden/make_sampler_golden.py [8s|30s]
+The oracle takes about 3.5 minutes (8s), 42 minutes (30s) or 30 minutes (b16) on 8 cores for the 24
+evaluations, too long for the GPU suite; the fixture holds the seeds, input checksums and the
+expected final latent (and z0 for the single-prompt workloads). Run from the repository root after
+building the oracle (make -C oracle):
+    python3 tests/golden/make_sampler_golden.py [8s|30s|b16]
 """
 import importlib
 import os
@@ -24,7 +28,10 @@ sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.join(ROOT, "oracle"))
 
 SEED, NORM_MEAN, STEPS, CFG = 4242, 0.0, 24, 5.0
-WORKLOADS = {"8s": (2, "sampler_8s_24steps.npz"), "30s": (3, "sampler_30s_24steps.npz")}   # default_spec index
+PROMPT_SEEDS = list(range(1, 9))
+# workload -> (default_spec index, fixture name)
+WORKLOADS = {"8s": (2, "sampler_8s_24steps.npz"), "30s": (3, "sampler_30s_24steps.npz"),
+             "b16": (4, "sampler_b16_24steps.npz")}
 
 
 def main():
@@ -35,16 +42,25 @@ def main():
     OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), name)
     spec = tsn.default_spec(idx)
     w16 = tsn.synth_weights(spec, SEED, NORM_MEAN)
-    inp = tsn.synth_inputs(spec, SEED, cfg_pairs=True)
+    if which == "b16":
+        inp = tsn.synth_prompt_inputs(spec, PROMPT_SEEDS)
+    else:
+        inp = tsn.synth_inputs(spec, SEED, cfg_pairs=True)
     x0 = inp["z"][0::2].copy()
     t0 = time.time()
     x = pyoracle.dit_sample(spec, tsn.bf16_to_f32(w16), x0, inp["text"], inp["pooled"], STEPS, CFG)
     print("oracle sampler: %.1f s on %d threads" % (time.time() - t0, pyoracle.num_threads()))
-    np.savez(OUT, x=x.astype(np.float32), x0=x0.astype(np.float32),
+    extra = {}
+    if which == "b16":
+        extra["prompt_seeds"] = np.array(PROMPT_SEEDS)
+        extra["x0_checksums"] = x0.astype(np.float64).reshape(len(PROMPT_SEEDS), -1).sum(axis=1)
+    else:
+        extra["x0"] = x0.astype(np.float32)
+    np.savez(OUT, x=x.astype(np.float32),
              seeds=np.array([SEED, STEPS]), norm_mean=np.float64(NORM_MEAN), cfg=np.float64(CFG),
              w_checksum=np.float64(tsn.bf16_to_f32(w16).astype(np.float64).sum()),
              text_checksum=np.float64(inp["text"].astype(np.float64).sum()),
-             pooled_checksum=np.float64(inp["pooled"].astype(np.float64).sum()))
+             pooled_checksum=np.float64(inp["pooled"].astype(np.float64).sum()), **extra)
     print("wrote", OUT)
 
 

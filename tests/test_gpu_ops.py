@@ -332,7 +332,10 @@ def test_elementwise(tsn, rt, orc):
     assert np.array_equal(yy.numpy(), orc.add_bcast_col(X, v))
 
 
-@pytest.mark.parametrize("S", [397, 1101, 1, 64, 65, 100, 500, 512])
+# routes (16 heads, one sample): S <= 512 the all-resident eight-wave kernel; 512 < S with at most
+# 256 query-tile workgroups (S = 600: 160, S = 1024: 256) the two-stage eight-wave kernel; more than
+# 256 workgroups (S = 1101: 288) the four-wave kernel
+@pytest.mark.parametrize("S", [397, 1101, 1, 64, 65, 100, 500, 512, 600, 1024])
 def test_attention(tsn, rt, orc, S):
     r = rng(61 + S)
     H, nh, hd = 1024, 16, 64

@@ -61,3 +61,54 @@ def test_gemm_noalloc_other_routes_and_limit(tsn, rt):
     with pytest.raises(tsn.TsnError) as e:
         rt.gemm_noalloc(F16, Wd, Xd, F32, Yd, F32, None, M, 64, K)
     assert e.value.code == 1 and "static scratch" in str(e.value)
+
+
+def test_gemm_noalloc_allocates_nothing_on_a_fresh_runtime(tsn):
+    """On a runtime that has never run tsn_gemm (so its grow-on-demand scratch does not exist), the
+    hi|lo route of tsn_gemm_noalloc leaves the runtime's allocations exactly as they were; a later
+    tsn_gemm of the same shape grows the scratch (so the accessor does see it) and gives the same
+    bits."""
+    r = rng(321)
+    M, N, K = 512, 1024, 1024
+    X, W, b = _case(None, r, M, N, K, F32)
+    with tsn.Runtime(0) as rt2:
+        Xd, Wd, bd = rt2.array(X), rt2.array(W), rt2.array(b)
+        Y1, Y0 = rt2.empty((M, N)), rt2.empty((M, N))
+        before = rt2.alloc_stats()
+        rt2.gemm_noalloc(F16, Wd, Xd, F32, Y1, F32, bd, M, N, K)
+        rt2.sync()
+        assert rt2.alloc_stats() == before
+        rt2.gemm(F16, Wd, Xd, F32, Y0, F32, bd, M, N, K)
+        rt2.sync()
+        cnt, nbytes = rt2.alloc_stats()
+        assert cnt == before[0] + 1 and nbytes >= before[1] + 4 * M * K
+        assert np.array_equal(Y0.numpy().view(np.uint32), Y1.numpy().view(np.uint32))
+        ref = X.astype(np.float64) @ W.astype(np.float64).T + b
+        assert rel_l2(Y1.numpy(), ref) < 2e-5
+        for a in (Xd, Wd, bd, Y1, Y0):
+            a.free()
+
+
+def test_gemm_noalloc_two_runtimes_in_a_row(tsn, rt):
+    """Two runtimes (two streams) share the per-GPU array: back-to-back calls from both, with no
+    host synchronisation between them, are ordered on the device and each matches tsn_gemm."""
+    r = rng(99)
+    shapes = [(794, 3072, 1024), (600, 1024, 2048)]
+    with tsn.Runtime(0) as rt2:
+        runs = []
+        for (M, N, K), R in zip(shapes, (rt, rt2)):
+            X, W, b = _case(None, r, M, N, K, F32)
+            runs.append((R, M, N, K, R.array(X), R.array(W), R.array(b), R.empty((M, N)), R.empty((M, N))))
+        for R, M, N, K, Xd, Wd, bd, Y0, Y1 in runs:
+            R.gemm(F16, Wd, Xd, F32, Y0, F32, bd, M, N, K)
+        rt.sync()
+        rt2.sync()
+        for _ in range(3):
+            for R, M, N, K, Xd, Wd, bd, Y0, Y1 in runs:
+                R.gemm_noalloc(F16, Wd, Xd, F32, Y1, F32, bd, M, N, K)
+        rt.sync()
+        rt2.sync()
+        for R, M, N, K, Xd, Wd, bd, Y0, Y1 in runs:
+            assert np.array_equal(Y0.numpy().view(np.uint32), Y1.numpy().view(np.uint32))
+            for a in (Xd, Wd, bd, Y0, Y1):
+                a.free()

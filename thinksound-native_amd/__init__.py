@@ -154,6 +154,7 @@ _SIGS = {
     "tsn_begin": [_P],
     "tsn_commit": [_P],
     "tsn_sync": [_P],
+    "tsn_runtime_alloc_stats": [_P, ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)],
     "tsn_gemm": [_P, _I, _P, _P, _I, _P, _I, _P, _U32, _U32, _U32, _U32, _U32, _U32],
     "tsn_gemm_noalloc": [_P, _I, _P, _P, _I, _P, _I, _P, _U32, _U32, _U32, _U32, _U32, _U32],
     "tsn_gemm_noalloc_max_elems": [],
@@ -853,6 +854,12 @@ class Runtime:
     def sync(self):
         call("tsn_sync", self.h)
 
+    def alloc_stats(self):
+        """(count, bytes) of the device allocations this runtime owns"""
+        c, b = _SZ(), _SZ()
+        call("tsn_runtime_alloc_stats", self.h, ctypes.byref(c), ctypes.byref(b))
+        return c.value, b.value
+
     def begin(self):
         call("tsn_begin", self.h)
 
@@ -1143,6 +1150,25 @@ def synth_inputs(spec, seed=4242, cfg_pairs=False):
         text = synth_normal_f32(seed, IDX_TEXT, 0.0, 1.0, (B, Lt, H))
         pooled = synth_normal_f32(seed, IDX_POOLED, 0.0, 1.0, (B, H))
         t = np.repeat(synth_uniform_f32(seed, IDX_T, 0.0, 1.0, (1,)), B).astype(np.float32)
+    return {"z": z, "t": t, "text": text, "pooled": pooled}
+
+
+def synth_prompt_inputs(spec, prompt_seeds, t_seed=4242):
+    """Independent prompts as (cond, uncond) pairs: prompt p's latent, text and pooled features come
+    from its own seed prompt_seeds[p] (the batch-16 throughput workload uses seeds 1..8), the
+    unconditional arm of each pair gets zeroed text and pooled features, and every sample shares
+    one t drawn from t_seed."""
+    B, La, Lt, H, lat = spec.B, spec.La, spec.Lt, spec.H, spec.latent
+    if len(prompt_seeds) * 2 != B:
+        raise ValueError("need B/2 = %d prompt seeds, got %d" % (B // 2, len(prompt_seeds)))
+    z = np.empty((B, La, lat), np.float32)
+    text = np.zeros((B, Lt, H), np.float32)
+    pooled = np.zeros((B, H), np.float32)
+    for p, s in enumerate(prompt_seeds):
+        z[2 * p] = z[2 * p + 1] = synth_normal_f32(s, IDX_Z, 0.0, 1.0, (La, lat))
+        text[2 * p] = synth_normal_f32(s, IDX_TEXT, 0.0, 1.0, (Lt, H))
+        pooled[2 * p] = synth_normal_f32(s, IDX_POOLED, 0.0, 1.0, (H,))
+    t = np.repeat(synth_uniform_f32(t_seed, IDX_T, 0.0, 1.0, (1,)), B).astype(np.float32)
     return {"z": z, "t": t, "text": text, "pooled": pooled}
 
 

@@ -158,6 +158,12 @@ int tsn_begin(tsn_runtime *rt) { RT_CHECK(rt); return rt->rt.dev.begin(); }
 int tsn_commit(tsn_runtime *rt) { RT_CHECK(rt); return rt->rt.dev.commit(); }
 double tsn_last_gpu_ms(tsn_runtime *rt) { return rt ? rt->rt.dev.last_gpu_ms() : -1.0; }
 int tsn_sync(tsn_runtime *rt) { RT_CHECK(rt); return rt->rt.dev.sync(); }
+int tsn_runtime_alloc_stats(tsn_runtime *rt, size_t *count, size_t *bytes) {
+    RT_CHECK(rt);
+    if (count) *count = rt->rt.dev.owned_count();
+    if (bytes) *bytes = rt->rt.dev.owned_bytes();
+    return TSN_OK;
+}
 
 int tsn_gemm(tsn_runtime *rt, int wdtype, const void *W, const void *X, int xdtype, void *Y, int ydtype,
              const float *bias, uint32_t M, uint32_t N, uint32_t K, uint32_t ldx, uint32_t ldw, uint32_t ldy) {

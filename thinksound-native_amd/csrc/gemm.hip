@@ -5,16 +5,29 @@
 // stored [OC][K][IC] so each 64-wide K tile is one tap of IC channels, and the A loader reads
 // row t - pad + tap of the same sample (zero outside the sample) — no im2col buffer.
 //
-// Tile: 128x128x64, 256 threads = 4 waves in 2x2, each wave 64x64 = 4x4 MFMA 16x16x32 f16
-// blocks (64 f32 accumulators per lane). LDS: A and B tiles, two stages, rows padded to 72
-// halves (144 B) so the 16 rows one MFMA operand read touches fall in distinct banks.
-// One barrier per K tile: the next tile is loaded into registers before the MFMAs of the
-// current tile and written to the other LDS stage after them.
+// Kernels in this file (all 128x128 C tiles over 64-wide K tiles unless noted; MFMA
+// v_mfma_f32_16x16x32_f16, or _bf16 for bf16 operands, with f32 accumulation):
+//  * gemm_pipe_kernel / _hl / _bf16 (the production path): 512 threads = 8 waves, two per SIMD,
+//    each wave a 32x64 block. Operands move global -> LDS by direct-to-LDS DMA
+//    (buffer_load_dwordx4 ... lds) into a ring of NS = 4 stages (128 KB), rows XOR-swizzled in
+//    16-byte chunks so MFMA operand reads are conflict-free; one barrier per K tile; the C tile is
+//    staged through LDS and the epilogue runs on 16-byte chunks. One workgroup per CU.
+//  * gemm_pipe2_kernel / _hl / _bf16: the same loop with two stages (68 KB), two workgroups per CU,
+//    for data-parallel grids of more than one round (one workgroup's epilogue and waits overlap the
+//    other's K loop).
+//  * gemm_small_kernel: 64x64 tiles, 4 waves of 32x32, five 16 KB stages, two workgroups per CU,
+//    residual epilogue in place, for N = K = 1024 GEMMs whose 128x128 grid cannot fill the chip.
+//  * gemm_sk_kernel + gemm_fixup_kernel: stream-K over (tile, K tile) units, with the cut tiles
+//    finished in-kernel by their last contributor or by the fixup launch.
+//  * splitk_reduce_kernel: classic split-K sum in split order, then the epilogue.
+//  * gemm_f16_kernel: register-staged 256-thread kernel (4 waves of 64x64, two padded LDS stages)
+//    for shapes the pipelined kernels do not take (f32 A, K not a multiple of 64, unaligned rows).
 //
-// Work order: grid = all tiles of all problems (<= 2, e.g. audio + text stream of a joint
-// block). Workgroup IDs are remapped so each XCD (8 per MI355X, dispatched round-robin by
-// workgroup ID) receives one contiguous range of tiles, and tiles are numbered n-major, so the
-// workgroups of one XCD share W column blocks in that XCD's L2.
+// Work order: grid = all tiles of all problems (<= 3, e.g. audio + text stream of a joint block).
+// Workgroup IDs are remapped so each XCD (8 per MI355X, dispatched round-robin by workgroup ID)
+// receives one contiguous range of tiles (xcd_remap), and tiles are grouped by up to 8 m tiles with
+// n slow inside a group (tile_mn), so the workgroups of one XCD share A rows and W columns in that
+// XCD's L2. Deterministic: every sum runs in a fixed order, no float atomics.
 #include "kernels.h"
 #include "dpp.h"
 #include "prefetch.h"
@@ -872,6 +885,21 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
         // raw partial tile written through to memory (sc1), so the tile's last contributor reads
         // it from any XCD; then the arrival. The last of the tile's contributors sums every
         // contributor's slot in K order into the LDS C tile and runs the epilogue.
+        //
+        // Why no release/acquire fence is needed: on gfx942/gfx950 the SC1 bit of a buffer access
+        // sets its scope to agent. An agent-scope store is written through the XCD's L2 to memory,
+        // and its vmcnt decrement comes with that write's acknowledgement; an agent-scope load is
+        // served from memory, never from a stale line of another XCD's L2. The AMDGPU memory
+        // model's agent-scope fences exist for PLAIN accesses: release = buffer_wbl2 sc1 (write
+        // back dirty L2 lines of plain stores), acquire = buffer_inv sc1 (drop L2 lines before
+        // plain loads). No plain access takes part in this hand-off: every slot store and every
+        // slot load is SC1. Order: each thread's slot stores complete (s_waitcnt vmcnt(0)) before
+        // the barrier; the arrival atomic (agent scope, performed at the coherence point) is
+        // issued after it; the slot loads are issued only after the counter's value came back
+        // and passed a second barrier (control dependence). So every contributor's partial is in
+        // memory before the last arrival is counted, and the last contributor reads it from
+        // there. A fence pair here would add an L2 write-back and an L2 invalidate (measured at
+        // about 7 us for buffer_inv sc1) per cut tile.
         const __amdgpu_buffer_rsrc_t rp = make_brsrc(part);
 #pragma unroll 1
         for (int p = 0; p < 8; ++p) {

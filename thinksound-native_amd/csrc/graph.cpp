@@ -169,17 +169,27 @@ int GraphRunner::resid_ln(GemmBatch &b, RedLnArgs &r, int H, float eps) {
     return run(r.ymode == LN_F16_HILO ? K_RLNHL : K_RLN16, 0, bytes, [&] { return launch_reduce_ln(r, st); });
 }
 
+// The batch's GEMV rows (GemmBatch::gv: run by extra workgroups of the grid, or as a kernel of its
+// own just before it) count toward the launch that runs them: 2*nb*N*K flops; W once at its
+// storage type, the nb rows of X, and Y (plus silu(Y) when Y2 is set) as f32.
+static double gemv_flops(const GemvArgs &g) { return g.N > 0 ? 2.0 * g.nb * (double)g.N * g.K : 0.0; }
+static double gemv_bytes(const GemvArgs &g) {
+    if (g.N <= 0) return 0.0;
+    const double wb = g.wdt == DT_F32 ? 4.0 : 2.0;
+    return wb * g.N * (double)g.K + 4.0 * g.nb * (double)g.K + 4.0 * g.nb * (double)g.N * (g.Y2 ? 2 : 1);
+}
+
 double gemm_flops(const GemmBatch &b) {
-    double f = 0;
+    double f = gemv_flops(b.gv);
     for (int i = 0; i < b.nprob; ++i) f += 2.0 * b.p[i].M * (double)b.p[i].N * b.p[i].K / (b.p[i].w_half ? 2 : 1);
     return f;
 }
 
 // A once (conv taps re-read the same rows), W once, output at its storage type (residual: read +
-// write f32; SwiGLU: half the columns). Flops of a hi|lo operand against half-width W count the
-// model's K (half the K the MFMAs run).
+// write f32; SwiGLU: half the columns), plus the batch's GEMV rows. Flops of a hi|lo operand
+// against half-width W count the model's K (half the K the MFMAs run).
 double gemm_bytes(const GemmBatch &b, int epi) {
-    double x = 0;
+    double x = gemv_bytes(b.gv);
     for (int i = 0; i < b.nprob; ++i) {
         const GemmProblem &p = b.p[i];
         double out = epi == EPI_RESID ? 8.0 : epi == EPI_SWIGLU ? 1.0 : epi == EPI_SNAKE ? 6.0

@@ -8,8 +8,15 @@
 // from hipGetSymbolAddress, taken once per device with that device current (noalloc_init, called
 // from the runtime's init), and only that address is ever passed to a kernel. Every call on one GPU
 // shares the array and leaves its contents behind; nothing in it has to start at zero (the split
-// kernel writes every element the GEMM reads). Calls that overlap on one GPU (two streams, two
-// threads, two runtimes) race on the array.
+// kernel writes every element the GEMM reads).
+//
+// Ordering on the device: every runtime has its own stream, so two runtimes (or two host threads)
+// calling one after the other could otherwise run their split and GEMM kernels at the same time on
+// one array. Each device keeps one event, created at init: a call waits on it when the previous
+// call came from another stream, and records it after its GEMM (hipStreamWaitEvent and
+// hipEventRecord allocate nothing). A call made while its stream is being captured into a graph
+// cannot order itself against work outside the capture this way; there the caller must order the
+// graph's launches against other users of the array (one stream, or its own events).
 #include "runtime.h"
 
 #include <mutex>
@@ -24,7 +31,9 @@ static __device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
 
 constexpr int MAX_DEVICES = 64;
 std::mutex g_mu;
-void *g_scratch_dev[MAX_DEVICES] = {};   // device address of `scratch` on each GPU
+void *g_scratch_dev[MAX_DEVICES] = {};         // device address of `scratch` on each GPU
+hipEvent_t g_done[MAX_DEVICES] = {};           // recorded after each (uncaptured) call's GEMM
+hipStream_t g_last_stream[MAX_DEVICES] = {};   // the stream that recorded it
 
 } // namespace
 
@@ -40,6 +49,9 @@ int noalloc_init(int device) {
     void *p = nullptr;
     TSN_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
     TSN_REQUIRE(p != nullptr, "noalloc: no device address for the scratch array");
+    hipEvent_t ev = nullptr;
+    TSN_HIP_CHECK(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+    g_done[device] = ev;
     g_scratch_dev[device] = p;
     return TSN_OK;
 }
@@ -59,18 +71,28 @@ int gemm_noalloc(Runtime &rt, int wdt, const void *W, const void *X, int xdt, vo
         return TSN_ERR_ARG;
     }
     TSN_TRY(rt.dev.make_current());
-    void *hl = nullptr;
+    const int d = rt.dev.device();
+    bool ready = false;
     {
         std::lock_guard<std::mutex> lock(g_mu);
-        hl = g_scratch_dev[rt.dev.device()];
+        ready = g_scratch_dev[d] != nullptr;
     }
-    if (!hl) TSN_TRY(noalloc_init(rt.dev.device()));
-    {
-        std::lock_guard<std::mutex> lock(g_mu);
-        hl = g_scratch_dev[rt.dev.device()];
+    if (!ready) TSN_TRY(noalloc_init(d));
+    const hipStream_t st = rt.dev.stream();
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    TSN_HIP_CHECK(hipStreamIsCapturing(st, &cap));
+    const bool order = cap == hipStreamCaptureStatusNone;
+    // one caller at a time per device from here to the event record, so the wait/record pairs of
+    // two host threads cannot interleave
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (order && g_last_stream[d] && g_last_stream[d] != st) TSN_HIP_CHECK(hipStreamWaitEvent(st, g_done[d], 0));
+    TSN_TRY(gemm_hilo((const half_t *)W, ldw, (const float *)X, ldx, Y, ydt, ldy, bias, p.M, p.N, p.K,
+                      (half_t *)g_scratch_dev[d], st));
+    if (order) {
+        TSN_HIP_CHECK(hipEventRecord(g_done[d], st));
+        g_last_stream[d] = st;
     }
-    return gemm_hilo((const half_t *)W, ldw, (const float *)X, ldx, Y, ydt, ldy, bias, p.M, p.N, p.K, (half_t *)hl,
-                     rt.dev.stream());
+    return TSN_OK;
 }
 
 } // namespace tsn

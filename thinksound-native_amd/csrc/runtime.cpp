@@ -69,6 +69,7 @@ int Device::alloc(size_t bytes, void **p) {
         return TSN_ERR_HIP;
     }
     owned_.push_back(q);
+    owned_sz_.push_back(bytes);
     *p = q;
     return TSN_OK;
 }
@@ -80,6 +81,7 @@ int Device::free(void *p) {
     TSN_TRY(make_current());
     TSN_HIP_CHECK(hipStreamSynchronize(stream_));
     TSN_HIP_CHECK(hipFree(p));
+    owned_sz_.erase(owned_sz_.begin() + (it - owned_.begin()));
     owned_.erase(it);
     return TSN_OK;
 }

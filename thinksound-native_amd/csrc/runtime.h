@@ -60,6 +60,13 @@ public:
     hipStream_t stream() const { return stream_; }
     int device() const { return dev_; }
     int make_current() const;
+    // live allocations owned by this Device (count and bytes as requested)
+    size_t owned_count() const { return owned_.size(); }
+    size_t owned_bytes() const {
+        size_t b = 0;
+        for (size_t s : owned_sz_) b += s;
+        return b;
+    }
 
 private:
     int dev_ = -1;
@@ -68,6 +75,7 @@ private:
     bool begun_ = false;
     double last_ms_ = 0.0;
     std::vector<void *> owned_;
+    std::vector<size_t> owned_sz_;   // bytes of owned_[i]
 };
 
 class Runtime {

@@ -17,6 +17,7 @@ import importlib
 import json
 import os
 import statistics
+import subprocess
 import sys
 import time
 
@@ -295,6 +296,97 @@ def pmc_util_summary(sq_csv, dram_csv, title, cmd):
     return "\n".join(lines) + "\n"
 
 
+STALL_COUNTERS = ("SQ_WAVE_CYCLES SQ_WAIT_ANY SQ_WAIT_INST_ANY SQ_WAIT_INST_LDS SQ_ACTIVE_INST_VALU SQ_ACTIVE_INST_LDS "
+                  "SQ_ACTIVE_INST_ANY SQ_LDS_IDX_ACTIVE")
+
+
+def pmc_stall_summary(csv_path, title, cmd):
+    """Per-kernel shares of resident wave-cycles (SQ_WAVE_CYCLES) from one counter pass: waiting on
+    anything (SQ_WAIT_ANY: s_waitcnt on memory or LDS, barriers, dependencies), waiting for an
+    instruction to issue (SQ_WAIT_INST_ANY, of which LDS: SQ_WAIT_INST_LDS), and issuing VALU, LDS or
+    any instruction (SQ_ACTIVE_INST_*), per dispatch."""
+    d_all = read_counter_rows(csv_path)
+    mean = statistics.mean
+    cols = [("wait_any", "SQ_WAIT_ANY"), ("wait_inst", "SQ_WAIT_INST_ANY"), ("wait_lds", "SQ_WAIT_INST_LDS"),
+            ("act_valu", "SQ_ACTIVE_INST_VALU"), ("act_lds", "SQ_ACTIVE_INST_LDS"), ("act_any", "SQ_ACTIVE_INST_ANY")]
+    lines = ["# rocprofv3 wave-state counters per dispatch, " + title,
+             "# command: " + cmd.replace("{P}", STALL_COUNTERS),
+             "# each column = counter / SQ_WAVE_CYCLES (the waves' resident cycles, summed over waves):",
+             "#   " + ", ".join("%s = %s" % c for c in cols),
+             "%-28s %5s %8s " % ("kernel", "disp", "avg us") + " ".join("%9s" % c[0] for c in cols)]
+    rows = []
+    for k, d in d_all.items():
+        if "SQ_WAVE_CYCLES" not in d or mean(d["SQ_WAVE_CYCLES"]) <= 0:
+            continue
+        wc = mean(d["SQ_WAVE_CYCLES"])
+        rows.append((k, len(d["__dur_ns"]), mean(d["__dur_ns"]) / 1e3) +
+                    tuple(mean(d[c]) / wc if c in d else float("nan") for _, c in cols))
+    for r in sorted(rows, key=lambda r: -r[1] * r[2]):
+        lines.append("%-28s %5d %8.2f " % r[:3] + " ".join("%9.3f" % v for v in r[3:]))
+    return "\n".join(lines) + "\n"
+
+
+# GEMM shapes of the DiT workloads (name, M, N, K) for the vendor yardstick
+YARDSTICK_SHAPES = [("8 s fused FFN1", 794, 4096, 1024), ("8 s fused FFN2", 794, 1024, 4096),
+                    ("8 s fused QKV", 794, 3072, 1024), ("8 s fused out-projection", 794, 1024, 1024),
+                    ("8 s joint FFN1 audio (K = 3 x 1024)", 512, 4096, 3072),
+                    ("30 s fused FFN1", 2202, 4096, 1024), ("30 s fused QKV", 2202, 3072, 1024),
+                    ("batch-16 fused FFN1", 6352, 4096, 1024), ("batch-16 fused FFN2", 6352, 1024, 4096),
+                    ("batch-16 fused QKV", 6352, 3072, 1024), ("batch-16 joint FFN1 audio", 4096, 4096, 3072),
+                    ("square 4096", 4096, 4096, 4096), ("square 8192", 8192, 8192, 8192)]
+
+
+def vendor_yardstick():
+    """Measurement only, never a product path: the vendor f16 GEMM (torch.nn.functional.linear, which
+    runs hipBLASLt on this image) against this library's tsn_gemm on f16 X and f16 W with f16 Y, at
+    the DiT's GEMM shapes; HIP events around 50 calls after 5 warm-up calls, same process, same GPU."""
+    import torch
+    tsn = importlib.import_module("thinksound-native_amd")
+    assert torch.cuda.is_available()
+    dev = torch.device("cuda:0")
+    rt = tsn.Runtime(0)
+    rng = np.random.default_rng(5)
+    lines = ["# vendor yardstick: f16 GEMM Y[M,N] = X[M,K] W[N,K]^T, f16 operands and output, f32 accumulation",
+             "# vendor = torch %s torch.nn.functional.linear (hipBLASLt); tsn = tsn_gemm (xdtype f16, wdtype f16, "
+             "ydtype f16); mean of 50 calls, HIP events" % torch.__version__,
+             "# command: python3 bench.py --vendor-yardstick",
+             "%-36s %5s %5s %5s %10s %9s %10s %9s %8s" % ("shape", "M", "N", "K", "vendor us", "TFLOP/s",
+                                                           "tsn us", "TFLOP/s", "tsn/vnd")]
+    for name, M, N, K in YARDSTICK_SHAPES:
+        x = torch.randn(M, K, device=dev, dtype=torch.float16)
+        w = torch.randn(N, K, device=dev, dtype=torch.float16)
+        for _ in range(5):
+            y = torch.nn.functional.linear(x, w)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(50):
+            y = torch.nn.functional.linear(x, w)
+        e1.record()
+        torch.cuda.synchronize()
+        vus = e0.elapsed_time(e1) / 50 * 1e3
+        del x, w, y
+        X = rt.array(rng.standard_normal((M, K)).astype(np.float16))
+        W = rt.array((0.05 * rng.standard_normal((N, K))).astype(np.float16))
+        Y = rt.empty((M, N), np.float16)
+        for _ in range(5):
+            rt.gemm(1, W, X, 1, Y, 1, None, M, N, K)
+        rt.sync()
+        rt.begin()
+        for _ in range(50):
+            rt.gemm(1, W, X, 1, Y, 1, None, M, N, K)
+        tus = rt.commit() / 50 * 1e3
+        for a in (X, W, Y):
+            a.free()
+        fl = 2.0 * M * N * K
+        lines.append("%-36s %5d %5d %5d %10.2f %9.1f %10.2f %9.1f %8.2f" % (
+            name, M, N, K, vus, fl / vus / 1e6, tus, fl / tus / 1e6, tus / vus))
+        log(lines[-1])
+    rt.close()
+    print("\n".join(lines), flush=True)
+    return 0
+
+
 UTIL_FILE = os.path.join(ROOT, "profiles", "mfma_util_dit_eval_b2_la256.txt")
 
 
@@ -311,16 +403,84 @@ def read_util_row(kernel, path=UTIL_FILE):
     return None
 
 
+def write_ref_gguf(tsn, spec, w16, path):
+    """the reference-size checkpoint as a BF16 GGUF (tensor names, dims and dit.* metadata of the
+    reference's file) holding the bits of w16; returns the file size"""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    import gguf_writer as gw
+    sd = spec.as_dict()
+    meta = [("dit.hidden_dim", gw.KV_U32, spec.H), ("dit.num_heads", gw.KV_U32, spec.NH),
+            ("dit.depth", gw.KV_U32, spec.n_joint + spec.n_fused), ("dit.fused_depth", gw.KV_U32, spec.n_fused),
+            ("dit.latent_dim", gw.KV_U32, spec.latent)]
+    return gw.write_bf16(path, [(n, gw.ref_ne(n, k, sd), w16[o:o + k]) for n, k, o in tsn.ref_manifest(spec)], meta)
+
+
+def gguf_load_pass(path):
+    """child process: a fresh runtime loads the reference-size GGUF; prints the load time and the
+    process's peak resident host memory as one JSON line"""
+    def vm_kb(key):   # this process image's own figures (getrusage's maxrss carries the parent's over exec)
+        with open("/proc/self/status") as f:
+            for line in f:
+                if line.startswith(key + ":"):
+                    return float(line.split()[1])
+        return float("nan")
+    tsn = importlib.import_module("thinksound-native_amd")
+    rt = tsn.Runtime(0)
+    rss0 = vm_kb("VmRSS")
+    t0 = time.perf_counter()
+    spec = tsn.ref_spec_from_gguf(path, 2, 172, 64, 154)
+    m = tsn.RefDitModel(rt, spec)
+    m.load_gguf(path)
+    rt.sync()
+    dt = time.perf_counter() - t0
+    print(json.dumps({"load_s": dt, "rss_before_mb": rss0 / 1024.0, "rss_peak_mb": vm_kb("VmHWM") / 1024.0}),
+          flush=True)
+    m.close()
+    rt.close()
+    return 0
+
+
 def bench_ref(tsn, rt, args):
-    """The reference checkpoint's own three-stream graph at 8 s (B=2, T=172, C=64, TS=154): graph
-    replays of one evaluation, the 24-step sampler, and per-kernel statistics."""
+    """The reference checkpoint's own three-stream graph at 8 s (B=2, T=172, C=64, TS=154): the
+    checkpoint is written as a reference-size BF16 GGUF and loaded through tsn_refdit_load_gguf
+    (raw payloads to HBM, converted on the device; load time, rate and the loading process's peak
+    host memory measured, the latter in a child process), then graph replays of one evaluation,
+    the 24-step sampler, and per-kernel statistics."""
+    import tempfile
     spec = tsn.ref_spec_for_duration(8, 2)
     t0 = time.time()
     w16 = tsn.ref_synth_weights(spec, 4242, 0.0)
     log("bench ref: synthetic weights %.1f s (%d params)" % (time.time() - t0, w16.size))
-    m = tsn.RefDitModel(rt, spec)
-    m.upload_weights(w16)
-    del w16
+    fd, path = tempfile.mkstemp(suffix=".gguf")
+    os.close(fd)
+    load = None
+    try:
+        t0 = time.time()
+        size = write_ref_gguf(tsn, spec, w16, path)
+        nparams = int(w16.size)
+        del w16
+        log("bench ref: wrote %.2f GB GGUF in %.1f s" % (size / 1e9, time.time() - t0))
+        child = subprocess.run([sys.executable, os.path.abspath(__file__), "--gguf-load-pass", path],
+                               capture_output=True, text=True, timeout=300)
+        cj = json.loads(child.stdout.strip().splitlines()[-1]) if child.returncode == 0 else None
+        if cj is None:
+            log("bench ref: load child failed: %s" % child.stderr[-500:])
+        t0 = time.perf_counter()
+        m = tsn.RefDitModel(rt, tsn.ref_spec_from_gguf(path, spec.B, spec.T, spec.C, spec.TS))
+        m.load_gguf(path)
+        rt.sync()
+        load_s = time.perf_counter() - t0
+    finally:
+        os.remove(path)
+    load = {"file_bytes": size, "params": nparams, "tensor_type": "BF16", "load_s": round(load_s, 4),
+            "gb_per_s": round(size / load_s / 1e9, 2),
+            "fresh_process_load_s": round(cj["load_s"], 4) if cj else None,
+            "fresh_process_rss_peak_mb": round(cj["rss_peak_mb"], 1) if cj else None,
+            "fresh_process_rss_before_load_mb": round(cj["rss_before_mb"], 1) if cj else None,
+            "path": "tsn_refdit_load_gguf: tensor payloads read from the file into two pinned 32 MiB buffers in "
+                    "turn and copied to HBM as stored (BF16), then converted and laid out on the device; "
+                    "no host f32 copy"}
+    log("bench ref: GGUF load %.3f s (%.2f GB/s); fresh process %s" % (load_s, size / load_s / 1e9, cj))
     inp = tsn.ref_synth_inputs(spec, 4242, cfg_pairs=True)
     d = {k: rt.array(v) for k, v in inp.items()}
     args_in = (d["clip_pp"], d["text_pp"], d["gcmlp"], d["sync_gather"])
@@ -365,6 +525,7 @@ def bench_ref(tsn, rt, args):
             "mfma_frac_eval": round(flops / (ms * 1e-3) / 1e12 / PEAK_F16_TFLOPS, 4),
             "kernels": [{"name": k["name"], "launches": k["launches"], "ms": round(k["ms"], 4),
                          "share": round(k["ms"] / tot, 4)} for k in stats[:10]],
+            "gguf_load": load,
             "launch": "hipGraph replay"}
 
 
@@ -434,15 +595,18 @@ def bench_vae(tsn, rt, args):
 
 
 def bench_workloads(tsn, rt, args):
-    """The other configured workloads, reported beside the metric: the 30 s clip (La=960, S=1101) as
-    one evaluation and the 24-step sampler, and the 16-sample batch (8 prompts x CFG) as one
-    evaluation; graph replays, synthetic BF16 weights."""
+    """The other configured workloads, reported beside the metric: the 30 s clip (La=960, S=1101) and
+    the 16-sample batch (8 prompts x CFG, prompt p's latent and text features from seed p + 1), each
+    as one evaluation and the 24-step sampler; graph replays, synthetic BF16 weights."""
     out = {}
     for wl, name in ((3, "clip_30s"), (4, "batch16")):
         spec = tsn.default_spec(wl)
         m = tsn.DitModel(rt, spec)
         m.upload_weights(tsn.synth_weights(spec, 4242, 0.0))
-        inp = tsn.synth_inputs(spec, 4242, cfg_pairs=True)
+        if wl == 4:
+            inp = tsn.synth_prompt_inputs(spec, list(range(1, spec.B // 2 + 1)))
+        else:
+            inp = tsn.synth_inputs(spec, 4242, cfg_pairs=True)
         z, tt, text, pooled = (rt.array(inp[k]) for k in ("z", "t", "text", "pooled"))
         v = rt.empty((spec.B, spec.La, spec.latent))
         m.capture_forward(z, tt, text, pooled, v)
@@ -685,9 +849,18 @@ def main():
                     help="print the MFMA-utilisation and DRAM summary of two counter CSVs (no GPU use)")
     ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "CMD"),
                     help="print the traffic summary of two counter-collection CSVs (no GPU use)")
+    ap.add_argument("--pmc-stall-summary", nargs=3, metavar=("CSV", "TITLE", "CMD"),
+                    help="print the wait-counter summary (SQ_WAIT_ANY, SQ_WAIT_INST_ANY over SQ_WAVE_CYCLES) of a "
+                         "counter CSV (no GPU use)")
+    ap.add_argument("--vendor-yardstick", action="store_true",
+                    help="only time the vendor f16 GEMM (torch -> hipBLASLt) beside tsn_gemm at the DiT's GEMM shapes "
+                         "(measurement only)")
     ap.add_argument("--stats-summary", nargs=2, metavar=("STATS_CSV", "CMD"),
                     help="print the summary of a rocprofv3 kernel_stats.csv (no GPU use)")
     ap.add_argument("--stats-title", default=None, help="workload line of --stats-summary")
+    ap.add_argument("--gguf-load-pass", metavar="GGUF",
+                    help="only load a reference-graph GGUF checkpoint in a fresh runtime and print the load time "
+                         "and peak host memory (run by the benchmark as a child process)")
     ap.add_argument("--profile-pass", choices=["vae", "enc", "ref"],
                     help="only run eager VAE decodes, text-encoder passes or reference-graph evaluations "
                          "(workload for rocprofv3 --kernel-trace)")
@@ -697,6 +870,9 @@ def main():
         return 0
     if args.pmc_util_summary:
         sys.stdout.write(pmc_util_summary(*args.pmc_util_summary))
+        return 0
+    if args.pmc_stall_summary:
+        sys.stdout.write(pmc_stall_summary(*args.pmc_stall_summary))
         return 0
     if args.stats_summary:
         if args.stats_title:
@@ -709,6 +885,10 @@ def main():
               % args.gpus, file=sys.stderr)
         return 2
 
+    if args.vendor_yardstick:
+        return vendor_yardstick()
+    if args.gguf_load_pass:
+        return gguf_load_pass(args.gguf_load_pass)
     if args.pmc_pass:
         return pmc_pass(args.pmc_pass)
     if args.profile_pass:

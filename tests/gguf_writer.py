@@ -123,3 +123,32 @@ def ref_ne(name, numel, spec):
     if name.endswith("linear1.weight"):
         return (3, H, H) if numel == 3 * H * H else (H, H)
     return (H, numel // H)
+
+
+def write_bf16(path, tensors, metadata=(), alignment=32, version=3):
+    """BF16 tensors given as raw bf16 bits, streamed to the file one tensor at a time (for
+    checkpoints of reference size, without an f32 copy in memory). tensors: list of (name, ne tuple
+    (ne[0] fastest), uint16 array). Returns the file size in bytes."""
+    meta = list(metadata)
+    if alignment != 32:
+        meta.append(("general.alignment", KV_U32, alignment))
+    head = b"GGUF" + struct.pack("<IQQ", version, len(tensors), len(meta))
+    head += b"".join(_kv(k, kind, v) for k, kind, v in meta)
+    infos, off, offs = b"", 0, []
+    for name, ne, bits in tensors:
+        assert bits.dtype == np.uint16 and int(np.prod(ne)) == bits.size, name
+        off += (-off) % alignment
+        offs.append(off)
+        infos += _s(name) + struct.pack("<I", len(ne)) + b"".join(struct.pack("<Q", n) for n in ne)
+        infos += struct.pack("<IQ", BF16, off)
+        off += 2 * bits.size
+    hdr = head + infos
+    hdr += b"\0" * ((-len(hdr)) % alignment)
+    with open(path, "wb") as f:
+        f.write(hdr)
+        pos = 0
+        for (name, ne, bits), o in zip(tensors, offs):
+            f.write(b"\0" * (o - pos))
+            np.ascontiguousarray(bits).tofile(f)
+            pos = o + 2 * bits.size
+    return len(hdr) + pos

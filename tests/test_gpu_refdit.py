@@ -170,6 +170,36 @@ def test_ref_gguf_checkpoint(tsn, rt, orc, tmp_path):
         m.close()
 
 
+def test_ref_gguf_bf16_reference_size(tsn, rt, ref, tmp_path):
+    """The reference-size checkpoint (every tensor of the 8 s graph, 1.2 G BF16 parameters) written
+    as a BF16 GGUF from the same bits the module's model was uploaded from: tsn_refdit_load_gguf
+    moves the raw payloads to HBM and converts them there, and the evaluation is bit-identical to
+    the model uploaded from the flat BF16 buffer."""
+    import os
+    import gguf_writer as gw
+    spec, m, _ = ref
+    sd = spec.as_dict()
+    w16 = tsn.ref_synth_weights(spec, 4242, 1.0)
+    man = tsn.ref_manifest(spec)
+    path = str(tmp_path / "ref8s.gguf")
+    meta = [("dit.hidden_dim", gw.KV_U32, spec.H), ("dit.num_heads", gw.KV_U32, spec.NH),
+            ("dit.depth", gw.KV_U32, spec.n_joint + spec.n_fused), ("dit.fused_depth", gw.KV_U32, spec.n_fused),
+            ("dit.latent_dim", gw.KV_U32, spec.latent)]
+    size = gw.write_bf16(path, [(n, gw.ref_ne(n, k, sd), w16[o:o + k]) for n, k, o in man], meta)
+    assert size > 2 * int(w16.size)
+    del w16
+    m2 = tsn.RefDitModel(rt, tsn.ref_spec_from_gguf(path, spec.B, spec.T, spec.C, spec.TS))
+    try:
+        m2.load_gguf(path)
+        os.remove(path)
+        inp, dev = _io(tsn, rt, spec, seed=12)
+        a = _fwd(m, rt, spec, dev).numpy()
+        b = _fwd(m2, rt, spec, dev).numpy()
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    finally:
+        m2.close()
+
+
 def test_ref_replay_refused_after_sampler_reallocation(tsn, rt, ref):
     """as for the configured graph: a sampler run with another step count reallocates what the
     captured sampler addresses; the old graph refuses to replay, a new capture matches eager"""

@@ -5,8 +5,9 @@ weights and inputs:
   * batch 16: 8 prompts x CFG at 8 s (La=256, Lt=141) — large-M GEMMs, 16-row GEMVs.
 
 Bars as for the 8 s evaluation: velocity rel-L2 <= 1e-3, every block output <= 2e-3; the batch-16
-sampler step (8 cond/uncond pairs) and the whole 24-step 30 s sampler (against a committed oracle
-fixture) <= 2e-3 on the displacement.
+sampler step (8 cond/uncond pairs), and the whole 24-step samplers of the 30 s clip and of the
+batch-16 workload (eight prompts from seeds 1..8, against committed oracle fixtures) <= 2e-3 on the
+displacement, for every prompt.
 """
 import numpy as np
 import pytest
@@ -109,6 +110,46 @@ def test_sampler_30s_24_steps_against_fixture(tsn, rt):
         err = rel_l2(out - x0, g["x"] - x0)
         print("30 s 24-step sampler: displacement rel-L2 %.3g, final latent rel-L2 %.3g" % (err, rel_l2(out, g["x"])))
         assert err <= 2e-3
+        x2 = rt.array(x0)
+        m.capture_sample(x2, dev["text"], dev["pooled"], 24, float(g["cfg"]))
+        m.replay()
+        rt.sync()
+        assert np.array_equal(out.view(np.uint32), x2.numpy().view(np.uint32))
+    finally:
+        m.close()
+
+
+def test_sampler_batch16_24_steps_against_fixture(tsn, rt):
+    """The whole 24-step CFG sampler of the throughput batch: eight independent prompts as
+    cond/uncond pairs (batch 16, La = 256, Lt = 141), prompt p's z0, text and pooled features from
+    seed p + 1 (p = 0..7), on the benchmark's weights (every weight N(0, 0.02), seed 4242), against
+    the oracle's final latents (tests/golden/sampler_b16_24steps.npz, written by
+    make_sampler_golden.py b16; about 30 minutes of oracle time): the displacement x - z0 of every
+    prompt within rel-L2 2e-3, eager and graph-captured runs bit-identical."""
+    import os
+    spec = tsn.default_spec(4)
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "sampler_b16_24steps.npz"))
+    seeds = [int(x) for x in g["prompt_seeds"]]
+    assert seeds == list(range(1, 9)) and spec.B == 2 * len(seeds)
+    assert int(g["seeds"][0]) == 4242 and int(g["seeds"][1]) == 24 and float(g["norm_mean"]) == 0.0
+    w16 = tsn.synth_weights(spec, 4242, 0.0)
+    assert np.isclose(tsn.bf16_to_f32(w16).astype(np.float64).sum(), float(g["w_checksum"]), rtol=0, atol=1e-6)
+    inp = tsn.synth_prompt_inputs(spec, seeds)
+    x0 = inp["z"][0::2].copy()
+    assert np.allclose(x0.astype(np.float64).reshape(len(seeds), -1).sum(axis=1), g["x0_checksums"], rtol=0, atol=1e-9)
+    assert np.isclose(inp["text"].astype(np.float64).sum(), float(g["text_checksum"]), rtol=0, atol=1e-6)
+    m = tsn.DitModel(rt, spec)
+    try:
+        m.upload_weights(w16)
+        dev = {k: rt.array(v) for k, v in inp.items()}
+        x = rt.array(x0)
+        m.sample(x, dev["text"], dev["pooled"], 24, float(g["cfg"]))
+        rt.sync()
+        out = x.numpy()
+        ref = g["x"]
+        errs = [rel_l2(out[p] - x0[p], ref[p] - x0[p]) for p in range(len(seeds))]
+        print("batch-16 24-step sampler: displacement rel-L2 per prompt " + " ".join("%.3g" % e for e in errs))
+        assert max(errs) <= 2e-3
         x2 = rt.array(x0)
         m.capture_sample(x2, dev["text"], dev["pooled"], 24, float(g["cfg"]))
         m.replay()

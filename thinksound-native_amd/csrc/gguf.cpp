@@ -7,7 +7,10 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <algorithm>
+
 #include "graph.h"
+#include "runtime.h"
 #include "tsn_common.h"
 
 namespace tsn {
@@ -86,6 +89,19 @@ int GgufReader::open(const char *path) {
     TSN_REQUIRE(m != MAP_FAILED, std::string("gguf: mmap failed: ") + path);
     map_ = m;
     return parse();
+}
+
+int GgufReader::read_at(const uint8_t *p, void *dst, size_t n) const {
+    const uint8_t *base = (const uint8_t *)map_;
+    TSN_REQUIRE(map_ && fd_ >= 0 && p >= base && (size_t)(p - base) <= len_ && n <= len_ - (size_t)(p - base),
+                "gguf: read outside the file");
+    size_t done = 0;
+    while (done < n) {
+        const ssize_t r = pread(fd_, (char *)dst + done, n - done, (off_t)(p - base) + (off_t)done);
+        TSN_REQUIRE(r > 0, "gguf: read failed");
+        done += (size_t)r;
+    }
+    return TSN_OK;
 }
 
 int GgufReader::parse() {
@@ -258,6 +274,105 @@ int gguf_read_manifest(const GgufReader &g, const std::vector<ManifestEntry> &ma
                                                         " elements, the graph needs " + std::to_string(e.numel));
         TSN_TRY(g.to_f32(*t, out.data() + e.offset));
     }
+    return TSN_OK;
+}
+
+namespace {
+int wp_type_of(uint32_t t) {
+    switch (t) {
+    case GGUF_T_BF16: return WP_SRC_BF16;
+    case GGUF_T_F32: return WP_SRC_F32;
+    case GGUF_T_F16: return WP_SRC_F16;
+    case GGUF_T_Q8_0: return WP_SRC_Q8_0;
+    default: return -1;
+    }
+}
+
+// pinned double buffer for host -> device transfers of file bytes
+struct PinnedPair {
+    void *buf[2] = {nullptr, nullptr};
+    hipEvent_t ev[2] = {nullptr, nullptr};
+    bool used[2] = {false, false};
+    ~PinnedPair() {
+        for (int i = 0; i < 2; ++i) {
+            if (ev[i]) { hipEventSynchronize(ev[i]); hipEventDestroy(ev[i]); }
+            if (buf[i]) hipHostFree(buf[i]);
+        }
+    }
+};
+constexpr size_t PIN_CHUNK = (size_t)32 << 20;
+} // namespace
+
+int gguf_stage_manifest(const GgufReader &g, const std::vector<ManifestEntry> &man, Device &dev,
+                        const std::function<int(size_t, void **)> &alloc, std::map<std::string, GgufDeviceTensor> &out,
+                        size_t *bytes_moved) {
+    TSN_REQUIRE(!man.empty(), "gguf: empty manifest");
+    struct Need {
+        const GgufTensorInfo *t;
+        const std::string *name;
+    };
+    std::vector<Need> need;
+    need.reserve(man.size());
+    for (const auto &e : man) {
+        const GgufTensorInfo *t = g.find(e.name);
+        TSN_REQUIRE(t, "gguf: missing tensor " + e.name);
+        TSN_REQUIRE((int64_t)t->numel() == e.numel, "gguf: " + e.name + " has " + std::to_string(t->numel()) +
+                                                        " elements, the graph needs " + std::to_string(e.numel));
+        TSN_REQUIRE(wp_type_of(t->type) >= 0, "gguf: unsupported tensor type " + std::to_string(t->type) + " for " + e.name);
+        TSN_REQUIRE(t->type != GGUF_T_Q8_0 || t->numel() % 32 == 0, "gguf: Q8_0 tensor " + e.name + " is not whole blocks");
+        need.push_back(Need{t, &e.name});
+    }
+    // runs of tensors adjacent in the file (gaps of at most 4 KiB, the alignment padding, travel along)
+    std::sort(need.begin(), need.end(), [](const Need &a, const Need &b) { return a.t->data < b.t->data; });
+    struct Run {
+        const uint8_t *src;
+        size_t bytes, dst;
+    };
+    std::vector<Run> runs;
+    std::vector<size_t> run_of(need.size());
+    size_t total = 0;
+    for (size_t i = 0; i < need.size(); ++i) {
+        const uint8_t *a = need[i].t->data, *b = a + need[i].t->nbytes;
+        if (!runs.empty() && a >= runs.back().src && a <= runs.back().src + runs.back().bytes + 4096) {
+            Run &r = runs.back();
+            const size_t end = std::max(r.bytes, (size_t)(b - r.src));
+            total += end - r.bytes;
+            r.bytes = end;
+        } else {
+            total = (total + 255) & ~(size_t)255;   // each run starts 256-byte aligned on the device
+            runs.push_back(Run{a, (size_t)(b - a), total});
+            total += runs.back().bytes;
+        }
+        run_of[i] = runs.size() - 1;
+    }
+    void *stage = nullptr;
+    TSN_TRY(alloc(total, &stage));
+    TSN_TRY(dev.make_current());
+    const hipStream_t st = dev.stream();
+    PinnedPair pin;
+    for (int i = 0; i < 2; ++i) {
+        TSN_HIP_CHECK(hipHostMalloc(&pin.buf[i], PIN_CHUNK, hipHostMallocDefault));
+        TSN_HIP_CHECK(hipEventCreateWithFlags(&pin.ev[i], hipEventDisableTiming));
+    }
+    int slot = 0;
+    for (const Run &r : runs)
+        for (size_t off = 0; off < r.bytes; off += PIN_CHUNK) {
+            const size_t n = std::min(PIN_CHUNK, r.bytes - off);
+            if (pin.used[slot]) TSN_HIP_CHECK(hipEventSynchronize(pin.ev[slot]));   // its previous DMA is done
+            TSN_TRY(g.read_at(r.src + off, pin.buf[slot], n));
+            TSN_HIP_CHECK(hipMemcpyAsync((char *)stage + r.dst + off, pin.buf[slot], n, hipMemcpyHostToDevice, st));
+            TSN_HIP_CHECK(hipEventRecord(pin.ev[slot], st));
+            pin.used[slot] = true;
+            slot ^= 1;
+        }
+    TSN_HIP_CHECK(hipStreamSynchronize(st));
+    out.clear();
+    for (size_t i = 0; i < need.size(); ++i) {
+        const Run &r = runs[run_of[i]];
+        const char *p = (const char *)stage + r.dst + (need[i].t->data - r.src);
+        out[*need[i].name] = GgufDeviceTensor{p, wp_type_of(need[i].t->type)};
+    }
+    if (bytes_moved) *bytes_moved = total;
     return TSN_OK;
 }
 

@@ -2,13 +2,15 @@
 //
 // Replaces tn::GgufFile / tn::to_f32 (src/gguf.h:42-86, src/gguf.cpp): GGUF v2/v3 header, typed
 // key-value metadata, tensor infos (ne[0] fastest), data section at the file's alignment
-// (general.alignment, default 32). Tensor payloads are read in place from the mapping and
-// dequantized on the host to f32 with the reference's semantics: F32 as is, BF16 exact, F16 and
-// the Q8_0 block scale with subnormals flushed to zero, Q8_0 = scale * int8.
+// (general.alignment, default 32). Tensor payloads are read in place from the mapping, either
+// copied raw to device memory (gguf_stage_manifest; the device converts them) or dequantized on the
+// host to f32 with the reference's semantics: F32 as is, BF16 exact, F16 and the Q8_0 block scale
+// with subnormals flushed to zero, Q8_0 = scale * int8.
 #pragma once
 #include <stddef.h>
 #include <stdint.h>
 
+#include <functional>
 #include <map>
 #include <string>
 #include <vector>
@@ -46,6 +48,9 @@ public:
     uint32_t version() const { return version_; }
     // dequantize to f32 (out holds numel floats)
     int to_f32(const GgufTensorInfo &t, float *out) const;
+    // n bytes of the file starting at p (an address inside the mapping), read with pread into dst:
+    // the bytes go from the page cache straight to dst, without faulting the mapping in
+    int read_at(const uint8_t *p, void *dst, size_t n) const;
 
 private:
     struct Kv {
@@ -74,5 +79,22 @@ struct ManifestEntry;
 // every tensor of a manifest looked up by name in the file, its element count checked, dequantized
 // to f32 into out at the manifest offsets (WeightSet::load's name map, src/net.mm:126-140)
 int gguf_read_manifest(const GgufReader &g, const std::vector<ManifestEntry> &man, std::vector<float> &out);
+
+// One manifest tensor's raw GGUF payload in device memory: its address and its encoding as a
+// weight_prep source type (WP_SRC_BF16 / F32 / F16 / Q8_0).
+struct GgufDeviceTensor {
+    const void *p;
+    int type;
+};
+class Device;
+// The raw payloads of every tensor of a manifest, copied as stored in the file (no host
+// conversion) from the mapping to one device buffer that `alloc` provides: tensors are looked up
+// by name, their element counts and types checked, and each run of tensors that lie next to each
+// other in the file goes over as one transfer, read from the file into two pinned host buffers in
+// turn, so the read of one chunk overlaps the previous chunk's DMA. The device buffer holds only the needed runs;
+// out maps each name to its bytes there. Bytes moved over PCIe are returned in *bytes_moved.
+int gguf_stage_manifest(const GgufReader &g, const std::vector<ManifestEntry> &man, Device &dev,
+                        const std::function<int(size_t, void **)> &alloc, std::map<std::string, GgufDeviceTensor> &out,
+                        size_t *bytes_moved);
 
 } // namespace tsn

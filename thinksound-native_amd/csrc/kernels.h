@@ -259,12 +259,16 @@ int launch_f16_to_f32(const half_t *src, float *dst, size_t n, hipStream_t st);
 // conv weight [OC][IC][K] (bf16 or f16, src_bf16 selects) -> [OC][K][IC] f16
 int launch_conv_weight_reorder(const void *src, int src_bf16, half_t *dst, int OC, int IC, int K, hipStream_t st);
 
-// Upload-time weight layout (source [OC][IC][KT], bf16 or f32 when src_f32; KT = 1 for a linear
-// weight or a vector): destination row r(oc) = (oc % ra)*rb + (oc / ra)*rc + rd (ra = 1, rb = 0,
-// rc = 1, rd = 0 keeps the order), tap-major [KT][IC] within the row, channels written twice
-// ([w | w]) when dup; f16 with the reference upload's f32 -> f16 rounding, or f32 when out_f32.
-// Every r(oc) must lie in [0, dst_rows).
-int launch_weight_prep(const void *src, int src_f32, void *dst, int out_f32, int OC, int IC, int KT, int dup, int ra,
+// Upload-time weight layout (source [OC][IC][KT] stored as src_type, KT = 1 for a linear weight or a
+// vector): destination row r(oc) = (oc % ra)*rb + (oc / ra)*rc + rd (ra = 1, rb = 0, rc = 1, rd = 0
+// keeps the order), tap-major [KT][IC] within the row, channels written twice ([w | w]) when dup;
+// f16 with the reference upload's f32 -> f16 rounding, or f32 when out_f32. Every r(oc) must lie in
+// [0, dst_rows). Source types are the GGUF encodings the reference's loader takes
+// (src/gguf.cpp to_f32): BF16 exact, F32, F16 with subnormals flushed to zero, and Q8_0 (blocks of
+// 32 elements: f16 scale, 32 int8; value = scale * q), so a checkpoint's raw tensor bytes can be
+// converted on the device.
+enum { WP_SRC_BF16 = 0, WP_SRC_F32 = 1, WP_SRC_F16 = 2, WP_SRC_Q8_0 = 3 };
+int launch_weight_prep(const void *src, int src_type, void *dst, int out_f32, int OC, int IC, int KT, int dup, int ra,
                        int rb, int rc, int rd, long long dst_rows, hipStream_t st);
 // y = silu(x[m] + v[m / L]) (x [M][H], v [M/L][H] f32) as f16 hi|lo rows [M][2H] (LN_F16_HILO layout)
 int launch_bcast_add_silu_f16(const float *x, const float *v, half_t *y, int L, int M, int H, hipStream_t st);

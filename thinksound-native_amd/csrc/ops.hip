@@ -314,7 +314,30 @@ __global__ void conv_reorder_kernel(const void *src, int src_bf16, half_t *dst, 
 // Upload-time weight layout: src [OC][IC][KT] (bf16, or f32 when src_f32) -> dst row
 // r(oc) = (oc % ra)*rb + (oc / ra)*rc + rd, tap-major [KT][IC] within the row, each tap's IC channels
 // written twice ([w | w]) when dup; f16 (reference upload rounding) or f32 when out_f32.
-__global__ void weight_prep_kernel(const void *src, int src_f32, void *dst, int out_f32, int OC, int IC, int KT,
+// f16 bits -> f32 with subnormals flushed to signed zero (the reference's host conversion of F16
+// tensors and Q8_0 block scales, src/gguf.cpp)
+__device__ inline float f16_bits_ftz(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31, e = (h >> 10) & 0x1F, m = h & 0x3FF;
+    const uint32_t f = e == 0 ? sign : e == 31 ? (sign | 0x7F800000u | (m << 13)) : (sign | ((e + 112) << 23) | (m << 13));
+    return __uint_as_float(f);
+}
+
+// element si of a source tensor stored as src_type (WP_SRC_*): BF16 exact, f32, F16 with
+// subnormals flushed, Q8_0 (blocks of 32: f16 scale, then 32 int8) as scale * q
+__device__ inline float wp_load(const void *src, int src_type, long long si) {
+    switch (src_type) {
+    case WP_SRC_F32: return ((const float *)src)[si];
+    case WP_SRC_F16: return f16_bits_ftz(((const uint16_t *)src)[si]);
+    case WP_SRC_Q8_0: {
+        const unsigned char *blk = (const unsigned char *)src + (si >> 5) * 34;
+        const float scale = f16_bits_ftz((uint16_t)(blk[0] | (blk[1] << 8)));
+        return scale * (float)(signed char)blk[2 + (si & 31)];
+    }
+    default: return bf16_to_f32(((const uint16_t *)src)[si]);
+    }
+}
+
+__global__ void weight_prep_kernel(const void *src, int src_type, void *dst, int out_f32, int OC, int IC, int KT,
                                    int dup, int ra, int rb, int rc, int rd) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long long)OC * IC * KT) return;
@@ -323,7 +346,7 @@ __global__ void weight_prep_kernel(const void *src, int src_f32, void *dst, int 
     const int k = (int)(q % KT);
     const int oc = (int)(q / KT);
     const long long si = ((long long)oc * IC + ic) * KT + k;
-    const float w = src_f32 ? ((const float *)src)[si] : bf16_to_f32(((const uint16_t *)src)[si]);
+    const float w = wp_load(src, src_type, si);
     const long long row = (long long)(oc % ra) * rb + (long long)(oc / ra) * rc + rd;
     const int w_ic = IC * (dup ? 2 : 1);
     const long long d = row * KT * w_ic + (long long)k * w_ic + ic;
@@ -642,15 +665,19 @@ int launch_conv_weight_reorder(const void *src, int src_bf16, half_t *dst, int O
     return TSN_OK;
 }
 
-int launch_weight_prep(const void *src, int src_f32, void *dst, int out_f32, int OC, int IC, int KT, int dup, int ra,
+int launch_weight_prep(const void *src, int src_type, void *dst, int out_f32, int OC, int IC, int KT, int dup, int ra,
                        int rb, int rc, int rd, long long dst_rows, hipStream_t st) {
     TSN_REQUIRE(src && dst && OC > 0 && IC > 0 && KT > 0 && ra > 0 && dst_rows > 0, "weight_prep: arguments");
+    TSN_REQUIRE(src_type >= WP_SRC_BF16 && src_type <= WP_SRC_Q8_0, "weight_prep: source type");
+    TSN_REQUIRE(src_type != WP_SRC_Q8_0 || ((long long)OC * IC * KT) % 32 == 0, "weight_prep: Q8_0 needs whole blocks of 32");
+    TSN_REQUIRE(((uintptr_t)src) % (src_type == WP_SRC_F32 ? 4 : src_type == WP_SRC_Q8_0 ? 1 : 2) == 0,
+                "weight_prep: misaligned source");
     for (int oc = 0; oc < OC; ++oc) {   // every destination row inside the destination
         const long long row = (long long)(oc % ra) * rb + (long long)(oc / ra) * rc + rd;
         TSN_REQUIRE(row >= 0 && row < dst_rows, "weight_prep: row map leaves the destination");
     }
     const size_t n = (size_t)OC * IC * KT;
-    TSN_LAUNCH(weight_prep_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, src_f32, dst, out_f32, OC, IC, KT, dup,
+    TSN_LAUNCH(weight_prep_kernel, dim3(blocks_for(n)), dim3(256), 0, st, src, src_type, dst, out_f32, OC, IC, KT, dup,
                ra, rb, rc, rd);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;

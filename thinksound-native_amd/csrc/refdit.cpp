@@ -181,16 +181,26 @@ int RefDitModel::upload(const void *host, bool src_f32, size_t numel) {
     const size_t esz = src_f32 ? 4 : 2;
     TSN_TRY(alloc(total * esz, &wraw_));
     TSN_TRY(rt->dev.upload(wraw_, host, total * esz));
+    std::map<std::string, GgufDeviceTensor> raw;
+    for (const auto &e : man)
+        raw[e.name] = GgufDeviceTensor{(const char *)wraw_ + e.offset * esz, src_f32 ? WP_SRC_F32 : WP_SRC_BF16};
+    return prepare(raw);
+}
+
+// Every tensor laid out and converted on the device from its raw source (address and encoding per
+// name), then the source buffer (wraw_) is freed.
+int RefDitModel::prepare(const std::map<std::string, GgufDeviceTensor> &raw) {
+    const auto man = refdit_manifest(s);
     std::map<std::string, const ManifestEntry *> idx;
     for (const auto &e : man) idx[e.name] = &e;
     const hipStream_t st = rt->dev.stream();
     const int H = s.H, F = s.F, L = s.latent;
-    auto raw = [&](const std::string &n) -> const void * { return (const char *)wraw_ + idx.at(n)->offset * esz; };
     // prep(name, OC, IC, KT, dup, row map ra/rb/rc/rd, dst, dst_rows, f32 out)
     auto prep = [&](const std::string &n, int OC, int IC, int KT, int dup, int ra, int rb, int rc, int rd, void *dst,
                     long long dst_rows, int out_f32) -> int {
         TSN_REQUIRE(idx.at(n)->numel == (int64_t)OC * IC * KT, "refdit: tensor size mismatch: " + n);
-        return launch_weight_prep(raw(n), src_f32 ? 1 : 0, dst, out_f32, OC, IC, KT, dup, ra, rb, rc, rd, dst_rows, st);
+        const GgufDeviceTensor &r = raw.at(n);
+        return launch_weight_prep(r.p, r.type, dst, out_f32, OC, IC, KT, dup, ra, rb, rc, rd, dst_rows, st);
     };
     auto new_f16 = [&](size_t n, half_t **p) { return alloc(n * 2, (void **)p); };
     auto new_f32 = [&](size_t n, float **p) { return alloc(n * 4, (void **)p); };
@@ -302,14 +312,26 @@ int RefDitModel::upload(const void *host, bool src_f32, size_t numel) {
 }
 
 // WeightSet::load + DitModel::load (src/net.mm:126-173, src/dit.cpp:29-47): every tensor the graph
-// needs is looked up by name, dequantized to f32 on the host (F32, F16, BF16, Q8_0) and uploaded;
-// GEMM and GEMV weights become f16 with the reference's rounding, vectors stay f32.
+// needs is looked up by name and its payload goes to HBM as stored in the file (BF16, F16, F32 or
+// Q8_0 bytes, no host conversion and no host copy beyond the mapping and two pinned transfer
+// buffers); the device then converts and lays out each tensor: GEMM and GEMV weights f16 with the
+// reference's rounding, vectors f32.
 int RefDitModel::load_gguf(const char *path) {
+    TSN_REQUIRE(rt, "refdit: not created");
+    TSN_REQUIRE(!ready_, "refdit: weights already uploaded");
     GgufReader g;
     TSN_TRY(g.open(path));
-    std::vector<float> host;
-    TSN_TRY(gguf_read_manifest(g, refdit_manifest(s), host));
-    return upload(host.data(), true, host.size());
+    std::map<std::string, GgufDeviceTensor> raw;
+    size_t moved = 0;
+    TSN_TRY(gguf_stage_manifest(g, refdit_manifest(s), rt->dev,
+                                [&](size_t n, void **p) {
+                                    TSN_TRY(alloc(n, p));
+                                    wraw_ = *p;
+                                    return (int)TSN_OK;
+                                },
+                                raw, &moved));
+    load_bytes_ = moved;
+    return prepare(raw);
 }
 
 int refdit_spec_from_gguf(const char *path, int B, int T, int C, int TS, RefDitSpec *out) {

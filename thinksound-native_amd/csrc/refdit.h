@@ -24,8 +24,11 @@
 // against the same weight columns (f32-accurate operands); the clip and text out-proj and FFN read
 // the hi halves only.
 #pragma once
+#include <map>
+#include <string>
 #include <vector>
 
+#include "gguf.h"
 #include "graph.h"
 
 namespace tsn {
@@ -56,8 +59,11 @@ public:
     int upload_weights(const uint16_t *host_bf16, size_t numel);
     // the same from an f32 buffer (dequantized checkpoint tensors)
     int upload_weights_f32(const float *host_f32, size_t numel);
-    // every tensor of the manifest from a GGUF checkpoint (any of F32, F16, BF16, Q8_0)
+    // every tensor of the manifest from a GGUF checkpoint (any of F32, F16, BF16, Q8_0): raw
+    // payloads to HBM, converted there
     int load_gguf(const char *path);
+    // bytes the last load_gguf moved to the device (the needed tensors' payloads)
+    size_t load_bytes() const { return load_bytes_; }
 
     // one velocity evaluation, device pointers: x [B][T][latent], t [B], clip_pp [B][C][H],
     // text_pp [B][TS][H], gcmlp [B][H], sync_gather [B][T][H] -> v [B][T][latent].
@@ -122,6 +128,8 @@ private:
     float *ws_ = nullptr;
     size_t ws_bytes_ = 0;
     void *wraw_ = nullptr;
+    size_t load_bytes_ = 0;
+    int prepare(const std::map<std::string, GgufDeviceTensor> &raw);
     // sampler state
     float *Vv_ = nullptr, *x2_ = nullptr, *tsched_ = nullptr;
     int tsched_steps_ = 0;

@@ -76,12 +76,17 @@ def test_gemm_f16_io_strided(tsn, rt, orc):
     assert rel_l2(Y, ref_orc) < 2e-3
 
 
-@pytest.mark.parametrize("M,N,K,ydt", [(4133, 4096, 1024, F16), (4096, 3200, 192, F32), (3900, 4160, 64, F32)])
+@pytest.mark.parametrize("M,N,K,ydt", [(4133, 4096, 1024, F16), (4096, 3200, 192, F32), (3900, 4160, 64, F32),
+                                        (6352, 4096, 1024, F16), (2048, 8192, 2048, F32), (4133, 4096, 2048, F16),
+                                        (4100, 4160, 2112, F32)])
 def test_gemm_f16_large_grids(tsn, rt, orc, M, N, K, ydt):
-    """f16 X at batch-16-sized shapes (grids of 800 to 1056 128x128 tiles: the two-stage kernel, two
-    workgroups per CU): a ragged M tail (4133 = 32*128 + 37), N not a multiple of 256 (3200, 4160),
-    K of 3 and 1 K tiles. Held against the float64 product of the same f16 operands (the oracle's
-    GEMM is the same product and would take tens of seconds at this size)"""
+    """f16 X at batch-16-sized shapes, grids of several rounds. K >= 2048 with a round of 256x256
+    tiles takes the wide kernel: 2048 x 8192 x 2048 (256 tiles), 4133 x 4096 x 2048 (272 tiles, a
+    37-row M tail), 4100 x 4160 x 2112 (289 tiles, tails in M and N, 66 K tiles); the rest the
+    two-stage 128x128 kernel with two workgroups per CU: a ragged M tail (4133 = 32*128 + 37), N
+    not a multiple of 256 (3200, 4160), K of 3 and 1 K tiles, the batch-16 FFN1 (6352 x 4096 x
+    1024). Held against the float64 product of the same f16 operands (the oracle's GEMM is the same
+    product and would take tens of seconds at this size)"""
     Y, ref64, _ = _gemm_case(tsn, rt, orc, M, N, K, F16, ydt, seed=11, oracle=False)
     assert not np.isnan(Y).any()
     assert rel_l2(Y, ref64) < (1e-3 if ydt == F16 else 1e-5)

@@ -52,6 +52,9 @@ constexpr int NCU = 256, SK_MIN_UNITS = 8, SK_OVERHEAD = 20;
 // it replaces (3.345 -> 3.324 ms per reference-graph evaluation with the same plans; a charge of 8
 // K tiles picked stream-K for more GEMMs and measured 3.369 -> 3.411 ms)
 constexpr int SK_OVERHEAD_IN = 20;
+// the wide kernel (gemm_wide_kernel) is taken for grids of at least a round of 256x256 tiles whose
+// every problem has K >= WIDE_MIN_K (measured faster there, slower at K = 1024)
+constexpr int WIDE_MIN_TILES = 256, WIDE_MIN_K = 2048;
 
 __device__ inline int xcd_remap(int bid, int nwg) {
     const int xcd = bid & 7, idx = bid >> 3;
@@ -378,7 +381,7 @@ constexpr int TP = 132;          // pitch (floats) of the f32 C tile staged in L
                                  // 4 rows apart = 528 floats = 16 banks apart, so MFMA-layout writes
                                  // from the 4 lane groups of a wave never collide
 
-// Epilogue on the LDS-staged C tile (row-major f32, pitch TP). Thread tid handles 8-column chunks
+// Epilogue on the LDS-staged C tile (128 x 128, row-major f32, pitch PITCH). Thread tid handles 8-column chunks
 // c = tid + 512*p (row c >> 4, columns (c & 15)*8 .. +7) — 16-byte reads from LDS and 16-byte
 // global stores. Requires N % 8 == 0 and 16-byte aligned output rows (checked by the launcher).
 __device__ __forceinline__ void load8(const float *t, float (&v)[8]) {
@@ -400,7 +403,7 @@ __device__ __forceinline__ void snake8(float (&v)[8], const float (&a)[8], const
     }
 }
 
-template <int EPI>
+template <int EPI, int PITCH = TP>
 __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float *tile, int m0, int n0, int ks, int tid) {
     const int M = P.M, N = P.N;
     if (P.splits > 1) {
@@ -413,7 +416,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             if (m < M && n < N) {
                 float *o = w + (long long)m * N + n;
                 float v[8];
-                ldsum8(tile, row * TP + col, v);
+                ldsum8(tile, row * PITCH + col, v);
                 *(float4 *)o = make_float4(v[0], v[1], v[2], v[3]);
                 *(float4 *)(o + 4) = make_float4(v[4], v[5], v[6], v[7]);
             }
@@ -427,7 +430,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             const int m = m0 + row, n = n0 + col;
             if (m >= M || n >= N) continue;
             float v[8];
-            ldsum8(tile, row * TP + col, v);
+            ldsum8(tile, row * PITCH + col, v);
             if (P.bias) add8(v, P.bias + n);
             if (P.silu)
 #pragma unroll
@@ -458,8 +461,8 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             const int m = m0 + row;
             if (m >= M) continue;
             float a[8], b[8];
-            ldsum8(tile, row * TP + col, a);
-            ldsum8(tile, row * TP + 64 + col, b);
+            ldsum8(tile, row * PITCH + col, a);
+            ldsum8(tile, row * PITCH + 64 + col, b);
             float y[8];
             half8 o;
 #pragma unroll
@@ -493,7 +496,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             const int m = m0 + row;
             if (m >= M || n >= N) continue;
             float v[8];
-            ldsum8(tile, row * TP + col, v);
+            ldsum8(tile, row * PITCH + col, v);
             if (P.bias)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] += bv[e];
@@ -530,7 +533,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             const int m = m0 + row;
             if (m >= M || n >= N) continue;
             float v[8];
-            ldsum8(tile, row * TP + col, v);
+            ldsum8(tile, row * PITCH + col, v);
             if (P.bias)
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] += bv[e];
@@ -560,7 +563,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             const int m = m0 + row, n = n0 + col;
             if (m >= M || n >= N) continue;
             float v[8];
-            ldsum8(tile, row * TP + col, v);
+            ldsum8(tile, row * PITCH + col, v);
             if (P.bias) add8(v, P.bias + n);
             const float *g = P.gate + (long long)(m / P.gate_L) * P.gate_ld + n;
             float *x = P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n;
@@ -599,7 +602,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
             for (int p = 0; p < 4; ++p) {
                 const int row = (tid >> 4) + 32 * p, m = m0 + row;
                 float v[8];
-                ldsum8(tile, row * TP + col, v);
+                ldsum8(tile, row * PITCH + col, v);
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] += bw[e];
                 // per-head RMS over the 64 columns held by 8 neighbouring lanes (same row, same head)
@@ -658,13 +661,13 @@ __device__ __forceinline__ void tile_epilogue(const GemmProblem &P, const float 
                 if (s8 >= P.q_soff + ta && s8 + 8 <= P.q_soff + tb) {
                     half8 hv;
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) hv[e] = (half_t)(ldsum1(tile, (r8 + e) * TP + col) + bn);
+                    for (int e = 0; e < 8; ++e) hv[e] = (half_t)(ldsum1(tile, (r8 + e) * PITCH + col) + bn);
                     *(half8 *)o = hv;
                 } else {
 #pragma unroll
                     for (int e = 0; e < 8; ++e) {
                         const int ss = s8 + e;
-                        if (ss >= P.q_soff + ta && ss < P.q_soff + tb) o[e] = (half_t)(ldsum1(tile, (r8 + e) * TP + col) + bn);
+                        if (ss >= P.q_soff + ta && ss < P.q_soff + tb) o[e] = (half_t)(ldsum1(tile, (r8 + e) * PITCH + col) + bn);
                     }
                 }
             }
@@ -1013,6 +1016,189 @@ __global__ __launch_bounds__(512, 2) void gemm_pipe2_kernel(const GemmBatch bt) 
 template <int EPI>
 __global__ __launch_bounds__(512, 2) void gemm_pipe2_hl_kernel(const GemmBatch bt) {
     pipe_dp<EPI, true, 2>(bt);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Wide kernel for data-parallel grids of several rounds: 256x256 C tiles, 512 threads = 8 waves
+// (two per SIMD); wave w owns the 128x64 block (rows 128*(w>>2), columns 64*(w&3)) over the full
+// K: 8 x 4 MFMA blocks of 16x16, 128 f32 accumulators per lane.
+//
+// Why this shape: every K tile's lines come from the MALL or HBM (about 1.5 us away under load),
+// so a CU must keep (operand bytes per flop) x (its MFMA rate) x (latency) in flight to stay busy.
+// A 128x128 tile reads 64 B of operands per 4096 flops (one CU clock of MFMA work) and would need
+// about 230 KB in flight, more than the 160 KB of LDS; a 256x256 tile reads 32 B and needs about
+// 115 KB. K tiles are 32 wide (64-byte LDS rows) in a ring of WNS = 5 stages of 256 A rows and 256
+// W rows (32 KB per stage, the whole LDS): four K tiles (128 KB) are in flight while the fifth is
+// multiplied, with one barrier per K tile. LDS operand reads per K tile: 8 waves x 12 KB against
+// 8 x 32 MFMAs.
+//
+// Stage layout: row r (64 B = 4 chunks of 8 halves) keeps chunk c at slot c ^ ((r >> 1) & 3). A
+// direct-to-LDS load writes lane l's 16 bytes to slot l of a 1 KB block (16 rows), so lane l loads
+// row 16b + (l >> 2), chunk (l & 3) ^ ((l >> 3) & 3). MFMA operand reads (lane: row l & 15,
+// chunk l >> 4) then touch 8 distinct 16-byte slots mod 128 bytes per 8 lanes: no bank conflicts.
+//
+// The C tile is staged through LDS in two passes of 128 rows (f32, pitch WTP) and each pass runs
+// the 128x128 epilogue on both column halves, so every epilogue of the pipelined kernels applies
+// (QKV and SwiGLU need a 128-column half inside one of q/k/v or one w1|w3 block pair, as there).
+// The per-element order of the f32 sums is that of the 128x128 kernels (K tiles in order, 32-wide
+// MFMA K steps in order), so both give the same bits.
+//
+// Where it pays (same box, f16 operands and output, against the two-stage 128x128 kernel): long
+// K. 4096^3 170.4 -> 144.8 us, 8192^3 1090 -> 962 us, 4096 x 4096 x 3072 128.1 -> 115.4 us; at
+// K = 1024 it loses (6352 x 4096: 79.8 -> 82.8 us, 6352 x 3072: 55.5 -> 70.2 us): 32 K tiles do
+// not amortise the four-stage fill and the 256x256 epilogue, and 400 tiles quantise to two rounds
+// of 256 CUs. A laboratory copy of the loop alone (4096^3, random operands) runs 0.83 us per
+// 32-wide K tile against 0.48 with the DMAs removed and 0.60 with the MFMAs removed: the
+// direct-to-LDS refill path, not the LDS port or the MFMA rate, sets the pace.
+// ---------------------------------------------------------------------------------------------
+constexpr int WB = 256, WK = 32, WNS = 5;
+constexpr int WSTAGE = WB * WK;   // halves per operand tile of one stage (16 KB)
+constexpr int WTP = 260;          // pitch (floats) of the staged f32 half C tile (128 x 256): 4 rows
+                                  // = 16 banks apart, as TP
+
+template <int EPI>
+__device__ __forceinline__ void wide_tile(const GemmProblem &P, int m0, int n0, int tid) {
+    // stage s: A tile at smem + s*WSTAGE, W tile at smem + (WNS + s)*WSTAGE; reused for the C tile
+    constexpr int SMEM = 2 * WNS * WSTAGE > 128 * WTP * 2 ? 2 * WNS * WSTAGE : 128 * WTP * 2;
+    __shared__ __attribute__((aligned(1024))) half_t smem[SMEM];
+
+    const int lane = tid & 63, wave = tid >> 6;
+    const int M = P.M, N = P.N, lda = P.lda, Kc = P.Kc, pad = P.pad, aT = P.a_T;
+    const RowMap am = P.amap;
+    const int ldw = P.ldw;
+    const i32x4 rsa = make_rsrc(P.A);
+    const i32x4 rsb = make_rsrc(P.W);
+
+    // loader rows of this lane: 32*wave + 16*i + (lane >> 2), chunk (lane & 3) ^ ((lane >> 3) & 3)
+    const int lr = lane >> 2, lc = (lane & 3) ^ ((lane >> 3) & 3);
+    int a_base[2], a_ts0[2], b_off[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int r = wave * 32 + i * 16 + lr;
+        const int m = m0 + r;
+        const int mm = m < M ? m : 0;
+        const int b = mm / am.L;
+        const int t = mm - b * am.L;
+        a_ts0[i] = m < M ? t - pad : -(1 << 29);
+        a_base[i] = ((b * am.seg + am.off + t - pad) * lda + lc * 8) * 2;
+        const int n = n0 + r;
+        b_off[i] = n < N ? (n * ldw + lc * 8) * 2 : -1;
+    }
+    const int lda2 = lda * 2;
+    // K tiles in order; the tap's source-row offset, the channel offset and the W column carried
+    int nt_trow = 0, nt_kin = 0, nt_kw = 0;
+    auto issue = [&](int stage) {
+        const int trow = nt_trow, kin = nt_kin, kw = nt_kw;
+        nt_kw += WK;
+        nt_kin += WK;
+        if (nt_kin == Kc) {
+            nt_kin = 0;
+            ++nt_trow;
+        }
+        const int kc2 = kin * 2 + trow * lda2;
+        lds_char *sa = (lds_char *)(smem + stage * WSTAGE) + wave * 2048;
+        lds_char *sb = (lds_char *)(smem + (WNS + stage) * WSTAGE) + wave * 2048;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int ts = a_ts0[i] + trow;
+            const unsigned vo = (ts >= 0 && ts < aT) ? (unsigned)(a_base[i] + kc2) : 0x80000000u;
+            dma16(rsa, vo, sa + i * 1024);
+        }
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const unsigned vo = b_off[i] >= 0 ? (unsigned)(b_off[i] + kw * 2) : 0x80000000u;
+            dma16(rsb, vo, sb + i * 1024);
+        }
+    };
+
+    floatx4 acc[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+    const int wm = wave >> 2, wn = wave & 3;
+    // operand read offsets (halves) inside a stage: row (lane & 15) of each 16-row block, chunk
+    // (lane >> 4) at slot (lane >> 4) ^ ((row >> 1) & 3)
+    const int rd = (lane & 15) * WK + (((lane >> 4) ^ (((lane & 15) >> 1) & 3)) * 8);
+    const int a_rd = wm * 128 * WK + rd, b_rd = wn * 64 * WK + rd;
+    auto compute = [&](int stage) {
+        const half_t *sa = smem + stage * WSTAGE + a_rd, *sb = smem + (WNS + stage) * WSTAGE + b_rd;
+        half8 af[8], bf[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bf[j] = *(const half8 *)(sb + j * 16 * WK);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) af[i] = *(const half8 *)(sa + i * 16 * WK);
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    };
+
+    // ring as in pipe_tile: at the top of a step tile kt has landed in stage kt % WNS for every
+    // wave and tiles kt+1 .. kt+WNS-1 are in flight (four DMAs per wave per tile)
+    const int nk = P.K / WK;
+    issue(0);
+#pragma unroll
+    for (int j = 1; j < WNS - 1; ++j)
+        if (nk > j) issue(j);
+    wait_vmcnt(4 * min(nk - 1, WNS - 2));
+    block_barrier();
+    if (nk > WNS - 1) issue(WNS - 1);
+    int kt = 0;
+    for (; kt + 2 * WNS <= nk; kt += WNS) {
+#pragma unroll
+        for (int s2 = 0; s2 < WNS; ++s2) {
+            compute(s2);
+            wait_vmcnt(4 * (WNS - 2));
+            block_barrier();
+            issue(s2);
+        }
+    }
+    for (; kt < nk; ++kt) {
+        const int st = kt % WNS;
+        compute(st);
+        if (kt + 1 < nk) {
+            wait_vmcnt(4 * min(nk - 2 - kt, WNS - 2));
+            block_barrier();
+            if (kt + WNS < nk) issue(st);
+        }
+    }
+    // two passes of 128 rows: the waves of that row half store their accumulators as a row-major
+    // f32 [128][256] tile in LDS, then all 8 waves run the epilogue on each 128-column half
+    block_barrier();
+    float *tile = (float *)smem;
+#pragma unroll 1
+    for (int p = 0; p < 2; ++p) {
+        if (wm == p) {
+            const int rb = (lane >> 4) * 4, cb = wn * 64 + (lane & 15);
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) tile[(rb + i * 16 + r) * WTP + cb + j * 16] = acc[i][j][r];
+        }
+        block_barrier();
+        if (m0 + p * 128 < M) {
+            tile_epilogue<EPI, WTP>(P, tile, m0 + p * 128, n0, 0, tid);
+            if (n0 + 128 < N) tile_epilogue<EPI, WTP>(P, tile + 128, m0 + p * 128, n0 + 128, 0, tid);
+        }
+        block_barrier();
+    }
+}
+
+// workgroup -> (problem, 256x256 tile) with the XCD remap and the grouped tile order of the
+// 128x128 kernels
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void gemm_wide_kernel(const GemmBatch bt) {
+    const int wg = xcd_remap(blockIdx.x, bt.total_tiles);
+    const int pi = (bt.nprob > 2 && wg >= bt.p[2].tile_start) ? 2 : (bt.nprob > 1 && wg >= bt.p[1].tile_start) ? 1 : 0;
+    const GemmProblem &P = bt.p[pi];
+    int tm, tn;
+    tile_mn(wg - P.tile_start, P.tiles_m, P.tiles_n, tm, tn);
+    wide_tile<EPI>(P, tm * WB, tn * WB, threadIdx.x);
 }
 
 // gemm_small_kernel: plain GEMMs (one tap), 64x64 C tiles over the full K, 4 waves of 32x32
@@ -1658,9 +1844,33 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
                                                                         : "gemm_f16_kernel<false, 2>");
     // two LDS stages and two workgroups per CU once the data-parallel grid exceeds one round
     b.ns2 = pipe && !b.sk && b.total_tiles > NCU ? 1 : 0;
+    // 256x256 tiles instead, when that grid still fills the chip and K is long (no split, no
+    // half-width W, one of the epilogues the wide kernel stages)
+    b.wide = 0;
+    if (b.ns2 && !b.hl && !b.bf16 && (epi == EPI_STORE || epi == EPI_RESID || epi == EPI_QKV || epi == EPI_SWIGLU)) {
+        bool nosplit = true;
+        long long wt = 0;
+        for (int i = 0; i < b.nprob; ++i) {
+            nosplit = nosplit && b.p[i].splits == 1 && b.p[i].K >= WIDE_MIN_K;
+            wt += (long long)((b.p[i].M + WB - 1) / WB) * ((b.p[i].N + WB - 1) / WB);
+        }
+        if (nosplit && wt >= WIDE_MIN_TILES) {
+            int t = 0;
+            for (int i = 0; i < b.nprob; ++i) {
+                GemmProblem &p = b.p[i];
+                p.tiles_m = (p.M + WB - 1) / WB;
+                p.tiles_n = (p.N + WB - 1) / WB;
+                p.tile_start = t;
+                t += p.tiles_m * p.tiles_n;
+            }
+            b.total_tiles = t;
+            b.wide = 1;
+            b.ns2 = 0;
+        }
+    }
     // weight prefetch workgroups after the tiles: data-parallel pipelined kernels only
     TSN_REQUIRE(pf_ranges_ok(b.pf), "gemm: prefetch ranges");
-    b.pf_nwg = pipe && !b.sk ? pf_workgroups(b.pf, 8) : 0;
+    b.pf_nwg = pipe && !b.sk && !b.wide ? pf_workgroups(b.pf, 8) : 0;
     // GEMV rows on the CUs a single-round grid leaves free (one pipelined workgroup per CU); they
     // replace the prefetch workgroups
     b.gv_nwg = 0;
@@ -1677,7 +1887,10 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         TSN_REQUIRE(pipe, "gemm bf16: needs K % 64 == 0, N % 8 == 0 and 16-byte aligned rows, W, bias and Y");
         b.kname = b.ns2 ? "gemm_pipe2_bf16_kernel<0>" : "gemm_pipe_bf16_kernel<0>";
     }
-    if (b.ns2 && b.hl)
+    if (b.wide)
+        b.kname = epi == EPI_STORE ? "gemm_wide_kernel<0>" : epi == EPI_RESID ? "gemm_wide_kernel<1>"
+                  : epi == EPI_QKV ? "gemm_wide_kernel<2>" : "gemm_wide_kernel<3>";
+    else if (b.ns2 && b.hl)
         b.kname = epi == EPI_STORE ? "gemm_pipe2_hl_kernel<0>" : epi == EPI_RESID ? "gemm_pipe2_hl_kernel<1>"
                   : epi == EPI_QKV ? "gemm_pipe2_hl_kernel<2>" : "gemm_pipe2_hl_kernel<3>";
     else if (b.ns2)
@@ -1704,6 +1917,15 @@ int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st)
         TSN_REQUIRE(b.pipe && epi == EPI_STORE, "gemm bf16: pipelined store kernel only");
         if (b.ns2) TSN_LAUNCH((gemm_pipe2_bf16_kernel<EPI_STORE>), grid, block, 0, st, b);
         else TSN_LAUNCH((gemm_pipe_bf16_kernel<EPI_STORE>), grid, block, 0, st, b);
+        TSN_HIP_CHECK(hipGetLastError());
+        return TSN_OK;
+    }
+    if (b.wide) {
+        if (epi == EPI_STORE) TSN_LAUNCH((gemm_wide_kernel<EPI_STORE>), grid, block, 0, st, b);
+        else if (epi == EPI_RESID) TSN_LAUNCH((gemm_wide_kernel<EPI_RESID>), grid, block, 0, st, b);
+        else if (epi == EPI_QKV) TSN_LAUNCH((gemm_wide_kernel<EPI_QKV>), grid, block, 0, st, b);
+        else if (epi == EPI_SWIGLU) TSN_LAUNCH((gemm_wide_kernel<EPI_SWIGLU>), grid, block, 0, st, b);
+        else { set_error("gemm: no wide kernel for this epilogue"); return TSN_ERR_ARG; }
         TSN_HIP_CHECK(hipGetLastError());
         return TSN_OK;
     }

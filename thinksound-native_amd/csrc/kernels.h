@@ -122,6 +122,9 @@ struct GemmBatch {
     // set by gemm_plan: the two-stage kernel (gemm_pipe2_kernel, two workgroups per CU) for
     // data-parallel grids of more than one round (256 tiles)
     int ns2 = 0;
+    // set by gemm_plan: 256x256 tiles (gemm_wide_kernel) for data-parallel grids of several rounds
+    // whose 256x256 grid still fills the chip; tiles_m/tiles_n/tile_start then count 256x256 tiles
+    int wide = 0;
     // nonzero: A and W hold bf16 values and the MFMAs run bf16 products (gemm_pipe_bf16_kernel /
     // gemm_pipe2_bf16_kernel: EPI_STORE with f32 Y, one tap, data-parallel, no split)
     int bf16 = 0;

@@ -273,7 +273,7 @@ void DitModel::next_ln(RedLnArgs &r, Next next, const RowMap *maps, int nseg) {
         case NEXT_JOINT: g.ln = 1; g.shift_off = (text ? jt_ : ja_)[next.idx].mod_off; break;
         case NEXT_FUSED: g.ln = 1; g.shift_off = fu_[next.idx].mod_off; break;
         case NEXT_FINAL:
-            g.ln = text ? 0 : 1;
+            g.ln = text || final_fused() ? 0 : 1;   // the fused final kernel normalises its own rows
             g.shift_off = fin_mod_off_;
             g.ln_len = m.L < s.La ? m.L : s.La;
             g.Y = XF2_; g.ldy = 2 * s.H; g.ymap = RowMap{m.L, s.La, 0};   // audio row t of sample b -> b*La + t
@@ -540,8 +540,22 @@ int DitModel::enqueue_eval(const float *z, const float *t, const float *text, co
         else TSN_TRY(block_fused(k - s.n_joint, k == 0, next));
         if (taps) TSN_TRY(rt->dev.copy_d2d(taps + tap_n * tap++, X_, tap_n * 4));
     }
-    // final layer: adaLN (2 chunks) on audio rows as f16 hi|lo, projection to latent by one MFMA
-    // GEMM against [W|W] (f32-accurate), split over K (src/dit_fwd.cpp:287-303)
+    // final layer (src/dit_fwd.cpp:287-303): adaLN (2 chunks) of the audio rows and the projection
+    // to the latent channels in one kernel
+    if (final_fused()) {
+        FinalArgs f;
+        memset(&f, 0, sizeof f);
+        f.X = X_; f.ldx = H; f.xmap = RowMap{s.La, S, 0};
+        f.mod = mod_; f.mod_ld = NMOD; f.mod_L = s.La; f.shift_off = fin_mod_off_; f.scale_off = fin_mod_off_ + H;
+        f.W = Wfin2_; f.ldw = 2 * H; f.bias = bfin_;
+        f.Y = v; f.ldy = s.latent;
+        f.rows = B * s.La; f.H = H; f.N = s.latent; f.eps = s.ln_eps;
+        return run("final_out_kernel", 2.0 * B * s.La * (double)s.latent * H,
+                   B * s.La * (double)H * 4.0 + (double)s.latent * H * 2.0 + B * s.La * (double)s.latent * 4.0,
+                   [&] { return launch_final_out(f, st); });
+    }
+    // otherwise: adaLN on audio rows as f16 hi|lo, projection to latent by one MFMA GEMM against
+    // [W|W] (f32-accurate), split over K
     if (nblk == 0) {
         LnArgs ln;
         memset(&ln, 0, sizeof ln);

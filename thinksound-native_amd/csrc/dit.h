@@ -108,6 +108,8 @@ private:
     const half_t *Win2_ = nullptr, *Wfin2_ = nullptr;   // [W|W] f16 for the hi|lo projections
     const float *bmod_ = nullptr, *bt0_ = nullptr, *bt2_ = nullptr, *bin_ = nullptr, *bfin_ = nullptr;
     int fin_mod_off_ = 0;
+    // the final adaLN + projection as one kernel (launch_final_out) where the shapes allow it
+    bool final_fused() const { return s.H % 256 == 0 && s.H <= 2048 && s.latent % 16 == 0 && s.latent <= 64; }
     float *rope_ = nullptr;
     float *X_ = nullptr, *MOD_ = nullptr, *g_ = nullptr, *gs_ = nullptr, *temb_ = nullptr, *h1_ = nullptr;
     half_t *XF2_ = nullptr, *Z2_ = nullptr;               // hi|lo operands of the projections

@@ -244,6 +244,21 @@ struct LinArgs {
 };
 int launch_linear_f32(const LinArgs &a, hipStream_t st);
 
+/* ------------------------------------------------------------------ final layer */
+// v[r] = (LN(x_r; eps)*(1 + scale) + shift) . W^T + bias for the audio rows r < rows (x row
+// xmap(r), sample r / mod_L), W f16 [N][ldw] (first H columns), N <= 64 and a multiple of 16,
+// H a multiple of 256 up to 2048; f32 statistics, f32-accurate product (hi|lo operand).
+struct FinalArgs {
+    const float *X; int ldx; RowMap xmap;
+    const float *mod; int mod_ld, mod_L, shift_off, scale_off;
+    const half_t *W; int ldw;
+    const float *bias;
+    float *Y; int ldy;
+    int rows, H, N;
+    float eps;
+};
+int launch_final_out(const FinalArgs &a, hipStream_t st);
+
 /* ------------------------------------------------------------------ small kernels */
 int launch_temb_sinusoid(const float *t, float *out, int nb, int D, float max_period, hipStream_t st);
 // dst[dmap(m)*ldd + c] = src[smap(m)*lds + c], c < H (f32)

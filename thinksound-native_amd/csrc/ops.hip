@@ -470,7 +470,103 @@ __global__ void rope_pairs_kernel(float *x, const int32_t *pos, int rows, int nh
 
 inline unsigned blocks_for(size_t n, unsigned t = 256) { return (unsigned)((n + t - 1) / t); }
 
+/* ---------------- final layer: adaLN + projection to the latent channels (src/dit_fwd.cpp:287-303) ---------------- */
+// 16 audio rows per workgroup. Wave w normalises rows 4w .. 4w + 3 exactly as ln_mod_kernel does
+// (f32 statistics, one wave per row) and parks y as an f16 hi|lo pair in an LDS tile (row pitch
+// 2H + 8 halves: the 16 rows of an MFMA operand read fall 16 bytes apart mod 128, no bank
+// conflicts). Then wave w computes output columns 16w .. 16w + 15 for the 16 rows with
+// v_mfma_f32_16x16x32_f16, the hi half and the lo half of each 32-wide K slice against the same f16
+// weight columns (an f32-accurate operand), and adds the bias. One launch instead of an LN launch, a
+// split-K GEMM and its reduce.
+template <int NV>
+__global__ __launch_bounds__(256) void final_out_kernel(const FinalArgs a) {
+    constexpr int H = 256 * NV, P = 2 * H + 8;
+    __shared__ __attribute__((aligned(16))) half_t tileA[16 * P];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int row0 = blockIdx.x * 16;
+#pragma unroll 1
+    for (int j = 0; j < 4; ++j) {
+        const int lr = wave * 4 + j, v = row0 + lr;
+        if (v >= a.rows) break;   // wave-uniform; rows past the end are never stored
+        const float *x = a.X + rowmap_phys(a.xmap, v) * (long long)a.ldx;
+        const float *mb = a.mod + (long long)(v / a.mod_L) * a.mod_ld;
+        float4 xv[NV], sh[NV], scl[NV];
+#pragma unroll
+        for (int c = 0; c < NV; ++c) {
+            xv[c] = *(const float4 *)(x + c * 256 + lane * 4);
+            sh[c] = *(const float4 *)(mb + a.shift_off + c * 256 + lane * 4);
+            scl[c] = *(const float4 *)(mb + a.scale_off + c * 256 + lane * 4);
+        }
+        float sum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NV; ++c) sum += (xv[c].x + xv[c].y) + (xv[c].z + xv[c].w);
+        const float inv_h = 1.0f / (float)H;
+        const float mean = wave_sum(sum) * inv_h;
+        float var = 0.0f;
+#pragma unroll
+        for (int c = 0; c < NV; ++c) {
+            const float d0 = xv[c].x - mean, d1 = xv[c].y - mean, d2 = xv[c].z - mean, d3 = xv[c].w - mean;
+            var += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+        }
+        var = wave_sum(var) * inv_h;
+        const float inv = 1.0f / sqrtf(var + a.eps);
+#pragma unroll
+        for (int c = 0; c < NV; ++c) {
+            const int col = c * 256 + lane * 4;
+            const float y0 = (xv[c].x - mean) * inv * (1.0f + scl[c].x) + sh[c].x;
+            const float y1 = (xv[c].y - mean) * inv * (1.0f + scl[c].y) + sh[c].y;
+            const float y2 = (xv[c].z - mean) * inv * (1.0f + scl[c].z) + sh[c].z;
+            const float y3 = (xv[c].w - mean) * inv * (1.0f + scl[c].w) + sh[c].w;
+            const half4 hi = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
+            *(half4 *)(tileA + lr * P + col) = hi;
+            *(half4 *)(tileA + lr * P + H + col) = half4{(half_t)(y0 - (float)hi[0]), (half_t)(y1 - (float)hi[1]),
+                                                         (half_t)(y2 - (float)hi[2]), (half_t)(y3 - (float)hi[3])};
+        }
+    }
+    __syncthreads();
+    const int n0 = wave * 16;
+    if (n0 >= a.N) return;   // wave-uniform
+    const int n = n0 + (lane & 15), kg = (lane >> 4) * 8;
+    const half_t *wrow = a.W + (long long)n * a.ldw + kg;
+    const half_t *arow = tileA + (lane & 15) * P + kg;
+    floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 8
+    for (int k0 = 0; k0 < H; k0 += 32) {
+        const half8 bf = *(const half8 *)(wrow + k0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8 *)(arow + k0), bf, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8 *)(arow + H + k0), bf, acc, 0, 0, 0);
+    }
+    const float bn = a.bias ? a.bias[n] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int v = row0 + 4 * (lane >> 4) + r;
+        if (v < a.rows) a.Y[(long long)v * a.ldy + n] = acc[r] + bn;
+    }
+}
+
 } // namespace
+
+int launch_final_out(const FinalArgs &a, hipStream_t st) {
+    TSN_REQUIRE(a.X && a.mod && a.W && a.Y && a.rows > 0 && a.mod_L > 0 && a.xmap.L > 0, "final: arguments");
+    TSN_REQUIRE(a.H % 256 == 0 && a.H >= 256 && a.H <= 2048, "final: H must be a multiple of 256 in [256, 2048]");
+    TSN_REQUIRE(a.N > 0 && a.N <= 64 && a.N % 16 == 0, "final: N must be a multiple of 16 up to 64");
+    TSN_REQUIRE(a.ldx % 4 == 0 && a.mod_ld % 4 == 0 && a.shift_off % 4 == 0 && a.scale_off % 4 == 0 && a.ldw % 8 == 0 &&
+                    a.ldw >= a.H && (((uintptr_t)a.W) & 15) == 0 && (((uintptr_t)a.X | (uintptr_t)a.mod) & 15) == 0,
+                "final: strides, offsets and alignment");
+    const dim3 grid((unsigned)((a.rows + 15) / 16)), block(256);
+    switch (a.H / 256) {
+        case 1: TSN_LAUNCH(final_out_kernel<1>, grid, block, 0, st, a); break;
+        case 2: TSN_LAUNCH(final_out_kernel<2>, grid, block, 0, st, a); break;
+        case 3: TSN_LAUNCH(final_out_kernel<3>, grid, block, 0, st, a); break;
+        case 4: TSN_LAUNCH(final_out_kernel<4>, grid, block, 0, st, a); break;
+        case 5: TSN_LAUNCH(final_out_kernel<5>, grid, block, 0, st, a); break;
+        case 6: TSN_LAUNCH(final_out_kernel<6>, grid, block, 0, st, a); break;
+        case 7: TSN_LAUNCH(final_out_kernel<7>, grid, block, 0, st, a); break;
+        default: TSN_LAUNCH(final_out_kernel<8>, grid, block, 0, st, a); break;
+    }
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
 
 bool pf_ranges_ok(const PfRange (&pf)[PF_RANGES]) {
     for (int i = 0; i < PF_RANGES; ++i)

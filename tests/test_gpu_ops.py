@@ -357,6 +357,25 @@ def test_attention(tsn, rt, orc, S):
     assert rel_l2(o, ref) < 3e-3
 
 
+@pytest.mark.parametrize("S", [910, 1024])
+def test_attention_two_group_route(tsn, rt, orc, S):
+    """64 heads: at least 512 workgroups of 128 queries, the route of the batch-16 workload (the
+    four-wave kernel with two 16-query groups per wave). S = 910 leaves a last tile of 14 queries,
+    so three of its four waves hold no query and only take their share of the key-block loads."""
+    r = rng(83 + S)
+    nh, hd = 64, 64
+    H = nh * hd
+    qkv = r.standard_normal((S, 3 * H)).astype(np.float32)
+    qkv[:, :2 * H] *= 1.5
+    out = rt.array(np.full((S, H), np.nan, np.float32))
+    rt.attention(rt.array(qkv), out, S, nh, hd, 3 * H, H, 0, H, 2 * H, 0, 0.125)
+    rt.sync()
+    o = out.numpy()
+    assert not np.isnan(o).any()
+    ref_m = orc.attention(f16r(qkv), S, nh, hd, 3 * H, H, 0, H, 2 * H, 0, 0.125)
+    assert rel_l2(o, ref_m) < 2e-3
+
+
 def test_launcher_surface_rest(tsn, rt, orc):
     """geglu, gelu_quick, ln_plain, ln_wb, rms_w, mean_cols and qkv_split3 against the oracle"""
     r = rng(71)

@@ -609,6 +609,183 @@ __global__ __launch_bounds__(256, 3) void flash_attn4_kernel(const AttnArgs a) {
     }
 }
 
+// Four-wave kernel with two query groups per wave: 128 queries per workgroup, wave w serves
+// queries 32w .. 32w + 31 as two groups of 16 over every key block. Each K and Vt fragment read from
+// LDS feeds both groups' MFMAs (half the LDS operand reads per flop of flash_attn4_kernel), and each
+// wave carries two independent softmax chains. Ring, MFMA formulation, online softmax and
+// probability rounding as flash_attn4_kernel; for grids whose 64-query version exceeds a round.
+__global__ __launch_bounds__(256, 3) void flash_attn4q2_kernel(const AttnArgs a) {
+    constexpr int STG = 8192;
+    constexpr int NST = 3;
+    __shared__ __attribute__((aligned(1024))) half_t smem[NST * STG];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nqt = (a.S + 127) >> 7;
+    const int wg = attn_xcd_remap(blockIdx.x, gridDim.x);
+    const int bh = wg / nqt, qt = wg - bh * nqt;
+    const int S = a.S, Sp = a.Sp;
+    const half_t *Qp = a.Q + (long long)bh * S * 64;
+    const unsigned long long ka = (unsigned long long)(a.K + (long long)bh * S * 64);
+    const i32x4 rk = i32x4{(int)(unsigned)ka, (int)((ka >> 32) & 0xFFFF), S * 128, 0x00020000};
+    const i32x4 rv = make_rsrc(a.Vt + (long long)bh * 64 * Sp);
+
+    const int g = lane >> 4;
+    int q[2];
+    half8 qf[2][2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        q[u] = qt * 128 + wave * 32 + u * 16 + (lane & 15);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+            qf[u][ks] = q[u] < S ? *(const half8 *)(Qp + (long long)q[u] * 64 + ks * 32 + g * 8) : zero_h8();
+    }
+    // whole wave past the last query: its MFMAs are skipped (it still takes its DMA share and barriers)
+    const bool live = qt * 128 + wave * 32 < S;
+
+    const int nkb = (S + AKB - 1) / AKB;
+    const int lr = lane >> 3;
+    unsigned voff[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int d = wave * 4 + i, part = d >> 3, sub = d & 7;
+        const int lc = (lane & 7) ^ lr ^ sub;
+        voff[i] = part == 0 ? (unsigned)(((sub * 8 + lr) * 64 + lc * 8) * 2)
+                            : (unsigned)(((sub * 8 + lr) * Sp + lc * 8) * 2);
+    }
+    auto issue = [&](int b, int st) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int d = wave * 4 + i, part = d >> 3, sub = d & 7;
+            const unsigned vo = voff[i] + (part == 0 ? (unsigned)b * 8192u : (unsigned)b * 128u);
+            dma16(part == 0 ? rk : rv, vo, (lds_char *)(smem + st * STG + part * 4096 + sub * 512));
+        }
+    };
+
+    float m_i[2] = {-INFINITY, -INFINITY};
+    floatx4 o[2][4], lsum[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        lsum[u] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[u][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    const half8 ones = half8{1, 1, 1, 1, 1, 1, 1, 1};
+    const float scale = a.scale_log2;
+
+    unsigned k_off[4][2], v_off[2][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int i = lane & 15;
+        const int r = 32 * (j >> 1) + 8 * (i >> 2) + 4 * (j & 1) + (i & 3);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) k_off[j][ks] = r * 64 + (((ks * 4 + g) ^ sw(r)) * 8);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            const int d = dt * 16 + (lane & 15);
+            v_off[c][dt] = 4096 + d * 64 + (((c * 4 + g) ^ sw(d)) * 8);
+        }
+
+    auto compute = [&](int st, int blk) {
+        const half_t *sK = smem + st * STG;
+        floatx4 sc[2][4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            sc[0][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            sc[1][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+                const half8 kf = *(const half8 *)(sK + k_off[j][ks]);
+                sc[0][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[0][ks], sc[0][j], 0, 0, 0);
+                sc[1][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[1][ks], sc[1][j], 0, 0, 0);
+            }
+        }
+        if (blk * AKB + AKB > S) {   // the last, partial key block only (wave-uniform)
+#pragma unroll
+            for (int u = 0; u < 2; ++u)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (blk * AKB + 32 * (j >> 1) + 8 * g + 4 * (j & 1) + r >= S) sc[u][j][r] = -INFINITY;
+        }
+        half8 pf[2][2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) mx = fmaxf(fmaxf(mx, fmaxf(sc[u][j][0], sc[u][j][1])), fmaxf(sc[u][j][2], sc[u][j][3]));
+            lazy_max(m_i[u], rows_max(mx) * scale, o[u], lsum[u]);
+            half_t ph[4][4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    ph[j][r] = (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[u][j][r], scale, -m_i[u]));
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+                pf[u][c] = half8{ph[2 * c][0], ph[2 * c][1], ph[2 * c][2], ph[2 * c][3],
+                                 ph[2 * c + 1][0], ph[2 * c + 1][1], ph[2 * c + 1][2], ph[2 * c + 1][3]};
+        }
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const half8 vf = *(const half8 *)(sK + v_off[c][dt]);
+                o[0][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[0][c], o[0][dt], 0, 0, 0);
+                o[1][dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[1][c], o[1][dt], 0, 0, 0);
+            }
+            lsum[0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[0][c], lsum[0], 0, 0, 0);
+            lsum[1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[1][c], lsum[1], 0, 0, 0);
+        }
+    };
+
+    issue(0, 0);
+    if (nkb > 1) issue(1, 1);
+    wait_vmcnt(nkb > 1 ? 4 : 0);
+    block_barrier();
+    if (nkb > 2) issue(2, 2);
+    for (int b0 = 0; b0 < nkb; b0 += NST) {
+#pragma unroll
+        for (int u = 0; u < NST; ++u) {
+            const int b = b0 + u;
+            if (b < nkb) {
+                if (live) compute(u, b);
+                if (b + 1 < nkb) {
+                    wait_vmcnt(b + 2 < nkb ? 4 : 0);
+                    block_barrier();
+                    if (b + NST < nkb) issue(b + NST, u);
+                }
+            }
+        }
+    }
+    const int bb = bh / a.nh, h = bh - bb * a.nh;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+        if (q[u] >= S) continue;
+        const float inv = 1.0f / lsum[u][0];
+        const long long orow = rowmap_phys(a.omap, bb * S + q[u]) * (long long)a.ldo + h * 64;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            const int d0 = dt * 16 + g * 4;
+            if (a.o_f32) {
+                float *op = (float *)a.O + orow + d0;
+                *(float4 *)op = make_float4(o[u][dt][0] * inv, o[u][dt][1] * inv, o[u][dt][2] * inv, o[u][dt][3] * inv);
+            } else {
+                half_t *op = (half_t *)a.O + orow + d0;
+                const float y0 = o[u][dt][0] * inv, y1 = o[u][dt][1] * inv, y2 = o[u][dt][2] * inv, y3 = o[u][dt][3] * inv;
+                const half4 hi = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
+                *(half4 *)op = hi;
+                if (a.o_lo)
+                    *(half4 *)(op + a.o_lo) = half4{(half_t)(y0 - (float)hi[0]), (half_t)(y1 - (float)hi[1]),
+                                                    (half_t)(y2 - (float)hi[2]), (half_t)(y3 - (float)hi[3])};
+            }
+        }
+    }
+}
+
 // f32 [S, ld] q/k/v slices -> Q/K [nh][S][64], Vt [nh][64][Sp] (f16), one thread per element
 __global__ void attn_pack_kernel(const float *qkv, int S, int nh, int ld, int q_off, int k_off, int v_off,
                                  half_t *Q, half_t *K, half_t *Vt, int Sp) {
@@ -648,7 +825,12 @@ int launch_attention(const AttnArgs &a, hipStream_t st) {
     dim3 grid((unsigned)((a.S + 63) / 64 * a.BH)), block(512);
     // up to 512 keys and at most one workgroup per CU: all key blocks in LDS at once; grids beyond
     // one round (256 workgroups): the four-wave kernel, up to four workgroups per CU
+    // grids of at least two workgroups per CU in 128-query workgroups: the two-group kernel (batch
+    // 16 at 8 s: 1024 workgroups, 7.25 -> 7.20-7.23 ms per evaluation); with fewer (30 s: 288) it
+    // leaves too few waves per CU and the 64-query kernel is faster (3.99 -> 4.05 ms measured)
+    const long long g2 = (long long)(a.S + 127) / 128 * a.BH;
     if (a.S <= 4 * 2 * AKB && grid.x <= 256) TSN_LAUNCH(flash_attn_kernel<4>, grid, block, 0, st, a);
+    else if (g2 >= 512) TSN_LAUNCH(flash_attn4q2_kernel, dim3((unsigned)g2), dim3(256), 0, st, a);
     else if (grid.x > 256) TSN_LAUNCH(flash_attn4_kernel, grid, dim3(256), 0, st, a);
     else TSN_LAUNCH(flash_attn_kernel<2>, grid, block, 0, st, a);
     TSN_HIP_CHECK(hipGetLastError());

@@ -353,6 +353,24 @@ __device__ __forceinline__ void dma16(i32x4 rs, unsigned voff, lds_char *lds) {
                  : "memory");
 }
 
+// The same with a wave-uniform byte offset in soffset: the per-row part of the address (voff) stays
+// in a register across K tiles and only the scalar K offset moves, so a K tile's refill costs no
+// vector instructions. Rows outside the operand carry voff = 0x80000000, out of range with or
+// without the scalar offset.
+// lds is the LDS byte address of the 1 KB block. Both scalars are wave-uniform; readfirstlane
+// costs nothing where the compiler already holds them in scalar registers.
+__device__ __forceinline__ void dma16s(i32x4 rs, unsigned voff, unsigned soff, unsigned lds) {
+    asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(voff), "s"(rs), "s"(__builtin_amdgcn_readfirstlane(soff)),
+                   "s"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+}
+// LDS byte address of element e of an LDS array (wave-uniform when e is)
+__device__ __forceinline__ unsigned lds_addr(const half_t *base) {
+    return (unsigned)(unsigned long)(const lds_char *)base;
+}
+
 // s_waitcnt vmcnt(n) (n in {0, 4, 8, 12}) with expcnt/lgkmcnt left at their maxima
 __device__ __forceinline__ void wait_vmcnt(int n) {
     if (n >= 12) __builtin_amdgcn_s_waitcnt(12 | (7 << 4) | (0xF << 8));
@@ -704,7 +722,7 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
     constexpr int SMEM = 2 * NSX * STAGE > BM * TP * 2 ? 2 * NSX * STAGE : BM * TP * 2;
     __shared__ __attribute__((aligned(1024))) half_t smem[SMEM];
 
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int M = P.M, N = P.N, lda = P.lda, Kc = P.Kc, pad = P.pad, aT = P.a_T;
     // w_half: W holds hc = Kc/2 channels per tap and the A row of a tap is [hi (hc) | lo (hc)]; the
     // tap's K tiles run interleaved (hi chunk c, lo chunk c, hi chunk c+1, ...) so the second read
@@ -756,9 +774,27 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
         nt_kin = c0 * BK;
         nt_kw = nt_tap * Kc + nt_kin;
     }
+    // A row offsets of the tap whose source-row shift is va_trow (byte offset of the source row, or
+    // out of range where it falls outside its sample), rebuilt after an issue whose successor
+    // shifts the rows (every K tile of the snake convs, once per tap otherwise): the rebuild's
+    // branch then follows the DMAs instead of splitting them from the MFMAs around the barrier.
+    // W row offsets are fixed.
+    unsigned va[2], vb[2];
+    int va_trow = nt_trow;
+    auto set_va = [&]() {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int ts = a_ts0[i] + va_trow;
+            va[i] = (ts >= 0 && ts < aT) ? (unsigned)(a_base[i] + va_trow * lda2) : 0x80000000u;
+        }
+    };
+    set_va();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) vb[i] = b_off[i] >= 0 ? (unsigned)b_off[i] : 0x80000000u;
+    const unsigned ldsw = lds_addr(smem) + wave * 2048;   // this wave's 2 KB of each operand tile
     auto issue = [&](int kt, int stage) {
         (void)kt;   // = the previous call's kt + 1
-        const int trow = nt_trow, kin = nt_kin, kw = nt_kw;
+        const int kin = nt_kin, kw = nt_kw;
         // hi|lo: K tile j of the tap is chunk j >> 1 of the hi (j even) or lo (j odd) half
         const int odd = (kin >> 6) & 1;
         const int acol = hl ? odd * hc + ((kin >> 7) << 6) : kin;
@@ -778,19 +814,14 @@ __device__ __forceinline__ void pipe_tile(const GemmProblem &P, int m0, int n0, 
             nt_trow += dil;
             nt_kw += Kc;
         }
-        const int kc2 = acol * 2 + trow * lda2;
-        lds_char *sa = (lds_char *)(smem + stage * STAGE) + wave * 2048;
-        lds_char *sb = (lds_char *)(smem + (NSX + stage) * STAGE) + wave * 2048;
+        const unsigned sa = ldsw + stage * STAGE * 2, sb = ldsw + (NSX + stage) * STAGE * 2;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int ts = a_ts0[i] + trow;
-            const unsigned vo = (ts >= 0 && ts < aT) ? (unsigned)(a_base[i] + kc2) : 0x80000000u;
-            dma16(rsa, vo, sa + i * 1024);
-        }
+        for (int i = 0; i < 2; ++i) dma16s(rsa, va[i], (unsigned)acol * 2, sa + i * 1024);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const unsigned vo = b_off[i] >= 0 ? (unsigned)(b_off[i] + kw * 2) : 0x80000000u;
-            dma16(rsb, vo, sb + i * 1024);
+        for (int i = 0; i < 2; ++i) dma16s(rsb, vb[i], (unsigned)kw * 2, sb + i * 1024);
+        if (nt_trow != va_trow) {
+            va_trow = nt_trow;
+            set_va();
         }
     };
 
@@ -1062,7 +1093,7 @@ __device__ __forceinline__ void wide_tile(const GemmProblem &P, int m0, int n0, 
     constexpr int SMEM = 2 * WNS * WSTAGE > 128 * WTP * 2 ? 2 * WNS * WSTAGE : 128 * WTP * 2;
     __shared__ __attribute__((aligned(1024))) half_t smem[SMEM];
 
-    const int lane = tid & 63, wave = tid >> 6;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int M = P.M, N = P.N, lda = P.lda, Kc = P.Kc, pad = P.pad, aT = P.a_T;
     const RowMap am = P.amap;
     const int ldw = P.ldw;
@@ -1087,27 +1118,36 @@ __device__ __forceinline__ void wide_tile(const GemmProblem &P, int m0, int n0, 
     const int lda2 = lda * 2;
     // K tiles in order; the tap's source-row offset, the channel offset and the W column carried
     int nt_trow = 0, nt_kin = 0, nt_kw = 0;
+    // per-row A offsets of the current tap and fixed W row offsets, as in pipe_tile
+    unsigned va[2], vb[2];
+    int va_trow = 0;
+    auto set_va = [&]() {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int ts = a_ts0[i] + va_trow;
+            va[i] = (ts >= 0 && ts < aT) ? (unsigned)(a_base[i] + va_trow * lda2) : 0x80000000u;
+        }
+    };
+    set_va();
+#pragma unroll
+    for (int i = 0; i < 2; ++i) vb[i] = b_off[i] >= 0 ? (unsigned)b_off[i] : 0x80000000u;
+    const unsigned ldsw = lds_addr(smem) + wave * 2048;
     auto issue = [&](int stage) {
-        const int trow = nt_trow, kin = nt_kin, kw = nt_kw;
+        const int kin = nt_kin, kw = nt_kw;
         nt_kw += WK;
         nt_kin += WK;
         if (nt_kin == Kc) {
             nt_kin = 0;
             ++nt_trow;
         }
-        const int kc2 = kin * 2 + trow * lda2;
-        lds_char *sa = (lds_char *)(smem + stage * WSTAGE) + wave * 2048;
-        lds_char *sb = (lds_char *)(smem + (WNS + stage) * WSTAGE) + wave * 2048;
+        const unsigned sa = ldsw + stage * WSTAGE * 2, sb = ldsw + (WNS + stage) * WSTAGE * 2;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int ts = a_ts0[i] + trow;
-            const unsigned vo = (ts >= 0 && ts < aT) ? (unsigned)(a_base[i] + kc2) : 0x80000000u;
-            dma16(rsa, vo, sa + i * 1024);
-        }
+        for (int i = 0; i < 2; ++i) dma16s(rsa, va[i], (unsigned)kin * 2, sa + i * 1024);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const unsigned vo = b_off[i] >= 0 ? (unsigned)(b_off[i] + kw * 2) : 0x80000000u;
-            dma16(rsb, vo, sb + i * 1024);
+        for (int i = 0; i < 2; ++i) dma16s(rsb, vb[i], (unsigned)kw * 2, sb + i * 1024);
+        if (nt_trow != va_trow) {   // the next K tile starts a tap
+            va_trow = nt_trow;
+            set_va();
         }
     };
 
@@ -1215,7 +1255,7 @@ template <int EPI>
 __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) {
     static_assert(EPI == EPI_RESID, "gemm_small_kernel: residual epilogue only");
     __shared__ __attribute__((aligned(1024))) half_t smem[2 * SNS * SSTAGE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     if ((int)blockIdx.x >= bt.total_tiles) {   // prefetch workgroups after the tiles (GemmBatch::pf)
         prefetch_wg<4>(bt.pf, blockIdx.x - bt.total_tiles, wave, lane);
         return;
@@ -1265,22 +1305,22 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
         b_off[i] = n < N ? (n * ldw + lc * 8) * 2 : -1;
     }
     int nt_k = 0;   // K column of the next K tile (plain GEMM: one tap, so A and W share it)
+    // row offsets fixed over K (out of range outside the operand); the K column goes in soffset
+    unsigned va[2], vb[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        va[i] = (a_ts0[i] >= 0 && a_ts0[i] < aT) ? (unsigned)a_base[i] : 0x80000000u;
+        vb[i] = b_off[i] >= 0 ? (unsigned)b_off[i] : 0x80000000u;
+    }
+    const unsigned ldsw = lds_addr(smem) + wave * 2048;
     auto issue = [&](int stage) {
         const int k = nt_k;
         nt_k += BK;
-        lds_char *sa = (lds_char *)(smem + stage * SSTAGE) + wave * 2048;
-        lds_char *sb = (lds_char *)(smem + (SNS + stage) * SSTAGE) + wave * 2048;
+        const unsigned sa = ldsw + stage * SSTAGE * 2, sb = ldsw + (SNS + stage) * SSTAGE * 2;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int ts = a_ts0[i];
-            const unsigned vo = (ts >= 0 && ts < aT) ? (unsigned)(a_base[i] + k * 2) : 0x80000000u;
-            dma16(rsa, vo, sa + i * 1024);
-        }
+        for (int i = 0; i < 2; ++i) dma16s(rsa, va[i], (unsigned)k * 2, sa + i * 1024);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const unsigned vo = b_off[i] >= 0 ? (unsigned)(b_off[i] + k * 2) : 0x80000000u;
-            dma16(rsb, vo, sb + i * 1024);
-        }
+        for (int i = 0; i < 2; ++i) dma16s(rsb, vb[i], (unsigned)k * 2, sb + i * 1024);
     };
 
     floatx4 acc[2][2];

@@ -1054,19 +1054,22 @@ __global__ __launch_bounds__(512, 2) void gemm_pipe2_hl_kernel(const GemmBatch b
 // (two per SIMD); wave w owns the 128x64 block (rows 128*(w>>2), columns 64*(w&3)) over the full
 // K: 8 x 4 MFMA blocks of 16x16, 128 f32 accumulators per lane.
 //
-// Why this shape: every K tile's lines come from the MALL or HBM (about 1.5 us away under load),
-// so a CU must keep (operand bytes per flop) x (its MFMA rate) x (latency) in flight to stay busy.
-// A 128x128 tile reads 64 B of operands per 4096 flops (one CU clock of MFMA work) and would need
-// about 230 KB in flight, more than the 160 KB of LDS; a 256x256 tile reads 32 B and needs about
-// 115 KB. K tiles are 32 wide (64-byte LDS rows) in a ring of WNS = 5 stages of 256 A rows and 256
-// W rows (32 KB per stage, the whole LDS): four K tiles (128 KB) are in flight while the fifth is
-// multiplied, with one barrier per K tile. LDS operand reads per K tile: 8 waves x 12 KB against
-// 8 x 32 MFMAs.
+// Why this shape: a 256x256 tile reads half the operand bytes per flop of a 128x128 tile, so half
+// the L2 -> LDS traffic and half the bytes in flight for the same MFMA rate. K tiles are 64 wide:
+// each stage holds 256 A rows and 256 W rows of 128 bytes (64 KB), in a ring of WNS = 2 stages (one
+// K tile in flight while the other is multiplied, one barrier per K tile). Every row of a stage is
+// one whole 128-byte L2 line and one request. A five-stage ring of 32-wide K tiles (64-byte rows,
+// four tiles in flight) measured slower on every shape although it kept twice the bytes in
+// flight: it needs twice the requests per byte (L2 requests per 8192^3 product 136 M against
+// hipBLASLt's 69 M), and a laboratory copy of that loop ran its DMA-only path at half the rate of
+// whole 1 KB blocks. Same box, two repetitions: 4096 x 4096 x 3072 102.3 -> 99.4 us, 4096^3 128.8
+// -> 124.6 us, 8192^3 952.8 -> 900.4 us, 6352 x 4096 x 2048 124.7 -> 118.4 us.
 //
-// Stage layout: row r (64 B = 4 chunks of 8 halves) keeps chunk c at slot c ^ ((r >> 1) & 3). A
-// direct-to-LDS load writes lane l's 16 bytes to slot l of a 1 KB block (16 rows), so lane l loads
-// row 16b + (l >> 2), chunk (l & 3) ^ ((l >> 3) & 3). MFMA operand reads (lane: row l & 15,
-// chunk l >> 4) then touch 8 distinct 16-byte slots mod 128 bytes per 8 lanes: no bank conflicts.
+// Stage layout as in pipe_tile: row r (128 B = 8 chunks of 8 halves) keeps chunk c at slot
+// c ^ (r & 7). A direct-to-LDS load writes lane l's 16 bytes to slot l of a 1 KB block (8 rows),
+// so lane l loads row 8b + (l >> 3), chunk (l & 7) ^ (l >> 3). MFMA operand reads (lane: row l &
+// 15, chunk 4kh + (l >> 4)) touch 8 distinct 16-byte slots mod 128 bytes per 8 lanes: no bank
+// conflicts. LDS operand reads per K tile: 8 waves x 24 KB against 8 x 64 MFMAs.
 //
 // The C tile is staged through LDS in two passes of 128 rows (f32, pitch WTP) and each pass runs
 // the 128x128 epilogue on both column halves, so every epilogue of the pipelined kernels applies
@@ -1074,23 +1077,21 @@ __global__ __launch_bounds__(512, 2) void gemm_pipe2_hl_kernel(const GemmBatch b
 // The per-element order of the f32 sums is that of the 128x128 kernels (K tiles in order, 32-wide
 // MFMA K steps in order), so both give the same bits.
 //
-// Where it pays (same box, f16 operands and output, against the two-stage 128x128 kernel): long
-// K. 4096^3 170.4 -> 144.8 us, 8192^3 1090 -> 962 us, 4096 x 4096 x 3072 128.1 -> 115.4 us; at
-// K = 1024 it loses (6352 x 4096: 79.8 -> 82.8 us, 6352 x 3072: 55.5 -> 70.2 us): 32 K tiles do
-// not amortise the four-stage fill and the 256x256 epilogue, and 400 tiles quantise to two rounds
-// of 256 CUs. A laboratory copy of the loop alone (4096^3, random operands) runs 0.83 us per
-// 32-wide K tile against 0.48 with the DMAs removed and 0.60 with the MFMAs removed: the
-// direct-to-LDS refill path, not the LDS port or the MFMA rate, sets the pace.
+// Where it pays: long K (K >= 2048 and a round of tiles; against the two-stage 128x128 kernel on
+// the box of the first measurements, 4096^3 170.4 -> 144.8 us with the five-stage ring). At K =
+// 1024 it loses: 6352 x 3072 x 1024 51.2 -> 65.7 us (300 tiles quantise to two rounds of 256
+// CUs), 6352 x 4096 x 1024 73.2 -> 71.2 us, and the batch-16 evaluation 6.75 -> 7.45 ms with it.
 // ---------------------------------------------------------------------------------------------
-constexpr int WB = 256, WK = 32, WNS = 5;
-constexpr int WSTAGE = WB * WK;   // halves per operand tile of one stage (16 KB)
+constexpr int WB = 256, WK = 64, WNS = 2;
+constexpr int WSTAGE = WB * WK;   // halves per operand tile of one stage (32 KB)
 constexpr int WTP = 260;          // pitch (floats) of the staged f32 half C tile (128 x 256): 4 rows
                                   // = 16 banks apart, as TP
 
 template <int EPI>
 __device__ __forceinline__ void wide_tile(const GemmProblem &P, int m0, int n0, int tid) {
+    constexpr int WKX = WK, WNX = WNS, WSX = WSTAGE, LPW = 4;   // LPW: DMAs per operand per wave per K tile
     // stage s: A tile at smem + s*WSTAGE, W tile at smem + (WNS + s)*WSTAGE; reused for the C tile
-    constexpr int SMEM = 2 * WNS * WSTAGE > 128 * WTP * 2 ? 2 * WNS * WSTAGE : 128 * WTP * 2;
+    constexpr int SMEM = 2 * WNX * WSX > 128 * WTP * 2 ? 2 * WNX * WSX : 128 * WTP * 2;
     __shared__ __attribute__((aligned(1024))) half_t smem[SMEM];
 
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1100,12 +1101,12 @@ __device__ __forceinline__ void wide_tile(const GemmProblem &P, int m0, int n0, 
     const i32x4 rsa = make_rsrc(P.A);
     const i32x4 rsb = make_rsrc(P.W);
 
-    // loader rows of this lane: 32*wave + 16*i + (lane >> 2), chunk (lane & 3) ^ ((lane >> 3) & 3)
-    const int lr = lane >> 2, lc = (lane & 3) ^ ((lane >> 3) & 3);
-    int a_base[2], a_ts0[2], b_off[2];
+    // loader rows of this lane: 32*wave + 8*i + (lane >> 3), chunk (lane & 7) ^ (lane >> 3)
+    const int lr = lane >> 3, lc = (lane & 7) ^ lr;
+    int a_base[LPW], a_ts0[LPW], b_off[LPW];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int r = wave * 32 + i * 16 + lr;
+    for (int i = 0; i < LPW; ++i) {
+        const int r = wave * 32 + i * (32 / LPW) + lr;
         const int m = m0 + r;
         const int mm = m < M ? m : 0;
         const int b = mm / am.L;
@@ -1119,32 +1120,32 @@ __device__ __forceinline__ void wide_tile(const GemmProblem &P, int m0, int n0, 
     // K tiles in order; the tap's source-row offset, the channel offset and the W column carried
     int nt_trow = 0, nt_kin = 0, nt_kw = 0;
     // per-row A offsets of the current tap and fixed W row offsets, as in pipe_tile
-    unsigned va[2], vb[2];
+    unsigned va[LPW], vb[LPW];
     int va_trow = 0;
     auto set_va = [&]() {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < LPW; ++i) {
             const int ts = a_ts0[i] + va_trow;
             va[i] = (ts >= 0 && ts < aT) ? (unsigned)(a_base[i] + va_trow * lda2) : 0x80000000u;
         }
     };
     set_va();
 #pragma unroll
-    for (int i = 0; i < 2; ++i) vb[i] = b_off[i] >= 0 ? (unsigned)b_off[i] : 0x80000000u;
-    const unsigned ldsw = lds_addr(smem) + wave * 2048;
+    for (int i = 0; i < LPW; ++i) vb[i] = b_off[i] >= 0 ? (unsigned)b_off[i] : 0x80000000u;
+    const unsigned ldsw = lds_addr(smem) + wave * LPW * 1024;
     auto issue = [&](int stage) {
         const int kin = nt_kin, kw = nt_kw;
-        nt_kw += WK;
-        nt_kin += WK;
+        nt_kw += WKX;
+        nt_kin += WKX;
         if (nt_kin == Kc) {
             nt_kin = 0;
             ++nt_trow;
         }
-        const unsigned sa = ldsw + stage * WSTAGE * 2, sb = ldsw + (WNS + stage) * WSTAGE * 2;
+        const unsigned sa = ldsw + stage * WSX * 2, sb = ldsw + (WNX + stage) * WSX * 2;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) dma16s(rsa, va[i], (unsigned)kin * 2, sa + i * 1024);
+        for (int i = 0; i < LPW; ++i) dma16s(rsa, va[i], (unsigned)kin * 2, sa + i * 1024);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) dma16s(rsb, vb[i], (unsigned)kw * 2, sb + i * 1024);
+        for (int i = 0; i < LPW; ++i) dma16s(rsb, vb[i], (unsigned)kw * 2, sb + i * 1024);
         if (nt_trow != va_trow) {   // the next K tile starts a tap
             va_trow = nt_trow;
             set_va();
@@ -1158,51 +1159,61 @@ __device__ __forceinline__ void wide_tile(const GemmProblem &P, int m0, int n0, 
         for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
     const int wm = wave >> 2, wn = wave & 3;
-    // operand read offsets (halves) inside a stage: row (lane & 15) of each 16-row block, chunk
-    // (lane >> 4) at slot (lane >> 4) ^ ((row >> 1) & 3)
-    const int rd = (lane & 15) * WK + (((lane >> 4) ^ (((lane & 15) >> 1) & 3)) * 8);
-    const int a_rd = wm * 128 * WK + rd, b_rd = wn * 64 * WK + rd;
+    // operand read offsets (halves) inside a stage, per 32-wide K half kh: row (lane & 15) of each
+    // 16-row block, chunk 4kh + (lane >> 4) at slot (4kh + (lane >> 4)) ^ (row & 7)
+    constexpr int NKH = WKX / 32;
+    int a_rd[NKH], b_rd[NKH];
+#pragma unroll
+    for (int kh = 0; kh < NKH; ++kh) {
+        const int slot = (kh * 4 + (lane >> 4)) ^ (lane & 7);
+        const int rd = (lane & 15) * WKX + slot * 8;
+        a_rd[kh] = wm * 128 * WKX + rd;
+        b_rd[kh] = wn * 64 * WKX + rd;
+    }
     auto compute = [&](int stage) {
-        const half_t *sa = smem + stage * WSTAGE + a_rd, *sb = smem + (WNS + stage) * WSTAGE + b_rd;
-        half8 af[8], bf[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bf[j] = *(const half8 *)(sb + j * 16 * WK);
+        for (int kh = 0; kh < NKH; ++kh) {
+            const half_t *sa = smem + stage * WSX + a_rd[kh], *sb = smem + (WNX + stage) * WSX + b_rd[kh];
+            half8 af[8], bf[4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) af[i] = *(const half8 *)(sa + i * 16 * WK);
+            for (int j = 0; j < 4; ++j) bf[j] = *(const half8 *)(sb + j * 16 * WKX);
 #pragma unroll
-        for (int i = 0; i < 8; ++i)
+            for (int i = 0; i < 8; ++i) af[i] = *(const half8 *)(sa + i * 16 * WKX);
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+        }
     };
 
     // ring as in pipe_tile: at the top of a step tile kt has landed in stage kt % WNS for every
     // wave and tiles kt+1 .. kt+WNS-1 are in flight (four DMAs per wave per tile)
-    const int nk = P.K / WK;
+    const int nk = P.K / WKX;
     issue(0);
 #pragma unroll
-    for (int j = 1; j < WNS - 1; ++j)
+    for (int j = 1; j < WNX - 1; ++j)
         if (nk > j) issue(j);
-    wait_vmcnt(4 * min(nk - 1, WNS - 2));
+    wait_vmcnt(2 * LPW * min(nk - 1, WNX - 2));
     block_barrier();
-    if (nk > WNS - 1) issue(WNS - 1);
+    if (nk > WNX - 1) issue(WNX - 1);
     int kt = 0;
-    for (; kt + 2 * WNS <= nk; kt += WNS) {
+    for (; kt + 2 * WNX <= nk; kt += WNX) {
 #pragma unroll
-        for (int s2 = 0; s2 < WNS; ++s2) {
+        for (int s2 = 0; s2 < WNX; ++s2) {
             compute(s2);
-            wait_vmcnt(4 * (WNS - 2));
+            wait_vmcnt(2 * LPW * (WNX - 2));
             block_barrier();
             issue(s2);
         }
     }
     for (; kt < nk; ++kt) {
-        const int st = kt % WNS;
+        const int st = kt % WNX;
         compute(st);
         if (kt + 1 < nk) {
-            wait_vmcnt(4 * min(nk - 2 - kt, WNS - 2));
+            wait_vmcnt(2 * LPW * min(nk - 2 - kt, WNX - 2));
             block_barrier();
-            if (kt + WNS < nk) issue(st);
+            if (kt + WNX < nk) issue(st);
         }
     }
     // two passes of 128 rows: the waves of that row half store their accumulators as a row-major

@@ -478,63 +478,89 @@ inline unsigned blocks_for(size_t n, unsigned t = 256) { return (unsigned)((n + 
 // v_mfma_f32_16x16x32_f16, the hi half and the lo half of each 32-wide K slice against the same f16
 // weight columns (an f32-accurate operand), and adds the bias. One launch instead of an LN launch, a
 // split-K GEMM and its reduce.
+//
+// Latency, not work, sets its time (32 workgroups at 8 s): the loads of the first eight weight
+// slices are issued at entry, before the normalisation they do not depend on, and each later slice
+// eight steps ahead of its use; a wave's rows are normalised in batches whose loads are all issued
+// before the first row's reductions.
 template <int NV>
 __global__ __launch_bounds__(256) void final_out_kernel(const FinalArgs a) {
     constexpr int H = 256 * NV, P = 2 * H + 8;
+    constexpr int RB = NV <= 4 ? 4 : 2;   // rows per load batch (RB * 3 * NV float4 registers)
+    constexpr int WD = 8;                 // weight slices in flight
     __shared__ __attribute__((aligned(16))) half_t tileA[16 * P];
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int row0 = blockIdx.x * 16;
+    const int n0 = wave * 16;
+    const bool has_n = n0 < a.N;   // wave-uniform
+    const int n = n0 + (lane & 15), kg = (lane >> 4) * 8;
+    const half_t *wrow = a.W + (long long)(has_n ? n : 0) * a.ldw + kg;
+    half8 wb[WD];
+    if (has_n) {
+#pragma unroll
+        for (int i = 0; i < WD; ++i) wb[i] = *(const half8 *)(wrow + 32 * i);
+    }
 #pragma unroll 1
-    for (int j = 0; j < 4; ++j) {
-        const int lr = wave * 4 + j, v = row0 + lr;
-        if (v >= a.rows) break;   // wave-uniform; rows past the end are never stored
-        const float *x = a.X + rowmap_phys(a.xmap, v) * (long long)a.ldx;
-        const float *mb = a.mod + (long long)(v / a.mod_L) * a.mod_ld;
-        float4 xv[NV], sh[NV], scl[NV];
+    for (int j0 = 0; j0 < 4; j0 += RB) {
+        float4 xv[RB][NV], sh[RB][NV], scl[RB][NV];
 #pragma unroll
-        for (int c = 0; c < NV; ++c) {
-            xv[c] = *(const float4 *)(x + c * 256 + lane * 4);
-            sh[c] = *(const float4 *)(mb + a.shift_off + c * 256 + lane * 4);
-            scl[c] = *(const float4 *)(mb + a.scale_off + c * 256 + lane * 4);
+        for (int r = 0; r < RB; ++r) {
+            const int v = row0 + wave * 4 + j0 + r;
+            if (v >= a.rows) break;   // wave-uniform
+            const float *x = a.X + rowmap_phys(a.xmap, v) * (long long)a.ldx;
+            const float *mb = a.mod + (long long)(v / a.mod_L) * a.mod_ld;
+#pragma unroll
+            for (int c = 0; c < NV; ++c) {
+                xv[r][c] = *(const float4 *)(x + c * 256 + lane * 4);
+                sh[r][c] = *(const float4 *)(mb + a.shift_off + c * 256 + lane * 4);
+                scl[r][c] = *(const float4 *)(mb + a.scale_off + c * 256 + lane * 4);
+            }
         }
-        float sum = 0.0f;
 #pragma unroll
-        for (int c = 0; c < NV; ++c) sum += (xv[c].x + xv[c].y) + (xv[c].z + xv[c].w);
-        const float inv_h = 1.0f / (float)H;
-        const float mean = wave_sum(sum) * inv_h;
-        float var = 0.0f;
+        for (int r = 0; r < RB; ++r) {
+            const int lr = wave * 4 + j0 + r, v = row0 + lr;
+            if (v >= a.rows) break;   // rows past the end are never stored
+            float sum = 0.0f;
 #pragma unroll
-        for (int c = 0; c < NV; ++c) {
-            const float d0 = xv[c].x - mean, d1 = xv[c].y - mean, d2 = xv[c].z - mean, d3 = xv[c].w - mean;
-            var += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
-        }
-        var = wave_sum(var) * inv_h;
-        const float inv = 1.0f / sqrtf(var + a.eps);
+            for (int c = 0; c < NV; ++c) sum += (xv[r][c].x + xv[r][c].y) + (xv[r][c].z + xv[r][c].w);
+            const float inv_h = 1.0f / (float)H;
+            const float mean = wave_sum(sum) * inv_h;
+            float var = 0.0f;
 #pragma unroll
-        for (int c = 0; c < NV; ++c) {
-            const int col = c * 256 + lane * 4;
-            const float y0 = (xv[c].x - mean) * inv * (1.0f + scl[c].x) + sh[c].x;
-            const float y1 = (xv[c].y - mean) * inv * (1.0f + scl[c].y) + sh[c].y;
-            const float y2 = (xv[c].z - mean) * inv * (1.0f + scl[c].z) + sh[c].z;
-            const float y3 = (xv[c].w - mean) * inv * (1.0f + scl[c].w) + sh[c].w;
-            const half4 hi = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
-            *(half4 *)(tileA + lr * P + col) = hi;
-            *(half4 *)(tileA + lr * P + H + col) = half4{(half_t)(y0 - (float)hi[0]), (half_t)(y1 - (float)hi[1]),
-                                                         (half_t)(y2 - (float)hi[2]), (half_t)(y3 - (float)hi[3])};
+            for (int c = 0; c < NV; ++c) {
+                const float d0 = xv[r][c].x - mean, d1 = xv[r][c].y - mean, d2 = xv[r][c].z - mean, d3 = xv[r][c].w - mean;
+                var += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+            }
+            var = wave_sum(var) * inv_h;
+            const float inv = 1.0f / sqrtf(var + a.eps);
+#pragma unroll
+            for (int c = 0; c < NV; ++c) {
+                const int col = c * 256 + lane * 4;
+                const float y0 = (xv[r][c].x - mean) * inv * (1.0f + scl[r][c].x) + sh[r][c].x;
+                const float y1 = (xv[r][c].y - mean) * inv * (1.0f + scl[r][c].y) + sh[r][c].y;
+                const float y2 = (xv[r][c].z - mean) * inv * (1.0f + scl[r][c].z) + sh[r][c].z;
+                const float y3 = (xv[r][c].w - mean) * inv * (1.0f + scl[r][c].w) + sh[r][c].w;
+                const half4 hi = half4{(half_t)y0, (half_t)y1, (half_t)y2, (half_t)y3};
+                *(half4 *)(tileA + lr * P + col) = hi;
+                *(half4 *)(tileA + lr * P + H + col) = half4{(half_t)(y0 - (float)hi[0]), (half_t)(y1 - (float)hi[1]),
+                                                             (half_t)(y2 - (float)hi[2]), (half_t)(y3 - (float)hi[3])};
+            }
         }
     }
     __syncthreads();
-    const int n0 = wave * 16;
-    if (n0 >= a.N) return;   // wave-uniform
-    const int n = n0 + (lane & 15), kg = (lane >> 4) * 8;
-    const half_t *wrow = a.W + (long long)n * a.ldw + kg;
+    if (!has_n) return;
     const half_t *arow = tileA + (lane & 15) * P + kg;
     floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll 8
-    for (int k0 = 0; k0 < H; k0 += 32) {
-        const half8 bf = *(const half8 *)(wrow + k0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8 *)(arow + k0), bf, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8 *)(arow + H + k0), bf, acc, 0, 0, 0);
+#pragma unroll 1
+    for (int k0 = 0; k0 < H; k0 += 32 * WD) {
+#pragma unroll
+        for (int i = 0; i < WD; ++i) {
+            const half8 bf = wb[i];
+            const int k = k0 + 32 * i;
+            if (k0 + 32 * WD < H) wb[i] = *(const half8 *)(wrow + k + 32 * WD);   // uniform
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8 *)(arow + k), bf, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8 *)(arow + H + k), bf, acc, 0, 0, 0);
+        }
     }
     const float bn = a.bias ? a.bias[n] : 0.0f;
 #pragma unroll

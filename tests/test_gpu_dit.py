@@ -84,14 +84,15 @@ def test_forward_parity_and_taps(tsn, rt, orc, model):
     assert max(blk) <= 2e-3
 
 
-@pytest.mark.parametrize("H,latent,La,Lt", [(512, 32, 100, 37), (2048, 64, 64, 20)])
-def test_forward_other_widths(tsn, rt, orc, H, latent, La, Lt):
+@pytest.mark.parametrize("B,H,latent,La,Lt", [(2, 512, 32, 100, 37), (2, 2048, 64, 64, 20), (16, 512, 32, 40, 9)])
+def test_forward_other_widths(tsn, rt, orc, B, H, latent, La, Lt):
     """The evaluation at hidden widths other than the benchmark's, one joint and one fused block,
-    B = 2, row counts that are not multiples of 16: H = 512 (8 heads, 32 latent channels) and
-    H = 2048 (32 heads), so the one-launch final layer runs with 2 and 8 float4 column groups per
-    lane (its 8-group build batches two rows per load instead of four). Velocity rel-L2 <= 1e-3,
-    every block tap <= 2e-3."""
-    spec = tsn.default_spec(1).copy(H=H, NH=H // 64, F=2 * H, latent=latent, La=La, Lt=Lt, n_joint=1, n_fused=1)
+    row counts that are not multiples of 16: H = 512 (8 heads, 32 latent channels) and H = 2048
+    (32 heads), so the one-launch final layer runs with 2 and 8 float4 column groups per lane (its
+    8-group build batches two rows per load instead of four); at B = 16 the conditioning GEMVs run
+    on MFMA with K = 256 and K = 512. Velocity rel-L2 <= 1e-3, every block tap <= 2e-3."""
+    spec = tsn.default_spec(1).copy(B=B, H=H, NH=H // 64, F=2 * H, latent=latent, La=La, Lt=Lt, n_joint=1,
+                                    n_fused=1)
     w16 = tsn.synth_weights(spec, 91, 1.0)
     w32 = tsn.bf16_to_f32(w16)
     m = tsn.DitModel(rt, spec)
@@ -107,7 +108,7 @@ def test_forward_other_widths(tsn, rt, orc, H, latent, La, Lt):
         err = rel_l2(v.numpy(), vr)
         tg = taps.numpy()
         blk = [rel_l2(tg[i], tr[i]) for i in range(2)]
-        print("H=%d: velocity rel-L2 %.3g; worst block %.3g" % (H, err, max(blk)))
+        print("B=%d H=%d: velocity rel-L2 %.3g; worst block %.3g" % (B, H, err, max(blk)))
         assert err <= 1e-3
         assert max(blk) <= 2e-3
     finally:

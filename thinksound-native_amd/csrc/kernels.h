@@ -229,7 +229,9 @@ int launch_copy_peak(const float *src, float *dst, size_t n4, hipStream_t st);
 
 /* ------------------------------------------------------------------ GEMV (small M) */
 // Y[b][n] = act(sum_k W[n][k] * X[b][k] + bias[n] + addv[b][n]); optional Y2 = silu(Y).
-// W is bf16, f16 or f32 (wdt); X, Y f32; nb <= 16 rows of X. HBM-bound: one wave per 4 rows of W.
+// W is bf16, f16 or f32 (wdt); X, Y f32; nb <= 16 rows of X. HBM-bound: one wave per 4 rows of W
+// on the VALU, or, for 16 rows of X with bf16 W and K = 256, 512 or 1024, 16 rows of W per wave on
+// MFMA with X split exactly into three bf16 terms.
 int launch_gemv(const GemvArgs &a, hipStream_t st);
 
 /* ------------------------------------------------------------------ f32 SIMT linear */

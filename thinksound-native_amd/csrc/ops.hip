@@ -13,6 +13,8 @@
 
 #include <string.h>
 
+#include <algorithm>
+
 namespace tsn {
 
 namespace {
@@ -182,6 +184,93 @@ __global__ __launch_bounds__(256) void gemv_kernel(const GemvArgs a) {
     const int n0 = (blockIdx.x * 4 + wave) * GEMV_ROWS;
     if (n0 >= a.N) return;
     gemv_rows<WT, NB>(a, n0, lane);
+}
+
+// Sixteen input rows with bf16 W on MFMA. X is split exactly into three bf16 terms (h = bf16(x),
+// m = bf16(x - h), l = x - h - m, which bf16 holds exactly: x - h keeps at most 16 significant bits
+// and x - h - m at most 8), so each product W*h, W*m, W*l is exact in f32 and the MFMA sums them in
+// f32: an f32-accurate GEMV whose work sits on the matrix cores instead of the VALU (the f32 body
+// above spends 8 FMAs and 32 bytes of X reads per weight byte at 16 rows and runs well below the
+// HBM rate). Workgroup: 8 waves; the three X planes in LDS (row pitch KS*32 + 8 halves: the 16
+// rows of an operand read sit 16 bytes apart mod 128); wave w takes groups of 16 W rows and, per
+// group, issues all KS 16-byte row-slice loads before its 3*KS MFMAs (v_mfma_f32_16x16x32_bf16:
+// A = 16 W rows x 32 K, B = 32 K x 16 X rows). Output lane l holds rows n0 + 4(l >> 4) + r of
+// X row l & 15.
+typedef __bf16 gv_bf16x8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ uint16_t f32_to_bf16_rne(float x) {
+    const unsigned u = __float_as_uint(x);
+    return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+template <int KS>
+__global__ __launch_bounds__(512, 1) void gemv_mfma16_kernel(const GemvArgs a) {
+    constexpr int K = KS * 32, KP = K + 8, NW = 8;
+    constexpr int XIT = 16 * K / 4 / (NW * 64);   // float4 of X per thread
+    __shared__ __attribute__((aligned(16))) uint16_t xs[3][16 * KP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // all of this thread's X loads first, then the splits (one load latency, not XIT)
+    float4 xv[XIT];
+#pragma unroll
+    for (int j = 0; j < XIT; ++j) {
+        const int i = tid + j * NW * 64, b = i / (K / 4), k = (i - b * (K / 4)) * 4;
+        xv[j] = *(const float4 *)(a.X + (long long)b * a.ldx + k);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 0; j < XIT; ++j) {
+        const int i = tid + j * NW * 64, b = i / (K / 4), k = (i - b * (K / 4)) * 4;
+        const float v[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+        ushort4 t[3];
+        uint16_t *tp[3] = {(uint16_t *)&t[0], (uint16_t *)&t[1], (uint16_t *)&t[2]};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const uint16_t h = f32_to_bf16_rne(v[e]);
+            const float r1 = v[e] - bf16_to_f32(h);
+            const uint16_t m = f32_to_bf16_rne(r1);
+            tp[0][e] = h;
+            tp[1][e] = m;
+            tp[2][e] = f32_to_bf16_rne(r1 - bf16_to_f32(m));
+        }
+#pragma unroll
+        for (int p = 0; p < 3; ++p) *(ushort4 *)(&xs[p][b * KP + k]) = t[p];
+    }
+    __syncthreads();
+    const uint16_t *W = (const uint16_t *)a.W;
+    const int kq = (lane >> 4) * 8;
+    const int xo = (lane & 15) * KP + kq;
+    const int ngroups = (a.N + 15) / 16;
+    for (int g = blockIdx.x * NW + wave; g < ngroups; g += gridDim.x * NW) {
+        // keeps the X fragment reads inside the loop: hoisted out of it, they hold 3 * KS * 4
+        // registers and push the KS row-slice loads into one dependent chain
+        asm volatile("" ::: "memory");
+        const int n0 = g * 16;
+        const int nr = min(n0 + (lane & 15), a.N - 1);
+        const uint16_t *wr = W + (long long)nr * a.ldw + kq;
+        u16x8 wf[KS];
+#pragma unroll
+        for (int s = 0; s < KS; ++s) wf[s] = *(const u16x8 *)(wr + 32 * s);
+        __builtin_amdgcn_sched_barrier(0);   // every slice load issued before the first use
+        floatx4 acc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            const gv_bf16x8 w = __builtin_bit_cast(gv_bf16x8, wf[s]);
+#pragma unroll
+            for (int p = 0; p < 3; ++p)
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    w, __builtin_bit_cast(gv_bf16x8, *(const u16x8 *)(&xs[p][xo + 32 * s])), acc, 0, 0, 0);
+        }
+        const int b = lane & 15;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int n = n0 + 4 * (lane >> 4) + r;
+            if (n >= a.N) continue;
+            float v = acc[r];
+            if (a.bias) v += a.bias[n];
+            if (a.addv) v += a.addv[(long long)b * a.ld_add + n];
+            if (a.silu) v = gemv_silu(v);
+            a.Y[(long long)b * a.ldy + n] = v;
+            if (a.Y2) a.Y2[(long long)b * a.ldy2 + n] = gemv_silu(v);
+        }
+    }
 }
 
 /* ---------------- f32 SIMT linear: 64x64 tile, 4x4 outputs per thread ---------------- */
@@ -706,7 +795,19 @@ int launch_gemv(const GemvArgs &a, hipStream_t st) {
         set_error("gemv: nb must be 1, 2, 4, 8 or 16");
         return TSN_ERR_UNSUPPORTED;
     }
-    if (a.wdt == DT_BF16) { TSN_GEMV_W(uint16_t) }
+    const int ks = a.K / 32;
+    // Sixteen rows of X on MFMA: a workgroup per CU at most, each wave over groups of 16 W rows
+    // (batch-16 adaLN modulation, 131072 x 1024: about 90 against 200 us per launch; batch-16
+    // evaluation 7.158 -> 7.048 ms, same box). Routing the 1024 x 1024 t-MLP layer (64 row groups)
+    // to the f32 body instead measured no better (7.060 ms).
+    if (a.wdt == DT_BF16 && nb == 16 && a.K % 32 == 0 && (ks == 8 || ks == 16 || ks == 32) &&
+        (((uintptr_t)a.W | (uintptr_t)a.X) & 15) == 0) {
+        const int groups = (a.N + 15) / 16;
+        const dim3 g2((unsigned)std::min(256, (groups + 7) / 8)), b2(512);
+        if (ks == 8) TSN_LAUNCH(gemv_mfma16_kernel<8>, g2, b2, 0, st, a);
+        else if (ks == 16) TSN_LAUNCH(gemv_mfma16_kernel<16>, g2, b2, 0, st, a);
+        else TSN_LAUNCH(gemv_mfma16_kernel<32>, g2, b2, 0, st, a);
+    } else if (a.wdt == DT_BF16) { TSN_GEMV_W(uint16_t) }
     else if (a.wdt == DT_F16) { TSN_GEMV_W(half_t) }
     else if (a.wdt == DT_F32) { TSN_GEMV_W(float) }
     else { set_error("gemv: weight dtype"); return TSN_ERR_ARG; }

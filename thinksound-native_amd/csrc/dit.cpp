@@ -347,7 +347,7 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
 
     GemmBatch ob;
     ob.nprob = 2;
-    ob.small = 1;   // 64x64 tiles over the full K while 128x128 tiles would fill under half the chip
+    ob.small = 1;   // 64x64 tiles over the full K while 128x128 tiles would fill under one round
     ob.ws = ws_;
     ob.ws_bytes = ws_bytes_;
     resid_problem(ob.p[0], AO_, H, Sa, 1, H, B * La, H, a.Wo, a.bo, X_, H, mod_ + a.mod_off + 2 * H, NMOD);
@@ -417,7 +417,7 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
 
     GemmBatch ob;
     ob.nprob = 1;
-    ob.small = 1;   // 64x64 tiles over the full K while 128x128 tiles would fill under half the chip
+    ob.small = 1;   // 64x64 tiles over the full K while 128x128 tiles would fill under one round
     ob.ws = ws_;
     ob.ws_bytes = ws_bytes_;
     resid_problem(ob.p[0], AO_, H, D, 1, H, M, H, w.Wo, w.bo, X_, H, mod_ + w.mod_off + 2 * H, NMOD);
@@ -437,9 +437,9 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
 
     GemmBatch f2;
     f2.nprob = 1;
-    // 64x64 tiles over the full K while 128x128 tiles would fill under half the chip (8 s: 794 rows,
-    // 56 tiles): no split-K partials, and the LN that follows is the plain ln_mod kernel instead of
-    // the reduce + LN over four partials (8 s evaluation 1.839 -> 1.820 ms, same box)
+    // 64x64 tiles over the full K while 128x128 tiles would fill under one round (8 s: 794 rows,
+    // 56 tiles; 30 s: 144 tiles): no split-K partials, and the LN that follows is the plain ln_mod
+    // kernel instead of the reduce + LN over the partials (8 s evaluation 1.839 -> 1.820 ms, same box)
     f2.small = 1;
     f2.ws = ws_;
     f2.ws_bytes = ws_bytes_;

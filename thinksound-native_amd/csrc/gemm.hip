@@ -1751,10 +1751,12 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
                 "gemm snake: needs the pipelined kernel (f16 A, 16-byte aligned rows)");
     TSN_REQUIRE(pipe || !any_half, "gemm: half-width W needs the pipelined kernel (f16 A, 16-byte aligned rows)");
     // small tiles when asked for, for plain GEMMs (one tap), when the 128x128 grid would fill under
-    // half the chip
+    // one round of the chip: they replace a K split and its reduce. Same box, two repetitions: the
+    // 30 s evaluation's residual GEMMs (144 tiles of 128x128) 3.825 -> 3.752 ms with them; at
+    // batch 16 (400 tiles) they measured 7.13 -> 7.64 ms, so the limit stays at one round
     bool one_tap = true;
     for (int i = 0; i < b.nprob; ++i) one_tap = one_tap && b.p[i].taps == 1;
-    b.small = b.small && one_tap && tiles < NCU / 2 ? 1 : 0;
+    b.small = b.small && one_tap && tiles < NCU ? 1 : 0;
     if (b.small) {
         TSN_REQUIRE(epi == EPI_RESID && pipe && !any_half,
                     "gemm small tiles: residual epilogue, f16 A and 16-byte aligned operands, no half-width W");

@@ -15,7 +15,8 @@
 //  * gemm_pipe2_kernel / _hl / _bf16: the same loop with two stages (68 KB), two workgroups per CU,
 //    for data-parallel grids of more than one round (one workgroup's epilogue and waits overlap the
 //    other's K loop).
-//  * gemm_small_kernel: 64x64 tiles, 4 waves of 32x32, five 16 KB stages, two workgroups per CU,
+//  * gemm_small_kernel / gemm_small2_kernel: 64x64 tiles, 4 waves of 32x32 (or two groups of 4
+//    waves over alternate K tiles), five (three per group) 16 KB stages, two workgroups per CU,
 //    residual epilogue in place, for N = K = 1024 GEMMs whose 128x128 grid cannot fill the chip.
 //  * gemm_sk_kernel + gemm_fixup_kernel: stream-K over (tile, K tile) units, with the cut tiles
 //    finished in-kernel by their last contributor or by the fixup launch.
@@ -1262,13 +1263,24 @@ constexpr int SSTAGE = SB * BK;     // halves per operand tile of one stage (8 K
 constexpr int SNS = 5;              // LDS stages of the small-tile ring (5 x 16 KB)
 constexpr int STP = 68;             // pitch (floats) of the staged f32 C tile: 4 rows = 16 banks apart
 
-template <int EPI>
-__global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) {
+// G = 2 (gemm_small2_kernel): two groups of four waves share the tile; group g multiplies the K
+// tiles of parity g through its own ring of SNS2 stages, and the two f32 partial tiles are summed
+// (group 0's first) before the epilogue. For grids of at most one workgroup per CU, where the
+// four-wave kernel leaves one wave per SIMD to cover every LDS and barrier latency alone. Same
+// box, 8 s evaluation (its out-projections and fused FFN2s, 208 tiles): 1.7816 -> 1.7554 ms with
+// four stages per group; three stages 1.7426 against 1.7597 (four) and 1.7674 (five); two
+// stages 1.883.
+constexpr int SNS2 = 3;   // stages per group of the two-group kernel (2 x 3 x 16 KB = 96 KB)
+template <int EPI, int G>
+__device__ __forceinline__ void small_tile(const GemmBatch &bt) {
     static_assert(EPI == EPI_RESID, "gemm_small_kernel: residual epilogue only");
-    __shared__ __attribute__((aligned(1024))) half_t smem[2 * SNS * SSTAGE];
+    constexpr int NSX = G == 2 ? SNS2 : SNS;
+    constexpr int SMEM = 2 * NSX * SSTAGE * G > 2 * SB * STP * G ? 2 * NSX * SSTAGE * G : 2 * SB * STP * G;
+    __shared__ __attribute__((aligned(1024))) half_t smem[SMEM];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int grp = G == 2 ? wave >> 2 : 0, w4 = wave & 3;   // group, wave inside the group
     if ((int)blockIdx.x >= bt.total_tiles) {   // prefetch workgroups after the tiles (GemmBatch::pf)
-        prefetch_wg<4>(bt.pf, blockIdx.x - bt.total_tiles, wave, lane);
+        prefetch_wg<4 * G>(bt.pf, blockIdx.x - bt.total_tiles, wave, lane);
         return;
     }
     const int wg = xcd_remap(blockIdx.x, bt.total_tiles);
@@ -1283,16 +1295,18 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
     const i32x4 rsb = make_rsrc(P.W);
 
     // The epilogue's operands (bias, gate rows and the stream rows this thread updates: columns
-    // (tid & 7)*8 .. +7 of rows (tid >> 3) and + 32) do not depend on the product: they are read
-    // here and arrive during the K loop. Read after it, each of the two passes would wait for a
-    // global load, the second behind the first pass's store (the pointers may alias).
+    // (tid & 7)*8 .. +7 of rows (tid >> 3) and + 32 (G = 1; one pass of rows tid >> 3 for G = 2))
+    // do not depend on the product: they are read here and arrive during the K loop. Read after it,
+    // each pass would wait for a global load, the second behind the first pass's store (the
+    // pointers may alias).
+    constexpr int NPASS = 2 / G;
     const int ecol = (tid & 7) * 8, en = n0 + ecol;
-    float eb[8], eg[2][8], ex[2][8];
+    float eb[8], eg[NPASS][8], ex[NPASS][8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) eb[e] = 0.0f;
     if (P.bias && en < N) load8(P.bias + en, eb);
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
+    for (int p = 0; p < NPASS; ++p) {
         const int m = m0 + (tid >> 3) + 32 * p;
         if (m < M && en < N) {
             load8(P.gate + (long long)(m / P.gate_L) * P.gate_ld + en, eg[p]);
@@ -1300,12 +1314,12 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
         }
     }
 
-    // loader rows of this lane: wave*16 + i*8 + (lane >> 3), 16-byte chunk (lane & 7) ^ (lane >> 3)
+    // loader rows of this lane: w4*16 + i*8 + (lane >> 3), 16-byte chunk (lane & 7) ^ (lane >> 3)
     const int lr = lane >> 3, lc = (lane & 7) ^ lr;
     int a_base[2], a_ts0[2], b_off[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-        const int r = wave * 16 + i * 8 + lr;
+        const int r = w4 * 16 + i * 8 + lr;
         const int m = m0 + r;
         const int mm = m < M ? m : 0;
         const int b = mm / am.L;
@@ -1315,7 +1329,7 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
         const int n = n0 + r;
         b_off[i] = n < N ? (n * ldw + lc * 8) * 2 : -1;
     }
-    int nt_k = 0;   // K column of the next K tile (plain GEMM: one tap, so A and W share it)
+    int nt_k = grp * BK;   // K column of the group's next K tile (one tap: A and W share it)
     // row offsets fixed over K (out of range outside the operand); the K column goes in soffset
     unsigned va[2], vb[2];
 #pragma unroll
@@ -1323,11 +1337,12 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
         va[i] = (a_ts0[i] >= 0 && a_ts0[i] < aT) ? (unsigned)a_base[i] : 0x80000000u;
         vb[i] = b_off[i] >= 0 ? (unsigned)b_off[i] : 0x80000000u;
     }
-    const unsigned ldsw = lds_addr(smem) + wave * 2048;
+    // the group's ring: A stages then W stages, NSX of each
+    const unsigned ldsw = lds_addr(smem) + grp * (2 * NSX * SSTAGE * 2) + w4 * 2048;
     auto issue = [&](int stage) {
         const int k = nt_k;
-        nt_k += BK;
-        const unsigned sa = ldsw + stage * SSTAGE * 2, sb = ldsw + (SNS + stage) * SSTAGE * 2;
+        nt_k += G * BK;
+        const unsigned sa = ldsw + stage * SSTAGE * 2, sb = ldsw + (NSX + stage) * SSTAGE * 2;
 #pragma unroll
         for (int i = 0; i < 2; ++i) dma16s(rsa, va[i], (unsigned)k * 2, sa + i * 1024);
 #pragma unroll
@@ -1339,7 +1354,7 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
     for (int i = 0; i < 2; ++i)
 #pragma unroll
         for (int j = 0; j < 2; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = w4 >> 1, wn = w4 & 1;
     int a_rd[2][2], b_rd[2][2];
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
@@ -1350,8 +1365,9 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
             b_rd[kh][i] = (wn * 32 + i * 16 + (lane & 15)) * BK + slot * 8;
         }
     }
+    const half_t *gring = smem + grp * 2 * NSX * SSTAGE;   // this group's ring
     auto compute = [&](int stage) {
-        const half_t *sa = smem + stage * SSTAGE, *sb = smem + (SNS + stage) * SSTAGE;
+        const half_t *sa = gring + stage * SSTAGE, *sb = gring + (NSX + stage) * SSTAGE;
 #pragma unroll
         for (int kh = 0; kh < 2; ++kh) {
             half8 af[2], bf[2];
@@ -1368,40 +1384,43 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
         }
     };
 
-    // the K loop of pipe_tile: tile kt landed in stage kt%SNS, tiles kt+1..kt+SNS-1 in flight
-    const int nk = P.K / BK;
+    // the K loop of pipe_tile over the group's K tiles (every G-th; the launcher makes K a
+    // multiple of G*BK, so both groups take the same count): the group's tile kt landed in stage
+    // kt%NSX, tiles kt+1..kt+NSX-1 in flight; the barriers are shared by both groups
+    const int nk = P.K / BK / G;
     issue(0);
 #pragma unroll
-    for (int j = 1; j < SNS - 1; ++j)
+    for (int j = 1; j < NSX - 1; ++j)
         if (nk > j) issue(j);
-    wait_vmcnt(4 * min(nk - 1, SNS - 2));
+    wait_vmcnt(4 * min(nk - 1, NSX - 2));
     block_barrier();
-    if (nk > SNS - 1) issue(SNS - 1);
+    if (nk > NSX - 1) issue(NSX - 1);
 #define TSN_SMALL_STEP(S)                                                                       \
     {                                                                                           \
         compute(S);                                                                             \
-        wait_vmcnt(4 * (SNS - 2));                                                               \
+        wait_vmcnt(4 * (NSX - 2));                                                              \
         block_barrier();                                                                        \
         issue(S);                                                                               \
     }
     int kt = 0;
-    for (; kt + 2 * SNS <= nk; kt += SNS) {
+    for (; kt + 2 * NSX <= nk; kt += NSX) {
 #pragma unroll
-        for (int s2 = 0; s2 < SNS; ++s2) TSN_SMALL_STEP(s2)
+        for (int s2 = 0; s2 < NSX; ++s2) TSN_SMALL_STEP(s2)
     }
 #undef TSN_SMALL_STEP
     for (; kt < nk; ++kt) {
-        const int st = kt % SNS;
+        const int st = kt % NSX;
         compute(st);
         if (kt + 1 < nk) {
-            wait_vmcnt(4 * min(nk - 2 - kt, SNS - 2));
+            wait_vmcnt(4 * min(nk - 2 - kt, NSX - 2));
             block_barrier();
-            if (kt + SNS < nk) issue(st);
+            if (kt + NSX < nk) issue(st);
         }
     }
-    // C tile through LDS, then 16-byte residual updates: x += gate * (acc + bias)
+    // C tile (one per group) through LDS, then 16-byte residual updates: x += gate * (acc + bias),
+    // acc = group 0's partial + group 1's
     block_barrier();
-    float *tile = (float *)smem;
+    float *tile = (float *)smem + grp * SB * STP;
     {
         const int rb = wm * 32 + (lane >> 4) * 4, cb = wn * 32 + (lane & 15);
 #pragma unroll
@@ -1412,13 +1431,20 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
                 for (int r = 0; r < 4; ++r) tile[(rb + i * 16 + r) * STP + cb + j * 16] = acc[i][j][r];
     }
     block_barrier();
+    tile = (float *)smem;
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
+    for (int p = 0; p < NPASS; ++p) {
         const int row = (tid >> 3) + 32 * p, col = ecol;
         const int m = m0 + row, n = en;
         if (m >= M || n >= N) continue;
         float v[8];
         load8(tile + row * STP + col, v);
+        if constexpr (G == 2) {
+            float v1[8];
+            load8(tile + SB * STP + row * STP + col, v1);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) v[e] += v1[e];
+        }
         if (P.bias)
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] += eb[e];
@@ -1428,6 +1454,14 @@ __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) 
         *(float4 *)x = make_float4(ex[p][0], ex[p][1], ex[p][2], ex[p][3]);
         *(float4 *)(x + 4) = make_float4(ex[p][4], ex[p][5], ex[p][6], ex[p][7]);
     }
+}
+template <int EPI>
+__global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) {
+    small_tile<EPI, 1>(bt);
+}
+template <int EPI>
+__global__ __launch_bounds__(512, 1) void gemm_small2_kernel(const GemmBatch bt) {
+    small_tile<EPI, 2>(bt);
 }
 
 // the workgroup w of G holding unit u: w*U/G <= u < (w + 1)*U/G
@@ -1772,9 +1806,20 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         b.sk = 0;
         b.pipe = 1;
         b.hl = 0;
-        b.kname = "gemm_small_kernel<1>";
         TSN_REQUIRE(pf_ranges_ok(b.pf), "gemm: prefetch ranges");
-        b.pf_nwg = pf_workgroups(b.pf, 4);
+        // two groups of four waves per tile (gemm_small2_kernel) when the grid, prefetch
+        // workgroups included, holds at most one workgroup per CU and every K splits into an even
+        // number of K tiles
+        bool even = true;
+        for (int i = 0; i < b.nprob; ++i) even = even && b.p[i].K % (2 * BK) == 0;
+        if (even && tiles + pf_workgroups(b.pf, 8) <= NCU) {
+            b.small = 2;
+            b.kname = "gemm_small2_kernel<1>";
+            b.pf_nwg = pf_workgroups(b.pf, 8);
+        } else {
+            b.kname = "gemm_small_kernel<1>";
+            b.pf_nwg = pf_workgroups(b.pf, 4);
+        }
         return TSN_OK;
     }
     const bool snake_epi = epi == EPI_SNAKE || epi == EPI_RSNAKE;
@@ -1961,7 +2006,8 @@ int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st)
     if (b.gv.N > 0 && b.gv_nwg == 0) TSN_TRY(launch_gemv(b.gv, st));   // no free CUs in this grid
     if (b.small) {
         TSN_REQUIRE(epi == EPI_RESID, "gemm small tiles: residual epilogue only");
-        TSN_LAUNCH((gemm_small_kernel<EPI_RESID>), dim3(b.total_tiles + b.pf_nwg), dim3(256), 0, st, b);
+        if (b.small == 2) TSN_LAUNCH((gemm_small2_kernel<EPI_RESID>), dim3(b.total_tiles + b.pf_nwg), dim3(512), 0, st, b);
+        else TSN_LAUNCH((gemm_small_kernel<EPI_RESID>), dim3(b.total_tiles + b.pf_nwg), dim3(256), 0, st, b);
         TSN_HIP_CHECK(hipGetLastError());
         return TSN_OK;
     }

@@ -116,8 +116,9 @@ struct GemmBatch {
     int split_waves = 0;
     // nonzero (EPI_RESID, pipelined-kernel operands, no half-width W): 64x64 tiles over the full K
     // (gemm_small_kernel), no split and no stream-K, for one-tap problems when the 128x128 grid has
-    // fewer than 128 tiles. gemm_plan clears it otherwise, and the workspace then serves the usual
-    // split-K / stream-K choice.
+    // fewer than 256 tiles. gemm_plan clears it otherwise, and the workspace then serves the usual
+    // split-K / stream-K choice; it sets 2 for the two-group kernel (gemm_small2_kernel) when the
+    // grid holds at most one workgroup per CU.
     int small = 0;
     // set by gemm_plan: the two-stage kernel (gemm_pipe2_kernel, two workgroups per CU) for
     // data-parallel grids of more than one round (256 tiles)

@@ -454,10 +454,11 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
 // processed in GEMV batches of up to 16 (the weights are read once per batch); pooled row r is
 // pooled[r % 16] (callers pass B rows for B <= 16 batches, or the 16-row repetition).
 int DitModel::enqueue_conditioning(const float *t, int rows, const float *pooled, float *temb, float *h1, float *g,
-                                   float *gs, float *mod, int mod_rows) {
+                                   float *gs, float *mod, int mod_rows, bool temb_done) {
     const hipStream_t st = rt->dev.stream();
     const int H = s.H;
-    TSN_TRY(run("temb_kernel", 0, 0, [&] { return launch_temb_sinusoid(t, temb, rows, s.temb_dim, s.t_max_period, st); }));
+    if (!temb_done)   // an evaluation computes it in its eval_prep launch
+        TSN_TRY(run("temb_kernel", 0, 0, [&] { return launch_temb_sinusoid(t, temb, rows, s.temb_dim, s.t_max_period, st); }));
     for (int r0 = 0; r0 < rows; r0 += 16) {
         const int rem = rows - r0;
         const int nb = rem >= 16 ? 16 : rem > 8 ? 16 : rem > 4 ? 8 : rem > 2 ? 4 : rem;   // rows past `rows` are padding
@@ -500,17 +501,30 @@ int DitModel::enqueue_eval(const float *z, const float *t, const float *text, co
     const hipStream_t st = rt->dev.stream();
     const int B = s.B, H = s.H;
     mod_in_grid_ = !mod_pre && mod_grid_ok();
+    // one launch for the timestep sinusoid, the hi|lo split of z (the input projection's operand)
+    // and the copy of the text rows into the residual stream (src/dit_fwd.cpp:111-119,142-149,160)
+    {
+        EvalPrepArgs ep;
+        memset(&ep, 0, sizeof ep);
+        if (!mod_pre) {
+            ep.t = t; ep.temb = temb_; ep.tnb = B; ep.tD = s.temb_dim; ep.tmax = s.t_max_period;
+        }
+        ep.z = z; ep.ldz = s.latent; ep.zmap = rowmap_dense(B * s.La); ep.z2 = Z2_; ep.sM = B * s.La; ep.sK = s.latent;
+        if (s.Lt > 0) {
+            ep.csrc = text; ep.clds = H; ep.csmap = rowmap_dense(B * s.Lt); ep.cdst = X_; ep.cldd = H;
+            ep.cdmap = RowMap{s.Lt, S, s.La}; ep.cM = B * s.Lt; ep.cH = H;
+        }
+        TSN_TRY(run("eval_prep_kernel", 0, 8.0 * B * s.La * s.latent + 8.0 * B * s.Lt * (double)H,
+                    [&] { return launch_eval_prep(ep, st); }));
+    }
     if (mod_pre) {
         mod_ = mod_pre;
     } else {
-        TSN_TRY(enqueue_conditioning(t, B, pooled, temb_, h1_, g_, gs_, MOD_, mod_in_grid_ ? 0 : NMOD));
+        TSN_TRY(enqueue_conditioning(t, B, pooled, temb_, h1_, g_, gs_, MOD_, mod_in_grid_ ? 0 : NMOD, true));
         mod_ = MOD_;
     }
-    // input projection (src/dit_fwd.cpp:142-149): z split into f16 hi|lo halves, one MFMA GEMM
-    // against [W|W] (f32-accurate), bias added, written into the audio rows of X
-    TSN_TRY(run(K_SPLIT, 0, 8.0 * B * s.La * s.latent, [&] {
-        return launch_split_hilo(z, s.latent, rowmap_dense(B * s.La), Z2_, B * s.La, s.latent, st);
-    }));
+    // input projection (src/dit_fwd.cpp:142-149): z split into f16 hi|lo halves (above), one MFMA
+    // GEMM against [W|W] (f32-accurate), bias added, written into the audio rows of X
     {
         GemmBatch ib;
         ib.nprob = 1;
@@ -523,10 +537,6 @@ int DitModel::enqueue_eval(const float *z, const float *t, const float *text, co
         if (mod_in_grid_) ib.gv = mod_args(gs_, 0, first_mod_rows());   // block 0's modulation rows
         TSN_TRY(gemm_run(ib, EPI_STORE));
     }
-    if (s.Lt > 0)
-        TSN_TRY(run("copy_rows_kernel", 0, 8.0 * B * s.Lt * (double)H, [&] {
-            return launch_copy_rows(text, H, rowmap_dense(B * s.Lt), X_, H, RowMap{s.Lt, S, s.La}, B * s.Lt, H, st);
-        }));
     const size_t tap_n = (size_t)B * S * H;
     int tap = 0;
     // each block's last reduce kernel also applies the next adaLN (the next block's LN1, or the

@@ -83,7 +83,7 @@ private:
     // (t [rows], pooled rows [rows][H] at ld H or repeated with period per, outputs [rows][.]),
     // in GEMV batches of up to 16 rows; modulation rows [0, mod_rows) only
     int enqueue_conditioning(const float *t, int rows, const float *pooled, float *temb, float *h1, float *g,
-                             float *gs, float *mod, int mod_rows);
+                             float *gs, float *mod, int mod_rows, bool temb_done = false);
     int enqueue_eval(const float *z, const float *t, const float *text, const float *pooled, float *v, float *taps,
                      const float *mod_pre);
     bool ln_prefetch() const;

@@ -271,6 +271,14 @@ int launch_copy_rows(const float *src, int lds, RowMap smap, float *dst, int ldd
 int launch_cfg_euler_pairs(const float *V, float *x2, int P, int n, float cfg, float dt, hipStream_t st);
 // x f32 rows -> out [M][2K] f16: out[m][k] = hi = f16(x), out[m][K + k] = f16(x - hi)
 int launch_split_hilo(const float *x, int ldx, RowMap xmap, half_t *out, int M, int K, hipStream_t st);
+// one launch at the start of an evaluation: temb = sinusoid(t) (skipped when t is null), z2 =
+// hi|lo split of z, and cM rows copied csrc -> cdst (each part as its standalone kernel)
+struct EvalPrepArgs {
+    const float *t; float *temb; int tnb, tD; float tmax;
+    const float *z; int ldz; RowMap zmap; half_t *z2; int sM, sK;
+    const float *csrc; int clds; RowMap csmap; float *cdst; int cldd; RowMap cdmap; int cM, cH;
+};
+int launch_eval_prep(const EvalPrepArgs &a, hipStream_t st);
 // bf16 [N][K] -> f16 [N][2K] = [W | W] (weight of a GEMM over a hi|lo operand)
 int launch_dup_cols_bf16_to_f16(const uint16_t *src, half_t *dst, int N, int K, hipStream_t st);
 // format conversions

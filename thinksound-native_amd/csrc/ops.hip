@@ -327,8 +327,7 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(const LinArgs a) {
 
 /* ---------------- small kernels ---------------- */
 // src/dit_fwd.cpp:111-119: fr_k = (10000/max_period) * 10000^(-2k/D), cos half then sin half
-__global__ void temb_kernel(const float *t, float *out, int nb, int D, float max_period) {
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void temb_elem(const float *t, float *out, int nb, int D, float max_period, int idx) {
     const int half = D / 2;
     if (idx >= nb * half) return;
     const int b = idx / half, k = idx - b * half;
@@ -337,13 +336,19 @@ __global__ void temb_kernel(const float *t, float *out, int nb, int D, float max
     out[(long long)b * D + k] = cosf(arg);
     out[(long long)b * D + half + k] = sinf(arg);
 }
+__global__ void temb_kernel(const float *t, float *out, int nb, int D, float max_period) {
+    temb_elem(t, out, nb, D, max_period, blockIdx.x * blockDim.x + threadIdx.x);
+}
 
-__global__ void copy_rows_kernel(const float *src, int lds, RowMap smap, float *dst, int ldd, RowMap dmap, int M, int H) {
-    const int m = blockIdx.x;
-    if (m >= M) return;
+__device__ __forceinline__ void copy_row(const float *src, int lds, RowMap smap, float *dst, int ldd, RowMap dmap, int H, int m) {
     const float *s = src + rowmap_phys(smap, m) * (long long)lds;
     float *d = dst + rowmap_phys(dmap, m) * (long long)ldd;
     for (int c = threadIdx.x; c < H; c += blockDim.x) d[c] = s[c];
+}
+__global__ void copy_rows_kernel(const float *src, int lds, RowMap smap, float *dst, int ldd, RowMap dmap, int M, int H) {
+    const int m = blockIdx.x;
+    if (m >= M) return;
+    copy_row(src, lds, smap, dst, ldd, dmap, H, m);
 }
 
 // shaders/ops_conv.metal:193-201 applied to CFG pairs; both arms of prompt p receive the new x
@@ -358,14 +363,32 @@ __global__ void cfg_euler_pairs_kernel(const float *V, float *x2, int P, int n, 
     x2[(long long)(2 * p + 1) * n + i] = xn;
 }
 
-__global__ void split_hilo_kernel(const float *x, int ldx, RowMap xmap, half_t *out, int M, int K) {
-    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+__device__ __forceinline__ void split_hilo_elem(const float *x, int ldx, RowMap xmap, half_t *out, int M, int K, long long i) {
     if (i >= (long long)M * K) return;
     const int m = (int)(i / K), k = (int)(i - (long long)m * K);
     const float v = x[rowmap_phys(xmap, m) * (long long)ldx + k];
     const half_t hi = (half_t)v;
     out[(long long)m * 2 * K + k] = hi;
     out[(long long)m * 2 * K + K + k] = (half_t)(v - (float)hi);
+}
+__global__ void split_hilo_kernel(const float *x, int ldx, RowMap xmap, half_t *out, int M, int K) {
+    split_hilo_elem(x, ldx, xmap, out, M, K, (long long)blockIdx.x * blockDim.x + threadIdx.x);
+}
+
+// The start of an evaluation in one launch: the timestep sinusoid (optional), the hi|lo split of
+// the input latent and the copy of the text rows into the residual stream run on disjoint ranges
+// of workgroups (the same element code as temb_kernel, split_hilo_kernel and copy_rows_kernel).
+__global__ void eval_prep_kernel(const EvalPrepArgs a) {
+    const int nt = a.t ? (int)((a.tnb * (a.tD / 2) + 255) / 256) : 0;
+    const int ns = (int)(((long long)a.sM * a.sK + 255) / 256);
+    const int blk = blockIdx.x;
+    if (blk < nt) {
+        temb_elem(a.t, a.temb, a.tnb, a.tD, a.tmax, blk * 256 + threadIdx.x);
+    } else if (blk < nt + ns) {
+        split_hilo_elem(a.z, a.ldz, a.zmap, a.z2, a.sM, a.sK, (long long)(blk - nt) * 256 + threadIdx.x);
+    } else if (blk - nt - ns < a.cM) {
+        copy_row(a.csrc, a.clds, a.csmap, a.cdst, a.cldd, a.cdmap, a.cH, blk - nt - ns);
+    }
 }
 __global__ void dup_cols_kernel(const uint16_t *src, half_t *dst, int N, int K) {
     const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
@@ -846,6 +869,17 @@ int launch_copy_rows(const float *src, int lds, RowMap smap, float *dst, int ldd
 int launch_cfg_euler_pairs(const float *V, float *x2, int P, int n, float cfg, float dt, hipStream_t st) {
     TSN_REQUIRE(V && x2 && P > 0 && n > 0, "cfg_euler_pairs: arguments");
     TSN_LAUNCH(cfg_euler_pairs_kernel, dim3(blocks_for((size_t)P * n)), dim3(256), 0, st, V, x2, P, n, cfg, dt);
+    TSN_HIP_CHECK(hipGetLastError());
+    return TSN_OK;
+}
+
+int launch_eval_prep(const EvalPrepArgs &a, hipStream_t st) {
+    TSN_REQUIRE(!a.t || (a.temb && a.tnb > 0 && a.tD > 0 && a.tD % 2 == 0), "eval_prep: timestep part");
+    TSN_REQUIRE(a.z && a.z2 && a.sM > 0 && a.sK > 0 && a.zmap.L > 0, "eval_prep: split part");
+    TSN_REQUIRE(a.cM == 0 || (a.csrc && a.cdst && a.cH > 0 && a.csmap.L > 0 && a.cdmap.L > 0), "eval_prep: copy part");
+    const long long nt = a.t ? (a.tnb * (long long)(a.tD / 2) + 255) / 256 : 0;
+    const long long ns = ((long long)a.sM * a.sK + 255) / 256;
+    TSN_LAUNCH(eval_prep_kernel, dim3((unsigned)(nt + ns + a.cM)), dim3(256), 0, st, a);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }

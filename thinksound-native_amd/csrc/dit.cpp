@@ -365,13 +365,29 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
     }
     TSN_TRY(resid_ln(ob, r, s.H, s.ln_eps));
 
-    GemmBatch f1;
-    f1.nprob = 2;
-    store_problem(f1.p[0], XN_, H, Sa, ta, H, B * La, s.F, a.W1, HF_, s.F, 1);
-    store_problem(f1.p[1], XN_, H, St, 1, H, B * Lt, s.F, t.W1, HF_, s.F, 1);
-    f1.pf[0] = PfRange{a.W2, H, ta * s.F * 2, (long long)ta * s.F * 2};   // FFN2's weights, read next
-    f1.pf[1] = PfRange{t.W2, H, s.F * 2, (long long)s.F * 2};
-    TSN_TRY(gemm_run(f1, EPI_STORE));
+    // When the audio conv alone fills a round of 256x256 tiles with its long K (batch 16: 4096 rows,
+    // K = 3072), it runs alone on the wide kernel and the text linear follows in its own launch;
+    // batched together they share the two-stage 128x128 kernel
+    if ((B * La + 255) / 256 * ((s.F + 255) / 256) >= 256 && ta * H >= 2048) {
+        GemmBatch fa;
+        fa.nprob = 1;
+        store_problem(fa.p[0], XN_, H, Sa, ta, H, B * La, s.F, a.W1, HF_, s.F, 1);
+        TSN_TRY(gemm_run(fa, EPI_STORE));
+        GemmBatch ft;
+        ft.nprob = 1;
+        store_problem(ft.p[0], XN_, H, St, 1, H, B * Lt, s.F, t.W1, HF_, s.F, 1);
+        ft.pf[0] = PfRange{a.W2, H, ta * s.F * 2, (long long)ta * s.F * 2};   // FFN2's weights, read next
+        ft.pf[1] = PfRange{t.W2, H, s.F * 2, (long long)s.F * 2};
+        TSN_TRY(gemm_run(ft, EPI_STORE));
+    } else {
+        GemmBatch f1;
+        f1.nprob = 2;
+        store_problem(f1.p[0], XN_, H, Sa, ta, H, B * La, s.F, a.W1, HF_, s.F, 1);
+        store_problem(f1.p[1], XN_, H, St, 1, H, B * Lt, s.F, t.W1, HF_, s.F, 1);
+        f1.pf[0] = PfRange{a.W2, H, ta * s.F * 2, (long long)ta * s.F * 2};   // FFN2's weights, read next
+        f1.pf[1] = PfRange{t.W2, H, s.F * 2, (long long)s.F * 2};
+        TSN_TRY(gemm_run(f1, EPI_STORE));
+    }
 
     GemmBatch f2;
     f2.nprob = 2;

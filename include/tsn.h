@@ -67,12 +67,16 @@ int tsn_runtime_alloc_stats(tsn_runtime *rt, size_t *count, size_t *bytes);
  * as given). TSN_F32 / TSN_BF16 weights run the f32 SIMT path (X, Y f32). TSN_BF16 weights with
  * TSN_BF16 X run bf16 products on MFMA (f32 accumulation, f32 Y; K % 64 == 0, N % 8 == 0, 16-byte
  * aligned rows, else TSN_ERR_UNSUPPORTED): the bf16-operand mode, beside the f16 one. ld* = 0 means packed.
- * Uses the runtime's grow-on-demand scratch (2*M*K halves). */
+ * Uses the runtime's grow-on-demand scratch (2*M*K halves). On the f16-W MFMA routes a long K over
+ * few 128x128 output tiles is split: the parts' f32 partial sums go to the runtime's fixed 32 MiB
+ * workspace (allocated by tsn_runtime_create) and are summed in split order, so results stay
+ * deterministic. */
 int tsn_gemm(tsn_runtime *rt, int wdtype, const void *W, const void *X, int xdtype, void *Y, int ydtype,
              const float *bias, uint32_t M, uint32_t N, uint32_t K, uint32_t ldx, uint32_t ldw, uint32_t ldy);
 /* tsn_gemm without any device allocation. No counterpart in the reference: it is for callers that
  * cannot allocate device memory (code under hipGraph capture, tight serving loops, harnesses that
- * forbid hipMalloc). Same arguments, kernels and results as tsn_gemm (bit-identical); the f16 hi|lo
+ * forbid hipMalloc). Same arguments, kernels and results as tsn_gemm (bit-identical; a K split uses
+ * the workspace tsn_runtime_create allocated); the f16 hi|lo
  * split of an f32 X goes to a fixed 32 MiB device array per GPU instead of the runtime's scratch, so
  * with f16 W and f32 X it needs M*K <= tsn_gemm_noalloc_max_elems() (TSN_ERR_ARG beyond). The array
  * is shared by every call on one GPU and keeps the last call's contents (nothing in it needs to

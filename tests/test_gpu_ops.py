@@ -92,6 +92,24 @@ def test_gemm_f16_large_grids(tsn, rt, orc, M, N, K, ydt):
     assert rel_l2(Y, ref64) < (1e-3 if ydt == F16 else 1e-5)
 
 
+@pytest.mark.parametrize("M,N,K,xdt,ydt", [(794, 1024, 4096, F16, F16), (794, 1024, 4096, F16, F32),
+                                            (130, 512, 3072, F16, F32), (1600, 1024, 1024, F16, F16),
+                                            (100, 200, 192, F16, F32), (282, 1024, 4096, F32, F16),
+                                            (282, 1024, 4096, F32, F32), (794, 1024, 4096, F32, F32)])
+def test_gemm_few_tiles(tsn, rt, orc, M, N, K, xdt, ydt):
+    """grids under one round of 128x128 tiles. f16 X: 64x64 tiles over the full K (two wave groups
+    on alternate K tiles for 208 and 16 tiles with K a multiple of 128; four waves for 400 tiles and
+    for K = 192 with ragged M and N = 200). f32 X (the hi|lo route, whose half-width W the 64x64
+    kernel does not take): a long K over 24 or 56 tiles is split into the runtime's workspace and
+    summed in split order by the reduce, which applies bias and the output type. The result does not
+    change from call to call"""
+    Y, ref64, _ = _gemm_case(tsn, rt, orc, M, N, K, xdt, ydt, seed=17, oracle=False)
+    assert not np.isnan(Y).any()
+    assert rel_l2(Y, ref64) < (1e-3 if ydt == F16 else (2e-5 if xdt == F32 else 1e-5))
+    Y2, _, _ = _gemm_case(tsn, rt, orc, M, N, K, xdt, ydt, seed=17, oracle=False)
+    assert np.array_equal(Y, Y2)
+
+
 def test_gemm_f32_weights(tsn, rt, orc):
     r = rng(5)
     M, N, K = 77, 1024, 1024

@@ -23,7 +23,9 @@ def test_gemm_noalloc_matches_gemm(tsn, rt):
     r = rng(123)
     # second call smaller than the first: the array keeps the first call's contents beyond the
     # second's operand, which the second must not read
-    for (M, N, K, ydt) in [(794, 4096, 1024, F32), (130, 1024, 512, F32), (256, 3072, 1024, F16)]:
+    # (282, 1024, 4096): a long K over 24 tiles, split into the runtime's fixed workspace
+    for (M, N, K, ydt) in [(794, 4096, 1024, F32), (130, 1024, 512, F32), (256, 3072, 1024, F16),
+                           (282, 1024, 4096, F32)]:
         X, W, b = _case(rt, r, M, N, K, ydt)
         Xd, Wd, bd = rt.array(X), rt.array(W), rt.array(b)
         ynp = np.float16 if ydt == F16 else np.float32

@@ -56,6 +56,8 @@ constexpr int SK_OVERHEAD_IN = 20;
 // the wide kernel (gemm_wide_kernel) is taken for grids of at least a round of 256x256 tiles whose
 // every problem has K >= WIDE_MIN_K (measured faster there, slower at K = 1024)
 constexpr int WIDE_MIN_TILES = 256, WIDE_MIN_K = 2048;
+// 64x64 grids of more tiles than this take the three-stage small kernel (three workgroups per CU)
+constexpr int SMALL3_MIN_TILES = 2 * NCU;
 
 __device__ inline int xcd_remap(int bid, int nwg) {
     const int xcd = bid & 7, idx = bid >> 3;
@@ -1271,10 +1273,12 @@ constexpr int STP = 68;             // pitch (floats) of the staged f32 C tile: 
 // four stages per group; three stages 1.7426 against 1.7597 (four) and 1.7674 (five); two
 // stages 1.883.
 constexpr int SNS2 = 3;   // stages per group of the two-group kernel (2 x 3 x 16 KB = 96 KB)
-template <int EPI, int G>
+// gemm_small3_kernel: the four-wave kernel with three stages (48 KB), three workgroups per CU, for
+// grids past one round of two workgroups per CU (the 30 s fused FFN2 and out-projections: 560 tiles)
+constexpr int SNS3 = 3;
+template <int EPI, int G, int NSX>
 __device__ __forceinline__ void small_tile(const GemmBatch &bt) {
-    static_assert(EPI == EPI_RESID, "gemm_small_kernel: residual epilogue only");
-    constexpr int NSX = G == 2 ? SNS2 : SNS;
+    static_assert(EPI == EPI_RESID || EPI == EPI_STORE, "gemm_small_kernel: residual or plain store epilogue");
     constexpr int SMEM = 2 * NSX * SSTAGE * G > 2 * SB * STP * G ? 2 * NSX * SSTAGE * G : 2 * SB * STP * G;
     __shared__ __attribute__((aligned(1024))) half_t smem[SMEM];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1305,12 +1309,14 @@ __device__ __forceinline__ void small_tile(const GemmBatch &bt) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) eb[e] = 0.0f;
     if (P.bias && en < N) load8(P.bias + en, eb);
+    if constexpr (EPI == EPI_RESID) {
 #pragma unroll
-    for (int p = 0; p < NPASS; ++p) {
-        const int m = m0 + (tid >> 3) + 32 * p;
-        if (m < M && en < N) {
-            load8(P.gate + (long long)(m / P.gate_L) * P.gate_ld + en, eg[p]);
-            load8(P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + en, ex[p]);
+        for (int p = 0; p < NPASS; ++p) {
+            const int m = m0 + (tid >> 3) + 32 * p;
+            if (m < M && en < N) {
+                load8(P.gate + (long long)(m / P.gate_L) * P.gate_ld + en, eg[p]);
+                load8(P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + en, ex[p]);
+            }
         }
     }
 
@@ -1418,7 +1424,8 @@ __device__ __forceinline__ void small_tile(const GemmBatch &bt) {
         }
     }
     // C tile (one per group) through LDS, then 16-byte residual updates: x += gate * (acc + bias),
-    // acc = group 0's partial + group 1's
+    // or 16-byte stores of acc + bias (SiLU on request) as f32 or f16; acc = group 0's partial +
+    // group 1's
     block_barrier();
     float *tile = (float *)smem + grp * SB * STP;
     {
@@ -1448,20 +1455,41 @@ __device__ __forceinline__ void small_tile(const GemmBatch &bt) {
         if (P.bias)
 #pragma unroll
             for (int e = 0; e < 8; ++e) v[e] += eb[e];
-        float *x = P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n;
+        if constexpr (EPI == EPI_STORE) {
+            if (P.silu)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ex[p][e] = ex[p][e] + v[e] * eg[p][e];
-        *(float4 *)x = make_float4(ex[p][0], ex[p][1], ex[p][2], ex[p][3]);
-        *(float4 *)(x + 4) = make_float4(ex[p][4], ex[p][5], ex[p][6], ex[p][7]);
+                for (int e = 0; e < 8; ++e) v[e] = silu_f(v[e]);
+            const long long o = rowmap_phys(P.ymap, m) * (long long)P.ldy + n;
+            if (P.y_f16) {
+                half8 h;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) h[e] = (half_t)v[e];
+                *(half8 *)((half_t *)P.Y + o) = h;
+            } else {
+                float *y = (float *)P.Y + o;
+                *(float4 *)y = make_float4(v[0], v[1], v[2], v[3]);
+                *(float4 *)(y + 4) = make_float4(v[4], v[5], v[6], v[7]);
+            }
+        } else {
+            float *x = P.R + rowmap_phys(P.rmap, m) * (long long)P.ldr + n;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ex[p][e] = ex[p][e] + v[e] * eg[p][e];
+            *(float4 *)x = make_float4(ex[p][0], ex[p][1], ex[p][2], ex[p][3]);
+            *(float4 *)(x + 4) = make_float4(ex[p][4], ex[p][5], ex[p][6], ex[p][7]);
+        }
     }
 }
 template <int EPI>
 __global__ __launch_bounds__(256, 2) void gemm_small_kernel(const GemmBatch bt) {
-    small_tile<EPI, 1>(bt);
+    small_tile<EPI, 1, SNS>(bt);
+}
+template <int EPI>
+__global__ __launch_bounds__(256, 3) void gemm_small3_kernel(const GemmBatch bt) {
+    small_tile<EPI, 1, SNS3>(bt);
 }
 template <int EPI>
 __global__ __launch_bounds__(512, 1) void gemm_small2_kernel(const GemmBatch bt) {
-    small_tile<EPI, 2>(bt);
+    small_tile<EPI, 2, SNS2>(bt);
 }
 
 // the workgroup w of G holding unit u: w*U/G <= u < (w + 1)*U/G
@@ -1791,9 +1819,20 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
     bool one_tap = true;
     for (int i = 0; i < b.nprob; ++i) one_tap = one_tap && b.p[i].taps == 1;
     b.small = b.small && one_tap && tiles < NCU ? 1 : 0;
+    // a plain store asks softly: operands outside what the small kernel takes keep the other plans,
+    // and so do grids of more than one round of 64x64 tiles (two workgroups per CU). Standalone f16
+    // GEMMs, same box: 794x1024x4096 31.8 -> 15.2 us, 1600x1024x1024 (400 tiles) 12.6 -> 9.8 us;
+    // past one round 2202x1024x1024 (560 tiles) 13.1 -> 14.5 us, 794x4096x1024 (832) 14.0 -> 17.5 us
+    if (b.small && epi == EPI_STORE) {
+        long long st = 0;
+        for (int i = 0; i < b.nprob; ++i)
+            st += (long long)((b.p[i].M + SB - 1) / SB) * ((b.p[i].N + SB - 1) / SB);
+        if (!(pipe && !any_half && !any_lo && !b.bf16) || st > 2 * NCU) b.small = 0;
+    }
     if (b.small) {
-        TSN_REQUIRE(epi == EPI_RESID && pipe && !any_half,
-                    "gemm small tiles: residual epilogue, f16 A and 16-byte aligned operands, no half-width W");
+        TSN_REQUIRE((epi == EPI_RESID || epi == EPI_STORE) && pipe && !any_half && !any_lo && !b.bf16,
+                    "gemm small tiles: residual or plain store epilogue, f16 A and 16-byte aligned operands, no "
+                    "half-width W, no hi|lo output");
         tiles = 0;
         for (int i = 0; i < b.nprob; ++i) {
             GemmProblem &p = b.p[i];
@@ -1812,12 +1851,17 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
         // number of K tiles
         bool even = true;
         for (int i = 0; i < b.nprob; ++i) even = even && b.p[i].K % (2 * BK) == 0;
+        const bool st = epi == EPI_STORE;
         if (even && tiles + pf_workgroups(b.pf, 8) <= NCU) {
             b.small = 2;
-            b.kname = "gemm_small2_kernel<1>";
+            b.kname = st ? "gemm_small2_kernel<0>" : "gemm_small2_kernel<1>";
             b.pf_nwg = pf_workgroups(b.pf, 8);
+        } else if (tiles > SMALL3_MIN_TILES) {
+            b.small = 3;
+            b.kname = st ? "gemm_small3_kernel<0>" : "gemm_small3_kernel<1>";
+            b.pf_nwg = pf_workgroups(b.pf, 4);
         } else {
-            b.kname = "gemm_small_kernel<1>";
+            b.kname = st ? "gemm_small_kernel<0>" : "gemm_small_kernel<1>";
             b.pf_nwg = pf_workgroups(b.pf, 4);
         }
         return TSN_OK;
@@ -1843,7 +1887,7 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
                 }
                 if (!divides) continue;
                 const bool split = kc < nkmin || wg > b.total_tiles;
-                const double cost = (double)((wg + NCU - 1) / NCU) * kc + (split ? 2.0 + part / 2.15e6 : 0.0);
+                const double cost = (double)((wg + NCU - 1) / NCU) * kc + (split ? b.split_overhead + part / 2.15e6 : 0.0);
                 if (cost < best_cost) {
                     best_cost = cost;
                     best = kc;
@@ -2005,9 +2049,19 @@ int gemm_plan(GemmBatch &b, int epi, bool a_f32) {
 int gemm_launch_planned(const GemmBatch &b, int epi, bool a_f32, hipStream_t st) {
     if (b.gv.N > 0 && b.gv_nwg == 0) TSN_TRY(launch_gemv(b.gv, st));   // no free CUs in this grid
     if (b.small) {
-        TSN_REQUIRE(epi == EPI_RESID, "gemm small tiles: residual epilogue only");
-        if (b.small == 2) TSN_LAUNCH((gemm_small2_kernel<EPI_RESID>), dim3(b.total_tiles + b.pf_nwg), dim3(512), 0, st, b);
-        else TSN_LAUNCH((gemm_small_kernel<EPI_RESID>), dim3(b.total_tiles + b.pf_nwg), dim3(256), 0, st, b);
+        const dim3 grid(b.total_tiles + b.pf_nwg);
+        if (epi == EPI_RESID) {
+            if (b.small == 2) TSN_LAUNCH((gemm_small2_kernel<EPI_RESID>), grid, dim3(512), 0, st, b);
+            else if (b.small == 3) TSN_LAUNCH((gemm_small3_kernel<EPI_RESID>), grid, dim3(256), 0, st, b);
+            else TSN_LAUNCH((gemm_small_kernel<EPI_RESID>), grid, dim3(256), 0, st, b);
+        } else if (epi == EPI_STORE) {
+            if (b.small == 2) TSN_LAUNCH((gemm_small2_kernel<EPI_STORE>), grid, dim3(512), 0, st, b);
+            else if (b.small == 3) TSN_LAUNCH((gemm_small3_kernel<EPI_STORE>), grid, dim3(256), 0, st, b);
+            else TSN_LAUNCH((gemm_small_kernel<EPI_STORE>), grid, dim3(256), 0, st, b);
+        } else {
+            set_error("gemm small tiles: residual or plain store epilogue only");
+            return TSN_ERR_ARG;
+        }
         TSN_HIP_CHECK(hipGetLastError());
         return TSN_OK;
     }

@@ -114,11 +114,16 @@ struct GemmBatch {
     // per split, plus the partial-sum traffic). For long-K GEMMs with few tiles, whose A and W tiles
     // would not be shared in L2 under stream-K's staggered K ranges.
     int split_waves = 0;
-    // nonzero (EPI_RESID, pipelined-kernel operands, no half-width W): 64x64 tiles over the full K
-    // (gemm_small_kernel), no split and no stream-K, for one-tap problems when the 128x128 grid has
-    // fewer than 256 tiles. gemm_plan clears it otherwise, and the workspace then serves the usual
-    // split-K / stream-K choice; it sets 2 for the two-group kernel (gemm_small2_kernel) when the
-    // grid holds at most one workgroup per CU.
+    // the split_waves estimate's fixed cost of a split (the reduce), in K-tile times: about 2 for
+    // launches replayed from a captured graph; an eager launch from the host costs about 10
+    float split_overhead = 2.0f;
+    // nonzero (EPI_RESID or EPI_STORE, pipelined-kernel operands, no half-width W, no hi|lo
+    // output): 64x64 tiles over the full K (gemm_small_kernel), no split and no stream-K, for
+    // one-tap problems when the 128x128 grid has fewer than 256 tiles. gemm_plan clears it
+    // otherwise (and for a plain store whose operands the kernel does not take, where a residual
+    // request is an error), and the workspace then serves the usual split-K / stream-K choice; it
+    // sets 2 for the two-group kernel (gemm_small2_kernel) when the grid holds at most one
+    // workgroup per CU.
     int small = 0;
     // set by gemm_plan: the two-stage kernel (gemm_pipe2_kernel, two workgroups per CU) for
     // data-parallel grids of more than one round (256 tiles)

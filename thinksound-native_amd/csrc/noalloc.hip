@@ -2,7 +2,9 @@
 // allocate device memory: code under hipGraph capture, tight serving loops, harnesses that forbid
 // hipMalloc. It runs exactly tsn_gemm's kernels and plans; the one buffer tsn_gemm takes from the
 // runtime's grow-on-demand scratch (the f16 hi|lo split of an f32 X, 4*M*K bytes) lives instead in
-// a file-scope device array of fixed size, one copy per GPU, held until the process ends.
+// a file-scope device array of fixed size, one copy per GPU, held until the process ends. The
+// partial sums of a K split go to the runtime's own fixed workspace, allocated when the runtime was
+// created, as in tsn_gemm.
 //
 // In host code the array's name is only a host-side stand-in: its device address on each GPU comes
 // from hipGetSymbolAddress, taken once per device with that device current (noalloc_init, called
@@ -87,7 +89,7 @@ int gemm_noalloc(Runtime &rt, int wdt, const void *W, const void *X, int xdt, vo
     std::lock_guard<std::mutex> lock(g_mu);
     if (order && g_last_stream[d] && g_last_stream[d] != st) TSN_HIP_CHECK(hipStreamWaitEvent(st, g_done[d], 0));
     TSN_TRY(gemm_hilo((const half_t *)W, ldw, (const float *)X, ldx, Y, ydt, ldy, bias, p.M, p.N, p.K,
-                      (half_t *)g_scratch_dev[d], st));
+                      (half_t *)g_scratch_dev[d], rt.split_ws(), rt.split_ws_bytes(), st));
     if (order) {
         TSN_HIP_CHECK(hipEventRecord(g_done[d], st));
         g_last_stream[d] = st;

@@ -136,6 +136,11 @@ int Device::sync() {
 
 /* ---------------------------------------------------------------- Runtime */
 
+int Runtime::init(int device) {
+    TSN_TRY(dev.init(device));
+    return dev.alloc(SPLIT_WS_BYTES, (void **)&split_ws_);
+}
+
 int Runtime::scratch(size_t bytes, void **p) {
     if (bytes > scratch_bytes_) {
         if (scratch_) TSN_TRY(dev.free(scratch_));
@@ -150,6 +155,19 @@ int Runtime::scratch(size_t bytes, void **p) {
 
 namespace {
 bool aligned16(const void *p) { return (((uintptr_t)p) & 15) == 0; }
+
+// one plain-store GEMM: 64x64 tiles when asked for and the kernel takes it, else the classic K
+// split chosen by estimated time (split_waves) when ws holds the partials, then the split-order
+// reduce that applies bias, SiLU and the output type
+int store_gemm(GemmBatch &b, float *ws, size_t ws_bytes, hipStream_t st) {
+    b.ws = ws;
+    b.ws_bytes = ws ? ws_bytes : 0;
+    b.split_waves = 1;
+    b.split_overhead = 10.0f;   // the reduce is an eager launch of its own (256x3072x1024 split in two
+                                // measured 12.1 -> 15.7 us under the graph-replay charge of 2)
+    TSN_TRY(launch_gemm(b, EPI_STORE, false, st));
+    return gemm_needs_reduce(b) ? launch_gemm_reduce(b, EPI_STORE, st) : TSN_OK;
+}
 }
 
 bool gemm_hilo_ok(const void *W, uint32_t ldw, const void *Y, int ydt, uint32_t ldy, const float *bias,
@@ -164,7 +182,8 @@ bool gemm_hilo_ok(const void *W, uint32_t ldw, const void *Y, int ydt, uint32_t 
 size_t gemm_hilo_bytes(uint32_t M, uint32_t K) { return (size_t)M * 2 * K * sizeof(half_t); }
 
 int gemm_hilo(const half_t *W, uint32_t ldw, const float *X, uint32_t ldx, void *Y, int ydt, uint32_t ldy,
-              const float *bias, uint32_t M, uint32_t N, uint32_t K, half_t *hl, hipStream_t st) {
+              const float *bias, uint32_t M, uint32_t N, uint32_t K, half_t *hl, float *ws, size_t ws_bytes,
+              hipStream_t st) {
     TSN_REQUIRE(W && X && Y && hl && aligned16(hl), "gemm: null operand or unaligned operand buffer");
     TSN_REQUIRE(ydt == DT_F32 || ydt == DT_F16, "gemm: Y must be f32 or f16");
     TSN_REQUIRE(gemm_hilo_ok(W, ldw, Y, ydt, ldy, bias, M, N, K), "gemm: shape outside the hi|lo MFMA path");
@@ -178,7 +197,7 @@ int gemm_hilo(const half_t *W, uint32_t ldw, const float *X, uint32_t ldx, void 
     q.M = (int)M; q.N = (int)N; q.K = (int)(2 * K);
     q.Y = Y; q.ldy = (int)ldy; q.ymap = rowmap_dense((int)M); q.y_f16 = ydt == DT_F16;
     b.nprob = 1;
-    return launch_gemm(b, EPI_STORE, false, st);
+    return store_gemm(b, ws, ws_bytes, st);
 }
 
 int Runtime::gemm(int wdt, const void *W, const void *X, int xdt, void *Y, int ydt, const float *bias,
@@ -195,7 +214,7 @@ int Runtime::gemm(int wdt, const void *W, const void *X, int xdt, void *Y, int y
             void *hl = nullptr;
             TSN_TRY(scratch(gemm_hilo_bytes(p.M, p.K), &hl));
             return gemm_hilo((const half_t *)W, ldw, (const float *)X, ldx, Y, ydt, ldy, bias, p.M, p.N, p.K,
-                             (half_t *)hl, st);
+                             (half_t *)hl, split_ws(), split_ws_bytes(), st);
         }
         if (ydt != DT_F32) {
             set_error("gemm: f32 X with f16 Y needs K % 64 == 0, N % 8 == 0 and 16-byte aligned W, bias and Y");
@@ -214,7 +233,8 @@ int Runtime::gemm(int wdt, const void *W, const void *X, int xdt, void *Y, int y
         q.M = (int)p.M; q.N = (int)p.N; q.K = (int)p.K;
         q.Y = Y; q.ldy = (int)ldy; q.ymap = rowmap_dense((int)p.M); q.y_f16 = ydt == DT_F16;
         b.nprob = 1;
-        return launch_gemm(b, EPI_STORE, false, st);
+        b.small = 1;   // 64x64 tiles over the full K when the 128x128 grid is under one round
+        return store_gemm(b, split_ws(), split_ws_bytes(), st);
     } else if (wdt == DT_BF16 && xdt == DT_BF16) {
         // bf16 operands on MFMA (bf16 products, f32 accumulation and Y)
         TSN_REQUIRE(ydt == DT_F32, "gemm: bf16 X and W give f32 Y");

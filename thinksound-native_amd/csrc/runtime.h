@@ -26,13 +26,16 @@ struct GemmParams {  // src/net.h:13-16; a zero ld means the packed default
 
 // Y = X·Wᵀ (+bias) with f32 X and f16 W as an f32-accurate MFMA product: X is split into an f16
 // hi|lo pair in hl (M x 2K halves) and multiplied against [W | W]. gemm_hilo_ok tells whether the
-// pipelined kernel takes the shape; hl needs gemm_hilo_bytes(M, K) bytes, 16-byte aligned. No
-// split-K or stream-K (no workspace), so the result depends only on the operands.
+// pipelined kernel takes the shape; hl needs gemm_hilo_bytes(M, K) bytes, 16-byte aligned. ws (f32,
+// ws_bytes; null for none) holds the partial sums of a classic K split, taken when the 128x128 grid
+// would leave most CUs idle over a long K; the partials are summed in split order, so the result
+// depends only on the operands and ws_bytes (no stream-K, no atomics).
 bool gemm_hilo_ok(const void *W, uint32_t ldw, const void *Y, int ydt, uint32_t ldy, const float *bias,
                   uint32_t M, uint32_t N, uint32_t K);
 size_t gemm_hilo_bytes(uint32_t M, uint32_t K);
 int gemm_hilo(const half_t *W, uint32_t ldw, const float *X, uint32_t ldx, void *Y, int ydt, uint32_t ldy,
-              const float *bias, uint32_t M, uint32_t N, uint32_t K, half_t *hl, hipStream_t st);
+              const float *bias, uint32_t M, uint32_t N, uint32_t K, half_t *hl, float *ws, size_t ws_bytes,
+              hipStream_t st);
 
 // The allocation-free GEMM (noalloc.hip): a fixed device array per GPU replaces the runtime scratch.
 // noalloc_init takes that array's device address on `device` (which must be current); Device::init
@@ -81,7 +84,8 @@ private:
 class Runtime {
 public:
     Device dev;
-    int init(int device) { return dev.init(device); }
+    // the Device, then the split-K workspace (allocated here, once, so no GEMM call allocates it)
+    int init(int device);
 
     // Y[M,N] = X[M,K]·W[N,K]ᵀ (+bias)                              (src/net.h:24-26)
     // wdt F16, X f32: f32-accurate MFMA product (X as an f16 hi|lo pair against [W | W]), Y f32 or f16;
@@ -131,7 +135,14 @@ public:
     // device-to-device copy GB/s (read + write of a 1 GiB buffer), timed with events on the stream
     int probe_peaks(double *mfma_tflops, double *hbm_gbs);
 
+    // the f32 workspace of the f16 GEMM routes' K split: fixed size, allocated by init
+    float *split_ws() const { return split_ws_; }
+    size_t split_ws_bytes() const { return split_ws_ ? SPLIT_WS_BYTES : 0; }
+
 private:
+    // 8 Mi floats of partial sums: M*N*splits <= 8 Mi (794 x 1024 x 4 splits takes 3.3 Mi)
+    static constexpr size_t SPLIT_WS_BYTES = (size_t)32 << 20;
+    float *split_ws_ = nullptr;
     // grow-on-demand scratch (the role of the reference's im2col buffer, src/net.h:34)
     int scratch(size_t bytes, void **p);
     void *scratch_ = nullptr;

@@ -1074,11 +1074,16 @@ __global__ __launch_bounds__(512, 2) void gemm_pipe2_hl_kernel(const GemmBatch b
 // 15, chunk 4kh + (l >> 4)) touch 8 distinct 16-byte slots mod 128 bytes per 8 lanes: no bank
 // conflicts. LDS operand reads per K tile: 8 waves x 24 KB against 8 x 64 MFMAs.
 //
-// The C tile is staged through LDS in two passes of 128 rows (f32, pitch WTP) and each pass runs
-// the 128x128 epilogue on both column halves, so every epilogue of the pipelined kernels applies
-// (QKV and SwiGLU need a 128-column half inside one of q/k/v or one w1|w3 block pair, as there).
-// The per-element order of the f32 sums is that of the 128x128 kernels (K tiles in order, 32-wide
-// MFMA K steps in order), so both give the same bits.
+// The MFMAs take the W fragment as their first operand, so each 16x16 accumulator block is C's
+// block transposed: a lane holds four adjacent columns of one row. The C tile is staged through
+// LDS in two passes of 128 rows (f32, pitch WTP, one 16-byte write per block row) and each pass
+// runs the 128x128 epilogue on both column halves, so every epilogue of the pipelined kernels
+// applies (QKV and SwiGLU need a 128-column half inside one of q/k/v or one w1|w3 block pair, as
+// there). Writing plain stores straight from the accumulators instead (8 bytes of f16 per row and
+// block, no LDS, no barrier) measured slower: 4096 x 4096 x 3072 98.5 -> 104 us, the batch-16
+// evaluation 6.77 -> 6.82 ms, same box; the staged 16-byte stores of whole rows write L2 lines
+// whole. The per-element order of the f32 sums is that of the 128x128 kernels (K tiles in order,
+// 32-wide MFMA K steps in order).
 //
 // Where it pays: long K (K >= 2048 and a round of tiles; against the two-stage 128x128 kernel on
 // the box of the first measurements, 4096^3 170.4 -> 144.8 us with the five-stage ring). At K =
@@ -1182,11 +1187,14 @@ __device__ __forceinline__ void wide_tile(const GemmProblem &P, int m0, int n0, 
             for (int j = 0; j < 4; ++j) bf[j] = *(const half8 *)(sb + j * 16 * WKX);
 #pragma unroll
             for (int i = 0; i < 8; ++i) af[i] = *(const half8 *)(sa + i * 16 * WKX);
+            // W rows as the MFMA's first operand: the block comes out transposed, so lane l holds
+            // C[row l & 15][columns 4 (l >> 4) .. + 3] of each 16x16 block (four adjacent columns of
+            // one row, stored as one vector); the products and their K order are unchanged
 #pragma unroll
             for (int i = 0; i < 8; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bf[j], af[i], acc[i][j], 0, 0, 0);
         }
     };
 
@@ -1220,19 +1228,20 @@ __device__ __forceinline__ void wide_tile(const GemmProblem &P, int m0, int n0, 
         }
     }
     // two passes of 128 rows: the waves of that row half store their accumulators as a row-major
-    // f32 [128][256] tile in LDS, then all 8 waves run the epilogue on each 128-column half
+    // f32 [128][256] tile in LDS (four adjacent columns per 16-byte write), then all 8 waves run
+    // the epilogue on each 128-column half
     block_barrier();
     float *tile = (float *)smem;
 #pragma unroll 1
     for (int p = 0; p < 2; ++p) {
         if (wm == p) {
-            const int rb = (lane >> 4) * 4, cb = wn * 64 + (lane & 15);
+            const int rb = lane & 15, cb = wn * 64 + (lane >> 4) * 4;
 #pragma unroll
             for (int i = 0; i < 8; ++i)
 #pragma unroll
                 for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) tile[(rb + i * 16 + r) * WTP + cb + j * 16] = acc[i][j][r];
+                    *(float4 *)(tile + (rb + i * 16) * WTP + cb + j * 16) =
+                        make_float4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]);
         }
         block_barrier();
         if (m0 + p * 128 < M) {

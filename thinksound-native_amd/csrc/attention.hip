@@ -79,34 +79,77 @@ __device__ __forceinline__ void block_barrier() {
 // with the gfx950 row-swap permutes (VALU, no LDS round trip). permlane16_swap(x, x) yields the
 // even-row and the odd-row copy of each row pair, permlane32_swap(x, x) the lower- and the
 // upper-half copy; combining them gives every lane of a group the same value.
+// With NaNs ruled out at compile time (this file's flags) fmaxf is one v_max_f32, and nested
+// fmaxf of three operands one v_max3_f32 (no quieting of the operands).
+__device__ __forceinline__ float max2f(float a, float b) { return fmaxf(a, b); }
+__device__ __forceinline__ float max3f(float a, float b, float c) { return fmaxf(fmaxf(a, b), c); }
 __device__ __forceinline__ float rows_max(float v) {
     const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    v = max2f(__uint_as_float(p[0]), __uint_as_float(p[1]));
     const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-    return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+    return max2f(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+// maximum of the lane's scores in the first nj (2 or 4) 16-key MFMA blocks: 4 or 8 instructions
+__device__ __forceinline__ float lane_max(const floatx4 (&sc)[4], int nj) {
+    float m = max3f(sc[0][0], sc[0][1], sc[0][2]);
+    m = max3f(m, sc[0][3], sc[1][0]);
+    m = max3f(m, sc[1][1], sc[1][2]);
+    if (nj <= 2) return max2f(m, sc[1][3]);
+    m = max3f(m, sc[1][3], sc[2][0]);
+    m = max3f(m, sc[2][1], sc[2][2]);
+    m = max3f(m, sc[2][3], sc[3][0]);
+    m = max3f(m, sc[3][1], sc[3][2]);
+    return max2f(m, sc[3][3]);
 }
 
 // LDS slot of 16-byte chunk c of row r: c ^ sw(r). Rows 8 apart get different slots too, so the
 // 16 rows one operand read touches (K rows 8 apart, see below) fall in distinct banks.
 __device__ __forceinline__ int sw(int r) { return (r & 7) ^ ((r >> 3) & 7); }
 
-// Online-softmax reference value with a slack of 2^8: the running reference m (log2 units) moves
-// only when a block's row maximum exceeds it by more than 8, so the probabilities exp2(s - m) stay
-// below 2^8 (well inside f16) and most blocks skip the rescale of O and the row sum. The wave
-// branches on whether any of its lanes moves; a lane that does not keeps alpha = 1. The result is
-// the softmax of the same scores: numerator and denominator share every factor. (A branchless
-// form, one exp2 and 20 multiplies every block, measured 0.35% slower per 8 s evaluation in the
-// pipelined resident path, where it was meant to let the next block's score products mix in.)
-__device__ __forceinline__ void lazy_max(float &m_i, float m_blk, floatx4 (&o)[4], floatx4 &lsum) {
-    const bool up = m_blk > m_i + 8.0f;
+// Online softmax of one 16-query group, with the reference subtracted inside the score product.
+// Q holds q * scale * log2(e), so q.k is the score s in log2 units, and the QK product of a key
+// block starts from the accumulator nb = -base: it yields s - base with no per-score VALU. base
+// is the running reference m (0 before the first block, where m holds the sentinel -1e30, whose
+// exp2 differences are 0). The reference moves only when a block's row maximum exceeds it by
+// more than 8, so the probabilities exp2(s - m) stay below 2^8 (well inside f16) and most blocks
+// skip the rescale of O and the row sum and the shift of the scores: the common path is the row
+// maximum, one compare, and per score one exp2 and half a packed f16 conversion. The wave branches
+// on whether any of its lanes moves; a lane that does not keeps alpha = 1 and shift = 0. The
+// result is the softmax of the same scores: numerator and denominator share every factor.
+// (A branchless form, one exp2 and 20 multiplies every block, measured 0.35% slower per 8 s
+// evaluation in the pipelined resident path.)
+struct SoftRef {
+    float m = -1e30f, base = 0.0f;
+    floatx4 nb = floatx4{0.f, 0.f, 0.f, 0.f};   // -base, the QK products' initial accumulator
+};
+// sc = s - base for the first nj 16-key blocks (-inf for masked keys); on return pf holds the f16
+// probabilities (zero beyond nj blocks) as the PV product's two B operands
+__device__ __forceinline__ void block_probs(floatx4 (&sc)[4], int nj, SoftRef &R, floatx4 (&o)[4], floatx4 &lsum,
+                                            half8 (&pf)[2]) {
+    const float mb = R.base + rows_max(lane_max(sc, nj));   // the block's row maximum
+    const bool up = mb > R.m + 8.0f;
     if (__builtin_amdgcn_ballot_w64(up) != 0) {
-        const float m_new = up ? m_blk : m_i;
-        const float alpha = __builtin_amdgcn_exp2f(m_i - m_new);
-        m_i = m_new;
+        const float m_new = up ? mb : R.m;
+        const float alpha = __builtin_amdgcn_exp2f(R.m - m_new), shift = m_new - R.base;
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
         lsum *= alpha;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (j < nj) sc[j] -= shift;
+        R.m = m_new;
+        R.base = m_new;
+        R.nb = floatx4{-m_new, -m_new, -m_new, -m_new};
     }
+    half_t ph[4][4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ph[j][r] = j < nj ? (half_t)__builtin_amdgcn_exp2f(sc[j][r]) : (half_t)0.0f;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+        pf[c] = half8{ph[2 * c][0], ph[2 * c][1], ph[2 * c][2], ph[2 * c][3],
+                      ph[2 * c + 1][0], ph[2 * c + 1][1], ph[2 * c + 1][2], ph[2 * c + 1][3]};
 }
 __device__ inline int attn_xcd_remap(int bid, int nwg) {
     const int xcd = bid & 7, idx = bid >> 3;
@@ -162,15 +205,14 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
         }
     };
 
-    // running max m_i (scaled, log2 units); Oᵀ and the running row sum live in MFMA accumulators:
-    // the sum is Pᵀ multiplied by a tile of ones, i.e. exactly the f32 sum of the f16 probabilities
-    // the numerator uses, already reduced over all keys of the block.
-    float m_i = -INFINITY;
+    // running reference (log2 units) of this half's queries; Oᵀ and the running row sum live in
+    // MFMA accumulators: the sum is Pᵀ multiplied by a tile of ones, i.e. exactly the f32 sum of
+    // the f16 probabilities the numerator uses, already reduced over all keys of the block.
+    SoftRef R;
     floatx4 o[4], lsum = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     const half8 ones = half8{1, 1, 1, 1, 1, 1, 1, 1};
-    const float scale = a.scale_log2;
 
     // key block blk of this half, resident in stage st
     auto compute = [&](int st, int blk) {
@@ -182,7 +224,7 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
         floatx4 sc[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            sc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            sc[j] = R.nb;
             const int i = lane & 15;
             const int r = 32 * (j >> 1) + 8 * (i >> 2) + 4 * (j & 1) + (i & 3);
 #pragma unroll
@@ -198,27 +240,18 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
                 for (int r = 0; r < 4; ++r)
                     if (blk * AKB + 32 * (j >> 1) + 8 * g + 4 * (j & 1) + r >= S) sc[j][r] = -INFINITY;
         }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) mx = fmaxf(fmaxf(mx, fmaxf(sc[j][0], sc[j][1])), fmaxf(sc[j][2], sc[j][3]));
-        lazy_max(m_i, rows_max(mx) * scale, o, lsum);   // scale > 0: max commutes with it
-        half_t ph[4][4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) ph[j][r] = (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r], scale, -m_i));
+        half8 pf[2];
+        block_probs(sc, 4, R, o, lsum, pf);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            const half8 pf = half8{ph[2 * c][0], ph[2 * c][1], ph[2 * c][2], ph[2 * c][3],
-                                   ph[2 * c + 1][0], ph[2 * c + 1][1], ph[2 * c + 1][2], ph[2 * c + 1][3]};
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
                 // Vt row d = 16dt + (lane&15), keys 32c + 8g + 0..7 (chunk 4c + g)
                 const int d = dt * 16 + (lane & 15);
                 const half8 vf = *(const half8 *)(sV + d * 64 + (((c * 4 + g) ^ sw(d)) * 8));
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[c], o[dt], 0, 0, 0);
             }
-            lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lsum, 0, 0, 0);
+            lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[c], lsum, 0, 0, 0);
         }
     };
 
@@ -284,7 +317,7 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
             const half_t *sK = smem + i * 8192;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                sc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+                sc[j] = R.nb;
                 if (j < nj) {
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) {
@@ -294,7 +327,9 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
                 }
             }
         };
-        // probabilities of keys < lim (the block's valid keys) as the PV product's B operands
+        // probabilities of keys < lim (the block's valid keys) as the PV product's B operands; the
+        // block's QK product started from R.nb, which no other block has moved since (each block's
+        // probabilities are formed before the next block's QK product is issued)
         auto softmax = [&](floatx4 (&sc)[4], int nj, int lim, half8 (&pf)[2]) {
             if (lim < AKB) {
 #pragma unroll
@@ -303,21 +338,7 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
                     for (int r = 0; r < 4; ++r)
                         if (32 * (j >> 1) + 8 * g + 4 * (j & 1) + r >= lim) sc[j][r] = -INFINITY;
             }
-            float mx = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                if (j < nj) mx = fmaxf(fmaxf(mx, fmaxf(sc[j][0], sc[j][1])), fmaxf(sc[j][2], sc[j][3]));
-            lazy_max(m_i, rows_max(mx) * scale, o, lsum);
-            half_t ph[4][4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    ph[j][r] = j < nj ? (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r], scale, -m_i)) : (half_t)0.0f;
-#pragma unroll
-            for (int c = 0; c < 2; ++c)
-                pf[c] = half8{ph[2 * c][0], ph[2 * c][1], ph[2 * c][2], ph[2 * c][3],
-                              ph[2 * c + 1][0], ph[2 * c + 1][1], ph[2 * c + 1][2], ph[2 * c + 1][3]};
+            block_probs(sc, nj, R, o, lsum, pf);
         };
         auto pv = [&](int i, int nc, const half8 (&pf)[2]) {
             const half_t *sV = smem + i * 8192;
@@ -398,6 +419,7 @@ __global__ __launch_bounds__(512, NSTG == 2 ? 2 : 1) void flash_attn_kernel(cons
     // Each half parks its (m, l) and the two column groups the other half stores in LDS; the
     // combination is the same per element whichever half forms it (o_0*f_0 + o_1*f_1, 1/l).
     block_barrier();
+    const float m_i = R.m;   // -1e30 for a half that had no key block: its terms get weight 0
     float *red = (float *)smem;
     float *mine = red + ((half * 4 + wq) * 64 + lane) * 10;
     const float *other = red + (((half ^ 1) * 4 + wq) * 64 + lane) * 10;
@@ -498,12 +520,11 @@ __global__ __launch_bounds__(256, 3) void flash_attn4_kernel(const AttnArgs a) {
         }
     };
 
-    float m_i = -INFINITY;
+    SoftRef R;
     floatx4 o[4], lsum = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) o[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     const half8 ones = half8{1, 1, 1, 1, 1, 1, 1, 1};
-    const float scale = a.scale_log2;
 
     // the lane's fragment offsets (halves) inside a stage, the same for every key block: K rows of
     // MFMA block j, K half ks; Vt rows of d tile dt, key chunk c
@@ -528,7 +549,7 @@ __global__ __launch_bounds__(256, 3) void flash_attn4_kernel(const AttnArgs a) {
         floatx4 sc[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            sc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            sc[j] = R.nb;
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 const half8 kf = *(const half8 *)(sK + k_off[j][ks]);
@@ -542,25 +563,16 @@ __global__ __launch_bounds__(256, 3) void flash_attn4_kernel(const AttnArgs a) {
                 for (int r = 0; r < 4; ++r)
                     if (blk * AKB + 32 * (j >> 1) + 8 * g + 4 * (j & 1) + r >= S) sc[j][r] = -INFINITY;
         }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) mx = fmaxf(fmaxf(mx, fmaxf(sc[j][0], sc[j][1])), fmaxf(sc[j][2], sc[j][3]));
-        lazy_max(m_i, rows_max(mx) * scale, o, lsum);
-        half_t ph[4][4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) ph[j][r] = (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[j][r], scale, -m_i));
+        half8 pf[2];
+        block_probs(sc, 4, R, o, lsum, pf);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            const half8 pf = half8{ph[2 * c][0], ph[2 * c][1], ph[2 * c][2], ph[2 * c][3],
-                                   ph[2 * c + 1][0], ph[2 * c + 1][1], ph[2 * c + 1][2], ph[2 * c + 1][3]};
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt) {
                 const half8 vf = *(const half8 *)(sK + v_off[c][dt]);
-                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[dt], 0, 0, 0);
+                o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[c], o[dt], 0, 0, 0);
             }
-            lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, lsum, 0, 0, 0);
+            lsum = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[c], lsum, 0, 0, 0);
         }
     };
 
@@ -661,7 +673,7 @@ __global__ __launch_bounds__(256, 3) void flash_attn4q2_kernel(const AttnArgs a)
         }
     };
 
-    float m_i[2] = {-INFINITY, -INFINITY};
+    SoftRef R[2];
     floatx4 o[2][4], lsum[2];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
@@ -670,7 +682,6 @@ __global__ __launch_bounds__(256, 3) void flash_attn4q2_kernel(const AttnArgs a)
         for (int dt = 0; dt < 4; ++dt) o[u][dt] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
     const half8 ones = half8{1, 1, 1, 1, 1, 1, 1, 1};
-    const float scale = a.scale_log2;
 
     unsigned k_off[4][2], v_off[2][4];
 #pragma unroll
@@ -693,8 +704,8 @@ __global__ __launch_bounds__(256, 3) void flash_attn4q2_kernel(const AttnArgs a)
         floatx4 sc[2][4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            sc[0][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-            sc[1][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+            sc[0][j] = R[0].nb;
+            sc[1][j] = R[1].nb;
 #pragma unroll
             for (int ks = 0; ks < 2; ++ks) {
                 const half8 kf = *(const half8 *)(sK + k_off[j][ks]);
@@ -713,22 +724,7 @@ __global__ __launch_bounds__(256, 3) void flash_attn4q2_kernel(const AttnArgs a)
         }
         half8 pf[2][2];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            float mx = -INFINITY;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) mx = fmaxf(fmaxf(mx, fmaxf(sc[u][j][0], sc[u][j][1])), fmaxf(sc[u][j][2], sc[u][j][3]));
-            lazy_max(m_i[u], rows_max(mx) * scale, o[u], lsum[u]);
-            half_t ph[4][4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-#pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    ph[j][r] = (half_t)__builtin_amdgcn_exp2f(__builtin_fmaf(sc[u][j][r], scale, -m_i[u]));
-#pragma unroll
-            for (int c = 0; c < 2; ++c)
-                pf[u][c] = half8{ph[2 * c][0], ph[2 * c][1], ph[2 * c][2], ph[2 * c][3],
-                                 ph[2 * c + 1][0], ph[2 * c + 1][1], ph[2 * c + 1][2], ph[2 * c + 1][3]};
-        }
+        for (int u = 0; u < 2; ++u) block_probs(sc[u], 4, R[u], o[u], lsum[u], pf[u]);
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
 #pragma unroll
@@ -787,8 +783,8 @@ __global__ __launch_bounds__(256, 3) void flash_attn4q2_kernel(const AttnArgs a)
 }
 
 // f32 [S, ld] q/k/v slices -> Q/K [nh][S][64], Vt [nh][64][Sp] (f16), one thread per element
-__global__ void attn_pack_kernel(const float *qkv, int S, int nh, int ld, int q_off, int k_off, int v_off,
-                                 half_t *Q, half_t *K, half_t *Vt, int Sp) {
+__global__ void attn_pack_kernel(const float *qkv, float q_scale, int S, int nh, int ld, int q_off, int k_off,
+                                 int v_off, half_t *Q, half_t *K, half_t *Vt, int Sp) {
     const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     const long long total = (long long)nh * Sp * 64;
     if (idx >= total) return;
@@ -798,7 +794,7 @@ __global__ void attn_pack_kernel(const float *qkv, int S, int nh, int ld, int q_
     const int h = (int)(rest / Sp);
     if (s < S) {
         const float *row = qkv + (long long)s * ld + h * 64 + d;
-        Q[((long long)h * S + s) * 64 + d] = (half_t)row[q_off];
+        Q[((long long)h * S + s) * 64 + d] = (half_t)(row[q_off] * q_scale);
         K[((long long)h * S + s) * 64 + d] = (half_t)row[k_off];
         Vt[((long long)h * 64 + d) * Sp + s] = (half_t)row[v_off];
     } else {
@@ -837,12 +833,13 @@ int launch_attention(const AttnArgs &a, hipStream_t st) {
     return TSN_OK;
 }
 
-int launch_attn_pack(const float *qkv, int S, int nh, int ld, int q_off, int k_off, int v_off,
+int launch_attn_pack(const float *qkv, float q_scale, int S, int nh, int ld, int q_off, int k_off, int v_off,
                      half_t *Q, half_t *K, half_t *Vt, int Sp, hipStream_t st) {
     TSN_REQUIRE(qkv && Q && K && Vt && S > 0 && nh > 0 && Sp >= S, "attn_pack: arguments");
     const long long total = (long long)nh * Sp * 64;
     const int blocks = (int)((total + 255) / 256);
-    TSN_LAUNCH(attn_pack_kernel, dim3(blocks), dim3(256), 0, st, qkv, S, nh, ld, q_off, k_off, v_off, Q, K, Vt, Sp);
+    TSN_LAUNCH(attn_pack_kernel, dim3(blocks), dim3(256), 0, st, qkv, q_scale, S, nh, ld, q_off, k_off, v_off, Q, K,
+               Vt, Sp);
     TSN_HIP_CHECK(hipGetLastError());
     return TSN_OK;
 }

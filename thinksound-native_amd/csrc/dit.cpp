@@ -341,7 +341,6 @@ int DitModel::block_joint(int i, bool ln1, Next next) {
     memset(&at, 0, sizeof at);
     at.Q = Q_; at.K = K_; at.Vt = Vt_; at.S = S; at.Sp = Sp; at.nh = s.NH; at.BH = B * s.NH;
     at.O = AO_; at.o_f32 = 0; at.ldo = H; at.omap = rowmap_dense(B * S);
-    at.scale_log2 = 1.4426950408889634f;
     TSN_TRY(run(K_ATTN, 4.0 * B * s.NH * (double)S * S * 64, 8.0 * B * (double)S * H,
                 [&] { return launch_attention(at, st); }));
 
@@ -431,7 +430,6 @@ int DitModel::block_fused(int i, bool ln1, Next next) {
     memset(&at, 0, sizeof at);
     at.Q = Q_; at.K = K_; at.Vt = Vt_; at.S = S; at.Sp = Sp; at.nh = s.NH; at.BH = B * s.NH;
     at.O = AO_; at.o_f32 = 0; at.ldo = H; at.omap = rowmap_dense(M);
-    at.scale_log2 = 1.4426950408889634f;
     TSN_TRY(run(K_ATTN, 4.0 * B * s.NH * (double)S * S * 64, 8.0 * B * (double)S * H,
                 [&] { return launch_attention(at, st); }));
 

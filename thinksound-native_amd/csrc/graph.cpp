@@ -214,7 +214,9 @@ void qkv_problem(GemmProblem &p, const half_t *A, RowMap amap, int M, const half
     p.W = W; p.ldw = H; p.bias = bias; p.M = M; p.N = 3 * H; p.K = H;
     p.Q = Q; p.Kd = K; p.Vt = Vt; p.S_att = S; p.Sp = Sp; p.nh = nh; p.Hq = H;
     p.q_L = q_L; p.q_soff = q_soff; p.rope_len = rope_len; p.rope = rope;
-    p.qn = qn; p.kn = kn; p.rms_eps = eps; p.q_scale = 0.125f;   // 1/sqrt(64), exact in f16
+    // softmax scale 1/sqrt(64) and log2(e), folded into q before its f16 rounding: attention's
+    // products are then scores in log2 units
+    p.qn = qn; p.kn = kn; p.rms_eps = eps; p.q_scale = 0.125f * 1.4426950408889634f;
 }
 
 void resid_problem(GemmProblem &p, const half_t *A, int lda, RowMap amap, int taps, int Kc, int M, int N,

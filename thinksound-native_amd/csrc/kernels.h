@@ -164,20 +164,21 @@ void gemm_problem_init(GemmProblem &p);
 
 /* ------------------------------------------------------------------ attention */
 // Flash attention, hd = 64, non-causal, no mask. Q/K [BH][S][64] f16, Vt [BH][64][Sp] f16
-// (keys >= S of Vt must hold finite values; the library keeps them zero).
+// (keys >= S of Vt must hold finite values; the library keeps them zero). Q holds q * softmax
+// scale * log2(e): its producer folds the factor in before the f16 rounding (the QKV epilogue's
+// q_scale, launch_attn_pack's q_scale), so a product q.k is the score in log2 units.
 // O row for (b, s) is rowmap_phys(omap, b*S + s); head h writes columns h*64..h*64+63.
 struct AttnArgs {
     const half_t *Q, *K, *Vt;
     int S, Sp, nh, BH;
     void *O; int o_f32; int ldo; RowMap omap;
     int o_lo;           // f16 O: nonzero also writes lo = f16(o - f16(o)) at column offset o_lo
-    float scale_log2;   // softmax scale * log2(e)
 };
 int launch_attention(const AttnArgs &a, hipStream_t st);
 
 // Pack f32 q/k/v column slices of a [S, ld] buffer into Q/K [nh][S][64] and Vt [nh][64][Sp]
-// (f16; Vt keys in [S, Sp) zeroed).
-int launch_attn_pack(const float *qkv, int S, int nh, int ld, int q_off, int k_off, int v_off,
+// (f16; Q = f16(q * q_scale); Vt keys in [S, Sp) zeroed).
+int launch_attn_pack(const float *qkv, float q_scale, int S, int nh, int ld, int q_off, int k_off, int v_off,
                      half_t *Q, half_t *K, half_t *Vt, int Sp, hipStream_t st);
 
 /* ------------------------------------------------------------------ LayerNorm + adaLN modulate */

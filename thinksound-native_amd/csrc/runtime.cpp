@@ -441,12 +441,13 @@ int Runtime::attention(const float *qkv, float *out, uint32_t S, uint32_t nh, ui
     half_t *Q = (half_t *)buf, *K = Q + qk, *Vt = K + qk;
     // keep Vt 16-byte aligned
     Vt = (half_t *)(((uintptr_t)Vt + 15) & ~(uintptr_t)15);
-    TSN_TRY(launch_attn_pack(qkv, (int)S, (int)nh, (int)ld, (int)q_off, (int)k_off, (int)v_off, Q, K, Vt, Sp, dev.stream()));
+    // q * scale * log2(e) before the f16 rounding: the kernels' products are scores in log2 units
+    TSN_TRY(launch_attn_pack(qkv, scale * 1.4426950408889634f, (int)S, (int)nh, (int)ld, (int)q_off, (int)k_off,
+                             (int)v_off, Q, K, Vt, Sp, dev.stream()));
     AttnArgs a;
     memset(&a, 0, sizeof a);
     a.Q = Q; a.K = K; a.Vt = Vt; a.S = (int)S; a.Sp = Sp; a.nh = (int)nh; a.BH = (int)nh;
     a.O = out + o_off; a.o_f32 = 1; a.ldo = (int)ldo; a.omap = rowmap_dense((int)S);
-    a.scale_log2 = scale * 1.4426950408889634f;
     return launch_attention(a, dev.stream());
 }
 

@@ -15,9 +15,13 @@
 //  * gemm_pipe2_kernel / _hl / _bf16: the same loop with two stages (68 KB), two workgroups per CU,
 //    for data-parallel grids of more than one round (one workgroup's epilogue and waits overlap the
 //    other's K loop).
-//  * gemm_small_kernel / gemm_small2_kernel: 64x64 tiles, 4 waves of 32x32 (or two groups of 4
-//    waves over alternate K tiles), five (three per group) 16 KB stages, two workgroups per CU,
-//    residual epilogue in place, for N = K = 1024 GEMMs whose 128x128 grid cannot fill the chip.
+//  * gemm_wide_kernel: 256x256 tiles, 8 waves of 128x64, two 64 KB stages, one workgroup per CU,
+//    for long-K grids of at least a round of such tiles.
+//  * gemm_small_kernel / gemm_small2_kernel / gemm_small3_kernel: 64x64 tiles over the full K,
+//    4 waves of 32x32 (small2: two groups of 4 waves over alternate K tiles), with 16 KB stages:
+//    five (two workgroups per CU), three per group (one per CU) or three (three per CU, for grids
+//    past 512 tiles); residual epilogue in place or plain store, for GEMMs whose 128x128 grid
+//    cannot fill one round of the chip.
 //  * gemm_sk_kernel + gemm_fixup_kernel: stream-K over (tile, K tile) units, with the cut tiles
 //    finished in-kernel by their last contributor or by the fixup launch.
 //  * splitk_reduce_kernel: classic split-K sum in split order, then the epilogue.

@@ -394,6 +394,40 @@ def test_attention_two_group_route(tsn, rt, orc, S):
     assert rel_l2(o, ref_m) < 2e-3
 
 
+@pytest.mark.parametrize("S,nh,sign", [(397, 16, 1), (397, 16, -1), (600, 16, 1), (1101, 16, 1), (1101, 16, -1),
+                                       (910, 64, 1), (910, 64, -1)])
+def test_attention_moving_reference(tsn, rt, S, nh, sign):
+    """Scores that rise along the keys by about 12 log2 units per 64-key block (sign 1), so every
+    block moves the running reference and rescales O and the row sum, or fall (sign -1), so later
+    blocks underflow against the first block's reference; on every route (397: eight-wave
+    resident, 600: eight-wave two-stage, 1101: four-wave, 910 with 64 heads: two query groups per
+    wave). Held against a float64 softmax of the operands as the kernel holds them: q rounded to f16
+    after the softmax scale and log2(e) are folded in, k and v rounded to f16."""
+    r = rng(97 + S)
+    H = nh * 64
+    qkv = (r.standard_normal((S, 3 * H)) * 0.3).astype(np.float32)
+    ramp = ((np.arange(S) - S / 2) / 64.0 * 8.4 * sign).astype(np.float32)   # natural-log units
+    for h in range(nh):
+        qkv[:, h * 64] = 4.0                   # q . k gains 4 * 2 * ramp, times the scale 1/8
+        qkv[:, H + h * 64] = 2.0 * ramp
+    out = rt.array(np.full((S, H), np.nan, np.float32))
+    rt.attention(rt.array(qkv), out, S, nh, 64, 3 * H, H, 0, H, 2 * H, 0, 0.125)
+    rt.sync()
+    o = out.numpy()
+    assert not np.isnan(o).any()
+    c = np.float32(0.125 * 1.4426950408889634)
+    q = (qkv[:, :H] * c).astype(np.float16).astype(np.float64)
+    k = qkv[:, H:2 * H].astype(np.float16).astype(np.float64)
+    v = qkv[:, 2 * H:].astype(np.float16).astype(np.float64)
+    ref = np.zeros((S, H))
+    for h in range(nh):
+        sl = slice(h * 64, (h + 1) * 64)
+        s2 = q[:, sl] @ k[:, sl].T                        # log2 units
+        p = np.exp2(s2 - s2.max(1, keepdims=True))
+        ref[:, sl] = (p @ v[:, sl]) / p.sum(1, keepdims=True)
+    assert rel_l2(o, ref) < 3e-3
+
+
 def test_launcher_surface_rest(tsn, rt, orc):
     """geglu, gelu_quick, ln_plain, ln_wb, rms_w, mean_cols and qkv_split3 against the oracle"""
     r = rng(71)

@@ -395,14 +395,16 @@ def test_attention_two_group_route(tsn, rt, orc, S):
 
 
 @pytest.mark.parametrize("S,nh,sign", [(397, 16, 1), (397, 16, -1), (600, 16, 1), (1101, 16, 1), (1101, 16, -1),
-                                       (910, 64, 1), (910, 64, -1)])
+                                       (910, 64, 1), (910, 64, -1), (910, 128, 1), (397, 256, -1)])
 def test_attention_moving_reference(tsn, rt, S, nh, sign):
     """Scores that rise along the keys by about 12 log2 units per 64-key block (sign 1), so every
     block moves the running reference and rescales O and the row sum, or fall (sign -1), so later
     blocks underflow against the first block's reference; on every route (397: eight-wave
     resident, 600: eight-wave two-stage, 1101: four-wave, 910 with 64 heads: two query groups per
-    wave). Held against a float64 softmax of the operands as the kernel holds them: q rounded to f16
-    after the softmax scale and log2(e) are folded in, k and v rounded to f16."""
+    wave (512 workgroups of 128 queries; 910 with 128 heads and 397 with 256 heads, the batch-16
+    shape, 1024 workgroups in more than one round)). Held against a float64 softmax of the operands
+    as the kernel holds them: q rounded to f16 after the softmax scale and log2(e) are folded in, k
+    and v rounded to f16."""
     r = rng(97 + S)
     H = nh * 64
     qkv = (r.standard_normal((S, 3 * H)) * 0.3).astype(np.float32)
